@@ -1,0 +1,203 @@
+"""Pin the CPU oracle against the reference's own outputs (tests/golden, written by
+tests/golden/make_golden.py from the reference CPU code), closed forms and brute force.
+CPU only."""
+import numpy as np
+import pytest
+
+import cora_oracle as orc
+from conftest import GOLDEN, read_fbin
+
+FIXTURES = ["l2_d96", "ip_d64"]
+
+
+def rel_close(a, b, rtol=1e-5, scale=None):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    s = np.maximum(np.abs(b), 1.0 if scale is None else scale)
+    return np.all(np.abs(a - b) <= rtol * s)
+
+
+@pytest.fixture(scope="module", params=FIXTURES)
+def fx(request, golden):
+    name = request.param
+    ref = golden(f"{name}/ref")
+    ivf = orc.read_ivf(GOLDEN / name / "ivf.index")
+    sd = orc.search_data(ivf)
+    q = read_fbin(GOLDEN / name / "queries.fbin")
+    return name, ref, ivf, sd, q
+
+
+def test_ivf_header_and_payload(fx):
+    _, ref, ivf, sd, _ = fx
+    n, dim, P, nl, ex, metric = (int(x) for x in ref["meta"])
+    assert (ivf.num, ivf.dim, ivf.padded_dim, ivf.nlist, ivf.ex_bits, ivf.metric) == (n, dim, P, nl, ex, metric)
+    assert np.array_equal(ivf.ids, ref["ids"])
+    assert np.array_equal(ivf.cluster_sizes, ref["cluster_sizes"])
+    assert np.array_equal(sd.centroids.view(np.uint32), ref["centroids"].view(np.uint32))
+    assert np.array_equal(sd.rotator.view(np.uint32), ref["rotator"].view(np.uint32))
+
+
+def test_search_data_unpack_bit_exact(fx):
+    _, ref, ivf, sd, _ = fx
+    assert np.array_equal(sd.short_data, ref["short_data"].reshape(-1))
+    assert np.array_equal(sd.short_factors.view(np.uint32), ref["short_factors"].view(np.uint32))
+    assert np.array_equal(sd.long_codes, ref["long_codes"])
+    assert np.array_equal(sd.ex_factors.view(np.uint32), ref["ex_factors"].view(np.uint32))
+    # word-major layout inverse
+    W = ivf.padded_dim // 32
+    for c in range(ivf.nlist):
+        s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+        assert np.array_equal(orc.cluster_bits_from_short(sd.short_data, s, n, W), sd.bits[s:s + n])
+
+
+def test_fastscan_pack_golden_and_round_trip(golden):
+    g = golden("quant_d128")
+    compact = g["compact_bits"]
+    blocks = orc.fastscan_pack(compact, 128)
+    assert np.array_equal(blocks, g["fastscan_blocks"])
+    n = compact.shape[0]
+    bits_ref = np.unpackbits(compact, axis=1)  # MSB first == pack_binary order
+    got = []
+    for b in range(0, n, 32):
+        blen = min(32, n - b)
+        got.append(orc.unpack_fastscan_bits(blocks[(b // 32) * 512:(b // 32 + 1) * 512], 128, blen))
+    assert np.array_equal(np.vstack(got), bits_ref)
+    # random round trip, ragged last block
+    rng = np.random.default_rng(5)
+    for n, P in [(1, 64), (33, 128), (70, 192)]:
+        bits = rng.integers(0, 2, (n, P), dtype=np.uint8)
+        blocks = orc.fastscan_pack(np.packbits(bits, axis=1), P)
+        out = [orc.unpack_fastscan_bits(blocks[(b // 32) * 4 * P:(b // 32 + 1) * 4 * P], P, min(32, n - b))
+               for b in range(0, n, 32)]
+        assert np.array_equal(np.vstack(out), bits)
+
+
+def test_rotation_and_query_factors(fx):
+    _, ref, ivf, sd, q = fx
+    qr = orc.rotate(q, sd.rotator)
+    scale = np.abs(q).sum(1, keepdims=True) * np.abs(sd.rotator).max()
+    assert np.all(np.abs(qr - ref["rotated_queries"]) <= 1e-5 * scale)
+    k1, kb = orc.query_factors(ref["rotated_queries"], ivf.ex_bits)
+    s = np.abs(ref["rotated_queries"]).sum(1)
+    assert np.all(np.abs(k1 - ref["est_qvals"][:, 0]) <= 1e-5 * s)
+    assert np.all(np.abs(kb - ref["est_qvals"][:, 1]) <= 1e-5 * 127.5 * s)
+
+
+def test_coarse_probe_distances(fx):
+    _, ref, ivf, sd, _ = fx
+    qr = ref["rotated_queries"]
+    nl = ivf.nlist
+    idx, g_add, g_err, l2 = orc.coarse_probe(qr, sd.centroids, nl, ivf.metric)
+    # order agrees with the reference flat initializer's distances
+    cd = ref["centroid_dist"]
+    for qi in range(qr.shape[0]):
+        d_sorted = cd[qi, idx[qi]]
+        assert np.all(np.diff(d_sorted.astype(np.float64)) >= -1e-5 * d_sorted.max())
+        assert rel_close(np.sqrt(l2[qi]), cd[qi, idx[qi]])
+    # g_add / g_error of the estimate cluster match SplitBatchQuery::set_g_add
+    for qi in range(qr.shape[0]):
+        c = int(ref["est_cluster"][qi])
+        p = int(np.nonzero(idx[qi] == c)[0][0])
+        assert rel_close(g_add[qi, p], ref["est_qvals"][qi, 2], scale=1.0)
+        assert rel_close(g_err[qi, p], ref["est_qvals"][qi, 3])
+
+
+def _est_rows(ref, sd, qi):
+    c = int(ref["est_cluster"][qi])
+    s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+    off = int(sum(int(sd.cluster_sizes[int(ref["est_cluster"][j])]) for j in range(qi)))
+    return c, s, n, off
+
+
+def test_low_and_est_reproduce_reference_estimator(fx):
+    _, ref, ivf, sd, _ = fx
+    for qi in range(ref["rotated_queries"].shape[0]):
+        c, s, n, off = _est_rows(ref, sd, qi)
+        k1, kb, gadd, gerr = ref["est_qvals"][qi, :4]
+        ipx0 = ref["est_ipx0"][off:off + n]
+        f = sd.short_factors[s:s + n]
+        est = orc.est_dist(f[:, 0], f[:, 1], gadd, ipx0, k1)
+        low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], gadd, gerr, ipx0, k1)
+        sc = np.abs(f[:, 1] * (ipx0 + k1)) + abs(gadd) + np.abs(f[:, 0]) + np.abs(f[:, 2] * gerr)
+        assert np.all(np.abs(est - ref["est_dist"][off:off + n]) <= 2e-5 * sc)
+        assert np.all(np.abs(low - ref["est_low"][off:off + n]) <= 2e-5 * sc)
+
+
+def test_refine_reproduces_reference_ex_distance(fx):
+    _, ref, ivf, sd, _ = fx
+    P = ivf.padded_dim
+    for qi in range(ref["rotated_queries"].shape[0]):
+        c, s, n, off = _est_rows(ref, sd, qi)
+        k1, kb, gadd, gerr = ref["est_qvals"][qi, :4]
+        ipx0 = ref["est_ipx0"][off:off + n]
+        ip2 = orc.excode_ip(ref["rotated_queries"][qi], sd.long_codes[s:s + n], P)
+        rd = orc.refine_dist(sd.ex_factors[s:s + n, 0], sd.ex_factors[s:s + n, 1], gadd, ipx0, ip2, kb,
+                             ivf.ex_bits)
+        sc = np.abs(sd.ex_factors[s:s + n, 1]) * (128 * np.abs(ipx0) + np.abs(ip2) + abs(kb)) \
+            + abs(gadd) + np.abs(sd.ex_factors[s:s + n, 0])
+        assert np.all(np.abs(rd - ref["est_exdist"][off:off + n]) <= 2e-5 * sc)
+
+
+def test_excode_pack_unpack_and_ip(golden):
+    g = golden("quant_d128")
+    codes = g["excode_l2"]
+    packed = g["packed7"]
+    assert np.array_equal(orc.unpack_excode7(packed, 128), codes)
+    assert np.array_equal(orc.pack_excode7(codes), packed)
+    centroid = np.fromfile(GOLDEN / "quant_d128" / "rows.f32", dtype=np.float32)[:128]
+    ip = orc.excode_ip(centroid, packed, 128)
+    sc = np.abs(centroid).sum() * 127
+    assert np.all(np.abs(ip - g["ip_fxu7"]) <= 1e-6 * sc)
+
+
+def test_quantize_query_closed_forms():
+    # zero query: width clamps to 1e-30, qint = 0
+    qint, w = orc.quantize_query_bitwise(np.zeros((1, 64), np.float32))
+    assert w[0] == np.float32(1e-30) and not qint.any()
+    # +-amax map to +-127, ties round half to even
+    v = np.zeros((1, 64), np.float32)
+    v[0, 0], v[0, 1] = 127.0, -127.0
+    v[0, 2], v[0, 3], v[0, 4], v[0, 5] = 0.5, 1.5, 2.5, -0.5
+    qint, w = orc.quantize_query_bitwise(v)
+    assert w[0] == 1.0
+    assert list(qint[0, :6]) == [127, -127, 0, 2, 2, 0]
+    # random: reconstruction error within width/2
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 3, (20, 128)).astype(np.float32)
+    qint, w = orc.quantize_query_bitwise(x)
+    assert np.all(np.abs(x - qint * w[:, None]) <= 0.5 * w[:, None] * (1 + 1e-5))
+    assert qint.min() >= -127 and qint.max() <= 127
+
+
+def test_popcount_planes_equal_direct_inner_product():
+    rng = np.random.default_rng(2)
+    for P in (64, 128, 768):
+        bits = rng.integers(0, 2, (50, P), dtype=np.uint8)
+        qint = rng.integers(-128, 128, (1, P)).astype(np.int32)
+        qint[0, :3] = [-128, 127, 0]
+        words = orc.bits_to_words_msb(bits)
+        planes = orc.query_planes_msb(qint)[0]
+        assert np.array_equal(orc.ip_int_planes(words, planes), orc.ip_int_direct(bits, qint[0]))
+
+
+def test_pair_order_comparator_cases():
+    probe_idx = np.array([[5, 1, 3], [1, 5, 2], [3, 2, 1]], dtype=np.int32)
+    rows = orc.pair_order(probe_idx, vanguard=1)
+    # vanguard pairs (probe 0) first, by cluster then query
+    assert [tuple(r) for r in rows[:3]] == [(1, 1, 0), (3, 2, 0), (5, 0, 0)]
+    far = [tuple(r) for r in rows[3:]]
+    assert far == sorted(far, key=lambda r: (r[0], r[2], r[1]))
+    assert len(rows) == 9
+
+
+def test_hybrid_search_all_probes_matches_brute_force(fx):
+    name, ref, ivf, sd, q = fx
+    base = read_fbin(GOLDEN / name / "base.fbin")
+    res = orc.hybrid_search(sd, q, 10, ivf.nlist, ivf.metric, ivf.ex_bits)
+    gt = orc.brute_force_gt(base, q, 10, ivf.metric)
+    assert orc.recall_at_k(res.ids, gt, 10) >= 0.95
+    # the reference CPU path's top-k at full nprobe agrees as closely
+    ref_ids = ref["search_ids"][-1]
+    assert orc.recall_at_k(res.ids, ref_ids.astype(np.uint32), 10) >= 0.95
+    # every vector of every probed cluster was a candidate with infinite thresholds
+    assert all(len(c) == ivf.num for c in res.candidates)
