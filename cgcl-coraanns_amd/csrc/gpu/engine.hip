@@ -1,0 +1,802 @@
+// C-ABI GPU engine (include/cora_gpu.h): owns HBM index residency, the search workspace,
+// the host-coherent GPU->CPU candidate ring and the launch sequence of
+// HybridIndex::search's GPU side (reference src/search/hybrid.cu:35-689).
+#include <float.h>
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../../include/cora_gpu.h"
+#include "engine_internal.h"
+
+using namespace cora;
+
+namespace {
+
+constexpr unsigned long long kDrainMaxSpins = 1ull << 23;  // ~30 s of 127-cycle sleeps
+constexpr uint32_t kScanGrid = 8192;                        // persistent waves
+constexpr uint32_t kVanguardGrid = 512;
+constexpr uint64_t kMaxQueryChunk = 65535;                  // parameters.hpp:12
+constexpr uint64_t kMaxProbeCount = 65536;                  // parameters.hpp:13
+
+template <class T>
+void dfree(T *&p) {
+    if (p)
+        (void)hipFree(p);
+    p = nullptr;
+}
+
+template <class T>
+void hfree(T *&p) {
+    if (p)
+        (void)hipHostFree(p);
+    p = nullptr;
+}
+
+}  // namespace
+
+struct cora_gpu_engine {
+    int device = 0;
+    std::string err;
+    hipStream_t stream = nullptr, stream_d2h = nullptr;
+    hipEvent_t ev_prep = nullptr, ev_probe = nullptr, ev_f0 = nullptr, ev_f1 = nullptr,
+               ev_s0 = nullptr, ev_s1 = nullptr;
+    // index
+    bool loaded = false;
+    uint64_t N = 0, dim = 0, P = 0, nl = 0, ex_bits = 0, max_cluster = 0, total_tiles = 0;
+    int metric = 0;
+    uint32_t W = 0, tile_bytes = 0;
+    float *d_cent = nullptr, *d_cnorm = nullptr, *d_rot = nullptr;
+    uint8_t *d_tiles = nullptr;
+    ClusterMeta *d_meta = nullptr;
+    // queue configuration (hybrid.cuh:105-106)
+    uint64_t qcap = 1ull << 26, spill_cap = 1ull << 24;
+    // workspace
+    bool ws = false;
+    uint64_t ws_q = 0, ws_k = 0, ws_np = 0, ws_van = 0, seed_words = 0;
+    float *d_raw = nullptr, *d_qrot = nullptr, *d_k1 = nullptr, *d_kb = nullptr,
+          *d_qnorm = nullptr, *d_qwidth = nullptr, *d_dist = nullptr, *d_gadd = nullptr,
+          *d_gerr = nullptr, *d_thr_snap = nullptr;
+    uint32_t *d_planes = nullptr, *d_bcount = nullptr, *d_bcursor = nullptr, *d_boff = nullptr,
+             *d_uoff = nullptr, *d_nunits = nullptr, *d_cursor = nullptr, *d_seed = nullptr;
+    int32_t *d_pidx = nullptr;
+    Pair *d_pairs = nullptr;
+    Unit *d_units = nullptr;
+    unsigned long long *d_stats = nullptr;
+    // queue
+    uint4 *h_items = nullptr;
+    ProgressDev *h_progress = nullptr;
+    float *h_thr = nullptr, *h_thr_stage = nullptr;
+    int *h_abort = nullptr;
+    unsigned long long *d_produced = nullptr, *d_cached_limit = nullptr, *d_spill_count = nullptr;
+    int *d_refresh = nullptr, *d_overflow = nullptr, *d_stalled = nullptr;
+    SpillRecord *d_spill = nullptr;
+    bool ring_dirty = false;
+    // pinned host copies for CPU refinement
+    float *h_qrot = nullptr, *h_kb = nullptr, *h_gadd = nullptr;
+    // last launch
+    bool launched = false;
+    cora_search_args last{};
+    uint32_t last_depth = 0, last_batch = 1;
+    bool last_timing = false;
+};
+
+namespace {
+
+int fail(cora_gpu_engine *e, int code, const std::string &msg) {
+    if (e)
+        e->err = msg;
+    return code;
+}
+
+#define HIPCHK(call)                                                                             \
+    do {                                                                                         \
+        hipError_t e_ = (call);                                                                  \
+        if (e_ != hipSuccess)                                                                    \
+            return fail(E, CORA_ERR_RUNTIME, std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+QueueDev queue_dev(cora_gpu_engine *E) {
+    QueueDev q{};
+    q.items = E->h_items;
+    q.progress = E->h_progress;
+    q.capacity = E->qcap;
+    q.mask = E->qcap - 1;
+    q.produced = E->d_produced;
+    q.cached_limit = E->d_cached_limit;
+    q.refresh_flag = E->d_refresh;
+    q.spill = E->d_spill;
+    q.spill_count = E->d_spill_count;
+    q.spill_capacity = E->spill_cap;
+    q.spill_overflow = E->d_overflow;
+    q.abort_flag = E->h_abort;
+    q.stalled = E->d_stalled;
+    return q;
+}
+
+ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool frozen) {
+    ScanParams p{};
+    p.tiles = E->d_tiles;
+    p.meta = E->d_meta;
+    p.qplanes = E->d_planes;
+    p.qwidth = E->d_qwidth;
+    p.k1 = E->d_k1;
+    p.pgadd = E->d_gadd;
+    p.pgerr = E->d_gerr;
+    p.pairs = E->d_pairs;
+    p.units = E->d_units;
+    p.num_units = E->d_nunits;
+    p.unit_cursor = E->d_cursor;
+    p.thresholds = frozen ? E->d_thr_snap : E->h_thr;
+    p.thresholds_live = frozen ? 0 : 1;
+    p.nprobe = E->last.nprobe;
+    p.vanguard = depth;
+    p.keep = keep;
+    p.tile_bytes = E->tile_bytes;
+    p.P = (uint32_t)E->P;
+    p.seed_words = (uint32_t)E->seed_words;
+    p.seed_bits = E->d_seed;
+    p.queue = queue_dev(E);
+    return p;
+}
+
+void release_queue(cora_gpu_engine *E) {
+    hfree(E->h_items);
+    hfree(E->h_progress);
+    hfree(E->h_thr);
+    hfree(E->h_thr_stage);
+    hfree(E->h_abort);
+    dfree(E->d_produced);
+    dfree(E->d_cached_limit);
+    dfree(E->d_spill_count);
+    dfree(E->d_refresh);
+    dfree(E->d_overflow);
+    dfree(E->d_stalled);
+    dfree(E->d_spill);
+}
+
+void release_workspace(cora_gpu_engine *E) {
+    if (E->stream)
+        (void)hipStreamSynchronize(E->stream);
+    if (E->stream_d2h)
+        (void)hipStreamSynchronize(E->stream_d2h);
+    E->ws = false;
+    E->launched = false;
+    E->ws_q = E->ws_k = E->ws_np = E->ws_van = E->seed_words = 0;
+    for (float **p : {&E->d_raw, &E->d_qrot, &E->d_k1, &E->d_kb, &E->d_qnorm, &E->d_qwidth,
+                      &E->d_dist, &E->d_gadd, &E->d_gerr, &E->d_thr_snap})
+        dfree(*p);
+    for (uint32_t **p : {&E->d_planes, &E->d_bcount, &E->d_bcursor, &E->d_boff, &E->d_uoff,
+                         &E->d_nunits, &E->d_cursor, &E->d_seed})
+        dfree(*p);
+    dfree(E->d_pidx);
+    dfree(E->d_pairs);
+    dfree(E->d_units);
+    dfree(E->d_stats);
+    hfree(E->h_qrot);
+    hfree(E->h_kb);
+    hfree(E->h_gadd);
+    release_queue(E);
+}
+
+template <class T>
+int dalloc(cora_gpu_engine *E, T *&p, size_t count) {
+    p = nullptr;
+    const hipError_t r = hipMalloc(reinterpret_cast<void **>(&p), std::max<size_t>(1, count) * sizeof(T));
+    if (r != hipSuccess) {
+        p = nullptr;
+        return fail(E, r == hipErrorOutOfMemory ? CORA_ERR_OUT_OF_MEMORY : CORA_ERR_RUNTIME,
+                    std::string("hipMalloc: ") + hipGetErrorString(r));
+    }
+    return CORA_OK;
+}
+
+template <class T>
+int halloc(cora_gpu_engine *E, T *&p, size_t count, unsigned flags) {
+    p = nullptr;
+    const hipError_t r =
+        hipHostMalloc(reinterpret_cast<void **>(&p), std::max<size_t>(1, count) * sizeof(T), flags);
+    if (r != hipSuccess) {
+        p = nullptr;
+        return fail(E, CORA_ERR_OUT_OF_MEMORY, std::string("hipHostMalloc: ") + hipGetErrorString(r));
+    }
+    return CORA_OK;
+}
+
+#define TRY(x)                  \
+    do {                        \
+        const int rc_ = (x);    \
+        if (rc_ != CORA_OK)     \
+            return rc_;         \
+    } while (0)
+
+bool is_pow2(uint64_t v) { return v && !(v & (v - 1)); }
+
+// validate_search_shape (reference include/coraanns/search/parameters.hpp:15-25)
+int validate_shape(cora_gpu_engine *E, uint64_t q, uint64_t k, uint64_t np) {
+    if (q == 0 || q > kMaxQueryChunk)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT,
+                    "query count must be in [1, 65535]; split larger batches");
+    if (k == 0 || k > (uint64_t)INT32_MAX / q)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT,
+                    "topk must be positive and queries * topk must fit an int");
+    if (np == 0 || np > kMaxProbeCount || np > E->nl)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "nprobe must be in [1, min(nlist, 65536)]");
+    if (E->nl > (uint64_t)INT32_MAX / q || E->P == 0 || E->P > (uint64_t)INT32_MAX / (q * 4))
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "query workspace exceeds kernel indexing limits");
+    if (np > (uint64_t)kSelectMaxProbe)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT,
+                    "nprobe above 4096 is not supported by the LDS probe select");
+    return CORA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cora_gpu_create(cora_gpu_engine **out, int device) {
+    if (!out)
+        return CORA_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    auto *E = new (std::nothrow) cora_gpu_engine();
+    if (!E)
+        return CORA_ERR_OUT_OF_MEMORY;
+    E->device = device;
+    auto init = [&]() -> int {
+        HIPCHK(hipSetDevice(device));
+        HIPCHK(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
+        HIPCHK(hipStreamCreateWithFlags(&E->stream_d2h, hipStreamNonBlocking));
+        for (hipEvent_t *ev : {&E->ev_prep, &E->ev_probe, &E->ev_f0, &E->ev_f1, &E->ev_s0, &E->ev_s1})
+            HIPCHK(hipEventCreate(ev));
+        return CORA_OK;
+    };
+    const int rc = init();
+    if (rc != CORA_OK) {
+        std::string msg = E->err;
+        cora_gpu_destroy(E);
+        (void)msg;
+        return rc;
+    }
+    *out = E;
+    return CORA_OK;
+}
+
+int cora_gpu_destroy(cora_gpu_engine *E) {
+    if (!E)
+        return CORA_OK;
+    (void)hipSetDevice(E->device);
+    release_workspace(E);
+    dfree(E->d_cent);
+    dfree(E->d_cnorm);
+    dfree(E->d_rot);
+    dfree(E->d_tiles);
+    dfree(E->d_meta);
+    for (hipEvent_t ev : {E->ev_prep, E->ev_probe, E->ev_f0, E->ev_f1, E->ev_s0, E->ev_s1})
+        if (ev)
+            (void)hipEventDestroy(ev);
+    if (E->stream)
+        (void)hipStreamDestroy(E->stream);
+    if (E->stream_d2h)
+        (void)hipStreamDestroy(E->stream_d2h);
+    delete E;
+    return CORA_OK;
+}
+
+int cora_gpu_last_error(const cora_gpu_engine *E, char *buf, size_t n) {
+    if (!E || !buf || !n)
+        return CORA_ERR_INVALID_ARGUMENT;
+    const size_t m = std::min(n - 1, E->err.size());
+    memcpy(buf, E->err.data(), m);
+    buf[m] = '\0';
+    return CORA_OK;
+}
+
+int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uint64_t padded_dim,
+                        uint64_t n_centroids, uint64_t ex_bits, int metric,
+                        const float *h_centroids, const float *h_rotator,
+                        const uint32_t *h_short_data, const float *h_short_factors,
+                        const uint64_t *h_cluster_sizes) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (E->loaded)
+        return fail(E, CORA_ERR_LOGIC, "index already loaded");
+    if (!num_vecs || num_vecs > UINT32_MAX || !dim || padded_dim < dim || padded_dim % 64 ||
+        !n_centroids || ex_bits > 8 || !h_centroids || !h_rotator || !h_short_data ||
+        !h_short_factors || !h_cluster_sizes || (metric != CORA_METRIC_L2 && metric != CORA_METRIC_IP))
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "invalid index shape or missing index data");
+    if (padded_dim > 1024)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "padded dimension above 1024 is not supported");
+    if (n_centroids > UINT32_MAX / 2)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "too many centroids");
+    HIPCHK(hipSetDevice(E->device));
+    std::vector<ClusterMeta> meta(n_centroids);
+    uint64_t count = 0, largest = 0, tiles = 0;
+    for (uint64_t c = 0; c < n_centroids; ++c) {
+        const uint64_t n = h_cluster_sizes[c];
+        if (n > num_vecs - count)
+            return fail(E, CORA_ERR_INVALID_ARGUMENT, "cluster sizes exceed index size");
+        meta[c] = ClusterMeta{(uint32_t)count, (uint32_t)n, (uint32_t)tiles, 0u};
+        count += n;
+        largest = std::max(largest, n);
+        tiles += (n + kTileVectors - 1) / kTileVectors;
+    }
+    if (count != num_vecs)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "cluster sizes differ from index size");
+    if (tiles > UINT32_MAX)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "index too large for 32-bit tile indices");
+    const uint32_t W = (uint32_t)(padded_dim / 32);
+    const uint32_t tile_bytes = 256u * W + 768u;
+    uint32_t *d_ref = nullptr;
+    float *d_reff = nullptr;
+    auto cleanup = [&]() {
+        dfree(d_ref);
+        dfree(d_reff);
+    };
+    int rc = CORA_OK;
+    do {
+        if ((rc = dalloc(E, E->d_meta, n_centroids)) ||
+            (rc = dalloc(E, E->d_tiles, std::max<uint64_t>(1, tiles) * tile_bytes)) ||
+            (rc = dalloc(E, E->d_cent, n_centroids * padded_dim)) ||
+            (rc = dalloc(E, E->d_cnorm, n_centroids)) ||
+            (rc = dalloc(E, E->d_rot, dim * padded_dim)) ||
+            (rc = dalloc(E, d_ref, num_vecs * W)) || (rc = dalloc(E, d_reff, num_vecs * 3)))
+            break;
+        hipError_t r = hipSuccess;
+        auto chk = [&](hipError_t x, const char *what) {
+            if (x != hipSuccess && r == hipSuccess) {
+                r = x;
+                E->err = std::string(what) + ": " + hipGetErrorString(x);
+            }
+        };
+        chk(hipMemcpyAsync(E->d_meta, meta.data(), n_centroids * sizeof(ClusterMeta),
+                           hipMemcpyHostToDevice, E->stream), "meta upload");
+        chk(hipMemcpyAsync(E->d_cent, h_centroids, n_centroids * padded_dim * 4,
+                           hipMemcpyHostToDevice, E->stream), "centroid upload");
+        chk(hipMemcpyAsync(E->d_rot, h_rotator, dim * padded_dim * 4, hipMemcpyHostToDevice,
+                           E->stream), "rotator upload");
+        chk(hipMemcpyAsync(d_ref, h_short_data, num_vecs * W * 4, hipMemcpyHostToDevice, E->stream),
+            "code upload");
+        chk(hipMemcpyAsync(d_reff, h_short_factors, num_vecs * 12, hipMemcpyHostToDevice, E->stream),
+            "factor upload");
+        if (r == hipSuccess) {
+            launch_repack(d_ref, d_reff, E->d_meta, (uint32_t)n_centroids, W, E->d_tiles, tile_bytes,
+                          E->stream);
+            launch_row_norms(E->d_cent, (uint32_t)n_centroids, (uint32_t)padded_dim, E->d_cnorm,
+                             E->stream);
+            chk(hipGetLastError(), "repack launch");
+            chk(hipStreamSynchronize(E->stream), "index upload");
+        }
+        if (r != hipSuccess)
+            rc = CORA_ERR_RUNTIME;
+    } while (0);
+    cleanup();
+    if (rc != CORA_OK) {
+        dfree(E->d_meta);
+        dfree(E->d_tiles);
+        dfree(E->d_cent);
+        dfree(E->d_cnorm);
+        dfree(E->d_rot);
+        return rc;
+    }
+    E->N = num_vecs;
+    E->dim = dim;
+    E->P = padded_dim;
+    E->nl = n_centroids;
+    E->ex_bits = ex_bits;
+    E->metric = metric;
+    E->W = W;
+    E->tile_bytes = tile_bytes;
+    E->max_cluster = largest;
+    E->total_tiles = tiles;
+    E->loaded = true;
+    return CORA_OK;
+}
+
+int cora_gpu_set_queue(cora_gpu_engine *E, uint64_t capacity, uint64_t spill_capacity) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!is_pow2(capacity) || capacity > (1ull << 40))
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "queue-capacity must be a positive power of two");
+    if (spill_capacity > (1ull << 36))
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "queue-spill-capacity is too large");
+    if (E->ws)
+        return fail(E, CORA_ERR_LOGIC, "set queue capacity before prepare_workspace");
+    E->qcap = capacity;
+    E->spill_cap = spill_capacity;
+    return CORA_OK;
+}
+
+int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_topk,
+                               uint64_t max_nprobe, uint64_t vanguard_size) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->loaded)
+        return fail(E, CORA_ERR_LOGIC, "load an index before preparing workspace");
+    TRY(validate_shape(E, max_q, max_topk, max_nprobe));
+    HIPCHK(hipSetDevice(E->device));
+    release_workspace(E);
+    const uint64_t nb = 2 * E->nl;
+    const uint64_t np = max_q * max_nprobe;
+    const uint64_t depth = std::min(vanguard_size, max_nprobe);
+    const uint64_t seed_words = (E->max_cluster + 31) / 32;
+    auto alloc_all = [&]() -> int {
+        TRY(dalloc(E, E->d_raw, max_q * E->dim));
+        TRY(dalloc(E, E->d_qrot, max_q * E->P));
+        TRY(dalloc(E, E->d_k1, max_q));
+        TRY(dalloc(E, E->d_kb, max_q));
+        TRY(dalloc(E, E->d_qnorm, max_q));
+        TRY(dalloc(E, E->d_qwidth, max_q));
+        TRY(dalloc(E, E->d_planes, max_q * kBq * E->W));
+        TRY(dalloc(E, E->d_dist, max_q * E->nl));
+        TRY(dalloc(E, E->d_pidx, np));
+        TRY(dalloc(E, E->d_gadd, np));
+        TRY(dalloc(E, E->d_gerr, np));
+        TRY(dalloc(E, E->d_bcount, nb));
+        TRY(dalloc(E, E->d_bcursor, nb));
+        TRY(dalloc(E, E->d_boff, nb + 1));
+        TRY(dalloc(E, E->d_uoff, nb + 1));
+        TRY(dalloc(E, E->d_nunits, 2));
+        TRY(dalloc(E, E->d_cursor, kNumXcd));
+        TRY(dalloc(E, E->d_stats, 3));
+        TRY(dalloc(E, E->d_pairs, np));
+        TRY(dalloc(E, E->d_units, np));
+        TRY(dalloc(E, E->d_thr_snap, max_q));
+        TRY(dalloc(E, E->d_seed, std::max<uint64_t>(1, max_q * depth * seed_words)));
+        TRY(halloc(E, E->h_qrot, max_q * E->P, hipHostMallocDefault));
+        TRY(halloc(E, E->h_kb, max_q, hipHostMallocDefault));
+        TRY(halloc(E, E->h_gadd, np, hipHostMallocDefault));
+        // ring, progress, thresholds: host-coherent so GPU stores and host stores are seen
+        // by the other side while kernels run (reference cudaHostAllocMapped, hybrid.cu:192-199)
+        const unsigned coherent = hipHostMallocMapped | hipHostMallocCoherent;
+        TRY(halloc(E, E->h_items, E->qcap, coherent));
+        TRY(halloc(E, E->h_progress, 1, coherent));
+        TRY(halloc(E, E->h_thr, max_q, coherent));
+        TRY(halloc(E, E->h_thr_stage, max_q, hipHostMallocDefault));
+        TRY(halloc(E, E->h_abort, 1, coherent));
+        TRY(dalloc(E, E->d_produced, 1));
+        TRY(dalloc(E, E->d_cached_limit, 1));
+        TRY(dalloc(E, E->d_spill_count, 1));
+        TRY(dalloc(E, E->d_refresh, 1));
+        TRY(dalloc(E, E->d_overflow, 1));
+        TRY(dalloc(E, E->d_stalled, 1));
+        TRY(dalloc(E, E->d_spill, std::max<uint64_t>(1, E->spill_cap)));
+        return CORA_OK;
+    };
+    const int rc = alloc_all();
+    if (rc != CORA_OK) {
+        const std::string msg = E->err;
+        release_workspace(E);
+        E->err = msg;
+        return rc;
+    }
+    memset(E->h_items, 0xFF, E->qcap * sizeof(uint4));
+    new (E->h_progress) ProgressDev{};
+    for (uint64_t i = 0; i < max_q; ++i)
+        E->h_thr[i] = FLT_MAX;
+    *E->h_abort = 0;
+    launch_queue_reset(queue_dev(E), E->stream);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipStreamSynchronize(E->stream));
+    E->ws_q = max_q;
+    E->ws_k = max_topk;
+    E->ws_np = max_nprobe;
+    E->ws_van = depth;
+    E->seed_words = seed_words;
+    E->ring_dirty = false;
+    E->ws = true;
+    return CORA_OK;
+}
+
+int cora_gpu_free_workspace(cora_gpu_engine *E) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    (void)hipSetDevice(E->device);
+    release_workspace(E);
+    return CORA_OK;
+}
+
+int cora_gpu_queue_view(cora_gpu_engine *E, cora_queue_view *out) {
+    if (!E || !out)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->ws)
+        return fail(E, CORA_ERR_LOGIC, "prepare workspace before searching");
+    out->items = E->h_items;
+    out->progress = E->h_progress;
+    out->capacity = E->qcap;
+    out->thresholds = E->h_thr;
+    out->abort_flag = E->h_abort;
+    return CORA_OK;
+}
+
+int cora_gpu_reset(cora_gpu_engine *E, const float *h_queries, uint64_t nq) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->ws)
+        return fail(E, CORA_ERR_LOGIC, "prepare workspace before searching");
+    if (nq == 0 || nq > E->ws_q)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "search shape exceeds the prepared workspace");
+    if (!h_queries)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "missing queries");
+    HIPCHK(hipSetDevice(E->device));
+    HIPCHK(hipStreamSynchronize(E->stream));
+    if (E->ring_dirty) {
+        memset(E->h_items, 0xFF, E->qcap * sizeof(uint4));
+        E->ring_dirty = false;
+    }
+    HIPCHK(hipMemcpyAsync(E->d_raw, h_queries, nq * E->dim * 4, hipMemcpyHostToDevice, E->stream));
+    launch_queue_reset(queue_dev(E), E->stream);
+    HIPCHK(hipGetLastError());
+    new (E->h_progress) ProgressDev{};
+    for (uint64_t i = 0; i < nq; ++i)
+        E->h_thr[i] = FLT_MAX;
+    *E->h_abort = 0;
+    E->launched = false;
+    return CORA_OK;
+}
+
+int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
+    if (!E || !a)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->ws)
+        return fail(E, CORA_ERR_LOGIC, "prepare workspace before searching");
+    if (a->num_queries == 0 || a->num_queries > E->ws_q || a->topk == 0 || a->topk > E->ws_k ||
+        a->nprobe == 0 || a->nprobe > E->ws_np)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "search shape exceeds the prepared workspace");
+    if (a->batch_q < 1 || a->batch_q > (uint32_t)kMaxBatchQ)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "invalid batch-q (expected 1..8)");
+    const uint64_t want_depth = std::min<uint64_t>(a->vanguard, a->nprobe);
+    if (want_depth > E->ws_van)
+        return fail(E, CORA_ERR_LOGIC, "prepare workspace again before increasing vanguard size");
+    HIPCHK(hipSetDevice(E->device));
+    const uint32_t nq = a->num_queries, np = a->nprobe;
+    const uint32_t keep = std::max<uint32_t>(a->topk, 20u);
+    const uint32_t depth = keep <= (uint32_t)kMaxVanguardKeep ? (uint32_t)want_depth : 0u;
+    const uint32_t batch = (a->flags & CORA_FLAG_CROSS_QUERY_REUSE) ? a->batch_q : 1u;
+    const bool frozen = (a->flags & CORA_FLAG_FROZEN_THRESHOLDS) != 0;
+    const bool timing = (a->flags & CORA_FLAG_FILTER_TIMING) != 0;
+    E->last = *a;
+    E->last_depth = depth;
+    E->last_batch = batch;
+    E->last_timing = timing;
+    hipStream_t s = E->stream;
+    const uint32_t P = (uint32_t)E->P;
+
+    // query preparation (hybrid.cu:436-463)
+    launch_rotate(E->d_raw, E->d_rot, E->d_qrot, nq, (uint32_t)E->dim, P, s);
+    launch_query_prep(E->d_qrot, nq, P, (uint32_t)E->ex_bits, E->d_k1, E->d_kb, E->d_qnorm,
+                      E->d_qwidth, E->d_planes, s);
+    HIPCHK(hipEventRecord(E->ev_prep, s));
+    HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_prep, 0));
+    HIPCHK(hipMemcpyAsync(E->h_qrot, E->d_qrot, (size_t)nq * P * 4, hipMemcpyDeviceToHost,
+                          E->stream_d2h));
+    HIPCHK(hipMemcpyAsync(E->h_kb, E->d_kb, (size_t)nq * 4, hipMemcpyDeviceToHost, E->stream_d2h));
+    // coarse probing (hybrid.cu:465-498)
+    launch_dist_gemm(E->d_qrot, E->d_qnorm, E->d_cent, E->d_cnorm, nq, (uint32_t)E->nl, P,
+                     E->d_dist, s);
+    launch_select(E->d_dist, nq, (uint32_t)E->nl, np, E->d_pidx, s);
+    launch_probe_refine(E->d_qrot, E->d_cent, E->d_pidx, nq, np, P, E->metric, E->d_gadd,
+                        E->d_gerr, s);
+    HIPCHK(hipEventRecord(E->ev_probe, s));
+    HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_probe, 0));
+    HIPCHK(hipMemcpyAsync(E->h_gadd, E->d_gadd, (size_t)nq * np * 4, hipMemcpyDeviceToHost,
+                          E->stream_d2h));
+    // pair scheduling (hybrid.cu:504-508)
+    launch_build_pairs(E->d_pidx, E->d_meta, nq, np, (uint32_t)E->nl, depth, batch,
+                       P / 8 + 12, E->d_bcount, E->d_bcursor, E->d_boff, E->d_uoff, E->d_pairs,
+                       E->d_units, E->d_nunits, E->d_stats, s);
+    if (frozen) {
+        memcpy(E->h_thr_stage, E->h_thr, (size_t)nq * 4);
+        HIPCHK(hipMemcpyAsync(E->d_thr_snap, E->h_thr_stage, (size_t)nq * 4, hipMemcpyHostToDevice, s));
+    }
+    const ScanParams p = scan_params(E, depth, keep, frozen);
+    if (timing)
+        HIPCHK(hipEventRecord(E->ev_f0, s));
+    if (depth > 0) {
+        launch_fill_u32(E->d_seed, 0u, (size_t)nq * depth * E->seed_words, s);
+        launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
+        launch_vanguard_seed(p, E->W, kVanguardGrid, s);
+    }
+    launch_cursor_init(E->d_cursor, E->d_nunits, 1, s);
+    if (timing)
+        HIPCHK(hipEventRecord(E->ev_s0, s));
+    launch_scan(p, E->W, batch, 0, kScanGrid, s);
+    if (timing)
+        HIPCHK(hipEventRecord(E->ev_s1, s));
+    if (depth > 0) {
+        launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
+        launch_scan(p, E->W, 1, 1, kScanGrid, s);
+    }
+    if (timing)
+        HIPCHK(hipEventRecord(E->ev_f1, s));
+    launch_finish(queue_dev(E), kDrainMaxSpins, s);
+    HIPCHK(hipGetLastError());
+    E->launched = true;
+    return CORA_OK;
+}
+
+int cora_gpu_wait_host_inputs(cora_gpu_engine *E, const float **rq, const float **kb,
+                              const float **gadd) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->launched)
+        return fail(E, CORA_ERR_LOGIC, "no search launched");
+    HIPCHK(hipSetDevice(E->device));
+    HIPCHK(hipStreamSynchronize(E->stream_d2h));
+    if (rq)
+        *rq = E->h_qrot;
+    if (kb)
+        *kb = E->h_kb;
+    if (gadd)
+        *gadd = E->h_gadd;
+    return CORA_OK;
+}
+
+int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->launched)
+        return fail(E, CORA_ERR_LOGIC, "no search launched");
+    HIPCHK(hipSetDevice(E->device));
+    HIPCHK(hipStreamSynchronize(E->stream));
+    HIPCHK(hipStreamSynchronize(E->stream_d2h));
+    unsigned long long stats[3] = {0, 0, 0};
+    int stalled = 0;
+    HIPCHK(hipMemcpy(stats, E->d_stats, sizeof(stats), hipMemcpyDeviceToHost));
+    HIPCHK(hipMemcpy(&stalled, E->d_stalled, sizeof(int), hipMemcpyDeviceToHost));
+    cora_search_stats out{};
+    out.produced = __atomic_load_n(&E->h_progress->produced, __ATOMIC_ACQUIRE);
+    out.spilled = __atomic_load_n(&E->h_progress->spilled, __ATOMIC_ACQUIRE);
+    const int overflow = __atomic_load_n(&E->h_progress->overflow, __ATOMIC_ACQUIRE);
+    out.stalled = stalled;
+    out.overflow = overflow && !stalled;
+    out.scan_bytes = stats[0];
+    out.scan_units = stats[1];
+    out.scan_vectors = stats[2];
+    if (E->last_timing) {
+        HIPCHK(hipEventElapsedTime(&out.filter_ms, E->ev_f0, E->ev_f1));
+        HIPCHK(hipEventElapsedTime(&out.scan_ms, E->ev_s0, E->ev_s1));
+    }
+    if (st)
+        *st = out;
+    if (overflow || stalled) {
+        memset(E->h_items, 0xFF, E->qcap * sizeof(uint4));
+        E->ring_dirty = false;
+        if (stalled)
+            return fail(E, CORA_ERR_QUEUE_STALLED,
+                        "candidate queue drain stopped waiting for the CPU consumer");
+        return fail(E, CORA_ERR_SPILL_EXHAUSTED,
+                    "HBM queue spill capacity exhausted; increase --queue-capacity or "
+                    "--queue-spill-capacity, or reduce --query-chunk.");
+    }
+    return CORA_OK;
+}
+
+int cora_gpu_capture_thresholds(cora_gpu_engine *E, float *out, uint64_t nq) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->ws)
+        return fail(E, CORA_ERR_LOGIC, "prepare workspace before searching");
+    if (nq == 0 || nq > E->ws_q)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "search shape exceeds the prepared workspace");
+    if (!out)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "missing threshold output");
+    memcpy(out, E->h_thr, nq * 4);
+    return CORA_OK;
+}
+
+int cora_gpu_seed_thresholds(cora_gpu_engine *E, const float *in, uint64_t nq) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->ws)
+        return fail(E, CORA_ERR_LOGIC, "prepare workspace before searching");
+    if (nq == 0 || nq > E->ws_q)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "search shape exceeds the prepared workspace");
+    if (!in)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "missing threshold input");
+    memcpy(E->h_thr, in, nq * 4);
+    return CORA_OK;
+}
+
+int cora_gpu_index_info(const cora_gpu_engine *E, uint64_t *num_vecs, uint64_t *dim,
+                        uint64_t *padded_dim, uint64_t *n_centroids, uint64_t *max_cluster) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (num_vecs)
+        *num_vecs = E->N;
+    if (dim)
+        *dim = E->dim;
+    if (padded_dim)
+        *padded_dim = E->P;
+    if (n_centroids)
+        *n_centroids = E->nl;
+    if (max_cluster)
+        *max_cluster = E->max_cluster;
+    return E->loaded ? CORA_OK : CORA_ERR_LOGIC;
+}
+
+int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes) {
+    if (!E || !dst)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->launched)
+        return fail(E, CORA_ERR_LOGIC, "no search launched");
+    HIPCHK(hipSetDevice(E->device));
+    HIPCHK(hipStreamSynchronize(E->stream));
+    const uint64_t nq = E->last.num_queries, np = E->last.nprobe;
+    const void *src = nullptr;
+    uint64_t size = 0;
+    switch (which) {
+    case CORA_DBG_ROTATED_QUERIES: src = E->d_qrot; size = nq * E->P * 4; break;
+    case CORA_DBG_K1XSUMQ: src = E->d_k1; size = nq * 4; break;
+    case CORA_DBG_KBXSUMQ: src = E->d_kb; size = nq * 4; break;
+    case CORA_DBG_Q_WIDTH: src = E->d_qwidth; size = nq * 4; break;
+    case CORA_DBG_Q_PLANES: src = E->d_planes; size = nq * kBq * E->W * 4; break;
+    case CORA_DBG_PROBE_IDX: src = E->d_pidx; size = nq * np * 4; break;
+    case CORA_DBG_PROBE_GADD: src = E->d_gadd; size = nq * np * 4; break;
+    case CORA_DBG_PROBE_GERR: src = E->d_gerr; size = nq * np * 4; break;
+    case CORA_DBG_PAIRS: {
+        if (bytes != nq * np * 12)
+            return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_read: size mismatch");
+        std::vector<Pair> pairs(nq * np);
+        HIPCHK(hipMemcpy(pairs.data(), E->d_pairs, pairs.size() * sizeof(Pair), hipMemcpyDeviceToHost));
+        int32_t *o = static_cast<int32_t *>(dst);
+        for (size_t i = 0; i < pairs.size(); ++i) {
+            o[3 * i] = (int32_t)pairs[i].cluster;
+            o[3 * i + 1] = (int32_t)(pairs[i].word0 & 0xFFFFu);
+            o[3 * i + 2] = (int32_t)(pairs[i].word0 >> 16);
+        }
+        return CORA_OK;
+    }
+    default: return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_read: unknown array");
+    }
+    if (bytes != size)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_read: size mismatch");
+    HIPCHK(hipMemcpy(dst, src, size, hipMemcpyDeviceToHost));
+    return CORA_OK;
+}
+
+int cora_gpu_debug_dense(cora_gpu_engine *E, int32_t *out_ip, float *out_low, uint64_t cap) {
+    if (!E || !out_ip || !out_low)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->launched)
+        return fail(E, CORA_ERR_LOGIC, "no search launched");
+    const uint64_t need = (uint64_t)E->last.num_queries * E->last.nprobe * E->max_cluster;
+    if (cap < need)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_dense: output too small");
+    HIPCHK(hipSetDevice(E->device));
+    HIPCHK(hipStreamSynchronize(E->stream));
+    int32_t *d_ip = nullptr;
+    float *d_low = nullptr;
+    int rc = dalloc(E, d_ip, need);
+    if (rc == CORA_OK)
+        rc = dalloc(E, d_low, need);
+    if (rc == CORA_OK) {
+        ScanParams p = scan_params(E, E->last_depth, 0, true);
+        p.dbg_ip = d_ip;
+        p.dbg_low = d_low;
+        p.dbg_stride = (uint32_t)E->max_cluster;
+        hipError_t r = hipMemcpy(d_ip, out_ip, need * 4, hipMemcpyHostToDevice);
+        if (r == hipSuccess)
+            r = hipMemcpy(d_low, out_low, need * 4, hipMemcpyHostToDevice);
+        for (uint32_t set = 0; set < 2 && r == hipSuccess; ++set) {
+            launch_cursor_init(E->d_cursor, E->d_nunits, set, E->stream);
+            launch_scan_set(p, E->W, 2, kScanGrid, set, E->stream);
+            r = hipGetLastError();
+            if (r == hipSuccess)
+                r = hipStreamSynchronize(E->stream);
+        }
+        if (r == hipSuccess)
+            r = hipMemcpy(out_ip, d_ip, need * 4, hipMemcpyDeviceToHost);
+        if (r == hipSuccess)
+            r = hipMemcpy(out_low, d_low, need * 4, hipMemcpyDeviceToHost);
+        if (r != hipSuccess)
+            rc = fail(E, CORA_ERR_RUNTIME, std::string("debug_dense: ") + hipGetErrorString(r));
+    }
+    dfree(d_ip);
+    dfree(d_low);
+    return rc;
+}
+
+}  // extern "C"

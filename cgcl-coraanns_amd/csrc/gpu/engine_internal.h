@@ -1,0 +1,144 @@
+// Internal declarations shared by the engine's HIP translation units.
+//
+// HBM layout of the index ("tile layout"): the vectors of each cluster are grouped in
+// tiles of 64 (one vector per lane of a wave64). A tile is
+//     codes   : ceil(W/4) groups; group g holds words [4g, 4g+4) of all 64 vectors as
+//               [lane][4 x u32] (16 B per lane, one 128-bit load per lane per group);
+//               when W % 4 == 2 the last group is [lane][2 x u32] (8 B per lane)
+//     factors : f_add[64], f_rescale[64], f_error[64] (f32, SoA)
+// where W = padded_dim / 32 and dimension 32w+l is bit l of word w (LSB first, the
+// order a wave64 ballot produces). Tile bytes = 8*P + 768. Lanes past the end of a
+// cluster hold zero codes and are masked by the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cora {
+
+constexpr int kTileVectors = 64;
+constexpr int kBq = 8;             // query quantisation bits (reference RABITQ_BQ)
+constexpr int kMaxBatchQ = 8;      // same-cluster pairs per scan pass
+constexpr int kMaxVanguardKeep = 1024;
+constexpr int kVanguardMaxCluster = 8192;  // LDS-resident lows in the vanguard seed pass
+constexpr int kSelectMaxProbe = 4096;       // top-nprobe select held in LDS
+constexpr uint32_t kNumXcd = 8;
+
+struct ClusterMeta {
+    uint32_t start;      // first global (cluster-order) vector index
+    uint32_t n;          // vectors in the cluster
+    uint32_t tile_base;  // first tile index
+    uint32_t pad;
+};
+
+// One cluster pass of the scan: up to batch_q pairs that probe the same cluster.
+struct Unit {
+    uint32_t cluster;
+    uint32_t pair_begin;
+    uint32_t count;
+    uint32_t bucket;
+};
+
+// Scheduled (query, probe) pair: word0 = probe << 16 | query (the Candidate's first
+// word), cluster alongside.
+struct Pair {
+    uint32_t word0;
+    uint32_t cluster;
+};
+
+// Byte-compatible with coraanns::queue::Progress (fields 64-byte aligned).
+struct alignas(64) ProgressDev {
+    alignas(64) unsigned long long released;
+    alignas(64) unsigned long long produced;
+    alignas(64) unsigned long long spilled;
+    alignas(64) int done;
+    alignas(64) int overflow;
+};
+static_assert(sizeof(ProgressDev) == 320, "Progress layout");
+
+struct SpillRecord {
+    uint4 item;
+    unsigned long long position;
+    unsigned long long pad;
+};
+
+struct QueueDev {
+    uint4 *items;                      // host-coherent ring
+    ProgressDev *progress;             // host-coherent
+    unsigned long long capacity;
+    unsigned long long mask;
+    unsigned long long *produced;      // HBM reservation counter
+    unsigned long long *cached_limit;  // HBM copy of released + capacity
+    int *refresh_flag;                 // HBM, one refresher at a time
+    SpillRecord *spill;                // HBM
+    unsigned long long *spill_count;
+    unsigned long long spill_capacity;
+    int *spill_overflow;
+    int *abort_flag;                   // host-coherent
+    int *stalled;                      // HBM
+};
+
+struct ScanParams {
+    const uint8_t *tiles;
+    const ClusterMeta *meta;
+    const uint32_t *qplanes;  // [nq][8][W]
+    const float *qwidth;      // [nq]
+    const float *k1;          // [nq]
+    const float *pgadd;       // [nq][nprobe]
+    const float *pgerr;       // [nq][nprobe]
+    const Pair *pairs;
+    const Unit *units;
+    const uint32_t *num_units;   // device scalar
+    uint32_t *unit_cursor;       // [kNumXcd] dynamic scheduling cursors
+    const float *thresholds;     // live host-coherent array or a device snapshot
+    int thresholds_live;
+    uint32_t nprobe;
+    uint32_t vanguard;
+    uint32_t keep;               // vanguard seed count per pair
+    uint32_t tile_bytes;
+    uint32_t P;
+    uint32_t seed_words;         // u32 words of seed bitmask per vanguard pair
+    uint32_t *seed_bits;         // [nq * vanguard][seed_words]
+    QueueDev queue;
+    // dense debug output
+    int32_t *dbg_ip;
+    float *dbg_low;
+    uint32_t dbg_stride;         // max cluster size
+};
+
+// ---- launchers (each defined in the translation unit holding its kernel) ----
+void launch_repack(const uint32_t *ref_words, const float *ref_factors, const ClusterMeta *meta,
+                   uint32_t nlist, uint32_t W, uint8_t *tiles, uint32_t tile_bytes,
+                   hipStream_t s);
+void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint32_t dim,
+                   uint32_t P, hipStream_t s);
+void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,
+                       float *kb, float *qnorm, float *qwidth, uint32_t *qplanes, hipStream_t s);
+void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s);
+void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,
+                      uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s);
+void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,
+                   hipStream_t s);
+void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,
+                         uint32_t nprobe, uint32_t P, int metric, float *gadd, float *gerr,
+                         hipStream_t s);
+void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint32_t nq,
+                        uint32_t nprobe, uint32_t nlist, uint32_t vanguard, uint32_t batch_q,
+                        uint32_t bytes_per_vector, uint32_t *bucket_count, uint32_t *bucket_cursor,
+                        uint32_t *bucket_offset, uint32_t *unit_offset, Pair *pairs, Unit *units,
+                        uint32_t *num_units /*[2]: vanguard, far*/,
+                        unsigned long long *scan_stats /*[3]*/, hipStream_t s);
+void launch_fill_u32(uint32_t *p, uint32_t value, size_t n, hipStream_t s);
+void launch_fill_u64(unsigned long long *p, unsigned long long value, size_t n, hipStream_t s);
+void launch_queue_reset(QueueDev q, hipStream_t s);
+void launch_cursor_init(uint32_t *cursor, const uint32_t *num_units, uint32_t set, hipStream_t s);
+// kind: 0 = far pairs (publish below cutoff), 1 = vanguard recovery, 2 = dense debug
+int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, uint32_t grid,
+                hipStream_t s);
+// dense debug pass over one unit set (0 = vanguard units, 1 = far units)
+int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t grid, uint32_t set,
+                    hipStream_t s);
+int launch_vanguard_seed(const ScanParams &p, uint32_t W, uint32_t grid, hipStream_t s);
+void launch_finish(QueueDev q, unsigned long long max_spins, hipStream_t s);
+
+}  // namespace cora

@@ -1,0 +1,359 @@
+// Query preparation and coarse probing kernels (gfx950, wave64).
+//
+//   rotate        Q' = Q . R                            (reference hybrid.cu:436-440)
+//   query_prep    k1/kb sums, ||q'||^2, Bq=8 planes     (query_kernels.cuh:73-103,117-197)
+//   dist_gemm     ||q'||^2 + ||c'||^2 - 2 q'.c'          (hybrid.cu:465-477, query_kernels.cuh:10-64)
+//   select        per-query nprobe smallest, ascending, ties by cluster id (hybrid.cu:485-493)
+//   probe_refine  exact ||q'-c'||^2 and <q',c'> of the selected probes -> g_add, g_error
+//                 (query.hpp:537-545: L2 g_add = ||q'-c'||^2, IP g_add = -<q',c'>)
+#include <float.h>
+#include <math.h>
+
+#include "engine_internal.h"
+
+namespace cora {
+namespace {
+
+constexpr int kTile = 64;
+constexpr int kTileK = 16;
+
+// C = A . B (row-major A [M][K], B [K][N]) when TRANS_B is false; with TRANS_B the second
+// operand is given as Bt [N][K] and the epilogue forms an L2 distance
+// an[m] + bn[n] - 2 * (A . Bt^T)[m][n].
+template <bool TRANS_B>
+__global__ __launch_bounds__(256) void gemm_kernel(const float *__restrict__ A,
+                                                   const float *__restrict__ B,
+                                                   float *__restrict__ C, uint32_t M, uint32_t N,
+                                                   uint32_t K, const float *__restrict__ an,
+                                                   const float *__restrict__ bn) {
+    __shared__ float As[kTileK][kTile + 4];
+    __shared__ float Bs[kTileK][kTile + 4];
+    const int tid = threadIdx.x;
+    const int tx = tid % 16, ty = tid / 16;
+    const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+    float acc[4][4] = {};
+    for (uint32_t k0 = 0; k0 < K; k0 += kTileK) {
+        // A tile: 64 rows x 16 k, 4 elements per thread
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int e = tid + r * 256;
+            const int row = e / kTileK, kk = e % kTileK;
+            const uint32_t gm = m0 + row, gk = k0 + kk;
+            As[kk][row] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int e = tid + r * 256;
+            if (TRANS_B) {
+                const int col = e / kTileK, kk = e % kTileK;
+                const uint32_t gn = n0 + col, gk = k0 + kk;
+                Bs[kk][col] = (gn < N && gk < K) ? B[(size_t)gn * K + gk] : 0.0f;
+            } else {
+                const int kk = e / kTile, col = e % kTile;
+                const uint32_t gn = n0 + col, gk = k0 + kk;
+                Bs[kk][col] = (gn < N && gk < K) ? B[(size_t)gk * N + gn] : 0.0f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kTileK; ++kk) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] = As[kk][ty * 4 + i];
+                b[i] = Bs[kk][tx * 4 + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t gm = m0 + ty * 4 + i;
+        if (gm >= M)
+            continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t gn = n0 + tx * 4 + j;
+            if (gn >= N)
+                continue;
+            float v = acc[i][j];
+            if (TRANS_B)
+                v = an[gm] + bn[gn] - 2.0f * v;
+            C[(size_t)gm * N + gn] = v;
+        }
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// One wave per query. Each lane owns dimensions lane + 64*i.
+__global__ __launch_bounds__(64) void query_prep_kernel(const float *__restrict__ qrot,
+                                                        uint32_t P, uint32_t ex_bits,
+                                                        float *__restrict__ k1,
+                                                        float *__restrict__ kb,
+                                                        float *__restrict__ qnorm,
+                                                        float *__restrict__ qwidth,
+                                                        uint32_t *__restrict__ planes) {
+    const uint32_t q = blockIdx.x;
+    const int lane = threadIdx.x;
+    const float *row = qrot + (size_t)q * P;
+    const uint32_t groups = P / 64;  // P is a multiple of 64
+    float v[16];
+    float sum = 0.0f, sq = 0.0f, amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        v[i] = (uint32_t)i < groups ? row[lane + 64 * i] : 0.0f;
+        sum += v[i];
+        sq = fmaf(v[i], v[i], sq);
+        amax = fmaxf(amax, fabsf(v[i]));
+    }
+    sum = wave_sum(sum);
+    sq = wave_sum(sq);
+    amax = wave_max(amax);
+    // Symmetric Bq=8 quantisation, IEEE single precision with round-half-even.
+    const float width = fmaxf(amax / 127.0f, 1e-30f);
+    const float inv = 1.0f / width;
+    const uint32_t W = P / 32;
+    uint32_t *out = planes + (size_t)q * kBq * W;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if ((uint32_t)i >= groups)
+            break;
+        int qi = (int)rintf(v[i] * inv);
+        qi = max(-128, min(127, qi));
+        const uint32_t u = (uint32_t)qi & 0xFFu;
+#pragma unroll
+        for (int j = 0; j < kBq; ++j) {
+            const unsigned long long m = __ballot((u >> j) & 1u);
+            if (lane == 0) {
+                out[j * W + 2 * i] = (uint32_t)m;
+                out[j * W + 2 * i + 1] = (uint32_t)(m >> 32);
+            }
+        }
+    }
+    if (lane == 0) {
+        const float cb = -(float)((1u << (ex_bits + 1)) - 1u) / 2.0f;
+        k1[q] = sum * -0.5f;
+        kb[q] = sum * cb;
+        qnorm[q] = sq;
+        qwidth[q] = width;
+    }
+}
+
+__global__ __launch_bounds__(64) void row_norms_kernel(const float *__restrict__ x, uint32_t P,
+                                                       float *__restrict__ out) {
+    const float *row = x + (size_t)blockIdx.x * P;
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < P; i += 64)
+        s = fmaf(row[i], row[i], s);
+    s = wave_sum(s);
+    if (threadIdx.x == 0)
+        out[blockIdx.x] = s;
+}
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+constexpr int kSelThreads = 256;
+
+__device__ void block_exclusive_scan2(uint32_t &a, uint32_t &b, uint32_t *sa, uint32_t *sb,
+                                      uint32_t &total_a, uint32_t &total_b) {
+    const int t = threadIdx.x;
+    sa[t] = a;
+    sb[t] = b;
+    __syncthreads();
+    for (int o = 1; o < kSelThreads; o <<= 1) {
+        uint32_t xa = t >= o ? sa[t - o] : 0, xb = t >= o ? sb[t - o] : 0;
+        __syncthreads();
+        sa[t] += xa;
+        sb[t] += xb;
+        __syncthreads();
+    }
+    total_a = sa[kSelThreads - 1];
+    total_b = sb[kSelThreads - 1];
+    a = sa[t] - a;
+    b = sb[t] - b;
+    __syncthreads();
+}
+
+// Per query: radix-select the key of the nprobe-th smallest distance (4 x 8-bit digits),
+// gather every smaller distance and the lowest-index ties in index order, then bitonic
+// sort (key, cluster) ascending in LDS.
+__global__ __launch_bounds__(kSelThreads) void select_kernel(const float *__restrict__ dist,
+                                                             uint32_t nl, uint32_t k,
+                                                             uint32_t kpow2,
+                                                             int32_t *__restrict__ out) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_prefix, s_remaining;
+    __shared__ uint32_t sa[kSelThreads], sb[kSelThreads];
+    extern __shared__ unsigned long long sel[];
+    const float *row = dist + (size_t)blockIdx.x * nl;
+    const int t = threadIdx.x;
+    uint32_t prefix = 0, pmask = 0;
+    if (t == 0) {
+        s_prefix = 0;
+        s_remaining = k;
+    }
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[t] = 0;
+        __syncthreads();
+        for (uint32_t i = t; i < nl; i += kSelThreads) {
+            const uint32_t key = order_key(row[i]);
+            if ((key & pmask) == prefix)
+                atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (t == 0) {
+            uint32_t rem = s_remaining, cum = 0, d = 0;
+            for (; d < 256; ++d) {
+                if (cum + hist[d] >= rem)
+                    break;
+                cum += hist[d];
+            }
+            s_remaining = rem - cum;
+            s_prefix = prefix | (d << shift);
+        }
+        __syncthreads();
+        prefix = s_prefix;
+        pmask |= 255u << shift;
+    }
+    const uint32_t kth = prefix;
+    const uint32_t take_eq = s_remaining;
+    const uint32_t chunk = (nl + kSelThreads - 1) / kSelThreads;
+    const uint32_t begin = min(nl, t * chunk), end = min(nl, begin + chunk);
+    uint32_t nless = 0, neq = 0;
+    for (uint32_t i = begin; i < end; ++i) {
+        const uint32_t key = order_key(row[i]);
+        nless += key < kth;
+        neq += key == kth;
+    }
+    uint32_t tot_less, tot_eq;
+    block_exclusive_scan2(nless, neq, sa, sb, tot_less, tot_eq);
+    for (uint32_t i = begin; i < end; ++i) {
+        const uint32_t key = order_key(row[i]);
+        if (key < kth) {
+            sel[nless++] = ((unsigned long long)key << 32) | i;
+        } else if (key == kth) {
+            if (neq < take_eq)
+                sel[tot_less + neq] = ((unsigned long long)key << 32) | i;
+            ++neq;
+        }
+    }
+    for (uint32_t i = k + t; i < kpow2; i += kSelThreads)
+        sel[i] = ~0ull;
+    __syncthreads();
+    for (uint32_t size = 2; size <= kpow2; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = t; i < kpow2; i += kSelThreads) {
+                const uint32_t j = i ^ stride;
+                if (j > i) {
+                    const bool asc = (i & size) == 0;
+                    const unsigned long long a = sel[i], b = sel[j];
+                    if ((a > b) == asc) {
+                        sel[i] = b;
+                        sel[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (uint32_t i = t; i < k; i += kSelThreads)
+        out[(size_t)blockIdx.x * k + i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
+}
+
+// One block (4 waves) per query; each wave takes probes p = wave, wave + 4, ...
+__global__ __launch_bounds__(256) void probe_refine_kernel(const float *__restrict__ qrot,
+                                                           const float *__restrict__ cent,
+                                                           const int32_t *__restrict__ idx,
+                                                           uint32_t nprobe, uint32_t P, int metric,
+                                                           float *__restrict__ gadd,
+                                                           float *__restrict__ gerr) {
+    const uint32_t q = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t groups = P / 64;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        v[i] = (uint32_t)i < groups ? qrot[(size_t)q * P + lane + 64 * i] : 0.0f;
+    for (uint32_t p = wave; p < nprobe; p += 4) {
+        const int32_t c = idx[(size_t)q * nprobe + p];
+        const float *crow = cent + (size_t)c * P;
+        float l2 = 0.0f, ip = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if ((uint32_t)i >= groups)
+                break;
+            const float cv = crow[lane + 64 * i];
+            const float d = v[i] - cv;
+            l2 = fmaf(d, d, l2);
+            ip = fmaf(v[i], cv, ip);
+        }
+        l2 = wave_sum(l2);
+        ip = wave_sum(ip);
+        if (lane == 0) {
+            gadd[(size_t)q * nprobe + p] = metric == 0 ? l2 : -ip;
+            gerr[(size_t)q * nprobe + p] = sqrtf(fmaxf(l2, 0.0f));
+        }
+    }
+}
+
+}  // namespace
+
+void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint32_t dim,
+                   uint32_t P, hipStream_t s) {
+    dim3 grid((P + kTile - 1) / kTile, (nq + kTile - 1) / kTile);
+    gemm_kernel<false><<<grid, 256, 0, s>>>(q, R, out, nq, P, dim, nullptr, nullptr);
+}
+
+void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,
+                       float *kb, float *qnorm, float *qwidth, uint32_t *qplanes, hipStream_t s) {
+    query_prep_kernel<<<nq, 64, 0, s>>>(qrot, P, ex_bits, k1, kb, qnorm, qwidth, qplanes);
+}
+
+void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s) {
+    if (rows)
+        row_norms_kernel<<<rows, 64, 0, s>>>(x, P, out);
+}
+
+void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,
+                      uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s) {
+    dim3 grid((nl + kTile - 1) / kTile, (nq + kTile - 1) / kTile);
+    gemm_kernel<true><<<grid, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
+}
+
+void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,
+                   hipStream_t s) {
+    uint32_t kp = 1;
+    while (kp < nprobe)
+        kp <<= 1;
+    select_kernel<<<nq, kSelThreads, kp * sizeof(unsigned long long), s>>>(dist, nl, nprobe, kp,
+                                                                            idx);
+}
+
+void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,
+                         uint32_t nprobe, uint32_t P, int metric, float *gadd, float *gerr,
+                         hipStream_t s) {
+    probe_refine_kernel<<<nq, 256, 0, s>>>(qrot, cent, idx, nprobe, P, metric, gadd, gerr);
+}
+
+}  // namespace cora

@@ -1,0 +1,663 @@
+// RaBitQ 1-bit scan, shared-threshold filtering and the device side of the GPU->CPU
+// candidate ring (gfx950, wave64).
+//
+// Estimator (reference Bitwise producer, filter_kernels.cuh:79-114):
+//     ip_int   = sum_{j<7} 2^j popc(x & q_j) - 2^7 popc(x & q_7)     (x: sign code words,
+//                q_j: bit plane j of the Bq=8 two's-complement query; = sum_i b_i*qint_i)
+//     exact_ip = width * ip_int
+//     low      = f_add + g_add + f_rescale * (exact_ip + k1) - f_error * g_error
+// A vector of a (query, probe) pair becomes a candidate when low < threshold[query]
+// (filter_kernels.cuh:116, 696, 754). Unlike the reference Bitwise producer there is
+// no 2*topk cap per pair and no fixed-size shared output array.
+//
+// Work decomposition: one wave per workgroup; the waves pull scan units (one cluster
+// pass serving up to batch_q pairs) from eight per-XCD cursors over eight contiguous
+// unit ranges (workgroup i runs on XCD i % 8), stealing from the next range once
+// their own is exhausted, so the passes over one cluster stay on one XCD's L2. Each
+// lane evaluates one vector of a 64-vector tile: 128-bit code loads, factor loads from
+// the tile's SoA block, q-planes read through uniform (scalar) loads.
+//
+// Publication (ring_queue.cuh:45-115): survivors of a wave are compacted with a ballot
+// and a lane-rank (mbcnt); lane 0 reserves all slots with one 64-bit atomicAdd on the
+// HBM counter; a slot whose position is below the cached write limit (released +
+// capacity) receives the 16-byte Candidate with one 128-bit store to the host-coherent
+// ring, otherwise the record goes to the HBM spill buffer and the drain kernel
+// publishes it once the CPU has released that slot.
+#include <float.h>
+
+#include "engine_internal.h"
+
+namespace cora {
+namespace {
+
+enum ScanKind { kFar = 0, kRecovery = 1, kDense = 2 };
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+__device__ __forceinline__ float uniformf(float v) {
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v)));
+}
+
+__device__ __forceinline__ unsigned long long shfl0_u64(unsigned long long v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint32_t lane_rank(unsigned long long mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// W > 0: compile-time word count; W == 0: runtime word count (any P % 64 == 0, P <= 1024).
+template <int W>
+struct Words {
+    static constexpr int kMax = W > 0 ? W : 32;
+};
+
+template <int W>
+__device__ __forceinline__ void load_codes(const uint8_t *__restrict__ tile, int lane, uint32_t rw,
+                                           uint32_t (&x)[Words<W>::kMax]) {
+    const uint32_t nw = W > 0 ? (uint32_t)W : rw;
+    const uint4 *g4 = reinterpret_cast<const uint4 *>(tile);
+#pragma unroll
+    for (int g = 0; g < Words<W>::kMax / 4; ++g) {
+        if ((uint32_t)(4 * g + 4) <= nw) {
+            const uint4 v = g4[g * 64 + lane];
+            x[4 * g] = v.x;
+            x[4 * g + 1] = v.y;
+            x[4 * g + 2] = v.z;
+            x[4 * g + 3] = v.w;
+        }
+    }
+    if (nw % 4 == 2) {
+        const uint2 *t2 = reinterpret_cast<const uint2 *>(tile + (size_t)(nw / 4) * 1024);
+        const uint2 v = t2[lane];
+        x[nw - 2] = v.x;
+        x[nw - 1] = v.y;
+    }
+}
+
+template <int W>
+__device__ __forceinline__ int popc_ip(const uint32_t (&x)[Words<W>::kMax],
+                                       const uint32_t *__restrict__ planes, uint32_t rw) {
+    const uint32_t nw = W > 0 ? (uint32_t)W : rw;
+    int a[kBq];
+#pragma unroll
+    for (int j = 0; j < kBq; ++j)
+        a[j] = 0;
+#pragma unroll
+    for (int w = 0; w < Words<W>::kMax; ++w) {
+        if ((uint32_t)w < nw) {
+#pragma unroll
+            for (int j = 0; j < kBq; ++j)
+                a[j] += __popc(x[w] & planes[j * nw + w]);
+        }
+    }
+    int ip = -(a[kBq - 1] << (kBq - 1));
+#pragma unroll
+    for (int j = 0; j < kBq - 1; ++j)
+        ip += a[j] << j;
+    return ip;
+}
+
+__device__ __noinline__ unsigned long long refresh_limit(unsigned long long *cached_limit,
+                                                         int *refresh_flag,
+                                                         unsigned long long *released,
+                                                         unsigned long long capacity,
+                                                         unsigned long long need) {
+    unsigned long long lim =
+        __hip_atomic_load(cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lim >= need)
+        return lim;
+    if (atomicCAS(refresh_flag, 0, 1) == 0) {
+        const unsigned long long rel =
+            __hip_atomic_load(released, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        const unsigned long long fresh = rel + capacity;
+        atomicMax(cached_limit, fresh);
+        __hip_atomic_store(refresh_flag, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        lim = lim > fresh ? lim : fresh;
+    } else {
+        lim = __hip_atomic_load(cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return lim;
+}
+
+// Must be called by all 64 lanes of the wave.
+__device__ __forceinline__ void publish(const QueueDev q, bool survive, uint4 rec,
+                                        unsigned long long &limit) {
+    const unsigned long long mask = __ballot(survive);
+    if (mask == 0)
+        return;
+    const uint32_t cnt = (uint32_t)__popcll(mask);
+    const int lane = threadIdx.x & 63;
+    unsigned long long base = 0;
+    if (lane == 0)
+        base = atomicAdd(q.produced, (unsigned long long)cnt);
+    base = shfl0_u64(base);
+    if (base + cnt > limit) {
+        unsigned long long fresh = 0;
+        if (lane == 0)
+            fresh = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released, q.capacity,
+                                  base + cnt);
+        limit = shfl0_u64(fresh);
+    }
+    if (survive) {
+        const unsigned long long pos = base + lane_rank(mask);
+        if (pos < limit) {
+            q.items[pos & q.mask] = rec;
+        } else {
+            const unsigned long long s = atomicAdd(q.spill_count, 1ull);
+            if (s < q.spill_capacity) {
+                q.spill[s].item = rec;
+                q.spill[s].position = pos;
+            } else {
+                atomicExch(q.spill_overflow, 1);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float read_threshold(const float *thresholds, int live, uint32_t query) {
+    if (live)
+        return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t *>(thresholds) + query,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM));
+    return thresholds[query];
+}
+
+// Next unit index in [0, U) for this wave, or U when every range is exhausted.
+__device__ __forceinline__ uint32_t next_unit(uint32_t *cursor, uint32_t U, uint32_t &range,
+                                              uint32_t &tries, uint32_t lane_id) {
+    const uint32_t per = (U + kNumXcd - 1) / kNumXcd;
+    while (tries < kNumXcd) {
+        uint32_t u = 0;
+        if (lane_id == 0)
+            u = atomicAdd(&cursor[range], 1u);
+        u = uniform(u);
+        const uint32_t end = min(U, (range + 1) * per);
+        if (u < end)
+            return u;
+        range = (range + 1) % kNumXcd;
+        ++tries;
+    }
+    return U;
+}
+
+// q-planes of the unit's queries: held in SGPRs (readfirstlane of a broadcast load) when
+// one query with P <= 128 is evaluated per pass, otherwise staged in LDS and read with
+// wave-uniform addresses.
+template <int W, int QMAX>
+struct PlaneStore {
+    static constexpr bool kRegs = W > 0 && W <= 4 && QMAX == 1;
+};
+
+template <int W, int QMAX, int KIND>
+__global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t unit_set) {
+    __shared__ uint32_t s_planes[PlaneStore<W, QMAX>::kRegs ? 1 : QMAX * kBq * 32];
+    const uint32_t lane = threadIdx.x;
+    const uint32_t rw = p.P / 32;
+    const uint32_t nw = W > 0 ? (uint32_t)W : rw;
+    const uint8_t *__restrict__ tiles = p.tiles;
+    const ClusterMeta *__restrict__ meta = p.meta;
+    const uint32_t *__restrict__ qplanes = p.qplanes;
+    const float *__restrict__ qwidth = p.qwidth;
+    const float *__restrict__ qk1 = p.k1;
+    const float *__restrict__ pgadd = p.pgadd;
+    const float *__restrict__ pgerr = p.pgerr;
+    const Pair *__restrict__ pairs = p.pairs;
+    const Unit *__restrict__ units = p.units;
+    const float *thresholds = p.thresholds;
+    const int live = p.thresholds_live;
+    const uint32_t nprobe = p.nprobe, tile_bytes = p.tile_bytes;
+    const uint32_t *seed_bits = p.seed_bits;
+    const uint32_t seed_words = p.seed_words, vanguard = p.vanguard;
+    const QueueDev q = p.queue;
+    const uint32_t U = p.num_units[unit_set];
+    const uint32_t ubase = unit_set ? p.num_units[0] : 0u;
+    uint32_t range = blockIdx.x % kNumXcd, tries = 0;
+    unsigned long long limit =
+        KIND == kDense ? 0ull
+                       : __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+        const uint32_t u = next_unit(p.unit_cursor, U, range, tries, lane);
+        if (u >= U)
+            break;
+        const Unit un = units[ubase + u];
+        const uint32_t cluster = uniform(un.cluster);
+        const uint32_t count = uniform(un.count);
+        const uint32_t pair_begin = uniform(un.pair_begin);
+        const ClusterMeta cm = meta[cluster];
+        const uint32_t n = uniform(cm.n), start = uniform(cm.start), tbase = uniform(cm.tile_base);
+
+        uint32_t word0[QMAX];
+        float width[QMAX], k1[QMAX], gadd[QMAX], gerr[QMAX], cutoff[QMAX];
+        uint32_t query0 = 0, probe0 = 0;
+#pragma unroll
+        for (int j = 0; j < QMAX; ++j) {
+            const uint32_t jj = (uint32_t)j < count ? (uint32_t)j : 0u;
+            const uint32_t w0 = uniform(pairs[pair_begin + jj].word0);
+            const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
+            if (j == 0) {
+                query0 = query;
+                probe0 = probe;
+            }
+            word0[j] = w0;
+            width[j] = uniformf(qwidth[query]);
+            k1[j] = uniformf(qk1[query]);
+            const size_t pi = (size_t)query * nprobe + probe;
+            gadd[j] = uniformf(pgadd[pi]);
+            gerr[j] = uniformf(pgerr[pi]);
+            cutoff[j] = KIND == kDense ? FLT_MAX : uniformf(read_threshold(thresholds, live, query));
+        }
+        uint32_t preg[PlaneStore<W, QMAX>::kRegs ? kBq * (W > 0 ? W : 1) : 1];
+        if constexpr (PlaneStore<W, QMAX>::kRegs) {
+            const uint32_t *src = qplanes + (size_t)query0 * kBq * W;
+#pragma unroll
+            for (int i = 0; i < kBq * W; ++i)
+                preg[i] = uniform(src[i]);
+        } else {
+            __syncthreads();
+            for (uint32_t i = lane; i < QMAX * kBq * nw; i += 64) {
+                const uint32_t j = i / (kBq * nw), r = i % (kBq * nw);
+                const uint32_t w0 = word0[0];
+                uint32_t wj = w0;
+#pragma unroll
+                for (int jj = 1; jj < QMAX; ++jj)
+                    if ((uint32_t)jj == j)
+                        wj = word0[jj];
+                (void)w0;
+                s_planes[i] = j < count ? qplanes[(size_t)(wj & 0xFFFFu) * kBq * nw + r] : 0u;
+            }
+            __syncthreads();
+        }
+        const uint32_t *seeds = nullptr;
+        if (KIND == kRecovery)
+            seeds = seed_bits + ((size_t)query0 * vanguard + probe0) * seed_words;
+        const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
+        for (uint32_t t = 0; t < ntiles; ++t) {
+            const uint8_t *tile = tiles + (size_t)(tbase + t) * tile_bytes;
+            uint32_t x[Words<W>::kMax];
+            load_codes<W>(tile, lane, rw, x);
+            const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
+            const float fa = fac[lane], fr = fac[64 + lane], fe = fac[128 + lane];
+            const uint32_t local = t * kTileVectors + lane;
+            const bool valid = local < n;
+            bool not_seed = true;
+            if (KIND == kRecovery)
+                not_seed = !valid || !((seeds[local >> 5] >> (local & 31)) & 1u);
+#pragma unroll
+            for (int j = 0; j < QMAX; ++j) {
+                if ((uint32_t)j >= count)
+                    break;
+                int ip;
+                if constexpr (PlaneStore<W, QMAX>::kRegs)
+                    ip = popc_ip<W>(x, preg, rw);
+                else
+                    ip = popc_ip<W>(x, s_planes + j * kBq * nw, rw);
+                const float ex = width[j] * (float)ip;
+                const float low = fa + gadd[j] + fr * (ex + k1[j]) - fe * gerr[j];
+                if (KIND == kDense) {
+                    if (valid) {
+                        const uint32_t query = word0[j] & 0xFFFFu, probe = word0[j] >> 16;
+                        const size_t o = ((size_t)query * nprobe + probe) * p.dbg_stride + local;
+                        p.dbg_ip[o] = ip;
+                        p.dbg_low[o] = low;
+                    }
+                } else {
+                    const bool survive = valid && not_seed && low < cutoff[j];
+                    const uint4 rec = make_uint4(word0[j], start + local, __float_as_uint(ex),
+                                                 __float_as_uint(low));
+                    publish(q, survive, rec, limit);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Vanguard seed pass (reference computeInnerProducts1BitLutProducerVanguard,
+// filter_kernels.cuh:308-468): for each vanguard pair (probe rank < vanguard) publish the
+// `keep` vectors with the smallest lower bounds below the query's threshold and mark
+// them in the pair's seed bitmask; the recovery pass later publishes the remaining
+// vectors against the thresholds the CPU has tightened meanwhile. Selection: radix
+// select of the keep-th smallest key, all smaller keys plus the lowest-index ties.
+// ---------------------------------------------------------------------------------
+constexpr int kVanThreads = 256;
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int W>
+__global__ __launch_bounds__(kVanThreads) void vanguard_seed_kernel(const ScanParams p) {
+    __shared__ float s_low[kVanguardMaxCluster];
+    __shared__ float s_ex[kVanguardMaxCluster];
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_scan[kVanThreads];
+    __shared__ uint32_t s_sel[kMaxVanguardKeep];
+    __shared__ uint32_t s_unit, s_prefix, s_remaining, s_valid;
+    __shared__ uint32_t s_range, s_tries;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t rw = p.P / 32;
+    const uint32_t U = p.num_units[0];
+    const uint32_t per = (U + kNumXcd - 1) / kNumXcd;
+    if (tid == 0) {
+        s_range = blockIdx.x % kNumXcd;
+        s_tries = 0;
+    }
+    const QueueDev q = p.queue;
+    unsigned long long limit =
+        __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+        if (tid == 0) {
+            uint32_t u = U;
+            while (s_tries < kNumXcd) {
+                const uint32_t v = atomicAdd(&p.unit_cursor[s_range], 1u);
+                if (v < min(U, (s_range + 1) * per)) {
+                    u = v;
+                    break;
+                }
+                s_range = (s_range + 1) % kNumXcd;
+                ++s_tries;
+            }
+            s_unit = u;
+        }
+        __syncthreads();
+        const uint32_t u = s_unit;
+        if (u >= U)
+            break;
+        const Unit un = p.units[u];
+        const ClusterMeta cm = p.meta[un.cluster];
+        const uint32_t n = cm.n;
+        const uint32_t w0 = p.pairs[un.pair_begin].word0;
+        const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
+        if (n > (uint32_t)kVanguardMaxCluster || p.keep == 0) {
+            __syncthreads();
+            continue;  // no seeds: the recovery pass publishes the whole pair
+        }
+        const float width = p.qwidth[query], k1 = p.k1[query];
+        const size_t pi = (size_t)query * p.nprobe + probe;
+        const float gadd = p.pgadd[pi], gerr = p.pgerr[pi];
+        const float cutoff = read_threshold(p.thresholds, p.thresholds_live, query);
+        const uint32_t *planes = p.qplanes + (size_t)query * kBq * rw;
+        const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
+        for (uint32_t t = wave; t < ntiles; t += kVanThreads / 64) {
+            const uint8_t *tile = p.tiles + (size_t)(cm.tile_base + t) * p.tile_bytes;
+            uint32_t x[Words<W>::kMax];
+            load_codes<W>(tile, lane, rw, x);
+            const float *fac = reinterpret_cast<const float *>(tile + 256u * rw);
+            const uint32_t local = t * kTileVectors + lane;
+            if (local < n) {
+                const int ip = popc_ip<W>(x, planes, rw);
+                const float ex = width * (float)ip;
+                const float low = fac[lane] + gadd + fac[64 + lane] * (ex + k1) -
+                                  fac[128 + lane] * gerr;
+                s_low[local] = low < cutoff ? low : __uint_as_float(0x7FFFFFFFu);  // NaN: excluded
+                s_ex[local] = ex;
+            }
+        }
+        if (tid == 0)
+            s_valid = 0;
+        __syncthreads();
+        uint32_t nv = 0;
+        for (uint32_t i = tid; i < n; i += kVanThreads)
+            nv += s_low[i] == s_low[i];
+        atomicAdd(&s_valid, nv);
+        __syncthreads();
+        const uint32_t take = min(p.keep, s_valid);
+        if (take == 0) {
+            __syncthreads();
+            continue;
+        }
+        // radix select of the take-th smallest key (NaN keys sort last)
+        uint32_t prefix = 0, pmask = 0;
+        if (tid == 0)
+            s_remaining = take;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            s_hist[tid] = 0;
+            __syncthreads();
+            for (uint32_t i = tid; i < n; i += kVanThreads) {
+                const uint32_t key = order_key(s_low[i]);
+                if ((key & pmask) == prefix)
+                    atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t rem = s_remaining, cum = 0, d = 0;
+                for (; d < 255; ++d) {
+                    if (cum + s_hist[d] >= rem)
+                        break;
+                    cum += s_hist[d];
+                }
+                s_remaining = rem - cum;
+                s_prefix = prefix | (d << shift);
+            }
+            __syncthreads();
+            prefix = s_prefix;
+            pmask |= 255u << shift;
+        }
+        const uint32_t kth = prefix, take_eq = s_remaining;
+        // deterministic gather in index order: contiguous index chunk per thread
+        const uint32_t chunk = (n + kVanThreads - 1) / kVanThreads;
+        const uint32_t b0 = min(n, tid * chunk), b1 = min(n, b0 + chunk);
+        uint32_t nless = 0, neq = 0;
+        for (uint32_t i = b0; i < b1; ++i) {
+            const uint32_t key = order_key(s_low[i]);
+            nless += key < kth;
+            neq += key == kth;
+        }
+        // exclusive scans (less first, then equal)
+        s_scan[tid] = nless;
+        __syncthreads();
+        for (uint32_t o = 1; o < kVanThreads; o <<= 1) {
+            const uint32_t v = tid >= o ? s_scan[tid - o] : 0;
+            __syncthreads();
+            s_scan[tid] += v;
+            __syncthreads();
+        }
+        const uint32_t less_off = s_scan[tid] - nless, tot_less = s_scan[kVanThreads - 1];
+        __syncthreads();
+        s_scan[tid] = neq;
+        __syncthreads();
+        for (uint32_t o = 1; o < kVanThreads; o <<= 1) {
+            const uint32_t v = tid >= o ? s_scan[tid - o] : 0;
+            __syncthreads();
+            s_scan[tid] += v;
+            __syncthreads();
+        }
+        uint32_t eq_rank = s_scan[tid] - neq, lo = less_off;
+        uint32_t *seed = p.seed_bits + ((size_t)query * p.vanguard + probe) * p.seed_words;
+        for (uint32_t i = b0; i < b1; ++i) {
+            const uint32_t key = order_key(s_low[i]);
+            bool pick = false;
+            if (key < kth) {
+                s_sel[lo++] = i;
+                pick = true;
+            } else if (key == kth) {
+                if (eq_rank < take_eq) {
+                    s_sel[tot_less + eq_rank] = i;
+                    pick = true;
+                }
+                ++eq_rank;
+            }
+            if (pick)
+                atomicOr(&seed[i >> 5], 1u << (i & 31));
+        }
+        __syncthreads();
+        const uint32_t rounds = (take + kVanThreads - 1) / kVanThreads;
+        for (uint32_t r = 0; r < rounds; ++r) {
+            const uint32_t s = r * kVanThreads + tid;
+            const bool ok = s < take;
+            const uint32_t local = ok ? s_sel[s] : 0u;
+            const uint4 rec = make_uint4(w0, cm.start + local, __float_as_uint(s_ex[local]),
+                                         __float_as_uint(s_low[local]));
+            publish(q, ok, rec, limit);
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void queue_reset_kernel(QueueDev q) {
+    *q.produced = 0;
+    *q.spill_count = 0;
+    *q.spill_overflow = 0;
+    *q.cached_limit = q.capacity;
+    *q.refresh_flag = 0;
+    *q.stalled = 0;
+}
+
+__global__ void cursor_init_kernel(uint32_t *cursor, const uint32_t *num_units, uint32_t set) {
+    const uint32_t U = num_units[set];
+    const uint32_t per = (U + kNumXcd - 1) / kNumXcd;
+    const uint32_t x = threadIdx.x;
+    if (x < kNumXcd)
+        cursor[x] = x * per;
+}
+
+// Queue completion (reference finish_queue, ring_queue.cuh:125-170): publish produced
+// and spilled counts, drain spilled records into the ring as the CPU releases space,
+// then set Progress::done with a system-scope release. The wait is bounded (max_spins
+// sleeps) and honours the host abort flag, so the kernel always ends.
+__global__ __launch_bounds__(256) void finish_kernel(QueueDev q, unsigned long long max_spins) {
+    __shared__ unsigned long long s_limit;
+    __shared__ uint32_t s_remaining;
+    __shared__ int s_abort;
+    const uint32_t t = threadIdx.x;
+    const unsigned long long produced = *q.produced;
+    const unsigned long long spill_total = *q.spill_count;
+    const unsigned long long spilled = spill_total < q.spill_capacity ? spill_total : q.spill_capacity;
+    const int overflow = *q.spill_overflow;
+    if (t == 0) {
+        __hip_atomic_store(&q.progress->produced, produced, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(&q.progress->spilled, spill_total, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    bool stalled = false;
+    if (!overflow) {
+        for (unsigned long long spin = 0;; ++spin) {
+            if (t == 0) {
+                s_limit = __hip_atomic_load(&q.progress->released, __ATOMIC_ACQUIRE,
+                                            __HIP_MEMORY_SCOPE_SYSTEM) +
+                          q.capacity;
+                s_remaining = 0;
+                s_abort = __hip_atomic_load(q.abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            __syncthreads();
+            if (s_abort) {
+                stalled = true;
+                break;
+            }
+            uint32_t rem = 0;
+            const unsigned long long lim = s_limit;
+            for (unsigned long long i = t; i < spilled; i += blockDim.x) {
+                const unsigned long long pos = q.spill[i].position;
+                if (pos == ~0ull)
+                    continue;
+                if (pos < lim) {
+                    q.items[pos & q.mask] = q.spill[i].item;
+                    q.spill[i].position = ~0ull;
+                } else {
+                    ++rem;
+                }
+            }
+            if (rem)
+                atomicAdd(&s_remaining, rem);
+            __syncthreads();
+            if (s_remaining == 0)
+                break;
+            if (spin >= max_spins) {
+                stalled = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(127);
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+    if (t == 0) {
+        if (stalled)
+            *q.stalled = 1;
+        __threadfence_system();
+        if (overflow || stalled)
+            __hip_atomic_store(&q.progress->overflow, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(&q.progress->done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+template <int W>
+int launch_scan_w(const ScanParams &p, uint32_t batch_q, int kind, uint32_t grid, uint32_t set,
+                  hipStream_t s) {
+    if (kind == kFar) {
+        if (batch_q <= 1)
+            scan_kernel<W, 1, kFar><<<grid, 64, 0, s>>>(p, set);
+        else
+            scan_kernel<W, kMaxBatchQ, kFar><<<grid, 64, 0, s>>>(p, set);
+    } else if (kind == kRecovery) {
+        scan_kernel<W, 1, kRecovery><<<grid, 64, 0, s>>>(p, set);
+    } else {
+        scan_kernel<W, kMaxBatchQ, kDense><<<grid, 64, 0, s>>>(p, set);
+    }
+    return 0;
+}
+
+}  // namespace
+
+int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, uint32_t grid,
+                hipStream_t s) {
+    // unit set: vanguard units for the recovery pass, far units otherwise; the dense
+    // debug pass runs over both sets (two launches)
+    const uint32_t set = kind == kRecovery ? 0u : 1u;
+    switch (W) {
+    case 2: return launch_scan_w<2>(p, batch_q, kind, grid, set, s);
+    case 4: return launch_scan_w<4>(p, batch_q, kind, grid, set, s);
+    case 6: return launch_scan_w<6>(p, batch_q, kind, grid, set, s);
+    case 8: return launch_scan_w<8>(p, batch_q, kind, grid, set, s);
+    case 12: return launch_scan_w<12>(p, batch_q, kind, grid, set, s);
+    case 16: return launch_scan_w<16>(p, batch_q, kind, grid, set, s);
+    case 24: return launch_scan_w<24>(p, batch_q, kind, grid, set, s);
+    case 32: return launch_scan_w<32>(p, batch_q, kind, grid, set, s);
+    default: return launch_scan_w<0>(p, batch_q, kind, grid, set, s);
+    }
+}
+
+int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t grid, uint32_t set,
+                    hipStream_t s) {
+    switch (W) {
+    case 2: return launch_scan_w<2>(p, 8, kind, grid, set, s);
+    case 4: return launch_scan_w<4>(p, 8, kind, grid, set, s);
+    case 6: return launch_scan_w<6>(p, 8, kind, grid, set, s);
+    case 8: return launch_scan_w<8>(p, 8, kind, grid, set, s);
+    case 12: return launch_scan_w<12>(p, 8, kind, grid, set, s);
+    case 16: return launch_scan_w<16>(p, 8, kind, grid, set, s);
+    case 24: return launch_scan_w<24>(p, 8, kind, grid, set, s);
+    case 32: return launch_scan_w<32>(p, 8, kind, grid, set, s);
+    default: return launch_scan_w<0>(p, 8, kind, grid, set, s);
+    }
+}
+
+int launch_vanguard_seed(const ScanParams &p, uint32_t W, uint32_t grid, hipStream_t s) {
+    switch (W) {
+    case 2: vanguard_seed_kernel<2><<<grid, kVanThreads, 0, s>>>(p); break;
+    case 4: vanguard_seed_kernel<4><<<grid, kVanThreads, 0, s>>>(p); break;
+    case 8: vanguard_seed_kernel<8><<<grid, kVanThreads, 0, s>>>(p); break;
+    case 24: vanguard_seed_kernel<24><<<grid, kVanThreads, 0, s>>>(p); break;
+    default: vanguard_seed_kernel<0><<<grid, kVanThreads, 0, s>>>(p); break;
+    }
+    return 0;
+}
+
+void launch_queue_reset(QueueDev q, hipStream_t s) { queue_reset_kernel<<<1, 1, 0, s>>>(q); }
+
+void launch_cursor_init(uint32_t *cursor, const uint32_t *num_units, uint32_t set, hipStream_t s) {
+    cursor_init_kernel<<<1, 64, 0, s>>>(cursor, num_units, set);
+}
+
+void launch_finish(QueueDev q, unsigned long long max_spins, hipStream_t s) {
+    finish_kernel<<<1, 256, 0, s>>>(q, max_spins);
+}
+
+}  // namespace cora

@@ -1,0 +1,180 @@
+// Pair scheduling: the reference flattens (cluster, query, probe) pairs and sorts them
+// with PairSortCompare — vanguard pairs (probe < vanguard) first, then by cluster
+// (query_kernels.cuh:105-113, kernel_types.cuh:34-60, hybrid.cu:504-508). Here the
+// same grouping is a counting sort into 2*nlist buckets (bucket = cluster for vanguard
+// pairs, nlist + cluster for the rest) followed by cutting every bucket into scan
+// units of at most batch_q pairs (1 for vanguard buckets). Pair order inside a bucket
+// is not fixed; every pair's results are independent of it.
+#include "engine_internal.h"
+
+namespace cora {
+namespace {
+
+__global__ void fill_u32_kernel(uint32_t *p, uint32_t v, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void fill_u64_kernel(unsigned long long *p, unsigned long long v, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void count_pairs_kernel(const int32_t *__restrict__ probe_idx, uint32_t nq,
+                                   uint32_t nprobe, uint32_t nlist, uint32_t vanguard,
+                                   uint32_t *__restrict__ count) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i >= (size_t)nq * nprobe)
+        return;
+    const uint32_t p = (uint32_t)(i % nprobe);
+    const uint32_t c = (uint32_t)probe_idx[i];
+    atomicAdd(&count[(p >= vanguard ? nlist : 0u) + c], 1u);
+}
+
+constexpr int kScanThreads = 1024;
+
+// Single block: exclusive scans of bucket sizes and unit counts, unit totals and the
+// algorithmic traffic of the far-pair scan.
+__global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
+    const uint32_t *__restrict__ count, const ClusterMeta *__restrict__ meta, uint32_t nlist,
+    uint32_t batch_q, uint32_t bpv, uint32_t *__restrict__ bucket_offset,
+    uint32_t *__restrict__ unit_offset, uint32_t *__restrict__ num_units,
+    unsigned long long *__restrict__ stats) {
+    __shared__ uint32_t s_pairs[kScanThreads], s_units[kScanThreads], s_van_units[kScanThreads];
+    __shared__ unsigned long long s_bytes[kScanThreads], s_fu[kScanThreads], s_vec[kScanThreads];
+    const uint32_t nb = 2 * nlist;
+    const int t = threadIdx.x;
+    const uint32_t chunk = (nb + kScanThreads - 1) / kScanThreads;
+    const uint32_t b0 = min(nb, t * chunk), b1 = min(nb, b0 + chunk);
+    uint32_t pairs = 0, units = 0, van_units = 0;
+    unsigned long long bytes = 0, fu = 0, vec = 0;
+    for (uint32_t b = b0; b < b1; ++b) {
+        const uint32_t m = count[b];
+        pairs += m;
+        if (b < nlist) {
+            units += m;
+            van_units += m;
+        } else {
+            const uint32_t u = (m + batch_q - 1) / batch_q;
+            const uint32_t n = meta[b - nlist].n;
+            units += u;
+            bytes += (unsigned long long)u * n * bpv;
+            fu += u;
+            vec += (unsigned long long)m * n;
+        }
+    }
+    s_pairs[t] = pairs;
+    s_units[t] = units;
+    s_van_units[t] = van_units;
+    s_bytes[t] = bytes;
+    s_fu[t] = fu;
+    s_vec[t] = vec;
+    __syncthreads();
+    for (int o = 1; o < kScanThreads; o <<= 1) {
+        const uint32_t xp = t >= o ? s_pairs[t - o] : 0, xu = t >= o ? s_units[t - o] : 0;
+        const uint32_t xv = t >= o ? s_van_units[t - o] : 0;
+        const unsigned long long xb = t >= o ? s_bytes[t - o] : 0, xf = t >= o ? s_fu[t - o] : 0;
+        const unsigned long long xe = t >= o ? s_vec[t - o] : 0;
+        __syncthreads();
+        s_pairs[t] += xp;
+        s_units[t] += xu;
+        s_van_units[t] += xv;
+        s_bytes[t] += xb;
+        s_fu[t] += xf;
+        s_vec[t] += xe;
+        __syncthreads();
+    }
+    uint32_t po = s_pairs[t] - pairs, uo = s_units[t] - units;
+    for (uint32_t b = b0; b < b1; ++b) {
+        const uint32_t m = count[b];
+        bucket_offset[b] = po;
+        unit_offset[b] = uo;
+        po += m;
+        uo += b < nlist ? m : (m + batch_q - 1) / batch_q;
+    }
+    if (t == kScanThreads - 1) {
+        bucket_offset[nb] = s_pairs[t];
+        unit_offset[nb] = s_units[t];
+        num_units[0] = s_van_units[t];
+        num_units[1] = s_units[t] - s_van_units[t];
+        stats[0] = s_bytes[t];
+        stats[1] = s_fu[t];
+        stats[2] = s_vec[t];
+    }
+}
+
+__global__ void scatter_pairs_kernel(const int32_t *__restrict__ probe_idx, uint32_t nq,
+                                     uint32_t nprobe, uint32_t nlist, uint32_t vanguard,
+                                     const uint32_t *__restrict__ bucket_offset,
+                                     uint32_t *__restrict__ cursor, Pair *__restrict__ pairs) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i >= (size_t)nq * nprobe)
+        return;
+    const uint32_t q = (uint32_t)(i / nprobe), p = (uint32_t)(i % nprobe);
+    const uint32_t c = (uint32_t)probe_idx[i];
+    const uint32_t b = (p >= vanguard ? nlist : 0u) + c;
+    const uint32_t pos = bucket_offset[b] + atomicAdd(&cursor[b], 1u);
+    pairs[pos] = Pair{(p << 16) | q, c};
+}
+
+__global__ void build_units_kernel(const uint32_t *__restrict__ bucket_offset,
+                                   const uint32_t *__restrict__ unit_offset,
+                                   const uint32_t *__restrict__ num_units, uint32_t nlist,
+                                   uint32_t batch_q, Unit *__restrict__ units) {
+    const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= num_units[0] + num_units[1])
+        return;
+    // last bucket b with unit_offset[b] <= u (empty buckets share offsets)
+    uint32_t lo = 0, hi = 2 * nlist;  // unit_offset[2*nlist] = total > u
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (unit_offset[mid] <= u)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    const uint32_t b = lo;
+    const uint32_t q = b < nlist ? 1u : batch_q;
+    const uint32_t local = u - unit_offset[b];
+    const uint32_t m = bucket_offset[b + 1] - bucket_offset[b];
+    units[u] = Unit{b % nlist, bucket_offset[b] + local * q, min(q, m - local * q), b};
+}
+
+}  // namespace
+
+void launch_fill_u32(uint32_t *p, uint32_t value, size_t n, hipStream_t s) {
+    if (!n)
+        return;
+    const uint32_t grid = (uint32_t)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    fill_u32_kernel<<<grid, 256, 0, s>>>(p, value, n);
+}
+
+void launch_fill_u64(unsigned long long *p, unsigned long long value, size_t n, hipStream_t s) {
+    if (!n)
+        return;
+    const uint32_t grid = (uint32_t)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    fill_u64_kernel<<<grid, 256, 0, s>>>(p, value, n);
+}
+
+void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint32_t nq,
+                        uint32_t nprobe, uint32_t nlist, uint32_t vanguard, uint32_t batch_q,
+                        uint32_t bytes_per_vector, uint32_t *bucket_count, uint32_t *bucket_cursor,
+                        uint32_t *bucket_offset, uint32_t *unit_offset, Pair *pairs, Unit *units,
+                        uint32_t *num_units, unsigned long long *scan_stats, hipStream_t s) {
+    const size_t np = (size_t)nq * nprobe;
+    launch_fill_u32(bucket_count, 0, 2 * (size_t)nlist, s);
+    launch_fill_u32(bucket_cursor, 0, 2 * (size_t)nlist, s);
+    const uint32_t grid = (uint32_t)((np + 255) / 256);
+    count_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard, bucket_count);
+    scan_buckets_kernel<<<1, kScanThreads, 0, s>>>(bucket_count, meta, nlist, batch_q,
+                                                   bytes_per_vector, bucket_offset, unit_offset,
+                                                   num_units, scan_stats);
+    scatter_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard,
+                                              bucket_offset, bucket_cursor, pairs);
+    build_units_kernel<<<grid, 256, 0, s>>>(bucket_offset, unit_offset, num_units, nlist, batch_q,
+                                            units);
+}
+
+}  // namespace cora

@@ -1,0 +1,248 @@
+// Index-build and evaluation tools on the GPU (C-ABI in include/cora_gpu.h, cora_tool_*):
+// rotation of a row block, Lloyd k-means, nearest-centroid assignment and exhaustive
+// top-k (ground truth). They reuse the engine's FP32 GEMM, row-norm and top-k select
+// kernels; host arrays in, host arrays out, device memory allocated per call.
+#include <float.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../../include/cora_gpu.h"
+#include "engine_internal.h"
+
+using namespace cora;
+
+namespace {
+
+thread_local std::string g_tool_error;
+
+// argmin over each row of dist [rows][k]; ties -> lower index.
+__global__ __launch_bounds__(64) void row_argmin_kernel(const float *__restrict__ dist, uint32_t k,
+                                                        uint32_t *__restrict__ out) {
+    const float *row = dist + (size_t)blockIdx.x * k;
+    float best = FLT_MAX;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t j = threadIdx.x; j < k; j += 64) {
+        const float v = row[j];
+        if (v < best || (v == best && j < bi)) {
+            best = v;
+            bi = j;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (ov < best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if (threadIdx.x == 0)
+        out[blockIdx.x] = bi == 0xFFFFFFFFu ? 0u : bi;
+}
+
+__global__ void accumulate_kernel(const float *__restrict__ x, const uint32_t *__restrict__ assign,
+                                  uint32_t rows, uint32_t dim, float *__restrict__ sums,
+                                  uint32_t *__restrict__ counts) {
+    const uint32_t r = blockIdx.x;
+    if (r >= rows)
+        return;
+    const uint32_t c = assign[r];
+    for (uint32_t d = threadIdx.x; d < dim; d += blockDim.x)
+        atomicAdd(&sums[(size_t)c * dim + d], x[(size_t)r * dim + d]);
+    if (threadIdx.x == 0)
+        atomicAdd(&counts[c], 1u);
+}
+
+__global__ void update_kernel(float *__restrict__ cent, const float *__restrict__ sums,
+                              const uint32_t *__restrict__ counts, uint32_t k, uint32_t dim) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i >= (size_t)k * dim)
+        return;
+    const uint32_t c = (uint32_t)(i / dim);
+    if (counts[c])
+        cent[i] = sums[i] / (float)counts[c];
+}
+
+struct DevBuf {
+    void *p = nullptr;
+    ~DevBuf() {
+        if (p)
+            (void)hipFree(p);
+    }
+};
+
+#define TCHK(call)                                                                  \
+    do {                                                                            \
+        hipError_t e_ = (call);                                                     \
+        if (e_ != hipSuccess) {                                                     \
+            g_tool_error = std::string(#call) + ": " + hipGetErrorString(e_);       \
+            return CORA_ERR_RUNTIME;                                                \
+        }                                                                           \
+    } while (0)
+
+template <class T>
+int dev(DevBuf &b, size_t n) {
+    TCHK(hipMalloc(&b.p, std::max<size_t>(1, n) * sizeof(T)));
+    return CORA_OK;
+}
+
+// Assign rows [0, n) of device matrix x to the nearest of k device centroids.
+int assign_rows(const float *d_x, size_t n, uint32_t dim, const float *d_c, const float *d_cn,
+                uint32_t k, uint32_t *d_assign, float *d_xn, float *d_dist, size_t chunk,
+                hipStream_t s) {
+    for (size_t b = 0; b < n; b += chunk) {
+        const uint32_t rows = (uint32_t)std::min(chunk, n - b);
+        launch_row_norms(d_x + b * dim, rows, dim, d_xn, s);
+        launch_dist_gemm(d_x + b * dim, d_xn, d_c, d_cn, rows, k, dim, d_dist, s);
+        row_argmin_kernel<<<rows, 64, 0, s>>>(d_dist, k, d_assign + b);
+    }
+    TCHK(hipGetLastError());
+    return CORA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *cora_tool_last_error(void) { return g_tool_error.c_str(); }
+
+int cora_tool_rotate(const float *h_x, uint64_t n, uint64_t dim, const float *h_R, uint64_t P,
+                     float *h_out, int device) {
+    if (!h_x || !h_R || !h_out || !n || !dim || P < dim)
+        return CORA_ERR_INVALID_ARGUMENT;
+    TCHK(hipSetDevice(device));
+    DevBuf x, r, o;
+    const size_t chunk = 1u << 20;
+    if (dev<float>(x, std::min<size_t>(n, chunk) * dim) || dev<float>(r, dim * P) ||
+        dev<float>(o, std::min<size_t>(n, chunk) * P))
+        return CORA_ERR_RUNTIME;
+    TCHK(hipMemcpy(r.p, h_R, dim * P * 4, hipMemcpyHostToDevice));
+    for (size_t b = 0; b < n; b += chunk) {
+        const size_t rows = std::min<size_t>(chunk, n - b);
+        TCHK(hipMemcpy(x.p, h_x + b * dim, rows * dim * 4, hipMemcpyHostToDevice));
+        launch_rotate((float *)x.p, (float *)r.p, (float *)o.p, (uint32_t)rows, (uint32_t)dim,
+                      (uint32_t)P, nullptr);
+        TCHK(hipGetLastError());
+        TCHK(hipMemcpy(h_out + b * P, o.p, rows * P * 4, hipMemcpyDeviceToHost));
+    }
+    return CORA_OK;
+}
+
+// Lloyd k-means on n rows (FP32 squared L2), initial centroids = k distinct rows chosen
+// with a seeded generator; an empty cluster keeps its previous centroid.
+int cora_tool_kmeans(const float *h_x, uint64_t n, uint64_t dim, uint64_t k, uint32_t iters,
+                     uint64_t seed, float *h_centroids, int device) {
+    if (!h_x || !h_centroids || !n || !dim || !k || k > n || k > 0x7FFFFFFF)
+        return CORA_ERR_INVALID_ARGUMENT;
+    TCHK(hipSetDevice(device));
+    std::vector<uint64_t> pick(n);
+    for (uint64_t i = 0; i < n; ++i)
+        pick[i] = i;
+    std::mt19937_64 gen(seed);
+    for (uint64_t i = 0; i < k; ++i) {
+        std::uniform_int_distribution<uint64_t> u(i, n - 1);
+        std::swap(pick[i], pick[u(gen)]);
+    }
+    std::vector<float> init(k * dim);
+    for (uint64_t i = 0; i < k; ++i)
+        memcpy(&init[i * dim], h_x + pick[i] * dim, dim * 4);
+    const size_t chunk = std::max<size_t>(1, std::min<size_t>(n, (size_t)(1u << 30) / (k * 4)));
+    DevBuf x, c, cn, xn, dist, asg, sums, cnt;
+    if (dev<float>(x, n * dim) || dev<float>(c, k * dim) || dev<float>(cn, k) ||
+        dev<float>(xn, chunk) || dev<float>(dist, chunk * k) || dev<uint32_t>(asg, n) ||
+        dev<float>(sums, k * dim) || dev<uint32_t>(cnt, k))
+        return CORA_ERR_RUNTIME;
+    TCHK(hipMemcpy(x.p, h_x, n * dim * 4, hipMemcpyHostToDevice));
+    TCHK(hipMemcpy(c.p, init.data(), k * dim * 4, hipMemcpyHostToDevice));
+    for (uint32_t it = 0; it < iters; ++it) {
+        launch_row_norms((float *)c.p, (uint32_t)k, (uint32_t)dim, (float *)cn.p, nullptr);
+        if (int rc = assign_rows((float *)x.p, n, (uint32_t)dim, (float *)c.p, (float *)cn.p,
+                                 (uint32_t)k, (uint32_t *)asg.p, (float *)xn.p, (float *)dist.p,
+                                 chunk, nullptr))
+            return rc;
+        TCHK(hipMemset(sums.p, 0, k * dim * 4));
+        TCHK(hipMemset(cnt.p, 0, k * 4));
+        accumulate_kernel<<<(uint32_t)n, 64>>>((float *)x.p, (uint32_t *)asg.p, (uint32_t)n,
+                                                (uint32_t)dim, (float *)sums.p, (uint32_t *)cnt.p);
+        update_kernel<<<(uint32_t)((k * dim + 255) / 256), 256>>>((float *)c.p, (float *)sums.p,
+                                                                   (uint32_t *)cnt.p, (uint32_t)k,
+                                                                   (uint32_t)dim);
+        TCHK(hipGetLastError());
+    }
+    TCHK(hipDeviceSynchronize());
+    TCHK(hipMemcpy(h_centroids, c.p, k * dim * 4, hipMemcpyDeviceToHost));
+    return CORA_OK;
+}
+
+int cora_tool_assign(const float *h_x, uint64_t n, uint64_t dim, const float *h_centroids,
+                     uint64_t k, uint32_t *h_assign, int device) {
+    if (!h_x || !h_centroids || !h_assign || !n || !dim || !k)
+        return CORA_ERR_INVALID_ARGUMENT;
+    TCHK(hipSetDevice(device));
+    const size_t rows_dev = std::min<size_t>(n, 1u << 22);
+    const size_t chunk = std::max<size_t>(1, std::min<size_t>(rows_dev, (size_t)(1u << 30) / (k * 4)));
+    DevBuf x, c, cn, xn, dist, asg;
+    if (dev<float>(x, rows_dev * dim) || dev<float>(c, k * dim) || dev<float>(cn, k) ||
+        dev<float>(xn, chunk) || dev<float>(dist, chunk * k) || dev<uint32_t>(asg, rows_dev))
+        return CORA_ERR_RUNTIME;
+    TCHK(hipMemcpy(c.p, h_centroids, k * dim * 4, hipMemcpyHostToDevice));
+    launch_row_norms((float *)c.p, (uint32_t)k, (uint32_t)dim, (float *)cn.p, nullptr);
+    for (size_t b = 0; b < n; b += rows_dev) {
+        const size_t rows = std::min(rows_dev, n - b);
+        TCHK(hipMemcpy(x.p, h_x + b * dim, rows * dim * 4, hipMemcpyHostToDevice));
+        if (int rc = assign_rows((float *)x.p, rows, (uint32_t)dim, (float *)c.p, (float *)cn.p,
+                                 (uint32_t)k, (uint32_t *)asg.p, (float *)xn.p, (float *)dist.p,
+                                 chunk, nullptr))
+            return rc;
+        TCHK(hipMemcpy(h_assign + b, asg.p, rows * 4, hipMemcpyDeviceToHost));
+    }
+    return CORA_OK;
+}
+
+// Exhaustive top-k of nq queries over nb base rows by FP32 distance (L2: ||q-x||^2 through
+// the norm expansion; IP: -<q,x>), ascending, ties by base index. Callers that need the
+// exact order re-rank a few extra candidates in FP64.
+int cora_tool_topk(const float *h_base, uint64_t nb, const float *h_q, uint64_t nq, uint64_t dim,
+                   uint64_t k, int metric, uint32_t *h_ids, int device) {
+    if (!h_base || !h_q || !h_ids || !nb || !nq || !dim || !k || k > nb ||
+        k > (uint64_t)kSelectMaxProbe || nb > 0x7FFFFFFF)
+        return CORA_ERR_INVALID_ARGUMENT;
+    TCHK(hipSetDevice(device));
+    const size_t qchunk = std::max<size_t>(1, std::min<size_t>(nq, (size_t)(2ull << 30) / (nb * 4)));
+    DevBuf b, bn, q, qn, dist, ids;
+    if (dev<float>(b, nb * dim) || dev<float>(bn, nb) || dev<float>(q, qchunk * dim) ||
+        dev<float>(qn, qchunk) || dev<float>(dist, qchunk * nb) || dev<int32_t>(ids, qchunk * k))
+        return CORA_ERR_RUNTIME;
+    TCHK(hipMemcpy(b.p, h_base, nb * dim * 4, hipMemcpyHostToDevice));
+    if (metric == 0)
+        launch_row_norms((float *)b.p, (uint32_t)nb, (uint32_t)dim, (float *)bn.p, nullptr);
+    else
+        TCHK(hipMemset(bn.p, 0, nb * 4));
+    for (size_t s = 0; s < nq; s += qchunk) {
+        const size_t rows = std::min(qchunk, nq - s);
+        TCHK(hipMemcpy(q.p, h_q + s * dim, rows * dim * 4, hipMemcpyHostToDevice));
+        if (metric == 0) {
+            launch_row_norms((float *)q.p, (uint32_t)rows, (uint32_t)dim, (float *)qn.p, nullptr);
+            launch_dist_gemm((float *)q.p, (float *)qn.p, (float *)b.p, (float *)bn.p,
+                             (uint32_t)rows, (uint32_t)nb, (uint32_t)dim, (float *)dist.p, nullptr);
+        } else {
+            // an[m] + bn[n] - 2 * ip with zero norms = -2 ip: same order as -ip
+            TCHK(hipMemset(qn.p, 0, rows * 4));
+            launch_dist_gemm((float *)q.p, (float *)qn.p, (float *)b.p, (float *)bn.p,
+                             (uint32_t)rows, (uint32_t)nb, (uint32_t)dim, (float *)dist.p, nullptr);
+        }
+        launch_select((float *)dist.p, (uint32_t)rows, (uint32_t)nb, (uint32_t)k, (int32_t *)ids.p,
+                      nullptr);
+        TCHK(hipGetLastError());
+        TCHK(hipMemcpy(h_ids + s * k, ids.p, rows * k * 4, hipMemcpyDeviceToHost));
+    }
+    return CORA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,432 @@
+// IVF file I/O, SearchData adaptation and index construction (host side of the
+// "src/index" layer). See include/coraanns/index/*.hpp for the formats.
+#include <omp.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <fstream>
+#include <limits>
+#include <numeric>
+#include <queue>
+#include <stdexcept>
+#include <utility>
+#include <vector>
+
+#include "coraanns/index/ivf_builder.hpp"
+#include "coraanns/index/ivf_file.hpp"
+#include "coraanns/index/search_data.hpp"
+
+namespace coraanns::index {
+namespace {
+
+// FastScan interleave of 16 vectors in a 32-vector block (fastscan.hpp:40-42).
+constexpr int kPerm0[16] = {0, 8, 1, 9, 2, 10, 3, 11, 4, 12, 5, 13, 6, 14, 7, 15};
+
+template <class T>
+void read_exact(std::ifstream &in, T *dst, std::size_t count, const char *what) {
+    in.read(reinterpret_cast<char *>(dst), static_cast<std::streamsize>(count * sizeof(T)));
+    if (!in)
+        throw std::runtime_error(std::string("truncated IVF index while reading ") + what);
+}
+
+template <class T>
+void write_all(std::ofstream &out, const T *src, std::size_t count) {
+    out.write(reinterpret_cast<const char *>(src), static_cast<std::streamsize>(count * sizeof(T)));
+}
+
+std::size_t round_up(std::size_t v, std::size_t m) { return (v + m - 1) / m * m; }
+
+}  // namespace
+
+IvfFile IvfFile::load(const std::string &path) {
+    std::ifstream in(path, std::ios::binary);
+    if (!in)
+        throw std::runtime_error("Cannot open IVF index: " + path);
+    IvfFile f;
+    uint64_t hdr[4];
+    read_exact(in, hdr, 4, "header");
+    f.num = hdr[0];
+    f.dim = hdr[1];
+    f.nlist = hdr[2];
+    f.ex_bits = hdr[3];
+    read_exact(in, &f.rotator_type, 1, "rotator type");
+    read_exact(in, &f.metric, 1, "metric");
+    if (f.rotator_type != 0)
+        throw std::runtime_error("only MatrixRotator indexes are supported");
+    if (f.metric > 1 || f.ex_bits > 8 || f.dim == 0 || f.nlist == 0 || f.num == 0)
+        throw std::runtime_error("invalid IVF header");
+    f.padded_dim = round_up(f.dim, 64);
+    f.cluster_sizes.resize(f.nlist);
+    read_exact(in, f.cluster_sizes.data(), f.nlist, "cluster sizes");
+    uint64_t total = 0, blocks = 0;
+    for (uint64_t s : f.cluster_sizes) {
+        total += s;
+        blocks += (s + 31) / 32;
+    }
+    if (total != f.num)
+        throw std::runtime_error("The sum of cluster num != total number of points");
+    f.rotator.resize(f.dim * f.padded_dim);
+    read_exact(in, f.rotator.data(), f.rotator.size(), "rotator");
+    const std::streampos here = in.tellg();
+    in.seekg(0, std::ios::end);
+    const std::streampos end = in.tellg();
+    in.seekg(here);
+    const uint64_t remaining = static_cast<uint64_t>(end - here);
+    const uint64_t batch_bytes = blocks * f.batch_block_bytes();
+    const uint64_t payload = batch_bytes + f.ex_stride() * f.num + 4 * f.num;
+    const uint64_t cent_bytes = 4 * f.padded_dim * f.nlist;
+    if (remaining == payload)
+        throw std::runtime_error("IVF index keeps its centroids in an HNSW sidecar; unsupported");
+    if (remaining != payload + cent_bytes)
+        throw std::runtime_error("IVF index size does not match a supported centroid layout");
+    f.centroids.resize(f.nlist * f.padded_dim);
+    read_exact(in, f.centroids.data(), f.centroids.size(), "centroids");
+    f.batch_data.resize(batch_bytes);
+    read_exact(in, f.batch_data.data(), batch_bytes, "batch data");
+    f.ex_data.resize(f.ex_stride() * f.num);
+    read_exact(in, f.ex_data.data(), f.ex_data.size(), "ex data");
+    f.ids.resize(f.num);
+    read_exact(in, f.ids.data(), f.num, "ids");
+    return f;
+}
+
+void IvfFile::save(const std::string &path) const {
+    std::ofstream out(path, std::ios::binary);
+    if (!out)
+        throw std::runtime_error("Cannot write IVF index: " + path);
+    const uint64_t hdr[4] = {num, dim, nlist, ex_bits};
+    write_all(out, hdr, 4);
+    write_all(out, &rotator_type, 1);
+    write_all(out, &metric, 1);
+    write_all(out, cluster_sizes.data(), cluster_sizes.size());
+    write_all(out, rotator.data(), rotator.size());
+    write_all(out, centroids.data(), centroids.size());
+    write_all(out, batch_data.data(), batch_data.size());
+    write_all(out, ex_data.data(), ex_data.size());
+    write_all(out, ids.data(), ids.size());
+    if (!out)
+        throw std::runtime_error("failed writing IVF index: " + path);
+}
+
+void unpack_fastscan_block(const uint8_t *codes, std::size_t P, std::size_t batch_len,
+                           uint32_t *out_words) {
+    int inv[16];
+    for (int j = 0; j < 16; ++j)
+        inv[kPerm0[j]] = j;
+    const std::size_t W = P / 32;
+    for (std::size_t v = 0; v < batch_len; ++v) {
+        const int slot = inv[v % 16];
+        const bool high = v >= 16;
+        for (std::size_t w = 0; w < W; ++w) {
+            uint32_t word = 0;
+            for (int l = 0; l < 32; ++l) {
+                const std::size_t d = w * 32 + l;
+                const std::size_t in_group = d % 8;
+                const uint8_t byte = codes[(d / 8) * 32 + (in_group < 4 ? 0 : 16) + slot];
+                const uint8_t nib = high ? (byte >> 4) : (byte & 0x0F);
+                word |= static_cast<uint32_t>((nib >> (3 - in_group % 4)) & 1u) << (31 - l);
+            }
+            out_words[v * W + w] = word;
+        }
+    }
+}
+
+SearchData::SearchData(IvfFile &src, bool include_extended, int cpu_threads) {
+    const std::size_t P = src.padded_dim, W = P / 32, N = src.num;
+    h_centroids = src.centroids;
+    host_rotator = src.rotator;
+    cluster_sizes.assign(src.cluster_sizes.begin(), src.cluster_sizes.end());
+    for (std::size_t s : cluster_sizes)
+        max_cluster_size = std::max(max_cluster_size, s);
+    host_short_data.assign(N * W, 0u);
+    host_short_factors.assign(N * 3, 0.0f);
+    // block offsets per cluster so clusters can be unpacked in parallel
+    std::vector<std::size_t> start(src.nlist), block0(src.nlist);
+    std::size_t g = 0, b = 0;
+    for (std::size_t c = 0; c < src.nlist; ++c) {
+        start[c] = g;
+        block0[c] = b;
+        g += cluster_sizes[c];
+        b += (cluster_sizes[c] + 31) / 32;
+    }
+    const std::size_t block_bytes = src.batch_block_bytes();
+    const int threads = cpu_threads > 0 ? cpu_threads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 16) num_threads(threads)
+    for (long long cl = 0; cl < static_cast<long long>(src.nlist); ++cl) {
+        const std::size_t c = static_cast<std::size_t>(cl);
+        const std::size_t n = cluster_sizes[c], s = start[c];
+        std::vector<uint32_t> words(32 * W);
+        for (std::size_t i = 0; i < n; i += 32) {
+            const uint8_t *blk = src.batch_data.data() + (block0[c] + i / 32) * block_bytes;
+            const std::size_t len = std::min<std::size_t>(32, n - i);
+            unpack_fastscan_block(blk, P, len, words.data());
+            const float *fl = reinterpret_cast<const float *>(blk + P * 4);
+            for (std::size_t v = 0; v < len; ++v) {
+                for (std::size_t w = 0; w < W; ++w)
+                    host_short_data[s * W + w * n + i + v] = words[v * W + w];
+                host_short_factors[(s + i + v) * 3 + 0] = fl[v];
+                host_short_factors[(s + i + v) * 3 + 1] = fl[32 + v];
+                host_short_factors[(s + i + v) * 3 + 2] = fl[64 + v];
+            }
+        }
+    }
+    if (include_extended && src.ex_bits > 0) {
+        const std::size_t lc = src.ex_code_bytes(), stride = src.ex_stride();
+        host_ex_factors.assign(N * 2, 0.0f);
+        extended_storage_ = std::move(src.ex_data);
+        uint8_t *ex = extended_storage_.data();
+        for (std::size_t i = 0; i < N; ++i) {
+            const uint8_t *rec = ex + i * stride;
+            float f[2];
+            std::memcpy(f, rec + lc, sizeof(f));
+            host_ex_factors[2 * i] = f[0];
+            host_ex_factors[2 * i + 1] = f[1];
+            std::memmove(ex + i * lc, rec, lc);  // destination never passes the source
+        }
+        extended_storage_.resize(N * lc);
+        extended_storage_.shrink_to_fit();
+        host_long_codes = extended_storage_.data();
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// Quantizer (rabitq_impl.hpp). Float reductions accumulate in double and round once.
+// ------------------------------------------------------------------------------------
+namespace {
+constexpr float kConstEpsilon = 1.9f;                          // rabitq_impl.hpp:18
+constexpr double kTightStart[9] = {0, 0.15, 0.20, 0.52, 0.59, 0.71, 0.75, 0.77, 0.81};  // :263-273
+
+// best_rescale_factor (rabitq_impl.hpp:276-333): sweep t upward through the points where
+// some coordinate's code increments and keep the t maximising <code + 1/2, |o|> / ||code + 1/2||.
+double best_rescale_factor(const float *o_abs, std::size_t dim, std::size_t ex_bits) {
+    constexpr double kEps = 1e-5;
+    constexpr int kNEnum = 10;
+    const double max_o = *std::max_element(o_abs, o_abs + dim);
+    const double t_end = static_cast<double>(((1 << ex_bits) - 1) + kNEnum) / max_o;
+    const double t_start = t_end * kTightStart[ex_bits];
+    std::vector<int> cur(dim);
+    double sqr_den = static_cast<double>(dim) * 0.25;
+    double num = 0;
+    for (std::size_t i = 0; i < dim; ++i) {
+        const int c = static_cast<int>((t_start * o_abs[i]) + kEps);
+        cur[i] = c;
+        sqr_den += c * c + c;
+        num += (c + 0.5) * o_abs[i];
+    }
+    using Item = std::pair<double, std::size_t>;
+    std::priority_queue<Item, std::vector<Item>, std::greater<>> next;
+    for (std::size_t i = 0; i < dim; ++i)
+        next.emplace(static_cast<double>(cur[i] + 1) / o_abs[i], i);
+    double best_ip = 0, best_t = 0;
+    while (!next.empty()) {
+        const double t = next.top().first;
+        const std::size_t id = next.top().second;
+        next.pop();
+        const int v = ++cur[id];
+        sqr_den += 2 * v;
+        num += o_abs[id];
+        const double ip = num / std::sqrt(sqr_den);
+        if (ip > best_ip) {
+            best_ip = ip;
+            best_t = t;
+        }
+        if (v < (1 << ex_bits) - 1) {
+            const double tn = static_cast<double>(v + 1) / o_abs[id];
+            if (tn < t_end)
+                next.emplace(tn, id);
+        }
+    }
+    return best_t;
+}
+
+double dot(const float *a, const float *b, std::size_t n) {
+    double s = 0;
+    for (std::size_t i = 0; i < n; ++i)
+        s += static_cast<double>(a[i]) * b[i];
+    return s;
+}
+}  // namespace
+
+void quantize_one_bit(const float *x, const float *c, std::size_t P, uint8_t *bits, float *f,
+                      int metric) {
+    std::vector<float> o(P), xu(P);
+    for (std::size_t i = 0; i < P; ++i) {
+        o[i] = x[i] - c[i];
+        bits[i] = o[i] > 0 ? 1 : 0;
+        xu[i] = static_cast<float>(bits[i]) - 0.5f;
+    }
+    const float l2_sqr = static_cast<float>(dot(o.data(), o.data(), P));
+    const float l2 = std::sqrt(l2_sqr);
+    float ip_resi = static_cast<float>(dot(o.data(), xu.data(), P));
+    const float ip_cent = static_cast<float>(dot(c, xu.data(), P));
+    if (ip_resi == 0)
+        ip_resi = std::numeric_limits<float>::infinity();
+    const float xu_sqr = static_cast<float>(dot(xu.data(), xu.data(), P));
+    const float err = l2 * kConstEpsilon *
+                      std::sqrt((((l2_sqr * xu_sqr) / (ip_resi * ip_resi)) - 1) /
+                                static_cast<float>(P - 1));
+    if (metric == 0) {
+        f[0] = l2_sqr + (2 * l2_sqr * ip_cent / ip_resi);
+        f[1] = -2 * l2_sqr / ip_resi;
+        f[2] = 2 * err;
+    } else {
+        f[0] = 1 - static_cast<float>(dot(o.data(), c, P)) + (l2_sqr * ip_cent / ip_resi);
+        f[1] = -l2_sqr / ip_resi;
+        f[2] = err;
+    }
+}
+
+void quantize_ex_bits(const float *x, const float *c, std::size_t P, std::size_t ex_bits,
+                      uint8_t *code, float *f, int metric) {
+    std::vector<float> o(P), o_abs(P);
+    for (std::size_t i = 0; i < P; ++i)
+        o[i] = x[i] - c[i];
+    const float norm = std::sqrt(static_cast<float>(dot(o.data(), o.data(), P)));
+    for (std::size_t i = 0; i < P; ++i)
+        o_abs[i] = std::fabs(o[i] / norm);
+    // quantize_ex (rabitq_impl.hpp:336-360)
+    constexpr double kEps = 1e-5;
+    const double t = best_rescale_factor(o_abs.data(), P, ex_bits);
+    const int cap = (1 << ex_bits) - 1;
+    double ipnorm = 0;
+    for (std::size_t i = 0; i < P; ++i) {
+        int v = static_cast<int>((t * o_abs[i]) + kEps);
+        v = std::min(v, cap);
+        code[i] = static_cast<uint8_t>(v);
+        ipnorm += (v + 0.5) * o_abs[i];
+    }
+    float ipnorm_inv = static_cast<float>(1 / ipnorm);
+    if (!std::isnormal(ipnorm_inv))
+        ipnorm_inv = 1.0f;
+    // negative residual dimensions store the bitwise complement (rabitq_impl.hpp:423-429)
+    for (std::size_t i = 0; i < P; ++i)
+        if (o[i] < 0)
+            code[i] = static_cast<uint8_t>((~code[i]) & cap);
+    // factors on total_code = code + (o >= 0) * 2^ex (rabitq_impl.hpp:455-499)
+    std::vector<float> xu(P);
+    const float cb = -(static_cast<float>(1 << ex_bits) - 0.5f);
+    for (std::size_t i = 0; i < P; ++i)
+        xu[i] = static_cast<float>(code[i] + ((o[i] >= 0) ? (1 << ex_bits) : 0)) + cb;
+    const float l2_sqr = static_cast<float>(dot(o.data(), o.data(), P));
+    const float l2 = std::sqrt(l2_sqr);
+    float ip_resi = static_cast<float>(dot(o.data(), xu.data(), P));
+    const float ip_cent = static_cast<float>(dot(c, xu.data(), P));
+    if (ip_resi == 0)
+        ip_resi = std::numeric_limits<float>::infinity();
+    if (metric == 0) {
+        f[0] = l2_sqr + (2 * l2_sqr * ip_cent / ip_resi);
+        f[1] = ipnorm_inv * -2 * l2;
+    } else {
+        f[0] = 1 - static_cast<float>(dot(o.data(), c, P)) + (l2_sqr * ip_cent / ip_resi);
+        f[1] = ipnorm_inv * -l2;
+    }
+}
+
+void pack_excode7(const uint8_t *code, std::size_t P, uint8_t *out) {
+    for (std::size_t g = 0; g < P; g += 64) {
+        const uint8_t *v = code + g;
+        uint8_t *o = out + g / 64 * 56;
+        for (int i = 0; i < 16; ++i) {
+            const uint8_t hi = v[48 + i];
+            o[i] = static_cast<uint8_t>((v[i] & 0x3F) | ((hi << 6) & 0xC0));
+            o[16 + i] = static_cast<uint8_t>((v[16 + i] & 0x3F) | ((hi << 4) & 0xC0));
+            o[32 + i] = static_cast<uint8_t>((v[32 + i] & 0x3F) | ((hi << 2) & 0xC0));
+        }
+        uint64_t top = 0;
+        for (int d = 0; d < 64; ++d)
+            top |= static_cast<uint64_t>((v[d] >> 6) & 1) << (8 * (d % 8) + d / 8);
+        std::memcpy(o + 48, &top, 8);
+    }
+}
+
+void fastscan_pack(const uint8_t *compact, std::size_t n, std::size_t P, uint8_t *blocks) {
+    const std::size_t cols = P / 8;
+    const std::size_t nb = (n + 31) / 32;
+    for (std::size_t b = 0; b < nb; ++b) {
+        for (std::size_t col = 0; col < cols; ++col) {
+            uint8_t hi[32], lo[32];
+            for (int r = 0; r < 32; ++r) {
+                const std::size_t row = b * 32 + r;
+                const uint8_t v = row < n ? compact[row * cols + col] : 0;
+                hi[r] = v >> 4;
+                lo[r] = v & 15;
+            }
+            uint8_t *o = blocks + (b * cols + col) * 32;
+            for (int j = 0; j < 16; ++j) {
+                o[j] = static_cast<uint8_t>(hi[kPerm0[j]] | (hi[kPerm0[j] + 16] << 4));
+                o[j + 16] = static_cast<uint8_t>(lo[kPerm0[j]] | (lo[kPerm0[j] + 16] << 4));
+            }
+        }
+    }
+}
+
+IvfFile build_ivf(const BuildInput &in, int threads) {
+    if (!in.rotated_data || !in.rotated_centroids || !in.assignments || !in.rotator || !in.n ||
+        !in.dim || in.padded_dim % 64 || in.padded_dim < in.dim || !in.nlist || in.ex_bits != 7)
+        throw std::invalid_argument("build_ivf: invalid input (ex_bits must be 7)");
+    const std::size_t P = in.padded_dim;
+    IvfFile f;
+    f.num = in.n;
+    f.dim = in.dim;
+    f.padded_dim = P;
+    f.nlist = in.nlist;
+    f.ex_bits = in.ex_bits;
+    f.metric = static_cast<uint8_t>(in.metric);
+    f.rotator.assign(in.rotator, in.rotator + in.dim * P);
+    f.centroids.assign(in.rotated_centroids, in.rotated_centroids + in.nlist * P);
+    f.cluster_sizes.assign(in.nlist, 0);
+    for (std::size_t i = 0; i < in.n; ++i) {
+        if (in.assignments[i] >= in.nlist)
+            throw std::invalid_argument("build_ivf: bad cluster id");
+        ++f.cluster_sizes[in.assignments[i]];
+    }
+    std::vector<std::size_t> start(in.nlist + 1, 0), block0(in.nlist + 1, 0);
+    for (std::size_t c = 0; c < in.nlist; ++c) {
+        start[c + 1] = start[c] + f.cluster_sizes[c];
+        block0[c + 1] = block0[c] + (f.cluster_sizes[c] + 31) / 32;
+    }
+    f.ids.resize(in.n);
+    {
+        std::vector<std::size_t> fill(start.begin(), start.end() - 1);
+        for (std::size_t i = 0; i < in.n; ++i)
+            f.ids[fill[in.assignments[i]]++] = static_cast<uint32_t>(i);
+    }
+    const std::size_t block_bytes = f.batch_block_bytes(), stride = f.ex_stride();
+    const std::size_t lc = f.ex_code_bytes();
+    f.batch_data.assign(block0[in.nlist] * block_bytes, 0);
+    f.ex_data.assign(in.n * stride, 0);
+    const int nt = threads > 0 ? threads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+    for (long long cl = 0; cl < static_cast<long long>(in.nlist); ++cl) {
+        const std::size_t c = static_cast<std::size_t>(cl);
+        const std::size_t n = f.cluster_sizes[c];
+        const float *cent = in.rotated_centroids + c * P;
+        std::vector<uint8_t> bits(P), compact(32 * P / 8), code(P);
+        for (std::size_t i0 = 0; i0 < n; i0 += 32) {
+            const std::size_t len = std::min<std::size_t>(32, n - i0);
+            uint8_t *blk = f.batch_data.data() + (block0[c] + i0 / 32) * block_bytes;
+            float *fl = reinterpret_cast<float *>(blk + P * 4);
+            std::fill(compact.begin(), compact.end(), 0);
+            for (std::size_t v = 0; v < len; ++v) {
+                const std::size_t gi = start[c] + i0 + v;
+                const float *x = in.rotated_data + static_cast<std::size_t>(f.ids[gi]) * P;
+                float f1[3], f2[2];
+                quantize_one_bit(x, cent, P, bits.data(), f1, in.metric);
+                for (std::size_t d = 0; d < P; ++d)
+                    compact[v * (P / 8) + d / 8] |= static_cast<uint8_t>(bits[d] << (7 - d % 8));
+                fl[v] = f1[0];
+                fl[32 + v] = f1[1];
+                fl[64 + v] = f1[2];
+                quantize_ex_bits(x, cent, P, in.ex_bits, code.data(), f2, in.metric);
+                uint8_t *rec = f.ex_data.data() + gi * stride;
+                pack_excode7(code.data(), P, rec);
+                std::memcpy(rec + lc, f2, sizeof(f2));
+            }
+            fastscan_pack(compact.data(), len, P, blk);
+        }
+    }
+    return f;
+}
+
+}  // namespace coraanns::index

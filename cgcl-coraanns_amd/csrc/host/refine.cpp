@@ -1,0 +1,250 @@
+// CPU refinement: the OpenMP consumer of the GPU->CPU candidate ring.
+//
+// Semantics of the reference consumer (src/search/cpu_refinement.cpp:71-284):
+//  * workers claim chunks of min(8192, capacity) consecutive ring positions from a shared
+//    read head; a claim in a later ring generation waits until its generation is live;
+//  * a slot is complete when none of its four 32-bit words holds the empty pattern (no
+//    field of a published Candidate can be all ones: query < 65535, gid < 2^32-1, and
+//    exact_ip / low_dist are finite), so a record is never read half-written even if the
+//    16-byte GPU store reaches host memory in pieces; the wait ends at done && position
+//    >= produced, or on overflow;
+//  * secondary filter: skip when low_dist >= threshold[query];
+//  * refine = f_ex_add + g_add + f_ex_rescale * (2^ex * exact_ip + <q', ex_code> + kbxSumq)
+//    (or the exact squared L2 distance to the base vector), inserted into the query's
+//    sorted top-k under a per-query spinlock; a full top-k publishes its k-th distance as
+//    the query's threshold, which the GPU filter reads;
+//  * a processed chunk is cleared to the empty pattern before its release, and released
+//    only as part of a contiguous prefix (ReleaseTracker).
+#include "refine.hpp"
+
+#include <immintrin.h>
+#include <omp.h>
+
+#include <atomic>
+#include <cfloat>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <stdexcept>
+#include <vector>
+
+#include "coraanns/queue/release_tracker.hpp"
+
+namespace coraanns::detail {
+
+float excode_ip7(const float *q, const uint8_t *packed, std::size_t P) {
+    __m256 acc0 = _mm256_setzero_ps(), acc1 = _mm256_setzero_ps();
+    constexpr uint64_t kLow6 = 0x3F3F3F3F3F3F3F3Full;
+    constexpr uint64_t kOnes = 0x0101010101010101ull;
+    for (std::size_t g = 0; g < P; g += 64) {
+        const uint8_t *c = packed + g / 64 * 56;
+        const float *qq = q + g;
+        uint64_t top;
+        std::memcpy(&top, c + 48, 8);
+        for (int k = 0; k < 8; ++k) {  // dimensions 8k .. 8k+7 of the group
+            uint64_t v;
+            if (k < 6) {
+                std::memcpy(&v, c + 8 * k, 8);
+                v &= kLow6;
+            } else {
+                uint64_t a, b, d;
+                const int off = (k - 6) * 8;
+                std::memcpy(&a, c + off, 8);
+                std::memcpy(&b, c + 16 + off, 8);
+                std::memcpy(&d, c + 32 + off, 8);
+                v = ((a >> 6) & 0x0303030303030303ull) | ((b >> 4) & 0x0C0C0C0C0C0C0C0Cull) |
+                    ((d >> 2) & 0x3030303030303030ull);
+            }
+            v |= ((top >> k) & kOnes) << 6;
+            const __m256 cf = _mm256_cvtepi32_ps(_mm256_cvtepu8_epi32(_mm_cvtsi64_si128((long long)v)));
+            if (k & 1)
+                acc1 = _mm256_fmadd_ps(cf, _mm256_loadu_ps(qq + 8 * k), acc1);
+            else
+                acc0 = _mm256_fmadd_ps(cf, _mm256_loadu_ps(qq + 8 * k), acc0);
+        }
+    }
+    const __m256 s = _mm256_add_ps(acc0, acc1);
+    __m128 h = _mm_add_ps(_mm256_castps256_ps128(s), _mm256_extractf128_ps(s, 1));
+    h = _mm_add_ps(h, _mm_movehl_ps(h, h));
+    h = _mm_add_ss(h, _mm_movehdup_ps(h));
+    return _mm_cvtss_f32(h);
+}
+
+namespace {
+
+inline bool slot_complete(const queue::Candidate *slot, queue::Candidate &out) {
+    const __m128i v = _mm_load_si128(reinterpret_cast<const __m128i *>(slot));
+    const __m128i empty = _mm_set1_epi32(-1);
+    if (_mm_movemask_epi8(_mm_cmpeq_epi32(v, empty)) != 0)
+        return false;
+    _mm_store_si128(reinterpret_cast<__m128i *>(&out), v);
+    return true;
+}
+
+inline void clear_slots(queue::Candidate *slots, std::size_t n) {
+    const __m128i empty = _mm_set1_epi32(-1);
+    for (std::size_t i = 0; i < n; ++i)
+        _mm_store_si128(reinterpret_cast<__m128i *>(slots + i), empty);
+}
+
+inline float load_threshold(const float *t, std::size_t q) {
+    uint32_t bits = __atomic_load_n(reinterpret_cast<const uint32_t *>(t) + q, __ATOMIC_RELAXED);
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+inline void store_threshold(float *t, std::size_t q, float v) {
+    uint32_t bits;
+    std::memcpy(&bits, &v, 4);
+    __atomic_store_n(reinterpret_cast<uint32_t *>(t) + q, bits, __ATOMIC_RELAXED);
+}
+
+struct alignas(64) QuerySlot {
+    std::atomic_flag lock = ATOMIC_FLAG_INIT;
+    int count = 0;
+};
+
+}  // namespace
+
+RefineOut cpu_refine(const RefineArgs &a, std::size_t nq, std::size_t topk, float *h_dists,
+                     uint32_t *h_pids) {
+    using queue::Position;
+    const bool exact = a.base_mapping != nullptr;
+    const std::size_t P = a.padded_dim;
+    const std::size_t lc = (P * a.ex_bits + 7) / 8;
+    const float scale = static_cast<float>(1u << a.ex_bits);
+    const std::size_t kstride = (topk + 15) / 16 * 16;
+    std::vector<float> td(nq * kstride);
+    std::vector<uint32_t> tp(nq * kstride);
+    std::unique_ptr<QuerySlot[]> slots(new QuerySlot[nq]);
+    const Position capacity = a.capacity, mask = capacity - 1;
+    const Position chunk = std::min<Position>(queue::consumer_chunk, capacity);
+    std::atomic<Position> head{0};
+    queue::ReleaseTracker tracker(*a.progress, capacity, chunk);
+    queue::Progress *pg = a.progress;
+    auto done = [&] { return __atomic_load_n(&pg->done, __ATOMIC_ACQUIRE) != 0; };
+    auto aborted = [&] { return __atomic_load_n(&pg->overflow, __ATOMIC_ACQUIRE) != 0; };
+    auto produced = [&] { return __atomic_load_n(&pg->produced, __ATOMIC_ACQUIRE); };
+    std::atomic<std::size_t> refined_total{0};
+    const int threads = a.threads > 0 ? a.threads : omp_get_max_threads();
+
+#pragma omp parallel num_threads(threads)
+    {
+        std::size_t refined = 0;
+        bool stop = false;
+        while (!stop && !aborted()) {
+            const Position start = head.fetch_add(chunk, std::memory_order_relaxed);
+            if (done() && start >= produced())
+                break;
+            if (start >= capacity) {
+                while (!tracker.readable_generation(start)) {
+                    if (aborted() || (done() && start >= produced())) {
+                        stop = true;
+                        break;
+                    }
+                    _mm_pause();
+                }
+                if (stop)
+                    break;
+            }
+            Position consumed = 0;
+            for (Position i = 0; i < chunk; ++i) {
+                const Position pos = start + i;
+                queue::Candidate *slot = &a.items[pos & mask];
+                queue::Candidate rec;
+                while (!slot_complete(slot, rec)) {
+                    if (aborted() || (done() && pos >= produced())) {
+                        stop = true;
+                        break;
+                    }
+                    _mm_pause();
+                }
+                if (stop)
+                    break;
+                ++consumed;
+                const std::size_t q = rec.query_idx;
+                if (q >= nq)
+                    continue;  // defensive: never produced by the engine
+                if (a.secondary_filter && rec.low_dist >= load_threshold(a.thresholds, q))
+                    continue;
+                float dist;
+                if (exact) {
+                    const uint32_t pid = a.ids[rec.gid];
+                    if (pid >= a.base_rows || a.base_dim != a.dim)
+                        continue;
+                    const float *x = reinterpret_cast<const float *>(
+                        a.base_mapping + a.base_offset + static_cast<std::size_t>(pid) * a.base_stride);
+                    const float *qv = a.raw_queries + q * a.dim;
+                    float s = 0.0f;
+#pragma omp simd reduction(+ : s)
+                    for (std::size_t d = 0; d < a.dim; ++d) {
+                        const float diff = qv[d] - x[d];
+                        s += diff * diff;
+                    }
+                    dist = s;
+                } else {
+                    const float ip2 = excode_ip7(a.rotated_queries + q * P,
+                                                 a.long_codes + static_cast<std::size_t>(rec.gid) * lc, P);
+                    const float g_add = a.probe_gadd[q * a.nprobe + rec.probe_idx];
+                    const float f_add = a.ex_factors[2 * static_cast<std::size_t>(rec.gid)];
+                    const float f_rescale = a.ex_factors[2 * static_cast<std::size_t>(rec.gid) + 1];
+                    dist = f_add + g_add + f_rescale * (scale * rec.exact_ip + ip2 + a.kbxsumq[q]);
+                }
+                ++refined;
+                if (dist >= load_threshold(a.thresholds, q))
+                    continue;
+                QuerySlot &s = slots[q];
+                while (s.lock.test_and_set(std::memory_order_acquire))
+                    _mm_pause();
+                float *d = td.data() + q * kstride;
+                uint32_t *p = tp.data() + q * kstride;
+                const uint32_t pid = a.ids[rec.gid];
+                if (s.count < static_cast<int>(topk)) {
+                    int i = s.count - 1;
+                    while (i >= 0 && d[i] > dist) {
+                        d[i + 1] = d[i];
+                        p[i + 1] = p[i];
+                        --i;
+                    }
+                    d[i + 1] = dist;
+                    p[i + 1] = pid;
+                    if (++s.count == static_cast<int>(topk))
+                        store_threshold(a.thresholds, q, d[topk - 1]);
+                } else if (dist < d[topk - 1]) {
+                    int i = static_cast<int>(topk) - 2;
+                    while (i >= 0 && d[i] > dist) {
+                        d[i + 1] = d[i];
+                        p[i + 1] = p[i];
+                        --i;
+                    }
+                    d[i + 1] = dist;
+                    p[i + 1] = pid;
+                    store_threshold(a.thresholds, q, d[topk - 1]);
+                }
+                s.lock.clear(std::memory_order_release);
+            }
+            if (consumed != 0) {
+                clear_slots(&a.items[start & mask], static_cast<std::size_t>(chunk));
+                tracker.complete(start);
+            }
+        }
+        refined_total.fetch_add(refined, std::memory_order_relaxed);
+    }
+
+    RefineOut out;
+    out.produced = produced();
+    out.refined = refined_total.load();
+    out.aborted = aborted();
+    for (std::size_t q = 0; q < nq; ++q) {
+        const int n = slots[q].count;
+        for (int i = 0; i < static_cast<int>(topk); ++i) {
+            h_dists[q * topk + i] = i < n ? td[q * kstride + i] : FLT_MAX;
+            h_pids[q * topk + i] = i < n ? tp[q * kstride + i] : 0u;
+        }
+    }
+    return out;
+}
+
+}  // namespace coraanns::detail

@@ -1,0 +1,195 @@
+/*
+ * cora_gpu.h — C-ABI of the MI355X (gfx950) GPU filter engine for IVF-RaBitQ search.
+ *
+ * This is the GPU half of the reference's coraanns::HybridIndex
+ * (include/coraanns/search/hybrid.cuh:18-203, src/search/hybrid.cu:35-689): index
+ * residency in HBM, query preparation, coarse probing, pair scheduling, the RaBitQ
+ * 1-bit popcount scan with shared-threshold filtering, and the device side of the
+ * GPU->CPU candidate ring (src/search/ring_queue.cuh). The CPU half (ex-code
+ * refinement consuming the ring) and the C++ HybridIndex shim live in libcoraanns and
+ * call these functions. Plain C types only: no HIP, torch or C++ types cross this ABI.
+ *
+ * Every entry point returns CORA_OK or one of the CORA_ERR_* codes below; the message
+ * of the last failure on an engine is available from cora_gpu_last_error(). The C++
+ * shim maps CORA_ERR_INVALID_ARGUMENT -> std::invalid_argument, CORA_ERR_LOGIC ->
+ * std::logic_error and everything else -> std::runtime_error, matching the exception
+ * types the reference throws (hybrid.cu:88-121,236-237,401-404,669-673;
+ * src/search/cuda_error.hpp:8-16).
+ *
+ * Threading: one search at a time per engine (reference docs/ARCHITECTURE.md:44).
+ */
+#ifndef CORA_GPU_H
+#define CORA_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum cora_status {
+    CORA_OK = 0,
+    CORA_ERR_INVALID_ARGUMENT = 1,
+    CORA_ERR_LOGIC = 2,
+    CORA_ERR_RUNTIME = 3,
+    CORA_ERR_SPILL_EXHAUSTED = 4,
+    CORA_ERR_OUT_OF_MEMORY = 5,
+    CORA_ERR_QUEUE_STALLED = 6
+};
+
+enum cora_metric { CORA_METRIC_L2 = 0, CORA_METRIC_IP = 1 }; /* rabitqlib MetricType (defines.hpp:65) */
+
+/* Search flags (cora_search_args.flags). */
+enum cora_search_flags {
+    /* The filter reads a device snapshot of the thresholds taken at launch instead of
+     * the live host array the CPU tightens (deterministic candidate sets; the reference
+     * has only the live mode, hybrid.cu:251-253). */
+    CORA_FLAG_FROZEN_THRESHOLDS = 1u << 0,
+    /* Record HIP events around the scan kernels (reference set_gpu_filter_timing,
+     * hybrid.cu:538-540,655-657). */
+    CORA_FLAG_FILTER_TIMING = 1u << 1,
+    /* Cross-query reuse: batch up to batch_q same-cluster pairs per pass
+     * (reference set_cross_query_reuse, hybrid.cu:594-597). */
+    CORA_FLAG_CROSS_QUERY_REUSE = 1u << 2
+};
+
+typedef struct cora_gpu_engine cora_gpu_engine;
+
+/* Host view of the GPU->CPU candidate ring. Byte layout of items/progress is
+ * coraanns::queue::Candidate[capacity] / coraanns::queue::Progress
+ * (include/coraanns/queue/candidate_queue.hpp:10-55). All pointers are host
+ * addresses of host-coherent pinned memory the GPU reads and writes. */
+typedef struct cora_queue_view {
+    void *items;
+    void *progress;
+    uint64_t capacity;
+    float *thresholds; /* [max_queries], read by the GPU filter, written by the CPU */
+    int *abort_flag;   /* host sets 1 to stop the queue drain kernel waiting */
+} cora_queue_view;
+
+typedef struct cora_search_args {
+    uint32_t num_queries;
+    uint32_t topk;
+    uint32_t nprobe;
+    uint32_t batch_q;  /* 1..8 same-cluster pairs per scan pass (reference accepts 1..6) */
+    uint32_t vanguard; /* vanguard depth: pairs with probe rank < vanguard are scanned first */
+    uint32_t flags;    /* cora_search_flags */
+} cora_search_args;
+
+typedef struct cora_search_stats {
+    uint64_t produced;      /* candidates published (reference Progress::produced) */
+    uint64_t spilled;       /* candidates that went through the HBM spill buffer */
+    int32_t overflow;       /* spill capacity exhausted */
+    int32_t stalled;        /* the drain kernel gave up waiting for ring space */
+    float filter_ms;        /* all scan kernels (FILTER_TIMING only) */
+    float scan_ms;          /* the far-pair scan kernel alone (FILTER_TIMING only) */
+    uint64_t scan_bytes;    /* algorithmic code+factor bytes the far-pair scan read */
+    uint64_t scan_units;    /* cluster passes the far-pair scan made */
+    uint64_t scan_vectors;  /* vector evaluations (vector x query) of the far-pair scan */
+} cora_search_stats;
+
+/* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */
+int cora_gpu_create(cora_gpu_engine **out, int device);
+int cora_gpu_destroy(cora_gpu_engine *engine);
+/* Copies the last error message (NUL-terminated, truncated to n). */
+int cora_gpu_last_error(const cora_gpu_engine *engine, char *buf, size_t n);
+
+/* Index upload (HybridIndex::load_from_raw_pointers, hybrid.cu:101-164), GPU arrays only.
+ * h_short_data: reference SearchData layout (search_data.cpp:45-82), per-cluster
+ * word-major u32 [num_vecs * padded_dim/32], dimension 32w+l at bit 31-l of word w.
+ * h_short_factors: f32 [num_vecs][3] (f_add, f_rescale, f_error).
+ * h_centroids: f32 [n_centroids][padded_dim] rotated; h_rotator: f32 [dim][padded_dim].
+ * The engine repacks the codes into its own tile layout in HBM. */
+int cora_gpu_load_index(cora_gpu_engine *engine, uint64_t num_vecs, uint64_t dim,
+                        uint64_t padded_dim, uint64_t n_centroids, uint64_t ex_bits, int metric,
+                        const float *h_centroids, const float *h_rotator,
+                        const uint32_t *h_short_data, const float *h_short_factors,
+                        const uint64_t *h_cluster_sizes);
+
+/* Ring sizing before prepare (HybridIndex::set_queue_capacity / set_queue_spill_capacity,
+ * hybrid.cu:166-185). capacity: power of two. */
+int cora_gpu_set_queue(cora_gpu_engine *engine, uint64_t capacity, uint64_t spill_capacity);
+
+/* Workspace (HybridIndex::prepare_workspace / free_workspace, hybrid.cu:235-378). */
+int cora_gpu_prepare_workspace(cora_gpu_engine *engine, uint64_t max_queries, uint64_t max_topk,
+                               uint64_t max_nprobe, uint64_t vanguard_size);
+int cora_gpu_free_workspace(cora_gpu_engine *engine);
+int cora_gpu_queue_view(cora_gpu_engine *engine, cora_queue_view *out);
+
+/* Per-chunk reset (HybridIndex::reset_buffer, hybrid.cu:380-396): uploads the raw
+ * queries f32 [nq][dim], resets device queue counters and the host Progress, and
+ * sets the thresholds of the first nq queries to FLT_MAX. */
+int cora_gpu_reset(cora_gpu_engine *engine, const float *h_queries, uint64_t nq);
+
+/* Enqueue the whole GPU side of HybridIndex::search (hybrid.cu:434-660) and return
+ * without waiting: rotation, query factors and Bq=8 quantisation, coarse probing,
+ * pair scheduling, vanguard seed scan, far-pair scan, vanguard recovery scan, and the
+ * queue drain kernel that publishes produced/spilled and sets Progress::done. */
+int cora_gpu_launch_search(cora_gpu_engine *engine, const cora_search_args *args);
+
+/* Wait until the host-side inputs of CPU refinement are in pinned memory
+ * (hybrid.cu:663) and return pointers to them: rotated queries f32 [nq][P],
+ * kbxSumq f32 [nq], probe g_add f32 [nq][nprobe] (||q'-c'||^2 for L2, -<q',c'> for IP). */
+int cora_gpu_wait_host_inputs(cora_gpu_engine *engine, const float **rotated_queries,
+                              const float **kbxsumq, const float **probe_gadd);
+
+/* Wait for all GPU work of the search and report its counters (hybrid.cu:667-677).
+ * Returns CORA_ERR_SPILL_EXHAUSTED when the spill buffer overflowed (the ring is
+ * cleared), CORA_ERR_QUEUE_STALLED when the drain kernel timed out. */
+int cora_gpu_sync(cora_gpu_engine *engine, cora_search_stats *stats);
+
+/* Threshold snapshot (HybridIndex::capture_thresholds / seed_thresholds,
+ * cpu_refinement.cpp:58-69). */
+int cora_gpu_capture_thresholds(cora_gpu_engine *engine, float *out, uint64_t nq);
+int cora_gpu_seed_thresholds(cora_gpu_engine *engine, const float *in, uint64_t nq);
+
+/* Index and workspace shape queries. */
+int cora_gpu_index_info(const cora_gpu_engine *engine, uint64_t *num_vecs, uint64_t *dim,
+                        uint64_t *padded_dim, uint64_t *n_centroids, uint64_t *max_cluster);
+
+/* Inspection for parity tests: copy an internal array of the last launched search to
+ * host memory. which: see cora_debug_array. bytes must equal the array size. */
+enum cora_debug_array {
+    CORA_DBG_ROTATED_QUERIES = 0, /* f32 [nq][P] */
+    CORA_DBG_K1XSUMQ = 1,         /* f32 [nq] */
+    CORA_DBG_KBXSUMQ = 2,         /* f32 [nq] */
+    CORA_DBG_Q_WIDTH = 3,         /* f32 [nq] Bq=8 quantisation step */
+    CORA_DBG_Q_PLANES = 4,        /* u32 [nq][8][P/32], dim 32w+l at bit l of word w */
+    CORA_DBG_PROBE_IDX = 5,       /* i32 [nq][nprobe] ascending distance */
+    CORA_DBG_PROBE_GADD = 6,      /* f32 [nq][nprobe] */
+    CORA_DBG_PROBE_GERR = 7,      /* f32 [nq][nprobe] */
+    CORA_DBG_PAIRS = 8            /* i32 [npairs][3] (cluster, query, probe), scan order */
+};
+int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t bytes);
+
+/* Dense estimator for parity tests: for every (query, probe) pair of the last launched
+ * search, evaluate every vector of the probed cluster with the scan kernel's estimator
+ * and write ip_int (i32) and low distance (f32) to out_ip / out_low, laid out
+ * [nq][nprobe][max_cluster] (entries past the cluster size are left untouched). */
+int cora_gpu_debug_dense(cora_gpu_engine *engine, int32_t *out_ip, float *out_low,
+                         uint64_t capacity_elems);
+
+/* ---- Index-build and evaluation tools (no counterpart in the reference's search path;
+ * they replace its offline Faiss k-means, tools/data/train_ivf.py:11-47, and the
+ * exhaustive ground-truth tool, tools/data/generate_gt_gpu.py). Host arrays in and out;
+ * each call allocates and frees its own device memory on `device`. ---- */
+const char *cora_tool_last_error(void);
+/* out [n][P] = x [n][dim] . R [dim][P] */
+int cora_tool_rotate(const float *x, uint64_t n, uint64_t dim, const float *R, uint64_t P,
+                     float *out, int device);
+/* Lloyd k-means (squared L2), `iters` iterations from k seeded distinct rows. */
+int cora_tool_kmeans(const float *x, uint64_t n, uint64_t dim, uint64_t k, uint32_t iters,
+                     uint64_t seed, float *centroids, int device);
+/* nearest centroid of every row (ties -> lower centroid id) */
+int cora_tool_assign(const float *x, uint64_t n, uint64_t dim, const float *centroids, uint64_t k,
+                     uint32_t *assign, int device);
+/* exhaustive top-k ids by FP32 distance (metric 0: L2, 1: IP), ascending */
+int cora_tool_topk(const float *base, uint64_t nb, const float *queries, uint64_t nq, uint64_t dim,
+                   uint64_t k, int metric, uint32_t *ids, int device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CORA_GPU_H */

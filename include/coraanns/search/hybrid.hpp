@@ -1,0 +1,140 @@
+// coraanns::HybridIndex — GPU filter / CPU refine IVF-RaBitQ search on MI355X.
+//
+// Drop-in for the reference's include/coraanns/search/hybrid.cuh:18-203: the same public
+// method set, argument meaning, ownership rules and exception types, with no HIP, CUDA
+// or cuBLAS types in the header. The GPU side is the C-ABI engine in cora_gpu.h; this
+// class adds the CPU side: the OpenMP consumer of the candidate ring that refines
+// candidates with the 7-bit ex-codes (or an exact FP32 base) and keeps per-query top-k
+// (reference src/search/cpu_refinement.cpp:71-284).
+//
+// Ownership (reference hybrid.cuh:185, docs/ARCHITECTURE.md:34-38): load_from_raw_pointers
+// copies centroids, rotator, sign codes and short factors to the GPU and borrows the
+// host ex-codes, ex-factors and ids until the engine is destroyed. One search at a time.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "coraanns/queue/candidate_queue.hpp"
+#include "coraanns/search/parameters.hpp"
+
+struct cora_gpu_engine;
+
+namespace coraanns {
+
+enum class KernelType { Lut4Bit, Bitwise };
+
+class HybridIndex {
+  public:
+    explicit HybridIndex(int device = 0);
+    HybridIndex(const HybridIndex &) = delete;
+    HybridIndex &operator=(const HybridIndex &) = delete;
+    ~HybridIndex();
+
+    void set_profiling(bool enabled) { profiling_enabled_ = enabled; }
+    void set_candidate_stats(bool enabled) { candidate_stats_enabled_ = enabled; }
+    void set_gpu_filter_timing(bool enabled) { gpu_filter_timing_enabled_ = enabled; }
+    void set_cross_query_reuse(bool enabled) { cross_query_reuse_enabled_ = enabled; }
+    void set_cpu_secondary_filter(bool enabled) { cpu_secondary_filter_enabled_ = enabled; }
+
+    queue::Position get_last_submitted_count() const { return last_written_count_; }
+    queue::Position get_last_spilled_count() const { return last_spilled_count_; }
+    void set_queue_capacity(std::size_t capacity);
+    void set_queue_spill_capacity(std::size_t capacity);
+    std::size_t get_queue_capacity() const { return queue_capacity_; }
+    std::size_t get_last_refined_count() const { return last_refined_count_; }
+    float get_last_gpu_filter_ms() const { return last_gpu_filter_ms_; }
+
+    void set_vanguard_size(std::size_t size);
+    std::size_t get_vanguard_size() const { return vanguard_size_; }
+
+    // Both kernel types run the same Bq=8 popcount estimator here (the reference's
+    // Bitwise arithmetic, filter_kernels.cuh:79-114); the setting is kept for API parity.
+    void set_ip_kernel_type(KernelType t) { ip_kernel_type_ = t; }
+    KernelType get_ip_kernel_type() const { return ip_kernel_type_; }
+
+    void prepare_workspace(std::size_t max_queries, std::size_t max_topk, std::size_t max_nprobe);
+    void free_workspace() noexcept;
+    void reset_buffer(const float *h_queries, std::size_t num_queries);
+
+    void enable_exact_refine(const uint8_t *base_mapping, std::size_t base_rows,
+                             std::size_t base_dim, std::size_t row_stride_bytes,
+                             std::size_t data_offset_bytes) {
+        exact_base_mapping_ = base_mapping;
+        exact_base_rows_ = base_rows;
+        exact_base_dim_ = base_dim;
+        exact_base_row_stride_bytes_ = row_stride_bytes;
+        exact_base_data_offset_bytes_ = data_offset_bytes;
+    }
+
+    // Host extended codes, factors and IDs are borrowed until this engine is destroyed.
+    void load_from_raw_pointers(std::size_t num_vecs, std::size_t d, std::size_t p_d,
+                                std::size_t n_centroids, std::size_t ex_b,
+                                const float *h_centroids, const float *h_rotator,
+                                const uint32_t *h_short_data, const float *h_short_factors,
+                                const uint8_t *h_long_code, const float *h_ex_factors,
+                                const uint32_t *h_ids, const std::size_t *h_cluster_sizes);
+
+    void capture_thresholds(float *out, std::size_t nq) const;
+    void seed_thresholds(const float *in, std::size_t nq);
+
+    void search(const float *h_queries, std::size_t num_queries, std::size_t topk,
+                std::size_t nprobe, float *h_final_dists, uint32_t *h_final_pids,
+                int batch_q = default_batch_q);
+
+    // ---- extensions of this engine (no counterpart in the reference API) ----
+    // Metric of the loaded index: 0 = L2, 1 = inner product (the reference hybrid path is
+    // L2-only; IP uses g_add = -<q',c'> as rabitq_cpu does, query.hpp:537-545).
+    void set_metric(int metric);
+    // Frozen thresholds: the GPU filter reads a snapshot taken at launch (deterministic
+    // candidate sets for parity tests).
+    void set_frozen_thresholds(bool enabled) { frozen_thresholds_ = enabled; }
+    // CPU refinement threads; 0 = omp_get_max_threads() (the reference always uses the
+    // caller's OpenMP setting, cpu_refinement.cpp:110).
+    void set_cpu_threads(int threads) { cpu_threads_ = threads < 0 ? 0 : threads; }
+    float get_last_scan_ms() const { return last_scan_ms_; }
+    uint64_t get_last_scan_bytes() const { return last_scan_bytes_; }
+    uint64_t get_last_scan_units() const { return last_scan_units_; }
+    uint64_t get_last_scan_vectors() const { return last_scan_vectors_; }
+    cora_gpu_engine *gpu_engine() const { return engine_; }
+
+  private:
+    void validate_workspace(std::size_t queries, std::size_t topk, std::size_t nprobe) const;
+
+    cora_gpu_engine *engine_ = nullptr;
+    int metric_ = 0;
+    std::size_t num_vectors_ = 0, dim_ = 0, padded_dim_ = 0, num_centroids_ = 0, ex_bits_ = 0;
+    bool loaded_ = false;
+
+    const uint8_t *h_long_codes_ = nullptr;
+    const float *h_ex_factors_ = nullptr;
+    const uint32_t *h_ids_ = nullptr;
+
+    const uint8_t *exact_base_mapping_ = nullptr;
+    std::size_t exact_base_rows_ = 0, exact_base_dim_ = 0;
+    std::size_t exact_base_row_stride_bytes_ = 0, exact_base_data_offset_bytes_ = 0;
+
+    bool workspace_ready_ = false;
+    std::size_t ws_max_queries_ = 0, ws_max_topk_ = 0, ws_max_nprobe_ = 0, ws_vanguard_ = 0;
+
+    bool profiling_enabled_ = false;
+    bool candidate_stats_enabled_ = false;
+    bool gpu_filter_timing_enabled_ = false;
+    bool cross_query_reuse_enabled_ = true;
+    bool cpu_secondary_filter_enabled_ = true;
+    bool frozen_thresholds_ = false;
+    int cpu_threads_ = 0;
+    std::size_t vanguard_size_ = default_vanguard_size;
+    KernelType ip_kernel_type_ = KernelType::Lut4Bit;
+
+    std::size_t queue_capacity_ = queue::default_capacity;
+    std::size_t queue_spill_capacity_ = queue::default_spill_capacity;
+    queue::Position last_written_count_ = 0;
+    queue::Position last_spilled_count_ = 0;
+    std::size_t last_refined_count_ = 0;
+    float last_gpu_filter_ms_ = 0.0f;
+    float last_scan_ms_ = 0.0f;
+    uint64_t last_scan_bytes_ = 0, last_scan_units_ = 0, last_scan_vectors_ = 0;
+};
+
+}  // namespace coraanns

@@ -1,0 +1,33 @@
+// Search shape limits (reference include/coraanns/search/parameters.hpp:9-25): query
+// chunks of at most 65,535 (the ring record keeps 16-bit query and probe indices) and at
+// most 65,536 probes, with the same accept/reject boundaries and exception type.
+#pragma once
+
+#include <climits>
+#include <cstddef>
+#include <stdexcept>
+
+namespace coraanns {
+
+inline constexpr std::size_t default_vanguard_size = 5;
+inline constexpr int default_batch_q = 4;
+inline constexpr std::size_t max_query_chunk = 65535;
+inline constexpr std::size_t max_probe_count = 65536;
+// This engine additionally batches up to 8 same-cluster pairs per scan pass and selects
+// at most 4096 probes per query in LDS.
+inline constexpr int max_batch_q = 8;
+inline constexpr std::size_t max_engine_nprobe = 4096;
+
+inline void validate_search_shape(std::size_t queries, std::size_t topk, std::size_t nprobe,
+                                  std::size_t centroids, std::size_t padded_dim) {
+    if (queries == 0 || queries > max_query_chunk)
+        throw std::invalid_argument("query count must be in [1, 65535]; split larger batches");
+    if (topk == 0 || topk > INT_MAX / queries)
+        throw std::invalid_argument("topk must be positive and queries * topk must fit an int");
+    if (nprobe == 0 || nprobe > max_probe_count || nprobe > centroids)
+        throw std::invalid_argument("nprobe must be in [1, min(nlist, 65536)]");
+    if (centroids > INT_MAX / queries || padded_dim == 0 || padded_dim > INT_MAX / (queries * 4))
+        throw std::invalid_argument("query workspace exceeds kernel indexing limits");
+}
+
+}  // namespace coraanns

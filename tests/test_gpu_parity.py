@@ -1,0 +1,323 @@
+"""GPU parity tests: every stage of the HIP path against the CPU oracle, through the C-ABI.
+
+Each stage is checked on the GPU's own inputs for that stage (e.g. the quantiser on the
+GPU-rotated queries), so integer results are compared bit-exactly and floating-point
+ones within 1e-5 relative (scaled by the magnitude of the terms), as the north star asks.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import cora_oracle as orc
+import coraanns_amd as ca
+from conftest import GOLDEN, read_fbin
+
+pytestmark = pytest.mark.gpu
+
+F32_MAX = np.finfo(np.float32).max
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def planes_to_bits(planes):
+    """GPU q-planes [nq][8][W] (dim 32w+l at bit l) -> qint bit planes [nq][8][P]."""
+    nq, B, W = planes.shape
+    sh = np.arange(32, dtype=np.uint32)
+    return ((planes[:, :, :, None] >> sh) & 1).reshape(nq, B, W * 32).astype(np.uint8)
+
+
+def qint_from_planes(planes):
+    bits = planes_to_bits(planes).astype(np.int64)
+    u = sum(bits[:, j, :] << j for j in range(8))
+    return np.where(u >= 128, u - 256, u).astype(np.int32)
+
+
+class Case:
+    def __init__(self, path, queries, base=None):
+        self.path = path
+        self.queries = np.ascontiguousarray(queries, np.float32)
+        self.base = base
+        self.file = orc.read_ivf(path)
+        self.sd = orc.search_data(self.file)
+        self.ivf = ca.IvfIndex(path)
+
+
+def make_engine(case, nprobe, topk, vanguard=0, frozen=True, secondary=False, reuse=True, **kw):
+    eng = ca.HybridIndex(0, vanguard_size=vanguard, frozen_thresholds=frozen,
+                         cpu_secondary_filter=secondary, cross_query_reuse=reuse,
+                         metric=case.file.metric, gpu_filter_timing=True, **kw)
+    eng.load_ivf(case.ivf)
+    eng.prepare_workspace(case.queries.shape[0], topk, nprobe)
+    return eng
+
+
+@pytest.fixture(scope="module")
+def golden_l2():
+    return Case(GOLDEN / "l2_d96" / "ivf.index", read_fbin(GOLDEN / "l2_d96" / "queries.fbin"),
+                read_fbin(GOLDEN / "l2_d96" / "base.fbin"))
+
+
+@pytest.fixture(scope="module")
+def golden_ip():
+    return Case(GOLDEN / "ip_d64" / "ivf.index", read_fbin(GOLDEN / "ip_d64" / "queries.fbin"),
+                read_fbin(GOLDEN / "ip_d64" / "base.fbin"))
+
+
+@pytest.fixture(scope="module")
+def synth(tmp_path_factory):
+    """20,000 x 128 (P = 128), 64 clusters, 96 queries, built by this repository's builder."""
+    rng = np.random.default_rng(7)
+    n, dim, nl, nq = 20000, 128, 64, 96
+    centers = rng.normal(0, 1, (nl, dim))
+    lab = rng.integers(0, nl, n)
+    x = (centers[lab] + rng.normal(0, 0.4, (n, dim))).astype(np.float32)
+    q = (centers[rng.integers(0, nl, nq)] + rng.normal(0, 0.4, (nq, dim))).astype(np.float32)
+    d = ((x[:, None, :] - centers[None]) ** 2).sum(2)
+    assign = d.argmin(1).astype(np.uint32)
+    cent = np.stack([x[assign == c].mean(0) for c in range(nl)])
+    a = rng.normal(size=(dim, dim))
+    R = np.linalg.qr(a)[0].T.astype(np.float32)
+    path = tmp_path_factory.mktemp("synth") / "synth.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32),
+                 (cent @ R).astype(np.float32), assign, R, metric=0)
+    return Case(path, q, x)
+
+
+def run_frozen(case, nprobe, topk, thresholds=None, **kw):
+    eng = make_engine(case, nprobe, topk, **kw)
+    nq = case.queries.shape[0]
+    eng.reset_buffer(case.queries)
+    if thresholds is not None:
+        eng.seed_thresholds(thresholds)
+    d, i = eng.search(case.queries, topk, nprobe)
+    return eng, d, i
+
+
+def gpu_intermediates(eng, case, nprobe):
+    nq, P = case.queries.shape[0], case.file.padded_dim
+    W = P // 32
+    g = {
+        "qr": eng.debug_read(ca.DBG_ROTATED_QUERIES, (nq, P), np.float32),
+        "k1": eng.debug_read(ca.DBG_K1XSUMQ, (nq,), np.float32),
+        "kb": eng.debug_read(ca.DBG_KBXSUMQ, (nq,), np.float32),
+        "width": eng.debug_read(ca.DBG_Q_WIDTH, (nq,), np.float32),
+        "planes": eng.debug_read(ca.DBG_Q_PLANES, (nq, 8, W), np.uint32),
+        "pidx": eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32),
+        "gadd": eng.debug_read(ca.DBG_PROBE_GADD, (nq, nprobe), np.float32),
+        "gerr": eng.debug_read(ca.DBG_PROBE_GERR, (nq, nprobe), np.float32),
+    }
+    return g
+
+
+CASES = ["golden_l2", "golden_ip", "synth"]
+
+
+@pytest.mark.parametrize("case_name", CASES)
+def test_query_preparation(case_name, request):
+    case = request.getfixturevalue(case_name)
+    say(f"[gpu] query prep parity on {case_name}")
+    nprobe = min(4, case.file.nlist)
+    eng, _, _ = run_frozen(case, nprobe, 10)
+    g = gpu_intermediates(eng, case, nprobe)
+    qr_ref = orc.rotate(case.queries, case.sd.rotator)
+    scale = np.abs(case.queries).sum(1, keepdims=True) * np.abs(case.sd.rotator).max()
+    assert np.all(np.abs(g["qr"] - qr_ref) <= 1e-5 * scale)
+    # k1/kb from the GPU-rotated queries
+    k1, kb = orc.query_factors(g["qr"], case.file.ex_bits)
+    s = np.abs(g["qr"]).sum(1) + 1e-30
+    assert np.all(np.abs(g["k1"] - k1) <= 1e-5 * s)
+    assert np.all(np.abs(g["kb"] - kb) <= 1e-5 * 127.5 * s)
+    # Bq=8 quantisation: bit-exact on the same rotated input
+    qint, width = orc.quantize_query_bitwise(g["qr"])
+    assert np.array_equal(g["width"].view(np.uint32), width.view(np.uint32))
+    assert np.array_equal(qint_from_planes(g["planes"]), qint)
+
+
+@pytest.mark.parametrize("case_name", CASES)
+def test_coarse_probe(case_name, request):
+    case = request.getfixturevalue(case_name)
+    nprobe = min(6, case.file.nlist)
+    say(f"[gpu] coarse probe parity on {case_name} nprobe={nprobe}")
+    eng, _, _ = run_frozen(case, nprobe, 10)
+    g = gpu_intermediates(eng, case, nprobe)
+    idx, gadd, gerr, l2 = orc.coarse_probe(g["qr"], case.sd.centroids, case.file.nlist, case.file.metric)
+    for q in range(idx.shape[0]):
+        got = g["pidx"][q]
+        # ascending exact distance; the selected set equals the oracle's up to ties at 1e-5
+        d_all = dict(zip(idx[q].tolist(), l2[q].tolist()))
+        dg = np.array([d_all[c] for c in got])
+        assert np.all(np.diff(dg) >= -1e-5 * (np.abs(dg).max() + 1))
+        kth = l2[q][nprobe - 1]
+        strict = set(idx[q][l2[q] < kth - 1e-5 * (abs(kth) + 1)].tolist())
+        assert strict <= set(got.tolist())
+        assert len(set(got.tolist())) == nprobe
+        # g_add / g_error of the selected probes
+        qq = g["qr"][q].astype(np.float64)
+        c = case.sd.centroids[got].astype(np.float64)
+        l2x = ((qq - c) ** 2).sum(1)
+        ipx = c @ qq
+        want = l2x if case.file.metric == 0 else -ipx
+        sc = (qq ** 2).sum() + (c ** 2).sum(1)
+        assert np.all(np.abs(g["gadd"][q] - want) <= 1e-5 * sc)
+        assert np.all(np.abs(g["gerr"][q] - np.sqrt(l2x)) <= 1e-5 * np.sqrt(sc))
+
+
+@pytest.mark.parametrize("case_name", CASES)
+def test_popcount_estimator_bit_exact(case_name, request):
+    case = request.getfixturevalue(case_name)
+    nprobe = min(8, case.file.nlist)
+    say(f"[gpu] dense popcount estimator parity on {case_name} nprobe={nprobe}")
+    eng, _, _ = run_frozen(case, nprobe, 10)
+    g = gpu_intermediates(eng, case, nprobe)
+    maxc = case.ivf.max_cluster
+    ip, low = eng.debug_dense(case.queries.shape[0], nprobe, maxc)
+    qint = qint_from_planes(g["planes"])
+    sd = case.sd
+    checked = 0
+    for q in range(case.queries.shape[0]):
+        for p in range(nprobe):
+            c = int(g["pidx"][q, p])
+            s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+            want_ip = orc.ip_int_direct(sd.bits[s:s + n], qint[q])
+            assert np.array_equal(ip[q, p, :n].astype(np.int64), want_ip), (q, p, c)
+            # the reference's bit-plane popcount restatement on the reference word layout
+            words = sd.short_data[s * (sd.bits.shape[1] // 32):(s + n) * (sd.bits.shape[1] // 32)]
+            words = words.reshape(-1, n).T
+            planes_msb = orc.query_planes_msb(qint[q:q + 1])[0]
+            assert np.array_equal(orc.ip_int_planes(np.ascontiguousarray(words), planes_msb), want_ip)
+            ex = orc.exact_ip_bitwise(want_ip, g["width"][q])
+            f = sd.short_factors[s:s + n]
+            want_low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p], ex, g["k1"][q])
+            sc = np.abs(f[:, 0]) + abs(g["gadd"][q, p]) + np.abs(f[:, 1] * (ex + g["k1"][q])) + \
+                np.abs(f[:, 2] * g["gerr"][q, p])
+            assert np.all(np.abs(low[q, p, :n] - want_low) <= 1e-5 * sc)
+            checked += n
+    assert checked > 0
+
+
+def oracle_topk_from_gpu(case, g, nprobe, topk, thresholds=None):
+    """Final top-k restated by the oracle from the GPU's query-side intermediates."""
+    sd, P = case.sd, case.file.padded_dim
+    qint = qint_from_planes(g["planes"])
+    nq = case.queries.shape[0]
+    out_d = np.full((nq, topk), F32_MAX, np.float32)
+    out_i = np.zeros((nq, topk), np.uint32)
+    cands = []
+    for q in range(nq):
+        items, cset = [], set()
+        thr = F32_MAX if thresholds is None else thresholds[q]
+        for p in range(nprobe):
+            c = int(g["pidx"][q, p])
+            s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+            ipi = orc.ip_int_direct(sd.bits[s:s + n], qint[q])
+            ex = orc.exact_ip_bitwise(ipi, g["width"][q])
+            f = sd.short_factors[s:s + n]
+            low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p], ex, g["k1"][q])
+            keep = np.nonzero(low < thr)[0]
+            gids = s + keep
+            ip2 = orc.excode_ip(g["qr"][q], sd.long_codes[gids], P)
+            rd = orc.refine_dist(sd.ex_factors[gids, 0], sd.ex_factors[gids, 1], g["gadd"][q, p], ex[keep], ip2,
+                                 g["kb"][q], case.file.ex_bits)
+            cset.update(int(x) for x in gids)
+            items += list(zip(rd.tolist(), sd.ids[gids].tolist()))
+        items.sort()
+        items = [t for t in items if t[0] < thr][:topk]
+        for r, (dv, pid) in enumerate(items):
+            out_d[q, r], out_i[q, r] = dv, pid
+        cands.append(cset)
+    return out_d, out_i, cands
+
+
+def assert_topk_equal(d, i, od, oi, rtol=1e-5):
+    for q in range(d.shape[0]):
+        scale = np.abs(od[q][od[q] < F32_MAX]).max() + 1 if (od[q] < F32_MAX).any() else 1
+        assert np.allclose(d[q], od[q], rtol=0, atol=rtol * scale), q
+        # ids equal except where neighbouring distances tie within tolerance
+        for r in range(d.shape[1]):
+            if i[q, r] != oi[q, r]:
+                close = np.abs(od[q] - d[q, r]) <= rtol * scale
+                assert i[q, r] in set(oi[q][close].tolist()), (q, r)
+
+
+@pytest.mark.parametrize("case_name", CASES)
+@pytest.mark.parametrize("vanguard", [0, 3])
+def test_end_to_end_frozen_infinite_thresholds(case_name, vanguard, request):
+    case = request.getfixturevalue(case_name)
+    nprobe, topk = min(8, case.file.nlist), 10
+    say(f"[gpu] end-to-end frozen parity on {case_name} vanguard={vanguard}")
+    eng, d, i = run_frozen(case, nprobe, topk, vanguard=vanguard)
+    st = eng.stats()
+    g = gpu_intermediates(eng, case, nprobe)
+    od, oi, cands = oracle_topk_from_gpu(case, g, nprobe, topk)
+    # every vector of every probed cluster is a candidate exactly once
+    assert st["submitted"] == sum(len(c) for c in cands)
+    assert st["refined"] == st["submitted"]
+    assert_topk_equal(d, i, od, oi)
+
+
+@pytest.mark.parametrize("case_name", ["golden_l2", "synth"])
+def test_filter_candidate_set_with_frozen_thresholds(case_name, request):
+    case = request.getfixturevalue(case_name)
+    nprobe, topk = min(8, case.file.nlist), 10
+    say(f"[gpu] frozen-threshold candidate count on {case_name}")
+    eng, _, _ = run_frozen(case, nprobe, topk)
+    g = gpu_intermediates(eng, case, nprobe)
+    od, oi, _ = oracle_topk_from_gpu(case, g, nprobe, topk)
+    thr = (od[:, topk - 1] * np.float32(1.02)).astype(np.float32)
+    eng2, d, i = run_frozen(case, nprobe, topk, thresholds=thr)
+    st = eng2.stats()
+    # candidate count equals the oracle's {low < thr} up to lows within 1e-5 of thr
+    ip, low = eng2.debug_dense(case.queries.shape[0], nprobe, case.ivf.max_cluster)
+    lo = hi = 0
+    for q in range(case.queries.shape[0]):
+        for p in range(nprobe):
+            n = int(case.sd.cluster_sizes[int(g["pidx"][q, p])])
+            l = low[q, p, :n].astype(np.float64)
+            lo += int((l < thr[q] - 1e-5 * abs(thr[q])).sum())
+            hi += int((l < thr[q] + 1e-5 * abs(thr[q])).sum())
+    assert lo <= st["submitted"] <= hi
+    od2, oi2, _ = oracle_topk_from_gpu(case, g, nprobe, topk, thresholds=thr)
+    assert_topk_equal(d, i, od2, oi2)
+
+
+@pytest.mark.parametrize("batch_q", [1, 2, 3, 4, 6, 8])
+def test_batch_q_and_reuse_do_not_change_results(synth, batch_q):
+    say(f"[gpu] batch_q={batch_q}")
+    nprobe, topk = 12, 10
+    _, d0, i0 = run_frozen(synth, nprobe, topk, reuse=False)
+    eng, d, i = run_frozen(synth, nprobe, topk, reuse=True)
+    eng.reset_buffer(synth.queries)
+    d, i = eng.search(synth.queries, topk, nprobe, batch_q)
+    assert np.array_equal(i, i0)
+    assert np.allclose(d, d0, rtol=1e-6)
+
+
+def test_live_thresholds_match_frozen_results(synth):
+    """Default production mode (live thresholds, secondary filter, vanguard 5) returns the
+    same top-k as the exhaustive frozen search, except where refine distances tie."""
+    nprobe, topk = 16, 10
+    say("[gpu] live vs frozen")
+    _, d0, i0 = run_frozen(synth, nprobe, topk, vanguard=0)
+    eng = make_engine(synth, nprobe, topk, vanguard=5, frozen=False, secondary=True)
+    eng.reset_buffer(synth.queries)
+    d, i = eng.search(synth.queries, topk, nprobe, 4)
+    st = eng.stats()
+    assert st["submitted"] < synth.queries.shape[0] * 20000  # the filter prunes
+    same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), i0.tolist())])
+    assert same >= 0.99, same
+
+
+@pytest.mark.parametrize("case_name", CASES)
+def test_recall_against_brute_force(case_name, request):
+    case = request.getfixturevalue(case_name)
+    nprobe, topk = case.file.nlist if case.file.nlist <= 8 else 24, 10
+    say(f"[gpu] recall on {case_name}")
+    eng = make_engine(case, nprobe, topk, vanguard=5, frozen=False, secondary=True)
+    d, i = eng.search_all(case.queries, topk, nprobe)
+    gt = orc.brute_force_gt(case.base, case.queries, topk, case.file.metric)
+    r = orc.recall_at_k(i, gt, topk)
+    assert r >= 0.9, r
