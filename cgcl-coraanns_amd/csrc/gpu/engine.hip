@@ -16,7 +16,7 @@ using namespace cora;
 
 namespace {
 
-constexpr unsigned long long kDrainMaxSpins = 1ull << 23;  // ~30 s of 127-cycle sleeps
+constexpr unsigned long long kDrainMaxSeconds = 20;        // drain wait for the CPU consumer
 constexpr uint32_t kScanGrid = 8192;                        // persistent waves
 constexpr uint32_t kVanguardGrid = 512;
 constexpr uint64_t kMaxQueryChunk = 65535;                  // parameters.hpp:12
@@ -41,6 +41,7 @@ void hfree(T *&p) {
 struct cora_gpu_engine {
     int device = 0;
     std::string err;
+    unsigned long long wall_clock_khz = 0;  // device wall_clock64() rate
     hipStream_t stream = nullptr, stream_d2h = nullptr;
     hipEvent_t ev_prep = nullptr, ev_probe = nullptr, ev_f0 = nullptr, ev_f1 = nullptr,
                ev_s0 = nullptr, ev_s1 = nullptr;
@@ -247,6 +248,11 @@ int cora_gpu_create(cora_gpu_engine **out, int device) {
     E->device = device;
     auto init = [&]() -> int {
         HIPCHK(hipSetDevice(device));
+        int khz = 0;
+        HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
+        if (khz <= 0)
+            return fail(E, CORA_ERR_RUNTIME, "device reports no wall clock rate");
+        E->wall_clock_khz = (unsigned long long)khz;
         HIPCHK(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
         HIPCHK(hipStreamCreateWithFlags(&E->stream_d2h, hipStreamNonBlocking));
         for (hipEvent_t *ev : {&E->ev_prep, &E->ev_probe, &E->ev_f0, &E->ev_f1, &E->ev_s0, &E->ev_s1})
@@ -611,7 +617,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     }
     if (timing)
         HIPCHK(hipEventRecord(E->ev_f1, s));
-    launch_finish(queue_dev(E), kDrainMaxSpins, s);
+    launch_finish(queue_dev(E), kDrainMaxSeconds * 1000ull * E->wall_clock_khz, s);
     HIPCHK(hipGetLastError());
     E->launched = true;
     return CORA_OK;

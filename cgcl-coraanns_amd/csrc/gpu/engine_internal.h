@@ -139,6 +139,7 @@ int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, uin
 int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t grid, uint32_t set,
                     hipStream_t s);
 int launch_vanguard_seed(const ScanParams &p, uint32_t W, uint32_t grid, hipStream_t s);
-void launch_finish(QueueDev q, unsigned long long max_spins, hipStream_t s);
+// max_ticks: drain wait limit in ticks of the device wall clock (wall_clock64)
+void launch_finish(QueueDev q, unsigned long long max_ticks, hipStream_t s);
 
 }  // namespace cora

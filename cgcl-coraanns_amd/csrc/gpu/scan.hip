@@ -103,6 +103,18 @@ __device__ __forceinline__ int popc_ip(const uint32_t (&x)[Words<W>::kMax],
     return ip;
 }
 
+// One 16-byte Candidate store to the host-coherent ring that writes through the GPU L2
+// (system-scope coherence bits sc0 sc1). A plain store to host memory may stay in L2
+// until the next system-scope release, which a producer still running never issues, so
+// the CPU consumer would not see the record and the drain kernel, waiting for the CPU
+// to release ring space, would never see progress.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void store_ring(uint4 *slot, uint4 rec) {
+    const u32x4_t v = {rec.x, rec.y, rec.z, rec.w};
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(slot), "v"(v) : "memory");
+}
+
 __device__ __noinline__ unsigned long long refresh_limit(unsigned long long *cached_limit,
                                                          int *refresh_flag,
                                                          unsigned long long *released,
@@ -147,7 +159,7 @@ __device__ __forceinline__ void publish(const QueueDev q, bool survive, uint4 re
     if (survive) {
         const unsigned long long pos = base + lane_rank(mask);
         if (pos < limit) {
-            q.items[pos & q.mask] = rec;
+            store_ring(&q.items[pos & q.mask], rec);
         } else {
             const unsigned long long s = atomicAdd(q.spill_count, 1ull);
             if (s < q.spill_capacity) {
@@ -519,12 +531,14 @@ __global__ void cursor_init_kernel(uint32_t *cursor, const uint32_t *num_units, 
 
 // Queue completion (reference finish_queue, ring_queue.cuh:125-170): publish produced
 // and spilled counts, drain spilled records into the ring as the CPU releases space,
-// then set Progress::done with a system-scope release. The wait is bounded (max_spins
-// sleeps) and honours the host abort flag, so the kernel always ends.
-__global__ __launch_bounds__(256) void finish_kernel(QueueDev q, unsigned long long max_spins) {
+// then set Progress::done with a system-scope release. The wait is bounded in time
+// (max_ticks of the constant-rate wall clock, whatever a drain pass costs) and honours
+// the host abort flag, so the kernel always ends.
+__global__ __launch_bounds__(256) void finish_kernel(QueueDev q, unsigned long long max_ticks) {
     __shared__ unsigned long long s_limit;
     __shared__ uint32_t s_remaining;
-    __shared__ int s_abort;
+    __shared__ int s_abort, s_expired;
+    const unsigned long long t_start = wall_clock64();
     const uint32_t t = threadIdx.x;
     const unsigned long long produced = *q.produced;
     const unsigned long long spill_total = *q.spill_count;
@@ -538,13 +552,14 @@ __global__ __launch_bounds__(256) void finish_kernel(QueueDev q, unsigned long l
     }
     bool stalled = false;
     if (!overflow) {
-        for (unsigned long long spin = 0;; ++spin) {
+        for (;;) {
             if (t == 0) {
                 s_limit = __hip_atomic_load(&q.progress->released, __ATOMIC_ACQUIRE,
                                             __HIP_MEMORY_SCOPE_SYSTEM) +
                           q.capacity;
                 s_remaining = 0;
                 s_abort = __hip_atomic_load(q.abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                s_expired = wall_clock64() - t_start > max_ticks;
             }
             __syncthreads();
             if (s_abort) {
@@ -558,7 +573,7 @@ __global__ __launch_bounds__(256) void finish_kernel(QueueDev q, unsigned long l
                 if (pos == ~0ull)
                     continue;
                 if (pos < lim) {
-                    q.items[pos & q.mask] = q.spill[i].item;
+                    store_ring(&q.items[pos & q.mask], q.spill[i].item);
                     q.spill[i].position = ~0ull;
                 } else {
                     ++rem;
@@ -569,7 +584,7 @@ __global__ __launch_bounds__(256) void finish_kernel(QueueDev q, unsigned long l
             __syncthreads();
             if (s_remaining == 0)
                 break;
-            if (spin >= max_spins) {
+            if (s_expired) {
                 stalled = true;
                 break;
             }
@@ -656,8 +671,8 @@ void launch_cursor_init(uint32_t *cursor, const uint32_t *num_units, uint32_t se
     cursor_init_kernel<<<1, 64, 0, s>>>(cursor, num_units, set);
 }
 
-void launch_finish(QueueDev q, unsigned long long max_spins, hipStream_t s) {
-    finish_kernel<<<1, 256, 0, s>>>(q, max_spins);
+void launch_finish(QueueDev q, unsigned long long max_ticks, hipStream_t s) {
+    finish_kernel<<<1, 256, 0, s>>>(q, max_ticks);
 }
 
 }  // namespace cora
