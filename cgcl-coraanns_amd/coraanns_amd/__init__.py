@@ -36,7 +36,7 @@ FLAG_FILTER_TIMING = 2
 FLAG_CROSS_QUERY_REUSE = 4
 
 DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range(5)
-DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS = range(5, 9)
+DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
 
 
 class EngineUnavailable(RuntimeError):
@@ -137,7 +137,7 @@ GPU_SIGNATURES = {
     "cora_gpu_seed_thresholds": [_P, _P, _U64],
     "cora_gpu_index_info": [_P, _P, _P, _P, _P, _P],
     "cora_gpu_debug_read": [_P, _I, _P, _U64],
-    "cora_gpu_debug_dense": [_P, _P, _P, _U64],
+    "cora_gpu_debug_dense": [_P, _P, _P, _P, _U64],
     "cora_tool_last_error": [],
     "cora_tool_rotate": [_P, _U64, _U64, _P, _U64, _P, _I],
     "cora_tool_kmeans": [_P, _U64, _U64, _U64, C.c_uint32, _U64, _P, _I],
@@ -372,11 +372,14 @@ class HybridIndex:
         return out
 
     def debug_dense(self, nq, nprobe, max_cluster):
+        """ip_int <b,qint>, residual <b,qres> and low distance of every probed vector,
+        [nq][nprobe][max_cluster]."""
         ip = np.full((nq, nprobe, max_cluster), -(1 << 30), np.int32)
+        ip2 = np.full((nq, nprobe, max_cluster), -(1 << 30), np.int32)
         low = np.full((nq, nprobe, max_cluster), np.nan, np.float32)
         eng = self.gpu
-        _gpu_check(eng, _load()[0].cora_gpu_debug_dense(eng, _ptr(ip), _ptr(low), ip.size))
-        return ip, low
+        _gpu_check(eng, _load()[0].cora_gpu_debug_dense(eng, _ptr(ip), _ptr(ip2), _ptr(low), ip.size))
+        return ip, ip2, low
 
     def close(self):
         if getattr(self, "_h", None):

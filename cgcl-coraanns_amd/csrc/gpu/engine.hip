@@ -17,8 +17,6 @@ using namespace cora;
 namespace {
 
 constexpr unsigned long long kDrainMaxSeconds = 20;        // drain wait for the CPU consumer
-constexpr uint32_t kScanGrid = 8192;                        // persistent waves
-constexpr uint32_t kVanguardGrid = 512;
 constexpr uint64_t kMaxQueryChunk = 65535;                  // parameters.hpp:12
 constexpr uint64_t kMaxProbeCount = 65536;                  // parameters.hpp:13
 
@@ -59,7 +57,7 @@ struct cora_gpu_engine {
     bool ws = false;
     uint64_t ws_q = 0, ws_k = 0, ws_np = 0, ws_van = 0, seed_words = 0;
     float *d_raw = nullptr, *d_qrot = nullptr, *d_k1 = nullptr, *d_kb = nullptr,
-          *d_qnorm = nullptr, *d_qwidth = nullptr, *d_dist = nullptr, *d_gadd = nullptr,
+          *d_qnorm = nullptr, *d_qwidth = nullptr, *d_qwidth2 = nullptr, *d_dist = nullptr, *d_gadd = nullptr,
           *d_gerr = nullptr, *d_thr_snap = nullptr;
     uint32_t *d_planes = nullptr, *d_bcount = nullptr, *d_bcursor = nullptr, *d_boff = nullptr,
              *d_uoff = nullptr, *d_nunits = nullptr, *d_cursor = nullptr, *d_seed = nullptr;
@@ -124,6 +122,7 @@ ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool f
     p.meta = E->d_meta;
     p.qplanes = E->d_planes;
     p.qwidth = E->d_qwidth;
+    p.qwidth2 = E->d_qwidth2;
     p.k1 = E->d_k1;
     p.pgadd = E->d_gadd;
     p.pgerr = E->d_gerr;
@@ -167,7 +166,7 @@ void release_workspace(cora_gpu_engine *E) {
     E->ws = false;
     E->launched = false;
     E->ws_q = E->ws_k = E->ws_np = E->ws_van = E->seed_words = 0;
-    for (float **p : {&E->d_raw, &E->d_qrot, &E->d_k1, &E->d_kb, &E->d_qnorm, &E->d_qwidth,
+    for (float **p : {&E->d_raw, &E->d_qrot, &E->d_k1, &E->d_kb, &E->d_qnorm, &E->d_qwidth, &E->d_qwidth2,
                       &E->d_dist, &E->d_gadd, &E->d_gerr, &E->d_thr_snap})
         dfree(*p);
     for (uint32_t **p : {&E->d_planes, &E->d_bcount, &E->d_bcursor, &E->d_boff, &E->d_uoff,
@@ -435,7 +434,8 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_kb, max_q));
         TRY(dalloc(E, E->d_qnorm, max_q));
         TRY(dalloc(E, E->d_qwidth, max_q));
-        TRY(dalloc(E, E->d_planes, max_q * kBq * E->W));
+        TRY(dalloc(E, E->d_qwidth2, max_q));
+        TRY(dalloc(E, E->d_planes, max_q * 2 * kBq * E->W));
         TRY(dalloc(E, E->d_dist, max_q * E->nl));
         TRY(dalloc(E, E->d_pidx, np));
         TRY(dalloc(E, E->d_gadd, np));
@@ -573,7 +573,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // query preparation (hybrid.cu:436-463)
     launch_rotate(E->d_raw, E->d_rot, E->d_qrot, nq, (uint32_t)E->dim, P, s);
     launch_query_prep(E->d_qrot, nq, P, (uint32_t)E->ex_bits, E->d_k1, E->d_kb, E->d_qnorm,
-                      E->d_qwidth, E->d_planes, s);
+                      E->d_qwidth, E->d_qwidth2, E->d_planes, s);
     HIPCHK(hipEventRecord(E->ev_prep, s));
     HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_prep, 0));
     HIPCHK(hipMemcpyAsync(E->h_qrot, E->d_qrot, (size_t)nq * P * 4, hipMemcpyDeviceToHost,
@@ -603,17 +603,17 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     if (depth > 0) {
         launch_fill_u32(E->d_seed, 0u, (size_t)nq * depth * E->seed_words, s);
         launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
-        launch_vanguard_seed(p, E->W, kVanguardGrid, s);
+        launch_vanguard_seed(p, E->W, s);
     }
     launch_cursor_init(E->d_cursor, E->d_nunits, 1, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_s0, s));
-    launch_scan(p, E->W, batch, 0, kScanGrid, s);
+    launch_scan(p, E->W, batch, 0, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_s1, s));
     if (depth > 0) {
         launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
-        launch_scan(p, E->W, 1, 1, kScanGrid, s);
+        launch_scan(p, E->W, 1, 1, s);
     }
     if (timing)
         HIPCHK(hipEventRecord(E->ev_f1, s));
@@ -738,7 +738,8 @@ int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes
     case CORA_DBG_K1XSUMQ: src = E->d_k1; size = nq * 4; break;
     case CORA_DBG_KBXSUMQ: src = E->d_kb; size = nq * 4; break;
     case CORA_DBG_Q_WIDTH: src = E->d_qwidth; size = nq * 4; break;
-    case CORA_DBG_Q_PLANES: src = E->d_planes; size = nq * kBq * E->W * 4; break;
+    case CORA_DBG_Q_PLANES: src = E->d_planes; size = nq * 2 * kBq * E->W * 4; break;
+    case CORA_DBG_Q_WIDTH2: src = E->d_qwidth2; size = nq * 4; break;
     case CORA_DBG_PROBE_IDX: src = E->d_pidx; size = nq * np * 4; break;
     case CORA_DBG_PROBE_GADD: src = E->d_gadd; size = nq * np * 4; break;
     case CORA_DBG_PROBE_GERR: src = E->d_gerr; size = nq * np * 4; break;
@@ -763,8 +764,9 @@ int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes
     return CORA_OK;
 }
 
-int cora_gpu_debug_dense(cora_gpu_engine *E, int32_t *out_ip, float *out_low, uint64_t cap) {
-    if (!E || !out_ip || !out_low)
+int cora_gpu_debug_dense(cora_gpu_engine *E, int32_t *out_ip, int32_t *out_ip2, float *out_low,
+                         uint64_t cap) {
+    if (!E || !out_ip || !out_ip2 || !out_low)
         return CORA_ERR_INVALID_ARGUMENT;
     if (!E->launched)
         return fail(E, CORA_ERR_LOGIC, "no search launched");
@@ -773,22 +775,27 @@ int cora_gpu_debug_dense(cora_gpu_engine *E, int32_t *out_ip, float *out_low, ui
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_dense: output too small");
     HIPCHK(hipSetDevice(E->device));
     HIPCHK(hipStreamSynchronize(E->stream));
-    int32_t *d_ip = nullptr;
+    int32_t *d_ip = nullptr, *d_ip2 = nullptr;
     float *d_low = nullptr;
     int rc = dalloc(E, d_ip, need);
+    if (rc == CORA_OK)
+        rc = dalloc(E, d_ip2, need);
     if (rc == CORA_OK)
         rc = dalloc(E, d_low, need);
     if (rc == CORA_OK) {
         ScanParams p = scan_params(E, E->last_depth, 0, true);
         p.dbg_ip = d_ip;
+        p.dbg_ip2 = d_ip2;
         p.dbg_low = d_low;
         p.dbg_stride = (uint32_t)E->max_cluster;
         hipError_t r = hipMemcpy(d_ip, out_ip, need * 4, hipMemcpyHostToDevice);
         if (r == hipSuccess)
+            r = hipMemcpy(d_ip2, out_ip2, need * 4, hipMemcpyHostToDevice);
+        if (r == hipSuccess)
             r = hipMemcpy(d_low, out_low, need * 4, hipMemcpyHostToDevice);
         for (uint32_t set = 0; set < 2 && r == hipSuccess; ++set) {
             launch_cursor_init(E->d_cursor, E->d_nunits, set, E->stream);
-            launch_scan_set(p, E->W, 2, kScanGrid, set, E->stream);
+            launch_scan_set(p, E->W, 2, set, E->stream);
             r = hipGetLastError();
             if (r == hipSuccess)
                 r = hipStreamSynchronize(E->stream);
@@ -796,11 +803,14 @@ int cora_gpu_debug_dense(cora_gpu_engine *E, int32_t *out_ip, float *out_low, ui
         if (r == hipSuccess)
             r = hipMemcpy(out_ip, d_ip, need * 4, hipMemcpyDeviceToHost);
         if (r == hipSuccess)
+            r = hipMemcpy(out_ip2, d_ip2, need * 4, hipMemcpyDeviceToHost);
+        if (r == hipSuccess)
             r = hipMemcpy(out_low, d_low, need * 4, hipMemcpyDeviceToHost);
         if (r != hipSuccess)
             rc = fail(E, CORA_ERR_RUNTIME, std::string("debug_dense: ") + hipGetErrorString(r));
     }
     dfree(d_ip);
+    dfree(d_ip2);
     dfree(d_low);
     return rc;
 }

@@ -81,8 +81,9 @@ struct QueueDev {
 struct ScanParams {
     const uint8_t *tiles;
     const ClusterMeta *meta;
-    const uint32_t *qplanes;  // [nq][8][W]
-    const float *qwidth;      // [nq]
+    const uint32_t *qplanes;  // [nq][16][W]: Bq=8 query planes 0..7, residual planes 8..15
+    const float *qwidth;      // [nq] Bq=8 step
+    const float *qwidth2;     // [nq] residual step (qwidth / 254)
     const float *k1;          // [nq]
     const float *pgadd;       // [nq][nprobe]
     const float *pgerr;       // [nq][nprobe]
@@ -102,6 +103,7 @@ struct ScanParams {
     QueueDev queue;
     // dense debug output
     int32_t *dbg_ip;
+    int32_t *dbg_ip2;            // residual inner product <b, qres>
     float *dbg_low;
     uint32_t dbg_stride;         // max cluster size
 };
@@ -113,7 +115,8 @@ void launch_repack(const uint32_t *ref_words, const float *ref_factors, const Cl
 void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint32_t dim,
                    uint32_t P, hipStream_t s);
 void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,
-                       float *kb, float *qnorm, float *qwidth, uint32_t *qplanes, hipStream_t s);
+                       float *kb, float *qnorm, float *qwidth, float *qwidth2, uint32_t *qplanes,
+                       hipStream_t s);
 void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s);
 void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,
                       uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s);
@@ -132,13 +135,12 @@ void launch_fill_u32(uint32_t *p, uint32_t value, size_t n, hipStream_t s);
 void launch_fill_u64(unsigned long long *p, unsigned long long value, size_t n, hipStream_t s);
 void launch_queue_reset(QueueDev q, hipStream_t s);
 void launch_cursor_init(uint32_t *cursor, const uint32_t *num_units, uint32_t set, hipStream_t s);
-// kind: 0 = far pairs (publish below cutoff), 1 = vanguard recovery, 2 = dense debug
-int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, uint32_t grid,
-                hipStream_t s);
+// kind: 0 = far pairs (publish below cutoff), 1 = vanguard recovery, 2 = dense debug.
+// The grid is the number of resident waves the kernel's occupancy allows (persistent).
+int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, hipStream_t s);
 // dense debug pass over one unit set (0 = vanguard units, 1 = far units)
-int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t grid, uint32_t set,
-                    hipStream_t s);
-int launch_vanguard_seed(const ScanParams &p, uint32_t W, uint32_t grid, hipStream_t s);
+int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t set, hipStream_t s);
+int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s);
 // max_ticks: drain wait limit in ticks of the device wall clock (wall_clock64)
 void launch_finish(QueueDev q, unsigned long long max_ticks, hipStream_t s);
 

@@ -104,12 +104,22 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // One wave per query. Each lane owns dimensions lane + 64*i.
+//
+// Planes [q][16][W]: planes 0..7 hold the Bq=8 query qint = clamp(rint(q' / width))
+// (reference quantize_query_bitwise_kernel, query_kernels.cuh:117-189), planes 8..15 the
+// quantised residual qres = clamp(rint((q' - width*qint) / width2), -127, 127) with
+// width2 = width / 254, so that width*<b,qint> + width2*<b,qres> estimates <q',b> to
+// about 16 bits. The filter uses planes 0..7 only; the residual pass refines the inner
+// product of surviving candidates. The residual is one fused multiply-add (the exact
+// q' - width*qint rounded once), so the CPU restatement reproduces it bit for bit
+// whatever the compiler's contraction setting.
 __global__ __launch_bounds__(64) void query_prep_kernel(const float *__restrict__ qrot,
                                                         uint32_t P, uint32_t ex_bits,
                                                         float *__restrict__ k1,
                                                         float *__restrict__ kb,
                                                         float *__restrict__ qnorm,
                                                         float *__restrict__ qwidth,
+                                                        float *__restrict__ qwidth2,
                                                         uint32_t *__restrict__ planes) {
     const uint32_t q = blockIdx.x;
     const int lane = threadIdx.x;
@@ -130,21 +140,29 @@ __global__ __launch_bounds__(64) void query_prep_kernel(const float *__restrict_
     // Symmetric Bq=8 quantisation, IEEE single precision with round-half-even.
     const float width = fmaxf(amax / 127.0f, 1e-30f);
     const float inv = 1.0f / width;
+    const float width2 = width / 254.0f;
+    const float inv2 = 1.0f / width2;
     const uint32_t W = P / 32;
-    uint32_t *out = planes + (size_t)q * kBq * W;
+    uint32_t *out = planes + (size_t)q * 2 * kBq * W;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         if ((uint32_t)i >= groups)
             break;
-        int qi = (int)rintf(v[i] * inv);
+        int qi = (int)rintf(__fmul_rn(v[i], inv));
         qi = max(-128, min(127, qi));
-        const uint32_t u = (uint32_t)qi & 0xFFu;
+        const float r = fmaf(-width, (float)qi, v[i]);
+        int qr = (int)rintf(__fmul_rn(r, inv2));
+        qr = max(-127, min(127, qr));
+        const uint32_t u = (uint32_t)qi & 0xFFu, ur = (uint32_t)qr & 0xFFu;
 #pragma unroll
         for (int j = 0; j < kBq; ++j) {
             const unsigned long long m = __ballot((u >> j) & 1u);
+            const unsigned long long mr = __ballot((ur >> j) & 1u);
             if (lane == 0) {
                 out[j * W + 2 * i] = (uint32_t)m;
                 out[j * W + 2 * i + 1] = (uint32_t)(m >> 32);
+                out[(kBq + j) * W + 2 * i] = (uint32_t)mr;
+                out[(kBq + j) * W + 2 * i + 1] = (uint32_t)(mr >> 32);
             }
         }
     }
@@ -154,6 +172,7 @@ __global__ __launch_bounds__(64) void query_prep_kernel(const float *__restrict_
         kb[q] = sum * cb;
         qnorm[q] = sq;
         qwidth[q] = width;
+        qwidth2[q] = width2;
     }
 }
 
@@ -326,8 +345,9 @@ void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint
 }
 
 void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,
-                       float *kb, float *qnorm, float *qwidth, uint32_t *qplanes, hipStream_t s) {
-    query_prep_kernel<<<nq, 64, 0, s>>>(qrot, P, ex_bits, k1, kb, qnorm, qwidth, qplanes);
+                       float *kb, float *qnorm, float *qwidth, float *qwidth2, uint32_t *qplanes,
+                       hipStream_t s) {
+    query_prep_kernel<<<nq, 64, 0, s>>>(qrot, P, ex_bits, k1, kb, qnorm, qwidth, qwidth2, qplanes);
 }
 
 void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s) {

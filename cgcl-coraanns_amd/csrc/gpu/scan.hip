@@ -10,20 +10,32 @@
 // (filter_kernels.cuh:116, 696, 754). Unlike the reference Bitwise producer there is
 // no 2*topk cap per pair and no fixed-size shared output array.
 //
+// The <q',b> a candidate carries to CPU refinement is refined beyond Bq=8: survivors
+// get a second popcount against the quantised residual planes, and
+//     exact_ip = width * ip_int + width2 * ip_res     (about 16-bit precision)
+// which is what keeps the refined distances as accurate as the reference's default
+// FP16-LUT producer (filter_kernels.cuh:655-708) rather than its Bq=8 Bitwise one; the
+// filter decision itself uses the Bq=8 lower bound above, bit-exact with Bitwise.
+//
 // Work decomposition: one wave per workgroup; the waves pull scan units (one cluster
 // pass serving up to batch_q pairs) from eight per-XCD cursors over eight contiguous
 // unit ranges (workgroup i runs on XCD i % 8), stealing from the next range once
 // their own is exhausted, so the passes over one cluster stay on one XCD's L2. Each
 // lane evaluates one vector of a 64-vector tile: 128-bit code loads, factor loads from
-// the tile's SoA block, q-planes read through uniform (scalar) loads.
+// the tile's SoA block, q-planes read through uniform (scalar) loads or LDS; the next
+// tile's loads are issued before the current tile is evaluated.
 //
-// Publication (ring_queue.cuh:45-115): survivors of a wave are compacted with a ballot
-// and a lane-rank (mbcnt); lane 0 reserves all slots with one 64-bit atomicAdd on the
-// HBM counter; a slot whose position is below the cached write limit (released +
-// capacity) receives the 16-byte Candidate with one 128-bit store to the host-coherent
-// ring, otherwise the record goes to the HBM spill buffer and the drain kernel
-// publishes it once the CPU has released that slot.
+// Publication (ring_queue.cuh:45-115): survivors are compacted with a ballot and a lane
+// rank (mbcnt) into a per-wave LDS stage (record + code words). A full stage, and the
+// last one, is flushed with one 64-bit atomicAdd on the HBM position counter for all of
+// its records; each record then gets its residual inner product and goes to the
+// host-coherent ring with one write-through 16-byte store when its position is below
+// the cached write limit (released + capacity), or to the HBM spill buffer, which the
+// drain kernel publishes once the CPU has released that slot.
 #include <float.h>
+
+#include <mutex>
+#include <unordered_map>
 
 #include "engine_internal.h"
 
@@ -57,9 +69,18 @@ struct Words {
     static constexpr int kMax = W > 0 ? W : 32;
 };
 
+// Survivor stage of one wave: kCap records of 16 bytes plus their code words, about
+// 4 KB, so LDS never limits the scan's occupancy below 32 waves per CU for P <= 128.
 template <int W>
-__device__ __forceinline__ void load_codes(const uint8_t *__restrict__ tile, int lane, uint32_t rw,
-                                           uint32_t (&x)[Words<W>::kMax]) {
+struct Stage {
+    static constexpr int kWords = Words<W>::kMax;
+    static constexpr int kFit = 4096 / (16 + 4 * kWords) / 64 * 64;
+    static constexpr int kCap = kFit < 64 ? 64 : kFit;
+};
+
+template <int W>
+__device__ __forceinline__ void load_codes(const uint8_t *__restrict__ tile, uint32_t lane,
+                                           uint32_t rw, uint32_t (&x)[Words<W>::kMax]) {
     const uint32_t nw = W > 0 ? (uint32_t)W : rw;
     const uint4 *g4 = reinterpret_cast<const uint4 *>(tile);
 #pragma unroll
@@ -103,6 +124,11 @@ __device__ __forceinline__ int popc_ip(const uint32_t (&x)[Words<W>::kMax],
     return ip;
 }
 
+// Two-stage <q',b>: width * ip_int rounded, then width2 * ip_res added with one rounding.
+__device__ __forceinline__ float two_stage_ip(float width, int ip, float width2, int ip_res) {
+    return __fmaf_rn(width2, (float)ip_res, __fmul_rn(width, (float)ip));
+}
+
 // One 16-byte Candidate store to the host-coherent ring that writes through the GPU L2
 // (system-scope coherence bits sc0 sc1). A plain store to host memory may stay in L2
 // until the next system-scope release, which a producer still running never issues, so
@@ -137,39 +163,57 @@ __device__ __noinline__ unsigned long long refresh_limit(unsigned long long *cac
     return lim;
 }
 
-// Must be called by all 64 lanes of the wave.
-__device__ __forceinline__ void publish(const QueueDev q, bool survive, uint4 rec,
-                                        unsigned long long &limit) {
-    const unsigned long long mask = __ballot(survive);
-    if (mask == 0)
-        return;
-    const uint32_t cnt = (uint32_t)__popcll(mask);
-    const int lane = threadIdx.x & 63;
+// Ring slot when pos is below the write limit, otherwise the HBM spill buffer.
+__device__ __forceinline__ void place_record(const QueueDev &q, unsigned long long pos,
+                                             unsigned long long limit, uint4 rec) {
+    if (pos < limit) {
+        store_ring(&q.items[pos & q.mask], rec);
+    } else {
+        const unsigned long long s = atomicAdd(q.spill_count, 1ull);
+        if (s < q.spill_capacity) {
+            q.spill[s].item = rec;
+            q.spill[s].position = pos;
+        } else {
+            atomicExch(q.spill_overflow, 1);
+        }
+    }
+}
+
+// Publish the n staged survivors of this wave (n wave-uniform, 0 < n <= kCap). Must be
+// called by all 64 lanes; the workgroup is this one wave. Staged records carry ip_int
+// in their exact_ip word; it is replaced by the two-stage estimate here.
+template <int W>
+__device__ __forceinline__ void flush_stage(const ScanParams &p, const QueueDev &q, uint32_t n,
+                                            const uint4 *s_rec, const uint32_t *s_code,
+                                            unsigned long long &limit, uint32_t lane) {
+    constexpr int K = Words<W>::kMax;
+    constexpr int CAP = Stage<W>::kCap;
+    const uint32_t nw = W > 0 ? (uint32_t)W : p.P / 32;
+    __syncthreads();  // staged LDS writes of every lane are visible
     unsigned long long base = 0;
     if (lane == 0)
-        base = atomicAdd(q.produced, (unsigned long long)cnt);
+        base = atomicAdd(q.produced, (unsigned long long)n);
     base = shfl0_u64(base);
-    if (base + cnt > limit) {
+    if (base + n > limit) {
         unsigned long long fresh = 0;
         if (lane == 0)
             fresh = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released, q.capacity,
-                                  base + cnt);
+                                  base + n);
         limit = shfl0_u64(fresh);
     }
-    if (survive) {
-        const unsigned long long pos = base + lane_rank(mask);
-        if (pos < limit) {
-            store_ring(&q.items[pos & q.mask], rec);
-        } else {
-            const unsigned long long s = atomicAdd(q.spill_count, 1ull);
-            if (s < q.spill_capacity) {
-                q.spill[s].item = rec;
-                q.spill[s].position = pos;
-            } else {
-                atomicExch(q.spill_overflow, 1);
-            }
-        }
+    for (uint32_t i = lane; i < n; i += 64) {
+        uint4 rec = s_rec[i];
+        uint32_t x[K];
+#pragma unroll
+        for (int w = 0; w < K; ++w)
+            x[w] = (uint32_t)w < nw ? s_code[w * CAP + i] : 0u;
+        const uint32_t query = rec.x & 0xFFFFu;
+        const uint32_t *res = p.qplanes + ((size_t)query * 2 + 1) * kBq * nw;
+        const int ip_res = popc_ip<W>(x, res, nw);
+        rec.z = __float_as_uint(two_stage_ip(p.qwidth[query], (int)rec.z, p.qwidth2[query], ip_res));
+        place_record(q, base + i, limit, rec);
     }
+    __syncthreads();  // the stage may be refilled
 }
 
 __device__ __forceinline__ float read_threshold(const float *thresholds, int live, uint32_t query) {
@@ -207,7 +251,13 @@ struct PlaneStore {
 
 template <int W, int QMAX, int KIND>
 __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t unit_set) {
-    __shared__ uint32_t s_planes[PlaneStore<W, QMAX>::kRegs ? 1 : QMAX * kBq * 32];
+    constexpr int K = Words<W>::kMax;
+    constexpr int CAP = Stage<W>::kCap;
+    constexpr bool kRegs = PlaneStore<W, QMAX>::kRegs;
+    constexpr bool kStaged = KIND != kDense;
+    __shared__ uint32_t s_planes[kRegs ? 1 : QMAX * kBq * K];
+    __shared__ uint4 s_rec[kStaged ? CAP : 1];
+    __shared__ uint32_t s_code[kStaged ? CAP * K : 1];
     const uint32_t lane = threadIdx.x;
     const uint32_t rw = p.P / 32;
     const uint32_t nw = W > 0 ? (uint32_t)W : rw;
@@ -229,6 +279,7 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
     const uint32_t U = p.num_units[unit_set];
     const uint32_t ubase = unit_set ? p.num_units[0] : 0u;
     uint32_t range = blockIdx.x % kNumXcd, tries = 0;
+    uint32_t staged = 0;
     unsigned long long limit =
         KIND == kDense ? 0ull
                        : __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -242,6 +293,8 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
         const uint32_t pair_begin = uniform(un.pair_begin);
         const ClusterMeta cm = meta[cluster];
         const uint32_t n = uniform(cm.n), start = uniform(cm.start), tbase = uniform(cm.tile_base);
+        if (n == 0)
+            continue;  // an empty cluster owns no tile (its tile_base may be one past the end)
 
         uint32_t word0[QMAX];
         float width[QMAX], k1[QMAX], gadd[QMAX], gerr[QMAX], cutoff[QMAX];
@@ -256,16 +309,16 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
                 probe0 = probe;
             }
             word0[j] = w0;
+            cutoff[j] = KIND == kDense ? FLT_MAX : uniformf(read_threshold(thresholds, live, query));
             width[j] = uniformf(qwidth[query]);
             k1[j] = uniformf(qk1[query]);
             const size_t pi = (size_t)query * nprobe + probe;
             gadd[j] = uniformf(pgadd[pi]);
             gerr[j] = uniformf(pgerr[pi]);
-            cutoff[j] = KIND == kDense ? FLT_MAX : uniformf(read_threshold(thresholds, live, query));
         }
-        uint32_t preg[PlaneStore<W, QMAX>::kRegs ? kBq * (W > 0 ? W : 1) : 1];
-        if constexpr (PlaneStore<W, QMAX>::kRegs) {
-            const uint32_t *src = qplanes + (size_t)query0 * kBq * W;
+        uint32_t preg[kRegs ? kBq * (W > 0 ? W : 1) : 1];
+        if constexpr (kRegs) {
+            const uint32_t *src = qplanes + (size_t)query0 * 2 * kBq * W;
 #pragma unroll
             for (int i = 0; i < kBq * W; ++i)
                 preg[i] = uniform(src[i]);
@@ -273,14 +326,12 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
             __syncthreads();
             for (uint32_t i = lane; i < QMAX * kBq * nw; i += 64) {
                 const uint32_t j = i / (kBq * nw), r = i % (kBq * nw);
-                const uint32_t w0 = word0[0];
-                uint32_t wj = w0;
+                uint32_t wj = word0[0];
 #pragma unroll
                 for (int jj = 1; jj < QMAX; ++jj)
                     if ((uint32_t)jj == j)
                         wj = word0[jj];
-                (void)w0;
-                s_planes[i] = j < count ? qplanes[(size_t)(wj & 0xFFFFu) * kBq * nw + r] : 0u;
+                s_planes[i] = j < count ? qplanes[(size_t)(wj & 0xFFFFu) * 2 * kBq * nw + r] : 0u;
             }
             __syncthreads();
         }
@@ -288,12 +339,27 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
         if (KIND == kRecovery)
             seeds = seed_bits + ((size_t)query0 * vanguard + probe0) * seed_words;
         const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
-        for (uint32_t t = 0; t < ntiles; ++t) {
-            const uint8_t *tile = tiles + (size_t)(tbase + t) * tile_bytes;
-            uint32_t x[Words<W>::kMax];
+        // tile t is evaluated while tile t+1 (or t again at the end) is being loaded
+        uint32_t x[K], xn[K];
+        float fa, fr, fe, fan, frn, fen;
+        {
+            const uint8_t *tile = tiles + (size_t)tbase * tile_bytes;
             load_codes<W>(tile, lane, rw, x);
             const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
-            const float fa = fac[lane], fr = fac[64 + lane], fe = fac[128 + lane];
+            fa = fac[lane];
+            fr = fac[64 + lane];
+            fe = fac[128 + lane];
+        }
+        for (uint32_t t = 0; t < ntiles; ++t) {
+            {
+                const uint32_t tn = t + 1 < ntiles ? t + 1 : t;
+                const uint8_t *tile = tiles + (size_t)(tbase + tn) * tile_bytes;
+                load_codes<W>(tile, lane, rw, xn);
+                const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
+                fan = fac[lane];
+                frn = fac[64 + lane];
+                fen = fac[128 + lane];
+            }
             const uint32_t local = t * kTileVectors + lane;
             const bool valid = local < n;
             bool not_seed = true;
@@ -304,27 +370,54 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
                 if ((uint32_t)j >= count)
                     break;
                 int ip;
-                if constexpr (PlaneStore<W, QMAX>::kRegs)
+                if constexpr (kRegs)
                     ip = popc_ip<W>(x, preg, rw);
                 else
                     ip = popc_ip<W>(x, s_planes + j * kBq * nw, rw);
                 const float ex = width[j] * (float)ip;
                 const float low = fa + gadd[j] + fr * (ex + k1[j]) - fe * gerr[j];
-                if (KIND == kDense) {
+                if constexpr (KIND == kDense) {
                     if (valid) {
                         const uint32_t query = word0[j] & 0xFFFFu, probe = word0[j] >> 16;
+                        const uint32_t *res = qplanes + ((size_t)query * 2 + 1) * kBq * nw;
                         const size_t o = ((size_t)query * nprobe + probe) * p.dbg_stride + local;
                         p.dbg_ip[o] = ip;
+                        p.dbg_ip2[o] = popc_ip<W>(x, res, rw);
                         p.dbg_low[o] = low;
                     }
                 } else {
                     const bool survive = valid && not_seed && low < cutoff[j];
-                    const uint4 rec = make_uint4(word0[j], start + local, __float_as_uint(ex),
-                                                 __float_as_uint(low));
-                    publish(q, survive, rec, limit);
+                    const unsigned long long mask = __ballot(survive);
+                    if (mask != 0) {
+                        const uint32_t cnt = (uint32_t)__popcll(mask);
+                        if (staged + cnt > (uint32_t)CAP) {
+                            flush_stage<W>(p, q, staged, s_rec, s_code, limit, lane);
+                            staged = 0;
+                        }
+                        if (survive) {
+                            const uint32_t k = staged + lane_rank(mask);
+                            s_rec[k] = make_uint4(word0[j], start + local, (uint32_t)ip,
+                                                  __float_as_uint(low));
+#pragma unroll
+                            for (int w = 0; w < K; ++w)
+                                if ((uint32_t)w < nw)
+                                    s_code[w * CAP + k] = x[w];
+                        }
+                        staged += cnt;
+                    }
                 }
             }
+#pragma unroll
+            for (int w = 0; w < K; ++w)
+                x[w] = xn[w];
+            fa = fan;
+            fr = frn;
+            fe = fen;
         }
+    }
+    if constexpr (kStaged) {
+        if (staged)
+            flush_stage<W>(p, q, staged, s_rec, s_code, limit, lane);
     }
 }
 
@@ -346,23 +439,23 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 template <int W>
 __global__ __launch_bounds__(kVanThreads) void vanguard_seed_kernel(const ScanParams p) {
     __shared__ float s_low[kVanguardMaxCluster];
-    __shared__ float s_ex[kVanguardMaxCluster];
+    __shared__ int s_ip[kVanguardMaxCluster];
     __shared__ uint32_t s_hist[256];
     __shared__ uint32_t s_scan[kVanThreads];
     __shared__ uint32_t s_sel[kMaxVanguardKeep];
     __shared__ uint32_t s_unit, s_prefix, s_remaining, s_valid;
     __shared__ uint32_t s_range, s_tries;
+    __shared__ unsigned long long s_base, s_limit;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t rw = p.P / 32;
     const uint32_t U = p.num_units[0];
     const uint32_t per = (U + kNumXcd - 1) / kNumXcd;
+    const QueueDev q = p.queue;
     if (tid == 0) {
         s_range = blockIdx.x % kNumXcd;
         s_tries = 0;
+        s_limit = __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const QueueDev q = p.queue;
-    unsigned long long limit =
-        __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (;;) {
         if (tid == 0) {
             uint32_t u = U;
@@ -394,7 +487,7 @@ __global__ __launch_bounds__(kVanThreads) void vanguard_seed_kernel(const ScanPa
         const size_t pi = (size_t)query * p.nprobe + probe;
         const float gadd = p.pgadd[pi], gerr = p.pgerr[pi];
         const float cutoff = read_threshold(p.thresholds, p.thresholds_live, query);
-        const uint32_t *planes = p.qplanes + (size_t)query * kBq * rw;
+        const uint32_t *planes = p.qplanes + (size_t)query * 2 * kBq * rw;
         const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
         for (uint32_t t = wave; t < ntiles; t += kVanThreads / 64) {
             const uint8_t *tile = p.tiles + (size_t)(cm.tile_base + t) * p.tile_bytes;
@@ -408,7 +501,7 @@ __global__ __launch_bounds__(kVanThreads) void vanguard_seed_kernel(const ScanPa
                 const float low = fac[lane] + gadd + fac[64 + lane] * (ex + k1) -
                                   fac[128 + lane] * gerr;
                 s_low[local] = low < cutoff ? low : __uint_as_float(0x7FFFFFFFu);  // NaN: excluded
-                s_ex[local] = ex;
+                s_ip[local] = ip;
             }
         }
         if (tid == 0)
@@ -498,15 +591,30 @@ __global__ __launch_bounds__(kVanThreads) void vanguard_seed_kernel(const ScanPa
             if (pick)
                 atomicOr(&seed[i >> 5], 1u << (i & 31));
         }
+        // one reservation for the pair's seeds, then the residual pass per seed
+        if (tid == 0) {
+            const unsigned long long base = atomicAdd(q.produced, (unsigned long long)take);
+            unsigned long long lim = s_limit;
+            if (base + take > lim)
+                lim = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released,
+                                    q.capacity, base + take);
+            s_base = base;
+            s_limit = lim;
+        }
         __syncthreads();
-        const uint32_t rounds = (take + kVanThreads - 1) / kVanThreads;
-        for (uint32_t r = 0; r < rounds; ++r) {
-            const uint32_t s = r * kVanThreads + tid;
-            const bool ok = s < take;
-            const uint32_t local = ok ? s_sel[s] : 0u;
-            const uint4 rec = make_uint4(w0, cm.start + local, __float_as_uint(s_ex[local]),
-                                         __float_as_uint(s_low[local]));
-            publish(q, ok, rec, limit);
+        const unsigned long long base = s_base, limit = s_limit;
+        const float width2 = p.qwidth2[query];
+        for (uint32_t s = tid; s < take; s += kVanThreads) {
+            const uint32_t local = s_sel[s];
+            const uint8_t *tile =
+                p.tiles + (size_t)(cm.tile_base + local / kTileVectors) * p.tile_bytes;
+            uint32_t x[Words<W>::kMax];
+            load_codes<W>(tile, local % kTileVectors, rw, x);
+            const int ip_res = popc_ip<W>(x, planes + kBq * rw, rw);
+            const float ex = two_stage_ip(width, s_ip[local], width2, ip_res);
+            place_record(q, base + s, limit,
+                         make_uint4(w0, cm.start + local, __float_as_uint(ex),
+                                    __float_as_uint(s_low[local])));
         }
         __syncthreads();
     }
@@ -603,64 +711,96 @@ __global__ __launch_bounds__(256) void finish_kernel(QueueDev q, unsigned long l
     }
 }
 
+// Persistent grid = workgroups of this kernel resident on the whole device at once.
+template <class F>
+uint32_t resident_grid(F kernel, int block) {
+    static std::mutex mu;
+    static std::unordered_map<const void *, uint32_t> cache;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const void *key = reinterpret_cast<const void *>(kernel);
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end())
+        return it->second;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        per_cu <= 0 || cus <= 0) {
+        per_cu = 8;
+        cus = 256;
+    }
+    const uint32_t grid = (uint32_t)(per_cu * cus);
+    cache.emplace(key, grid);
+    return grid;
+}
+
+template <int W, int Q, int KIND>
+void launch_one(const ScanParams &p, uint32_t set, hipStream_t s) {
+    auto *k = scan_kernel<W, Q, KIND>;
+    k<<<resident_grid(k, 64), 64, 0, s>>>(p, set);
+}
+
 template <int W>
-int launch_scan_w(const ScanParams &p, uint32_t batch_q, int kind, uint32_t grid, uint32_t set,
-                  hipStream_t s) {
+int launch_scan_w(const ScanParams &p, uint32_t batch_q, int kind, uint32_t set, hipStream_t s) {
     if (kind == kFar) {
         if (batch_q <= 1)
-            scan_kernel<W, 1, kFar><<<grid, 64, 0, s>>>(p, set);
+            launch_one<W, 1, kFar>(p, set, s);
         else
-            scan_kernel<W, kMaxBatchQ, kFar><<<grid, 64, 0, s>>>(p, set);
+            launch_one<W, kMaxBatchQ, kFar>(p, set, s);
     } else if (kind == kRecovery) {
-        scan_kernel<W, 1, kRecovery><<<grid, 64, 0, s>>>(p, set);
+        launch_one<W, 1, kRecovery>(p, set, s);
     } else {
-        scan_kernel<W, kMaxBatchQ, kDense><<<grid, 64, 0, s>>>(p, set);
+        launch_one<W, kMaxBatchQ, kDense>(p, set, s);
     }
     return 0;
 }
 
+template <int W>
+void launch_seed_w(const ScanParams &p, hipStream_t s) {
+    auto *k = vanguard_seed_kernel<W>;
+    k<<<resident_grid(k, kVanThreads), kVanThreads, 0, s>>>(p);
+}
+
 }  // namespace
 
-int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, uint32_t grid,
-                hipStream_t s) {
-    // unit set: vanguard units for the recovery pass, far units otherwise; the dense
-    // debug pass runs over both sets (two launches)
+int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, hipStream_t s) {
+    // unit set: vanguard units for the recovery pass, far units otherwise
     const uint32_t set = kind == kRecovery ? 0u : 1u;
     switch (W) {
-    case 2: return launch_scan_w<2>(p, batch_q, kind, grid, set, s);
-    case 4: return launch_scan_w<4>(p, batch_q, kind, grid, set, s);
-    case 6: return launch_scan_w<6>(p, batch_q, kind, grid, set, s);
-    case 8: return launch_scan_w<8>(p, batch_q, kind, grid, set, s);
-    case 12: return launch_scan_w<12>(p, batch_q, kind, grid, set, s);
-    case 16: return launch_scan_w<16>(p, batch_q, kind, grid, set, s);
-    case 24: return launch_scan_w<24>(p, batch_q, kind, grid, set, s);
-    case 32: return launch_scan_w<32>(p, batch_q, kind, grid, set, s);
-    default: return launch_scan_w<0>(p, batch_q, kind, grid, set, s);
+    case 2: return launch_scan_w<2>(p, batch_q, kind, set, s);
+    case 4: return launch_scan_w<4>(p, batch_q, kind, set, s);
+    case 6: return launch_scan_w<6>(p, batch_q, kind, set, s);
+    case 8: return launch_scan_w<8>(p, batch_q, kind, set, s);
+    case 12: return launch_scan_w<12>(p, batch_q, kind, set, s);
+    case 16: return launch_scan_w<16>(p, batch_q, kind, set, s);
+    case 24: return launch_scan_w<24>(p, batch_q, kind, set, s);
+    case 32: return launch_scan_w<32>(p, batch_q, kind, set, s);
+    default: return launch_scan_w<0>(p, batch_q, kind, set, s);
     }
 }
 
-int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t grid, uint32_t set,
-                    hipStream_t s) {
+int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t set, hipStream_t s) {
     switch (W) {
-    case 2: return launch_scan_w<2>(p, 8, kind, grid, set, s);
-    case 4: return launch_scan_w<4>(p, 8, kind, grid, set, s);
-    case 6: return launch_scan_w<6>(p, 8, kind, grid, set, s);
-    case 8: return launch_scan_w<8>(p, 8, kind, grid, set, s);
-    case 12: return launch_scan_w<12>(p, 8, kind, grid, set, s);
-    case 16: return launch_scan_w<16>(p, 8, kind, grid, set, s);
-    case 24: return launch_scan_w<24>(p, 8, kind, grid, set, s);
-    case 32: return launch_scan_w<32>(p, 8, kind, grid, set, s);
-    default: return launch_scan_w<0>(p, 8, kind, grid, set, s);
+    case 2: return launch_scan_w<2>(p, 8, kind, set, s);
+    case 4: return launch_scan_w<4>(p, 8, kind, set, s);
+    case 6: return launch_scan_w<6>(p, 8, kind, set, s);
+    case 8: return launch_scan_w<8>(p, 8, kind, set, s);
+    case 12: return launch_scan_w<12>(p, 8, kind, set, s);
+    case 16: return launch_scan_w<16>(p, 8, kind, set, s);
+    case 24: return launch_scan_w<24>(p, 8, kind, set, s);
+    case 32: return launch_scan_w<32>(p, 8, kind, set, s);
+    default: return launch_scan_w<0>(p, 8, kind, set, s);
     }
 }
 
-int launch_vanguard_seed(const ScanParams &p, uint32_t W, uint32_t grid, hipStream_t s) {
+int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s) {
     switch (W) {
-    case 2: vanguard_seed_kernel<2><<<grid, kVanThreads, 0, s>>>(p); break;
-    case 4: vanguard_seed_kernel<4><<<grid, kVanThreads, 0, s>>>(p); break;
-    case 8: vanguard_seed_kernel<8><<<grid, kVanThreads, 0, s>>>(p); break;
-    case 24: vanguard_seed_kernel<24><<<grid, kVanThreads, 0, s>>>(p); break;
-    default: vanguard_seed_kernel<0><<<grid, kVanThreads, 0, s>>>(p); break;
+    case 2: launch_seed_w<2>(p, s); break;
+    case 4: launch_seed_w<4>(p, s); break;
+    case 8: launch_seed_w<8>(p, s); break;
+    case 24: launch_seed_w<24>(p, s); break;
+    default: launch_seed_w<0>(p, s); break;
     }
     return 0;
 }

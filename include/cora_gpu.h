@@ -155,20 +155,23 @@ enum cora_debug_array {
     CORA_DBG_K1XSUMQ = 1,         /* f32 [nq] */
     CORA_DBG_KBXSUMQ = 2,         /* f32 [nq] */
     CORA_DBG_Q_WIDTH = 3,         /* f32 [nq] Bq=8 quantisation step */
-    CORA_DBG_Q_PLANES = 4,        /* u32 [nq][8][P/32], dim 32w+l at bit l of word w */
+    CORA_DBG_Q_PLANES = 4,        /* u32 [nq][16][P/32], dim 32w+l at bit l of word w: planes
+                                     0..7 = Bq=8 query qint, 8..15 = quantised residual qres */
     CORA_DBG_PROBE_IDX = 5,       /* i32 [nq][nprobe] ascending distance */
     CORA_DBG_PROBE_GADD = 6,      /* f32 [nq][nprobe] */
     CORA_DBG_PROBE_GERR = 7,      /* f32 [nq][nprobe] */
-    CORA_DBG_PAIRS = 8            /* i32 [npairs][3] (cluster, query, probe), scan order */
+    CORA_DBG_PAIRS = 8,           /* i32 [npairs][3] (cluster, query, probe), scan order */
+    CORA_DBG_Q_WIDTH2 = 9         /* f32 [nq] residual quantisation step (width / 254) */
 };
 int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t bytes);
 
 /* Dense estimator for parity tests: for every (query, probe) pair of the last launched
  * search, evaluate every vector of the probed cluster with the scan kernel's estimator
- * and write ip_int (i32) and low distance (f32) to out_ip / out_low, laid out
- * [nq][nprobe][max_cluster] (entries past the cluster size are left untouched). */
-int cora_gpu_debug_dense(cora_gpu_engine *engine, int32_t *out_ip, float *out_low,
-                         uint64_t capacity_elems);
+ * and write ip_int = <b, qint> (i32), the residual inner product <b, qres> (i32) and the
+ * low distance (f32) to out_ip / out_ip2 / out_low, laid out [nq][nprobe][max_cluster]
+ * (entries past the cluster size are left untouched). */
+int cora_gpu_debug_dense(cora_gpu_engine *engine, int32_t *out_ip, int32_t *out_ip2,
+                         float *out_low, uint64_t capacity_elems);
 
 /* ---- Index-build and evaluation tools (no counterpart in the reference's search path;
  * they replace its offline Faiss k-means, tools/data/train_ivf.py:11-47, and the

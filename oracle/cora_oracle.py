@@ -223,6 +223,31 @@ def quantize_query_bitwise(qr: np.ndarray):
     return qint, width
 
 
+def quantize_query_residual(qr: np.ndarray, qint: np.ndarray, width: np.ndarray):
+    """Second-stage query quantisation of this engine (no counterpart in the reference's
+    Bitwise producer; it replaces the precision the reference's default FP16-LUT producer
+    gives the <q',b> it hands to CPU refinement, query_kernels.cuh:199-221):
+    r = fma(-width, qint, q') (the exact difference rounded once to f32; in float64 the
+    product of an f32 and an 8-bit integer and this difference are exact), width2 =
+    width/254, qres = clamp(rint(r * (1/width2)), -127, 127).
+    Returns qres int32 [nq, P], width2 f32."""
+    qr = np.asarray(qr, dtype=np.float32)
+    width = np.asarray(width, dtype=np.float32)
+    r = (qr.astype(np.float64) - width[:, None].astype(np.float64) * qint.astype(np.float64)).astype(np.float32)
+    width2 = (width / np.float32(254.0)).astype(np.float32)
+    inv2 = (np.float32(1.0) / width2).astype(np.float32)
+    qres = np.clip(np.rint((r * inv2[:, None]).astype(np.float32)), -127, 127).astype(np.int32)
+    return qres, width2
+
+
+def exact_ip_two_stage(ip_int, ip_res, width, width2):
+    """<q',b> carried to CPU refinement: fl(fl(width*ip_int) + width2*ip_res), one
+    rounding for the multiply-add (float64 evaluation of an exact product)."""
+    e1 = (np.float32(width) * np.asarray(ip_int, dtype=np.float32)).astype(np.float32)
+    v = np.float64(np.float32(width2)) * np.asarray(ip_res, np.float64) + e1.astype(np.float64)
+    return v.astype(np.float32)
+
+
 def query_planes_msb(qint: np.ndarray) -> np.ndarray:
     """Bit planes of (qint & 0xFF): plane j word w bit (31-l) = bit j of dim 32w+l
     (query_kernels.cuh:171-188). Returns u32 [nq, 8, P/32]."""
@@ -405,6 +430,7 @@ def hybrid_search(sd: SearchData, queries: np.ndarray, topk: int, nprobe: int, m
     qr = rotate(queries, sd.rotator)
     k1, kb = query_factors(qr, ex_bits)
     qint, width = quantize_query_bitwise(qr)
+    qres, width2 = quantize_query_residual(qr, qint, width)
     planes = query_planes_msb(qint)
     idx, g_add, g_err, _ = coarse_probe(qr, sd.centroids, nprobe, metric)
     thr = np.full(nq, F32_MAX, np.float32) if thresholds is None else np.asarray(thresholds, np.float32)
@@ -429,13 +455,15 @@ def hybrid_search(sd: SearchData, queries: np.ndarray, topk: int, nprobe: int, m
             if keep.size == 0:
                 continue
             gids = s + keep
+            ipr = ip_int_direct(sd.bits[gids], qres[q])
+            eip2 = exact_ip_two_stage(ipi[keep], ipr, width[q], width2[q])
             ip2 = excode_ip(qr[q], sd.long_codes[gids], P)
-            rd = refine_dist(sd.ex_factors[gids, 0], sd.ex_factors[gids, 1], g_add[q, p], eip[keep],
+            rd = refine_dist(sd.ex_factors[gids, 0], sd.ex_factors[gids, 1], g_add[q, p], eip2,
                              ip2, kb[q], ex_bits)
             for j, gid in enumerate(gids):
                 cset.add(int(gid))
                 lows[(q, int(gid))] = low[keep[j]]
-                eips[(q, int(gid))] = eip[keep[j]]
+                eips[(q, int(gid))] = eip2[j]
                 items.append((float(rd[j]), int(sd.ids[gid])))
         cands.append(cset)
         items.sort(key=lambda t: t[0])
@@ -474,6 +502,9 @@ PINNED = {
     "rotate": "golden: ref_dump rotated_queries (reference MatrixRotator::rotate), 1e-5",
     "query_factors": "golden: ref_dump est_qvals k1xsumq/kbxsumq (reference SplitBatchQuery), 1e-5",
     "quantize_query_bitwise": "closed forms: zero query, +-amax -> +-127, half-even ties, |err|<=width/2",
+    "quantize_query_residual": "closed forms: |q' - width*qint - width2*qres| <= width2/2 (+ f32 rounding), "
+                               "zero query -> 0, exact multiples of width -> qres 0",
+    "exact_ip_two_stage": "bound: |two_stage - <q',b>_f64| <= popc(b)*width2/2 (+ f32 rounding) on random data",
     "ip_int_planes": "brute force: equals ip_int_direct on random bits / qint, incl. -128",
     "low_dist": "golden: reproduces reference est_low from est_ipx0 (estimator.hpp:315-318), 1e-5",
     "est_dist": "golden: reproduces reference est_dist from est_ipx0, 1e-5",

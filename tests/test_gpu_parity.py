@@ -4,7 +4,9 @@ Each stage is checked on the GPU's own inputs for that stage (e.g. the quantiser
 GPU-rotated queries), so integer results are compared bit-exactly and floating-point
 ones within 1e-5 relative (scaled by the magnitude of the terms), as the north star asks.
 """
+import subprocess
 import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -105,7 +107,8 @@ def gpu_intermediates(eng, case, nprobe):
         "k1": eng.debug_read(ca.DBG_K1XSUMQ, (nq,), np.float32),
         "kb": eng.debug_read(ca.DBG_KBXSUMQ, (nq,), np.float32),
         "width": eng.debug_read(ca.DBG_Q_WIDTH, (nq,), np.float32),
-        "planes": eng.debug_read(ca.DBG_Q_PLANES, (nq, 8, W), np.uint32),
+        "width2": eng.debug_read(ca.DBG_Q_WIDTH2, (nq,), np.float32),
+        "planes": eng.debug_read(ca.DBG_Q_PLANES, (nq, 16, W), np.uint32),
         "pidx": eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32),
         "gadd": eng.debug_read(ca.DBG_PROBE_GADD, (nq, nprobe), np.float32),
         "gerr": eng.debug_read(ca.DBG_PROBE_GERR, (nq, nprobe), np.float32),
@@ -131,10 +134,13 @@ def test_query_preparation(case_name, request):
     s = np.abs(g["qr"]).sum(1) + 1e-30
     assert np.all(np.abs(g["k1"] - k1) <= 1e-5 * s)
     assert np.all(np.abs(g["kb"] - kb) <= 1e-5 * 127.5 * s)
-    # Bq=8 quantisation: bit-exact on the same rotated input
+    # Bq=8 quantisation and its residual: bit-exact on the same rotated input
     qint, width = orc.quantize_query_bitwise(g["qr"])
     assert np.array_equal(g["width"].view(np.uint32), width.view(np.uint32))
-    assert np.array_equal(qint_from_planes(g["planes"]), qint)
+    assert np.array_equal(qint_from_planes(g["planes"][:, :8]), qint)
+    qres, width2 = orc.quantize_query_residual(g["qr"], qint, width)
+    assert np.array_equal(g["width2"].view(np.uint32), width2.view(np.uint32))
+    assert np.array_equal(qint_from_planes(g["planes"][:, 8:]), qres)
 
 
 @pytest.mark.parametrize("case_name", CASES)
@@ -174,8 +180,9 @@ def test_popcount_estimator_bit_exact(case_name, request):
     eng, _, _ = run_frozen(case, nprobe, 10)
     g = gpu_intermediates(eng, case, nprobe)
     maxc = case.ivf.max_cluster
-    ip, low = eng.debug_dense(case.queries.shape[0], nprobe, maxc)
-    qint = qint_from_planes(g["planes"])
+    ip, ipr, low = eng.debug_dense(case.queries.shape[0], nprobe, maxc)
+    qint = qint_from_planes(g["planes"][:, :8])
+    qres = qint_from_planes(g["planes"][:, 8:])
     sd = case.sd
     checked = 0
     for q in range(case.queries.shape[0]):
@@ -184,6 +191,8 @@ def test_popcount_estimator_bit_exact(case_name, request):
             s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
             want_ip = orc.ip_int_direct(sd.bits[s:s + n], qint[q])
             assert np.array_equal(ip[q, p, :n].astype(np.int64), want_ip), (q, p, c)
+            want_res = orc.ip_int_direct(sd.bits[s:s + n], qres[q])
+            assert np.array_equal(ipr[q, p, :n].astype(np.int64), want_res), (q, p, c)
             # the reference's bit-plane popcount restatement on the reference word layout
             words = sd.short_data[s * (sd.bits.shape[1] // 32):(s + n) * (sd.bits.shape[1] // 32)]
             words = words.reshape(-1, n).T
@@ -202,7 +211,8 @@ def test_popcount_estimator_bit_exact(case_name, request):
 def oracle_topk_from_gpu(case, g, nprobe, topk, thresholds=None):
     """Final top-k restated by the oracle from the GPU's query-side intermediates."""
     sd, P = case.sd, case.file.padded_dim
-    qint = qint_from_planes(g["planes"])
+    qint = qint_from_planes(g["planes"][:, :8])
+    qres = qint_from_planes(g["planes"][:, 8:])
     nq = case.queries.shape[0]
     out_d = np.full((nq, topk), F32_MAX, np.float32)
     out_i = np.zeros((nq, topk), np.uint32)
@@ -219,8 +229,10 @@ def oracle_topk_from_gpu(case, g, nprobe, topk, thresholds=None):
             low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p], ex, g["k1"][q])
             keep = np.nonzero(low < thr)[0]
             gids = s + keep
+            ipr = orc.ip_int_direct(sd.bits[gids], qres[q])
+            ex2 = orc.exact_ip_two_stage(ipi[keep], ipr, g["width"][q], g["width2"][q])
             ip2 = orc.excode_ip(g["qr"][q], sd.long_codes[gids], P)
-            rd = orc.refine_dist(sd.ex_factors[gids, 0], sd.ex_factors[gids, 1], g["gadd"][q, p], ex[keep], ip2,
+            rd = orc.refine_dist(sd.ex_factors[gids, 0], sd.ex_factors[gids, 1], g["gadd"][q, p], ex2, ip2,
                                  g["kb"][q], case.file.ex_bits)
             cset.update(int(x) for x in gids)
             items += list(zip(rd.tolist(), sd.ids[gids].tolist()))
@@ -271,7 +283,7 @@ def test_filter_candidate_set_with_frozen_thresholds(case_name, request):
     eng2, d, i = run_frozen(case, nprobe, topk, thresholds=thr)
     st = eng2.stats()
     # candidate count equals the oracle's {low < thr} up to lows within 1e-5 of thr
-    ip, low = eng2.debug_dense(case.queries.shape[0], nprobe, case.ivf.max_cluster)
+    _, _, low = eng2.debug_dense(case.queries.shape[0], nprobe, case.ivf.max_cluster)
     lo = hi = 0
     for q in range(case.queries.shape[0]):
         for p in range(nprobe):
@@ -321,3 +333,35 @@ def test_recall_against_brute_force(case_name, request):
     gt = orc.brute_force_gt(case.base, case.queries, topk, case.file.metric)
     r = orc.recall_at_k(i, gt, topk)
     assert r >= 0.9, r
+
+
+REF_DUMP = Path(__file__).resolve().parent.parent / "oracle" / "_ref" / "ref_dump"
+
+
+@pytest.mark.skipif(not REF_DUMP.exists(), reason="oracle/_ref/ref_dump not built (needs /root/reference)")
+def test_topk_and_recall_match_reference_cpu_path(synth, tmp_path):
+    """Final top-k ids and recall against the reference's own CPU search (rabitqlib
+    IVF::search with the FastScan-hacc estimator, ivf.hpp:670-732, run by the ref_dump
+    checker built from the reference sources) on the same index file, same queries and
+    same nprobe; production mode (live thresholds, vanguard 5, secondary filter)."""
+    from coraanns_amd.workloads import write_fbin
+
+    nprobes, topk = [4, 8, 16], 10
+    say("[gpu] top-k vs reference IVF::search")
+    qf = tmp_path / "q.fbin"
+    write_fbin(qf, synth.queries)
+    out = tmp_path / "ref"
+    out.mkdir()
+    subprocess.run([str(REF_DUMP), "index", str(synth.path), str(qf), str(out), str(topk)] +
+                   [str(n) for n in nprobes], check=True, capture_output=True, timeout=300)
+    ref_ids = np.fromfile(out / "search_ids.bin", np.uint32).reshape(len(nprobes), -1, topk)
+    gt = orc.brute_force_gt(synth.base, synth.queries, topk, 0)
+    eng = make_engine(synth, max(nprobes), topk, vanguard=5, frozen=False, secondary=True)
+    for li, nprobe in enumerate(nprobes):
+        _, ids = eng.search_all(synth.queries, topk, nprobe)
+        agree = np.mean([len(set(a) & set(b)) / topk for a, b in zip(ids.tolist(), ref_ids[li].tolist())])
+        r_gpu = orc.recall_at_k(ids, gt, topk)
+        r_ref = orc.recall_at_k(ref_ids[li], gt, topk)
+        say(f"[gpu]   nprobe={nprobe}: id agreement {agree:.4f}, recall gpu {r_gpu:.4f} ref {r_ref:.4f}")
+        assert agree >= 0.98, (nprobe, agree)
+        assert abs(r_gpu - r_ref) <= 0.01, (nprobe, r_gpu, r_ref)

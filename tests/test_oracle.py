@@ -169,6 +169,56 @@ def test_quantize_query_closed_forms():
     assert qint.min() >= -127 and qint.max() <= 127
 
 
+def test_residual_quantize_closed_forms():
+    # zero query: residual 0
+    z = np.zeros((1, 64), np.float32)
+    qint, w = orc.quantize_query_bitwise(z)
+    qres, w2 = orc.quantize_query_residual(z, qint, w)
+    assert not qres.any() and w2[0] == np.float32(1e-30) / np.float32(254.0)
+    # integer queries with amax 127: width 1, q' = qint exactly, residual 0
+    rng = np.random.default_rng(11)
+    v = rng.integers(-127, 128, (3, 128)).astype(np.float32)
+    v[:, 0] = 127.0
+    qint, w = orc.quantize_query_bitwise(v)
+    qres, w2 = orc.quantize_query_residual(v, qint, w)
+    assert np.all(w == 1.0) and not qres.any()
+    assert np.all(w2 == np.float32(1.0) / np.float32(254.0))
+    # random: two-stage reconstruction within width2/2 (plus f32 rounding of q')
+    x = rng.normal(0, 3, (20, 128)).astype(np.float32)
+    qint, w = orc.quantize_query_bitwise(x)
+    qres, w2 = orc.quantize_query_residual(x, qint, w)
+    recon = qint * w[:, None].astype(np.float64) + qres * w2[:, None].astype(np.float64)
+    err = np.abs(x.astype(np.float64) - recon)
+    assert np.all(err <= 0.5 * w2[:, None] + 4e-7 * np.abs(x))
+    assert qres.min() >= -127 and qres.max() <= 127
+    # the residual really refines: the one-stage error is about 127x larger on average
+    assert np.abs(x - qint * w[:, None]).mean() > 50 * err.mean()
+    # a plausible mistake (residual step = width instead of width / 254) breaks the bound
+    bad = np.clip(np.rint((x - qint * w[:, None]) / w[:, None]), -127, 127)
+    recon_bad = qint * w[:, None] + bad * w2[:, None]
+    assert not np.all(np.abs(x - recon_bad) <= 0.5 * w2[:, None] + 4e-7 * np.abs(x))
+
+
+def test_two_stage_inner_product_error_bound():
+    rng = np.random.default_rng(12)
+    for P in (64, 128, 768):
+        x = rng.normal(0, 1, (4, P)).astype(np.float32)
+        bits = rng.integers(0, 2, (200, P), dtype=np.uint8)
+        qint, w = orc.quantize_query_bitwise(x)
+        qres, w2 = orc.quantize_query_residual(x, qint, w)
+        for q in range(x.shape[0]):
+            ip1 = orc.ip_int_direct(bits, qint[q])
+            ipr = orc.ip_int_direct(bits, qres[q])
+            est = orc.exact_ip_two_stage(ip1, ipr, w[q], w2[q]).astype(np.float64)
+            exact = bits.astype(np.float64) @ x[q].astype(np.float64)
+            pc = bits.sum(1)
+            bound = pc * 0.5 * w2[q] + 2e-7 * (np.abs(est) + pc * np.abs(x[q]).max())
+            assert np.all(np.abs(est - exact) <= bound), P
+            # the Bq=8 estimate alone violates the same bound (the refinement matters)
+            one = orc.exact_ip_bitwise(ip1, w[q]).astype(np.float64)
+            assert not np.all(np.abs(one - exact) <= bound)
+
+
 def test_popcount_planes_equal_direct_inner_product():
     rng = np.random.default_rng(2)
     for P in (64, 128, 768):
