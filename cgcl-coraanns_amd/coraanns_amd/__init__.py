@@ -37,6 +37,8 @@ FLAG_CROSS_QUERY_REUSE = 4
 
 DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range(5)
 DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
+DBG_SEED_DIST, DBG_THRESHOLDS = 10, 11
+FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN = 1 << 3, 1 << 4
 
 
 class EngineUnavailable(RuntimeError):
@@ -74,7 +76,8 @@ class cora_search_stats(C.Structure):
     _fields_ = [("produced", C.c_uint64), ("spilled", C.c_uint64), ("overflow", C.c_int32),
                 ("stalled", C.c_int32), ("filter_ms", C.c_float), ("scan_ms", C.c_float),
                 ("scan_bytes", C.c_uint64), ("scan_units", C.c_uint64),
-                ("scan_vectors", C.c_uint64)]
+                ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float), ("probe_flops", C.c_uint64),
+                ("pass_produced", C.c_uint64 * 3), ("seeded_queries", C.c_uint64)]
 
 
 class cora_queue_view(C.Structure):
@@ -87,13 +90,16 @@ class cora_hybrid_config(C.Structure):
                 ("gpu_filter_timing", C.c_int), ("cross_query_reuse", C.c_int),
                 ("cpu_secondary_filter", C.c_int), ("vanguard_size", C.c_uint64),
                 ("queue_capacity", C.c_uint64), ("queue_spill_capacity", C.c_uint64),
-                ("metric", C.c_int), ("frozen_thresholds", C.c_int), ("cpu_threads", C.c_int)]
+                ("metric", C.c_int), ("frozen_thresholds", C.c_int), ("cpu_threads", C.c_int),
+                ("gpu_seed_refine", C.c_int), ("extra_flags", C.c_uint32)]
 
 
 class cora_hybrid_stats(C.Structure):
     _fields_ = [("submitted", C.c_uint64), ("spilled", C.c_uint64), ("refined", C.c_uint64),
                 ("gpu_filter_ms", C.c_float), ("scan_ms", C.c_float), ("scan_bytes", C.c_uint64),
-                ("scan_units", C.c_uint64), ("scan_vectors", C.c_uint64)]
+                ("scan_units", C.c_uint64), ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float),
+                ("probe_flops", C.c_uint64), ("pass_produced", C.c_uint64 * 3),
+                ("seeded_queries", C.c_uint64)]
 
 
 class cora_ivf_info(C.Structure):
@@ -125,6 +131,7 @@ GPU_SIGNATURES = {
     "cora_gpu_destroy": [_P],
     "cora_gpu_last_error": [_P, C.c_char_p, C.c_size_t],
     "cora_gpu_load_index": [_P, _U64, _U64, _U64, _U64, _U64, _I, _P, _P, _P, _P, _P],
+    "cora_gpu_load_excodes": [_P, _P, _P],
     "cora_gpu_set_queue": [_P, _U64, _U64],
     "cora_gpu_prepare_workspace": [_P, _U64, _U64, _U64, _U64],
     "cora_gpu_free_workspace": [_P],
@@ -267,7 +274,7 @@ class HybridIndex:
     def __init__(self, device=0, *, profiling=False, candidate_stats=False, gpu_filter_timing=False,
                  cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                  queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
-                 cpu_threads=0):
+                 cpu_threads=0, gpu_seed_refine=True, extra_flags=0):
         _, host = _load()
         h = C.c_void_p()
         _host_check(host.cora_hybrid_create(C.byref(h), device))
@@ -277,17 +284,19 @@ class HybridIndex:
                        gpu_filter_timing=gpu_filter_timing, cross_query_reuse=cross_query_reuse,
                        cpu_secondary_filter=cpu_secondary_filter, vanguard_size=vanguard_size,
                        queue_capacity=queue_capacity, queue_spill_capacity=queue_spill_capacity,
-                       metric=metric, frozen_thresholds=frozen_thresholds, cpu_threads=cpu_threads)
+                       metric=metric, frozen_thresholds=frozen_thresholds, cpu_threads=cpu_threads,
+                       gpu_seed_refine=gpu_seed_refine, extra_flags=extra_flags)
 
     def configure(self, *, profiling=False, candidate_stats=False, gpu_filter_timing=False,
                   cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                   queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
-                  cpu_threads=0):
+                  cpu_threads=0, gpu_seed_refine=True, extra_flags=0):
         cfg = cora_hybrid_config(int(profiling), int(candidate_stats), int(gpu_filter_timing),
                                  int(cross_query_reuse), int(cpu_secondary_filter), int(vanguard_size),
                                  int(queue_capacity or 0),
                                  (1 << 64) - 1 if queue_spill_capacity is None else int(queue_spill_capacity),
-                                 int(metric), int(frozen_thresholds), int(cpu_threads))
+                                 int(metric), int(frozen_thresholds), int(cpu_threads),
+                                 int(gpu_seed_refine), int(extra_flags))
         _host_check(_load()[1].cora_hybrid_configure(self._h, C.byref(cfg)))
 
     def load_from_raw_pointers(self, num_vecs, dim, padded_dim, n_centroids, ex_bits, centroids,
@@ -350,7 +359,9 @@ class HybridIndex:
     def stats(self):
         s = cora_hybrid_stats()
         _load()[1].cora_hybrid_stats_get(self._h, C.byref(s))
-        return {k: getattr(s, k) for k, _ in cora_hybrid_stats._fields_}
+        out = {k: getattr(s, k) for k, _ in cora_hybrid_stats._fields_}
+        out["pass_produced"] = list(out["pass_produced"])
+        return out
 
     def capture_thresholds(self, nq):
         out = np.empty(nq, np.float32)

@@ -42,7 +42,7 @@ struct cora_gpu_engine {
     unsigned long long wall_clock_khz = 0;  // device wall_clock64() rate
     hipStream_t stream = nullptr, stream_d2h = nullptr;
     hipEvent_t ev_prep = nullptr, ev_probe = nullptr, ev_f0 = nullptr, ev_f1 = nullptr,
-               ev_s0 = nullptr, ev_s1 = nullptr;
+               ev_s0 = nullptr, ev_s1 = nullptr, ev_p0 = nullptr, ev_p1 = nullptr;
     // index
     bool loaded = false;
     uint64_t N = 0, dim = 0, P = 0, nl = 0, ex_bits = 0, max_cluster = 0, total_tiles = 0;
@@ -51,6 +51,8 @@ struct cora_gpu_engine {
     float *d_cent = nullptr, *d_cnorm = nullptr, *d_rot = nullptr;
     uint8_t *d_tiles = nullptr;
     ClusterMeta *d_meta = nullptr;
+    uint8_t *d_excodes = nullptr;  // optional HBM copy of the 7-bit ex-codes
+    float *d_exfac = nullptr;
     // queue configuration (hybrid.cuh:105-106)
     uint64_t qcap = 1ull << 26, spill_cap = 1ull << 24;
     // workspace
@@ -62,6 +64,10 @@ struct cora_gpu_engine {
     uint32_t *d_planes = nullptr, *d_bcount = nullptr, *d_bcursor = nullptr, *d_boff = nullptr,
              *d_uoff = nullptr, *d_nunits = nullptr, *d_cursor = nullptr, *d_seed = nullptr;
     int32_t *d_pidx = nullptr;
+    float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
+    float *d_van_low = nullptr;
+    int32_t *d_van_ip = nullptr;
+    uint32_t van_blocks = 0;
     Pair *d_pairs = nullptr;
     Unit *d_units = nullptr;
     unsigned long long *d_stats = nullptr;
@@ -140,6 +146,10 @@ ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool f
     p.seed_words = (uint32_t)E->seed_words;
     p.seed_bits = E->d_seed;
     p.queue = queue_dev(E);
+    p.van_low = E->d_van_low;
+    p.van_ip = E->d_van_ip;
+    p.van_stride = (uint32_t)E->max_cluster;
+    p.van_blocks = E->van_blocks;
     return p;
 }
 
@@ -173,6 +183,12 @@ void release_workspace(cora_gpu_engine *E) {
                          &E->d_nunits, &E->d_cursor, &E->d_seed})
         dfree(*p);
     dfree(E->d_pidx);
+    dfree(E->d_seed_dist);
+    dfree(E->d_seed_low);
+    dfree(E->d_seed_err);
+    dfree(E->d_van_low);
+    dfree(E->d_van_ip);
+    E->van_blocks = 0;
     dfree(E->d_pairs);
     dfree(E->d_units);
     dfree(E->d_stats);
@@ -254,7 +270,8 @@ int cora_gpu_create(cora_gpu_engine **out, int device) {
         E->wall_clock_khz = (unsigned long long)khz;
         HIPCHK(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
         HIPCHK(hipStreamCreateWithFlags(&E->stream_d2h, hipStreamNonBlocking));
-        for (hipEvent_t *ev : {&E->ev_prep, &E->ev_probe, &E->ev_f0, &E->ev_f1, &E->ev_s0, &E->ev_s1})
+        for (hipEvent_t *ev : {&E->ev_prep, &E->ev_probe, &E->ev_f0, &E->ev_f1, &E->ev_s0, &E->ev_s1,
+                               &E->ev_p0, &E->ev_p1})
             HIPCHK(hipEventCreate(ev));
         return CORA_OK;
     };
@@ -279,7 +296,10 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
     dfree(E->d_rot);
     dfree(E->d_tiles);
     dfree(E->d_meta);
-    for (hipEvent_t ev : {E->ev_prep, E->ev_probe, E->ev_f0, E->ev_f1, E->ev_s0, E->ev_s1})
+    dfree(E->d_excodes);
+    dfree(E->d_exfac);
+    for (hipEvent_t ev : {E->ev_prep, E->ev_probe, E->ev_f0, E->ev_f1, E->ev_s0, E->ev_s1, E->ev_p0,
+                          E->ev_p1})
         if (ev)
             (void)hipEventDestroy(ev);
     if (E->stream)
@@ -400,6 +420,37 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
     return CORA_OK;
 }
 
+int cora_gpu_load_excodes(cora_gpu_engine *E, const uint8_t *h_long_codes,
+                          const float *h_ex_factors) {
+    if (!E)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->loaded)
+        return fail(E, CORA_ERR_LOGIC, "load the index before its ex-codes");
+    if (E->d_excodes)
+        return fail(E, CORA_ERR_LOGIC, "ex-codes already loaded");
+    if (E->ws)
+        return fail(E, CORA_ERR_LOGIC, "load ex-codes before prepare_workspace");
+    if (!h_long_codes || !h_ex_factors || E->ex_bits != 7)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "GPU ex-codes need 7 ex-bits and both arrays");
+    HIPCHK(hipSetDevice(E->device));
+    const uint64_t lc = E->P * 7 / 8;
+    int rc = dalloc(E, E->d_excodes, E->N * lc);
+    if (rc == CORA_OK)
+        rc = dalloc(E, E->d_exfac, E->N * 2);
+    hipError_t r = hipSuccess;
+    if (rc == CORA_OK)
+        r = hipMemcpy(E->d_excodes, h_long_codes, E->N * lc, hipMemcpyHostToDevice);
+    if (rc == CORA_OK && r == hipSuccess)
+        r = hipMemcpy(E->d_exfac, h_ex_factors, E->N * 2 * sizeof(float), hipMemcpyHostToDevice);
+    if (rc == CORA_OK && r != hipSuccess)
+        rc = fail(E, CORA_ERR_RUNTIME, std::string("ex-code upload: ") + hipGetErrorString(r));
+    if (rc != CORA_OK) {
+        dfree(E->d_excodes);
+        dfree(E->d_exfac);
+    }
+    return rc;
+}
+
 int cora_gpu_set_queue(cora_gpu_engine *E, uint64_t capacity, uint64_t spill_capacity) {
     if (!E)
         return CORA_ERR_INVALID_ARGUMENT;
@@ -446,11 +497,22 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_uoff, nb + 1));
         TRY(dalloc(E, E->d_nunits, 2));
         TRY(dalloc(E, E->d_cursor, kNumXcd));
-        TRY(dalloc(E, E->d_stats, 3));
+        TRY(dalloc(E, E->d_stats, 8));
         TRY(dalloc(E, E->d_pairs, np));
         TRY(dalloc(E, E->d_units, np));
         TRY(dalloc(E, E->d_thr_snap, max_q));
         TRY(dalloc(E, E->d_seed, std::max<uint64_t>(1, max_q * depth * seed_words)));
+        if (depth > 0 && E->max_cluster > (uint64_t)kVanguardMaxCluster) {
+            E->van_blocks = vanguard_seed_grid(E->W);
+            TRY(dalloc(E, E->d_van_low, (uint64_t)E->van_blocks * E->max_cluster));
+            TRY(dalloc(E, E->d_van_ip, (uint64_t)E->van_blocks * E->max_cluster));
+        }
+        if (E->d_excodes) {
+            const uint64_t slots = max_q * depth * std::max<uint64_t>(max_topk, 20);
+            TRY(dalloc(E, E->d_seed_dist, slots));
+            TRY(dalloc(E, E->d_seed_low, slots));
+            TRY(dalloc(E, E->d_seed_err, slots));
+        }
         TRY(halloc(E, E->h_qrot, max_q * E->P, hipHostMallocDefault));
         TRY(halloc(E, E->h_kb, max_q, hipHostMallocDefault));
         TRY(halloc(E, E->h_gadd, np, hipHostMallocDefault));
@@ -580,8 +642,12 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
                           E->stream_d2h));
     HIPCHK(hipMemcpyAsync(E->h_kb, E->d_kb, (size_t)nq * 4, hipMemcpyDeviceToHost, E->stream_d2h));
     // coarse probing (hybrid.cu:465-498)
+    if (timing)
+        HIPCHK(hipEventRecord(E->ev_p0, s));
     launch_dist_gemm(E->d_qrot, E->d_qnorm, E->d_cent, E->d_cnorm, nq, (uint32_t)E->nl, P,
                      E->d_dist, s);
+    if (timing)
+        HIPCHK(hipEventRecord(E->ev_p1, s));
     launch_select(E->d_dist, nq, (uint32_t)E->nl, np, E->d_pidx, s);
     launch_probe_refine(E->d_qrot, E->d_cent, E->d_pidx, nq, np, P, E->metric, E->d_gadd,
                         E->d_gerr, s);
@@ -597,24 +663,47 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         memcpy(E->h_thr_stage, E->h_thr, (size_t)nq * 4);
         HIPCHK(hipMemcpyAsync(E->d_thr_snap, E->h_thr_stage, (size_t)nq * 4, hipMemcpyHostToDevice, s));
     }
-    const ScanParams p = scan_params(E, depth, keep, frozen);
+    ScanParams p = scan_params(E, depth, keep, frozen);
+    // GPU seed thresholds: live thresholds only (frozen mode keeps the launch snapshot)
+    const bool gpu_seed = depth > 0 && E->d_excodes && E->d_seed_dist &&
+                          !(a->flags & CORA_FLAG_NO_GPU_SEED) &&
+                          (!frozen || (a->flags & CORA_FLAG_GPU_SEED_FROZEN));
+    if (gpu_seed) {
+        p.ex_codes = E->d_excodes;
+        p.ex_factors = E->d_exfac;
+        p.qrot = E->d_qrot;
+        p.kb = E->d_kb;
+        p.seed_dist = E->d_seed_dist;
+        p.seed_low = E->d_seed_low;
+        p.seed_err = E->d_seed_err;
+    }
+    launch_fill_u64(E->d_stats + 3, 0ull, 4, s);  // per-pass counters of this launch
     if (timing)
         HIPCHK(hipEventRecord(E->ev_f0, s));
     if (depth > 0) {
         launch_fill_u32(E->d_seed, 0u, (size_t)nq * depth * E->seed_words, s);
+        if (gpu_seed)  // +inf marks seed slots the seed pass leaves unused
+            launch_fill_u32(reinterpret_cast<uint32_t *>(E->d_seed_dist), 0x7F800000u,
+                            (size_t)nq * depth * keep, s);
         launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
         launch_vanguard_seed(p, E->W, s);
+        if (gpu_seed)
+            launch_seed_thresholds(E->d_seed_dist, E->d_seed_low, E->d_seed_err, nq, depth * keep,
+                                   a->topk, frozen ? E->d_thr_snap : E->h_thr, E->d_stats + 6, s);
     }
+    launch_copy_u64(E->d_produced, E->d_stats + 3, s);
     launch_cursor_init(E->d_cursor, E->d_nunits, 1, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_s0, s));
     launch_scan(p, E->W, batch, 0, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_s1, s));
+    launch_copy_u64(E->d_produced, E->d_stats + 4, s);
     if (depth > 0) {
         launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
         launch_scan(p, E->W, 1, 1, s);
     }
+    launch_copy_u64(E->d_produced, E->d_stats + 5, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_f1, s));
     launch_finish(queue_dev(E), kDrainMaxSeconds * 1000ull * E->wall_clock_khz, s);
@@ -648,7 +737,7 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     HIPCHK(hipSetDevice(E->device));
     HIPCHK(hipStreamSynchronize(E->stream));
     HIPCHK(hipStreamSynchronize(E->stream_d2h));
-    unsigned long long stats[3] = {0, 0, 0};
+    unsigned long long stats[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int stalled = 0;
     HIPCHK(hipMemcpy(stats, E->d_stats, sizeof(stats), hipMemcpyDeviceToHost));
     HIPCHK(hipMemcpy(&stalled, E->d_stalled, sizeof(int), hipMemcpyDeviceToHost));
@@ -661,9 +750,14 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     out.scan_bytes = stats[0];
     out.scan_units = stats[1];
     out.scan_vectors = stats[2];
+    out.probe_flops = 2ull * E->last.num_queries * E->P * E->nl;
+    for (int i = 0; i < 3; ++i)
+        out.pass_produced[i] = stats[3 + i];
+    out.seeded_queries = stats[6];
     if (E->last_timing) {
         HIPCHK(hipEventElapsedTime(&out.filter_ms, E->ev_f0, E->ev_f1));
         HIPCHK(hipEventElapsedTime(&out.scan_ms, E->ev_s0, E->ev_s1));
+        HIPCHK(hipEventElapsedTime(&out.probe_ms, E->ev_p0, E->ev_p1));
     }
     if (st)
         *st = out;
@@ -740,6 +834,23 @@ int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes
     case CORA_DBG_Q_WIDTH: src = E->d_qwidth; size = nq * 4; break;
     case CORA_DBG_Q_PLANES: src = E->d_planes; size = nq * 2 * kBq * E->W * 4; break;
     case CORA_DBG_Q_WIDTH2: src = E->d_qwidth2; size = nq * 4; break;
+    case CORA_DBG_SEED_DIST: {
+        const uint64_t keep = std::max<uint64_t>(E->last.topk, 20);
+        if (!E->d_seed_dist)
+            return fail(E, CORA_ERR_LOGIC, "debug_read: no GPU ex-codes, no seed distances");
+        src = E->d_seed_dist;
+        size = nq * E->last_depth * keep * 4;
+        break;
+    }
+    case CORA_DBG_THRESHOLDS: {
+        if (bytes != nq * 4)
+            return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_read: size mismatch");
+        if (E->last.flags & CORA_FLAG_FROZEN_THRESHOLDS)
+            HIPCHK(hipMemcpy(dst, E->d_thr_snap, bytes, hipMemcpyDeviceToHost));
+        else
+            memcpy(dst, E->h_thr, bytes);
+        return CORA_OK;
+    }
     case CORA_DBG_PROBE_IDX: src = E->d_pidx; size = nq * np * 4; break;
     case CORA_DBG_PROBE_GADD: src = E->d_gadd; size = nq * np * 4; break;
     case CORA_DBG_PROBE_GERR: src = E->d_gerr; size = nq * np * 4; break;

@@ -101,6 +101,24 @@ struct ScanParams {
     uint32_t seed_words;         // u32 words of seed bitmask per vanguard pair
     uint32_t *seed_bits;         // [nq * vanguard][seed_words]
     QueueDev queue;
+    // GPU seed refinement (optional: ex_codes == nullptr disables it). The seed pass
+    // refines each seed with the HBM copy of the ex-codes exactly as the CPU consumer
+    // will (cpu_refinement.cpp:183-192) and records, per seed slot
+    // [nq][vanguard][keep], its refined distance, its lower bound and a bound on the
+    // rounding difference between this and the CPU's evaluation.
+    const uint8_t *ex_codes;     // [N][P*7/8] packed 7-bit ex-codes (pack_excode.hpp:216-265)
+    const float *ex_factors;     // [N][2] f_add_ex, f_rescale_ex
+    const float *qrot;           // [nq][P] rotated queries
+    const float *kb;             // [nq] kbxSumq
+    float *seed_dist;            // [nq][vanguard][keep], +inf when unused
+    float *seed_low;
+    float *seed_err;
+    // HBM scratch of the seed pass for clusters larger than its LDS window:
+    // [van_blocks][van_stride] lower bounds and ip_int, one slice per workgroup
+    float *van_low;
+    int *van_ip;
+    uint32_t van_stride;
+    uint32_t van_blocks;
     // dense debug output
     int32_t *dbg_ip;
     int32_t *dbg_ip2;            // residual inner product <b, qres>
@@ -141,6 +159,16 @@ int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, hip
 // dense debug pass over one unit set (0 = vanguard units, 1 = far units)
 int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t set, hipStream_t s);
 int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s);
+// workgroups the seed pass launches (its persistent grid), for sizing van_low / van_ip
+uint32_t vanguard_seed_grid(uint32_t W);
+// Per query: the topk-th smallest refined seed distance, raised by the largest rounding
+// bound and above the lower bounds of the seeds at or below it, lowers the query's
+// threshold (see scan.hip). count = vanguard * keep seed slots per query.
+void launch_seed_thresholds(const float *seed_dist, const float *seed_low, const float *seed_err,
+                            uint32_t nq, uint32_t count, uint32_t topk, float *thresholds,
+                            unsigned long long *seeded, hipStream_t s);
+// *dst = *src in stream order (per-pass snapshots of the ring position counter)
+void launch_copy_u64(const unsigned long long *src, unsigned long long *dst, hipStream_t s);
 // max_ticks: drain wait limit in ticks of the device wall clock (wall_clock64)
 void launch_finish(QueueDev q, unsigned long long max_ticks, hipStream_t s);
 

@@ -1,8 +1,8 @@
 // Query preparation and coarse probing kernels (gfx950, wave64).
 //
-//   rotate        Q' = Q . R                            (reference hybrid.cu:436-440)
+//   rotate        Q' = Q . R on MFMA                    (reference hybrid.cu:436-440)
 //   query_prep    k1/kb sums, ||q'||^2, Bq=8 planes     (query_kernels.cuh:73-103,117-197)
-//   dist_gemm     ||q'||^2 + ||c'||^2 - 2 q'.c'          (hybrid.cu:465-477, query_kernels.cuh:10-64)
+//   dist_gemm     ||q'||^2 + ||c'||^2 - 2 q'.c' on MFMA  (hybrid.cu:465-477, query_kernels.cuh:10-64)
 //   select        per-query nprobe smallest, ascending, ties by cluster id (hybrid.cu:485-493)
 //   probe_refine  exact ||q'-c'||^2 and <q',c'> of the selected probes -> g_add, g_error
 //                 (query.hpp:537-545: L2 g_add = ||q'-c'||^2, IP g_add = -<q',c'>)
@@ -14,79 +14,117 @@
 namespace cora {
 namespace {
 
-constexpr int kTile = 64;
-constexpr int kTileK = 16;
+constexpr int kTile = 64;   // output tile per workgroup: 64 x 64
+constexpr int kTileK = 16;  // K slice staged in LDS per step
 
-// C = A . B (row-major A [M][K], B [K][N]) when TRANS_B is false; with TRANS_B the second
-// operand is given as Bt [N][K] and the epilogue forms an L2 distance
-// an[m] + bn[n] - 2 * (A . Bt^T)[m][n].
-template <bool TRANS_B>
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// C[m][n] = sum_k A[m][k] * B(k, n) on the matrix cores (v_mfma_f32_16x16x4f32: FP32
+// inputs, FP32 accumulation). A is row-major [M][K]. With TRANS_B the second operand is
+// Bt [N][K] (B(k, n) = Bt[n][k]) and the epilogue forms the L2 distance
+// an[m] + bn[n] - 2 * C[m][n]; without it B is row-major [K][N] (the rotation Q . R).
+// Four waves per workgroup, each owning a 32 x 32 quarter of the 64 x 64 tile as 2 x 2
+// MFMA blocks. MFMA 16x16x4 operand layout: lane l supplies A[l % 16][l / 16] and
+// B[l / 16][l % 16] of the 16x4 / 4x16 blocks, and holds D[4 (l / 16) + r][l % 16],
+// r = 0..3, of the 16x16 result. VEC: K % 4 == 0 and 16-byte aligned rows, loaded as
+// float4; otherwise element loads (any K). Every global access is bounds-checked.
+template <bool TRANS_B, bool VEC>
 __global__ __launch_bounds__(256) void gemm_kernel(const float *__restrict__ A,
                                                    const float *__restrict__ B,
                                                    float *__restrict__ C, uint32_t M, uint32_t N,
                                                    uint32_t K, const float *__restrict__ an,
                                                    const float *__restrict__ bn) {
-    __shared__ float As[kTileK][kTile + 4];
-    __shared__ float Bs[kTileK][kTile + 4];
-    const int tid = threadIdx.x;
-    const int tx = tid % 16, ty = tid / 16;
+    __shared__ float As[kTileK][kTile + 4];  // [k][m]
+    __shared__ float Bs[kTileK][kTile + 4];  // [k][n]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
-    float acc[4][4] = {};
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    f32x4_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // staging coordinates: 256 threads x 4 elements = one 64 x 16 slice of each operand
+    const int row = tid >> 2, kq = (tid & 3) * 4;  // A and Bt: row, 4 consecutive k
+    const int bk = tid >> 4, bn4 = (tid & 15) * 4;  // row-major B: k row, 4 consecutive n
     for (uint32_t k0 = 0; k0 < K; k0 += kTileK) {
-        // A tile: 64 rows x 16 k, 4 elements per thread
+        {
+            const uint32_t gm = m0 + row, gk = k0 + kq;
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (gm < M) {
+                const float *src = A + (size_t)gm * K + gk;
+                if (VEC && gk + 4 <= K) {
+                    const float4 t = *reinterpret_cast<const float4 *>(src);
+                    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+                } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int e = tid + r * 256;
-            const int row = e / kTileK, kk = e % kTileK;
-            const uint32_t gm = m0 + row, gk = k0 + kk;
-            As[kk][row] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.0f;
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int e = tid + r * 256;
-            if (TRANS_B) {
-                const int col = e / kTileK, kk = e % kTileK;
-                const uint32_t gn = n0 + col, gk = k0 + kk;
-                Bs[kk][col] = (gn < N && gk < K) ? B[(size_t)gn * K + gk] : 0.0f;
-            } else {
-                const int kk = e / kTile, col = e % kTile;
-                const uint32_t gn = n0 + col, gk = k0 + kk;
-                Bs[kk][col] = (gn < N && gk < K) ? B[(size_t)gk * N + gn] : 0.0f;
+                    for (int e = 0; e < 4; ++e)
+                        v[e] = gk + e < K ? src[e] : 0.0f;
+                }
             }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                As[kq + e][row] = v[e];
+        }
+        if (TRANS_B) {
+            const uint32_t gn = n0 + row, gk = k0 + kq;
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (gn < N) {
+                const float *src = B + (size_t)gn * K + gk;
+                if (VEC && gk + 4 <= K) {
+                    const float4 t = *reinterpret_cast<const float4 *>(src);
+                    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        v[e] = gk + e < K ? src[e] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                Bs[kq + e][row] = v[e];
+        } else {
+            const uint32_t gk = k0 + bk, gn = n0 + bn4;
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (gk < K) {
+                const float *src = B + (size_t)gk * N + gn;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[e] = gn + e < N ? src[e] : 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                Bs[bk][bn4 + e] = v[e];
         }
         __syncthreads();
 #pragma unroll
-        for (int kk = 0; kk < kTileK; ++kk) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a[i] = As[kk][ty * 4 + i];
-                b[i] = Bs[kk][tx * 4 + i];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        for (int kk = 0; kk < kTileK; kk += 4) {
+            const int i = lane & 15, kl = kk + (lane >> 4);
+            const float a0 = As[kl][wm + i], a1 = As[kl][wm + 16 + i];
+            const float b0 = Bs[kl][wn + i], b1 = Bs[kl][wn + 16 + i];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t gm = m0 + ty * 4 + i;
-        if (gm >= M)
-            continue;
+    for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t gn = n0 + tx * 4 + j;
-            if (gn >= N)
-                continue;
-            float v = acc[i][j];
-            if (TRANS_B)
-                v = an[gm] + bn[gn] - 2.0f * v;
-            C[(size_t)gm * N + gn] = v;
-        }
-    }
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t gm = m0 + wm + 16 * ti + 4 * (lane >> 4) + r;
+                const uint32_t gn = n0 + wn + 16 * tj + (lane & 15);
+                if (gm < M && gn < N) {
+                    float v = acc[ti][tj][r];
+                    if (TRANS_B)
+                        v = an[gm] + bn[gn] - 2.0f * v;
+                    C[(size_t)gm * N + gn] = v;
+                }
+            }
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -341,7 +379,7 @@ __global__ __launch_bounds__(256) void probe_refine_kernel(const float *__restri
 void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint32_t dim,
                    uint32_t P, hipStream_t s) {
     dim3 grid((P + kTile - 1) / kTile, (nq + kTile - 1) / kTile);
-    gemm_kernel<false><<<grid, 256, 0, s>>>(q, R, out, nq, P, dim, nullptr, nullptr);
+    gemm_kernel<false, false><<<grid, 256, 0, s>>>(q, R, out, nq, P, dim, nullptr, nullptr);
 }
 
 void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,
@@ -358,7 +396,12 @@ void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hip
 void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,
                       uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s) {
     dim3 grid((nl + kTile - 1) / kTile, (nq + kTile - 1) / kTile);
-    gemm_kernel<true><<<grid, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
+    const bool vec = P % 4 == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(c) & 15) == 0;
+    if (vec)
+        gemm_kernel<true, true><<<grid, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
+    else
+        gemm_kernel<true, false><<<grid, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
 }
 
 void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,

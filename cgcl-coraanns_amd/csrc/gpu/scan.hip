@@ -429,6 +429,37 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
 // vectors against the thresholds the CPU has tightened meanwhile. Selection: radix
 // select of the keep-th smallest key, all smaller keys plus the lowest-index ties.
 // ---------------------------------------------------------------------------------
+// <q', ex_code> over one 8-dimension chunk c (group g = c / 8 of 64 dimensions, k = c % 8)
+// of a packed 7-bit ex-code (pack_excode.hpp:216-265): per 64 dimensions, bytes 0..47
+// hold the low six bits of dimensions 0..47, and in their top two bits the bit pairs of
+// dimensions 48..63 (bits 0-1 in bytes 0..15, 2-3 in 16..31, 4-5 in 32..47); the u64 at
+// bytes 48..55 holds bit 6 of dimension 8k+j at bit 8j+k. l1 accumulates sum |q'|.
+__device__ __forceinline__ float excode_chunk_ip(const uint8_t *__restrict__ code,
+                                                 const float *__restrict__ q, uint32_t c,
+                                                 float &l1) {
+    const uint32_t g = c >> 3, k = c & 7;
+    const uint64_t *grp = reinterpret_cast<const uint64_t *>(code + (size_t)g * 56);
+    uint64_t v;
+    if (k < 6) {
+        v = grp[k] & 0x3F3F3F3F3F3F3F3Full;
+    } else {
+        const uint32_t o = k - 6;
+        v = ((grp[o] >> 6) & 0x0303030303030303ull) | ((grp[2 + o] >> 4) & 0x0C0C0C0C0C0C0C0Cull) |
+            ((grp[4 + o] >> 2) & 0x3030303030303030ull);
+    }
+    v |= ((grp[6] >> k) & 0x0101010101010101ull) << 6;
+    const float4 q0 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k);
+    const float4 q1 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k + 4);
+    const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sum = fmaf((float)((v >> (8 * j)) & 0xFFu), qq[j], sum);
+        l1 += fabsf(qq[j]);
+    }
+    return sum;
+}
+
 constexpr int kVanThreads = 256;
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -436,189 +467,337 @@ __device__ __forceinline__ uint32_t order_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Inclusive prefix sum of v over the workgroup's 256 threads (wave shuffles, then one
+// exchange of the four wave totals); total receives the sum over all threads.
+__device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t *s_wave, uint32_t &total) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o, 64);
+        if (lane >= (uint32_t)o)
+            x += y;
+    }
+    if (lane == 63)
+        s_wave[wave] = x;
+    __syncthreads();
+    uint32_t off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kVanThreads / 64; ++w) {
+        const uint32_t sw = s_wave[w];
+        off += (uint32_t)w < wave ? sw : 0u;
+        tot += sw;
+    }
+    __syncthreads();  // s_wave may be reused
+    total = tot;
+    return x + off;
+}
+
+struct SeedShared {
+    uint32_t hist[256];
+    uint32_t wave_sum[kVanThreads / 64];
+    uint32_t sel[kMaxVanguardKeep];
+    float exk[kMaxVanguardKeep];
+    uint32_t unit, digit, remaining, range, tries;
+    unsigned long long base, limit;
+};
+
+// One vanguard pair: lower bounds of the cluster into lows / ips (LDS for clusters of up
+// to kVanguardMaxCluster vectors, this workgroup's HBM scratch slice for larger ones),
+// radix select of the `keep` smallest below the threshold (8-bit digits, digit found by
+// a parallel scan of the histogram), publication with one reservation, the seed bitmask
+// and, with HBM ex-codes, the GPU refinement of the seeds. Called by all 256 threads.
+template <int W>
+__device__ __forceinline__ void seed_pair(const ScanParams &p, SeedShared &sh, float *lows,
+                                          int *ips, const Unit &un) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t rw = p.P / 32;
+    const QueueDev q = p.queue;
+    const ClusterMeta cm = p.meta[un.cluster];
+    const uint32_t n = cm.n;
+    const uint32_t w0 = p.pairs[un.pair_begin].word0;
+    const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
+    const float width = p.qwidth[query], k1 = p.k1[query];
+    const size_t pi = (size_t)query * p.nprobe + probe;
+    const float gadd = p.pgadd[pi], gerr = p.pgerr[pi];
+    const float cutoff = read_threshold(p.thresholds, p.thresholds_live, query);
+    const uint32_t *planes = p.qplanes + (size_t)query * 2 * kBq * rw;
+    const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
+    uint32_t nv = 0;
+    for (uint32_t t = wave; t < ntiles; t += kVanThreads / 64) {
+        const uint8_t *tile = p.tiles + (size_t)(cm.tile_base + t) * p.tile_bytes;
+        uint32_t x[Words<W>::kMax];
+        load_codes<W>(tile, lane, rw, x);
+        const float *fac = reinterpret_cast<const float *>(tile + 256u * rw);
+        const uint32_t local = t * kTileVectors + lane;
+        if (local < n) {
+            const int ip = popc_ip<W>(x, planes, rw);
+            const float ex = width * (float)ip;
+            const float low = fac[lane] + gadd + fac[64 + lane] * (ex + k1) - fac[128 + lane] * gerr;
+            const bool ok = low < cutoff;
+            lows[local] = ok ? low : __uint_as_float(0x7FFFFFFFu);  // NaN: excluded, sorts last
+            ips[local] = ip;
+            nv += ok ? 1u : 0u;
+        }
+    }
+    uint32_t valid;
+    (void)block_scan(nv, sh.wave_sum, valid);  // its barrier also publishes the lows
+    const uint32_t take = min(p.keep, valid);
+    if (take == 0)
+        return;
+    // radix select of the take-th smallest key
+    uint32_t prefix = 0, pmask = 0, rem = take;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        sh.hist[tid] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < n; i += kVanThreads) {
+            const uint32_t key = order_key(lows[i]);
+            if ((key & pmask) == prefix)
+                atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        const uint32_t h = sh.hist[tid];
+        uint32_t tot;
+        const uint32_t incl = block_scan(h, sh.wave_sum, tot);
+        if (incl - h < rem && rem <= incl) {  // exactly one digit holds the rem-th key
+            sh.digit = tid;
+            sh.remaining = rem - (incl - h);
+        }
+        __syncthreads();
+        prefix |= sh.digit << shift;
+        rem = sh.remaining;
+        pmask |= 255u << shift;
+    }
+    const uint32_t kth = prefix, take_eq = rem;
+    // deterministic gather in index order: a contiguous index chunk per thread, all keys
+    // below the take-th plus its lowest-index ties
+    const uint32_t chunk = (n + kVanThreads - 1) / kVanThreads;
+    const uint32_t b0 = min(n, tid * chunk), b1 = min(n, b0 + chunk);
+    uint32_t nless = 0, neq = 0;
+    for (uint32_t i = b0; i < b1; ++i) {
+        const uint32_t key = order_key(lows[i]);
+        nless += key < kth;
+        neq += key == kth;
+    }
+    uint32_t tot_less, tot_eq;
+    uint32_t lo = block_scan(nless, sh.wave_sum, tot_less) - nless;
+    uint32_t eq_rank = block_scan(neq, sh.wave_sum, tot_eq) - neq;
+    uint32_t *seed = p.seed_bits + ((size_t)query * p.vanguard + probe) * p.seed_words;
+    for (uint32_t i = b0; i < b1; ++i) {
+        const uint32_t key = order_key(lows[i]);
+        bool pick = false;
+        // tot_less + take_eq == take <= keep by the radix select; the guards keep the LDS
+        // writes inside sel[] whatever the keys
+        if (key < kth) {
+            if (lo < take) {
+                sh.sel[lo] = i;
+                pick = true;
+            }
+            ++lo;
+        } else if (key == kth) {
+            if (eq_rank < take_eq && tot_less + eq_rank < take) {
+                sh.sel[tot_less + eq_rank] = i;
+                pick = true;
+            }
+            ++eq_rank;
+        }
+        if (pick)
+            atomicOr(&seed[i >> 5], 1u << (i & 31));
+    }
+    // one reservation for the pair's seeds, then the residual pass per seed
+    if (tid == 0) {
+        const unsigned long long base = atomicAdd(q.produced, (unsigned long long)take);
+        unsigned long long lim = sh.limit;
+        if (base + take > lim)
+            lim = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released, q.capacity,
+                                base + take);
+        sh.base = base;
+        sh.limit = lim;
+    }
+    __syncthreads();
+    const unsigned long long base = sh.base, limit = sh.limit;
+    const float width2 = p.qwidth2[query];
+    for (uint32_t s = tid; s < take; s += kVanThreads) {
+        const uint32_t local = sh.sel[s];
+        const uint8_t *tile = p.tiles + (size_t)(cm.tile_base + local / kTileVectors) * p.tile_bytes;
+        uint32_t x[Words<W>::kMax];
+        load_codes<W>(tile, local % kTileVectors, rw, x);
+        const int ip_res = popc_ip<W>(x, planes + kBq * rw, rw);
+        const float ex = two_stage_ip(width, ips[local], width2, ip_res);
+        sh.exk[s] = ex;
+        place_record(q, base + s, limit,
+                     make_uint4(w0, cm.start + local, __float_as_uint(ex), __float_as_uint(lows[local])));
+    }
+    if (p.ex_codes) {
+        // Refined distance of every seed, 16 lanes per seed (cpu_refinement.cpp:183-192):
+        // f_add_ex + g_add + f_rescale_ex * (2^7 * exact_ip + <q', ex_code> + kbxSumq),
+        // with a bound on its rounding difference from the CPU's evaluation.
+        __syncthreads();
+        const uint32_t sub = tid & 15, chunks = p.P / 8;
+        const size_t lc = (size_t)p.P * 7 / 8;
+        const float *qv = p.qrot + (size_t)query * p.P;
+        const float kbq = p.kb[query];
+        for (uint32_t s = tid >> 4; s < take; s += kVanThreads / 16) {
+            const uint32_t local = sh.sel[s];
+            const size_t gid = (size_t)cm.start + local;
+            const uint8_t *code = p.ex_codes + gid * lc;
+            float ip = 0.0f, l1 = 0.0f;
+            for (uint32_t c = sub; c < chunks; c += 16)
+                ip += excode_chunk_ip(code, qv, c, l1);
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) {
+                ip += __shfl_xor(ip, o, 16);
+                l1 += __shfl_xor(l1, o, 16);
+            }
+            if (sub == 0) {
+                const float fa = p.ex_factors[2 * gid], fr = p.ex_factors[2 * gid + 1];
+                const float ex = sh.exk[s];
+                const float dist = fa + gadd + fr * (128.0f * ex + ip + kbq);
+                const float mag = fabsf(fa) + fabsf(gadd) +
+                                  fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq));
+                const size_t o = ((size_t)query * p.vanguard + probe) * p.keep + s;
+                p.seed_dist[o] = dist;
+                p.seed_low[o] = lows[local];
+                p.seed_err[o] = 1e-4f * mag;
+            }
+        }
+    }
+}
+
 template <int W>
 __global__ __launch_bounds__(kVanThreads) void vanguard_seed_kernel(const ScanParams p) {
     __shared__ float s_low[kVanguardMaxCluster];
     __shared__ int s_ip[kVanguardMaxCluster];
-    __shared__ uint32_t s_hist[256];
-    __shared__ uint32_t s_scan[kVanThreads];
-    __shared__ uint32_t s_sel[kMaxVanguardKeep];
-    __shared__ uint32_t s_unit, s_prefix, s_remaining, s_valid;
-    __shared__ uint32_t s_range, s_tries;
-    __shared__ unsigned long long s_base, s_limit;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t rw = p.P / 32;
+    __shared__ SeedShared sh;
+    const uint32_t tid = threadIdx.x;
     const uint32_t U = p.num_units[0];
     const uint32_t per = (U + kNumXcd - 1) / kNumXcd;
-    const QueueDev q = p.queue;
     if (tid == 0) {
-        s_range = blockIdx.x % kNumXcd;
-        s_tries = 0;
-        s_limit = __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh.range = blockIdx.x % kNumXcd;
+        sh.tries = 0;
+        sh.limit = __hip_atomic_load(p.queue.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     for (;;) {
         if (tid == 0) {
             uint32_t u = U;
-            while (s_tries < kNumXcd) {
-                const uint32_t v = atomicAdd(&p.unit_cursor[s_range], 1u);
-                if (v < min(U, (s_range + 1) * per)) {
+            while (sh.tries < kNumXcd) {
+                const uint32_t v = atomicAdd(&p.unit_cursor[sh.range], 1u);
+                if (v < min(U, (sh.range + 1) * per)) {
                     u = v;
                     break;
                 }
-                s_range = (s_range + 1) % kNumXcd;
-                ++s_tries;
+                sh.range = (sh.range + 1) % kNumXcd;
+                ++sh.tries;
             }
-            s_unit = u;
+            sh.unit = u;
         }
         __syncthreads();
-        const uint32_t u = s_unit;
+        const uint32_t u = sh.unit;
         if (u >= U)
             break;
         const Unit un = p.units[u];
-        const ClusterMeta cm = p.meta[un.cluster];
-        const uint32_t n = cm.n;
-        const uint32_t w0 = p.pairs[un.pair_begin].word0;
-        const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
-        if (n > (uint32_t)kVanguardMaxCluster || p.keep == 0) {
-            __syncthreads();
-            continue;  // no seeds: the recovery pass publishes the whole pair
-        }
-        const float width = p.qwidth[query], k1 = p.k1[query];
-        const size_t pi = (size_t)query * p.nprobe + probe;
-        const float gadd = p.pgadd[pi], gerr = p.pgerr[pi];
-        const float cutoff = read_threshold(p.thresholds, p.thresholds_live, query);
-        const uint32_t *planes = p.qplanes + (size_t)query * 2 * kBq * rw;
-        const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
-        for (uint32_t t = wave; t < ntiles; t += kVanThreads / 64) {
-            const uint8_t *tile = p.tiles + (size_t)(cm.tile_base + t) * p.tile_bytes;
-            uint32_t x[Words<W>::kMax];
-            load_codes<W>(tile, lane, rw, x);
-            const float *fac = reinterpret_cast<const float *>(tile + 256u * rw);
-            const uint32_t local = t * kTileVectors + lane;
-            if (local < n) {
-                const int ip = popc_ip<W>(x, planes, rw);
-                const float ex = width * (float)ip;
-                const float low = fac[lane] + gadd + fac[64 + lane] * (ex + k1) -
-                                  fac[128 + lane] * gerr;
-                s_low[local] = low < cutoff ? low : __uint_as_float(0x7FFFFFFFu);  // NaN: excluded
-                s_ip[local] = ip;
+        const uint32_t n = p.meta[un.cluster].n;
+        if (p.keep > 0 && n > 0) {
+            if (n <= (uint32_t)kVanguardMaxCluster) {
+                seed_pair<W>(p, sh, s_low, s_ip, un);
+            } else if (p.van_low && blockIdx.x < p.van_blocks && n <= p.van_stride) {
+                const size_t off = (size_t)blockIdx.x * p.van_stride;
+                seed_pair<W>(p, sh, p.van_low + off, p.van_ip + off, un);
             }
-        }
-        if (tid == 0)
-            s_valid = 0;
-        __syncthreads();
-        uint32_t nv = 0;
-        for (uint32_t i = tid; i < n; i += kVanThreads)
-            nv += s_low[i] == s_low[i];
-        atomicAdd(&s_valid, nv);
-        __syncthreads();
-        const uint32_t take = min(p.keep, s_valid);
-        if (take == 0) {
-            __syncthreads();
-            continue;
-        }
-        // radix select of the take-th smallest key (NaN keys sort last)
-        uint32_t prefix = 0, pmask = 0;
-        if (tid == 0)
-            s_remaining = take;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            s_hist[tid] = 0;
-            __syncthreads();
-            for (uint32_t i = tid; i < n; i += kVanThreads) {
-                const uint32_t key = order_key(s_low[i]);
-                if ((key & pmask) == prefix)
-                    atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
-            }
-            __syncthreads();
-            if (tid == 0) {
-                uint32_t rem = s_remaining, cum = 0, d = 0;
-                for (; d < 255; ++d) {
-                    if (cum + s_hist[d] >= rem)
-                        break;
-                    cum += s_hist[d];
-                }
-                s_remaining = rem - cum;
-                s_prefix = prefix | (d << shift);
-            }
-            __syncthreads();
-            prefix = s_prefix;
-            pmask |= 255u << shift;
-        }
-        const uint32_t kth = prefix, take_eq = s_remaining;
-        // deterministic gather in index order: contiguous index chunk per thread
-        const uint32_t chunk = (n + kVanThreads - 1) / kVanThreads;
-        const uint32_t b0 = min(n, tid * chunk), b1 = min(n, b0 + chunk);
-        uint32_t nless = 0, neq = 0;
-        for (uint32_t i = b0; i < b1; ++i) {
-            const uint32_t key = order_key(s_low[i]);
-            nless += key < kth;
-            neq += key == kth;
-        }
-        // exclusive scans (less first, then equal)
-        s_scan[tid] = nless;
-        __syncthreads();
-        for (uint32_t o = 1; o < kVanThreads; o <<= 1) {
-            const uint32_t v = tid >= o ? s_scan[tid - o] : 0;
-            __syncthreads();
-            s_scan[tid] += v;
-            __syncthreads();
-        }
-        const uint32_t less_off = s_scan[tid] - nless, tot_less = s_scan[kVanThreads - 1];
-        __syncthreads();
-        s_scan[tid] = neq;
-        __syncthreads();
-        for (uint32_t o = 1; o < kVanThreads; o <<= 1) {
-            const uint32_t v = tid >= o ? s_scan[tid - o] : 0;
-            __syncthreads();
-            s_scan[tid] += v;
-            __syncthreads();
-        }
-        uint32_t eq_rank = s_scan[tid] - neq, lo = less_off;
-        uint32_t *seed = p.seed_bits + ((size_t)query * p.vanguard + probe) * p.seed_words;
-        for (uint32_t i = b0; i < b1; ++i) {
-            const uint32_t key = order_key(s_low[i]);
-            bool pick = false;
-            if (key < kth) {
-                s_sel[lo++] = i;
-                pick = true;
-            } else if (key == kth) {
-                if (eq_rank < take_eq) {
-                    s_sel[tot_less + eq_rank] = i;
-                    pick = true;
-                }
-                ++eq_rank;
-            }
-            if (pick)
-                atomicOr(&seed[i >> 5], 1u << (i & 31));
-        }
-        // one reservation for the pair's seeds, then the residual pass per seed
-        if (tid == 0) {
-            const unsigned long long base = atomicAdd(q.produced, (unsigned long long)take);
-            unsigned long long lim = s_limit;
-            if (base + take > lim)
-                lim = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released,
-                                    q.capacity, base + take);
-            s_base = base;
-            s_limit = lim;
-        }
-        __syncthreads();
-        const unsigned long long base = s_base, limit = s_limit;
-        const float width2 = p.qwidth2[query];
-        for (uint32_t s = tid; s < take; s += kVanThreads) {
-            const uint32_t local = s_sel[s];
-            const uint8_t *tile =
-                p.tiles + (size_t)(cm.tile_base + local / kTileVectors) * p.tile_bytes;
-            uint32_t x[Words<W>::kMax];
-            load_codes<W>(tile, local % kTileVectors, rw, x);
-            const int ip_res = popc_ip<W>(x, planes + kBq * rw, rw);
-            const float ex = two_stage_ip(width, s_ip[local], width2, ip_res);
-            place_record(q, base + s, limit,
-                         make_uint4(w0, cm.start + local, __float_as_uint(ex),
-                                    __float_as_uint(s_low[local])));
+            // otherwise no seeds: the recovery pass publishes the whole pair
         }
         __syncthreads();
     }
 }
+
+// Per query (one workgroup): the topk-th smallest refined seed distance d_k becomes the
+// threshold max(d_k + e, l) + 1 ulp, where e is the largest rounding bound and l the
+// largest lower bound among the seeds with distance <= d_k. Those seeds are published
+// candidates, so the CPU consumer, evaluating them later, finds at least topk of them
+// strictly below the threshold and passing its secondary filter: the threshold is one
+// the CPU would publish itself once it has refined them, set before the far and
+// recovery passes read it. Written only when lower than the current value; a racing CPU
+// store is harmless, every value written is at least the final topk-th distance.
+constexpr int kThrThreads = 256;
+
+__device__ __forceinline__ float key_to_float(uint32_t key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+__global__ __launch_bounds__(kThrThreads) void seed_threshold_kernel(
+    const float *__restrict__ seed_dist, const float *__restrict__ seed_low,
+    const float *__restrict__ seed_err, uint32_t count, uint32_t topk, float *thresholds,
+    unsigned long long *seeded) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_prefix, s_remaining, s_finite, s_ekey, s_lkey;
+    const uint32_t q = blockIdx.x, t = threadIdx.x;
+    const size_t base = (size_t)q * count;
+    const float *d = seed_dist + base;
+    if (t == 0) {
+        s_finite = 0;
+        s_remaining = topk;
+        s_ekey = 0;
+        s_lkey = 0;
+    }
+    __syncthreads();
+    uint32_t nf = 0;
+    for (uint32_t i = t; i < count; i += kThrThreads)
+        nf += isfinite(d[i]) ? 1u : 0u;
+    atomicAdd(&s_finite, nf);
+    __syncthreads();
+    if (s_finite < topk)
+        return;  // fewer refined seeds than topk: nothing to seed (uniform exit)
+    // radix select of the topk-th smallest distance (non-finite keys sort last)
+    uint32_t prefix = 0, pmask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[t] = 0;
+        __syncthreads();
+        for (uint32_t i = t; i < count; i += kThrThreads) {
+            const uint32_t key = order_key(d[i]);
+            if ((key & pmask) == prefix)
+                atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (t == 0) {
+            uint32_t rem = s_remaining, cum = 0, dg = 0;
+            for (; dg < 255; ++dg) {
+                if (cum + hist[dg] >= rem)
+                    break;
+                cum += hist[dg];
+            }
+            s_remaining = rem - cum;
+            s_prefix = prefix | (dg << shift);
+        }
+        __syncthreads();
+        prefix = s_prefix;
+        pmask |= 255u << shift;
+    }
+    const uint32_t kth = prefix;
+    // largest rounding bound (>= 0, so its bits order like the value) and largest lower
+    // bound among the seeds at or below the topk-th distance
+    uint32_t ekey = 0, lkey = 0;
+    for (uint32_t i = t; i < count; i += kThrThreads) {
+        if (order_key(d[i]) <= kth) {
+            ekey = max(ekey, __float_as_uint(seed_err[base + i]));
+            lkey = max(lkey, order_key(seed_low[base + i]));
+        }
+    }
+    atomicMax(&s_ekey, ekey);
+    atomicMax(&s_lkey, lkey);
+    __syncthreads();
+    if (t == 0) {
+        const float thr = nextafterf(fmaxf(key_to_float(kth) + __uint_as_float(s_ekey),
+                                           key_to_float(s_lkey)),
+                                     FLT_MAX);
+        uint32_t *slot = reinterpret_cast<uint32_t *>(thresholds) + q;
+        const float cur = __uint_as_float(__hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM));
+        if (thr < cur)
+            __hip_atomic_store(slot, __float_as_uint(thr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        atomicAdd(seeded, 1ull);
+    }
+}
+
+__global__ void copy_u64_kernel(const unsigned long long *src, unsigned long long *dst) { *dst = *src; }
 
 __global__ void queue_reset_kernel(QueueDev q) {
     *q.produced = 0;
@@ -762,6 +941,11 @@ void launch_seed_w(const ScanParams &p, hipStream_t s) {
     k<<<resident_grid(k, kVanThreads), kVanThreads, 0, s>>>(p);
 }
 
+template <int W>
+uint32_t seed_grid_w() {
+    return resident_grid(vanguard_seed_kernel<W>, kVanThreads);
+}
+
 }  // namespace
 
 int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, hipStream_t s) {
@@ -794,6 +978,16 @@ int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t set, hip
     }
 }
 
+uint32_t vanguard_seed_grid(uint32_t W) {
+    switch (W) {
+    case 2: return seed_grid_w<2>();
+    case 4: return seed_grid_w<4>();
+    case 8: return seed_grid_w<8>();
+    case 24: return seed_grid_w<24>();
+    default: return seed_grid_w<0>();
+    }
+}
+
 int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s) {
     switch (W) {
     case 2: launch_seed_w<2>(p, s); break;
@@ -803,6 +997,17 @@ int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s) {
     default: launch_seed_w<0>(p, s); break;
     }
     return 0;
+}
+
+void launch_seed_thresholds(const float *seed_dist, const float *seed_low, const float *seed_err,
+                            uint32_t nq, uint32_t count, uint32_t topk, float *thresholds,
+                            unsigned long long *seeded, hipStream_t s) {
+    seed_threshold_kernel<<<nq, kThrThreads, 0, s>>>(seed_dist, seed_low, seed_err, count, topk,
+                                                     thresholds, seeded);
+}
+
+void launch_copy_u64(const unsigned long long *src, unsigned long long *dst, hipStream_t s) {
+    copy_u64_kernel<<<1, 1, 0, s>>>(src, dst);
 }
 
 void launch_queue_reset(QueueDev q, hipStream_t s) { queue_reset_kernel<<<1, 1, 0, s>>>(q); }

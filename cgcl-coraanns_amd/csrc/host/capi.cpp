@@ -110,6 +110,8 @@ int cora_hybrid_configure(cora_hybrid *h, const cora_hybrid_config *c) {
         x.set_metric(c->metric);
         x.set_frozen_thresholds(c->frozen_thresholds != 0);
         x.set_cpu_threads(c->cpu_threads);
+        x.set_gpu_seed_refine(c->gpu_seed_refine != 0);
+        x.set_extra_search_flags(c->extra_flags);
     });
 }
 
@@ -167,6 +169,11 @@ int cora_hybrid_stats_get(cora_hybrid *h, cora_hybrid_stats *out) {
     out->scan_bytes = x.get_last_scan_bytes();
     out->scan_units = x.get_last_scan_units();
     out->scan_vectors = x.get_last_scan_vectors();
+    out->probe_ms = x.get_last_probe_ms();
+    out->probe_flops = x.get_last_probe_flops();
+    for (int i = 0; i < 3; ++i)
+        out->pass_produced[i] = x.get_last_pass_produced(i);
+    out->seeded_queries = x.get_last_seeded_queries();
     return CORA_OK;
 }
 
@@ -410,6 +417,7 @@ int cora_test_ring(cora_ring_test *t, float *dists, uint32_t *ids) {
         a.long_codes = codes.data();
         a.ex_factors = exf.data();
         a.ids = pid.data();
+        a.num_vectors = pid.size();
         a.secondary_filter = t->secondary_filter != 0;
         a.threads = static_cast<int>(t->consumers ? t->consumers : 1);
         const detail::RefineOut out = detail::cpu_refine(a, nq, t->topk, dists, ids);

@@ -12,7 +12,8 @@
 //  * refine = f_ex_add + g_add + f_ex_rescale * (2^ex * exact_ip + <q', ex_code> + kbxSumq)
 //    (or the exact squared L2 distance to the base vector), inserted into the query's
 //    sorted top-k under a per-query spinlock; a full top-k publishes its k-th distance as
-//    the query's threshold, which the GPU filter reads;
+//    the query's threshold (as an atomic minimum, since the GPU may have lowered it with
+//    its seed thresholds), which the GPU filter reads;
 //  * a processed chunk is cleared to the empty pattern before its release, and released
 //    only as part of a contiguous prefix (ReleaseTracker).
 #include "refine.hpp"
@@ -82,10 +83,29 @@ inline bool slot_complete(const queue::Candidate *slot, queue::Candidate &out) {
     return true;
 }
 
+// Non-temporal clear (the consumed chunk is not read again by this CPU); the fence
+// orders the clear before the release that lets the GPU write the slots again.
 inline void clear_slots(queue::Candidate *slots, std::size_t n) {
     const __m128i empty = _mm_set1_epi32(-1);
     for (std::size_t i = 0; i < n; ++i)
-        _mm_store_si128(reinterpret_cast<__m128i *>(slots + i), empty);
+        _mm_stream_si128(reinterpret_cast<__m128i *>(slots + i), empty);
+    _mm_sfence();
+}
+
+// Records this many ring positions ahead have their ex-code, ex-factors and id lines
+// prefetched: candidates are random accesses into arrays far larger than the caches, and
+// their gids are in the ring well before the records are processed.
+constexpr std::size_t kPrefetchAhead = 12;
+
+inline void prefetch_record(const queue::Candidate *slot, const RefineArgs &a, std::size_t lc) {
+    const uint32_t gid = __atomic_load_n(&slot->gid, __ATOMIC_RELAXED);
+    if (gid >= a.num_vectors)  // empty (all ones) or not yet written
+        return;
+    const char *code = reinterpret_cast<const char *>(a.long_codes + static_cast<std::size_t>(gid) * lc);
+    for (std::size_t off = 0; off < lc; off += 64)
+        _mm_prefetch(code + off, _MM_HINT_T0);
+    _mm_prefetch(reinterpret_cast<const char *>(a.ex_factors + 2 * static_cast<std::size_t>(gid)), _MM_HINT_T0);
+    _mm_prefetch(reinterpret_cast<const char *>(a.ids + gid), _MM_HINT_T0);
 }
 
 inline float load_threshold(const float *t, std::size_t q) {
@@ -95,10 +115,23 @@ inline float load_threshold(const float *t, std::size_t q) {
     return f;
 }
 
+// Publish a query's k-th distance as an atomic minimum: the GPU may have lowered the
+// threshold below this consumer's running k-th (seed thresholds), which a plain store
+// would undo. With the CPU as the only writer this equals the reference's plain store,
+// its k-th only ever decreasing (cpu_refinement.cpp:218,228).
 inline void store_threshold(float *t, std::size_t q, float v) {
+    uint32_t *slot = reinterpret_cast<uint32_t *>(t) + q;
+    uint32_t cur = __atomic_load_n(slot, __ATOMIC_RELAXED);
     uint32_t bits;
     std::memcpy(&bits, &v, 4);
-    __atomic_store_n(reinterpret_cast<uint32_t *>(t) + q, bits, __ATOMIC_RELAXED);
+    for (;;) {
+        float f;
+        std::memcpy(&f, &cur, 4);
+        if (!(v < f))
+            return;
+        if (__atomic_compare_exchange_n(slot, &cur, bits, true, __ATOMIC_RELAXED, __ATOMIC_RELAXED))
+            return;
+    }
 }
 
 struct alignas(64) QuerySlot {
@@ -150,9 +183,15 @@ RefineOut cpu_refine(const RefineArgs &a, std::size_t nq, std::size_t topk, floa
                     break;
             }
             Position consumed = 0;
+            const bool prefetch = !exact && a.num_vectors != 0;
+            if (prefetch)
+                for (Position i = 0; i < std::min<Position>(kPrefetchAhead, chunk); ++i)
+                    prefetch_record(&a.items[(start + i) & mask], a, lc);
             for (Position i = 0; i < chunk; ++i) {
                 const Position pos = start + i;
                 queue::Candidate *slot = &a.items[pos & mask];
+                if (prefetch && i + kPrefetchAhead < chunk)
+                    prefetch_record(&a.items[(pos + kPrefetchAhead) & mask], a, lc);
                 queue::Candidate rec;
                 while (!slot_complete(slot, rec)) {
                     if (aborted() || (done() && pos >= produced())) {

@@ -23,6 +23,7 @@ struct RefineArgs {
     const uint8_t *long_codes = nullptr;     // [N][P*ex/8]
     const float *ex_factors = nullptr;       // [N][2]
     const uint32_t *ids = nullptr;           // [N]
+    std::size_t num_vectors = 0;             // N (bounds the prefetch of upcoming records)
     // exact FP32 refine (reference enable_exact_refine)
     const uint8_t *base_mapping = nullptr;
     std::size_t base_rows = 0, base_dim = 0, base_stride = 0, base_offset = 0;

@@ -51,7 +51,14 @@ enum cora_search_flags {
     CORA_FLAG_FILTER_TIMING = 1u << 1,
     /* Cross-query reuse: batch up to batch_q same-cluster pairs per pass
      * (reference set_cross_query_reuse, hybrid.cu:594-597). */
-    CORA_FLAG_CROSS_QUERY_REUSE = 1u << 2
+    CORA_FLAG_CROSS_QUERY_REUSE = 1u << 2,
+    /* Do not seed thresholds on the GPU even when ex-codes are resident in HBM (the
+     * reference's behaviour: only the CPU consumer tightens thresholds). */
+    CORA_FLAG_NO_GPU_SEED = 1u << 3,
+    /* Test mode: with FROZEN_THRESHOLDS, the GPU seed thresholds lower the launch
+     * snapshot, so seeding is deterministic and checkable (CORA_DBG_SEED_DIST,
+     * CORA_DBG_THRESHOLDS). */
+    CORA_FLAG_GPU_SEED_FROZEN = 1u << 4
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -87,6 +94,11 @@ typedef struct cora_search_stats {
     uint64_t scan_bytes;    /* algorithmic code+factor bytes the far-pair scan read */
     uint64_t scan_units;    /* cluster passes the far-pair scan made */
     uint64_t scan_vectors;  /* vector evaluations (vector x query) of the far-pair scan */
+    float probe_ms;         /* coarse-probe distance GEMM alone (FILTER_TIMING only) */
+    uint64_t probe_flops;   /* its algorithmic flops, 2 * nq * padded_dim * nlist */
+    uint64_t pass_produced[3]; /* candidates published by the end of the vanguard seed,
+                                  far-pair and recovery passes (cumulative) */
+    uint64_t seeded_queries;   /* queries that received a GPU seed threshold */
 } cora_search_stats;
 
 /* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */
@@ -106,6 +118,17 @@ int cora_gpu_load_index(cora_gpu_engine *engine, uint64_t num_vecs, uint64_t dim
                         const float *h_centroids, const float *h_rotator,
                         const uint32_t *h_short_data, const float *h_short_factors,
                         const uint64_t *h_cluster_sizes);
+
+/* Optional HBM copy of the 7-bit ex-codes [num_vecs][padded_dim*7/8] (reference packed
+ * layout, pack_excode.hpp:216-265) and ex-factors [num_vecs][2] (no counterpart in the
+ * reference, whose ex-codes live on the host only). With them the vanguard seed pass
+ * refines its seeds on the GPU with the CPU consumer's formula (cpu_refinement.cpp:
+ * 183-192) and, before the far and recovery passes, lowers each query's live threshold
+ * to a value the CPU would publish after refining those seeds (see scan.hip). The CPU
+ * still refines every published candidate. Requires ex_bits == 7; call after
+ * cora_gpu_load_index. */
+int cora_gpu_load_excodes(cora_gpu_engine *engine, const uint8_t *h_long_codes,
+                          const float *h_ex_factors);
 
 /* Ring sizing before prepare (HybridIndex::set_queue_capacity / set_queue_spill_capacity,
  * hybrid.cu:166-185). capacity: power of two. */
@@ -161,7 +184,11 @@ enum cora_debug_array {
     CORA_DBG_PROBE_GADD = 6,      /* f32 [nq][nprobe] */
     CORA_DBG_PROBE_GERR = 7,      /* f32 [nq][nprobe] */
     CORA_DBG_PAIRS = 8,           /* i32 [npairs][3] (cluster, query, probe), scan order */
-    CORA_DBG_Q_WIDTH2 = 9         /* f32 [nq] residual quantisation step (width / 254) */
+    CORA_DBG_Q_WIDTH2 = 9,        /* f32 [nq] residual quantisation step (width / 254) */
+    CORA_DBG_SEED_DIST = 10,      /* f32 [nq][vanguard depth][keep] GPU-refined seed distances
+                                     (+inf: unused slot); keep = max(topk, 20) */
+    CORA_DBG_THRESHOLDS = 11      /* f32 [nq] thresholds the GPU filter read last (the
+                                     snapshot in frozen mode, else the live array) */
 };
 int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t bytes);
 

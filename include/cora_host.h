@@ -40,6 +40,8 @@ typedef struct cora_hybrid_config {
     int metric;               /* 0 = L2, 1 = IP */
     int frozen_thresholds;    /* GPU filter reads a snapshot taken at launch */
     int cpu_threads;          /* CPU refinement threads, 0 = omp_get_max_threads() */
+    int gpu_seed_refine;      /* set_gpu_seed_refine (HBM ex-codes, GPU seed thresholds) */
+    uint32_t extra_flags;     /* set_extra_search_flags (cora_search_flags test modes) */
 } cora_hybrid_config;
 
 typedef struct cora_hybrid_stats {
@@ -51,6 +53,10 @@ typedef struct cora_hybrid_stats {
     uint64_t scan_bytes; /* algorithmic code+factor bytes of the far-pair scan */
     uint64_t scan_units;
     uint64_t scan_vectors;
+    float probe_ms;       /* coarse-probe distance GEMM alone */
+    uint64_t probe_flops; /* 2 * nq * padded_dim * nlist */
+    uint64_t pass_produced[3]; /* cumulative candidates after the seed, far, recovery passes */
+    uint64_t seeded_queries;   /* queries given a GPU seed threshold */
 } cora_hybrid_stats;
 
 int cora_hybrid_create(cora_hybrid **out, int device);                 /* HybridIndex() */

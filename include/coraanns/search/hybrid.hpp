@@ -89,6 +89,16 @@ class HybridIndex {
     // Frozen thresholds: the GPU filter reads a snapshot taken at launch (deterministic
     // candidate sets for parity tests).
     void set_frozen_thresholds(bool enabled) { frozen_thresholds_ = enabled; }
+    // GPU seed thresholds (default on): load_from_raw_pointers also keeps a copy of the
+    // ex-codes and ex-factors in HBM, the vanguard seed pass refines its seeds on the GPU
+    // and lowers each query's threshold before the far and recovery passes (live
+    // thresholds only). Off: only the CPU tightens thresholds, as in the reference. Set
+    // before load_from_raw_pointers to skip the HBM copy.
+    void set_gpu_seed_refine(bool enabled) { gpu_seed_refine_ = enabled; }
+    // Extra cora_search_flags ORed into every launch (test modes such as
+    // CORA_FLAG_GPU_SEED_FROZEN).
+    void set_extra_search_flags(uint32_t flags) { extra_flags_ = flags; }
+    bool get_gpu_seed_refine() const { return gpu_seed_refine_; }
     // CPU refinement threads; 0 = omp_get_max_threads() (the reference always uses the
     // caller's OpenMP setting, cpu_refinement.cpp:110).
     void set_cpu_threads(int threads) { cpu_threads_ = threads < 0 ? 0 : threads; }
@@ -96,6 +106,11 @@ class HybridIndex {
     uint64_t get_last_scan_bytes() const { return last_scan_bytes_; }
     uint64_t get_last_scan_units() const { return last_scan_units_; }
     uint64_t get_last_scan_vectors() const { return last_scan_vectors_; }
+    float get_last_probe_ms() const { return last_probe_ms_; }
+    uint64_t get_last_probe_flops() const { return last_probe_flops_; }
+    // cumulative candidates after the vanguard seed, far-pair and recovery passes
+    uint64_t get_last_pass_produced(int pass) const { return last_pass_produced_[pass]; }
+    uint64_t get_last_seeded_queries() const { return last_seeded_queries_; }
     cora_gpu_engine *gpu_engine() const { return engine_; }
 
   private:
@@ -123,6 +138,8 @@ class HybridIndex {
     bool cross_query_reuse_enabled_ = true;
     bool cpu_secondary_filter_enabled_ = true;
     bool frozen_thresholds_ = false;
+    bool gpu_seed_refine_ = true;
+    uint32_t extra_flags_ = 0;
     int cpu_threads_ = 0;
     std::size_t vanguard_size_ = default_vanguard_size;
     KernelType ip_kernel_type_ = KernelType::Lut4Bit;
@@ -135,6 +152,10 @@ class HybridIndex {
     float last_gpu_filter_ms_ = 0.0f;
     float last_scan_ms_ = 0.0f;
     uint64_t last_scan_bytes_ = 0, last_scan_units_ = 0, last_scan_vectors_ = 0;
+    float last_probe_ms_ = 0.0f;
+    uint64_t last_probe_flops_ = 0;
+    uint64_t last_pass_produced_[3] = {0, 0, 0};
+    uint64_t last_seeded_queries_ = 0;
 };
 
 }  // namespace coraanns

@@ -474,6 +474,44 @@ def hybrid_search(sd: SearchData, queries: np.ndarray, topk: int, nprobe: int, m
     return HybridResult(dists, out_ids, cands, lows, eips)
 
 
+def vanguard_seeds(low: np.ndarray, keep: int, cutoff) -> np.ndarray:
+    """Seeds of one vanguard pair (filter_kernels.cuh:308-468, whose CUB radix sort keeps
+    max(topk, 20) lowest bounds below the cutoff): the min(keep, #valid) smallest lows
+    below the cutoff, ties to the lower index (this engine's radix select; CUB's tie order
+    is unpinned). Returns local indices in ascending low order."""
+    valid = np.nonzero(np.asarray(low) < np.float32(cutoff))[0]
+    return valid[np.argsort(np.asarray(low)[valid], kind="stable")][:keep]
+
+
+def refine_error_bound(f_ex_add, f_ex_rescale, g_add, exact_ip, q_l1, kb, ex_bits):
+    """Bound on the rounding difference between two FP32 evaluations of refine_dist in
+    different summation orders (GPU seed refinement vs the CPU consumer): 1e-4 times the
+    magnitude of its terms, |f_add| + |g_add| + |f_rescale| (2^ex |ip| + (2^ex - 1) ||q'||_1
+    + |kb|). The ex-code inner product is at most (2^ex - 1) ||q'||_1."""
+    s = float(1 << ex_bits)
+    mag = np.abs(np.asarray(f_ex_add, np.float64)) + abs(float(g_add)) + np.abs(
+        np.asarray(f_ex_rescale, np.float64)) * (s * np.abs(np.asarray(exact_ip, np.float64)) +
+                                                 (s - 1) * float(q_l1) + abs(float(kb)))
+    return (1e-4 * mag).astype(np.float32)
+
+
+def seed_threshold(dists, lows, errs, topk: int):
+    """GPU seed threshold of this engine (no counterpart in the reference, whose CPU
+    consumer alone publishes thresholds, cpu_refinement.cpp:207-230): with d_k the topk-th
+    smallest refined seed distance, e the largest rounding bound and l the largest lower
+    bound among the seeds with distance <= d_k, thr = nextafter(max(d_k + e, l), +inf)
+    in FP32. None when fewer than topk seeds exist."""
+    d = np.asarray(dists, np.float32)
+    fin = np.isfinite(d)
+    if fin.sum() < topk:
+        return None
+    kth = np.sort(d[fin])[topk - 1]
+    sel = fin & (d <= kth)
+    e = np.float32(np.asarray(errs, np.float32)[sel].max())
+    l = np.float32(np.asarray(lows, np.float32)[sel].max())
+    return np.nextafter(np.float32(max(np.float32(kth + e), l)), np.float32(np.inf))
+
+
 def brute_force_gt(base: np.ndarray, queries: np.ndarray, k: int, metric: int) -> np.ndarray:
     """Exact top-k by float64 brute force (tools/data/generate_gt_gpu.py semantics)."""
     b = base.astype(np.float64)
@@ -515,4 +553,7 @@ PINNED = {
     "excode_ip": "golden: ref_dump ip_fxu7 (reference ip64_fxu7_avx), 1e-5",
     "refine_dist": "golden: reproduces reference est_exdist from est_ipx0 (split_distance_boosting), 1e-5",
     "hybrid_search": "composition of the pinned functions; top-k ids vs brute force on all-probe search",
+    "vanguard_seeds": "brute force: equals the first min(keep, #valid) of a full stable sort of valid lows",
+    "refine_error_bound": "property: bounds |f32 refine - f64 refine| of refine_dist on golden ex-codes",
+    "seed_threshold": "properties: >= topk seeds strictly below it with lows below it; >= true topk-th",
 }

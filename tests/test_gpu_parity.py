@@ -308,18 +308,120 @@ def test_batch_q_and_reuse_do_not_change_results(synth, batch_q):
     assert np.allclose(d, d0, rtol=1e-6)
 
 
-def test_live_thresholds_match_frozen_results(synth):
-    """Default production mode (live thresholds, secondary filter, vanguard 5) returns the
-    same top-k as the exhaustive frozen search, except where refine distances tie."""
+@pytest.mark.parametrize("gpu_seed", [True, False])
+def test_live_thresholds_match_frozen_results(synth, gpu_seed):
+    """Default production mode (live thresholds, secondary filter, vanguard 5, with or
+    without GPU seed thresholds) returns the same top-k as the exhaustive frozen search,
+    except where refine distances tie."""
     nprobe, topk = 16, 10
-    say("[gpu] live vs frozen")
+    say(f"[gpu] live vs frozen, gpu_seed={gpu_seed}")
     _, d0, i0 = run_frozen(synth, nprobe, topk, vanguard=0)
-    eng = make_engine(synth, nprobe, topk, vanguard=5, frozen=False, secondary=True)
+    eng = make_engine(synth, nprobe, topk, vanguard=5, frozen=False, secondary=True,
+                      gpu_seed_refine=gpu_seed)
     eng.reset_buffer(synth.queries)
     d, i = eng.search(synth.queries, topk, nprobe, 4)
     st = eng.stats()
+    say(f"[gpu]   candidates per query {st['submitted'] / synth.queries.shape[0]:.1f}")
     assert st["submitted"] < synth.queries.shape[0] * 20000  # the filter prunes
     same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), i0.tolist())])
+    assert same >= 0.99, same
+
+
+def test_gpu_seed_thresholds_frozen_parity(synth):
+    """GPU seed refinement in its deterministic test mode (frozen snapshot lowered by the
+    seed thresholds): seed choice and refined seed distances vs the oracle, the seeded
+    threshold vs the oracle's rule and its safety, the candidate count of the far and
+    recovery passes against it, and an unchanged final top-k."""
+    nprobe, topk, van = 8, 10, 3
+    keep = max(topk, 20)
+    say("[gpu] GPU seed thresholds, frozen parity")
+    case = synth
+    nq, P = case.queries.shape[0], case.file.padded_dim
+    eng = make_engine(case, nprobe, topk, vanguard=van, frozen=True,
+                      extra_flags=ca.FLAG_GPU_SEED_FROZEN)
+    eng.reset_buffer(case.queries)
+    d, i = eng.search(case.queries, topk, nprobe)
+    st = eng.stats()
+    g = gpu_intermediates(eng, case, nprobe)
+    sdist = eng.debug_read(ca.DBG_SEED_DIST, (nq, van, keep), np.float32)
+    thr = eng.debug_read(ca.DBG_THRESHOLDS, (nq,), np.float32)
+    qint = qint_from_planes(g["planes"][:, :8])
+    qres = qint_from_planes(g["planes"][:, 8:])
+    sd = case.sd
+    lo_cnt = hi_cnt = 0
+    od = np.full((nq, topk), F32_MAX, np.float32)
+    oi = np.zeros((nq, topk), np.uint32)
+    for q in range(nq):
+        dists, lows, errs, l1 = [], [], [], float(np.abs(g["qr"][q]).sum())
+        pair_lows, seed_sets = [], []
+        for p in range(nprobe):
+            c = int(g["pidx"][q, p])
+            s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+            ipi = orc.ip_int_direct(sd.bits[s:s + n], qint[q])
+            f = sd.short_factors[s:s + n]
+            low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p],
+                               orc.exact_ip_bitwise(ipi, g["width"][q]), g["k1"][q])
+            pair_lows.append(low)
+            if p >= van:
+                seed_sets.append(None)
+                continue
+            seeds = orc.vanguard_seeds(low, keep, F32_MAX)
+            seed_sets.append(set(seeds.tolist()))
+            gids = s + seeds
+            ipr = orc.ip_int_direct(sd.bits[gids], qres[q])
+            ex2 = orc.exact_ip_two_stage(ipi[seeds], ipr, g["width"][q], g["width2"][q])
+            ipx = orc.excode_ip(g["qr"][q], sd.long_codes[gids], P)
+            fa, fr = sd.ex_factors[gids, 0], sd.ex_factors[gids, 1]
+            rd = orc.refine_dist(fa, fr, g["gadd"][q, p], ex2, ipx, g["kb"][q], 7)
+            err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], 7)
+            got = sdist[q, p][np.isfinite(sdist[q, p])]
+            assert got.size == seeds.size, (q, p)
+            assert np.all(np.abs(np.sort(got) - np.sort(rd)) <= np.sort(err)[::-1][0]), (q, p)
+            dists.append(rd)
+            lows.append(low[seeds])
+            errs.append(err)
+        dists, lows, errs = np.concatenate(dists), np.concatenate(lows), np.concatenate(errs)
+        want = orc.seed_threshold(dists, lows, errs, topk)
+        assert want is not None
+        assert abs(float(thr[q]) - float(want)) <= 2e-5 * (abs(float(want)) + 1) + float(errs.max()), q
+        # safety: the topk best seeds stay strictly below the threshold, lows included
+        best = np.argsort(dists, kind="stable")[:topk]
+        assert np.all(dists[best] < thr[q]) and np.all(lows[best] < thr[q]), q
+        # published: every seed, plus non-seeds (vanguard) and far vectors with low < thr;
+        # the oracle's top-k over that candidate set is what the CPU must return
+        band = 1e-5 * (abs(float(thr[q])) + 1)
+        items = []
+        for p in range(nprobe):
+            c = int(g["pidx"][q, p])
+            s = int(sd.cluster_start[c])
+            low = pair_lows[p].astype(np.float64)
+            mask = np.ones(low.size, bool)
+            if seed_sets[p] is not None:
+                idx = np.fromiter(seed_sets[p], np.int64, len(seed_sets[p]))
+                mask[idx] = False
+                lo_cnt += idx.size
+                hi_cnt += idx.size
+            lo_cnt += int((low[mask] < thr[q] - band).sum())
+            hi_cnt += int((low[mask] < thr[q] + band).sum())
+            keep_local = np.nonzero(~mask | (low < thr[q] - band))[0]
+            gids = s + keep_local
+            ipi = orc.ip_int_direct(sd.bits[gids], qint[q])
+            ipr = orc.ip_int_direct(sd.bits[gids], qres[q])
+            ex2 = orc.exact_ip_two_stage(ipi, ipr, g["width"][q], g["width2"][q])
+            rd = orc.refine_dist(sd.ex_factors[gids, 0], sd.ex_factors[gids, 1], g["gadd"][q, p], ex2,
+                                 orc.excode_ip(g["qr"][q], sd.long_codes[gids], P), g["kb"][q], 7)
+            items += list(zip(rd.tolist(), sd.ids[gids].tolist()))
+        items.sort()
+        for r, (dv, pid) in enumerate(items[:topk]):
+            od[q, r], oi[q, r] = dv, pid
+    assert lo_cnt <= st["submitted"] <= hi_cnt, (lo_cnt, st["submitted"], hi_cnt)
+    assert_topk_equal(d, i, od, oi)
+    # against the exhaustive search: seeding pruned, and only rare RaBitQ lower-bound
+    # misses (low above the refined distance) differ
+    ed, ei, cands = oracle_topk_from_gpu(case, g, nprobe, topk)
+    assert st["submitted"] < sum(len(c) for c in cands)
+    same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), ei.tolist())])
+    say(f"[gpu]   candidates {st['submitted']} of {sum(len(c) for c in cands)}, top-k overlap {same:.4f}")
     assert same >= 0.99, same
 
 

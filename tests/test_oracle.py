@@ -251,3 +251,62 @@ def test_hybrid_search_all_probes_matches_brute_force(fx):
     assert orc.recall_at_k(res.ids, ref_ids.astype(np.uint32), 10) >= 0.95
     # every vector of every probed cluster was a candidate with infinite thresholds
     assert all(len(c) == ivf.num for c in res.candidates)
+
+
+def test_vanguard_seed_selection_brute_force():
+    rng = np.random.default_rng(21)
+    for n, keep in ((50, 20), (300, 20), (10, 20), (1000, 100)):
+        low = rng.integers(0, 40, n).astype(np.float32)  # many ties
+        cutoff = np.float32(30)
+        got = orc.vanguard_seeds(low, keep, cutoff)
+        valid = [i for i in range(n) if low[i] < cutoff]
+        want = sorted(valid, key=lambda i: (low[i], i))[:keep]
+        assert got.tolist() == want
+
+
+def test_refine_error_bound_covers_f32_evaluation(fx):
+    name, ref, ivf, sd, q = fx
+    P = ivf.padded_dim
+    qr = orc.rotate(q, sd.rotator)
+    _, kb = orc.query_factors(qr, ivf.ex_bits)
+    rng = np.random.default_rng(22)
+    for i in range(min(8, q.shape[0])):
+        gids = rng.integers(0, ivf.num, 64)
+        ip_ex = orc.excode_ip(qr[i], sd.long_codes[gids], P)
+        ex = rng.normal(0, 1, 64).astype(np.float32)
+        g = np.float32(abs(rng.normal(0, 5)))
+        fa, fr = sd.ex_factors[gids, 0], sd.ex_factors[gids, 1]
+        d64 = fa.astype(np.float64) + g + fr.astype(np.float64) * (128.0 * ex + ip_ex.astype(np.float64) + kb[i])
+        # a deliberately different f32 order: sequential accumulation of the ex-code dot
+        codes = orc.unpack_excode7(sd.long_codes[gids], P).astype(np.float32)
+        dot32 = np.zeros(64, np.float32)
+        for d in range(P):
+            dot32 = (dot32 + codes[:, d] * qr[i, d]).astype(np.float32)
+        d32 = (fa + g + fr * ((np.float32(128) * ex + dot32).astype(np.float32) + kb[i])).astype(np.float32)
+        bound = orc.refine_error_bound(fa, fr, g, ex, np.abs(qr[i]).sum(), kb[i], 7)
+        assert np.all(np.abs(d32 - d64) <= bound), name
+
+
+def test_seed_threshold_properties():
+    rng = np.random.default_rng(23)
+    for topk in (1, 10, 100):
+        n = 5 * max(topk, 20)
+        d = rng.normal(0, 3, n).astype(np.float32)
+        d[rng.random(n) < 0.2] = np.inf  # unused slots
+        lows = (d - np.abs(rng.normal(0, 1, n))).astype(np.float32)
+        errs = np.abs(rng.normal(0, 1e-3, n)).astype(np.float32)
+        thr = orc.seed_threshold(d, lows, errs, topk)
+        fin = np.isfinite(d)
+        if fin.sum() < topk:
+            assert thr is None
+            continue
+        best = np.argsort(np.where(fin, d, np.inf), kind="stable")[:topk]
+        # the topk best seeds stay strictly below it, with their rounding and their lows
+        assert np.all(d[best] + errs[best] < thr) and np.all(lows[best] < thr)
+        assert thr >= np.sort(d[fin])[topk - 1]
+    # a low above every distance lifts the threshold above it
+    d = np.arange(20, dtype=np.float32)
+    lows = d.copy()
+    lows[3] = 50.0
+    assert orc.seed_threshold(d, lows, np.zeros(20, np.float32), 10) > 50.0
+    assert orc.seed_threshold(d[:5], lows[:5], np.zeros(5, np.float32), 10) is None
