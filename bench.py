@@ -208,7 +208,8 @@ def main():
         "config": {"workload": c.describe(), "nprobe": nprobe, "recall_at_10": round(float(np.mean(recalls)), 4),
                    "qps_with_upload": round(queries.shape[0] * args.steps / sum(times_up), 1),
                    "batch_q": batch_q, "vanguard": c.vanguard, "cpu_secondary_filter": c.secondary_filter,
-                   "cpu_refine_threads": threads, "query_chunk": chunk, "sweep": sweep},
+                   "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
+                   "query_chunk": chunk, "sweep": sweep},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                      "kernel": "scan_kernel<W=4,Q=1|8,far> (far-pair RaBitQ popcount scan)",

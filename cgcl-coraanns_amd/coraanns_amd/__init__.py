@@ -175,6 +175,7 @@ HOST_SIGNATURES = {
     "cora_build_ivf": [_P, _P, _P, _P, _U64, _U64, _U64, _U64, _U64, _I, _I, C.c_char_p],
     "cora_quantize_rows": [_P, _P, _U64, _U64, _U64, _I, _P, _P, _P, _P],
     "cora_excode_ip7": [_P, _P, _U64, _U64, _P],
+    "cora_cpu_refine_isa": [],
     "cora_test_ring": [C.POINTER(cora_ring_test), _P, _P],
 }
 
@@ -483,6 +484,11 @@ def gpu_topk(base, queries, k, metric=0, device=0):
     _tool_check(_load()[0].cora_tool_topk(_ptr(b), b.shape[0], _ptr(q), q.shape[0], q.shape[1], k, metric,
                                           _ptr(ids), device))
     return ids
+
+
+def cpu_refine_isa():
+    """Vector width (512 or 256) of the CPU refinement's ex-code inner product."""
+    return _load()[1].cora_cpu_refine_isa()
 
 
 def gpu_available():

@@ -275,6 +275,8 @@ int cora_quantize_rows(const float *rows, const float *centroid, uint64_t n, uin
     });
 }
 
+int cora_cpu_refine_isa(void) { return detail::excode_ip7_isa(); }
+
 int cora_excode_ip7(const float *q, const uint8_t *packed, uint64_t n, uint64_t P, float *out) {
     NEED(q);
     NEED(packed);

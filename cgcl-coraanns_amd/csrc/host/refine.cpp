@@ -34,7 +34,9 @@
 
 namespace coraanns::detail {
 
-float excode_ip7(const float *q, const uint8_t *packed, std::size_t P) {
+// AVX2: eight dimensions per step (the reference's ip64_fxu7_avx granularity,
+// space.hpp:677-761).
+float excode_ip7_avx2(const float *q, const uint8_t *packed, std::size_t P) {
     __m256 acc0 = _mm256_setzero_ps(), acc1 = _mm256_setzero_ps();
     constexpr uint64_t kLow6 = 0x3F3F3F3F3F3F3F3Full;
     constexpr uint64_t kOnes = 0x0101010101010101ull;
@@ -72,6 +74,67 @@ float excode_ip7(const float *q, const uint8_t *packed, std::size_t P) {
     return _mm_cvtss_f32(h);
 }
 
+// AVX-512: sixteen dimensions per step. Per 64-dimension group, dimensions 0..47 are the
+// low six bits of bytes 0..47, dimensions 48..63 gather their bit pairs from the top two
+// bits of bytes j, 16+j and 32+j, and bit 6 of dimension 16i+m (bit 8(m%8) + 2i + m/8 of
+// the group's u64 at byte 48) enters as a masked +64 built with pext.
+__attribute__((target("avx512f,avx512bw,avx512vl,bmi2"))) float
+excode_ip7_avx512(const float *q, const uint8_t *packed, std::size_t P) {
+    __m512 acc0 = _mm512_setzero_ps(), acc1 = _mm512_setzero_ps();
+    const __m512i low6 = _mm512_set1_epi32(0x3F), two = _mm512_set1_epi32(3), c64 = _mm512_set1_epi32(64);
+    for (std::size_t g = 0; g < P; g += 64) {
+        const uint8_t *c = packed + g / 64 * 56;
+        const float *qq = q + g;
+        uint64_t top;
+        std::memcpy(&top, c + 48, 8);
+        const __m512i v0 = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i *>(c)));
+        const __m512i v1 = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i *>(c + 16)));
+        const __m512i v2 = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i *>(c + 32)));
+        __m512i d[4];
+        d[0] = _mm512_and_si512(v0, low6);
+        d[1] = _mm512_and_si512(v1, low6);
+        d[2] = _mm512_and_si512(v2, low6);
+        d[3] = _mm512_or_si512(
+            _mm512_and_si512(_mm512_srli_epi32(v0, 6), two),
+            _mm512_or_si512(_mm512_slli_epi32(_mm512_and_si512(_mm512_srli_epi32(v1, 6), two), 2),
+                            _mm512_slli_epi32(_mm512_and_si512(_mm512_srli_epi32(v2, 6), two), 4)));
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = static_cast<uint32_t>(_pext_u64(top, 0x0303030303030303ull << (2 * i)));
+            const __mmask16 m = static_cast<__mmask16>(_pext_u32(r, 0x5555u) | (_pext_u32(r, 0xAAAAu) << 8));
+            const __m512i code = _mm512_mask_add_epi32(d[i], m, d[i], c64);
+            const __m512 prod = _mm512_cvtepi32_ps(code);
+            if (i & 1)
+                acc1 = _mm512_fmadd_ps(prod, _mm512_loadu_ps(qq + 16 * i), acc1);
+            else
+                acc0 = _mm512_fmadd_ps(prod, _mm512_loadu_ps(qq + 16 * i), acc0);
+        }
+    }
+    return _mm512_reduce_add_ps(_mm512_add_ps(acc0, acc1));
+}
+
+namespace {
+
+using ExcodeIpFn = float (*)(const float *, const uint8_t *, std::size_t);
+
+// AVX-512 when the CPU has it, unless CORA_CPU_ISA=avx2 asks for the AVX2 path.
+ExcodeIpFn pick_excode_ip() {
+    const char *isa = std::getenv("CORA_CPU_ISA");
+    const bool force_avx2 = isa && std::strcmp(isa, "avx2") == 0;
+    __builtin_cpu_init();
+    if (!force_avx2 && __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+        __builtin_cpu_supports("avx512vl") && __builtin_cpu_supports("bmi2"))
+        return excode_ip7_avx512;
+    return excode_ip7_avx2;
+}
+
+const ExcodeIpFn g_excode_ip = pick_excode_ip();
+
+}  // namespace
+
+float excode_ip7(const float *q, const uint8_t *packed, std::size_t P) { return g_excode_ip(q, packed, P); }
+
+int excode_ip7_isa() { return g_excode_ip == excode_ip7_avx512 ? 512 : 256; }
+
 namespace {
 
 inline bool slot_complete(const queue::Candidate *slot, queue::Candidate &out) {
@@ -95,15 +158,16 @@ inline void clear_slots(queue::Candidate *slots, std::size_t n) {
 // Records this many ring positions ahead have their ex-code, ex-factors and id lines
 // prefetched: candidates are random accesses into arrays far larger than the caches, and
 // their gids are in the ring well before the records are processed.
-constexpr std::size_t kPrefetchAhead = 12;
+constexpr std::size_t kPrefetchAhead = 20;
 
 inline void prefetch_record(const queue::Candidate *slot, const RefineArgs &a, std::size_t lc) {
     const uint32_t gid = __atomic_load_n(&slot->gid, __ATOMIC_RELAXED);
     if (gid >= a.num_vectors)  // empty (all ones) or not yet written
         return;
-    const char *code = reinterpret_cast<const char *>(a.long_codes + static_cast<std::size_t>(gid) * lc);
-    for (std::size_t off = 0; off < lc; off += 64)
-        _mm_prefetch(code + off, _MM_HINT_T0);
+    // every cache line the code touches (112 bytes at a 112-byte stride often span three)
+    const uintptr_t first = reinterpret_cast<uintptr_t>(a.long_codes + static_cast<std::size_t>(gid) * lc);
+    for (uintptr_t line = first & ~uintptr_t{63}; line < first + lc; line += 64)
+        _mm_prefetch(reinterpret_cast<const char *>(line), _MM_HINT_T0);
     _mm_prefetch(reinterpret_cast<const char *>(a.ex_factors + 2 * static_cast<std::size_t>(gid)), _MM_HINT_T0);
     _mm_prefetch(reinterpret_cast<const char *>(a.ids + gid), _MM_HINT_T0);
 }

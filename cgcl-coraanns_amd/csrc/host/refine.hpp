@@ -8,8 +8,12 @@
 
 namespace coraanns::detail {
 
-// <q', ex_code> for one 7-bit packed ex-code of P dims (P % 64 == 0), AVX2.
+// <q', ex_code> for one 7-bit packed ex-code of P dims (P % 64 == 0): AVX-512 when the
+// CPU has it (and CORA_CPU_ISA is not "avx2"), otherwise AVX2.
 float excode_ip7(const float *q, const uint8_t *packed, std::size_t P);
+float excode_ip7_avx2(const float *q, const uint8_t *packed, std::size_t P);
+// vector width of the path excode_ip7 uses: 512 or 256
+int excode_ip7_isa();
 
 struct RefineArgs {
     queue::Candidate *items = nullptr;  // host ring

@@ -114,8 +114,11 @@ int cora_build_ivf(const float *rotated_data, const float *rotated_centroids,
 int cora_quantize_rows(const float *rows, const float *centroid, uint64_t n, uint64_t P,
                        uint64_t ex_bits, int metric, uint8_t *bits, float *f1, uint8_t *excode,
                        float *f2);
-/* <q', ex_code> of n packed 7-bit codes (AVX2 path of the CPU refinement). */
+/* <q', ex_code> of n packed 7-bit codes (the CPU refinement's inner product). */
 int cora_excode_ip7(const float *q, const uint8_t *packed, uint64_t n, uint64_t P, float *out);
+/* Vector width of the CPU refinement's inner product: 512 (AVX-512) or 256 (AVX2;
+ * forced with CORA_CPU_ISA=avx2 in the environment). */
+int cora_cpu_refine_isa(void);
 
 /* Ring protocol check without a GPU: producer threads run the device publication
  * protocol (reserve, cached write limit, HBM-style spill, drain, done) against the real

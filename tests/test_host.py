@@ -2,6 +2,7 @@
 
 No GPU is touched: the libraries are loaded and only host entry points are called.
 """
+import os
 import re
 import shutil
 import subprocess
@@ -214,3 +215,30 @@ def test_cpp_unit(tmp_path, src):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "PASS" in r.stdout
+
+
+def test_excode_ip7_avx2_and_dispatched_paths_agree(golden, tmp_path):
+    """The CPU refinement's inner product gives the same values on its AVX-512 path (when
+    the CPU has it) and its AVX2 path (CORA_CPU_ISA=avx2, checked in a child process)."""
+    g = golden("quant_d128")
+    packed = np.ascontiguousarray(g["packed7"])
+    rng = np.random.default_rng(31)
+    q = rng.normal(0, 1, 128).astype(np.float32)
+    np.save(tmp_path / "q.npy", q)
+    np.save(tmp_path / "packed.npy", packed)
+    code = (
+        "import sys, numpy as np; sys.path.insert(0, sys.argv[1]); import coraanns_amd as ca; "
+        "q = np.load(sys.argv[2]); p = np.load(sys.argv[3]); "
+        "np.save(sys.argv[4], ca.excode_ip7(q, p)); print(ca.cpu_refine_isa())")
+    outs = {}
+    for isa in ("", "avx2"):
+        env = dict(os.environ, CORA_CPU_ISA=isa)
+        out = tmp_path / f"ip_{isa or 'auto'}.npy"
+        r = subprocess.run([sys.executable, "-c", code, str(REPO / "cgcl-coraanns_amd"), str(tmp_path / "q.npy"),
+                            str(tmp_path / "packed.npy"), str(out)], env=env, capture_output=True, text=True,
+                           check=True)
+        outs[isa or "auto"] = (int(r.stdout.strip()), np.load(out))
+    assert outs["avx2"][0] == 256
+    want = orc.excode_ip(q, packed, 128)
+    for isa, (width, ip) in outs.items():
+        assert np.all(np.abs(ip - want) <= 1e-6 * np.abs(q).sum() * 127), isa
