@@ -158,7 +158,8 @@ def main():
         log(f"[sweep] nprobe={nprobe} QPS={queries.shape[0] / dt:.1f} recall={r:.4f} "
             f"cand/q={st['submitted'] / queries.shape[0]:.1f} (seed {pp[0] / queries.shape[0]:.1f}, "
             f"far {(pp[1] - pp[0]) / queries.shape[0]:.1f}, recovery {(pp[2] - pp[1]) / queries.shape[0]:.1f}; "
-            f"gpu-seeded queries {st['seeded_queries']}) scan={st['scan_ms']:.3f}ms filter={st['gpu_filter_ms']:.3f}ms")
+            f"gpu-seeded queries {st['seeded_queries']}, pre-filter dropped "
+            f"{st['prefilter_dropped'] / queries.shape[0]:.1f}) scan={st['scan_ms']:.3f}ms filter={st['gpu_filter_ms']:.3f}ms")
     nprobe = args.nprobe
     if not nprobe:
         ok = [s["nprobe"] for s in sweep if s["recall"] >= args.recall_target]

@@ -38,7 +38,7 @@ FLAG_CROSS_QUERY_REUSE = 4
 DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range(5)
 DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
 DBG_SEED_DIST, DBG_THRESHOLDS = 10, 11
-FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN = 1 << 3, 1 << 4
+FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
 
 
 class EngineUnavailable(RuntimeError):
@@ -77,7 +77,8 @@ class cora_search_stats(C.Structure):
                 ("stalled", C.c_int32), ("filter_ms", C.c_float), ("scan_ms", C.c_float),
                 ("scan_bytes", C.c_uint64), ("scan_units", C.c_uint64),
                 ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float), ("probe_flops", C.c_uint64),
-                ("pass_produced", C.c_uint64 * 3), ("seeded_queries", C.c_uint64)]
+                ("pass_produced", C.c_uint64 * 3), ("seeded_queries", C.c_uint64),
+                ("prefilter_dropped", C.c_uint64)]
 
 
 class cora_queue_view(C.Structure):
@@ -91,7 +92,7 @@ class cora_hybrid_config(C.Structure):
                 ("cpu_secondary_filter", C.c_int), ("vanguard_size", C.c_uint64),
                 ("queue_capacity", C.c_uint64), ("queue_spill_capacity", C.c_uint64),
                 ("metric", C.c_int), ("frozen_thresholds", C.c_int), ("cpu_threads", C.c_int),
-                ("gpu_seed_refine", C.c_int), ("extra_flags", C.c_uint32)]
+                ("gpu_seed_refine", C.c_int), ("gpu_refine_filter", C.c_int), ("extra_flags", C.c_uint32)]
 
 
 class cora_hybrid_stats(C.Structure):
@@ -99,7 +100,7 @@ class cora_hybrid_stats(C.Structure):
                 ("gpu_filter_ms", C.c_float), ("scan_ms", C.c_float), ("scan_bytes", C.c_uint64),
                 ("scan_units", C.c_uint64), ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float),
                 ("probe_flops", C.c_uint64), ("pass_produced", C.c_uint64 * 3),
-                ("seeded_queries", C.c_uint64)]
+                ("seeded_queries", C.c_uint64), ("prefilter_dropped", C.c_uint64)]
 
 
 class cora_ivf_info(C.Structure):
@@ -275,7 +276,7 @@ class HybridIndex:
     def __init__(self, device=0, *, profiling=False, candidate_stats=False, gpu_filter_timing=False,
                  cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                  queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
-                 cpu_threads=0, gpu_seed_refine=True, extra_flags=0):
+                 cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0):
         _, host = _load()
         h = C.c_void_p()
         _host_check(host.cora_hybrid_create(C.byref(h), device))
@@ -286,18 +287,19 @@ class HybridIndex:
                        cpu_secondary_filter=cpu_secondary_filter, vanguard_size=vanguard_size,
                        queue_capacity=queue_capacity, queue_spill_capacity=queue_spill_capacity,
                        metric=metric, frozen_thresholds=frozen_thresholds, cpu_threads=cpu_threads,
-                       gpu_seed_refine=gpu_seed_refine, extra_flags=extra_flags)
+                       gpu_seed_refine=gpu_seed_refine, gpu_refine_filter=gpu_refine_filter,
+                       extra_flags=extra_flags)
 
     def configure(self, *, profiling=False, candidate_stats=False, gpu_filter_timing=False,
                   cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                   queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
-                  cpu_threads=0, gpu_seed_refine=True, extra_flags=0):
+                  cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0):
         cfg = cora_hybrid_config(int(profiling), int(candidate_stats), int(gpu_filter_timing),
                                  int(cross_query_reuse), int(cpu_secondary_filter), int(vanguard_size),
                                  int(queue_capacity or 0),
                                  (1 << 64) - 1 if queue_spill_capacity is None else int(queue_spill_capacity),
                                  int(metric), int(frozen_thresholds), int(cpu_threads),
-                                 int(gpu_seed_refine), int(extra_flags))
+                                 int(gpu_seed_refine), int(gpu_refine_filter), int(extra_flags))
         _host_check(_load()[1].cora_hybrid_configure(self._h, C.byref(cfg)))
 
     def load_from_raw_pointers(self, num_vecs, dim, padded_dim, n_centroids, ex_bits, centroids,

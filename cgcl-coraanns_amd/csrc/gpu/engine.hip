@@ -664,20 +664,26 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         HIPCHK(hipMemcpyAsync(E->d_thr_snap, E->h_thr_stage, (size_t)nq * 4, hipMemcpyHostToDevice, s));
     }
     ScanParams p = scan_params(E, depth, keep, frozen);
-    // GPU seed thresholds: live thresholds only (frozen mode keeps the launch snapshot)
-    const bool gpu_seed = depth > 0 && E->d_excodes && E->d_seed_dist &&
-                          !(a->flags & CORA_FLAG_NO_GPU_SEED) &&
-                          (!frozen || (a->flags & CORA_FLAG_GPU_SEED_FROZEN));
-    if (gpu_seed) {
+    // GPU ex-code stages (seed thresholds, refined pre-filter): live thresholds only, or
+    // the frozen snapshot in the GPU_SEED_FROZEN test mode
+    const bool ex_stage_mode = !frozen || (a->flags & CORA_FLAG_GPU_SEED_FROZEN);
+    const bool gpu_seed = depth > 0 && E->d_excodes && E->d_seed_dist && ex_stage_mode &&
+                          !(a->flags & CORA_FLAG_NO_GPU_SEED);
+    const bool prefilter = E->d_excodes && ex_stage_mode && !(a->flags & CORA_FLAG_NO_GPU_PREFILTER);
+    if (gpu_seed || prefilter) {
         p.ex_codes = E->d_excodes;
         p.ex_factors = E->d_exfac;
         p.qrot = E->d_qrot;
         p.kb = E->d_kb;
+    }
+    if (gpu_seed) {
         p.seed_dist = E->d_seed_dist;
         p.seed_low = E->d_seed_low;
         p.seed_err = E->d_seed_err;
     }
-    launch_fill_u64(E->d_stats + 3, 0ull, 4, s);  // per-pass counters of this launch
+    p.prefilter = prefilter ? 1 : 0;
+    p.dropped = E->d_stats + 7;
+    launch_fill_u64(E->d_stats + 3, 0ull, 5, s);  // per-pass counters of this launch
     if (timing)
         HIPCHK(hipEventRecord(E->ev_f0, s));
     if (depth > 0) {
@@ -754,6 +760,7 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     for (int i = 0; i < 3; ++i)
         out.pass_produced[i] = stats[3 + i];
     out.seeded_queries = stats[6];
+    out.prefilter_dropped = stats[7];
     if (E->last_timing) {
         HIPCHK(hipEventElapsedTime(&out.filter_ms, E->ev_f0, E->ev_f1));
         HIPCHK(hipEventElapsedTime(&out.scan_ms, E->ev_s0, E->ev_s1));

@@ -119,6 +119,9 @@ struct ScanParams {
     int *van_ip;
     uint32_t van_stride;
     uint32_t van_blocks;
+    // refined pre-filter of the far and recovery passes (needs ex_codes)
+    int prefilter;
+    unsigned long long *dropped;  // records the pre-filter dropped
     // dense debug output
     int32_t *dbg_ip;
     int32_t *dbg_ip2;            // residual inner product <b, qres>

@@ -26,12 +26,14 @@
 // tile's loads are issued before the current tile is evaluated.
 //
 // Publication (ring_queue.cuh:45-115): survivors are compacted with a ballot and a lane
-// rank (mbcnt) into a per-wave LDS stage (record + code words). A full stage, and the
-// last one, is flushed with one 64-bit atomicAdd on the HBM position counter for all of
-// its records; each record then gets its residual inner product and goes to the
-// host-coherent ring with one write-through 16-byte store when its position is below
-// the cached write limit (released + capacity), or to the HBM spill buffer, which the
-// drain kernel publishes once the CPU has released that slot.
+// rank (mbcnt) into a per-wave LDS stage (record, code words, threshold). A full stage,
+// and the last one, is flushed 64 records at a time: each record gets its residual inner
+// product (and, with the HBM ex-codes, an optional refined-distance check against its
+// threshold), the kept records of the round take one 64-bit atomicAdd on the HBM
+// position counter, and each goes to the host-coherent ring with one write-through
+// 16-byte store when its position is below the cached write limit (released +
+// capacity), or to the HBM spill buffer, which the drain kernel publishes once the CPU
+// has released that slot.
 #include <float.h>
 
 #include <mutex>
@@ -129,6 +131,37 @@ __device__ __forceinline__ float two_stage_ip(float width, int ip, float width2,
     return __fmaf_rn(width2, (float)ip_res, __fmul_rn(width, (float)ip));
 }
 
+// <q', ex_code> over one 8-dimension chunk c (group g = c / 8 of 64 dimensions, k = c % 8)
+// of a packed 7-bit ex-code (pack_excode.hpp:216-265): per 64 dimensions, bytes 0..47
+// hold the low six bits of dimensions 0..47, and in their top two bits the bit pairs of
+// dimensions 48..63 (bits 0-1 in bytes 0..15, 2-3 in 16..31, 4-5 in 32..47); the u64 at
+// bytes 48..55 holds bit 6 of dimension 8k+j at bit 8j+k. l1 accumulates sum |q'|.
+__device__ __forceinline__ float excode_chunk_ip(const uint8_t *__restrict__ code,
+                                                 const float *__restrict__ q, uint32_t c,
+                                                 float &l1) {
+    const uint32_t g = c >> 3, k = c & 7;
+    const uint64_t *grp = reinterpret_cast<const uint64_t *>(code + (size_t)g * 56);
+    uint64_t v;
+    if (k < 6) {
+        v = grp[k] & 0x3F3F3F3F3F3F3F3Full;
+    } else {
+        const uint32_t o = k - 6;
+        v = ((grp[o] >> 6) & 0x0303030303030303ull) | ((grp[2 + o] >> 4) & 0x0C0C0C0C0C0C0C0Cull) |
+            ((grp[4 + o] >> 2) & 0x3030303030303030ull);
+    }
+    v |= ((grp[6] >> k) & 0x0101010101010101ull) << 6;
+    const float4 q0 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k);
+    const float4 q1 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k + 4);
+    const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sum = fmaf((float)((v >> (8 * j)) & 0xFFu), qq[j], sum);
+        l1 += fabsf(qq[j]);
+    }
+    return sum;
+}
+
 // One 16-byte Candidate store to the host-coherent ring that writes through the GPU L2
 // (system-scope coherence bits sc0 sc1). A plain store to host memory may stay in L2
 // until the next system-scope release, which a producer still running never issues, so
@@ -179,39 +212,85 @@ __device__ __forceinline__ void place_record(const QueueDev &q, unsigned long lo
     }
 }
 
-// Publish the n staged survivors of this wave (n wave-uniform, 0 < n <= kCap). Must be
-// called by all 64 lanes; the workgroup is this one wave. Staged records carry ip_int
-// in their exact_ip word; it is replaced by the two-stage estimate here.
+// Refined distance of a candidate (cpu_refinement.cpp:183-192) from the HBM copy of the
+// ex-codes, evaluated by one lane, and a bound on its rounding difference from the CPU
+// consumer's evaluation (1e-4 of the magnitude of the terms).
+__device__ __forceinline__ float refine_one(const ScanParams &p, uint32_t query, uint32_t probe,
+                                            uint32_t gid, float ex, float &err) {
+    const size_t lc = (size_t)p.P * 7 / 8;
+    const uint8_t *code = p.ex_codes + (size_t)gid * lc;
+    const float *qv = p.qrot + (size_t)query * p.P;
+    float ip = 0.0f, l1 = 0.0f;
+    for (uint32_t c = 0; c < p.P / 8; ++c)
+        ip += excode_chunk_ip(code, qv, c, l1);
+    const float fa = p.ex_factors[2 * (size_t)gid], fr = p.ex_factors[2 * (size_t)gid + 1];
+    const float gadd = p.pgadd[(size_t)query * p.nprobe + probe], kbq = p.kb[query];
+    err = 1e-4f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq)));
+    return fa + gadd + fr * (128.0f * ex + ip + kbq);
+}
+
+// Publish the n staged survivors of this wave (n wave-uniform, 0 < n <= kCap), 64 at a
+// time. Must be called by all 64 lanes; the workgroup is this one wave. Staged records
+// carry ip_int in their exact_ip word; it is replaced by the two-stage estimate. With
+// the refined pre-filter (p.prefilter) a record whose refined distance exceeds its
+// unit's threshold by more than the rounding bound is dropped: every published threshold
+// is backed by at least topk candidates the CPU consumer will refine, so such a record
+// can never enter the top-k and the consumer would discard it. Kept records of each
+// round take one reservation on the ring position counter.
 template <int W>
 __device__ __forceinline__ void flush_stage(const ScanParams &p, const QueueDev &q, uint32_t n,
                                             const uint4 *s_rec, const uint32_t *s_code,
-                                            unsigned long long &limit, uint32_t lane) {
+                                            const float *s_cut, unsigned long long &limit,
+                                            uint32_t lane) {
     constexpr int K = Words<W>::kMax;
     constexpr int CAP = Stage<W>::kCap;
     const uint32_t nw = W > 0 ? (uint32_t)W : p.P / 32;
     __syncthreads();  // staged LDS writes of every lane are visible
-    unsigned long long base = 0;
-    if (lane == 0)
-        base = atomicAdd(q.produced, (unsigned long long)n);
-    base = shfl0_u64(base);
-    if (base + n > limit) {
-        unsigned long long fresh = 0;
-        if (lane == 0)
-            fresh = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released, q.capacity,
-                                  base + n);
-        limit = shfl0_u64(fresh);
-    }
-    for (uint32_t i = lane; i < n; i += 64) {
-        uint4 rec = s_rec[i];
-        uint32_t x[K];
+    for (uint32_t i0 = 0; i0 < n; i0 += 64) {
+        const uint32_t i = i0 + lane;
+        bool keep = false;
+        uint4 rec = make_uint4(0u, 0u, 0u, 0u);
+        if (i < n) {
+            rec = s_rec[i];
+            uint32_t x[K];
 #pragma unroll
-        for (int w = 0; w < K; ++w)
-            x[w] = (uint32_t)w < nw ? s_code[w * CAP + i] : 0u;
-        const uint32_t query = rec.x & 0xFFFFu;
-        const uint32_t *res = p.qplanes + ((size_t)query * 2 + 1) * kBq * nw;
-        const int ip_res = popc_ip<W>(x, res, nw);
-        rec.z = __float_as_uint(two_stage_ip(p.qwidth[query], (int)rec.z, p.qwidth2[query], ip_res));
-        place_record(q, base + i, limit, rec);
+            for (int w = 0; w < K; ++w)
+                x[w] = (uint32_t)w < nw ? s_code[w * CAP + i] : 0u;
+            const uint32_t query = rec.x & 0xFFFFu;
+            const uint32_t *res = p.qplanes + ((size_t)query * 2 + 1) * kBq * nw;
+            const int ip_res = popc_ip<W>(x, res, nw);
+            const float ex = two_stage_ip(p.qwidth[query], (int)rec.z, p.qwidth2[query], ip_res);
+            rec.z = __float_as_uint(ex);
+            keep = true;
+            if (p.prefilter) {
+                float err;
+                const float dist = refine_one(p, query, rec.x >> 16, rec.y, ex, err);
+                keep = dist <= s_cut[i] + err;
+            }
+        }
+        const unsigned long long m = __ballot(keep);
+        if (p.prefilter && lane == 0) {
+            const uint32_t in_round = min(64u, n - i0);
+            const uint32_t dropped = in_round - (uint32_t)__popcll(m);
+            if (dropped)
+                atomicAdd(p.dropped, (unsigned long long)dropped);
+        }
+        if (m == 0)
+            continue;
+        const uint32_t cnt = (uint32_t)__popcll(m);
+        unsigned long long base = 0;
+        if (lane == 0)
+            base = atomicAdd(q.produced, (unsigned long long)cnt);
+        base = shfl0_u64(base);
+        if (base + cnt > limit) {
+            unsigned long long fresh = 0;
+            if (lane == 0)
+                fresh = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released, q.capacity,
+                                      base + cnt);
+            limit = shfl0_u64(fresh);
+        }
+        if (keep)
+            place_record(q, base + lane_rank(m), limit, rec);
     }
     __syncthreads();  // the stage may be refilled
 }
@@ -258,6 +337,7 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
     __shared__ uint32_t s_planes[kRegs ? 1 : QMAX * kBq * K];
     __shared__ uint4 s_rec[kStaged ? CAP : 1];
     __shared__ uint32_t s_code[kStaged ? CAP * K : 1];
+    __shared__ float s_cut[kStaged ? CAP : 1];
     const uint32_t lane = threadIdx.x;
     const uint32_t rw = p.P / 32;
     const uint32_t nw = W > 0 ? (uint32_t)W : rw;
@@ -391,13 +471,14 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
                     if (mask != 0) {
                         const uint32_t cnt = (uint32_t)__popcll(mask);
                         if (staged + cnt > (uint32_t)CAP) {
-                            flush_stage<W>(p, q, staged, s_rec, s_code, limit, lane);
+                            flush_stage<W>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
                             staged = 0;
                         }
                         if (survive) {
                             const uint32_t k = staged + lane_rank(mask);
                             s_rec[k] = make_uint4(word0[j], start + local, (uint32_t)ip,
                                                   __float_as_uint(low));
+                            s_cut[k] = cutoff[j];
 #pragma unroll
                             for (int w = 0; w < K; ++w)
                                 if ((uint32_t)w < nw)
@@ -417,7 +498,7 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
     }
     if constexpr (kStaged) {
         if (staged)
-            flush_stage<W>(p, q, staged, s_rec, s_code, limit, lane);
+            flush_stage<W>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
     }
 }
 
@@ -429,37 +510,6 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
 // vectors against the thresholds the CPU has tightened meanwhile. Selection: radix
 // select of the keep-th smallest key, all smaller keys plus the lowest-index ties.
 // ---------------------------------------------------------------------------------
-// <q', ex_code> over one 8-dimension chunk c (group g = c / 8 of 64 dimensions, k = c % 8)
-// of a packed 7-bit ex-code (pack_excode.hpp:216-265): per 64 dimensions, bytes 0..47
-// hold the low six bits of dimensions 0..47, and in their top two bits the bit pairs of
-// dimensions 48..63 (bits 0-1 in bytes 0..15, 2-3 in 16..31, 4-5 in 32..47); the u64 at
-// bytes 48..55 holds bit 6 of dimension 8k+j at bit 8j+k. l1 accumulates sum |q'|.
-__device__ __forceinline__ float excode_chunk_ip(const uint8_t *__restrict__ code,
-                                                 const float *__restrict__ q, uint32_t c,
-                                                 float &l1) {
-    const uint32_t g = c >> 3, k = c & 7;
-    const uint64_t *grp = reinterpret_cast<const uint64_t *>(code + (size_t)g * 56);
-    uint64_t v;
-    if (k < 6) {
-        v = grp[k] & 0x3F3F3F3F3F3F3F3Full;
-    } else {
-        const uint32_t o = k - 6;
-        v = ((grp[o] >> 6) & 0x0303030303030303ull) | ((grp[2 + o] >> 4) & 0x0C0C0C0C0C0C0C0Cull) |
-            ((grp[4 + o] >> 2) & 0x3030303030303030ull);
-    }
-    v |= ((grp[6] >> k) & 0x0101010101010101ull) << 6;
-    const float4 q0 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k);
-    const float4 q1 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k + 4);
-    const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        sum = fmaf((float)((v >> (8 * j)) & 0xFFu), qq[j], sum);
-        l1 += fabsf(qq[j]);
-    }
-    return sum;
-}
-
 constexpr int kVanThreads = 256;
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -628,7 +678,7 @@ __device__ __forceinline__ void seed_pair(const ScanParams &p, SeedShared &sh, f
         place_record(q, base + s, limit,
                      make_uint4(w0, cm.start + local, __float_as_uint(ex), __float_as_uint(lows[local])));
     }
-    if (p.ex_codes) {
+    if (p.seed_dist) {
         // Refined distance of every seed, 16 lanes per seed (cpu_refinement.cpp:183-192):
         // f_add_ex + g_add + f_rescale_ex * (2^7 * exact_ip + <q', ex_code> + kbxSumq),
         // with a bound on its rounding difference from the CPU's evaluation.

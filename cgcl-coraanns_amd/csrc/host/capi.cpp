@@ -111,6 +111,7 @@ int cora_hybrid_configure(cora_hybrid *h, const cora_hybrid_config *c) {
         x.set_frozen_thresholds(c->frozen_thresholds != 0);
         x.set_cpu_threads(c->cpu_threads);
         x.set_gpu_seed_refine(c->gpu_seed_refine != 0);
+        x.set_gpu_refine_filter(c->gpu_refine_filter != 0);
         x.set_extra_search_flags(c->extra_flags);
     });
 }
@@ -174,6 +175,7 @@ int cora_hybrid_stats_get(cora_hybrid *h, cora_hybrid_stats *out) {
     for (int i = 0; i < 3; ++i)
         out->pass_produced[i] = x.get_last_pass_produced(i);
     out->seeded_queries = x.get_last_seeded_queries();
+    out->prefilter_dropped = x.get_last_prefilter_dropped();
     return CORA_OK;
 }
 

@@ -86,7 +86,7 @@ void HybridIndex::load_from_raw_pointers(std::size_t num_vecs, std::size_t d, st
     check(engine_, cora_gpu_load_index(engine_, num_vecs, d, p_d, n_centroids, ex_b, metric_,
                                        h_centroids, h_rotator, h_short_data, h_short_factors,
                                        reinterpret_cast<const uint64_t *>(h_cluster_sizes)));
-    if (gpu_seed_refine_ && h_long_code && h_ex_factors && ex_b == 7)
+    if ((gpu_seed_refine_ || gpu_refine_filter_) && h_long_code && h_ex_factors && ex_b == 7)
         check(engine_, cora_gpu_load_excodes(engine_, h_long_code, h_ex_factors));
     num_vectors_ = num_vecs;
     dim_ = d;
@@ -186,7 +186,8 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
                  (gpu_filter_timing_enabled_ || profiling_enabled_ ? uint32_t{CORA_FLAG_FILTER_TIMING}
                                                                    : 0u) |
                  (cross_query_reuse_enabled_ ? uint32_t{CORA_FLAG_CROSS_QUERY_REUSE} : 0u) |
-                 (gpu_seed_refine_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_SEED}) | extra_flags_;
+                 (gpu_seed_refine_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_SEED}) |
+                 (gpu_refine_filter_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_PREFILTER}) | extra_flags_;
     last_gpu_filter_ms_ = 0.0f;
     check(engine_, cora_gpu_launch_search(engine_, &args));
 
@@ -244,6 +245,7 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
     for (int i = 0; i < 3; ++i)
         last_pass_produced_[i] = st.pass_produced[i];
     last_seeded_queries_ = st.seeded_queries;
+    last_prefilter_dropped_ = st.prefilter_dropped;
     if (rc != CORA_OK)
         throw std::runtime_error(engine_error(engine_));
     if (profiling_enabled_) {

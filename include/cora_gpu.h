@@ -58,7 +58,11 @@ enum cora_search_flags {
     /* Test mode: with FROZEN_THRESHOLDS, the GPU seed thresholds lower the launch
      * snapshot, so seeding is deterministic and checkable (CORA_DBG_SEED_DIST,
      * CORA_DBG_THRESHOLDS). */
-    CORA_FLAG_GPU_SEED_FROZEN = 1u << 4
+    CORA_FLAG_GPU_SEED_FROZEN = 1u << 4,
+    /* Do not use the refined pre-filter: with ex-codes in HBM the far and recovery passes
+     * otherwise drop candidates whose refined distance (the CPU consumer's formula)
+     * already exceeds their threshold by more than a rounding bound. */
+    CORA_FLAG_NO_GPU_PREFILTER = 1u << 5
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -99,6 +103,7 @@ typedef struct cora_search_stats {
     uint64_t pass_produced[3]; /* candidates published by the end of the vanguard seed,
                                   far-pair and recovery passes (cumulative) */
     uint64_t seeded_queries;   /* queries that received a GPU seed threshold */
+    uint64_t prefilter_dropped; /* candidates the refined pre-filter dropped */
 } cora_search_stats;
 
 /* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */

@@ -41,6 +41,7 @@ typedef struct cora_hybrid_config {
     int frozen_thresholds;    /* GPU filter reads a snapshot taken at launch */
     int cpu_threads;          /* CPU refinement threads, 0 = omp_get_max_threads() */
     int gpu_seed_refine;      /* set_gpu_seed_refine (HBM ex-codes, GPU seed thresholds) */
+    int gpu_refine_filter;    /* set_gpu_refine_filter (GPU refined pre-filter) */
     uint32_t extra_flags;     /* set_extra_search_flags (cora_search_flags test modes) */
 } cora_hybrid_config;
 
@@ -57,6 +58,7 @@ typedef struct cora_hybrid_stats {
     uint64_t probe_flops; /* 2 * nq * padded_dim * nlist */
     uint64_t pass_produced[3]; /* cumulative candidates after the seed, far, recovery passes */
     uint64_t seeded_queries;   /* queries given a GPU seed threshold */
+    uint64_t prefilter_dropped; /* candidates the GPU refined pre-filter dropped */
 } cora_hybrid_stats;
 
 int cora_hybrid_create(cora_hybrid **out, int device);                 /* HybridIndex() */

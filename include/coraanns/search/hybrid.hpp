@@ -95,6 +95,11 @@ class HybridIndex {
     // thresholds only). Off: only the CPU tightens thresholds, as in the reference. Set
     // before load_from_raw_pointers to skip the HBM copy.
     void set_gpu_seed_refine(bool enabled) { gpu_seed_refine_ = enabled; }
+    // GPU refined pre-filter (default on; uses the same HBM ex-codes): the far and
+    // recovery passes drop candidates whose refined distance already exceeds their
+    // threshold by more than a rounding bound, which the CPU would discard.
+    void set_gpu_refine_filter(bool enabled) { gpu_refine_filter_ = enabled; }
+    bool get_gpu_refine_filter() const { return gpu_refine_filter_; }
     // Extra cora_search_flags ORed into every launch (test modes such as
     // CORA_FLAG_GPU_SEED_FROZEN).
     void set_extra_search_flags(uint32_t flags) { extra_flags_ = flags; }
@@ -111,6 +116,7 @@ class HybridIndex {
     // cumulative candidates after the vanguard seed, far-pair and recovery passes
     uint64_t get_last_pass_produced(int pass) const { return last_pass_produced_[pass]; }
     uint64_t get_last_seeded_queries() const { return last_seeded_queries_; }
+    uint64_t get_last_prefilter_dropped() const { return last_prefilter_dropped_; }
     cora_gpu_engine *gpu_engine() const { return engine_; }
 
   private:
@@ -139,6 +145,7 @@ class HybridIndex {
     bool cpu_secondary_filter_enabled_ = true;
     bool frozen_thresholds_ = false;
     bool gpu_seed_refine_ = true;
+    bool gpu_refine_filter_ = true;
     uint32_t extra_flags_ = 0;
     int cpu_threads_ = 0;
     std::size_t vanguard_size_ = default_vanguard_size;
@@ -156,6 +163,7 @@ class HybridIndex {
     uint64_t last_probe_flops_ = 0;
     uint64_t last_pass_produced_[3] = {0, 0, 0};
     uint64_t last_seeded_queries_ = 0;
+    uint64_t last_prefilter_dropped_ = 0;
 };
 
 }  // namespace coraanns

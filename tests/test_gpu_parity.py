@@ -327,18 +327,20 @@ def test_live_thresholds_match_frozen_results(synth, gpu_seed):
     assert same >= 0.99, same
 
 
-def test_gpu_seed_thresholds_frozen_parity(synth):
-    """GPU seed refinement in its deterministic test mode (frozen snapshot lowered by the
+@pytest.mark.parametrize("prefilter", [False, True])
+def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
+    """GPU ex-code stages in their deterministic test mode (frozen snapshot lowered by the
     seed thresholds): seed choice and refined seed distances vs the oracle, the seeded
     threshold vs the oracle's rule and its safety, the candidate count of the far and
-    recovery passes against it, and an unchanged final top-k."""
+    recovery passes against it (with the refined pre-filter: low below the threshold and
+    refined distance within the rounding bound of it), and an unchanged final top-k."""
     nprobe, topk, van = 8, 10, 3
     keep = max(topk, 20)
-    say("[gpu] GPU seed thresholds, frozen parity")
+    say(f"[gpu] GPU seed thresholds, frozen parity, prefilter={prefilter}")
     case = synth
     nq, P = case.queries.shape[0], case.file.padded_dim
     eng = make_engine(case, nprobe, topk, vanguard=van, frozen=True,
-                      extra_flags=ca.FLAG_GPU_SEED_FROZEN)
+                      extra_flags=ca.FLAG_GPU_SEED_FROZEN, gpu_refine_filter=prefilter)
     eng.reset_buffer(case.queries)
     d, i = eng.search(case.queries, topk, nprobe)
     st = eng.stats()
@@ -401,20 +403,31 @@ def test_gpu_seed_thresholds_frozen_parity(synth):
                 mask[idx] = False
                 lo_cnt += idx.size
                 hi_cnt += idx.size
-            lo_cnt += int((low[mask] < thr[q] - band).sum())
-            hi_cnt += int((low[mask] < thr[q] + band).sum())
-            keep_local = np.nonzero(~mask | (low < thr[q] - band))[0]
-            gids = s + keep_local
-            ipi = orc.ip_int_direct(sd.bits[gids], qint[q])
-            ipr = orc.ip_int_direct(sd.bits[gids], qres[q])
-            ex2 = orc.exact_ip_two_stage(ipi, ipr, g["width"][q], g["width2"][q])
-            rd = orc.refine_dist(sd.ex_factors[gids, 0], sd.ex_factors[gids, 1], g["gadd"][q, p], ex2,
-                                 orc.excode_ip(g["qr"][q], sd.long_codes[gids], P), g["kb"][q], 7)
-            items += list(zip(rd.tolist(), sd.ids[gids].tolist()))
+            # refined distance and rounding bound of every vector of the pair
+            gall = s + np.arange(low.size)
+            ipa = orc.ip_int_direct(sd.bits[gall], qint[q])
+            ipra = orc.ip_int_direct(sd.bits[gall], qres[q])
+            exa = orc.exact_ip_two_stage(ipa, ipra, g["width"][q], g["width2"][q])
+            fa, fr = sd.ex_factors[gall, 0], sd.ex_factors[gall, 1]
+            rda = orc.refine_dist(fa, fr, g["gadd"][q, p], exa,
+                                  orc.excode_ip(g["qr"][q], sd.long_codes[gall], P), g["kb"][q], 7)
+            erra = orc.refine_error_bound(fa, fr, g["gadd"][q, p], exa, l1, g["kb"][q], 7)
+            lo_ok = low < thr[q] - band
+            hi_ok = low < thr[q] + band
+            if prefilter:
+                lo_ok &= rda <= thr[q] + 0.9 * erra
+                hi_ok &= rda <= thr[q] + 1.1 * erra
+            lo_cnt += int((mask & lo_ok).sum())
+            hi_cnt += int((mask & hi_ok).sum())
+            # top-k over the seeds and the vectors with low below the threshold: the
+            # pre-filter only drops refined distances above the threshold
+            sel = np.nonzero(~mask | (low < thr[q] - band))[0]
+            items += list(zip(rda[sel].tolist(), sd.ids[gall[sel]].tolist()))
         items.sort()
         for r, (dv, pid) in enumerate(items[:topk]):
             od[q, r], oi[q, r] = dv, pid
     assert lo_cnt <= st["submitted"] <= hi_cnt, (lo_cnt, st["submitted"], hi_cnt)
+    assert (st["prefilter_dropped"] > 0) == prefilter
     assert_topk_equal(d, i, od, oi)
     # against the exhaustive search: seeding pruned, and only rare RaBitQ lower-bound
     # misses (low above the refined distance) differ

@@ -44,6 +44,10 @@ class AllPass:
         self.expected = np.sort(order[:k]).astype(np.uint32)
 
     def engine(self, capacity, spill, vanguard, **kw):
+        # the reference's ring scenarios: every candidate reaches the CPU, so the GPU
+        # ex-code stages (seed thresholds, refined pre-filter) are off unless asked for
+        kw.setdefault("gpu_seed_refine", False)
+        kw.setdefault("gpu_refine_filter", False)
         e = ca.HybridIndex(0, queue_capacity=capacity, queue_spill_capacity=spill,
                            vanguard_size=vanguard, candidate_stats=True, **kw)
         e.load_from_raw_pointers(self.count, self.dim, self.padded, self.clusters, 7, self.centroids,
@@ -52,7 +56,7 @@ class AllPass:
         e.prepare_workspace(self.queries, self.k, self.clusters)
         return e
 
-    def check(self, e, chunk, batch_q=4, expect_all_consumed=False):
+    def check(self, e, chunk, batch_q=4, expect_all_consumed=False, expect_all_published=True):
         ids = np.zeros((self.queries, self.k), np.uint32)
         dists = np.zeros((self.queries, self.k), np.float32)
         for b in range(0, self.queries, chunk):
@@ -60,7 +64,10 @@ class AllPass:
             e.reset_buffer(q)
             d, i = e.search(q, self.k, self.clusters, batch_q)
             st = e.stats()
-            assert st["submitted"] == q.shape[0] * self.count, "dropped or duplicated candidates"
+            if expect_all_published:
+                assert st["submitted"] == q.shape[0] * self.count, "dropped or duplicated candidates"
+            else:
+                assert st["submitted"] <= q.shape[0] * self.count, "duplicated candidates"
             if expect_all_consumed:
                 assert st["refined"] == q.shape[0] * self.count
             ids[b:b + chunk], dists[b:b + chunk] = i, d
@@ -90,6 +97,19 @@ def test_all_pass_wraps_threads_secondary_chunks(allpass, capacity, vanguard):
                 if capacity > allpass.queries * allpass.count:
                     assert e.stats()["spilled"] == 0
                 allpass.check(e, 2, 4, not secondary)
+
+
+@pytest.mark.parametrize("capacity", [8192, 262144])
+def test_all_pass_with_gpu_excode_stages(allpass, capacity):
+    """The same scenarios with the GPU seed thresholds and refined pre-filter on: fewer
+    candidates reach the CPU, the top-k and its distances are unchanged."""
+    say(f"[gpu] all-pass with GPU ex-code stages, capacity={capacity}")
+    for threads in (1, 16):
+        e = allpass.engine(capacity, 262144, 5, gpu_seed_refine=True, gpu_refine_filter=True,
+                           cpu_threads=threads)
+        allpass.check(e, allpass.queries, 4, False, False)
+        assert e.stats()["submitted"] < allpass.queries * allpass.count
+        allpass.check(e, 2, 4, False, False)
 
 
 def test_forced_spill_and_refill():
