@@ -97,6 +97,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--n", type=int, default=0, help="override base size (testing only)")
     ap.add_argument("--nq", type=int, default=0, help="override query count (testing only)")
+    ap.add_argument("--no-gpu-seed", action="store_true",
+                    help="CPU-only thresholds (the reference's behaviour), no GPU seed thresholds")
+    ap.add_argument("--no-gpu-prefilter", action="store_true", help="no GPU refined pre-filter")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (PMC byte-count calibration)")
     args = ap.parse_args()
@@ -128,7 +131,8 @@ def main():
     ivf = ca.IvfIndex(index_path)
     eng = ca.HybridIndex(0, vanguard_size=c.vanguard, cpu_secondary_filter=c.secondary_filter,
                          cross_query_reuse=True, gpu_filter_timing=True, metric=c.metric,
-                         cpu_threads=threads)
+                         cpu_threads=threads, gpu_seed_refine=not args.no_gpu_seed,
+                         gpu_refine_filter=not args.no_gpu_prefilter)
     eng.load_ivf(ivf)
     chunk = min(queries.shape[0], 65535)
     eng.prepare_workspace(chunk, c.topk, max(c.nprobes))
@@ -153,13 +157,15 @@ def main():
         r = recall_at_k(ids, gt, c.topk)
         sweep.append({"nprobe": nprobe, "qps": round(queries.shape[0] / dt, 1), "recall": round(r, 4),
                       "candidates_per_query": round(st["submitted"] / queries.shape[0], 1),
-                      "scan_ms": round(st["scan_ms"], 3), "filter_ms": round(st["gpu_filter_ms"], 3)})
+                      "seed_ms": round(st["seed_ms"], 3), "scan_ms": round(st["scan_ms"], 3),
+                      "recovery_ms": round(st["recovery_ms"], 3), "filter_ms": round(st["gpu_filter_ms"], 3)})
         pp = st["pass_produced"]
         log(f"[sweep] nprobe={nprobe} QPS={queries.shape[0] / dt:.1f} recall={r:.4f} "
             f"cand/q={st['submitted'] / queries.shape[0]:.1f} (seed {pp[0] / queries.shape[0]:.1f}, "
             f"far {(pp[1] - pp[0]) / queries.shape[0]:.1f}, recovery {(pp[2] - pp[1]) / queries.shape[0]:.1f}; "
             f"gpu-seeded queries {st['seeded_queries']}, pre-filter dropped "
-            f"{st['prefilter_dropped'] / queries.shape[0]:.1f}) scan={st['scan_ms']:.3f}ms filter={st['gpu_filter_ms']:.3f}ms")
+            f"{st['prefilter_dropped'] / queries.shape[0]:.1f}) seed={st['seed_ms']:.3f}ms far={st['scan_ms']:.3f}ms "
+            f"recovery={st['recovery_ms']:.3f}ms filter={st['gpu_filter_ms']:.3f}ms")
     nprobe = args.nprobe
     if not nprobe:
         ok = [s["nprobe"] for s in sweep if s["recall"] >= args.recall_target]
@@ -210,6 +216,7 @@ def main():
                    "qps_with_upload": round(queries.shape[0] * args.steps / sum(times_up), 1),
                    "batch_q": batch_q, "vanguard": c.vanguard, "cpu_secondary_filter": c.secondary_filter,
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
+                   "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
                    "query_chunk": chunk, "sweep": sweep},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,

@@ -78,7 +78,7 @@ class cora_search_stats(C.Structure):
                 ("scan_bytes", C.c_uint64), ("scan_units", C.c_uint64),
                 ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float), ("probe_flops", C.c_uint64),
                 ("pass_produced", C.c_uint64 * 3), ("seeded_queries", C.c_uint64),
-                ("prefilter_dropped", C.c_uint64)]
+                ("prefilter_dropped", C.c_uint64), ("seed_ms", C.c_float), ("recovery_ms", C.c_float)]
 
 
 class cora_queue_view(C.Structure):
@@ -100,7 +100,8 @@ class cora_hybrid_stats(C.Structure):
                 ("gpu_filter_ms", C.c_float), ("scan_ms", C.c_float), ("scan_bytes", C.c_uint64),
                 ("scan_units", C.c_uint64), ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float),
                 ("probe_flops", C.c_uint64), ("pass_produced", C.c_uint64 * 3),
-                ("seeded_queries", C.c_uint64), ("prefilter_dropped", C.c_uint64)]
+                ("seeded_queries", C.c_uint64), ("prefilter_dropped", C.c_uint64),
+                ("seed_ms", C.c_float), ("recovery_ms", C.c_float)]
 
 
 class cora_ivf_info(C.Structure):

@@ -65,9 +65,9 @@ struct cora_gpu_engine {
              *d_uoff = nullptr, *d_nunits = nullptr, *d_cursor = nullptr, *d_seed = nullptr;
     int32_t *d_pidx = nullptr;
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
-    float *d_van_low = nullptr;
-    int32_t *d_van_ip = nullptr;
-    uint32_t van_blocks = 0;
+    uint4 *d_seed_rec = nullptr;
+    float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
+    uint64_t van_stride = 0;
     Pair *d_pairs = nullptr;
     Unit *d_units = nullptr;
     unsigned long long *d_stats = nullptr;
@@ -136,8 +136,8 @@ ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool f
     p.units = E->d_units;
     p.num_units = E->d_nunits;
     p.unit_cursor = E->d_cursor;
-    p.thresholds = frozen ? E->d_thr_snap : E->h_thr;
-    p.thresholds_live = frozen ? 0 : 1;
+    // frozen: the launch snapshot; live: a copy of the host thresholds taken before each pass
+    p.thresholds = E->d_thr_snap;
     p.nprobe = E->last.nprobe;
     p.vanguard = depth;
     p.keep = keep;
@@ -146,10 +146,12 @@ ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool f
     p.seed_words = (uint32_t)E->seed_words;
     p.seed_bits = E->d_seed;
     p.queue = queue_dev(E);
-    p.van_low = E->d_van_low;
-    p.van_ip = E->d_van_ip;
-    p.van_stride = (uint32_t)E->max_cluster;
-    p.van_blocks = E->van_blocks;
+    p.van_lows = E->d_van_lows;
+    p.van_stride = (uint32_t)E->van_stride;
+    uint32_t buf = 128;  // seed pass buffer: power of two >= keep + one tile
+    while (buf < keep + kTileVectors)
+        buf <<= 1;
+    p.seed_buf = buf;
     return p;
 }
 
@@ -186,9 +188,9 @@ void release_workspace(cora_gpu_engine *E) {
     dfree(E->d_seed_dist);
     dfree(E->d_seed_low);
     dfree(E->d_seed_err);
-    dfree(E->d_van_low);
-    dfree(E->d_van_ip);
-    E->van_blocks = 0;
+    dfree(E->d_seed_rec);
+    dfree(E->d_van_lows);
+    E->van_stride = 0;
     dfree(E->d_pairs);
     dfree(E->d_units);
     dfree(E->d_stats);
@@ -499,19 +501,19 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_cursor, kNumXcd));
         TRY(dalloc(E, E->d_stats, 8));
         TRY(dalloc(E, E->d_pairs, np));
-        TRY(dalloc(E, E->d_units, np));
+        TRY(dalloc(E, E->d_units, np * unit_splits((uint32_t)E->max_cluster)));
         TRY(dalloc(E, E->d_thr_snap, max_q));
         TRY(dalloc(E, E->d_seed, std::max<uint64_t>(1, max_q * depth * seed_words)));
-        if (depth > 0 && E->max_cluster > (uint64_t)kVanguardMaxCluster) {
-            E->van_blocks = vanguard_seed_grid(E->W);
-            TRY(dalloc(E, E->d_van_low, (uint64_t)E->van_blocks * E->max_cluster));
-            TRY(dalloc(E, E->d_van_ip, (uint64_t)E->van_blocks * E->max_cluster));
+        if (depth > 0) {
+            E->van_stride = (E->max_cluster + kTileVectors - 1) / kTileVectors * kTileVectors;
+            TRY(dalloc(E, E->d_van_lows, max_q * depth * std::max<uint64_t>(E->van_stride, 1)));
         }
         if (E->d_excodes) {
             const uint64_t slots = max_q * depth * std::max<uint64_t>(max_topk, 20);
             TRY(dalloc(E, E->d_seed_dist, slots));
             TRY(dalloc(E, E->d_seed_low, slots));
             TRY(dalloc(E, E->d_seed_err, slots));
+            TRY(dalloc(E, E->d_seed_rec, slots));
         }
         TRY(halloc(E, E->h_qrot, max_q * E->P, hipHostMallocDefault));
         TRY(halloc(E, E->h_kb, max_q, hipHostMallocDefault));
@@ -658,7 +660,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // pair scheduling (hybrid.cu:504-508)
     launch_build_pairs(E->d_pidx, E->d_meta, nq, np, (uint32_t)E->nl, depth, batch,
                        P / 8 + 12, E->d_bcount, E->d_bcursor, E->d_boff, E->d_uoff, E->d_pairs,
-                       E->d_units, E->d_nunits, E->d_stats, s);
+                       E->d_units, (uint64_t)nq * np * unit_splits((uint32_t)E->max_cluster),
+                       E->d_nunits, E->d_stats, s);
     if (frozen) {
         memcpy(E->h_thr_stage, E->h_thr, (size_t)nq * 4);
         HIPCHK(hipMemcpyAsync(E->d_thr_snap, E->h_thr_stage, (size_t)nq * 4, hipMemcpyHostToDevice, s));
@@ -680,25 +683,34 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         p.seed_dist = E->d_seed_dist;
         p.seed_low = E->d_seed_low;
         p.seed_err = E->d_seed_err;
+        p.seed_rec = E->d_seed_rec;
     }
     p.prefilter = prefilter ? 1 : 0;
     p.dropped = E->d_stats + 7;
     launch_fill_u64(E->d_stats + 3, 0ull, 5, s);  // per-pass counters of this launch
     if (timing)
         HIPCHK(hipEventRecord(E->ev_f0, s));
+    // live thresholds: each pass reads a copy of the host array taken just before it
+    auto snapshot = [&]() {
+        if (!frozen)
+            launch_snapshot_thresholds(E->h_thr, E->d_thr_snap, nq, s);
+    };
     if (depth > 0) {
         launch_fill_u32(E->d_seed, 0u, (size_t)nq * depth * E->seed_words, s);
+        snapshot();
         if (gpu_seed)  // +inf marks seed slots the seed pass leaves unused
             launch_fill_u32(reinterpret_cast<uint32_t *>(E->d_seed_dist), 0x7F800000u,
                             (size_t)nq * depth * keep, s);
         launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
         launch_vanguard_seed(p, E->W, s);
         if (gpu_seed)
-            launch_seed_thresholds(E->d_seed_dist, E->d_seed_low, E->d_seed_err, nq, depth * keep,
-                                   a->topk, frozen ? E->d_thr_snap : E->h_thr, E->d_stats + 6, s);
+            launch_seed_thresholds(E->d_seed_dist, E->d_seed_low, E->d_seed_err, E->d_seed_rec, nq,
+                                   depth * keep, a->topk, frozen ? E->d_thr_snap : E->h_thr,
+                                   E->d_stats + 6, queue_dev(E), s);
     }
     launch_copy_u64(E->d_produced, E->d_stats + 3, s);
     launch_cursor_init(E->d_cursor, E->d_nunits, 1, s);
+    snapshot();
     if (timing)
         HIPCHK(hipEventRecord(E->ev_s0, s));
     launch_scan(p, E->W, batch, 0, s);
@@ -707,6 +719,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     launch_copy_u64(E->d_produced, E->d_stats + 4, s);
     if (depth > 0) {
         launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
+        snapshot();
         launch_scan(p, E->W, 1, 1, s);
     }
     launch_copy_u64(E->d_produced, E->d_stats + 5, s);
@@ -765,6 +778,8 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
         HIPCHK(hipEventElapsedTime(&out.filter_ms, E->ev_f0, E->ev_f1));
         HIPCHK(hipEventElapsedTime(&out.scan_ms, E->ev_s0, E->ev_s1));
         HIPCHK(hipEventElapsedTime(&out.probe_ms, E->ev_p0, E->ev_p1));
+        HIPCHK(hipEventElapsedTime(&out.seed_ms, E->ev_f0, E->ev_s0));
+        HIPCHK(hipEventElapsedTime(&out.recovery_ms, E->ev_s1, E->ev_f1));
     }
     if (st)
         *st = out;

@@ -20,7 +20,6 @@ constexpr int kTileVectors = 64;
 constexpr int kBq = 8;             // query quantisation bits (reference RABITQ_BQ)
 constexpr int kMaxBatchQ = 8;      // same-cluster pairs per scan pass
 constexpr int kMaxVanguardKeep = 1024;
-constexpr int kVanguardMaxCluster = 8192;  // LDS-resident lows in the vanguard seed pass
 constexpr int kSelectMaxProbe = 4096;       // top-nprobe select held in LDS
 constexpr uint32_t kNumXcd = 8;
 
@@ -31,12 +30,25 @@ struct ClusterMeta {
     uint32_t pad;
 };
 
-// One cluster pass of the scan: up to batch_q pairs that probe the same cluster.
+// Tiles one scan unit covers at most (8,192 vectors): a pass over a very large cluster
+// is cut into several units so no wave walks it alone. Each unit costs a chain of
+// dependent metadata loads before its first tile, so smaller units lose more than
+// they balance (16-tile units measured 1.6x slower on a skewed 1M-vector index).
+constexpr uint32_t kUnitTiles = 128;
+
+// Units a cluster of n vectors is cut into.
+__host__ __device__ inline uint32_t unit_splits(uint32_t n) {
+    const uint32_t tiles = (n + kTileVectors - 1) / kTileVectors;
+    return tiles ? (tiles + kUnitTiles - 1) / kUnitTiles : 1u;
+}
+
+// One scan unit: up to batch_q pairs that probe the same cluster, over the tile range
+// [tiles >> 8, (tiles >> 8) + (tiles & 255)) of that cluster.
 struct Unit {
     uint32_t cluster;
     uint32_t pair_begin;
     uint32_t count;
-    uint32_t bucket;
+    uint32_t tiles;
 };
 
 // Scheduled (query, probe) pair: word0 = probe << 16 | query (the Candidate's first
@@ -91,8 +103,8 @@ struct ScanParams {
     const Unit *units;
     const uint32_t *num_units;   // device scalar
     uint32_t *unit_cursor;       // [kNumXcd] dynamic scheduling cursors
-    const float *thresholds;     // live host-coherent array or a device snapshot
-    int thresholds_live;
+    const float *thresholds;     // device copy of the thresholds (snapshot per pass, or the
+                                 // launch snapshot in frozen mode)
     uint32_t nprobe;
     uint32_t vanguard;
     uint32_t keep;               // vanguard seed count per pair
@@ -113,12 +125,12 @@ struct ScanParams {
     float *seed_dist;            // [nq][vanguard][keep], +inf when unused
     float *seed_low;
     float *seed_err;
-    // HBM scratch of the seed pass for clusters larger than its LDS window:
-    // [van_blocks][van_stride] lower bounds and ip_int, one slice per workgroup
-    float *van_low;
-    int *van_ip;
+    uint4 *seed_rec;             // the seeds' Candidate records, published after the threshold
+    // lower bounds of every vector of every vanguard pair, written by the seed pass and
+    // read by the recovery pass: [nq][vanguard][van_stride]
+    float *van_lows;
     uint32_t van_stride;
-    uint32_t van_blocks;
+    uint32_t seed_buf;           // seed pass LDS buffer entries (power of two >= keep + 64)
     // refined pre-filter of the far and recovery passes (needs ex_codes)
     int prefilter;
     unsigned long long *dropped;  // records the pre-filter dropped
@@ -146,11 +158,12 @@ void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,
                          uint32_t nprobe, uint32_t P, int metric, float *gadd, float *gerr,
                          hipStream_t s);
+// max_units: capacity of units (nq * nprobe * unit_splits(largest cluster))
 void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint32_t nq,
                         uint32_t nprobe, uint32_t nlist, uint32_t vanguard, uint32_t batch_q,
                         uint32_t bytes_per_vector, uint32_t *bucket_count, uint32_t *bucket_cursor,
                         uint32_t *bucket_offset, uint32_t *unit_offset, Pair *pairs, Unit *units,
-                        uint32_t *num_units /*[2]: vanguard, far*/,
+                        uint64_t max_units, uint32_t *num_units /*[2]: vanguard, far*/,
                         unsigned long long *scan_stats /*[3]*/, hipStream_t s);
 void launch_fill_u32(uint32_t *p, uint32_t value, size_t n, hipStream_t s);
 void launch_fill_u64(unsigned long long *p, unsigned long long value, size_t n, hipStream_t s);
@@ -162,14 +175,16 @@ int launch_scan(const ScanParams &p, uint32_t W, uint32_t batch_q, int kind, hip
 // dense debug pass over one unit set (0 = vanguard units, 1 = far units)
 int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t set, hipStream_t s);
 int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s);
-// workgroups the seed pass launches (its persistent grid), for sizing van_low / van_ip
-uint32_t vanguard_seed_grid(uint32_t W);
 // Per query: the topk-th smallest refined seed distance, raised by the largest rounding
 // bound and above the lower bounds of the seeds at or below it, lowers the query's
 // threshold (see scan.hip). count = vanguard * keep seed slots per query.
 void launch_seed_thresholds(const float *seed_dist, const float *seed_low, const float *seed_err,
-                            uint32_t nq, uint32_t count, uint32_t topk, float *thresholds,
-                            unsigned long long *seeded, hipStream_t s);
+                            const uint4 *seed_rec, uint32_t nq, uint32_t count, uint32_t topk,
+                            float *thresholds, unsigned long long *seeded, QueueDev q,
+                            hipStream_t s);
+// dev[0..n) = the host-coherent thresholds, read with system scope (the per-pass copy the
+// scan kernels read, so no unit waits on a host-memory round trip)
+void launch_snapshot_thresholds(const float *host, float *dev, uint32_t n, hipStream_t s);
 // *dst = *src in stream order (per-pass snapshots of the ring position counter)
 void launch_copy_u64(const unsigned long long *src, unsigned long long *dst, hipStream_t s);
 // max_ticks: drain wait limit in ticks of the device wall clock (wall_clock64)

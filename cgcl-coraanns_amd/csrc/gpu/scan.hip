@@ -36,8 +36,9 @@
 // has released that slot.
 #include <float.h>
 
+#include <map>
 #include <mutex>
-#include <unordered_map>
+#include <utility>
 
 #include "engine_internal.h"
 
@@ -295,10 +296,7 @@ __device__ __forceinline__ void flush_stage(const ScanParams &p, const QueueDev 
     __syncthreads();  // the stage may be refilled
 }
 
-__device__ __forceinline__ float read_threshold(const float *thresholds, int live, uint32_t query) {
-    if (live)
-        return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t *>(thresholds) + query,
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM));
+__device__ __forceinline__ float read_threshold(const float *thresholds, uint32_t query) {
     return thresholds[query];
 }
 
@@ -351,7 +349,6 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
     const Pair *__restrict__ pairs = p.pairs;
     const Unit *__restrict__ units = p.units;
     const float *thresholds = p.thresholds;
-    const int live = p.thresholds_live;
     const uint32_t nprobe = p.nprobe, tile_bytes = p.tile_bytes;
     const uint32_t *seed_bits = p.seed_bits;
     const uint32_t seed_words = p.seed_words, vanguard = p.vanguard;
@@ -373,7 +370,8 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
         const uint32_t pair_begin = uniform(un.pair_begin);
         const ClusterMeta cm = meta[cluster];
         const uint32_t n = uniform(cm.n), start = uniform(cm.start), tbase = uniform(cm.tile_base);
-        if (n == 0)
+        const uint32_t t_begin = uniform(un.tiles) >> 8, t_end = t_begin + (uniform(un.tiles) & 255u);
+        if (n == 0 || t_begin >= t_end)
             continue;  // an empty cluster owns no tile (its tile_base may be one past the end)
 
         uint32_t word0[QMAX];
@@ -389,7 +387,7 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
                 probe0 = probe;
             }
             word0[j] = w0;
-            cutoff[j] = KIND == kDense ? FLT_MAX : uniformf(read_threshold(thresholds, live, query));
+            cutoff[j] = KIND == kDense ? FLT_MAX : uniformf(read_threshold(thresholds, query));
             width[j] = uniformf(qwidth[query]);
             k1[j] = uniformf(qk1[query]);
             const size_t pi = (size_t)query * nprobe + probe;
@@ -418,21 +416,71 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
         const uint32_t *seeds = nullptr;
         if (KIND == kRecovery)
             seeds = seed_bits + ((size_t)query0 * vanguard + probe0) * seed_words;
-        const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
+        if constexpr (KIND == kRecovery) {
+            // lower bounds stored by the seed pass; code words are loaded only for the tiles
+            // holding a survivor (a non-seed below the current threshold)
+            const float *lows = p.van_lows + ((size_t)query0 * vanguard + probe0) * p.van_stride;
+            constexpr uint32_t kAhead = 4;  // tiles whose lower bounds are loaded together
+            float lb[kAhead];
+            for (uint32_t t = t_begin; t < t_end; ++t) {
+                const uint32_t r = (t - t_begin) % kAhead;
+                if (r == 0) {
+#pragma unroll
+                    for (uint32_t i = 0; i < kAhead; ++i) {
+                        const uint32_t li = (t + i) * kTileVectors + lane;
+                        lb[i] = t + i < t_end && li < n ? lows[li] : 0.0f;
+                    }
+                }
+                const uint32_t local = t * kTileVectors + lane;
+                const bool valid = local < n;
+                float low = lb[0];
+#pragma unroll
+                for (uint32_t i = 1; i < kAhead; ++i)
+                    low = r == i ? lb[i] : low;
+                const bool survive =
+                    valid && low < cutoff[0] && !((seeds[local >> 5] >> (local & 31)) & 1u);
+                const unsigned long long mask = __ballot(survive);
+                if (mask == 0)
+                    continue;
+                uint32_t xr[K];
+                load_codes<W>(tiles + (size_t)(tbase + t) * tile_bytes, lane, rw, xr);
+                int ip;
+                if constexpr (kRegs)
+                    ip = popc_ip<W>(xr, preg, rw);
+                else
+                    ip = popc_ip<W>(xr, s_planes, rw);
+                const uint32_t cnt = (uint32_t)__popcll(mask);
+                if (staged + cnt > (uint32_t)CAP) {
+                    flush_stage<W>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
+                    staged = 0;
+                }
+                if (survive) {
+                    const uint32_t k = staged + lane_rank(mask);
+                    s_rec[k] = make_uint4(word0[0], start + local, (uint32_t)ip, __float_as_uint(low));
+                    s_cut[k] = cutoff[0];
+#pragma unroll
+                    for (int w = 0; w < K; ++w)
+                        if ((uint32_t)w < nw)
+                            s_code[w * CAP + k] = xr[w];
+                }
+                staged += cnt;
+            }
+            continue;
+        }
         // tile t is evaluated while tile t+1 (or t again at the end) is being loaded
         uint32_t x[K], xn[K];
         float fa, fr, fe, fan, frn, fen;
         {
-            const uint8_t *tile = tiles + (size_t)tbase * tile_bytes;
+            const uint8_t *tile = tiles + (size_t)(tbase + t_begin) * tile_bytes;
             load_codes<W>(tile, lane, rw, x);
             const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
             fa = fac[lane];
             fr = fac[64 + lane];
             fe = fac[128 + lane];
         }
-        for (uint32_t t = 0; t < ntiles; ++t) {
+        for (uint32_t t = t_begin; t < t_end; ++t) {
             {
-                const uint32_t tn = t + 1 < ntiles ? t + 1 : t;
+                const uint32_t tn = t + 1 < t_end ? t + 1 : t;
                 const uint8_t *tile = tiles + (size_t)(tbase + tn) * tile_bytes;
                 load_codes<W>(tile, lane, rw, xn);
                 const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
@@ -510,278 +558,241 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
 // vectors against the thresholds the CPU has tightened meanwhile. Selection: radix
 // select of the keep-th smallest key, all smaller keys plus the lowest-index ties.
 // ---------------------------------------------------------------------------------
-constexpr int kVanThreads = 256;
-
 __device__ __forceinline__ uint32_t order_key(float f) {
     const uint32_t u = __float_as_uint(f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Inclusive prefix sum of v over the workgroup's 256 threads (wave shuffles, then one
-// exchange of the four wave totals); total receives the sum over all threads.
-__device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t *s_wave, uint32_t &total) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = __shfl_up(x, o, 64);
-        if (lane >= (uint32_t)o)
-            x += y;
-    }
-    if (lane == 63)
-        s_wave[wave] = x;
-    __syncthreads();
-    uint32_t off = 0, tot = 0;
-#pragma unroll
-    for (int w = 0; w < kVanThreads / 64; ++w) {
-        const uint32_t sw = s_wave[w];
-        off += (uint32_t)w < wave ? sw : 0u;
-        tot += sw;
-    }
-    __syncthreads();  // s_wave may be reused
-    total = tot;
-    return x + off;
+__device__ __forceinline__ float key_to_float(uint32_t key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
 }
 
-struct SeedShared {
-    uint32_t hist[256];
-    uint32_t wave_sum[kVanThreads / 64];
-    uint32_t sel[kMaxVanguardKeep];
-    float exk[kMaxVanguardKeep];
-    uint32_t unit, digit, remaining, range, tries;
-    unsigned long long base, limit;
-};
-
-// One vanguard pair: lower bounds of the cluster into lows / ips (LDS for clusters of up
-// to kVanguardMaxCluster vectors, this workgroup's HBM scratch slice for larger ones),
-// radix select of the `keep` smallest below the threshold (8-bit digits, digit found by
-// a parallel scan of the histogram), publication with one reservation, the seed bitmask
-// and, with HBM ex-codes, the GPU refinement of the seeds. Called by all 256 threads.
-template <int W>
-__device__ __forceinline__ void seed_pair(const ScanParams &p, SeedShared &sh, float *lows,
-                                          int *ips, const Unit &un) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t rw = p.P / 32;
-    const QueueDev q = p.queue;
-    const ClusterMeta cm = p.meta[un.cluster];
-    const uint32_t n = cm.n;
-    const uint32_t w0 = p.pairs[un.pair_begin].word0;
-    const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
-    const float width = p.qwidth[query], k1 = p.k1[query];
-    const size_t pi = (size_t)query * p.nprobe + probe;
-    const float gadd = p.pgadd[pi], gerr = p.pgerr[pi];
-    const float cutoff = read_threshold(p.thresholds, p.thresholds_live, query);
-    const uint32_t *planes = p.qplanes + (size_t)query * 2 * kBq * rw;
-    const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
-    uint32_t nv = 0;
-    for (uint32_t t = wave; t < ntiles; t += kVanThreads / 64) {
-        const uint8_t *tile = p.tiles + (size_t)(cm.tile_base + t) * p.tile_bytes;
-        uint32_t x[Words<W>::kMax];
-        load_codes<W>(tile, lane, rw, x);
-        const float *fac = reinterpret_cast<const float *>(tile + 256u * rw);
-        const uint32_t local = t * kTileVectors + lane;
-        if (local < n) {
-            const int ip = popc_ip<W>(x, planes, rw);
-            const float ex = width * (float)ip;
-            const float low = fac[lane] + gadd + fac[64 + lane] * (ex + k1) - fac[128 + lane] * gerr;
-            const bool ok = low < cutoff;
-            lows[local] = ok ? low : __uint_as_float(0x7FFFFFFFu);  // NaN: excluded, sorts last
-            ips[local] = ip;
-            nv += ok ? 1u : 0u;
-        }
-    }
-    uint32_t valid;
-    (void)block_scan(nv, sh.wave_sum, valid);  // its barrier also publishes the lows
-    const uint32_t take = min(p.keep, valid);
-    if (take == 0)
-        return;
-    // radix select of the take-th smallest key
-    uint32_t prefix = 0, pmask = 0, rem = take;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        sh.hist[tid] = 0;
-        __syncthreads();
-        for (uint32_t i = tid; i < n; i += kVanThreads) {
-            const uint32_t key = order_key(lows[i]);
-            if ((key & pmask) == prefix)
-                atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        const uint32_t h = sh.hist[tid];
-        uint32_t tot;
-        const uint32_t incl = block_scan(h, sh.wave_sum, tot);
-        if (incl - h < rem && rem <= incl) {  // exactly one digit holds the rem-th key
-            sh.digit = tid;
-            sh.remaining = rem - (incl - h);
-        }
-        __syncthreads();
-        prefix |= sh.digit << shift;
-        rem = sh.remaining;
-        pmask |= 255u << shift;
-    }
-    const uint32_t kth = prefix, take_eq = rem;
-    // deterministic gather in index order: a contiguous index chunk per thread, all keys
-    // below the take-th plus its lowest-index ties
-    const uint32_t chunk = (n + kVanThreads - 1) / kVanThreads;
-    const uint32_t b0 = min(n, tid * chunk), b1 = min(n, b0 + chunk);
-    uint32_t nless = 0, neq = 0;
-    for (uint32_t i = b0; i < b1; ++i) {
-        const uint32_t key = order_key(lows[i]);
-        nless += key < kth;
-        neq += key == kth;
-    }
-    uint32_t tot_less, tot_eq;
-    uint32_t lo = block_scan(nless, sh.wave_sum, tot_less) - nless;
-    uint32_t eq_rank = block_scan(neq, sh.wave_sum, tot_eq) - neq;
-    uint32_t *seed = p.seed_bits + ((size_t)query * p.vanguard + probe) * p.seed_words;
-    for (uint32_t i = b0; i < b1; ++i) {
-        const uint32_t key = order_key(lows[i]);
-        bool pick = false;
-        // tot_less + take_eq == take <= keep by the radix select; the guards keep the LDS
-        // writes inside sel[] whatever the keys
-        if (key < kth) {
-            if (lo < take) {
-                sh.sel[lo] = i;
-                pick = true;
-            }
-            ++lo;
-        } else if (key == kth) {
-            if (eq_rank < take_eq && tot_less + eq_rank < take) {
-                sh.sel[tot_less + eq_rank] = i;
-                pick = true;
-            }
-            ++eq_rank;
-        }
-        if (pick)
-            atomicOr(&seed[i >> 5], 1u << (i & 31));
-    }
-    // one reservation for the pair's seeds, then the residual pass per seed
-    if (tid == 0) {
-        const unsigned long long base = atomicAdd(q.produced, (unsigned long long)take);
-        unsigned long long lim = sh.limit;
-        if (base + take > lim)
-            lim = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released, q.capacity,
-                                base + take);
-        sh.base = base;
-        sh.limit = lim;
-    }
-    __syncthreads();
-    const unsigned long long base = sh.base, limit = sh.limit;
-    const float width2 = p.qwidth2[query];
-    for (uint32_t s = tid; s < take; s += kVanThreads) {
-        const uint32_t local = sh.sel[s];
-        const uint8_t *tile = p.tiles + (size_t)(cm.tile_base + local / kTileVectors) * p.tile_bytes;
-        uint32_t x[Words<W>::kMax];
-        load_codes<W>(tile, local % kTileVectors, rw, x);
-        const int ip_res = popc_ip<W>(x, planes + kBq * rw, rw);
-        const float ex = two_stage_ip(width, ips[local], width2, ip_res);
-        sh.exk[s] = ex;
-        place_record(q, base + s, limit,
-                     make_uint4(w0, cm.start + local, __float_as_uint(ex), __float_as_uint(lows[local])));
-    }
-    if (p.seed_dist) {
-        // Refined distance of every seed, 16 lanes per seed (cpu_refinement.cpp:183-192):
-        // f_add_ex + g_add + f_rescale_ex * (2^7 * exact_ip + <q', ex_code> + kbxSumq),
-        // with a bound on its rounding difference from the CPU's evaluation.
-        __syncthreads();
-        const uint32_t sub = tid & 15, chunks = p.P / 8;
-        const size_t lc = (size_t)p.P * 7 / 8;
-        const float *qv = p.qrot + (size_t)query * p.P;
-        const float kbq = p.kb[query];
-        for (uint32_t s = tid >> 4; s < take; s += kVanThreads / 16) {
-            const uint32_t local = sh.sel[s];
-            const size_t gid = (size_t)cm.start + local;
-            const uint8_t *code = p.ex_codes + gid * lc;
-            float ip = 0.0f, l1 = 0.0f;
-            for (uint32_t c = sub; c < chunks; c += 16)
-                ip += excode_chunk_ip(code, qv, c, l1);
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1) {
-                ip += __shfl_xor(ip, o, 16);
-                l1 += __shfl_xor(l1, o, 16);
-            }
-            if (sub == 0) {
-                const float fa = p.ex_factors[2 * gid], fr = p.ex_factors[2 * gid + 1];
-                const float ex = sh.exk[s];
-                const float dist = fa + gadd + fr * (128.0f * ex + ip + kbq);
-                const float mag = fabsf(fa) + fabsf(gadd) +
-                                  fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq));
-                const size_t o = ((size_t)query * p.vanguard + probe) * p.keep + s;
-                p.seed_dist[o] = dist;
-                p.seed_low[o] = lows[local];
-                p.seed_err[o] = 1e-4f * mag;
-            }
-        }
-    }
-}
-
-template <int W>
-__global__ __launch_bounds__(kVanThreads) void vanguard_seed_kernel(const ScanParams p) {
-    __shared__ float s_low[kVanguardMaxCluster];
-    __shared__ int s_ip[kVanguardMaxCluster];
-    __shared__ SeedShared sh;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t U = p.num_units[0];
-    const uint32_t per = (U + kNumXcd - 1) / kNumXcd;
-    if (tid == 0) {
-        sh.range = blockIdx.x % kNumXcd;
-        sh.tries = 0;
-        sh.limit = __hip_atomic_load(p.queue.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    for (;;) {
-        if (tid == 0) {
-            uint32_t u = U;
-            while (sh.tries < kNumXcd) {
-                const uint32_t v = atomicAdd(&p.unit_cursor[sh.range], 1u);
-                if (v < min(U, (sh.range + 1) * per)) {
-                    u = v;
-                    break;
+// Ascending bitonic sort of buf[0, cap) (cap a power of two) by the 64 lanes of a
+// one-wave workgroup; the barrier makes each step's LDS writes visible to all lanes.
+__device__ void wave_sort(unsigned long long *buf, uint32_t cap, uint32_t lane) {
+    for (uint32_t size = 2; size <= cap; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = lane; i < cap / 2; i += 64) {
+                const uint32_t a = (i / stride) * 2 * stride + (i % stride), b = a + stride;
+                const bool asc = (a & size) == 0;
+                const unsigned long long x = buf[a], y = buf[b];
+                if ((x > y) == asc) {
+                    buf[a] = y;
+                    buf[b] = x;
                 }
-                sh.range = (sh.range + 1) % kNumXcd;
-                ++sh.tries;
             }
-            sh.unit = u;
+            __syncthreads();
         }
-        __syncthreads();
-        const uint32_t u = sh.unit;
+    }
+}
+
+// Vanguard seed pass (reference computeInnerProducts1BitLutProducerVanguard,
+// filter_kernels.cuh:308-468): for each vanguard pair (probe rank < vanguard) publish the
+// `keep` vectors with the smallest lower bounds below the query's threshold (ties to
+// the lower index) and mark them in the pair's seed bitmask; the recovery pass later
+// publishes the remaining vectors against the thresholds tightened meanwhile.
+//
+// One wave per pair, streaming the cluster's tiles: candidates enter an LDS buffer as
+// keys order_key(low) << 32 | index while below the key of the current keep-th entry;
+// a full buffer is sorted (wave bitonic sort) and cut back to keep entries. Every lower
+// bound also goes to the pair's slice of the HBM lows buffer, which the recovery pass
+// reads instead of recomputing the estimator. With the HBM ex-codes, the seeds are then
+// refined on the GPU (16 lanes per seed) for the seed thresholds.
+template <int W>
+__global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
+    extern __shared__ unsigned long long s_buf[];  // [cap] keys, then [cap] f32 exact_ip
+    const uint32_t cap = p.seed_buf;
+    float *s_exk = reinterpret_cast<float *>(s_buf + cap);
+    const uint32_t lane = threadIdx.x;
+    const uint32_t rw = p.P / 32;
+    const uint32_t keep = p.keep;
+    const uint32_t U = p.num_units[0];
+    const QueueDev q = p.queue;
+    uint32_t range = blockIdx.x % kNumXcd, tries = 0;
+    unsigned long long limit =
+        __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+        const uint32_t u = next_unit(p.unit_cursor, U, range, tries, lane);
         if (u >= U)
             break;
         const Unit un = p.units[u];
-        const uint32_t n = p.meta[un.cluster].n;
-        if (p.keep > 0 && n > 0) {
-            if (n <= (uint32_t)kVanguardMaxCluster) {
-                seed_pair<W>(p, sh, s_low, s_ip, un);
-            } else if (p.van_low && blockIdx.x < p.van_blocks && n <= p.van_stride) {
-                const size_t off = (size_t)blockIdx.x * p.van_stride;
-                seed_pair<W>(p, sh, p.van_low + off, p.van_ip + off, un);
-            }
-            // otherwise no seeds: the recovery pass publishes the whole pair
+        if ((uniform(un.tiles) >> 8) != 0)
+            continue;  // a pair's seeds need its whole cluster: only its first unit seeds
+        const ClusterMeta cm = p.meta[uniform(un.cluster)];
+        const uint32_t n = uniform(cm.n), start = uniform(cm.start), tbase = uniform(cm.tile_base);
+        if (n == 0 || keep == 0)
+            continue;
+        const uint32_t w0 = uniform(p.pairs[uniform(un.pair_begin)].word0);
+        const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
+        const float width = uniformf(p.qwidth[query]), k1 = uniformf(p.k1[query]);
+        const size_t pi = (size_t)query * p.nprobe + probe;
+        const float gadd = uniformf(p.pgadd[pi]), gerr = uniformf(p.pgerr[pi]);
+        const float cutoff = uniformf(read_threshold(p.thresholds, query));
+        const uint32_t *planes = p.qplanes + (size_t)query * 2 * kBq * rw;
+        float *lows_out = p.van_lows ? p.van_lows + ((size_t)query * p.vanguard + probe) * p.van_stride
+                                     : nullptr;
+        const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
+        uint32_t count = 0;
+        unsigned long long bound = ~0ull;
+        // tile t is evaluated while tile t+1 (or t again at the end) is being loaded
+        uint32_t x[Words<W>::kMax], xn[Words<W>::kMax];
+        float fa, fr, fe, fan, frn, fen;
+        {
+            const uint8_t *tile = p.tiles + (size_t)tbase * p.tile_bytes;
+            load_codes<W>(tile, lane, rw, x);
+            const float *fac = reinterpret_cast<const float *>(tile + 256u * rw);
+            fa = fac[lane];
+            fr = fac[64 + lane];
+            fe = fac[128 + lane];
         }
+        for (uint32_t t = 0; t < ntiles; ++t) {
+            {
+                const uint8_t *tile = p.tiles + (size_t)(tbase + (t + 1 < ntiles ? t + 1 : t)) * p.tile_bytes;
+                load_codes<W>(tile, lane, rw, xn);
+                const float *fac = reinterpret_cast<const float *>(tile + 256u * rw);
+                fan = fac[lane];
+                frn = fac[64 + lane];
+                fen = fac[128 + lane];
+            }
+            const uint32_t local = t * kTileVectors + lane;
+            const bool valid = local < n;
+            const int ip = popc_ip<W>(x, planes, rw);
+            const float ex = width * (float)ip;
+            const float low = fa + gadd + fr * (ex + k1) - fe * gerr;
+#pragma unroll
+            for (int w = 0; w < Words<W>::kMax; ++w)
+                x[w] = xn[w];
+            fa = fan;
+            fr = frn;
+            fe = fen;
+            if (lows_out && valid)
+                lows_out[local] = low;
+            const unsigned long long key = ((unsigned long long)order_key(low) << 32) | local;
+            bool cand = valid && low < cutoff && key < bound;
+            unsigned long long m = __ballot(cand);
+            uint32_t c = (uint32_t)__popcll(m);
+            if (count + c > cap) {
+                // cut the buffer back to its keep smallest keys
+                for (uint32_t i = count + lane; i < cap; i += 64)
+                    s_buf[i] = ~0ull;
+                __syncthreads();
+                wave_sort(s_buf, cap, lane);
+                count = min(count, keep);
+                bound = count == keep ? s_buf[keep - 1] : ~0ull;
+                cand = cand && key < bound;
+                m = __ballot(cand);
+                c = (uint32_t)__popcll(m);
+            }
+            if (cand)
+                s_buf[count + lane_rank(m)] = key;
+            count += c;
+        }
+        if (count == 0)
+            continue;
+        for (uint32_t i = count + lane; i < cap; i += 64)
+            s_buf[i] = ~0ull;
         __syncthreads();
+        wave_sort(s_buf, cap, lane);
+        const uint32_t take = min(count, keep);
+        // Seeds refined on the GPU are published later by the seed threshold kernel (only
+        // those that can still reach the top-k); otherwise they are published now, with one
+        // reservation for the pair (the reference's early publication of vanguard seeds).
+        const bool defer = p.seed_dist != nullptr;
+        unsigned long long base = 0;
+        if (!defer) {
+            if (lane == 0)
+                base = atomicAdd(q.produced, (unsigned long long)take);
+            base = shfl0_u64(base);
+            if (base + take > limit) {
+                unsigned long long fresh = 0;
+                if (lane == 0)
+                    fresh = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released,
+                                          q.capacity, base + take);
+                limit = shfl0_u64(fresh);
+            }
+        }
+        uint32_t *seed = p.seed_bits + ((size_t)query * p.vanguard + probe) * p.seed_words;
+        const float width2 = uniformf(p.qwidth2[query]);
+        for (uint32_t sidx = lane; sidx < take; sidx += 64) {
+            const unsigned long long key = s_buf[sidx];
+            const uint32_t local = (uint32_t)key;
+            const uint8_t *tile = p.tiles + (size_t)(tbase + local / kTileVectors) * p.tile_bytes;
+            uint32_t x[Words<W>::kMax];
+            load_codes<W>(tile, local % kTileVectors, rw, x);
+            const int ip = popc_ip<W>(x, planes, rw);
+            const int ip_res = popc_ip<W>(x, planes + kBq * rw, rw);
+            const float ex = two_stage_ip(width, ip, width2, ip_res);
+            s_exk[sidx] = ex;
+            atomicOr(&seed[local >> 5], 1u << (local & 31));
+            const uint4 rec = make_uint4(w0, start + local, __float_as_uint(ex),
+                                         __float_as_uint(key_to_float((uint32_t)(key >> 32))));
+            if (defer)
+                p.seed_rec[((size_t)query * p.vanguard + probe) * keep + sidx] = rec;
+            else
+                place_record(q, base + sidx, limit, rec);
+        }
+        if (p.seed_dist) {
+            // Refined distance of every seed, 16 lanes per seed (cpu_refinement.cpp:183-192):
+            // f_add_ex + g_add + f_rescale_ex * (2^7 * exact_ip + <q', ex_code> + kbxSumq),
+            // with a bound on its rounding difference from the CPU's evaluation.
+            __syncthreads();
+            const uint32_t sub = lane & 15, chunks = p.P / 8;
+            const size_t lc = (size_t)p.P * 7 / 8;
+            const float *qv = p.qrot + (size_t)query * p.P;
+            const float kbq = uniformf(p.kb[query]);
+            for (uint32_t sidx = lane >> 4; sidx < take; sidx += 4) {
+                const unsigned long long key = s_buf[sidx];
+                const uint32_t local = (uint32_t)key;
+                const size_t gid = (size_t)start + local;
+                const uint8_t *code = p.ex_codes + gid * lc;
+                float ip = 0.0f, l1 = 0.0f;
+                for (uint32_t c = sub; c < chunks; c += 16)
+                    ip += excode_chunk_ip(code, qv, c, l1);
+#pragma unroll
+                for (int o = 8; o > 0; o >>= 1) {
+                    ip += __shfl_xor(ip, o, 16);
+                    l1 += __shfl_xor(l1, o, 16);
+                }
+                if (sub == 0) {
+                    const float fa = p.ex_factors[2 * gid], fr = p.ex_factors[2 * gid + 1];
+                    const float ex = s_exk[sidx];
+                    const float dist = fa + gadd + fr * (128.0f * ex + ip + kbq);
+                    const float mag = fabsf(fa) + fabsf(gadd) +
+                                      fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq));
+                    const size_t o = ((size_t)query * p.vanguard + probe) * keep + sidx;
+                    p.seed_dist[o] = dist;
+                    p.seed_low[o] = key_to_float((uint32_t)(key >> 32));
+                    p.seed_err[o] = 1e-4f * mag;
+                }
+            }
+        }
+        __syncthreads();  // the buffer is refilled by the next pair
     }
 }
 
 // Per query (one workgroup): the topk-th smallest refined seed distance d_k becomes the
 // threshold max(d_k + e, l) + 1 ulp, where e is the largest rounding bound and l the
 // largest lower bound among the seeds with distance <= d_k. Those seeds are published
-// candidates, so the CPU consumer, evaluating them later, finds at least topk of them
-// strictly below the threshold and passing its secondary filter: the threshold is one
-// the CPU would publish itself once it has refined them, set before the far and
-// recovery passes read it. Written only when lower than the current value; a racing CPU
-// store is harmless, every value written is at least the final topk-th distance.
+// here, so the CPU consumer, evaluating them, finds at least topk of them strictly below
+// the threshold and passing its secondary filter: the threshold is one the CPU would
+// publish itself once it has refined them, set before the far and recovery passes read
+// it. Written only when lower than the current value; a racing CPU store is harmless,
+// every value written is at least the final topk-th distance. The other seeds are
+// published only when their refined distance is within their rounding bound of the
+// threshold.
 constexpr int kThrThreads = 256;
-
-__device__ __forceinline__ float key_to_float(uint32_t key) {
-    return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
-}
 
 __global__ __launch_bounds__(kThrThreads) void seed_threshold_kernel(
     const float *__restrict__ seed_dist, const float *__restrict__ seed_low,
-    const float *__restrict__ seed_err, uint32_t count, uint32_t topk, float *thresholds,
-    unsigned long long *seeded) {
+    const float *__restrict__ seed_err, const uint4 *__restrict__ seed_rec, uint32_t count,
+    uint32_t topk, float *thresholds, unsigned long long *seeded, const QueueDev q) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_prefix, s_remaining, s_finite, s_ekey, s_lkey;
-    const uint32_t q = blockIdx.x, t = threadIdx.x;
-    const size_t base = (size_t)q * count;
+    __shared__ uint32_t s_wave[kThrThreads / 64];
+    __shared__ float s_thr;
+    __shared__ unsigned long long s_base, s_limit;
+    const uint32_t qi = blockIdx.x, t = threadIdx.x;
+    const size_t base = (size_t)qi * count;
     const float *d = seed_dist + base;
     if (t == 0) {
         s_finite = 0;
@@ -794,9 +805,12 @@ __global__ __launch_bounds__(kThrThreads) void seed_threshold_kernel(
     for (uint32_t i = t; i < count; i += kThrThreads)
         nf += isfinite(d[i]) ? 1u : 0u;
     atomicAdd(&s_finite, nf);
+    if (t == 0) {
+        s_thr = FLT_MAX;  // fewer refined seeds than topk: no threshold, every seed published
+        s_limit = __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __syncthreads();
-    if (s_finite < topk)
-        return;  // fewer refined seeds than topk: nothing to seed (uniform exit)
+    if (s_finite >= topk) {
     // radix select of the topk-th smallest distance (non-finite keys sort last)
     uint32_t prefix = 0, pmask = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
@@ -839,15 +853,59 @@ __global__ __launch_bounds__(kThrThreads) void seed_threshold_kernel(
         const float thr = nextafterf(fmaxf(key_to_float(kth) + __uint_as_float(s_ekey),
                                            key_to_float(s_lkey)),
                                      FLT_MAX);
-        uint32_t *slot = reinterpret_cast<uint32_t *>(thresholds) + q;
+        uint32_t *slot = reinterpret_cast<uint32_t *>(thresholds) + qi;
         const float cur = __uint_as_float(__hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM));
         if (thr < cur)
             __hip_atomic_store(slot, __float_as_uint(thr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        s_thr = thr;
         atomicAdd(seeded, 1ull);
+    }
+    __syncthreads();
+    }
+    // Publish the seeds that can still reach the top-k: refined distance within the
+    // rounding bound of the threshold (the refined pre-filter's rule); the topk seeds the
+    // threshold rests on always qualify. One reservation per round of 256 slots.
+    const float thr = s_thr;
+    const uint32_t lane = t & 63, wave = t >> 6;
+    for (uint32_t r0 = 0; r0 < count; r0 += kThrThreads) {
+        const uint32_t i = r0 + t;
+        const bool pub = i < count && isfinite(d[i]) && d[i] <= thr + seed_err[base + i];
+        const unsigned long long m = __ballot(pub);
+        if (lane == 0)
+            s_wave[wave] = (uint32_t)__popcll(m);
+        __syncthreads();
+        uint32_t before = 0, total = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kThrThreads / 64; ++w) {
+            before += w < wave ? s_wave[w] : 0u;
+            total += s_wave[w];
+        }
+        if (total != 0) {
+            if (t == 0) {
+                const unsigned long long b = atomicAdd(q.produced, (unsigned long long)total);
+                unsigned long long lim = s_limit;
+                if (b + total > lim)
+                    lim = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released,
+                                        q.capacity, b + total);
+                s_base = b;
+                s_limit = lim;
+            }
+            __syncthreads();
+            if (pub)
+                place_record(q, s_base + before + lane_rank(m), s_limit, seed_rec[base + i]);
+        }
+        __syncthreads();  // s_wave / s_base reused by the next round
     }
 }
 
 __global__ void copy_u64_kernel(const unsigned long long *src, unsigned long long *dst) { *dst = *src; }
+
+__global__ void snapshot_thresholds_kernel(const float *host, float *dev, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        dev[i] = __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t *>(host) + i,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM));
+}
 
 __global__ void queue_reset_kernel(QueueDev q) {
     *q.produced = 0;
@@ -942,18 +1000,18 @@ __global__ __launch_bounds__(256) void finish_kernel(QueueDev q, unsigned long l
 
 // Persistent grid = workgroups of this kernel resident on the whole device at once.
 template <class F>
-uint32_t resident_grid(F kernel, int block) {
+uint32_t resident_grid(F kernel, int block, size_t dyn_lds = 0) {
     static std::mutex mu;
-    static std::unordered_map<const void *, uint32_t> cache;
+    static std::map<std::pair<const void *, size_t>, uint32_t> cache;
     int dev = 0;
     (void)hipGetDevice(&dev);
-    const void *key = reinterpret_cast<const void *>(kernel);
+    const std::pair<const void *, size_t> key(reinterpret_cast<const void *>(kernel), dyn_lds);
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(key);
     if (it != cache.end())
         return it->second;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, dyn_lds) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         per_cu <= 0 || cus <= 0) {
         per_cu = 8;
@@ -987,13 +1045,9 @@ int launch_scan_w(const ScanParams &p, uint32_t batch_q, int kind, uint32_t set,
 
 template <int W>
 void launch_seed_w(const ScanParams &p, hipStream_t s) {
-    auto *k = vanguard_seed_kernel<W>;
-    k<<<resident_grid(k, kVanThreads), kVanThreads, 0, s>>>(p);
-}
-
-template <int W>
-uint32_t seed_grid_w() {
-    return resident_grid(vanguard_seed_kernel<W>, kVanThreads);
+    auto *k = seed_kernel<W>;
+    const size_t lds = (size_t)p.seed_buf * (sizeof(unsigned long long) + sizeof(float));
+    k<<<resident_grid(k, 64, lds), 64, lds, s>>>(p);
 }
 
 }  // namespace
@@ -1028,16 +1082,6 @@ int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t set, hip
     }
 }
 
-uint32_t vanguard_seed_grid(uint32_t W) {
-    switch (W) {
-    case 2: return seed_grid_w<2>();
-    case 4: return seed_grid_w<4>();
-    case 8: return seed_grid_w<8>();
-    case 24: return seed_grid_w<24>();
-    default: return seed_grid_w<0>();
-    }
-}
-
 int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s) {
     switch (W) {
     case 2: launch_seed_w<2>(p, s); break;
@@ -1050,10 +1094,16 @@ int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s) {
 }
 
 void launch_seed_thresholds(const float *seed_dist, const float *seed_low, const float *seed_err,
-                            uint32_t nq, uint32_t count, uint32_t topk, float *thresholds,
-                            unsigned long long *seeded, hipStream_t s) {
-    seed_threshold_kernel<<<nq, kThrThreads, 0, s>>>(seed_dist, seed_low, seed_err, count, topk,
-                                                     thresholds, seeded);
+                            const uint4 *seed_rec, uint32_t nq, uint32_t count, uint32_t topk,
+                            float *thresholds, unsigned long long *seeded, QueueDev q,
+                            hipStream_t s) {
+    seed_threshold_kernel<<<nq, kThrThreads, 0, s>>>(seed_dist, seed_low, seed_err, seed_rec, count,
+                                                     topk, thresholds, seeded, q);
+}
+
+void launch_snapshot_thresholds(const float *host, float *dev, uint32_t n, hipStream_t s) {
+    if (n)
+        snapshot_thresholds_kernel<<<(n + 255) / 256, 256, 0, s>>>(host, dev, n);
 }
 
 void launch_copy_u64(const unsigned long long *src, unsigned long long *dst, hipStream_t s) {

@@ -3,8 +3,9 @@
 // (query_kernels.cuh:105-113, kernel_types.cuh:34-60, hybrid.cu:504-508). Here the
 // same grouping is a counting sort into 2*nlist buckets (bucket = cluster for vanguard
 // pairs, nlist + cluster for the rest) followed by cutting every bucket into scan
-// units of at most batch_q pairs (1 for vanguard buckets). Pair order inside a bucket
-// is not fixed; every pair's results are independent of it.
+// units of at most batch_q pairs (1 for vanguard buckets), each split further into
+// ranges of at most kUnitTiles tiles of the cluster. Pair order inside a bucket is not
+// fixed; every pair's results are independent of it.
 #include "engine_internal.h"
 
 namespace cora {
@@ -53,13 +54,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
     for (uint32_t b = b0; b < b1; ++b) {
         const uint32_t m = count[b];
         pairs += m;
+        const uint32_t n = meta[b < nlist ? b : b - nlist].n, sp = unit_splits(n);
         if (b < nlist) {
-            units += m;
-            van_units += m;
+            units += m * sp;
+            van_units += m * sp;
         } else {
             const uint32_t u = (m + batch_q - 1) / batch_q;
-            const uint32_t n = meta[b - nlist].n;
-            units += u;
+            units += u * sp;
             bytes += (unsigned long long)u * n * bpv;
             fu += u;
             vec += (unsigned long long)m * n;
@@ -92,7 +93,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
         bucket_offset[b] = po;
         unit_offset[b] = uo;
         po += m;
-        uo += b < nlist ? m : (m + batch_q - 1) / batch_q;
+        const uint32_t sp = unit_splits(meta[b < nlist ? b : b - nlist].n);
+        uo += (b < nlist ? m : (m + batch_q - 1) / batch_q) * sp;
     }
     if (t == kScanThreads - 1) {
         bucket_offset[nb] = s_pairs[t];
@@ -121,11 +123,13 @@ __global__ void scatter_pairs_kernel(const int32_t *__restrict__ probe_idx, uint
 
 __global__ void build_units_kernel(const uint32_t *__restrict__ bucket_offset,
                                    const uint32_t *__restrict__ unit_offset,
-                                   const uint32_t *__restrict__ num_units, uint32_t nlist,
-                                   uint32_t batch_q, Unit *__restrict__ units) {
-    const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
-    if (u >= num_units[0] + num_units[1])
+                                   const uint32_t *__restrict__ num_units,
+                                   const ClusterMeta *__restrict__ meta, uint32_t nlist,
+                                   uint32_t batch_q, uint64_t max_units, Unit *__restrict__ units) {
+    const uint64_t u64 = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x;
+    if (u64 >= max_units || u64 >= (uint64_t)num_units[0] + num_units[1])
         return;
+    const uint32_t u = (uint32_t)u64;
     // last bucket b with unit_offset[b] <= u (empty buckets share offsets)
     uint32_t lo = 0, hi = 2 * nlist;  // unit_offset[2*nlist] = total > u
     while (hi - lo > 1) {
@@ -135,11 +139,14 @@ __global__ void build_units_kernel(const uint32_t *__restrict__ bucket_offset,
         else
             hi = mid;
     }
-    const uint32_t b = lo;
+    const uint32_t b = lo, c = b % nlist;
     const uint32_t q = b < nlist ? 1u : batch_q;
+    const uint32_t n = meta[c].n, sp = unit_splits(n), ntiles = (n + kTileVectors - 1) / kTileVectors;
     const uint32_t local = u - unit_offset[b];
+    const uint32_t group = local / sp, split = local % sp;
     const uint32_t m = bucket_offset[b + 1] - bucket_offset[b];
-    units[u] = Unit{b % nlist, bucket_offset[b] + local * q, min(q, m - local * q), b};
+    const uint32_t t0 = split * kUnitTiles, tc = min(kUnitTiles, ntiles - min(ntiles, t0));
+    units[u] = Unit{c, bucket_offset[b] + group * q, min(q, m - group * q), (t0 << 8) | tc};
 }
 
 }  // namespace
@@ -162,7 +169,8 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
                         uint32_t nprobe, uint32_t nlist, uint32_t vanguard, uint32_t batch_q,
                         uint32_t bytes_per_vector, uint32_t *bucket_count, uint32_t *bucket_cursor,
                         uint32_t *bucket_offset, uint32_t *unit_offset, Pair *pairs, Unit *units,
-                        uint32_t *num_units, unsigned long long *scan_stats, hipStream_t s) {
+                        uint64_t max_units, uint32_t *num_units, unsigned long long *scan_stats,
+                        hipStream_t s) {
     const size_t np = (size_t)nq * nprobe;
     launch_fill_u32(bucket_count, 0, 2 * (size_t)nlist, s);
     launch_fill_u32(bucket_cursor, 0, 2 * (size_t)nlist, s);
@@ -173,8 +181,8 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
                                                    num_units, scan_stats);
     scatter_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard,
                                               bucket_offset, bucket_cursor, pairs);
-    build_units_kernel<<<grid, 256, 0, s>>>(bucket_offset, unit_offset, num_units, nlist, batch_q,
-                                            units);
+    build_units_kernel<<<(uint32_t)((max_units + 255) / 256), 256, 0, s>>>(
+        bucket_offset, unit_offset, num_units, meta, nlist, batch_q, max_units, units);
 }
 
 }  // namespace cora

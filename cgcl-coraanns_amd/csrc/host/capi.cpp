@@ -176,6 +176,8 @@ int cora_hybrid_stats_get(cora_hybrid *h, cora_hybrid_stats *out) {
         out->pass_produced[i] = x.get_last_pass_produced(i);
     out->seeded_queries = x.get_last_seeded_queries();
     out->prefilter_dropped = x.get_last_prefilter_dropped();
+    out->seed_ms = x.get_last_seed_ms();
+    out->recovery_ms = x.get_last_recovery_ms();
     return CORA_OK;
 }
 

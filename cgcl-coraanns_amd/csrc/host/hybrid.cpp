@@ -246,6 +246,8 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
         last_pass_produced_[i] = st.pass_produced[i];
     last_seeded_queries_ = st.seeded_queries;
     last_prefilter_dropped_ = st.prefilter_dropped;
+    last_seed_ms_ = st.seed_ms;
+    last_recovery_ms_ = st.recovery_ms;
     if (rc != CORA_OK)
         throw std::runtime_error(engine_error(engine_));
     if (profiling_enabled_) {

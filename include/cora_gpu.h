@@ -104,6 +104,8 @@ typedef struct cora_search_stats {
                                   far-pair and recovery passes (cumulative) */
     uint64_t seeded_queries;   /* queries that received a GPU seed threshold */
     uint64_t prefilter_dropped; /* candidates the refined pre-filter dropped */
+    float seed_ms;          /* vanguard seed pass + seed thresholds (FILTER_TIMING only) */
+    float recovery_ms;      /* vanguard recovery pass (FILTER_TIMING only) */
 } cora_search_stats;
 
 /* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */

@@ -59,6 +59,8 @@ typedef struct cora_hybrid_stats {
     uint64_t pass_produced[3]; /* cumulative candidates after the seed, far, recovery passes */
     uint64_t seeded_queries;   /* queries given a GPU seed threshold */
     uint64_t prefilter_dropped; /* candidates the GPU refined pre-filter dropped */
+    float seed_ms;        /* vanguard seed pass + seed thresholds */
+    float recovery_ms;    /* vanguard recovery pass */
 } cora_hybrid_stats;
 
 int cora_hybrid_create(cora_hybrid **out, int device);                 /* HybridIndex() */

@@ -117,6 +117,8 @@ class HybridIndex {
     uint64_t get_last_pass_produced(int pass) const { return last_pass_produced_[pass]; }
     uint64_t get_last_seeded_queries() const { return last_seeded_queries_; }
     uint64_t get_last_prefilter_dropped() const { return last_prefilter_dropped_; }
+    float get_last_seed_ms() const { return last_seed_ms_; }
+    float get_last_recovery_ms() const { return last_recovery_ms_; }
     cora_gpu_engine *gpu_engine() const { return engine_; }
 
   private:
@@ -164,6 +166,7 @@ class HybridIndex {
     uint64_t last_pass_produced_[3] = {0, 0, 0};
     uint64_t last_seeded_queries_ = 0;
     uint64_t last_prefilter_dropped_ = 0;
+    float last_seed_ms_ = 0.0f, last_recovery_ms_ = 0.0f;
 };
 
 }  // namespace coraanns

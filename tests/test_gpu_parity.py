@@ -333,7 +333,8 @@ def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
     seed thresholds): seed choice and refined seed distances vs the oracle, the seeded
     threshold vs the oracle's rule and its safety, the candidate count of the far and
     recovery passes against it (with the refined pre-filter: low below the threshold and
-    refined distance within the rounding bound of it), and an unchanged final top-k."""
+    refined distance within the rounding bound of it), the seeds published after the
+    threshold (refined distance within their bound of it), and an unchanged final top-k."""
     nprobe, topk, van = 8, 10, 3
     keep = max(topk, 20)
     say(f"[gpu] GPU seed thresholds, frozen parity, prefilter={prefilter}")
@@ -398,11 +399,10 @@ def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
             s = int(sd.cluster_start[c])
             low = pair_lows[p].astype(np.float64)
             mask = np.ones(low.size, bool)
+            idx = None
             if seed_sets[p] is not None:
                 idx = np.fromiter(seed_sets[p], np.int64, len(seed_sets[p]))
                 mask[idx] = False
-                lo_cnt += idx.size
-                hi_cnt += idx.size
             # refined distance and rounding bound of every vector of the pair
             gall = s + np.arange(low.size)
             ipa = orc.ip_int_direct(sd.bits[gall], qint[q])
@@ -412,6 +412,10 @@ def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
             rda = orc.refine_dist(fa, fr, g["gadd"][q, p], exa,
                                   orc.excode_ip(g["qr"][q], sd.long_codes[gall], P), g["kb"][q], 7)
             erra = orc.refine_error_bound(fa, fr, g["gadd"][q, p], exa, l1, g["kb"][q], 7)
+            if idx is not None:
+                # seeds refined on the GPU are published when within their bound of the threshold
+                lo_cnt += int((rda[idx] <= thr[q] + 0.9 * erra[idx]).sum())
+                hi_cnt += int((rda[idx] <= thr[q] + 1.1 * erra[idx]).sum())
             lo_ok = low < thr[q] - band
             hi_ok = low < thr[q] + band
             if prefilter:
