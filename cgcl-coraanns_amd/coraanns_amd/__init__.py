@@ -39,6 +39,7 @@ DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range
 DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
 DBG_SEED_DIST, DBG_THRESHOLDS = 10, 11
 FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
+FLAG_PAIR_SEEDS = 1 << 6
 
 
 class EngineUnavailable(RuntimeError):
@@ -78,7 +79,8 @@ class cora_search_stats(C.Structure):
                 ("scan_bytes", C.c_uint64), ("scan_units", C.c_uint64),
                 ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float), ("probe_flops", C.c_uint64),
                 ("pass_produced", C.c_uint64 * 3), ("seeded_queries", C.c_uint64),
-                ("prefilter_dropped", C.c_uint64), ("seed_ms", C.c_float), ("recovery_ms", C.c_float)]
+                ("prefilter_dropped", C.c_uint64), ("seed_ms", C.c_float), ("recovery_ms", C.c_float),
+                ("gpu_refined", C.c_uint64)]
 
 
 class cora_queue_view(C.Structure):
@@ -101,7 +103,7 @@ class cora_hybrid_stats(C.Structure):
                 ("scan_units", C.c_uint64), ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float),
                 ("probe_flops", C.c_uint64), ("pass_produced", C.c_uint64 * 3),
                 ("seeded_queries", C.c_uint64), ("prefilter_dropped", C.c_uint64),
-                ("seed_ms", C.c_float), ("recovery_ms", C.c_float)]
+                ("seed_ms", C.c_float), ("recovery_ms", C.c_float), ("gpu_refined", C.c_uint64)]
 
 
 class cora_ivf_info(C.Structure):

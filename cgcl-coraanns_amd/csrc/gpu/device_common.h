@@ -1,0 +1,187 @@
+// Device helpers shared by the scan and vanguard translation units: wave-uniform values,
+// the tile layout's code loads, the Bq=8 popcount inner product, the packed 7-bit
+// ex-code inner product, ring publication and float order keys.
+#pragma once
+
+#include "engine_internal.h"
+
+namespace cora {
+namespace {
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+__device__ __forceinline__ float uniformf(float v) {
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v)));
+}
+
+__device__ __forceinline__ unsigned long long shfl0_u64(unsigned long long v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint32_t lane_rank(unsigned long long mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// W > 0: compile-time word count; W == 0: runtime word count (any P % 64 == 0, P <= 1024).
+template <int W>
+struct Words {
+    static constexpr int kMax = W > 0 ? W : 32;
+};
+
+// Survivor stage of one wave: kCap records of 16 bytes plus their code words, about
+// 4 KB, so LDS never limits the scan's occupancy below 32 waves per CU for P <= 128.
+template <int W>
+struct Stage {
+    static constexpr int kWords = Words<W>::kMax;
+    static constexpr int kFit = 4096 / (16 + 4 * kWords) / 64 * 64;
+    static constexpr int kCap = kFit < 64 ? 64 : kFit;
+};
+
+template <int W>
+__device__ __forceinline__ void load_codes(const uint8_t *__restrict__ tile, uint32_t lane,
+                                           uint32_t rw, uint32_t (&x)[Words<W>::kMax]) {
+    const uint32_t nw = W > 0 ? (uint32_t)W : rw;
+    const uint4 *g4 = reinterpret_cast<const uint4 *>(tile);
+#pragma unroll
+    for (int g = 0; g < Words<W>::kMax / 4; ++g) {
+        if ((uint32_t)(4 * g + 4) <= nw) {
+            const uint4 v = g4[g * 64 + lane];
+            x[4 * g] = v.x;
+            x[4 * g + 1] = v.y;
+            x[4 * g + 2] = v.z;
+            x[4 * g + 3] = v.w;
+        }
+    }
+    if (nw % 4 == 2) {
+        const uint2 *t2 = reinterpret_cast<const uint2 *>(tile + (size_t)(nw / 4) * 1024);
+        const uint2 v = t2[lane];
+        x[nw - 2] = v.x;
+        x[nw - 1] = v.y;
+    }
+}
+
+template <int W>
+__device__ __forceinline__ int popc_ip(const uint32_t (&x)[Words<W>::kMax],
+                                       const uint32_t *__restrict__ planes, uint32_t rw) {
+    const uint32_t nw = W > 0 ? (uint32_t)W : rw;
+    int a[kBq];
+#pragma unroll
+    for (int j = 0; j < kBq; ++j)
+        a[j] = 0;
+#pragma unroll
+    for (int w = 0; w < Words<W>::kMax; ++w) {
+        if ((uint32_t)w < nw) {
+#pragma unroll
+            for (int j = 0; j < kBq; ++j)
+                a[j] += __popc(x[w] & planes[j * nw + w]);
+        }
+    }
+    int ip = -(a[kBq - 1] << (kBq - 1));
+#pragma unroll
+    for (int j = 0; j < kBq - 1; ++j)
+        ip += a[j] << j;
+    return ip;
+}
+
+// Two-stage <q',b>: width * ip_int rounded, then width2 * ip_res added with one rounding.
+__device__ __forceinline__ float two_stage_ip(float width, int ip, float width2, int ip_res) {
+    return __fmaf_rn(width2, (float)ip_res, __fmul_rn(width, (float)ip));
+}
+
+// <q', ex_code> over one 8-dimension chunk c (group g = c / 8 of 64 dimensions, k = c % 8)
+// of a packed 7-bit ex-code (pack_excode.hpp:216-265): per 64 dimensions, bytes 0..47
+// hold the low six bits of dimensions 0..47, and in their top two bits the bit pairs of
+// dimensions 48..63 (bits 0-1 in bytes 0..15, 2-3 in 16..31, 4-5 in 32..47); the u64 at
+// bytes 48..55 holds bit 6 of dimension 8k+j at bit 8j+k. l1 accumulates sum |q'|.
+__device__ __forceinline__ float excode_chunk_ip(const uint8_t *__restrict__ code,
+                                                 const float *__restrict__ q, uint32_t c,
+                                                 float &l1) {
+    const uint32_t g = c >> 3, k = c & 7;
+    const uint64_t *grp = reinterpret_cast<const uint64_t *>(code + (size_t)g * 56);
+    uint64_t v;
+    if (k < 6) {
+        v = grp[k] & 0x3F3F3F3F3F3F3F3Full;
+    } else {
+        const uint32_t o = k - 6;
+        v = ((grp[o] >> 6) & 0x0303030303030303ull) | ((grp[2 + o] >> 4) & 0x0C0C0C0C0C0C0C0Cull) |
+            ((grp[4 + o] >> 2) & 0x3030303030303030ull);
+    }
+    v |= ((grp[6] >> k) & 0x0101010101010101ull) << 6;
+    const float4 q0 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k);
+    const float4 q1 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k + 4);
+    const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sum = fmaf((float)((v >> (8 * j)) & 0xFFu), qq[j], sum);
+        l1 += fabsf(qq[j]);
+    }
+    return sum;
+}
+
+// One 16-byte Candidate store to the host-coherent ring that writes through the GPU L2
+// (system-scope coherence bits sc0 sc1). A plain store to host memory may stay in L2
+// until the next system-scope release, which a producer still running never issues, so
+// the CPU consumer would not see the record and the drain kernel, waiting for the CPU
+// to release ring space, would never see progress.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void store_ring(uint4 *slot, uint4 rec) {
+    const u32x4_t v = {rec.x, rec.y, rec.z, rec.w};
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(slot), "v"(v) : "memory");
+}
+
+__device__ __noinline__ unsigned long long refresh_limit(unsigned long long *cached_limit,
+                                                         int *refresh_flag,
+                                                         unsigned long long *released,
+                                                         unsigned long long capacity,
+                                                         unsigned long long need) {
+    unsigned long long lim =
+        __hip_atomic_load(cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lim >= need)
+        return lim;
+    if (atomicCAS(refresh_flag, 0, 1) == 0) {
+        const unsigned long long rel =
+            __hip_atomic_load(released, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        const unsigned long long fresh = rel + capacity;
+        atomicMax(cached_limit, fresh);
+        __hip_atomic_store(refresh_flag, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        lim = lim > fresh ? lim : fresh;
+    } else {
+        lim = __hip_atomic_load(cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return lim;
+}
+
+// Ring slot when pos is below the write limit, otherwise the HBM spill buffer.
+__device__ __forceinline__ void place_record(const QueueDev &q, unsigned long long pos,
+                                             unsigned long long limit, uint4 rec) {
+    if (pos < limit) {
+        store_ring(&q.items[pos & q.mask], rec);
+    } else {
+        const unsigned long long s = atomicAdd(q.spill_count, 1ull);
+        if (s < q.spill_capacity) {
+            q.spill[s].item = rec;
+            q.spill[s].position = pos;
+        } else {
+            atomicExch(q.spill_overflow, 1);
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_to_float(uint32_t key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+}  // namespace
+}  // namespace cora

@@ -86,7 +86,7 @@ struct cora_gpu_engine {
     bool launched = false;
     cora_search_args last{};
     uint32_t last_depth = 0, last_batch = 1;
-    bool last_timing = false;
+    bool last_timing = false, last_fused = false;
 };
 
 namespace {
@@ -350,6 +350,7 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
         largest = std::max(largest, n);
         tiles += (n + kTileVectors - 1) / kTileVectors;
     }
+
     if (count != num_vecs)
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "cluster sizes differ from index size");
     if (tiles > UINT32_MAX)
@@ -499,7 +500,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_uoff, nb + 1));
         TRY(dalloc(E, E->d_nunits, 2));
         TRY(dalloc(E, E->d_cursor, kNumXcd));
-        TRY(dalloc(E, E->d_stats, 8));
+        TRY(dalloc(E, E->d_stats, 9));
         TRY(dalloc(E, E->d_pairs, np));
         TRY(dalloc(E, E->d_units, np * unit_splits((uint32_t)E->max_cluster)));
         TRY(dalloc(E, E->d_thr_snap, max_q));
@@ -687,7 +688,21 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     }
     p.prefilter = prefilter ? 1 : 0;
     p.dropped = E->d_stats + 7;
-    launch_fill_u64(E->d_stats + 3, 0ull, 5, s);  // per-pass counters of this launch
+    // fused per-query vanguard pass (vanguard.hip) unless the reference's per-pair passes
+    // are asked for or the shape exceeds its limits
+    const bool fused = gpu_seed && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
+                       a->topk <= kVanguardMaxTopk;
+    VanguardArgs va{};
+    E->last_fused = fused && depth > 0;
+    if (fused) {
+        va.probe_idx = E->d_pidx;
+        va.depth = depth;
+        va.topk = a->topk;
+        va.thr_out = frozen ? E->d_thr_snap : E->h_thr;
+        va.seeded = E->d_stats + 6;
+        va.refined = E->d_stats + 8;
+    }
+    launch_fill_u64(E->d_stats + 3, 0ull, 6, s);  // per-pass counters of this launch
     if (timing)
         HIPCHK(hipEventRecord(E->ev_f0, s));
     // live thresholds: each pass reads a copy of the host array taken just before it
@@ -695,7 +710,10 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         if (!frozen)
             launch_snapshot_thresholds(E->h_thr, E->d_thr_snap, nq, s);
     };
-    if (depth > 0) {
+    if (depth > 0 && fused) {
+        snapshot();
+        launch_vanguard_query(p, va, E->W, nq, s);
+    } else if (depth > 0) {
         launch_fill_u32(E->d_seed, 0u, (size_t)nq * depth * E->seed_words, s);
         snapshot();
         if (gpu_seed)  // +inf marks seed slots the seed pass leaves unused
@@ -717,7 +735,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     if (timing)
         HIPCHK(hipEventRecord(E->ev_s1, s));
     launch_copy_u64(E->d_produced, E->d_stats + 4, s);
-    if (depth > 0) {
+    if (depth > 0 && !fused) {
         launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
         snapshot();
         launch_scan(p, E->W, 1, 1, s);
@@ -756,7 +774,7 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     HIPCHK(hipSetDevice(E->device));
     HIPCHK(hipStreamSynchronize(E->stream));
     HIPCHK(hipStreamSynchronize(E->stream_d2h));
-    unsigned long long stats[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    unsigned long long stats[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     int stalled = 0;
     HIPCHK(hipMemcpy(stats, E->d_stats, sizeof(stats), hipMemcpyDeviceToHost));
     HIPCHK(hipMemcpy(&stalled, E->d_stalled, sizeof(int), hipMemcpyDeviceToHost));
@@ -774,12 +792,15 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
         out.pass_produced[i] = stats[3 + i];
     out.seeded_queries = stats[6];
     out.prefilter_dropped = stats[7];
+    out.gpu_refined = stats[8];
     if (E->last_timing) {
         HIPCHK(hipEventElapsedTime(&out.filter_ms, E->ev_f0, E->ev_f1));
         HIPCHK(hipEventElapsedTime(&out.scan_ms, E->ev_s0, E->ev_s1));
         HIPCHK(hipEventElapsedTime(&out.probe_ms, E->ev_p0, E->ev_p1));
         HIPCHK(hipEventElapsedTime(&out.seed_ms, E->ev_f0, E->ev_s0));
         HIPCHK(hipEventElapsedTime(&out.recovery_ms, E->ev_s1, E->ev_f1));
+        if (E->last_fused)
+            out.recovery_ms = 0.0f;  // no recovery pass
     }
     if (st)
         *st = out;

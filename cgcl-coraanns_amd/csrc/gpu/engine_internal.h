@@ -22,6 +22,8 @@ constexpr int kMaxBatchQ = 8;      // same-cluster pairs per scan pass
 constexpr int kMaxVanguardKeep = 1024;
 constexpr int kSelectMaxProbe = 4096;       // top-nprobe select held in LDS
 constexpr uint32_t kNumXcd = 8;
+constexpr uint32_t kVanguardMaxPairs = 64;  // fused vanguard pass: vanguard depth limit
+constexpr uint32_t kVanguardMaxTopk = 128;  // fused vanguard pass: top-k limit
 
 struct ClusterMeta {
     uint32_t start;      // first global (cluster-order) vector index
@@ -141,6 +143,17 @@ struct ScanParams {
     uint32_t dbg_stride;         // max cluster size
 };
 
+// Fused vanguard pass (vanguard.hip): one workgroup per query over its vanguard pairs.
+struct VanguardArgs {
+    const int32_t *probe_idx;      // [nq][nprobe] probed clusters, nearest first
+    uint32_t depth;                // vanguard pairs per query (probe ranks 0..depth-1)
+    uint32_t topk;
+    float *thr_out;                // thresholds lowered by the pass (host-coherent, or the
+                                   // frozen snapshot in the test mode)
+    unsigned long long *seeded;    // queries whose threshold the pass lowered
+    unsigned long long *refined;   // vectors refined on the GPU
+};
+
 // ---- launchers (each defined in the translation unit holding its kernel) ----
 void launch_repack(const uint32_t *ref_words, const float *ref_factors, const ClusterMeta *meta,
                    uint32_t nlist, uint32_t W, uint8_t *tiles, uint32_t tile_bytes,
@@ -182,6 +195,10 @@ void launch_seed_thresholds(const float *seed_dist, const float *seed_low, const
                             const uint4 *seed_rec, uint32_t nq, uint32_t count, uint32_t topk,
                             float *thresholds, unsigned long long *seeded, QueueDev q,
                             hipStream_t s);
+// LDS bytes of the fused vanguard pass besides q' and the lower bounds
+size_t vanguard_static_lds();
+void launch_vanguard_query(const ScanParams &p, const VanguardArgs &va, uint32_t W, uint32_t nq,
+                           hipStream_t s);
 // dev[0..n) = the host-coherent thresholds, read with system scope (the per-pass copy the
 // scan kernels read, so no unit waits on a host-memory round trip)
 void launch_snapshot_thresholds(const float *host, float *dev, uint32_t n, hipStream_t s);

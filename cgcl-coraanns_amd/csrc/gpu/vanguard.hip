@@ -1,0 +1,628 @@
+// Fused vanguard pass: one workgroup per query over all of its vanguard pairs (probe rank
+// < vanguard), replacing the per-pair seed pass, the seed threshold kernel and the
+// per-pair recovery pass when the ex-codes are resident in HBM.
+//
+// The reference runs the vanguard pairs as a seed kernel that publishes the best
+// max(topk, 20) lower bounds of each pair (filter_kernels.cuh:308-468), and a recovery
+// kernel that later publishes the pair's other vectors with low < threshold
+// (filter_kernels.cuh:470-582), the threshold being lowered meanwhile by the CPU
+// consumer from the refined distances. Here the whole query is handled in one place:
+//
+//   1. the four waves stream the tiles of the query's vanguard clusters (nearest first)
+//      and evaluate the Bitwise lower bound of the scan kernels (same expression); a
+//      vector whose bound is below the query's current threshold joins an LDS candidate
+//      list (lower bound, position), compacted per wave with a ballot;
+//   2. every 8 tiles per wave, once the list holds 1,024 entries (and at the end), the
+//      list is refined: while fewer than topk vectors are refined, the 128 smallest
+//      bounds first (radix select), then every remaining bound below the threshold, in
+//      chunks of 128 vectors (two lanes each) with the CPU's formula
+//      (cpu_refinement.cpp:183-192) on the HBM ex-codes and a bound on the rounding
+//      difference to the CPU's own evaluation; each chunk is merged into the query's
+//      top-k of refined distances, which lowers the threshold to max(d_k + e, l) + 1 ulp
+//      (d_k the k-th distance, e the largest rounding bound and l the largest lower bound
+//      among those k); a vector whose bound is at or above the threshold is skipped;
+//   3. every refined vector whose distance is within its rounding bound of the final
+//      threshold is published to the ring (the refined pre-filter rule), and the
+//      threshold is lowered (atomic minimum) for the far pass and the CPU consumer.
+//
+// Only bounds below a threshold backed by refined distances are ever dropped, and the
+// threshold only falls, so every vector whose bound is below the final threshold is
+// refined. Safety is that of the refined pre-filter: the k vectors behind the threshold
+// are published, the CPU evaluates each below the threshold (distance and lower bound),
+// so the CPU's final k-th distance is at most the threshold, and a vector dropped here
+// has a CPU-evaluated distance above the threshold, which the CPU consumer itself would
+// reject.
+#include <float.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "device_common.h"
+
+namespace cora {
+namespace {
+
+constexpr int kVqThreads = 256;
+constexpr int kVqWaves = kVqThreads / 64;
+constexpr uint32_t kVqWin = 512;     // window capacity (sorted u64 keys in LDS)
+constexpr uint32_t kVqChunk = 128;   // refinements between threshold updates
+constexpr uint32_t kVqHeld = 256;    // refined vectors held before publication
+constexpr uint32_t kVqMaxW = 32;     // P <= 1024
+constexpr uint32_t kVqSegTiles = 8;  // tiles per wave between list checks
+constexpr uint32_t kVqHigh = 1024;   // list entries that trigger a refinement round
+constexpr uint32_t kVqList = kVqHigh + kVqWaves * kVqSegTiles * kTileVectors;  // list capacity
+static_assert(kVqChunk * 2 == kVqThreads, "one chunk vector per two lanes");
+
+__device__ __forceinline__ float processed_mark() { return __uint_as_float(0x7FC00000u); }
+
+// Inclusive prefix sum over the workgroup (thread order); s_red holds kVqWaves words.
+__device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t *s_red) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(v, o);
+        if (lane >= (uint32_t)o)
+            v += y;
+    }
+    if (lane == 63)
+        s_red[wave] = v;
+    __syncthreads();
+    uint32_t add = 0;
+    for (uint32_t w = 0; w < wave; ++w)
+        add += s_red[w];
+    __syncthreads();
+    return v + add;
+}
+
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t *s_red) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v += __shfl_xor(v, o);
+    if (lane == 0)
+        s_red[wave] = v;
+    __syncthreads();
+    uint32_t s = 0;
+#pragma unroll
+    for (int w = 0; w < kVqWaves; ++w)
+        s += s_red[w];
+    __syncthreads();
+    return s;
+}
+
+__device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t *s_red) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v = max(v, (uint32_t)__shfl_xor(v, o));
+    if (lane == 0)
+        s_red[wave] = v;
+    __syncthreads();
+    uint32_t s = 0;
+#pragma unroll
+    for (int w = 0; w < kVqWaves; ++w)
+        s = max(s, s_red[w]);
+    __syncthreads();
+    return s;
+}
+
+// The k-th smallest (k >= 1) order key among lows(i) < thr, i < n (4 radix passes of 8
+// bits; the caller guarantees at least k such entries).
+template <class L>
+__device__ uint32_t block_select(L lows, uint32_t n, float thr, uint32_t k, uint32_t *s_hist,
+                                 uint32_t *s_red, uint32_t *s_sc) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t prefix = 0, pmask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        s_hist[tid] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < n; i += kVqThreads) {
+            const float l = lows(i);
+            if (l < thr) {
+                const uint32_t key = order_key(l);
+                if ((key & pmask) == prefix)
+                    atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+            }
+        }
+        __syncthreads();
+        const uint32_t h = s_hist[tid];
+        const uint32_t incl = block_incl_scan(h, s_red);
+        if (incl >= k && incl - h < k) {
+            s_sc[0] = tid;
+            s_sc[1] = k - (incl - h);
+        }
+        __syncthreads();
+        prefix |= s_sc[0] << shift;
+        pmask |= 255u << shift;
+        k = s_sc[1];
+        __syncthreads();
+    }
+    return prefix;
+}
+
+struct VqShared {
+    uint32_t planes[2 * kBq * kVqMaxW];
+    uint32_t start[kVanguardMaxPairs], n[kVanguardMaxPairs], tbase[kVanguardMaxPairs];
+    uint32_t off[kVanguardMaxPairs + 1], toff[kVanguardMaxPairs + 1];
+    float gadd[kVanguardMaxPairs], gerr[kVanguardMaxPairs];
+    uint32_t win[kVqWin];
+    uint32_t hist[256];
+    uint32_t red[kVqWaves];
+    uint32_t sc[4];
+    uint32_t cnt[kVqChunk / 64][2];
+    // refined vectors awaiting publication
+    uint32_t h_word0[kVqHeld], h_gid[kVqHeld];
+    float h_ex[kVqHeld], h_low[kVqHeld], h_rd[kVqHeld], h_err[kVqHeld];
+    // the query's current top-k (double buffered): order_key(rd) << 32 | position
+    unsigned long long t_key[2][kVanguardMaxTopk];
+    float t_err[2][kVanguardMaxTopk], t_low[2][kVanguardMaxTopk];
+    // results of the current chunk (~0 key: not refined)
+    unsigned long long c_key[kVqChunk];
+    float c_err[kVqChunk], c_low[kVqChunk];
+    // candidate list: lower bound and position of vectors below the threshold
+    float l_low[kVqList];
+    uint32_t l_pos[kVqList];
+    float thr;
+    uint32_t nheld, kc, tb, nlist;
+    unsigned long long base, limit;
+};
+
+// Append list index i to the window when take (wave-level compaction, one LDS atomic
+// per wave); entries beyond the window capacity are left for a later window.
+__device__ __forceinline__ void append_window(VqShared &S, uint32_t i, bool take) {
+    const uint32_t lane = threadIdx.x & 63;
+    const unsigned long long m = __ballot(take);
+    if (m == 0)
+        return;
+    uint32_t base = 0;
+    if (lane == 0)
+        base = atomicAdd(&S.sc[2], (uint32_t)__popcll(m));
+    base = __builtin_amdgcn_readfirstlane(base);
+    const uint32_t slot = base + lane_rank(m);
+    if (take && slot < kVqWin)
+        S.win[slot] = i;
+}
+
+// Publish the held refined vectors whose distance is within their rounding bound of the
+// current threshold (one ring reservation per round of 256), count the others as dropped.
+__device__ void publish_held(VqShared &S, const QueueDev &q, uint32_t &dropped) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float thr = S.thr;
+    const uint32_t nheld = S.nheld;
+    for (uint32_t r0 = 0; r0 < nheld; r0 += kVqThreads) {
+        const uint32_t i = r0 + tid;
+        bool pub = false;
+        if (i < nheld) {
+            const float rd = S.h_rd[i];
+            pub = rd <= thr + S.h_err[i];
+            dropped += (!pub && !isnan(rd)) ? 1u : 0u;
+        }
+        const unsigned long long m = __ballot(pub);
+        if (lane == 0)
+            S.red[wave] = (uint32_t)__popcll(m);
+        __syncthreads();
+        uint32_t before = 0, total = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < (uint32_t)kVqWaves; ++w) {
+            before += w < wave ? S.red[w] : 0u;
+            total += S.red[w];
+        }
+        if (total != 0) {
+            if (tid == 0) {
+                const unsigned long long b = atomicAdd(q.produced, (unsigned long long)total);
+                unsigned long long lim = S.limit;
+                if (b + total > lim)
+                    lim = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released,
+                                        q.capacity, b + total);
+                S.base = b;
+                S.limit = lim;
+            }
+            __syncthreads();
+            if (pub)
+                place_record(q, S.base + before + lane_rank(m), S.limit,
+                             make_uint4(S.h_word0[i], S.h_gid[i], __float_as_uint(S.h_ex[i]),
+                                        __float_as_uint(S.h_low[i])));
+        }
+        __syncthreads();  // S.red / S.base reused by the next round
+    }
+    if (tid == 0)
+        S.nheld = 0;
+    __syncthreads();
+}
+
+template <int W>
+__global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanParams p,
+                                                                   const VanguardArgs va) {
+    extern __shared__ __align__(16) float s_dyn[];  // q' [P]
+    __shared__ VqShared S;
+    constexpr int K = Words<W>::kMax;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t qi = blockIdx.x;
+    const uint32_t V = va.depth, topk = va.topk;
+    const uint32_t P = p.P, nw = W > 0 ? (uint32_t)W : P / 32;
+    const QueueDev q = p.queue;
+    float *s_q = s_dyn;
+
+    // ---- set-up: pair metadata, q-planes and q' in LDS ----
+    if (tid < V) {
+        const size_t pi = (size_t)qi * p.nprobe + tid;
+        const ClusterMeta cm = p.meta[va.probe_idx[pi]];
+        S.start[tid] = cm.start;
+        S.n[tid] = cm.n;
+        S.tbase[tid] = cm.tile_base;
+        S.gadd[tid] = p.pgadd[pi];
+        S.gerr[tid] = p.pgerr[pi];
+    }
+    for (uint32_t i = tid; i < 2 * kBq * nw; i += kVqThreads)
+        S.planes[i] = p.qplanes[(size_t)qi * 2 * kBq * nw + i];
+    for (uint32_t i = tid; i < P; i += kVqThreads)
+        s_q[i] = p.qrot[(size_t)qi * P + i];
+    if (tid == 0) {
+        S.thr = p.thresholds[qi];
+        S.nheld = 0;
+        S.kc = 0;
+        S.tb = 0;
+        S.nlist = 0;
+        S.limit = __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t o = 0, to = 0;
+        for (uint32_t j = 0; j < V; ++j) {
+            S.off[j] = o;
+            S.toff[j] = to;
+            o += S.n[j];
+            to += (S.n[j] + kTileVectors - 1) / kTileVectors;
+        }
+        S.off[V] = o;
+        S.toff[V] = to;
+    }
+    __syncthreads();
+    const uint32_t T = S.toff[V];
+    const float thr_in = S.thr;
+    const float width = p.qwidth[qi], width2 = p.qwidth2[qi], k1 = p.k1[qi], kbq = p.kb[qi];
+
+    // ---- lower bounds streamed into the candidate list, refined when it fills ----
+    uint32_t preg[W > 0 && W <= 4 ? kBq * W : 1];
+    if constexpr (W > 0 && W <= 4) {
+#pragma unroll
+        for (int i = 0; i < kBq * W; ++i)
+            preg[i] = uniform(S.planes[i]);
+    }
+    auto tile_at = [&](uint32_t t, uint32_t &j) -> const uint8_t * {
+        while (t >= S.toff[j + 1])
+            ++j;
+        return p.tiles + (size_t)(S.tbase[j] + t - S.toff[j]) * p.tile_bytes;
+    };
+    const size_t lc = (size_t)P * 7 / 8;
+    uint32_t dropped = 0, refined = 0;
+    auto process_list = [&]() {
+        const uint32_t nl = S.nlist;
+        for (;;) {
+            const float thr0 = S.thr;
+            const bool seeding = S.kc < topk;
+            // window: the remaining bounds below the threshold, up to kVqWin of them; while
+            // fewer than topk vectors are refined, only the kVqChunk smallest (all keys up
+            // to the selected one), which then set the first threshold
+            if (tid == 0)
+                S.sc[2] = 0;
+            __syncthreads();
+            for (uint32_t i0 = 0; i0 < nl; i0 += kVqThreads) {
+                const uint32_t i = i0 + tid;
+                append_window(S, i, i < nl && S.l_low[i] < thr0);
+            }
+            __syncthreads();
+            const uint32_t cnt = S.sc[2];
+            if (cnt == 0)
+                break;
+            if (seeding && cnt > kVqChunk) {
+                const uint32_t kth = block_select([&](uint32_t i) -> float { return S.l_low[i]; }, nl,
+                                                  thr0, kVqChunk, S.hist, S.red, S.sc);
+                if (tid == 0)
+                    S.sc[2] = 0;
+                __syncthreads();
+                for (uint32_t i0 = 0; i0 < nl; i0 += kVqThreads) {
+                    const uint32_t i = i0 + tid;
+                    const float l = i < nl ? S.l_low[i] : processed_mark();
+                    append_window(S, i, l < thr0 && order_key(l) <= kth);
+                }
+                __syncthreads();
+            }
+            const uint32_t nwin = min(S.sc[2], kVqWin);
+            for (uint32_t c0 = 0; c0 < nwin; c0 += kVqChunk) {
+                const float thr = S.thr;
+                if (S.nheld + kVqChunk > kVqHeld)
+                    publish_held(S, q, dropped);
+                const uint32_t cn = min(kVqChunk, nwin - c0);
+                const uint32_t held0 = S.nheld;
+                {
+                    // vector e of the chunk on lanes 2e, 2e+1; each lane takes every other code
+                    // word and every other 8-dimension ex-code chunk, so all loads of the chunk
+                    // are in flight together
+                    const uint32_t e = tid >> 1, sub = tid & 1;
+                    const uint32_t li = e < cn ? S.win[c0 + e] : 0u;
+                    const float low = e < cn ? S.l_low[li] : processed_mark();
+                    const bool have = low < thr;
+                    const uint32_t pos = have ? S.l_pos[li] : 0u;
+                    uint32_t j = 0;
+                    while (have && pos >= S.off[j + 1])
+                        ++j;
+                    const uint32_t local = pos - S.off[j];
+                    const uint8_t *tile =
+                        p.tiles + (size_t)(S.tbase[j] + local / kTileVectors) * p.tile_bytes;
+                    const uint32_t vl = local % kTileVectors;
+                    const size_t gid = (size_t)S.start[j] + local;
+                    const uint8_t *code = p.ex_codes + gid * lc;
+                    int ipa = 0, ipb = 0;
+                    float ipx = 0.0f, l1 = 0.0f, fa = 0.0f, fr = 0.0f;
+                    if (have) {
+                        if (sub == 0) {
+                            fa = p.ex_factors[2 * gid];
+                            fr = p.ex_factors[2 * gid + 1];
+                        }
+                        constexpr int kWl = W > 0 ? (W + 1) / 2 : kVqMaxW / 2;
+#pragma unroll
+                        for (int i = 0; i < kWl; ++i) {
+                            const uint32_t w = sub + 2 * i;
+                            if (w < nw) {
+                                const uint32_t *wp =
+                                    (nw & 3u) == 2u && w >= nw - 2
+                                        ? reinterpret_cast<const uint32_t *>(tile + (size_t)(nw / 4) * 1024 +
+                                                                             vl * 8 + (w & 1u) * 4)
+                                        : reinterpret_cast<const uint32_t *>(tile + (size_t)(w / 4) * 1024 +
+                                                                             vl * 16 + (w & 3u) * 4);
+                                const uint32_t xw = *wp;
+#pragma unroll
+                                for (int b = 0; b < kBq - 1; ++b) {
+                                    ipa += __popc(xw & S.planes[b * nw + w]) << b;
+                                    ipb += __popc(xw & S.planes[(kBq + b) * nw + w]) << b;
+                                }
+                                ipa -= __popc(xw & S.planes[(kBq - 1) * nw + w]) << (kBq - 1);
+                                ipb -= __popc(xw & S.planes[(2 * kBq - 1) * nw + w]) << (kBq - 1);
+                            }
+                        }
+                        constexpr int kCl = W > 0 ? 2 * W : 2 * kVqMaxW;  // P/8 chunks over 2 lanes
+#pragma unroll 8
+                        for (int i = 0; i < kCl; ++i) {
+                            const uint32_t c = sub + 2 * i;
+                            if (c < P / 8)
+                                ipx += excode_chunk_ip(code, s_q, c, l1);
+                        }
+                    }
+                    ipa += __shfl_xor(ipa, 1, 2);
+                    ipb += __shfl_xor(ipb, 1, 2);
+                    ipx += __shfl_xor(ipx, 1, 2);
+                    l1 += __shfl_xor(l1, 1, 2);
+                    if (sub == 0 && e < kVqChunk) {
+                        if (!have) {
+                            S.c_key[e] = ~0ull;
+                            if (e < cn)
+                                S.h_rd[held0 + e] = processed_mark();
+                        } else {
+                            const float ex = two_stage_ip(width, ipa, width2, ipb);
+                            const float gadd = S.gadd[j];
+                            const float rd = fa + gadd + fr * (128.0f * ex + ipx + kbq);
+                            const float err =
+                                1e-4f * (fabsf(fa) + fabsf(gadd) +
+                                         fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq)));
+                            S.c_key[e] = ((unsigned long long)order_key(rd) << 32) | pos;
+                            S.c_err[e] = err;
+                            S.c_low[e] = low;
+                            const uint32_t h = held0 + e;
+                            S.h_word0[h] = (j << 16) | qi;
+                            S.h_gid[h] = (uint32_t)gid;
+                            S.h_ex[h] = ex;
+                            S.h_low[h] = low;
+                            S.h_rd[h] = rd;
+                            S.h_err[h] = err;
+                        }
+                    }
+                }
+                __syncthreads();
+                // merge the chunk into the top-k (rank = entries with a smaller key) when any of
+                // its vectors enters it
+                const uint32_t kc = S.kc, tb = S.tb;
+                if (wave < kVqChunk / 64) {
+                    const unsigned long long key = S.c_key[tid];
+                    const unsigned long long worst = kc == topk ? S.t_key[tb][topk - 1] : ~0ull;
+                    const unsigned long long vm = __ballot(key != ~0ull);
+                    const unsigned long long em = __ballot(key != ~0ull && key < worst);
+                    if (lane == 0) {
+                        S.cnt[wave][0] = (uint32_t)__popcll(vm);
+                        S.cnt[wave][1] = (uint32_t)__popcll(em);
+                    }
+                }
+                __syncthreads();
+                uint32_t valid = 0, enter = 0;
+#pragma unroll
+                for (uint32_t w = 0; w < kVqChunk / 64; ++w) {
+                    valid += S.cnt[w][0];
+                    enter += S.cnt[w][1];
+                }
+                refined += valid;
+                if (enter) {
+                    for (uint32_t i = tid; i < kc + kVqChunk; i += kVqThreads) {
+                        unsigned long long key;
+                        float err, low;
+                        uint32_t rank = 0;
+                        if (i < kc) {
+                            key = S.t_key[tb][i];
+                            err = S.t_err[tb][i];
+                            low = S.t_low[tb][i];
+                            rank = i;
+                        } else {
+                            const uint32_t e = i - kc;
+                            key = S.c_key[e];
+                            if (key == ~0ull)
+                                continue;
+                            err = S.c_err[e];
+                            low = S.c_low[e];
+                            uint32_t lo = 0, hi = kc;  // top-k keys below key (sorted)
+                            while (lo < hi) {
+                                const uint32_t mid = (lo + hi) >> 1;
+                                if (S.t_key[tb][mid] < key)
+                                    lo = mid + 1;
+                                else
+                                    hi = mid;
+                            }
+                            rank = lo;
+                        }
+                        for (uint32_t e = 0; e < kVqChunk; ++e)
+                            rank += S.c_key[e] < key ? 1u : 0u;
+                        if (rank < topk) {
+                            S.t_key[tb ^ 1][rank] = key;
+                            S.t_err[tb ^ 1][rank] = err;
+                            S.t_low[tb ^ 1][rank] = low;
+                        }
+                    }
+                    __syncthreads();
+                    const uint32_t kn = min(topk, kc + valid);
+                    if (kn == topk) {
+                        // threshold backed by the k best: max(d_k + e, l) + 1 ulp
+                        uint32_t ekey = 0, lkey = 0;
+                        if (tid < topk) {
+                            ekey = __float_as_uint(S.t_err[tb ^ 1][tid]);  // >= 0: bits order like values
+                            lkey = order_key(S.t_low[tb ^ 1][tid]);
+                        }
+                        ekey = block_max(ekey, S.red);
+                        lkey = block_max(lkey, S.red);
+                        if (tid == 0) {
+                            const float dk = key_to_float((uint32_t)(S.t_key[tb ^ 1][topk - 1] >> 32));
+                            const float t =
+                                nextafterf(fmaxf(dk + __uint_as_float(ekey), key_to_float(lkey)), FLT_MAX);
+                            if (t < S.thr)
+                                S.thr = t;
+                        }
+                    }
+                    if (tid == 0) {
+                        S.kc = kn;
+                        S.tb = tb ^ 1;
+                    }
+                }
+                if (tid == 0)
+                    S.nheld = held0 + cn;
+                __syncthreads();
+            }
+            // every window entry is done: refined, or at/above the threshold
+            for (uint32_t i = tid; i < nwin; i += kVqThreads)
+                S.l_low[S.win[i]] = processed_mark();
+            __syncthreads();
+        }
+
+    };
+    // tiles t + 4, ..., t + 4 * kAhead of this wave are in flight while tile t is
+    // evaluated; every kVqSegTiles tiles per wave the list is refined once it holds
+    // kVqHigh entries
+    constexpr int kAhead = W > 0 && W <= 8 ? 3 : 1;
+    struct TileRegs {
+        uint32_t x[K];
+        float fa, fr, fe;
+        uint32_t j;
+    };
+    TileRegs buf[kAhead + 1];
+    uint32_t jf = 0;  // pair of the last fetched tile (fetches are in increasing order)
+    auto fetch = [&](uint32_t tt, TileRegs &r) {
+        const uint8_t *tile = tile_at(tt < T ? tt : T - 1, jf);
+        load_codes<W>(tile, lane, nw, r.x);
+        const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
+        r.fa = fac[lane];
+        r.fr = fac[64 + lane];
+        r.fe = fac[128 + lane];
+        r.j = jf;
+    };
+    uint32_t t = wave;
+    if (t < T) {
+#pragma unroll
+        for (int a = 0; a <= kAhead; ++a)
+            fetch(t + a * kVqWaves, buf[a]);
+    }
+    const uint32_t nseg = (T + kVqWaves * kVqSegTiles - 1) / (kVqWaves * kVqSegTiles);
+    for (uint32_t seg = 0; seg < nseg; ++seg) {
+        const float cut = S.thr;
+        const uint32_t seg_end = min(T, (seg + 1) * kVqWaves * kVqSegTiles);
+        for (; t < seg_end; t += kVqWaves) {
+            const uint32_t j = buf[0].j;
+            int ip;
+            if constexpr (W > 0 && W <= 4)
+                ip = popc_ip<W>(buf[0].x, preg, nw);
+            else
+                ip = popc_ip<W>(buf[0].x, S.planes, nw);
+            const float ex = width * (float)ip;
+            const float low = buf[0].fa + S.gadd[j] + buf[0].fr * (ex + k1) - buf[0].fe * S.gerr[j];
+            const uint32_t local = (t - S.toff[j]) * kTileVectors + lane;
+            const bool pass = local < S.n[j] && low < cut;
+            const unsigned long long m = __ballot(pass);
+            if (m) {
+                uint32_t base = 0;
+                if (lane == 0)
+                    base = atomicAdd(&S.nlist, (uint32_t)__popcll(m));
+                base = uniform(base);
+                if (pass) {
+                    const uint32_t k = base + lane_rank(m);
+                    S.l_low[k] = low;
+                    S.l_pos[k] = S.off[j] + local;
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < kAhead; ++a)
+                buf[a] = buf[a + 1];
+            if (t + (kAhead + 1) * kVqWaves < T)
+                fetch(t + (kAhead + 1) * kVqWaves, buf[kAhead]);
+        }
+        __syncthreads();
+        if (S.nlist >= kVqHigh || seg + 1 == nseg) {
+            process_list();
+            if (tid == 0)
+                S.nlist = 0;
+            __syncthreads();
+        }
+    }
+
+    // ---- 3. publication and the query's threshold ----
+    publish_held(S, q, dropped);
+    dropped = block_sum(dropped, S.red);
+    if (tid == 0) {
+        if (dropped)
+            atomicAdd(p.dropped, (unsigned long long)dropped);
+        if (refined)
+            atomicAdd(va.refined, (unsigned long long)refined);
+        const float thr = S.thr;
+        if (S.kc == topk && thr < thr_in) {
+            uint32_t *slot = reinterpret_cast<uint32_t *>(va.thr_out) + qi;
+            uint32_t cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            while (thr < __uint_as_float(cur)) {
+                if (__hip_atomic_compare_exchange_strong(slot, &cur, __float_as_uint(thr),
+                                                         __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_SYSTEM))
+                    break;
+            }
+            atomicAdd(va.seeded, 1ull);
+        }
+    }
+}
+
+template <int W>
+void launch_vq_w(const ScanParams &p, const VanguardArgs &va, uint32_t nq, hipStream_t s) {
+    const size_t dyn = (size_t)p.P * sizeof(float);
+    vanguard_query_kernel<W><<<nq, kVqThreads, dyn, s>>>(p, va);
+}
+
+}  // namespace
+
+size_t vanguard_static_lds() { return sizeof(VqShared); }
+
+void launch_vanguard_query(const ScanParams &p, const VanguardArgs &va, uint32_t W, uint32_t nq,
+                           hipStream_t s) {
+    if (nq == 0 || va.depth == 0)
+        return;
+    switch (W) {
+    case 2: launch_vq_w<2>(p, va, nq, s); break;
+    case 4: launch_vq_w<4>(p, va, nq, s); break;
+    case 8: launch_vq_w<8>(p, va, nq, s); break;
+    case 24: launch_vq_w<24>(p, va, nq, s); break;
+    default: launch_vq_w<0>(p, va, nq, s); break;
+    }
+}
+
+}  // namespace cora

@@ -178,6 +178,7 @@ int cora_hybrid_stats_get(cora_hybrid *h, cora_hybrid_stats *out) {
     out->prefilter_dropped = x.get_last_prefilter_dropped();
     out->seed_ms = x.get_last_seed_ms();
     out->recovery_ms = x.get_last_recovery_ms();
+    out->gpu_refined = x.get_last_gpu_refined();
     return CORA_OK;
 }
 

@@ -248,6 +248,7 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
     last_prefilter_dropped_ = st.prefilter_dropped;
     last_seed_ms_ = st.seed_ms;
     last_recovery_ms_ = st.recovery_ms;
+    last_gpu_refined_ = st.gpu_refined;
     if (rc != CORA_OK)
         throw std::runtime_error(engine_error(engine_));
     if (profiling_enabled_) {

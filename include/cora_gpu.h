@@ -62,7 +62,11 @@ enum cora_search_flags {
     /* Do not use the refined pre-filter: with ex-codes in HBM the far and recovery passes
      * otherwise drop candidates whose refined distance (the CPU consumer's formula)
      * already exceeds their threshold by more than a rounding bound. */
-    CORA_FLAG_NO_GPU_PREFILTER = 1u << 5
+    CORA_FLAG_NO_GPU_PREFILTER = 1u << 5,
+    /* Run the vanguard pairs as the reference does, a per-pair seed pass followed by a
+     * recovery pass over each pair, instead of the fused per-query vanguard pass that is
+     * used when the ex-codes are resident in HBM (vanguard depth <= 64, topk <= 128). */
+    CORA_FLAG_PAIR_SEEDS = 1u << 6
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -104,8 +108,10 @@ typedef struct cora_search_stats {
                                   far-pair and recovery passes (cumulative) */
     uint64_t seeded_queries;   /* queries that received a GPU seed threshold */
     uint64_t prefilter_dropped; /* candidates the refined pre-filter dropped */
-    float seed_ms;          /* vanguard seed pass + seed thresholds (FILTER_TIMING only) */
-    float recovery_ms;      /* vanguard recovery pass (FILTER_TIMING only) */
+    float seed_ms;          /* vanguard seed pass + seed thresholds, or the fused vanguard
+                               pass (FILTER_TIMING only) */
+    float recovery_ms;      /* vanguard recovery pass (FILTER_TIMING only; 0 when fused) */
+    uint64_t gpu_refined;   /* vectors the fused vanguard pass refined on the GPU */
 } cora_search_stats;
 
 /* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */

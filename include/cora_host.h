@@ -61,6 +61,7 @@ typedef struct cora_hybrid_stats {
     uint64_t prefilter_dropped; /* candidates the GPU refined pre-filter dropped */
     float seed_ms;        /* vanguard seed pass + seed thresholds */
     float recovery_ms;    /* vanguard recovery pass */
+    uint64_t gpu_refined; /* vectors the fused vanguard pass refined on the GPU */
 } cora_hybrid_stats;
 
 int cora_hybrid_create(cora_hybrid **out, int device);                 /* HybridIndex() */

@@ -308,16 +308,18 @@ def test_batch_q_and_reuse_do_not_change_results(synth, batch_q):
     assert np.allclose(d, d0, rtol=1e-6)
 
 
-@pytest.mark.parametrize("gpu_seed", [True, False])
-def test_live_thresholds_match_frozen_results(synth, gpu_seed):
-    """Default production mode (live thresholds, secondary filter, vanguard 5, with or
-    without GPU seed thresholds) returns the same top-k as the exhaustive frozen search,
-    except where refine distances tie."""
+@pytest.mark.parametrize("mode", ["fused", "pair", "none"])
+def test_live_thresholds_match_frozen_results(synth, mode):
+    """Default production mode (live thresholds, secondary filter, vanguard 5; the fused
+    vanguard pass, the per-pair seed and recovery passes, or no GPU seed thresholds)
+    returns the same top-k as the exhaustive frozen search, except where refine distances
+    tie."""
     nprobe, topk = 16, 10
-    say(f"[gpu] live vs frozen, gpu_seed={gpu_seed}")
+    say(f"[gpu] live vs frozen, vanguard mode {mode}")
     _, d0, i0 = run_frozen(synth, nprobe, topk, vanguard=0)
     eng = make_engine(synth, nprobe, topk, vanguard=5, frozen=False, secondary=True,
-                      gpu_seed_refine=gpu_seed)
+                      gpu_seed_refine=mode != "none",
+                      extra_flags=ca.FLAG_PAIR_SEEDS if mode == "pair" else 0)
     eng.reset_buffer(synth.queries)
     d, i = eng.search(synth.queries, topk, nprobe, 4)
     st = eng.stats()
@@ -329,7 +331,8 @@ def test_live_thresholds_match_frozen_results(synth, gpu_seed):
 
 @pytest.mark.parametrize("prefilter", [False, True])
 def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
-    """GPU ex-code stages in their deterministic test mode (frozen snapshot lowered by the
+    """Per-pair vanguard passes (the reference's structure), GPU ex-code stages in their
+    deterministic test mode (frozen snapshot lowered by the
     seed thresholds): seed choice and refined seed distances vs the oracle, the seeded
     threshold vs the oracle's rule and its safety, the candidate count of the far and
     recovery passes against it (with the refined pre-filter: low below the threshold and
@@ -341,7 +344,8 @@ def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
     case = synth
     nq, P = case.queries.shape[0], case.file.padded_dim
     eng = make_engine(case, nprobe, topk, vanguard=van, frozen=True,
-                      extra_flags=ca.FLAG_GPU_SEED_FROZEN, gpu_refine_filter=prefilter)
+                      extra_flags=ca.FLAG_GPU_SEED_FROZEN | ca.FLAG_PAIR_SEEDS,
+                      gpu_refine_filter=prefilter)
     eng.reset_buffer(case.queries)
     d, i = eng.search(case.queries, topk, nprobe)
     st = eng.stats()
@@ -437,6 +441,103 @@ def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
     # misses (low above the refined distance) differ
     ed, ei, cands = oracle_topk_from_gpu(case, g, nprobe, topk)
     assert st["submitted"] < sum(len(c) for c in cands)
+    same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), ei.tolist())])
+    say(f"[gpu]   candidates {st['submitted']} of {sum(len(c) for c in cands)}, top-k overlap {same:.4f}")
+    assert same >= 0.99, same
+
+
+def probed_vectors(case, g, q, nprobe):
+    """Every vector of the query's probed clusters: probe rank, global index, oracle lower
+    bound, refined distance (CPU formula) and its rounding bound."""
+    sd, P = case.sd, case.file.padded_dim
+    qint = qint_from_planes(g["planes"][q:q + 1, :8])[0]
+    qres = qint_from_planes(g["planes"][q:q + 1, 8:])[0]
+    l1 = float(np.abs(g["qr"][q]).sum())
+    out = []
+    for p in range(nprobe):
+        c = int(g["pidx"][q, p])
+        s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+        gid = s + np.arange(n)
+        ipi = orc.ip_int_direct(sd.bits[gid], qint)
+        f = sd.short_factors[gid]
+        low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p],
+                           orc.exact_ip_bitwise(ipi, g["width"][q]), g["k1"][q])
+        ex2 = orc.exact_ip_two_stage(ipi, orc.ip_int_direct(sd.bits[gid], qres), g["width"][q], g["width2"][q])
+        fa, fr = sd.ex_factors[gid, 0], sd.ex_factors[gid, 1]
+        rd = orc.refine_dist(fa, fr, g["gadd"][q, p], ex2, orc.excode_ip(g["qr"][q], sd.long_codes[gid], P),
+                             g["kb"][q], 7)
+        err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], 7)
+        out.append((p, gid, low.astype(np.float64), rd.astype(np.float64), err.astype(np.float64)))
+    return out
+
+
+@pytest.mark.parametrize("vanguard", [3, 8])
+def test_fused_vanguard_frozen_parity(synth, vanguard):
+    """Fused per-query vanguard pass in its deterministic test mode (frozen snapshot,
+    lowered by the pass): the threshold is backed by topk published vanguard vectors below
+    it; the vanguard pass publishes every vector with low and refined distance below the
+    threshold and nothing beyond its rounding bound; the far pass publishes exactly the
+    vectors with low < threshold and refined distance within the bound; the final top-k is
+    the top-k of that candidate set by the CPU consumer's distance."""
+    nprobe, topk = 8, 10
+    case = synth
+    nq = case.queries.shape[0]
+    say(f"[gpu] fused vanguard pass, frozen parity, vanguard={vanguard}")
+    eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True,
+                      extra_flags=ca.FLAG_GPU_SEED_FROZEN)
+    eng.reset_buffer(case.queries)
+    d, i = eng.search(case.queries, topk, nprobe)
+    st = eng.stats()
+    g = gpu_intermediates(eng, case, nprobe)
+    thr = eng.debug_read(ca.DBG_THRESHOLDS, (nq,), np.float32)
+    assert st["seeded_queries"] == nq
+    assert st["recovery_ms"] == 0.0
+    van_lo = van_hi = far_lo = far_hi = 0
+    sd = case.sd
+    for q in range(nq):
+        T = float(thr[q])
+        assert np.isfinite(T), q
+        band = 1e-5 * (abs(T) + 1)
+        vecs = probed_vectors(case, g, q, nprobe)
+        backing = 0
+        info = {}
+        for p, gid, low, rd, err in vecs:
+            if p < vanguard:
+                # the GPU's k best are within their rounding bound of the CPU's values, and
+                # the threshold sits above d_k plus the largest such bound
+                backing += int(((rd < T) & (low < T)).sum())
+                van_lo += int(((low < T - band) & (rd <= T + 0.9 * err)).sum())
+                van_hi += int((rd <= T + 1.1 * err).sum())
+            else:
+                far_lo += int(((low < T - band) & (rd <= T + 0.9 * err)).sum())
+                far_hi += int(((low < T + band) & (rd <= T + 1.1 * err)).sum())
+            for k in range(gid.size):
+                info[int(sd.ids[gid[k]])] = (p, low[k], rd[k], err[k])
+        assert backing >= topk, (q, backing)
+        # the returned list: oracle distances, at or below the threshold
+        scale = abs(T) + 1
+        for r in range(topk):
+            p, low, rd, err = info[int(i[q, r])]
+            assert abs(float(d[q, r]) - rd) <= 1e-5 * scale + err, (q, r)
+            # every candidate passed the filter: low below the threshold, or a vanguard
+            # vector refined before the threshold fell, within its bound of the threshold
+            assert low < T + band or (p < vanguard and rd <= T + 1.1 * err), (q, r)
+        assert float(d[q, topk - 1]) <= T + band, q
+        # completeness: every vector below the threshold closer than the returned k-th
+        got = set(i[q].tolist())
+        kth = float(d[q, topk - 1])
+        for pid, (p, low, rd, err) in info.items():
+            if low < T - band and rd < kth - 1e-5 * scale - 2 * err:
+                assert pid in got, (q, pid)
+    produced = st["pass_produced"]
+    say(f"[gpu]   vanguard published {produced[0]} in [{van_lo}, {van_hi}], far "
+        f"{produced[1] - produced[0]} in [{far_lo}, {far_hi}], refined on the GPU {st['gpu_refined']}")
+    assert van_lo <= produced[0] <= van_hi
+    assert far_lo <= produced[1] - produced[0] <= far_hi
+    assert produced[2] == produced[1]
+    assert st["gpu_refined"] >= produced[0]
+    # against the exhaustive search: only rare RaBitQ lower-bound misses differ
+    ed, ei, cands = oracle_topk_from_gpu(case, g, nprobe, topk)
     same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), ei.tolist())])
     say(f"[gpu]   candidates {st['submitted']} of {sum(len(c) for c in cands)}, top-k overlap {same:.4f}")
     assert same >= 0.99, same

@@ -100,13 +100,15 @@ def test_all_pass_wraps_threads_secondary_chunks(allpass, capacity, vanguard):
 
 
 @pytest.mark.parametrize("capacity", [8192, 262144])
-def test_all_pass_with_gpu_excode_stages(allpass, capacity):
-    """The same scenarios with the GPU seed thresholds and refined pre-filter on: fewer
-    candidates reach the CPU, the top-k and its distances are unchanged."""
-    say(f"[gpu] all-pass with GPU ex-code stages, capacity={capacity}")
+@pytest.mark.parametrize("pair_seeds", [False, True])
+def test_all_pass_with_gpu_excode_stages(allpass, capacity, pair_seeds):
+    """The same scenarios with the GPU ex-code stages on (the fused vanguard pass, or the
+    per-pair seed thresholds, and the refined pre-filter): fewer candidates reach the
+    CPU, the top-k and its distances are unchanged."""
+    say(f"[gpu] all-pass with GPU ex-code stages, capacity={capacity}, pair_seeds={pair_seeds}")
     for threads in (1, 16):
         e = allpass.engine(capacity, 262144, 5, gpu_seed_refine=True, gpu_refine_filter=True,
-                           cpu_threads=threads)
+                           cpu_threads=threads, extra_flags=ca.FLAG_PAIR_SEEDS if pair_seeds else 0)
         allpass.check(e, allpass.queries, 4, False, False)
         assert e.stats()["submitted"] < allpass.queries * allpass.count
         allpass.check(e, 2, 4, False, False)
