@@ -252,61 +252,89 @@ __device__ void block_exclusive_scan2(uint32_t &a, uint32_t &b, uint32_t *sa, ui
     __syncthreads();
 }
 
-// Per query: radix-select the key of the nprobe-th smallest distance (4 x 8-bit digits),
-// gather every smaller distance and the lowest-index ties in index order, then bitonic
-// sort (key, cluster) ascending in LDS.
+// Inclusive prefix sum over the block (thread order); s_red holds one word per wave.
+__device__ __forceinline__ uint32_t sel_incl_scan(uint32_t v, uint32_t *s_red) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(v, o);
+        if (lane >= (uint32_t)o)
+            v += y;
+    }
+    if (lane == 63)
+        s_red[wave] = v;
+    __syncthreads();
+    uint32_t add = 0;
+    for (uint32_t w = 0; w < wave; ++w)
+        add += s_red[w];
+    __syncthreads();
+    return v + add;
+}
+
+constexpr uint32_t kSelLdsRow = 8192;  // rows up to this many clusters are staged in LDS
+
+// Per query: radix-select the key of the nprobe-th smallest distance (4 x 8-bit digits,
+// each digit found by a block prefix sum over the 256-bin histogram), gather every
+// smaller distance and the lowest-index ties in index order, then bitonic sort
+// (key, cluster) ascending in LDS. With kLds the row's order keys are staged in LDS once.
+template <bool kLds>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(const float *__restrict__ dist,
                                                              uint32_t nl, uint32_t k,
                                                              uint32_t kpow2,
                                                              int32_t *__restrict__ out) {
     __shared__ uint32_t hist[256];
-    __shared__ uint32_t s_prefix, s_remaining;
+    __shared__ uint32_t s_red[kSelThreads / 64], s_sc[2];
     __shared__ uint32_t sa[kSelThreads], sb[kSelThreads];
-    extern __shared__ unsigned long long sel[];
+    extern __shared__ unsigned long long sel[];  // [kpow2], then the row's keys with kLds
+    uint32_t *keys = reinterpret_cast<uint32_t *>(sel + kpow2);
     const float *row = dist + (size_t)blockIdx.x * nl;
-    const int t = threadIdx.x;
-    uint32_t prefix = 0, pmask = 0;
-    if (t == 0) {
-        s_prefix = 0;
-        s_remaining = k;
+    const uint32_t t = threadIdx.x;
+    auto key_at = [&](uint32_t i) -> uint32_t {
+        if constexpr (kLds)
+            return keys[i];
+        else
+            return order_key(row[i]);
+    };
+    if constexpr (kLds) {
+        for (uint32_t i = t; i < nl; i += kSelThreads)
+            keys[i] = order_key(row[i]);
     }
+    uint32_t prefix = 0, pmask = 0, rem = k;
     for (int shift = 24; shift >= 0; shift -= 8) {
         hist[t] = 0;
         __syncthreads();
         for (uint32_t i = t; i < nl; i += kSelThreads) {
-            const uint32_t key = order_key(row[i]);
+            const uint32_t key = key_at(i);
             if ((key & pmask) == prefix)
                 atomicAdd(&hist[(key >> shift) & 255u], 1u);
         }
         __syncthreads();
-        if (t == 0) {
-            uint32_t rem = s_remaining, cum = 0, d = 0;
-            for (; d < 256; ++d) {
-                if (cum + hist[d] >= rem)
-                    break;
-                cum += hist[d];
-            }
-            s_remaining = rem - cum;
-            s_prefix = prefix | (d << shift);
+        const uint32_t h = hist[t];
+        const uint32_t incl = sel_incl_scan(h, s_red);
+        if (incl >= rem && incl - h < rem) {
+            s_sc[0] = t;
+            s_sc[1] = rem - (incl - h);
         }
         __syncthreads();
-        prefix = s_prefix;
+        prefix |= s_sc[0] << shift;
         pmask |= 255u << shift;
+        rem = s_sc[1];
+        __syncthreads();
     }
     const uint32_t kth = prefix;
-    const uint32_t take_eq = s_remaining;
+    const uint32_t take_eq = rem;
     const uint32_t chunk = (nl + kSelThreads - 1) / kSelThreads;
     const uint32_t begin = min(nl, t * chunk), end = min(nl, begin + chunk);
     uint32_t nless = 0, neq = 0;
     for (uint32_t i = begin; i < end; ++i) {
-        const uint32_t key = order_key(row[i]);
+        const uint32_t key = key_at(i);
         nless += key < kth;
         neq += key == kth;
     }
     uint32_t tot_less, tot_eq;
     block_exclusive_scan2(nless, neq, sa, sb, tot_less, tot_eq);
     for (uint32_t i = begin; i < end; ++i) {
-        const uint32_t key = order_key(row[i]);
+        const uint32_t key = key_at(i);
         if (key < kth) {
             sel[nless++] = ((unsigned long long)key << 32) | i;
         } else if (key == kth) {
@@ -409,8 +437,12 @@ void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
     uint32_t kp = 1;
     while (kp < nprobe)
         kp <<= 1;
-    select_kernel<<<nq, kSelThreads, kp * sizeof(unsigned long long), s>>>(dist, nl, nprobe, kp,
-                                                                            idx);
+    if (nl <= kSelLdsRow)
+        select_kernel<true><<<nq, kSelThreads, kp * sizeof(unsigned long long) + (size_t)nl * 4, s>>>(
+            dist, nl, nprobe, kp, idx);
+    else
+        select_kernel<false><<<nq, kSelThreads, kp * sizeof(unsigned long long), s>>>(dist, nl, nprobe,
+                                                                                     kp, idx);
 }
 
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,

@@ -23,6 +23,63 @@ __global__ void fill_u64_kernel(unsigned long long *p, unsigned long long v, siz
         p[i] = v;
 }
 
+// Bucket of pair i: cluster for vanguard pairs (probe rank < vanguard), nlist + cluster
+// for the rest.
+__device__ __forceinline__ uint32_t pair_bucket(const int32_t *__restrict__ probe_idx, size_t i,
+                                                uint32_t nprobe, uint32_t nlist, uint32_t vanguard) {
+    const uint32_t p = (uint32_t)(i % nprobe);
+    return (p >= vanguard ? nlist : 0u) + (uint32_t)probe_idx[i];
+}
+
+// Counting with a per-block LDS histogram over contiguous pair ranges, so a bucket takes
+// one global atomic per block instead of one per pair (popular clusters otherwise
+// serialise thousands of same-address atomics). Needs 2 * nlist <= kLdsBuckets.
+constexpr uint32_t kLdsBuckets = 16384;
+constexpr uint32_t kHistThreads = 1024;
+constexpr uint32_t kHistPairs = 4096;  // pairs per block
+
+__global__ __launch_bounds__(kHistThreads) void count_pairs_lds_kernel(
+    const int32_t *__restrict__ probe_idx, size_t np, uint32_t nprobe, uint32_t nlist,
+    uint32_t vanguard, uint32_t *__restrict__ count) {
+    extern __shared__ uint32_t h[];
+    const uint32_t nb = 2 * nlist, t = threadIdx.x;
+    for (uint32_t b = t; b < nb; b += kHistThreads)
+        h[b] = 0;
+    __syncthreads();
+    const size_t b0 = (size_t)blockIdx.x * kHistPairs, b1 = min(np, b0 + kHistPairs);
+    for (size_t i = b0 + t; i < b1; i += kHistThreads)
+        atomicAdd(&h[pair_bucket(probe_idx, i, nprobe, nlist, vanguard)], 1u);
+    __syncthreads();
+    for (uint32_t b = t; b < nb; b += kHistThreads)
+        if (h[b])
+            atomicAdd(&count[b], h[b]);
+}
+
+// Each block reserves one range per bucket it touches, then places its pairs in it.
+__global__ __launch_bounds__(kHistThreads) void scatter_pairs_lds_kernel(
+    const int32_t *__restrict__ probe_idx, size_t np, uint32_t nprobe, uint32_t nlist,
+    uint32_t vanguard, const uint32_t *__restrict__ bucket_offset, uint32_t *__restrict__ cursor,
+    Pair *__restrict__ pairs) {
+    extern __shared__ uint32_t h[];
+    const uint32_t nb = 2 * nlist, t = threadIdx.x;
+    for (uint32_t b = t; b < nb; b += kHistThreads)
+        h[b] = 0;
+    __syncthreads();
+    const size_t b0 = (size_t)blockIdx.x * kHistPairs, b1 = min(np, b0 + kHistPairs);
+    for (size_t i = b0 + t; i < b1; i += kHistThreads)
+        atomicAdd(&h[pair_bucket(probe_idx, i, nprobe, nlist, vanguard)], 1u);
+    __syncthreads();
+    for (uint32_t b = t; b < nb; b += kHistThreads)
+        if (h[b])
+            h[b] = bucket_offset[b] + atomicAdd(&cursor[b], h[b]);
+    __syncthreads();
+    for (size_t i = b0 + t; i < b1; i += kHistThreads) {
+        const uint32_t q = (uint32_t)(i / nprobe), p = (uint32_t)(i % nprobe);
+        const uint32_t pos = atomicAdd(&h[pair_bucket(probe_idx, i, nprobe, nlist, vanguard)], 1u);
+        pairs[pos] = Pair{(p << 16) | q, (uint32_t)probe_idx[i]};
+    }
+}
+
 __global__ void count_pairs_kernel(const int32_t *__restrict__ probe_idx, uint32_t nq,
                                    uint32_t nprobe, uint32_t nlist, uint32_t vanguard,
                                    uint32_t *__restrict__ count) {
@@ -175,12 +232,23 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
     launch_fill_u32(bucket_count, 0, 2 * (size_t)nlist, s);
     launch_fill_u32(bucket_cursor, 0, 2 * (size_t)nlist, s);
     const uint32_t grid = (uint32_t)((np + 255) / 256);
-    count_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard, bucket_count);
+    const bool lds = 2 * (size_t)nlist <= kLdsBuckets;
+    const uint32_t hgrid = (uint32_t)((np + kHistPairs - 1) / kHistPairs);
+    const size_t hbytes = 2 * (size_t)nlist * sizeof(uint32_t);
+    if (lds)
+        count_pairs_lds_kernel<<<hgrid, kHistThreads, hbytes, s>>>(probe_idx, np, nprobe, nlist, vanguard,
+                                                                  bucket_count);
+    else
+        count_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard, bucket_count);
     scan_buckets_kernel<<<1, kScanThreads, 0, s>>>(bucket_count, meta, nlist, batch_q,
                                                    bytes_per_vector, bucket_offset, unit_offset,
                                                    num_units, scan_stats);
-    scatter_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard,
-                                              bucket_offset, bucket_cursor, pairs);
+    if (lds)
+        scatter_pairs_lds_kernel<<<hgrid, kHistThreads, hbytes, s>>>(probe_idx, np, nprobe, nlist, vanguard,
+                                                                    bucket_offset, bucket_cursor, pairs);
+    else
+        scatter_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard,
+                                                  bucket_offset, bucket_cursor, pairs);
     build_units_kernel<<<(uint32_t)((max_units + 255) / 256), 256, 0, s>>>(
         bucket_offset, unit_offset, num_units, meta, nlist, batch_q, max_units, units);
 }
