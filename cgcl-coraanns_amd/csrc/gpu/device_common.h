@@ -98,29 +98,42 @@ __device__ __forceinline__ float two_stage_ip(float width, int ip, float width2,
 // hold the low six bits of dimensions 0..47, and in their top two bits the bit pairs of
 // dimensions 48..63 (bits 0-1 in bytes 0..15, 2-3 in 16..31, 4-5 in 32..47); the u64 at
 // bytes 48..55 holds bit 6 of dimension 8k+j at bit 8j+k. l1 accumulates sum |q'|.
+// kL1: also accumulate sum |q'| of the chunk into *l1. Unpacked in 32-bit halves (four
+// dimensions per word) so each code byte converts with one byte-to-float instruction.
+template <bool kL1 = true>
 __device__ __forceinline__ float excode_chunk_ip(const uint8_t *__restrict__ code,
                                                  const float *__restrict__ q, uint32_t c,
-                                                 float &l1) {
+                                                 float *l1 = nullptr) {
     const uint32_t g = c >> 3, k = c & 7;
-    const uint64_t *grp = reinterpret_cast<const uint64_t *>(code + (size_t)g * 56);
-    uint64_t v;
+    const uint2 *grp = reinterpret_cast<const uint2 *>(code + (size_t)g * 56);
+    uint32_t lo, hi;
     if (k < 6) {
-        v = grp[k] & 0x3F3F3F3F3F3F3F3Full;
+        const uint2 v = grp[k];
+        lo = v.x & 0x3F3F3F3Fu;
+        hi = v.y & 0x3F3F3F3Fu;
     } else {
         const uint32_t o = k - 6;
-        v = ((grp[o] >> 6) & 0x0303030303030303ull) | ((grp[2 + o] >> 4) & 0x0C0C0C0C0C0C0C0Cull) |
-            ((grp[4 + o] >> 2) & 0x3030303030303030ull);
+        const uint2 a = grp[o], b = grp[2 + o], d = grp[4 + o];
+        lo = ((a.x >> 6) & 0x03030303u) | ((b.x >> 4) & 0x0C0C0C0Cu) | ((d.x >> 2) & 0x30303030u);
+        hi = ((a.y >> 6) & 0x03030303u) | ((b.y >> 4) & 0x0C0C0C0Cu) | ((d.y >> 2) & 0x30303030u);
     }
-    v |= ((grp[6] >> k) & 0x0101010101010101ull) << 6;
+    const uint2 top = grp[6];
+    lo |= ((top.x >> k) & 0x01010101u) << 6;
+    hi |= ((top.y >> k) & 0x01010101u) << 6;
     const float4 q0 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k);
     const float4 q1 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k + 4);
-    const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        sum = fmaf((float)((v >> (8 * j)) & 0xFFu), qq[j], sum);
-        l1 += fabsf(qq[j]);
-    }
+    sum = fmaf((float)(lo & 0xFFu), q0.x, sum);
+    sum = fmaf((float)((lo >> 8) & 0xFFu), q0.y, sum);
+    sum = fmaf((float)((lo >> 16) & 0xFFu), q0.z, sum);
+    sum = fmaf((float)(lo >> 24), q0.w, sum);
+    sum = fmaf((float)(hi & 0xFFu), q1.x, sum);
+    sum = fmaf((float)((hi >> 8) & 0xFFu), q1.y, sum);
+    sum = fmaf((float)((hi >> 16) & 0xFFu), q1.z, sum);
+    sum = fmaf((float)(hi >> 24), q1.w, sum);
+    if constexpr (kL1)
+        *l1 += fabsf(q0.x) + fabsf(q0.y) + fabsf(q0.z) + fabsf(q0.w) + fabsf(q1.x) + fabsf(q1.y) +
+               fabsf(q1.z) + fabsf(q1.w);
     return sum;
 }
 

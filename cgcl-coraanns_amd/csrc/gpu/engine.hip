@@ -64,6 +64,7 @@ struct cora_gpu_engine {
     uint32_t *d_planes = nullptr, *d_bcount = nullptr, *d_bcursor = nullptr, *d_boff = nullptr,
              *d_uoff = nullptr, *d_nunits = nullptr, *d_cursor = nullptr, *d_seed = nullptr;
     int32_t *d_pidx = nullptr;
+    uint32_t *d_qorder = nullptr;  // queries by nearest cluster (fused vanguard pass)
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
     uint4 *d_seed_rec = nullptr;
     float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
@@ -185,6 +186,7 @@ void release_workspace(cora_gpu_engine *E) {
                          &E->d_nunits, &E->d_cursor, &E->d_seed})
         dfree(*p);
     dfree(E->d_pidx);
+    dfree(E->d_qorder);
     dfree(E->d_seed_dist);
     dfree(E->d_seed_low);
     dfree(E->d_seed_err);
@@ -492,6 +494,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_planes, max_q * 2 * kBq * E->W));
         TRY(dalloc(E, E->d_dist, max_q * E->nl));
         TRY(dalloc(E, E->d_pidx, np));
+        TRY(dalloc(E, E->d_qorder, max_q));
         TRY(dalloc(E, E->d_gadd, np));
         TRY(dalloc(E, E->d_gerr, np));
         TRY(dalloc(E, E->d_bcount, nb));
@@ -696,6 +699,9 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     E->last_fused = fused && depth > 0;
     if (fused) {
         va.probe_idx = E->d_pidx;
+        va.nq = nq;
+        va.order = launch_order_queries(E->d_pidx, nq, np, (uint32_t)E->nl, E->d_qorder, s) ? E->d_qorder
+                                                                                          : nullptr;
         va.depth = depth;
         va.topk = a->topk;
         va.thr_out = frozen ? E->d_thr_snap : E->h_thr;

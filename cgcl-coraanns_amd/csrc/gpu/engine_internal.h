@@ -146,6 +146,8 @@ struct ScanParams {
 // Fused vanguard pass (vanguard.hip): one workgroup per query over its vanguard pairs.
 struct VanguardArgs {
     const int32_t *probe_idx;      // [nq][nprobe] probed clusters, nearest first
+    const uint32_t *order;         // [nq] queries by nearest cluster (nullptr: identity)
+    uint32_t nq;
     uint32_t depth;                // vanguard pairs per query (probe ranks 0..depth-1)
     uint32_t topk;
     float *thr_out;                // thresholds lowered by the pass (host-coherent, or the
@@ -197,6 +199,10 @@ void launch_seed_thresholds(const float *seed_dist, const float *seed_low, const
                             hipStream_t s);
 // LDS bytes of the fused vanguard pass besides q' and the lower bounds
 size_t vanguard_static_lds();
+// order[0..nq) = queries sorted by their nearest probed cluster; false (nothing launched)
+// when nlist is above the kernel's LDS histogram
+bool launch_order_queries(const int32_t *probe_idx, uint32_t nq, uint32_t nprobe, uint32_t nlist,
+                          uint32_t *order, hipStream_t s);
 void launch_vanguard_query(const ScanParams &p, const VanguardArgs &va, uint32_t W, uint32_t nq,
                            hipStream_t s);
 // dev[0..n) = the host-coherent thresholds, read with system scope (the per-pass copy the

@@ -57,7 +57,7 @@ __device__ __forceinline__ float refine_one(const ScanParams &p, uint32_t query,
     const float *qv = p.qrot + (size_t)query * p.P;
     float ip = 0.0f, l1 = 0.0f;
     for (uint32_t c = 0; c < p.P / 8; ++c)
-        ip += excode_chunk_ip(code, qv, c, l1);
+        ip += excode_chunk_ip(code, qv, c, &l1);
     const float fa = p.ex_factors[2 * (size_t)gid], fr = p.ex_factors[2 * (size_t)gid + 1];
     const float gadd = p.pgadd[(size_t)query * p.nprobe + probe], kbq = p.kb[query];
     err = 1e-4f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq)));
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
                 const uint8_t *code = p.ex_codes + gid * lc;
                 float ip = 0.0f, l1 = 0.0f;
                 for (uint32_t c = sub; c < chunks; c += 16)
-                    ip += excode_chunk_ip(code, qv, c, l1);
+                    ip += excode_chunk_ip(code, qv, c, &l1);
 #pragma unroll
                 for (int o = 8; o > 0; o >>= 1) {
                     ip += __shfl_xor(ip, o, 16);

@@ -160,6 +160,10 @@ struct VqShared {
     // results of the current chunk (~0 key: not refined)
     unsigned long long c_key[kVqChunk];
     float c_err[kVqChunk], c_low[kVqChunk];
+    // the chunk's vectors entering the top-k
+    unsigned long long e_key[kVqChunk];
+    float e_err[kVqChunk], e_low[kVqChunk];
+    float l1;  // sum |q'| of the query
     // candidate list: lower bound and position of vectors below the threshold
     float l_low[kVqList];
     uint32_t l_pos[kVqList];
@@ -231,14 +235,23 @@ __device__ void publish_held(VqShared &S, const QueueDev &q, uint32_t &dropped) 
     __syncthreads();
 }
 
+// P <= 128: at most 168 VGPRs so three workgroups (12 waves) share a CU, which the LDS
+// footprint also allows
 template <int W>
-__global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanParams p,
-                                                                   const VanguardArgs va) {
+__global__ __launch_bounds__(kVqThreads, W > 0 && W <= 4 ? 3 : 1) void vanguard_query_kernel(
+    const ScanParams p, const VanguardArgs va) {
     extern __shared__ __align__(16) float s_dyn[];  // q' [P]
     __shared__ VqShared S;
     constexpr int K = Words<W>::kMax;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t qi = blockIdx.x;
+    // workgroup b runs on XCD b % 8 and takes the (b / 8)-th query of that XCD's slice of
+    // the queries ordered by nearest cluster, so each XCD's L2 serves about an eighth of
+    // the clusters
+    const uint32_t per_xcd = (va.nq + kNumXcd - 1) / kNumXcd;
+    const uint32_t slot = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+    if (slot >= va.nq)
+        return;
+    const uint32_t qi = va.order ? va.order[slot] : slot;
     const uint32_t V = va.depth, topk = va.topk;
     const uint32_t P = p.P, nw = W > 0 ? (uint32_t)W : P / 32;
     const QueueDev q = p.queue;
@@ -256,8 +269,12 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
     }
     for (uint32_t i = tid; i < 2 * kBq * nw; i += kVqThreads)
         S.planes[i] = p.qplanes[(size_t)qi * 2 * kBq * nw + i];
-    for (uint32_t i = tid; i < P; i += kVqThreads)
-        s_q[i] = p.qrot[(size_t)qi * P + i];
+    float l1p = 0.0f;
+    for (uint32_t i = tid; i < P; i += kVqThreads) {
+        const float v = p.qrot[(size_t)qi * P + i];
+        s_q[i] = v;
+        l1p += fabsf(v);
+    }
     if (tid == 0) {
         S.thr = p.thresholds[qi];
         S.nheld = 0;
@@ -281,20 +298,25 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
     __syncthreads();
     const uint32_t T = S.toff[V];
     const float thr_in = S.thr;
+    // sum |q'| for the rounding bound (the same for every vector of the query)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        l1p += __shfl_xor(l1p, o);
+    if (lane == 0)
+        S.red[wave] = __float_as_uint(l1p);
+    __syncthreads();
+    float l1q = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kVqWaves; ++w)
+        l1q += __uint_as_float(S.red[w]);
+    __syncthreads();
     const float width = p.qwidth[qi], width2 = p.qwidth2[qi], k1 = p.k1[qi], kbq = p.kb[qi];
 
     // ---- lower bounds streamed into the candidate list, refined when it fills ----
+    // W <= 4: the Bq=8 planes held in VGPRs during the tile stream (the same value in every
+    // lane; as SGPRs they would be spilled and re-read per tile), reloaded from LDS for
+    // every segment so they are not live across the list refinement
     uint32_t preg[W > 0 && W <= 4 ? kBq * W : 1];
-    if constexpr (W > 0 && W <= 4) {
-#pragma unroll
-        for (int i = 0; i < kBq * W; ++i)
-            preg[i] = uniform(S.planes[i]);
-    }
-    auto tile_at = [&](uint32_t t, uint32_t &j) -> const uint8_t * {
-        while (t >= S.toff[j + 1])
-            ++j;
-        return p.tiles + (size_t)(S.tbase[j] + t - S.toff[j]) * p.tile_bytes;
-    };
     const size_t lc = (size_t)P * 7 / 8;
     uint32_t dropped = 0, refined = 0;
     auto process_list = [&]() {
@@ -355,7 +377,7 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
                     const size_t gid = (size_t)S.start[j] + local;
                     const uint8_t *code = p.ex_codes + gid * lc;
                     int ipa = 0, ipb = 0;
-                    float ipx = 0.0f, l1 = 0.0f, fa = 0.0f, fr = 0.0f;
+                    float ipx = 0.0f, fa = 0.0f, fr = 0.0f;
                     if (have) {
                         if (sub == 0) {
                             fa = p.ex_factors[2 * gid];
@@ -383,17 +405,16 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
                             }
                         }
                         constexpr int kCl = W > 0 ? 2 * W : 2 * kVqMaxW;  // P/8 chunks over 2 lanes
-#pragma unroll 8
+#pragma unroll 4
                         for (int i = 0; i < kCl; ++i) {
                             const uint32_t c = sub + 2 * i;
                             if (c < P / 8)
-                                ipx += excode_chunk_ip(code, s_q, c, l1);
+                                ipx += excode_chunk_ip<false>(code, s_q, c);
                         }
                     }
                     ipa += __shfl_xor(ipa, 1, 2);
                     ipb += __shfl_xor(ipb, 1, 2);
                     ipx += __shfl_xor(ipx, 1, 2);
-                    l1 += __shfl_xor(l1, 1, 2);
                     if (sub == 0 && e < kVqChunk) {
                         if (!have) {
                             S.c_key[e] = ~0ull;
@@ -405,7 +426,7 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
                             const float rd = fa + gadd + fr * (128.0f * ex + ipx + kbq);
                             const float err =
                                 1e-4f * (fabsf(fa) + fabsf(gadd) +
-                                         fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq)));
+                                         fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
                             S.c_key[e] = ((unsigned long long)order_key(rd) << 32) | pos;
                             S.c_err[e] = err;
                             S.c_low[e] = low;
@@ -420,29 +441,38 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
                     }
                 }
                 __syncthreads();
-                // merge the chunk into the top-k (rank = entries with a smaller key) when any of
-                // its vectors enters it
+                // merge the chunk's entering vectors (refined, below the current k-th key) into
+                // the top-k: rank = entries with a smaller key
                 const uint32_t kc = S.kc, tb = S.tb;
+                const unsigned long long worst = kc == topk ? S.t_key[tb][topk - 1] : ~0ull;
+                unsigned long long ckey = ~0ull, em = 0;
                 if (wave < kVqChunk / 64) {
-                    const unsigned long long key = S.c_key[tid];
-                    const unsigned long long worst = kc == topk ? S.t_key[tb][topk - 1] : ~0ull;
-                    const unsigned long long vm = __ballot(key != ~0ull);
-                    const unsigned long long em = __ballot(key != ~0ull && key < worst);
+                    ckey = S.c_key[tid];
+                    const unsigned long long vm = __ballot(ckey != ~0ull);
+                    em = __ballot(ckey != ~0ull && ckey < worst);
                     if (lane == 0) {
                         S.cnt[wave][0] = (uint32_t)__popcll(vm);
                         S.cnt[wave][1] = (uint32_t)__popcll(em);
                     }
                 }
                 __syncthreads();
-                uint32_t valid = 0, enter = 0;
+                uint32_t valid = 0, enter = 0, before = 0;
 #pragma unroll
                 for (uint32_t w = 0; w < kVqChunk / 64; ++w) {
                     valid += S.cnt[w][0];
                     enter += S.cnt[w][1];
+                    before += w < wave ? S.cnt[w][1] : 0u;
                 }
                 refined += valid;
                 if (enter) {
-                    for (uint32_t i = tid; i < kc + kVqChunk; i += kVqThreads) {
+                    if (wave < kVqChunk / 64 && ((em >> lane) & 1ull)) {
+                        const uint32_t o = before + lane_rank(em);
+                        S.e_key[o] = ckey;
+                        S.e_err[o] = S.c_err[tid];
+                        S.e_low[o] = S.c_low[tid];
+                    }
+                    __syncthreads();
+                    for (uint32_t i = tid; i < kc + enter; i += kVqThreads) {
                         unsigned long long key;
                         float err, low;
                         uint32_t rank = 0;
@@ -453,11 +483,9 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
                             rank = i;
                         } else {
                             const uint32_t e = i - kc;
-                            key = S.c_key[e];
-                            if (key == ~0ull)
-                                continue;
-                            err = S.c_err[e];
-                            low = S.c_low[e];
+                            key = S.e_key[e];
+                            err = S.e_err[e];
+                            low = S.e_low[e];
                             uint32_t lo = 0, hi = kc;  // top-k keys below key (sorted)
                             while (lo < hi) {
                                 const uint32_t mid = (lo + hi) >> 1;
@@ -468,8 +496,8 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
                             }
                             rank = lo;
                         }
-                        for (uint32_t e = 0; e < kVqChunk; ++e)
-                            rank += S.c_key[e] < key ? 1u : 0u;
+                        for (uint32_t e = 0; e < enter; ++e)
+                            rank += S.e_key[e] < key ? 1u : 0u;
                         if (rank < topk) {
                             S.t_key[tb ^ 1][rank] = key;
                             S.t_err[tb ^ 1][rank] = err;
@@ -477,7 +505,7 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
                         }
                     }
                     __syncthreads();
-                    const uint32_t kn = min(topk, kc + valid);
+                    const uint32_t kn = min(topk, kc + enter);
                     if (kn == topk) {
                         // threshold backed by the k best: max(d_k + e, l) + 1 ulp
                         uint32_t ekey = 0, lkey = 0;
@@ -511,64 +539,95 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
         }
 
     };
-    // tiles t + 4, ..., t + 4 * kAhead of this wave are in flight while tile t is
-    // evaluated; every kVqSegTiles tiles per wave the list is refined once it holds
-    // kVqHigh entries
-    constexpr int kAhead = W > 0 && W <= 8 ? 3 : 1;
+    // kBufs tile buffers per wave in turn: tile t is evaluated from one while tiles
+    // t + 4, ..., t + 4 (kBufs - 1) are in flight into the others, then t + 4 kBufs is
+    // fetched into the first; every kVqSegTiles tiles per wave the list is refined once
+    // it holds kVqHigh entries
+    constexpr int kBufs = W > 0 && W <= 8 ? 4 : 2;
     struct TileRegs {
         uint32_t x[K];
         float fa, fr, fe;
-        uint32_t j;
+        // wave-uniform: the pair's g_add / g_error, the valid lanes of the tile and the
+        // list position of its lane 0
+        float gadd, gerr;
+        uint32_t lim, posbase;
     };
-    TileRegs buf[kAhead + 1];
-    uint32_t jf = 0;  // pair of the last fetched tile (fetches are in increasing order)
+    TileRegs bufs[kBufs];
+    // pair of the fetch cursor and its constants, wave-uniform (scalar registers); the
+    // fetches are in increasing tile order
+    uint32_t jf = 0, f_next = uniform(S.toff[1]), f_toff = 0, f_tbase = uniform(S.tbase[0]);
+    uint32_t f_n = uniform(S.n[0]), f_off = 0;
+    float f_gadd = uniformf(S.gadd[0]), f_gerr = uniformf(S.gerr[0]);
     auto fetch = [&](uint32_t tt, TileRegs &r) {
-        const uint8_t *tile = tile_at(tt < T ? tt : T - 1, jf);
+        while (tt >= f_next) {
+            ++jf;
+            f_toff = f_next;
+            f_next = uniform(S.toff[jf + 1]);
+            f_tbase = uniform(S.tbase[jf]);
+            f_n = uniform(S.n[jf]);
+            f_off = uniform(S.off[jf]);
+            f_gadd = uniformf(S.gadd[jf]);
+            f_gerr = uniformf(S.gerr[jf]);
+        }
+        const uint32_t lt = tt - f_toff;
+        const uint8_t *tile = p.tiles + (size_t)(f_tbase + lt) * p.tile_bytes;
         load_codes<W>(tile, lane, nw, r.x);
         const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
         r.fa = fac[lane];
         r.fr = fac[64 + lane];
         r.fe = fac[128 + lane];
-        r.j = jf;
+        r.gadd = f_gadd;
+        r.gerr = f_gerr;
+        r.lim = f_n - lt * kTileVectors;
+        r.posbase = f_off + lt * kTileVectors;
     };
     uint32_t t = wave;
-    if (t < T) {
 #pragma unroll
-        for (int a = 0; a <= kAhead; ++a)
-            fetch(t + a * kVqWaves, buf[a]);
-    }
+    for (int b = 0; b < kBufs; ++b)
+        if (t + b * kVqWaves < T)
+            fetch(t + b * kVqWaves, bufs[b]);
+    auto step = [&](TileRegs &cur, float cut) {
+        int ip;
+        if constexpr (W > 0 && W <= 4)
+            ip = popc_ip<W>(cur.x, preg, nw);
+        else
+            ip = popc_ip<W>(cur.x, S.planes, nw);
+        const float ex = width * (float)ip;
+        const float low = cur.fa + cur.gadd + cur.fr * (ex + k1) - cur.fe * cur.gerr;
+        const bool pass = lane < cur.lim && low < cut;
+        const unsigned long long m = __ballot(pass);
+        if (m) {
+            uint32_t base = 0;
+            if (lane == 0)
+                base = atomicAdd(&S.nlist, (uint32_t)__popcll(m));
+            base = uniform(base);
+            if (pass) {
+                const uint32_t k = base + lane_rank(m);
+                S.l_low[k] = low;
+                S.l_pos[k] = cur.posbase + lane;
+            }
+        }
+        if (t + kBufs * kVqWaves < T)
+            fetch(t + kBufs * kVqWaves, cur);
+        t += kVqWaves;
+    };
+    // a segment is kVqSegTiles (a multiple of kBufs) tiles per wave, so every segment
+    // starts on buffer 0 and the buffer of each step is a constant
+    static_assert(kVqSegTiles % kBufs == 0, "segments start on the first buffer");
     const uint32_t nseg = (T + kVqWaves * kVqSegTiles - 1) / (kVqWaves * kVqSegTiles);
     for (uint32_t seg = 0; seg < nseg; ++seg) {
         const float cut = S.thr;
         const uint32_t seg_end = min(T, (seg + 1) * kVqWaves * kVqSegTiles);
-        for (; t < seg_end; t += kVqWaves) {
-            const uint32_t j = buf[0].j;
-            int ip;
-            if constexpr (W > 0 && W <= 4)
-                ip = popc_ip<W>(buf[0].x, preg, nw);
-            else
-                ip = popc_ip<W>(buf[0].x, S.planes, nw);
-            const float ex = width * (float)ip;
-            const float low = buf[0].fa + S.gadd[j] + buf[0].fr * (ex + k1) - buf[0].fe * S.gerr[j];
-            const uint32_t local = (t - S.toff[j]) * kTileVectors + lane;
-            const bool pass = local < S.n[j] && low < cut;
-            const unsigned long long m = __ballot(pass);
-            if (m) {
-                uint32_t base = 0;
-                if (lane == 0)
-                    base = atomicAdd(&S.nlist, (uint32_t)__popcll(m));
-                base = uniform(base);
-                if (pass) {
-                    const uint32_t k = base + lane_rank(m);
-                    S.l_low[k] = low;
-                    S.l_pos[k] = S.off[j] + local;
-                }
-            }
+        if constexpr (W > 0 && W <= 4) {
 #pragma unroll
-            for (int a = 0; a < kAhead; ++a)
-                buf[a] = buf[a + 1];
-            if (t + (kAhead + 1) * kVqWaves < T)
-                fetch(t + (kAhead + 1) * kVqWaves, buf[kAhead]);
+            for (int i = 0; i < kBq * W; ++i)
+                preg[i] = S.planes[i];
+        }
+        for (uint32_t r = 0; r < kVqSegTiles / kBufs; ++r) {
+#pragma unroll
+            for (int b = 0; b < kBufs; ++b)
+                if (t < seg_end)
+                    step(bufs[b], cut);
         }
         __syncthreads();
         if (S.nlist >= kVqHigh || seg + 1 == nseg) {
@@ -605,12 +664,70 @@ __global__ __launch_bounds__(kVqThreads) void vanguard_query_kernel(const ScanPa
 template <int W>
 void launch_vq_w(const ScanParams &p, const VanguardArgs &va, uint32_t nq, hipStream_t s) {
     const size_t dyn = (size_t)p.P * sizeof(float);
-    vanguard_query_kernel<W><<<nq, kVqThreads, dyn, s>>>(p, va);
+    const uint32_t grid = (nq + kNumXcd - 1) / kNumXcd * kNumXcd;
+    vanguard_query_kernel<W><<<grid, kVqThreads, dyn, s>>>(p, va);
+}
+
+// Queries ordered by nearest probed cluster (counting sort in one workgroup; the order
+// inside a cluster is not fixed). nlist <= kOrderBins.
+constexpr uint32_t kOrderBins = 16384;
+constexpr uint32_t kOrderThreads = 1024;
+
+__global__ __launch_bounds__(kOrderThreads) void order_queries_kernel(const int32_t *__restrict__ probe_idx,
+                                                                      uint32_t nq, uint32_t nprobe,
+                                                                      uint32_t nlist,
+                                                                      uint32_t *__restrict__ order) {
+    extern __shared__ uint32_t h[];
+    __shared__ uint32_t s_red[kOrderThreads / 64];
+    const uint32_t t = threadIdx.x;
+    for (uint32_t c = t; c < nlist; c += kOrderThreads)
+        h[c] = 0;
+    __syncthreads();
+    for (uint32_t q = t; q < nq; q += kOrderThreads)
+        atomicAdd(&h[probe_idx[(size_t)q * nprobe]], 1u);
+    __syncthreads();
+    // exclusive scan: thread t owns bins [t * per, (t + 1) * per)
+    const uint32_t per = (nlist + kOrderThreads - 1) / kOrderThreads;
+    const uint32_t c0 = min(nlist, t * per), c1 = min(nlist, c0 + per);
+    uint32_t sum = 0;
+    for (uint32_t c = c0; c < c1; ++c)
+        sum += h[c];
+    const uint32_t lane = t & 63, wave = t >> 6;
+    uint32_t v = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(v, o);
+        if (lane >= (uint32_t)o)
+            v += y;
+    }
+    if (lane == 63)
+        s_red[wave] = v;
+    __syncthreads();
+    uint32_t base = v - sum;
+    for (uint32_t w = 0; w < wave; ++w)
+        base += s_red[w];
+    for (uint32_t c = c0; c < c1; ++c) {
+        const uint32_t n = h[c];
+        h[c] = base;
+        base += n;
+    }
+    __syncthreads();
+    for (uint32_t q = t; q < nq; q += kOrderThreads)
+        order[atomicAdd(&h[probe_idx[(size_t)q * nprobe]], 1u)] = q;
 }
 
 }  // namespace
 
 size_t vanguard_static_lds() { return sizeof(VqShared); }
+
+bool launch_order_queries(const int32_t *probe_idx, uint32_t nq, uint32_t nprobe, uint32_t nlist,
+                          uint32_t *order, hipStream_t s) {
+    if (nlist > kOrderBins || nq == 0)
+        return false;
+    order_queries_kernel<<<1, kOrderThreads, (size_t)nlist * sizeof(uint32_t), s>>>(probe_idx, nq, nprobe,
+                                                                                  nlist, order);
+    return true;
+}
 
 void launch_vanguard_query(const ScanParams &p, const VanguardArgs &va, uint32_t W, uint32_t nq,
                            hipStream_t s) {
