@@ -71,6 +71,20 @@ def cpu_baseline(index_path, queries, gt, topk, nprobe, threads, workdir):
                       f"same index file, rabitq_cpu --hacc true built -mavx2 -mfma"}
 
 
+def hbm_traffic(cfg, nprobe, kernel):
+    """HBM bytes per launch of the kernel (FETCH_SIZE + WRITE_SIZE, each scaled by the
+    reading of a 1 GiB copy) from the committed rocprofv3 summary of this workload, or
+    None when there is none."""
+    f = REPO / "profiles" / f"hbm_traffic_cfg{cfg}_nprobe{nprobe}.json"
+    if not f.exists():
+        return None
+    data = json.loads(f.read_text())
+    for name, v in data.get("kernels", {}).items():
+        if kernel in name:
+            return int(v["fetch_bytes"] + v["write_bytes"])
+    return None
+
+
 def copy_calibration():
     """A plain device-to-device copy of 1 GiB, 5 times: the reference kernel for scaling
     the FETCH_SIZE / WRITE_SIZE counters (each launch reads and writes 1 GiB)."""
@@ -174,6 +188,7 @@ def main():
     for _ in range(args.warmup):
         step(nprobe)
     times, times_up, scan_ms, scan_bytes, recalls, probe_ms, probe_flops = [], [], [], [], [], [], []
+    van_ms, van_bytes = [], []
     for _ in range(args.steps):
         dt, ids, st = step(nprobe)
         times.append(dt)
@@ -182,6 +197,8 @@ def main():
         probe_flops.append(st["probe_flops"])
         scan_ms.append(st["scan_ms"])
         scan_bytes.append(st["scan_bytes"])
+        van_ms.append(st["vanguard_ms"])
+        van_bytes.append(st["vanguard_bytes"])
         recalls.append(recall_at_k(ids, gt, c.topk))
     total = sum(times)
     qps = queries.shape[0] * args.steps / total
@@ -189,11 +206,35 @@ def main():
     avg_scan_ms = float(np.mean(scan_ms))
     bytes_per_launch = float(np.mean(scan_bytes))
     achieved = bytes_per_launch / (avg_scan_ms * 1e-3) / 1e9 if avg_scan_ms > 0 else 0.0
+    avg_van_ms = float(np.mean(van_ms))
+    van_bpl = float(np.mean(van_bytes))
+    van_achieved = van_bpl / (avg_van_ms * 1e-3) / 1e9 if avg_van_ms > 0 else 0.0
     avg_probe_ms = float(np.mean(probe_ms))
     probe_tflops = float(np.mean(probe_flops)) / (avg_probe_ms * 1e-3) / 1e12 if avg_probe_ms > 0 else 0.0
     log(f"[timed] nprobe={nprobe} steps={args.steps} QPS={qps:.1f} recall={np.mean(recalls):.4f} "
-        f"scan={avg_scan_ms:.3f}ms {bytes_per_launch / 1e6:.1f}MB -> {achieved:.1f} GB/s; "
+        f"vanguard={avg_van_ms:.3f}ms {van_bpl / 1e6:.1f}MB -> {van_achieved:.1f} GB/s; "
+        f"far scan={avg_scan_ms:.3f}ms {bytes_per_launch / 1e6:.1f}MB -> {achieved:.1f} GB/s; "
         f"probe GEMM {avg_probe_ms:.3f}ms -> {probe_tflops:.2f} TFLOP/s")
+
+    # the dominant scan kernel of the step (HIP events on the engine stream around it)
+    W = c.padded_dim // 32
+    kernels = {
+        "vanguard_query_kernel": {
+            "kernel": f"vanguard_query_kernel<{W}> (fused per-query vanguard pass: popcount lower bounds, "
+                      "GPU refinement, top-k threshold)",
+            "avg_launch_ms": round(avg_van_ms, 4), "bytes_per_launch": int(van_bpl), "achieved": van_achieved},
+        "scan_kernel": {
+            "kernel": f"scan_kernel<{W}, {8 if batch_q > 1 else 1}, 0> (far-pair RaBitQ popcount scan)",
+            "avg_launch_ms": round(avg_scan_ms, 4), "bytes_per_launch": int(bytes_per_launch),
+            "achieved": achieved},
+    }
+    dom = max(kernels, key=lambda k: kernels[k]["avg_launch_ms"])
+    d = kernels[dom]
+    roofline = {"bound": "hbm", "achieved": round(d["achieved"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(d["achieved"] / HBM_PEAK_GBPS, 4),
+                "traffic": hbm_traffic(args.config, nprobe, dom), "kernel": d["kernel"],
+                "bytes_per_launch": d["bytes_per_launch"], "avg_launch_ms": d["avg_launch_ms"],
+                "other": [dict(v, achieved=round(v["achieved"], 1)) for k, v in kernels.items() if k != dom]}
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -218,10 +259,7 @@ def main():
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
                    "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
                    "query_chunk": chunk, "sweep": sweep},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "scan_kernel<W=4,Q=1|8,far> (far-pair RaBitQ popcount scan)",
-                     "bytes_per_launch": int(bytes_per_launch), "avg_launch_ms": round(avg_scan_ms, 4)},
+        "roofline": roofline,
         "probe_mfma": {"kernel": "gemm_kernel<true> (coarse-probe L2 distances, v_mfma_f32_16x16x4f32)",
                        "flops_per_launch": int(np.mean(probe_flops)), "avg_launch_ms": round(avg_probe_ms, 4),
                        "achieved": round(probe_tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -80,7 +80,7 @@ class cora_search_stats(C.Structure):
                 ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float), ("probe_flops", C.c_uint64),
                 ("pass_produced", C.c_uint64 * 3), ("seeded_queries", C.c_uint64),
                 ("prefilter_dropped", C.c_uint64), ("seed_ms", C.c_float), ("recovery_ms", C.c_float),
-                ("gpu_refined", C.c_uint64)]
+                ("gpu_refined", C.c_uint64), ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64)]
 
 
 class cora_queue_view(C.Structure):
@@ -103,7 +103,8 @@ class cora_hybrid_stats(C.Structure):
                 ("scan_units", C.c_uint64), ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float),
                 ("probe_flops", C.c_uint64), ("pass_produced", C.c_uint64 * 3),
                 ("seeded_queries", C.c_uint64), ("prefilter_dropped", C.c_uint64),
-                ("seed_ms", C.c_float), ("recovery_ms", C.c_float), ("gpu_refined", C.c_uint64)]
+                ("seed_ms", C.c_float), ("recovery_ms", C.c_float), ("gpu_refined", C.c_uint64),
+                ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64)]
 
 
 class cora_ivf_info(C.Structure):

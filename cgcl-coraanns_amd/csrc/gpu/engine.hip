@@ -42,7 +42,8 @@ struct cora_gpu_engine {
     unsigned long long wall_clock_khz = 0;  // device wall_clock64() rate
     hipStream_t stream = nullptr, stream_d2h = nullptr;
     hipEvent_t ev_prep = nullptr, ev_probe = nullptr, ev_f0 = nullptr, ev_f1 = nullptr,
-               ev_s0 = nullptr, ev_s1 = nullptr, ev_p0 = nullptr, ev_p1 = nullptr;
+               ev_s0 = nullptr, ev_s1 = nullptr, ev_p0 = nullptr, ev_p1 = nullptr, ev_v0 = nullptr,
+               ev_v1 = nullptr;
     // index
     bool loaded = false;
     uint64_t N = 0, dim = 0, P = 0, nl = 0, ex_bits = 0, max_cluster = 0, total_tiles = 0;
@@ -275,7 +276,7 @@ int cora_gpu_create(cora_gpu_engine **out, int device) {
         HIPCHK(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
         HIPCHK(hipStreamCreateWithFlags(&E->stream_d2h, hipStreamNonBlocking));
         for (hipEvent_t *ev : {&E->ev_prep, &E->ev_probe, &E->ev_f0, &E->ev_f1, &E->ev_s0, &E->ev_s1,
-                               &E->ev_p0, &E->ev_p1})
+                               &E->ev_p0, &E->ev_p1, &E->ev_v0, &E->ev_v1})
             HIPCHK(hipEventCreate(ev));
         return CORA_OK;
     };
@@ -303,7 +304,7 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
     dfree(E->d_excodes);
     dfree(E->d_exfac);
     for (hipEvent_t ev : {E->ev_prep, E->ev_probe, E->ev_f0, E->ev_f1, E->ev_s0, E->ev_s1, E->ev_p0,
-                          E->ev_p1})
+                          E->ev_p1, E->ev_v0, E->ev_v1})
         if (ev)
             (void)hipEventDestroy(ev);
     if (E->stream)
@@ -503,7 +504,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_uoff, nb + 1));
         TRY(dalloc(E, E->d_nunits, 2));
         TRY(dalloc(E, E->d_cursor, kNumXcd));
-        TRY(dalloc(E, E->d_stats, 9));
+        TRY(dalloc(E, E->d_stats, 10));
         TRY(dalloc(E, E->d_pairs, np));
         TRY(dalloc(E, E->d_units, np * unit_splits((uint32_t)E->max_cluster)));
         TRY(dalloc(E, E->d_thr_snap, max_q));
@@ -718,7 +719,11 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     };
     if (depth > 0 && fused) {
         snapshot();
+        if (timing)
+            HIPCHK(hipEventRecord(E->ev_v0, s));
         launch_vanguard_query(p, va, E->W, nq, s);
+        if (timing)
+            HIPCHK(hipEventRecord(E->ev_v1, s));
     } else if (depth > 0) {
         launch_fill_u32(E->d_seed, 0u, (size_t)nq * depth * E->seed_words, s);
         snapshot();
@@ -780,7 +785,7 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     HIPCHK(hipSetDevice(E->device));
     HIPCHK(hipStreamSynchronize(E->stream));
     HIPCHK(hipStreamSynchronize(E->stream_d2h));
-    unsigned long long stats[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    unsigned long long stats[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     int stalled = 0;
     HIPCHK(hipMemcpy(stats, E->d_stats, sizeof(stats), hipMemcpyDeviceToHost));
     HIPCHK(hipMemcpy(&stalled, E->d_stalled, sizeof(int), hipMemcpyDeviceToHost));
@@ -799,14 +804,18 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     out.seeded_queries = stats[6];
     out.prefilter_dropped = stats[7];
     out.gpu_refined = stats[8];
+    if (E->last_fused)  // code + factors of every vanguard vector, then P/8 + 7P/8 + 8 per refined one
+        out.vanguard_bytes = stats[9] + stats[8] * (E->P + 8);
     if (E->last_timing) {
         HIPCHK(hipEventElapsedTime(&out.filter_ms, E->ev_f0, E->ev_f1));
         HIPCHK(hipEventElapsedTime(&out.scan_ms, E->ev_s0, E->ev_s1));
         HIPCHK(hipEventElapsedTime(&out.probe_ms, E->ev_p0, E->ev_p1));
         HIPCHK(hipEventElapsedTime(&out.seed_ms, E->ev_f0, E->ev_s0));
         HIPCHK(hipEventElapsedTime(&out.recovery_ms, E->ev_s1, E->ev_f1));
-        if (E->last_fused)
+        if (E->last_fused) {
             out.recovery_ms = 0.0f;  // no recovery pass
+            HIPCHK(hipEventElapsedTime(&out.vanguard_ms, E->ev_v0, E->ev_v1));
+        }
     }
     if (st)
         *st = out;

@@ -102,12 +102,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
     unsigned long long *__restrict__ stats) {
     __shared__ uint32_t s_pairs[kScanThreads], s_units[kScanThreads], s_van_units[kScanThreads];
     __shared__ unsigned long long s_bytes[kScanThreads], s_fu[kScanThreads], s_vec[kScanThreads];
+    __shared__ unsigned long long s_vbytes[kScanThreads];
     const uint32_t nb = 2 * nlist;
     const int t = threadIdx.x;
     const uint32_t chunk = (nb + kScanThreads - 1) / kScanThreads;
     const uint32_t b0 = min(nb, t * chunk), b1 = min(nb, b0 + chunk);
     uint32_t pairs = 0, units = 0, van_units = 0;
-    unsigned long long bytes = 0, fu = 0, vec = 0;
+    unsigned long long bytes = 0, fu = 0, vec = 0, vbytes = 0;
     for (uint32_t b = b0; b < b1; ++b) {
         const uint32_t m = count[b];
         pairs += m;
@@ -115,6 +116,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
         if (b < nlist) {
             units += m * sp;
             van_units += m * sp;
+            vbytes += (unsigned long long)m * n * bpv;  // vanguard pairs: one pass per pair
         } else {
             const uint32_t u = (m + batch_q - 1) / batch_q;
             units += u * sp;
@@ -129,12 +131,14 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
     s_bytes[t] = bytes;
     s_fu[t] = fu;
     s_vec[t] = vec;
+    s_vbytes[t] = vbytes;
     __syncthreads();
     for (int o = 1; o < kScanThreads; o <<= 1) {
         const uint32_t xp = t >= o ? s_pairs[t - o] : 0, xu = t >= o ? s_units[t - o] : 0;
         const uint32_t xv = t >= o ? s_van_units[t - o] : 0;
         const unsigned long long xb = t >= o ? s_bytes[t - o] : 0, xf = t >= o ? s_fu[t - o] : 0;
         const unsigned long long xe = t >= o ? s_vec[t - o] : 0;
+        const unsigned long long xvb = t >= o ? s_vbytes[t - o] : 0;
         __syncthreads();
         s_pairs[t] += xp;
         s_units[t] += xu;
@@ -142,6 +146,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
         s_bytes[t] += xb;
         s_fu[t] += xf;
         s_vec[t] += xe;
+        s_vbytes[t] += xvb;
         __syncthreads();
     }
     uint32_t po = s_pairs[t] - pairs, uo = s_units[t] - units;
@@ -161,6 +166,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
         stats[0] = s_bytes[t];
         stats[1] = s_fu[t];
         stats[2] = s_vec[t];
+        stats[9] = s_vbytes[t];
     }
 }
 

@@ -179,6 +179,8 @@ int cora_hybrid_stats_get(cora_hybrid *h, cora_hybrid_stats *out) {
     out->seed_ms = x.get_last_seed_ms();
     out->recovery_ms = x.get_last_recovery_ms();
     out->gpu_refined = x.get_last_gpu_refined();
+    out->vanguard_ms = x.get_last_vanguard_ms();
+    out->vanguard_bytes = x.get_last_vanguard_bytes();
     return CORA_OK;
 }
 

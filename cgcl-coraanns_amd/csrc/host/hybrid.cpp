@@ -249,6 +249,8 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
     last_seed_ms_ = st.seed_ms;
     last_recovery_ms_ = st.recovery_ms;
     last_gpu_refined_ = st.gpu_refined;
+    last_vanguard_ms_ = st.vanguard_ms;
+    last_vanguard_bytes_ = st.vanguard_bytes;
     if (rc != CORA_OK)
         throw std::runtime_error(engine_error(engine_));
     if (profiling_enabled_) {

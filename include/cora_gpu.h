@@ -112,6 +112,10 @@ typedef struct cora_search_stats {
                                pass (FILTER_TIMING only) */
     float recovery_ms;      /* vanguard recovery pass (FILTER_TIMING only; 0 when fused) */
     uint64_t gpu_refined;   /* vectors the fused vanguard pass refined on the GPU */
+    float vanguard_ms;      /* the fused vanguard pass kernel alone (FILTER_TIMING only) */
+    uint64_t vanguard_bytes; /* its algorithmic bytes: code + factor bytes of every vector of
+                                every vanguard pair, plus sign code, ex-code and ex-factor
+                                bytes of every vector it refined */
 } cora_search_stats;
 
 /* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */

@@ -62,6 +62,8 @@ typedef struct cora_hybrid_stats {
     float seed_ms;        /* vanguard seed pass + seed thresholds */
     float recovery_ms;    /* vanguard recovery pass */
     uint64_t gpu_refined; /* vectors the fused vanguard pass refined on the GPU */
+    float vanguard_ms;    /* fused vanguard pass kernel alone */
+    uint64_t vanguard_bytes; /* its algorithmic bytes */
 } cora_hybrid_stats;
 
 int cora_hybrid_create(cora_hybrid **out, int device);                 /* HybridIndex() */
