@@ -114,6 +114,8 @@ def main():
     ap.add_argument("--no-gpu-seed", action="store_true",
                     help="CPU-only thresholds (the reference's behaviour), no GPU seed thresholds")
     ap.add_argument("--no-gpu-prefilter", action="store_true", help="no GPU refined pre-filter")
+    ap.add_argument("--workdir", default="",
+                    help="keep the built index and ground truth in this directory and reuse them")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (PMC byte-count calibration)")
     args = ap.parse_args()
@@ -131,16 +133,25 @@ def main():
     c = wl.CONFIGS[args.config]
     threads = args.cpu_threads or min(16, os.cpu_count() or 16)
     batch_q = args.batch_q or c.batch_q
-    workdir = tempfile.mkdtemp(prefix="cora_bench_")
-    t0 = time.time()
-    base, queries = wl.generate(c, n=args.n or None, nq=args.nq or None)
-    log(f"[data] {c.describe()}: generated {base.shape} + {queries.shape} in {time.time() - t0:.1f}s")
+    workdir = args.workdir or tempfile.mkdtemp(prefix="cora_bench_")
+    os.makedirs(workdir, exist_ok=True)
     index_path = Path(workdir) / f"cfg{c.cfg}.index"
-    wl.build_index(c, base, index_path, log=log)
-    t = time.time()
-    gt = wl.ground_truth(base, queries, c.topk, c.metric)
-    log(f"[gt] exact top-{c.topk} (GPU FP32 + FP64 re-rank): {time.time() - t:.1f}s")
-    del base
+    gt_path = Path(workdir) / f"cfg{c.cfg}_gt.npy"
+    t0 = time.time()
+    if args.workdir and index_path.exists() and gt_path.exists():
+        _, queries = wl.generate(c, n=args.n or None, nq=args.nq or None, queries_only=True)
+        gt = np.load(gt_path)
+        log(f"[data] {c.describe()}: index and ground truth reused from {workdir}")
+    else:
+        base, queries = wl.generate(c, n=args.n or None, nq=args.nq or None)
+        log(f"[data] {c.describe()}: generated {base.shape} + {queries.shape} in {time.time() - t0:.1f}s")
+        wl.build_index(c, base, index_path, log=log)
+        t = time.time()
+        gt = wl.ground_truth(base, queries, c.topk, c.metric)
+        log(f"[gt] exact top-{c.topk} (GPU FP32 + FP64 re-rank): {time.time() - t:.1f}s")
+        del base
+        if args.workdir:
+            np.save(gt_path, gt)
 
     ivf = ca.IvfIndex(index_path)
     eng = ca.HybridIndex(0, vanguard_size=c.vanguard, cpu_secondary_filter=c.secondary_filter,

@@ -68,8 +68,9 @@ def _normal(rng, shape, chunk=1 << 22):
     return out
 
 
-def generate(c: Config, n=None, nq=None):
-    """Base vectors and queries from the config's Gaussian mixture."""
+def generate(c: Config, n=None, nq=None, queries_only=False):
+    """Base vectors and queries from the config's Gaussian mixture (base None when
+    queries_only: the queries depend only on the centres and their own seed)."""
     n = c.n if n is None else n
     nq = c.nq if nq is None else nq
     rng_c = np.random.default_rng(c.cfg)
@@ -86,7 +87,7 @@ def generate(c: Config, n=None, nq=None):
             x /= np.linalg.norm(x, axis=1, keepdims=True)
         return x
 
-    base = draw(np.random.default_rng(c.cfg + 10_000), n)
+    base = None if queries_only else draw(np.random.default_rng(c.cfg + 10_000), n)
     queries = draw(np.random.default_rng(1000 + c.cfg), nq)
     return base, queries
 

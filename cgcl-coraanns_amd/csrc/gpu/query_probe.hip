@@ -232,6 +232,7 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 
 constexpr int kSelThreads = 256;
 
+
 __device__ void block_exclusive_scan2(uint32_t &a, uint32_t &b, uint32_t *sa, uint32_t *sb,
                                       uint32_t &total_a, uint32_t &total_b) {
     const int t = threadIdx.x;
@@ -252,26 +253,81 @@ __device__ void block_exclusive_scan2(uint32_t &a, uint32_t &b, uint32_t *sa, ui
     __syncthreads();
 }
 
-// Inclusive prefix sum over the block (thread order); s_red holds one word per wave.
-__device__ __forceinline__ uint32_t sel_incl_scan(uint32_t v, uint32_t *s_red) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = __shfl_up(v, o);
-        if (lane >= (uint32_t)o)
-            v += y;
-    }
-    if (lane == 63)
-        s_red[wave] = v;
-    __syncthreads();
-    uint32_t add = 0;
-    for (uint32_t w = 0; w < wave; ++w)
-        add += s_red[w];
-    __syncthreads();
-    return v + add;
-}
+constexpr uint32_t kSelLdsRow = 32768;  // rows up to this many clusters are staged in LDS (128 KB)
+constexpr size_t kSelMaxDynLds = 144 * 1024;  // of the 160 KB a gfx950 workgroup may hold
 
-constexpr uint32_t kSelLdsRow = 8192;  // rows up to this many clusters are staged in LDS
+// The k-th smallest order key (k >= 1) of a block's keys, each thread visiting its own
+// with each_key(f). The keys first give their minimum and maximum; every pass then
+// histograms the keys of the current range [lo, lo + span] into 256 bins of equal width
+// (a power of two) and keeps the bin holding the k-th, narrowing the range by 8 bits, so
+// keys spread over the bins even when they share their high bits. Returns the key and in
+// take_eq how many keys equal to it belong to the k smallest. Block size kThreads >= 256;
+// s_red holds one word per wave.
+template <int kThreads, class EachKey>
+__device__ uint32_t block_kth_key(EachKey each_key, uint32_t k, uint32_t *hist, uint32_t *s_red,
+                                  uint32_t *s_sc, uint32_t &take_eq) {
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    constexpr uint32_t kWaves = kThreads / 64;
+    uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+    each_key([&](uint32_t key) {
+        mn = min(mn, key);
+        mx = max(mx, key);
+    });
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        mn = min(mn, (uint32_t)__shfl_xor(mn, o));
+        mx = max(mx, (uint32_t)__shfl_xor(mx, o));
+    }
+    if (lane == 0) {
+        s_red[wave] = mn;
+        s_red[kWaves + wave] = mx;
+    }
+    __syncthreads();
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+    for (uint32_t w = 0; w < kWaves; ++w) {
+        lo = min(lo, s_red[w]);
+        hi = max(hi, s_red[kWaves + w]);
+    }
+    __syncthreads();
+    uint32_t span = hi - lo, rem = k;
+    while (span > 0) {
+        const uint32_t bits = 32u - (uint32_t)__clz(span);
+        const uint32_t shift = bits > 8 ? bits - 8 : 0u;
+        if (t < 256)
+            hist[t] = 0;
+        __syncthreads();
+        each_key([&](uint32_t key) {
+            if (key >= lo && key - lo <= span)
+                atomicAdd(&hist[(key - lo) >> shift], 1u);
+        });
+        __syncthreads();
+        uint32_t h = t < 256 ? hist[t] : 0u, v = h;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(v, o);
+            if (lane >= (uint32_t)o)
+                v += y;
+        }
+        if (lane == 63)
+            s_red[wave] = v;
+        __syncthreads();
+        for (uint32_t w = 0; w < wave; ++w)
+            v += s_red[w];
+        if (t < 256 && v >= rem && v - h < rem) {
+            s_sc[0] = t;
+            s_sc[1] = rem - (v - h);
+        }
+        __syncthreads();
+        const uint32_t b = s_sc[0];
+        rem = s_sc[1];
+        lo += b << shift;
+        span = min(span - (b << shift), (1u << shift) - 1u);
+        __syncthreads();
+    }
+    take_eq = rem;
+    return lo;
+}
+  // rows up to this many clusters are staged in LDS
 
 // Per query: radix-select the key of the nprobe-th smallest distance (4 x 8-bit digits,
 // each digit found by a block prefix sum over the 256-bin histogram), gather every
@@ -283,7 +339,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float *__rest
                                                              uint32_t kpow2,
                                                              int32_t *__restrict__ out) {
     __shared__ uint32_t hist[256];
-    __shared__ uint32_t s_red[kSelThreads / 64], s_sc[2];
+    __shared__ uint32_t s_red[2 * kSelThreads / 64], s_sc[2];
     __shared__ uint32_t sa[kSelThreads], sb[kSelThreads];
     extern __shared__ unsigned long long sel[];  // [kpow2], then the row's keys with kLds
     uint32_t *keys = reinterpret_cast<uint32_t *>(sel + kpow2);
@@ -299,30 +355,15 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float *__rest
         for (uint32_t i = t; i < nl; i += kSelThreads)
             keys[i] = order_key(row[i]);
     }
-    uint32_t prefix = 0, pmask = 0, rem = k;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[t] = 0;
+    if constexpr (kLds)
         __syncthreads();
-        for (uint32_t i = t; i < nl; i += kSelThreads) {
-            const uint32_t key = key_at(i);
-            if ((key & pmask) == prefix)
-                atomicAdd(&hist[(key >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        const uint32_t h = hist[t];
-        const uint32_t incl = sel_incl_scan(h, s_red);
-        if (incl >= rem && incl - h < rem) {
-            s_sc[0] = t;
-            s_sc[1] = rem - (incl - h);
-        }
-        __syncthreads();
-        prefix |= s_sc[0] << shift;
-        pmask |= 255u << shift;
-        rem = s_sc[1];
-        __syncthreads();
-    }
-    const uint32_t kth = prefix;
-    const uint32_t take_eq = rem;
+    uint32_t take_eq = 0;
+    const uint32_t kth = block_kth_key<kSelThreads>(
+        [&](auto f) {
+            for (uint32_t i = t; i < nl; i += kSelThreads)
+                f(key_at(i));
+        },
+        k, hist, s_red, s_sc, take_eq);
     const uint32_t chunk = (nl + kSelThreads - 1) / kSelThreads;
     const uint32_t begin = min(nl, t * chunk), end = min(nl, begin + chunk);
     uint32_t nless = 0, neq = 0;
@@ -363,6 +404,288 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float *__rest
         }
     }
     for (uint32_t i = t; i < k; i += kSelThreads)
+        out[(size_t)blockIdx.x * k + i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
+}
+
+// One wave per query (four per workgroup), no workgroup barriers: the k-th smallest order
+// key by range narrowing (a min/max pass, then passes that histogram the keys of the
+// current range into 256 equal power-of-two bins held in the wave's LDS and keep the bin
+// holding the k-th), then every smaller key and the lowest-index ties in index order
+// (ballot compaction), then a bitonic sort of the kpow2 slots in the wave's LDS. The row
+// is read once from HBM and the later passes hit L2.
+constexpr int kSelWaveThreads = 256;
+constexpr uint32_t kSelWaveMaxK = 1024;  // kpow2 limit (8 KB of LDS per wave)
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+__global__ __launch_bounds__(kSelWaveThreads) void select_wave_kernel(const float *__restrict__ dist,
+                                                                      uint32_t nq, uint32_t nl, uint32_t k,
+                                                                      uint32_t kpow2,
+                                                                      int32_t *__restrict__ out) {
+    extern __shared__ unsigned long long s_sel_all[];  // [4 waves][kpow2]
+    __shared__ uint32_t s_hist_all[kSelWaveThreads / 64][256];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = blockIdx.x * (kSelWaveThreads / 64) + wave;
+    if (q >= nq)
+        return;  // whole wave: no barrier below involves other waves
+    unsigned long long *sel = s_sel_all + (size_t)wave * kpow2;
+    uint32_t *hist = s_hist_all[wave];
+    const float *row = dist + (size_t)q * nl;
+    // keys visited 4 per lane per load (float4 when the row is 16-byte aligned), four
+    // loads in flight per lane: chunk c of the row is indices [256 c, 256 c + 256), lane l
+    // holding [256 c + 4 l, 256 c + 4 l + 4)
+    const bool vec = (nl & 3u) == 0;
+    const uint32_t nchunks = (nl + 255) / 256;
+    auto load4 = [&](uint32_t c, uint32_t (&key)[4]) {
+        const uint32_t i = 256 * c + 4 * lane;
+        if (vec && i + 4 <= nl) {
+            const float4 v = *reinterpret_cast<const float4 *>(row + i);
+            key[0] = order_key(v.x);
+            key[1] = order_key(v.y);
+            key[2] = order_key(v.z);
+            key[3] = order_key(v.w);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                key[j] = i + j < nl ? order_key(row[i + j]) : 0xFFFFFFFFu;
+        }
+    };
+    // f(key, index) for every key of the row (index >= nl marks padding)
+    auto each = [&](auto f) {
+        uint32_t c = 0;
+        for (; c + 4 <= nchunks; c += 4) {
+            uint32_t key[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                load4(c + u, key[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    f(key[u][j], 256 * (c + u) + 4 * lane + j);
+        }
+        for (; c < nchunks; ++c) {
+            uint32_t key[4];
+            load4(c, key);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                f(key[j], 256 * c + 4 * lane + j);
+        }
+    };
+    uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+    each([&](uint32_t key, uint32_t i) {
+        if (i < nl) {
+            mn = min(mn, key);
+            mx = max(mx, key);
+        }
+    });
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        mn = min(mn, (uint32_t)__shfl_xor(mn, o));
+        mx = max(mx, (uint32_t)__shfl_xor(mx, o));
+    }
+    uint32_t lo = mn, span = mx - mn, rem = k;
+    while (span > 0) {
+        const uint32_t bits = 32u - (uint32_t)__clz(span);
+        const uint32_t shift = bits > 8 ? bits - 8 : 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            hist[4 * lane + j] = 0;
+        wave_sync();
+        each([&](uint32_t key, uint32_t i) {
+            if (i < nl && key >= lo && key - lo <= span)
+                atomicAdd(&hist[(key - lo) >> shift], 1u);
+        });
+        wave_sync();
+        uint32_t h[4], sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h[j] = hist[4 * lane + j];
+            sum += h[j];
+        }
+        uint32_t incl = sum;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(incl, o);
+            if (lane >= (uint32_t)o)
+                incl += y;
+        }
+        const uint32_t before = incl - sum;
+        const unsigned long long m = __ballot(before < rem && incl >= rem);
+        const uint32_t src = (uint32_t)__ffsll((long long)m) - 1u;
+        uint32_t b = 0, r2 = 0;
+        if (lane == src) {
+            uint32_t c = before;
+            int j = 0;
+            while (j < 3 && c + h[j] < rem) {
+                c += h[j];
+                ++j;
+            }
+            b = 4 * lane + (uint32_t)j;
+            r2 = rem - c;
+        }
+        b = __shfl(b, (int)src);
+        rem = __shfl(r2, (int)src);
+        lo += b << shift;
+        span = min(span - (b << shift), (1u << shift) - 1u);
+        wave_sync();
+    }
+    const uint32_t kth = lo, take_eq = rem, strict_total = k - take_eq;
+    // gather in index order: per chunk, lane l's keys precede lane l + 1's
+    uint32_t n_less = 0, n_eq = 0;
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        uint32_t key[4];
+        load4(c, key);
+        uint32_t cl = 0, ce = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool valid = 256 * c + 4 * lane + j < nl;
+            cl += valid && key[j] < kth;
+            ce += valid && key[j] == kth;
+        }
+        uint32_t il = cl, ie = ce;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t yl = __shfl_up(il, o), ye = __shfl_up(ie, o);
+            if (lane >= (uint32_t)o) {
+                il += yl;
+                ie += ye;
+            }
+        }
+        uint32_t pl = n_less + il - cl, pe = n_eq + ie - ce;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = 256 * c + 4 * lane + j;
+            if (i < nl && key[j] < kth) {
+                sel[pl++] = ((unsigned long long)key[j] << 32) | i;
+            } else if (i < nl && key[j] == kth) {
+                if (pe < take_eq)
+                    sel[strict_total + pe] = ((unsigned long long)key[j] << 32) | i;
+                ++pe;
+            }
+        }
+        n_less += __shfl(il, 63);
+        n_eq += __shfl(ie, 63);
+    }
+    for (uint32_t i = k + lane; i < kpow2; i += 64)
+        sel[i] = ~0ull;
+    wave_sync();
+    for (uint32_t size = 2; size <= kpow2; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = lane; i < kpow2; i += 64) {
+                const uint32_t j = i ^ stride;
+                if (j > i) {
+                    const bool asc = (i & size) == 0;
+                    const unsigned long long a = sel[i], c = sel[j];
+                    if ((a > c) == asc) {
+                        sel[i] = c;
+                        sel[j] = a;
+                    }
+                }
+            }
+            wave_sync();
+        }
+    }
+    for (uint32_t i = lane; i < k; i += 64)
+        out[(size_t)q * k + i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
+}
+
+// Large nlist: one block of 1,024 threads per query, thread t holding the order keys of
+// clusters [t * R, t * R + R) in registers (nl <= 1024 * R), so the row is read once.
+// Same selection as select_kernel: radix select of the nprobe-th key, every smaller key
+// plus the lowest-index ties in index order, bitonic sort in LDS.
+constexpr int kSelBigThreads = 1024;
+
+template <int R>
+__global__ __launch_bounds__(kSelBigThreads) void select_regs_kernel(const float *__restrict__ dist,
+                                                                     uint32_t nl, uint32_t k,
+                                                                     uint32_t kpow2,
+                                                                     int32_t *__restrict__ out) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_red[2 * kSelBigThreads / 64], s_sc[2];
+    extern __shared__ unsigned long long sel[];  // [kpow2]
+    const float *row = dist + (size_t)blockIdx.x * nl;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t begin = t * R;
+    uint32_t key[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        key[r] = begin + r < nl ? order_key(row[begin + r]) : 0xFFFFFFFFu;
+    // inclusive block scan over 1,024 threads (s_red: one word per wave)
+    auto incl_scan = [&](uint32_t v) -> uint32_t {
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(v, o);
+            if (lane >= (uint32_t)o)
+                v += y;
+        }
+        if (lane == 63)
+            s_red[wave] = v;
+        __syncthreads();
+        uint32_t add = 0;
+        for (uint32_t w = 0; w < wave; ++w)
+            add += s_red[w];
+        __syncthreads();
+        return v + add;
+    };
+    uint32_t take_eq = 0;
+    const uint32_t kth = block_kth_key<kSelBigThreads>(
+        [&](auto f) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (begin + r < nl)
+                    f(key[r]);
+        },
+        k, hist, s_red, s_sc, take_eq);
+    uint32_t nless = 0, neq = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (begin + r < nl) {
+            nless += key[r] < kth;
+            neq += key[r] == kth;
+        }
+    }
+    // exclusive prefixes of both counts in index order; the keys below kth number
+    // k - take_eq, so the ties are placed after them
+    const uint32_t less_before = incl_scan(nless) - nless;
+    const uint32_t eq_before = incl_scan(neq) - neq;
+    const uint32_t strict_total = k - take_eq;
+    uint32_t nl_i = less_before, ne_i = eq_before;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (begin + r < nl) {
+            if (key[r] < kth) {
+                sel[nl_i++] = ((unsigned long long)key[r] << 32) | (begin + r);
+            } else if (key[r] == kth) {
+                if (ne_i < take_eq)
+                    sel[strict_total + ne_i] = ((unsigned long long)key[r] << 32) | (begin + r);
+                ++ne_i;
+            }
+        }
+    }
+    for (uint32_t i = k + t; i < kpow2; i += kSelBigThreads)
+        sel[i] = ~0ull;
+    __syncthreads();
+    for (uint32_t size = 2; size <= kpow2; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = t; i < kpow2; i += kSelBigThreads) {
+                const uint32_t j = i ^ stride;
+                if (j > i) {
+                    const bool asc = (i & size) == 0;
+                    const unsigned long long a = sel[i], b = sel[j];
+                    if ((a > b) == asc) {
+                        sel[i] = b;
+                        sel[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (uint32_t i = t; i < k; i += kSelBigThreads)
         out[(size_t)blockIdx.x * k + i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
 }
 
@@ -437,12 +760,27 @@ void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
     uint32_t kp = 1;
     while (kp < nprobe)
         kp <<= 1;
-    if (nl <= kSelLdsRow)
-        select_kernel<true><<<nq, kSelThreads, kp * sizeof(unsigned long long) + (size_t)nl * 4, s>>>(
-            dist, nl, nprobe, kp, idx);
+    const size_t sel_bytes = kp * sizeof(unsigned long long);
+    const size_t lds = sel_bytes + (size_t)nl * 4;
+    if (kp <= kSelWaveMaxK) {
+        const uint32_t per = kSelWaveThreads / 64;
+        select_wave_kernel<<<(nq + per - 1) / per, kSelWaveThreads, per * sel_bytes, s>>>(dist, nq, nl, nprobe,
+                                                                                        kp, idx);
+    } else if (nl <= kSelLdsRow && lds <= kSelMaxDynLds) {
+        static bool raised = false;  // dynamic LDS above 64 KB must be allowed explicitly
+        if (!raised) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void *>(&select_kernel<true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSelMaxDynLds) != hipSuccess)
+                (void)hipGetLastError();  // leave no sticky error; a launch above 64 KB then reports it
+            raised = true;
+        }
+        select_kernel<true><<<nq, kSelThreads, lds, s>>>(dist, nl, nprobe, kp, idx);
+    } else if (nl <= 32u * kSelBigThreads)
+        select_regs_kernel<32><<<nq, kSelBigThreads, sel_bytes, s>>>(dist, nl, nprobe, kp, idx);
+    else if (nl <= 64u * kSelBigThreads)
+        select_regs_kernel<64><<<nq, kSelBigThreads, sel_bytes, s>>>(dist, nl, nprobe, kp, idx);
     else
-        select_kernel<false><<<nq, kSelThreads, kp * sizeof(unsigned long long), s>>>(dist, nl, nprobe,
-                                                                                     kp, idx);
+        select_kernel<false><<<nq, kSelThreads, sel_bytes, s>>>(dist, nl, nprobe, kp, idx);
 }
 
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,

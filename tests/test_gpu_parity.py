@@ -172,6 +172,40 @@ def test_coarse_probe(case_name, request):
         assert np.all(np.abs(g["gerr"][q] - np.sqrt(l2x)) <= 1e-5 * np.sqrt(sc))
 
 
+@pytest.mark.parametrize("nlist", [9000, 20000, 40000])
+def test_coarse_probe_large_nlist(nlist, tmp_path):
+    """Top-nprobe selection over nlist above the LDS-staged select (register-staged select,
+    1,024 threads per query) against the oracle's FP64 probe distances."""
+    rng = np.random.default_rng(nlist)
+    dim, nq, nprobe = 64, 64, 16
+    n = 2 * nlist
+    cent = rng.normal(0, 1, (nlist, dim)).astype(np.float32)
+    assign = rng.integers(0, nlist, n).astype(np.uint32)
+    x = (cent[assign] + rng.normal(0, 0.1, (n, dim))).astype(np.float32)
+    q = (cent[rng.integers(0, nlist, nq)] + rng.normal(0, 0.1, (nq, dim))).astype(np.float32)
+    R = np.linalg.qr(rng.normal(size=(dim, dim)))[0].T.astype(np.float32)
+    path = tmp_path / "wide.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32), (cent.astype(np.float64) @ R).astype(np.float32),
+                 assign, R, metric=0)
+    case = Case(path, q)
+    say(f"[gpu] coarse probe parity, nlist={nlist}")
+    eng, _, _ = run_frozen(case, nprobe, 10)
+    g = gpu_intermediates(eng, case, nprobe)
+    for qi in range(nq):
+        if qi % 8 == 0:  # oracle distances to every cluster, 8 queries at a time
+            idx, _, _, l2 = orc.coarse_probe(g["qr"][qi:qi + 8], case.sd.centroids, case.file.nlist,
+                                             case.file.metric)
+            idx, l2 = {qi + r: idx[r] for r in range(idx.shape[0])}, {qi + r: l2[r] for r in range(l2.shape[0])}
+        got = g["pidx"][qi]
+        d_all = dict(zip(idx[qi].tolist(), l2[qi].tolist()))
+        dg = np.array([d_all[c] for c in got])
+        assert np.all(np.diff(dg) >= -1e-5 * (np.abs(dg).max() + 1)), qi
+        kth = l2[qi][nprobe - 1]
+        strict = set(idx[qi][l2[qi] < kth - 1e-5 * (abs(kth) + 1)].tolist())
+        assert strict <= set(got.tolist()), qi
+        assert len(set(got.tolist())) == nprobe
+
+
 @pytest.mark.parametrize("case_name", CASES)
 def test_popcount_estimator_bit_exact(case_name, request):
     case = request.getfixturevalue(case_name)
