@@ -40,6 +40,7 @@ DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5
 DBG_SEED_DIST, DBG_THRESHOLDS = 10, 11
 FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
 FLAG_PAIR_SEEDS = 1 << 6
+FLAG_NO_MFMA_SCAN = 1 << 7
 
 
 class EngineUnavailable(RuntimeError):

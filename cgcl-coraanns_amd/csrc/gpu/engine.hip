@@ -66,6 +66,7 @@ struct cora_gpu_engine {
              *d_uoff = nullptr, *d_nunits = nullptr, *d_cursor = nullptr, *d_seed = nullptr;
     int32_t *d_pidx = nullptr;
     uint32_t *d_qorder = nullptr;  // queries by nearest cluster (fused vanguard pass)
+    int8_t *d_qbytes = nullptr;    // [max_q][2][P] qint, qres (MFMA far scan operands)
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
     uint4 *d_seed_rec = nullptr;
     float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
@@ -88,7 +89,7 @@ struct cora_gpu_engine {
     bool launched = false;
     cora_search_args last{};
     uint32_t last_depth = 0, last_batch = 1;
-    bool last_timing = false, last_fused = false;
+    bool last_timing = false, last_fused = false, last_mfma = false;
 };
 
 namespace {
@@ -129,6 +130,7 @@ ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool f
     p.tiles = E->d_tiles;
     p.meta = E->d_meta;
     p.qplanes = E->d_planes;
+    p.qbytes = E->d_qbytes;
     p.qwidth = E->d_qwidth;
     p.qwidth2 = E->d_qwidth2;
     p.k1 = E->d_k1;
@@ -188,6 +190,7 @@ void release_workspace(cora_gpu_engine *E) {
         dfree(*p);
     dfree(E->d_pidx);
     dfree(E->d_qorder);
+    dfree(E->d_qbytes);
     dfree(E->d_seed_dist);
     dfree(E->d_seed_low);
     dfree(E->d_seed_err);
@@ -496,6 +499,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_dist, max_q * E->nl));
         TRY(dalloc(E, E->d_pidx, np));
         TRY(dalloc(E, E->d_qorder, max_q));
+        TRY(dalloc(E, E->d_qbytes, max_q * 2 * E->P));
         TRY(dalloc(E, E->d_gadd, np));
         TRY(dalloc(E, E->d_gerr, np));
         TRY(dalloc(E, E->d_bcount, nb));
@@ -629,12 +633,18 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const uint32_t nq = a->num_queries, np = a->nprobe;
     const uint32_t keep = std::max<uint32_t>(a->topk, 20u);
     const uint32_t depth = keep <= (uint32_t)kMaxVanguardKeep ? (uint32_t)want_depth : 0u;
-    const uint32_t batch = (a->flags & CORA_FLAG_CROSS_QUERY_REUSE) ? a->batch_q : 1u;
+    // Cross-query reuse: the far pairs of one cluster are scanned together, batch_q at a time
+    // by the popcount kernel, or kMfmaBatchQ at a time by the matrix-core kernel when the
+    // padded dimension allows it (the unit size changes only the speed, never the result).
+    const bool reuse = (a->flags & CORA_FLAG_CROSS_QUERY_REUSE) != 0;
+    const bool mfma_far = reuse && far_mfma_supported(E->W) && !(a->flags & CORA_FLAG_NO_MFMA_SCAN);
+    const uint32_t batch = mfma_far ? kMfmaBatchQ : reuse ? a->batch_q : 1u;
     const bool frozen = (a->flags & CORA_FLAG_FROZEN_THRESHOLDS) != 0;
     const bool timing = (a->flags & CORA_FLAG_FILTER_TIMING) != 0;
     E->last = *a;
     E->last_depth = depth;
     E->last_batch = batch;
+    E->last_mfma = mfma_far;
     E->last_timing = timing;
     hipStream_t s = E->stream;
     const uint32_t P = (uint32_t)E->P;
@@ -642,7 +652,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // query preparation (hybrid.cu:436-463)
     launch_rotate(E->d_raw, E->d_rot, E->d_qrot, nq, (uint32_t)E->dim, P, s);
     launch_query_prep(E->d_qrot, nq, P, (uint32_t)E->ex_bits, E->d_k1, E->d_kb, E->d_qnorm,
-                      E->d_qwidth, E->d_qwidth2, E->d_planes, s);
+                      E->d_qwidth, E->d_qwidth2, E->d_planes, E->d_qbytes, s);
     HIPCHK(hipEventRecord(E->ev_prep, s));
     HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_prep, 0));
     HIPCHK(hipMemcpyAsync(E->h_qrot, E->d_qrot, (size_t)nq * P * 4, hipMemcpyDeviceToHost,
@@ -742,7 +752,10 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     snapshot();
     if (timing)
         HIPCHK(hipEventRecord(E->ev_s0, s));
-    launch_scan(p, E->W, batch, 0, s);
+    if (mfma_far)
+        launch_far_mfma(p, E->W, false, s);
+    else
+        launch_scan(p, E->W, batch, 0, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_s1, s));
     launch_copy_u64(E->d_produced, E->d_stats + 4, s);
@@ -963,8 +976,12 @@ int cora_gpu_debug_dense(cora_gpu_engine *E, int32_t *out_ip, int32_t *out_ip2, 
         if (r == hipSuccess)
             r = hipMemcpy(d_low, out_low, need * 4, hipMemcpyHostToDevice);
         for (uint32_t set = 0; set < 2 && r == hipSuccess; ++set) {
+            // the kernel the search ran: the matrix-core far scan for the far units
             launch_cursor_init(E->d_cursor, E->d_nunits, set, E->stream);
-            launch_scan_set(p, E->W, 2, set, E->stream);
+            if (set == 1 && E->last_mfma)
+                launch_far_mfma(p, E->W, true, E->stream);
+            else
+                launch_scan_set(p, E->W, 2, set, E->stream);
             r = hipGetLastError();
             if (r == hipSuccess)
                 r = hipStreamSynchronize(E->stream);

@@ -96,6 +96,7 @@ struct ScanParams {
     const uint8_t *tiles;
     const ClusterMeta *meta;
     const uint32_t *qplanes;  // [nq][16][W]: Bq=8 query planes 0..7, residual planes 8..15
+    const int8_t *qbytes;     // [nq][2][P]: qint and qres as int8 (MFMA operands)
     const float *qwidth;      // [nq] Bq=8 step
     const float *qwidth2;     // [nq] residual step (qwidth / 254)
     const float *k1;          // [nq]
@@ -164,7 +165,7 @@ void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint
                    uint32_t P, hipStream_t s);
 void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,
                        float *kb, float *qnorm, float *qwidth, float *qwidth2, uint32_t *qplanes,
-                       hipStream_t s);
+                       int8_t *qbytes, hipStream_t s);
 void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s);
 void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,
                       uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s);
@@ -205,6 +206,10 @@ bool launch_order_queries(const int32_t *probe_idx, uint32_t nq, uint32_t nprobe
                           uint32_t *order, hipStream_t s);
 void launch_vanguard_query(const ScanParams &p, const VanguardArgs &va, uint32_t W, uint32_t nq,
                            hipStream_t s);
+// far-pair scan on the matrix cores (scan_mfma.hip): units of up to kMfmaBatchQ pairs
+constexpr uint32_t kMfmaBatchQ = 16;
+bool far_mfma_supported(uint32_t W);
+void launch_far_mfma(const ScanParams &p, uint32_t W, bool dense, hipStream_t s);
 // dev[0..n) = the host-coherent thresholds, read with system scope (the per-pass copy the
 // scan kernels read, so no unit waits on a host-memory round trip)
 void launch_snapshot_thresholds(const float *host, float *dev, uint32_t n, hipStream_t s);

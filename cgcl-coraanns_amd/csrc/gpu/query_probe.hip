@@ -158,7 +158,8 @@ __global__ __launch_bounds__(64) void query_prep_kernel(const float *__restrict_
                                                         float *__restrict__ qnorm,
                                                         float *__restrict__ qwidth,
                                                         float *__restrict__ qwidth2,
-                                                        uint32_t *__restrict__ planes) {
+                                                        uint32_t *__restrict__ planes,
+                                                        int8_t *__restrict__ qbytes) {
     const uint32_t q = blockIdx.x;
     const int lane = threadIdx.x;
     const float *row = qrot + (size_t)q * P;
@@ -192,6 +193,10 @@ __global__ __launch_bounds__(64) void query_prep_kernel(const float *__restrict_
         int qr = (int)rintf(__fmul_rn(r, inv2));
         qr = max(-127, min(127, qr));
         const uint32_t u = (uint32_t)qi & 0xFFu, ur = (uint32_t)qr & 0xFFu;
+        if (qbytes) {
+            qbytes[(size_t)q * 2 * P + lane + 64 * i] = (int8_t)qi;
+            qbytes[(size_t)q * 2 * P + P + lane + 64 * i] = (int8_t)qr;
+        }
 #pragma unroll
         for (int j = 0; j < kBq; ++j) {
             const unsigned long long m = __ballot((u >> j) & 1u);
@@ -735,8 +740,8 @@ void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint
 
 void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,
                        float *kb, float *qnorm, float *qwidth, float *qwidth2, uint32_t *qplanes,
-                       hipStream_t s) {
-    query_prep_kernel<<<nq, 64, 0, s>>>(qrot, P, ex_bits, k1, kb, qnorm, qwidth, qwidth2, qplanes);
+                       int8_t *qbytes, hipStream_t s) {
+    query_prep_kernel<<<nq, 64, 0, s>>>(qrot, P, ex_bits, k1, kb, qnorm, qwidth, qwidth2, qplanes, qbytes);
 }
 
 void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s) {

@@ -47,23 +47,6 @@ namespace {
 
 enum ScanKind { kFar = 0, kRecovery = 1, kDense = 2 };
 
-// Refined distance of a candidate (cpu_refinement.cpp:183-192) from the HBM copy of the
-// ex-codes, evaluated by one lane, and a bound on its rounding difference from the CPU
-// consumer's evaluation (1e-4 of the magnitude of the terms).
-__device__ __forceinline__ float refine_one(const ScanParams &p, uint32_t query, uint32_t probe,
-                                            uint32_t gid, float ex, float &err) {
-    const size_t lc = (size_t)p.P * 7 / 8;
-    const uint8_t *code = p.ex_codes + (size_t)gid * lc;
-    const float *qv = p.qrot + (size_t)query * p.P;
-    float ip = 0.0f, l1 = 0.0f;
-    for (uint32_t c = 0; c < p.P / 8; ++c)
-        ip += excode_chunk_ip(code, qv, c, &l1);
-    const float fa = p.ex_factors[2 * (size_t)gid], fr = p.ex_factors[2 * (size_t)gid + 1];
-    const float gadd = p.pgadd[(size_t)query * p.nprobe + probe], kbq = p.kb[query];
-    err = 1e-4f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq)));
-    return fa + gadd + fr * (128.0f * ex + ip + kbq);
-}
-
 // Publish the n staged survivors of this wave (n wave-uniform, 0 < n <= kCap), 64 at a
 // time. Must be called by all 64 lanes; the workgroup is this one wave. Staged records
 // carry ip_int in their exact_ip word; it is replaced by the two-stage estimate. With

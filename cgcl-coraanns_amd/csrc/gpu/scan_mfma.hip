@@ -1,0 +1,291 @@
+// Far-pair scan on the matrix cores (gfx950 v_mfma_i32_16x16x32_i8).
+//
+// The Bitwise estimator's integer inner product (filter_kernels.cuh:79-114)
+//     ip_int = sum_i b_i * qint_i        (b_i the sign bit of dimension i, qint_i in [-128, 127])
+// is a product of a 0/1 matrix with an int8 matrix, exact in int32. A scan unit serves up
+// to 16 same-cluster pairs, so a 64-vector tile against the unit's queries is a
+// [64 x P] x [P x 16] integer product: four 16x16 output blocks, P/32 K-steps each, plus
+// the same product against the residual query (qres) for the two-stage exact_ip. The
+// code bits are widened to int8 in registers (one multiply spreads a nibble over four
+// bytes); the queries' int8 values come from the query preparation. ip_int and ip_res are
+// therefore bit-identical to the popcount kernel's (scan.hip), and the lower bound uses
+// the same expression, so the candidate set is the same.
+//
+// MFMA lane layout (16x16x32 i8): lane l supplies A[l%16][8(l/16)+e] and B[8(l/16)+e][l%16]
+// (byte e of a 64-bit operand) and holds D[4(l/16)+r][l%16], r = 0..3. Here rows are
+// vectors (16 m + ...) and columns are the unit's pair slots, so lane l evaluates pair slot
+// l % 16 for vectors 16 m + 4 (l / 16) + r.
+//
+// Work distribution, thresholds, staging and publication follow the popcount far scan:
+// one wave per workgroup, persistent grid, per-XCD unit cursors, per-pass threshold
+// snapshot, survivors staged in LDS and flushed 64 at a time (refined pre-filter with the
+// HBM ex-codes, one reservation per round, write-through ring stores).
+#include <float.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "device_common.h"
+
+namespace cora {
+namespace {
+
+typedef int32_t v4i32 __attribute__((ext_vector_type(4)));
+constexpr int kStage = 256;  // staged survivor records per wave
+
+// Bits 0..7 of b as eight int8 0/1 values (bit e in byte e), the 64-bit MFMA operand.
+__device__ __forceinline__ long spread_byte(uint32_t b) {
+    const uint32_t lo = ((b & 15u) * 0x00204081u) & 0x01010101u;
+    const uint32_t hi = (((b >> 4) & 15u) * 0x00204081u) & 0x01010101u;
+    return (long)(((unsigned long long)hi << 32) | lo);
+}
+
+__device__ __forceinline__ uint32_t next_far_unit(uint32_t *cursor, uint32_t U, uint32_t &range,
+                                                  uint32_t &tries, uint32_t lane) {
+    const uint32_t per = (U + kNumXcd - 1) / kNumXcd;
+    while (tries < kNumXcd) {
+        uint32_t u = 0;
+        if (lane == 0)
+            u = atomicAdd(&cursor[range], 1u);
+        u = uniform(u);
+        const uint32_t end = min(U, (range + 1) * per);
+        if (u < end)
+            return u;
+        range = (range + 1) % kNumXcd;
+        ++tries;
+    }
+    return U;
+}
+
+// Publish n staged records (n wave-uniform, 0 < n <= kStage), 64 at a time; records carry
+// their final exact_ip. With the refined pre-filter a record whose refined distance
+// exceeds its cutoff by more than the rounding bound is dropped.
+__device__ void flush_records(const ScanParams &p, const QueueDev &q, uint32_t n, const uint4 *s_rec,
+                              const float *s_cut, unsigned long long &limit, uint32_t lane) {
+    __syncthreads();
+    for (uint32_t i0 = 0; i0 < n; i0 += 64) {
+        const uint32_t i = i0 + lane;
+        bool keep = false;
+        uint4 rec = make_uint4(0u, 0u, 0u, 0u);
+        if (i < n) {
+            rec = s_rec[i];
+            keep = true;
+            if (p.prefilter) {
+                float err;
+                const float dist = refine_one(p, rec.x & 0xFFFFu, rec.x >> 16, rec.y,
+                                              __uint_as_float(rec.z), err);
+                keep = dist <= s_cut[i] + err;
+            }
+        }
+        const unsigned long long m = __ballot(keep);
+        if (p.prefilter && lane == 0) {
+            const uint32_t dropped = min(64u, n - i0) - (uint32_t)__popcll(m);
+            if (dropped)
+                atomicAdd(p.dropped, (unsigned long long)dropped);
+        }
+        if (m == 0)
+            continue;
+        const uint32_t cnt = (uint32_t)__popcll(m);
+        unsigned long long base = 0;
+        if (lane == 0)
+            base = atomicAdd(q.produced, (unsigned long long)cnt);
+        base = shfl0_u64(base);
+        if (base + cnt > limit) {
+            unsigned long long fresh = 0;
+            if (lane == 0)
+                fresh = refresh_limit(q.cached_limit, q.refresh_flag, &q.progress->released, q.capacity,
+                                      base + cnt);
+            limit = shfl0_u64(fresh);
+        }
+        if (keep)
+            place_record(q, base + lane_rank(m), limit, rec);
+    }
+    __syncthreads();
+}
+
+// W = P / 32 words per vector (W even, W <= 8: the unit's query operands stay in VGPRs).
+// kDense: write ip_int, ip_res and the lower bound of every (vector, pair) to the debug
+// arrays instead of publishing (the estimator parity test of the kernel the search runs).
+template <int W, bool kDense>
+__global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
+    static_assert(W % 2 == 0 && W >= 2 && W <= 8, "query operands in registers");
+    constexpr int G = (W + 3) / 4;  // code word groups of a tile
+    __shared__ uint4 s_rec[kDense ? 1 : kStage];
+    __shared__ float s_cut[kDense ? 1 : kStage];
+    const uint32_t lane = threadIdx.x, col = lane & 15, quad = lane >> 4;
+    const uint32_t P = 32u * W;
+    const QueueDev q = p.queue;
+    const uint32_t U = p.num_units[1];
+    const uint32_t ubase = p.num_units[0];
+    uint32_t range = blockIdx.x % kNumXcd, tries = 0;
+    uint32_t staged = 0;
+    unsigned long long limit =
+        kDense ? 0ull : __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+        const uint32_t u = next_far_unit(p.unit_cursor, U, range, tries, lane);
+        if (u >= U)
+            break;
+        const Unit un = p.units[ubase + u];
+        const uint32_t cluster = uniform(un.cluster), count = uniform(un.count);
+        const ClusterMeta cm = p.meta[cluster];
+        const uint32_t n = uniform(cm.n), start = uniform(cm.start), tbase = uniform(cm.tile_base);
+        const uint32_t t_begin = uniform(un.tiles) >> 8, t_end = t_begin + (uniform(un.tiles) & 255u);
+        if (n == 0 || t_begin >= t_end)
+            continue;
+        // this lane's pair slot
+        const bool slot = col < count;
+        const uint32_t w0 = slot ? p.pairs[uniform(un.pair_begin) + col].word0 : 0u;
+        const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
+        float width = 0.0f, width2 = 0.0f, k1 = 0.0f, gadd = 0.0f, gerr = 0.0f, cutoff = -FLT_MAX;
+        long bq[W], br[W];
+        if (slot) {
+            width = p.qwidth[query];
+            width2 = p.qwidth2[query];
+            k1 = p.k1[query];
+            const size_t pi = (size_t)query * p.nprobe + probe;
+            gadd = p.pgadd[pi];
+            gerr = p.pgerr[pi];
+            cutoff = kDense ? FLT_MAX : p.thresholds[query];
+            const int8_t *qb = p.qbytes + (size_t)query * 2 * P + 8 * quad;
+#pragma unroll
+            for (int kc = 0; kc < W; ++kc) {
+                bq[kc] = *reinterpret_cast<const long *>(qb + 32 * kc);
+                br[kc] = *reinterpret_cast<const long *>(qb + P + 32 * kc);
+            }
+        } else {
+#pragma unroll
+            for (int kc = 0; kc < W; ++kc)
+                bq[kc] = br[kc] = 0;
+        }
+        for (uint32_t t = t_begin; t < t_end; ++t) {
+            const uint8_t *tile = p.tiles + (size_t)(tbase + t) * p.tile_bytes;
+            const float *fac = reinterpret_cast<const float *>(tile + 256u * W);
+            // words of vector 16 m + col for the four row blocks, and the factors of
+            // vectors 16 m + 4 quad + r
+            uint32_t xw[4][W];
+            float4 fa[4], fr[4], fe[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t v = 16 * m + col;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    if (4 * g + 4 <= W) {
+                        const uint4 c = *reinterpret_cast<const uint4 *>(tile + (size_t)g * 1024 + v * 16);
+                        xw[m][4 * g] = c.x;
+                        xw[m][4 * g + 1] = c.y;
+                        xw[m][4 * g + 2] = c.z;
+                        xw[m][4 * g + 3] = c.w;
+                    } else {
+                        const uint2 c = *reinterpret_cast<const uint2 *>(tile + (size_t)g * 1024 + v * 8);
+                        xw[m][4 * g] = c.x;
+                        xw[m][4 * g + 1] = c.y;
+                    }
+                }
+                const uint32_t o = 16 * m + 4 * quad;
+                fa[m] = *reinterpret_cast<const float4 *>(fac + o);
+                fr[m] = *reinterpret_cast<const float4 *>(fac + 64 + o);
+                fe[m] = *reinterpret_cast<const float4 *>(fac + 128 + o);
+            }
+            v4i32 acc[4], accr[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                acc[m] = v4i32{0, 0, 0, 0};
+                accr[m] = v4i32{0, 0, 0, 0};
+#pragma unroll
+                for (int kc = 0; kc < W; ++kc) {
+                    const long a = spread_byte((xw[m][kc] >> (8 * quad)) & 0xFFu);
+                    acc[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq[kc], acc[m], 0, 0, 0);
+                    accr[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, br[kc], accr[m], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const float fav[4] = {fa[m].x, fa[m].y, fa[m].z, fa[m].w};
+                const float frv[4] = {fr[m].x, fr[m].y, fr[m].z, fr[m].w};
+                const float fev[4] = {fe[m].x, fe[m].y, fe[m].z, fe[m].w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t local = t * kTileVectors + 16 * m + 4 * quad + r;
+                    const bool valid = slot && local < n;
+                    const int ip = acc[m][r];
+                    const float ex = width * (float)ip;
+                    const float low = fav[r] + gadd + frv[r] * (ex + k1) - fev[r] * gerr;
+                    if constexpr (kDense) {
+                        if (valid) {
+                            const size_t o = ((size_t)query * p.nprobe + probe) * p.dbg_stride + local;
+                            p.dbg_ip[o] = ip;
+                            p.dbg_ip2[o] = accr[m][r];
+                            p.dbg_low[o] = low;
+                        }
+                    } else {
+                        const bool survive = valid && low < cutoff;
+                        const unsigned long long mask = __ballot(survive);
+                        if (mask == 0)
+                            continue;
+                        const uint32_t cnt = (uint32_t)__popcll(mask);
+                        if (staged + cnt > (uint32_t)kStage) {
+                            flush_records(p, q, staged, s_rec, s_cut, limit, lane);
+                            staged = 0;
+                        }
+                        if (survive) {
+                            const uint32_t k = staged + lane_rank(mask);
+                            const float exact = two_stage_ip(width, ip, width2, accr[m][r]);
+                            s_rec[k] = make_uint4(w0, start + local, __float_as_uint(exact), __float_as_uint(low));
+                            s_cut[k] = cutoff;
+                        }
+                        staged += cnt;
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (!kDense) {
+        if (staged)
+            flush_records(p, q, staged, s_rec, s_cut, limit, lane);
+    }
+}
+
+template <class F>
+uint32_t resident_grid_mfma(F kernel) {
+    static std::mutex mu;
+    static std::map<const void *, uint32_t> cache;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(reinterpret_cast<const void *>(kernel));
+    if (it != cache.end())
+        return it->second;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 ||
+        cus <= 0) {
+        per_cu = 8;
+        cus = 256;
+    }
+    const uint32_t grid = (uint32_t)(per_cu * cus);
+    cache.emplace(reinterpret_cast<const void *>(kernel), grid);
+    return grid;
+}
+
+template <int W, bool kDense>
+void launch_w(const ScanParams &p, hipStream_t s) {
+    auto *k = far_mfma_kernel<W, kDense>;
+    k<<<resident_grid_mfma(k), 64, 0, s>>>(p);
+}
+
+}  // namespace
+
+bool far_mfma_supported(uint32_t W) { return W == 2 || W == 4 || W == 6 || W == 8; }
+
+void launch_far_mfma(const ScanParams &p, uint32_t W, bool dense, hipStream_t s) {
+    switch (W) {
+    case 2: dense ? launch_w<2, true>(p, s) : launch_w<2, false>(p, s); break;
+    case 4: dense ? launch_w<4, true>(p, s) : launch_w<4, false>(p, s); break;
+    case 6: dense ? launch_w<6, true>(p, s) : launch_w<6, false>(p, s); break;
+    case 8: dense ? launch_w<8, true>(p, s) : launch_w<8, false>(p, s); break;
+    default: break;
+    }
+}
+
+}  // namespace cora

@@ -66,7 +66,10 @@ enum cora_search_flags {
     /* Run the vanguard pairs as the reference does, a per-pair seed pass followed by a
      * recovery pass over each pair, instead of the fused per-query vanguard pass that is
      * used when the ex-codes are resident in HBM (vanguard depth <= 64, topk <= 128). */
-    CORA_FLAG_PAIR_SEEDS = 1u << 6
+    CORA_FLAG_PAIR_SEEDS = 1u << 6,
+    /* Scan the far pairs with the popcount kernel even where the matrix-core kernel
+     * applies (cross-query reuse with padded dimension 64..256). */
+    CORA_FLAG_NO_MFMA_SCAN = 1u << 7
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;

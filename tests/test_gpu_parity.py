@@ -207,11 +207,15 @@ def test_coarse_probe_large_nlist(nlist, tmp_path):
 
 
 @pytest.mark.parametrize("case_name", CASES)
-def test_popcount_estimator_bit_exact(case_name, request):
+@pytest.mark.parametrize("mfma", [True, False])
+def test_popcount_estimator_bit_exact(case_name, mfma, request):
+    """ip_int and ip_res of every (vector, probe) bit-exact, the lower bound within 1e-5,
+    from the far-scan kernel the search ran: the matrix-core one (int8 MFMA) or the
+    popcount one."""
     case = request.getfixturevalue(case_name)
     nprobe = min(8, case.file.nlist)
-    say(f"[gpu] dense popcount estimator parity on {case_name} nprobe={nprobe}")
-    eng, _, _ = run_frozen(case, nprobe, 10)
+    say(f"[gpu] dense estimator parity on {case_name} nprobe={nprobe} mfma={mfma}")
+    eng, _, _ = run_frozen(case, nprobe, 10, extra_flags=0 if mfma else ca.FLAG_NO_MFMA_SCAN)
     g = gpu_intermediates(eng, case, nprobe)
     maxc = case.ivf.max_cluster
     ip, ipr, low = eng.debug_dense(case.queries.shape[0], nprobe, maxc)
