@@ -229,13 +229,16 @@ def main():
 
     # the dominant scan kernel of the step (HIP events on the engine stream around it)
     W = c.padded_dim // 32
+    mfma_far = W in (2, 4, 6, 8)  # the engine's matrix-core far scan (cross-query reuse is on)
     kernels = {
         "vanguard_query_kernel": {
             "kernel": f"vanguard_query_kernel<{W}> (fused per-query vanguard pass: popcount lower bounds, "
                       "GPU refinement, top-k threshold)",
             "avg_launch_ms": round(avg_van_ms, 4), "bytes_per_launch": int(van_bpl), "achieved": van_achieved},
-        "scan_kernel": {
-            "kernel": f"scan_kernel<{W}, {8 if batch_q > 1 else 1}, 0> (far-pair RaBitQ popcount scan)",
+        "far_mfma_kernel" if mfma_far else "scan_kernel": {
+            "kernel": (f"far_mfma_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA ip_int/ip_res, units of "
+                       "16 same-cluster pairs)") if mfma_far else
+                      f"scan_kernel<{W}, {8 if batch_q > 1 else 1}, 0> (far-pair RaBitQ popcount scan)",
             "avg_launch_ms": round(avg_scan_ms, 4), "bytes_per_launch": int(bytes_per_launch),
             "achieved": achieved},
     }

@@ -199,42 +199,103 @@ constexpr double kTightStart[9] = {0, 0.15, 0.20, 0.52, 0.59, 0.71, 0.75, 0.77, 
 
 // best_rescale_factor (rabitq_impl.hpp:276-333): sweep t upward through the points where
 // some coordinate's code increments and keep the t maximising <code + 1/2, |o|> / ||code + 1/2||.
+// The reference pops these events from a priority queue of (t, coordinate) pairs; the
+// events it pops are fixed in advance (per coordinate: its first increment, then each next
+// one while the code is below 2^ex - 1 and t < t_end), so the same sequence is produced
+// here by a bucket sort of all events on t, ties in coordinate order, in O(events), and
+// swept with the same double-precision updates in the same order.
 double best_rescale_factor(const float *o_abs, std::size_t dim, std::size_t ex_bits) {
     constexpr double kEps = 1e-5;
     constexpr int kNEnum = 10;
+    const int cap = (1 << ex_bits) - 1;
     const double max_o = *std::max_element(o_abs, o_abs + dim);
-    const double t_end = static_cast<double>(((1 << ex_bits) - 1) + kNEnum) / max_o;
+    const double t_end = static_cast<double>(cap + kNEnum) / max_o;
     const double t_start = t_end * kTightStart[ex_bits];
-    std::vector<int> cur(dim);
+    struct Event {
+        double t;
+        uint32_t dim;
+    };
+    thread_local std::vector<Event> ev, sorted;
+    thread_local std::vector<uint32_t> bucket;
+    ev.clear();
     double sqr_den = static_cast<double>(dim) * 0.25;
     double num = 0;
     for (std::size_t i = 0; i < dim; ++i) {
         const int c = static_cast<int>((t_start * o_abs[i]) + kEps);
-        cur[i] = c;
         sqr_den += c * c + c;
         num += (c + 0.5) * o_abs[i];
+        const double oi = o_abs[i];
+        ev.push_back({static_cast<double>(c + 1) / oi, static_cast<uint32_t>(i)});
+        for (int v = c + 1; v < cap; ++v) {  // code after the previous pop is v
+            const double tn = static_cast<double>(v + 1) / oi;
+            if (!(tn < t_end))
+                break;
+            ev.push_back({tn, static_cast<uint32_t>(i)});
+        }
     }
-    using Item = std::pair<double, std::size_t>;
-    std::priority_queue<Item, std::vector<Item>, std::greater<>> next;
+    // Events below t_end are bucket-sorted over [lo, t_end) (bucket index monotone in t;
+    // stable, so coordinate order within a bucket, then insertion-sorted on (t, coordinate)).
+    // The few events at or above t_end (first increments of near-zero coordinates, +inf for a
+    // zero one) all come after them and are sorted on their own.
+    double lo = t_end;
+    std::size_t n_main = 0;
+    for (const Event &e : ev)
+        if (e.t < t_end) {
+            lo = std::min(lo, e.t);
+            ++n_main;
+        }
+    // one bucket per event; the bucket of each event is computed once
+    const std::size_t nb = n_main + 1;
+    const double scale = t_end > lo ? static_cast<double>(nb - 1) / (t_end - lo) : 0.0;
+    thread_local std::vector<uint32_t> bid;
+    bid.resize(ev.size());
+    bucket.assign(nb + 1, 0);
+    for (std::size_t k = 0; k < ev.size(); ++k) {
+        const double t = ev[k].t;
+        const uint32_t b = t < t_end ? static_cast<uint32_t>(std::min<double>((t - lo) * scale, nb - 1))
+                                     : static_cast<uint32_t>(nb);
+        bid[k] = b;
+        if (b < nb)
+            ++bucket[b + 1];
+    }
+    for (std::size_t b = 0; b < nb; ++b)
+        bucket[b + 1] += bucket[b];
+    sorted.resize(ev.size());
+    std::size_t n_over = 0;
+    for (std::size_t k = 0; k < ev.size(); ++k) {
+        if (bid[k] < nb)
+            sorted[bucket[bid[k]]++] = ev[k];
+        else
+            sorted[n_main + n_over++] = ev[k];
+    }
+    auto before = [](const Event &a, const Event &b) { return a.t < b.t || (a.t == b.t && a.dim < b.dim); };
+    for (std::size_t b = 0, s0 = 0; b < nb; ++b) {
+        const std::size_t s1 = bucket[b];
+        for (std::size_t i = s0 + 1; i < s1; ++i) {
+            const Event x = sorted[i];
+            std::size_t j = i;
+            while (j > s0 && before(x, sorted[j - 1])) {
+                sorted[j] = sorted[j - 1];
+                --j;
+            }
+            sorted[j] = x;
+        }
+        s0 = s1;
+    }
+    std::sort(sorted.begin() + n_main, sorted.end(), before);
+    thread_local std::vector<int> cur;
+    cur.resize(dim);
     for (std::size_t i = 0; i < dim; ++i)
-        next.emplace(static_cast<double>(cur[i] + 1) / o_abs[i], i);
+        cur[i] = static_cast<int>((t_start * o_abs[i]) + kEps);
     double best_ip = 0, best_t = 0;
-    while (!next.empty()) {
-        const double t = next.top().first;
-        const std::size_t id = next.top().second;
-        next.pop();
-        const int v = ++cur[id];
+    for (const Event &e : sorted) {
+        const int v = ++cur[e.dim];
         sqr_den += 2 * v;
-        num += o_abs[id];
+        num += o_abs[e.dim];
         const double ip = num / std::sqrt(sqr_den);
         if (ip > best_ip) {
             best_ip = ip;
-            best_t = t;
-        }
-        if (v < (1 << ex_bits) - 1) {
-            const double tn = static_cast<double>(v + 1) / o_abs[id];
-            if (tn < t_end)
-                next.emplace(tn, id);
+            best_t = e.t;
         }
     }
     return best_t;

@@ -532,6 +532,71 @@ def recall_at_k(result_ids: np.ndarray, gt: np.ndarray, k: int) -> float:
 
 
 # How each function is pinned (see tests/test_oracle.py):
+_TIGHT_START = [0.0, 0.15, 0.20, 0.52, 0.59, 0.71, 0.75, 0.77, 0.81]  # rabitq_impl.hpp:263-273
+
+
+def excode_residual_abs(x: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """|o| / ||o|| in the builder's arithmetic (quantize_ex_bits): o = x - c in f32,
+    ||o||^2 accumulated sequentially in f64 and rounded to f32, sqrt and division in f32."""
+    o = (np.asarray(x, np.float32) - np.asarray(c, np.float32)).astype(np.float32)
+    acc = 0.0
+    for v in o.tolist():
+        acc += v * v
+    norm = np.sqrt(np.float32(acc))
+    return o, np.abs((o / norm).astype(np.float32))
+
+
+def best_rescale_factor(o_abs: np.ndarray, ex_bits: int) -> float:
+    """The reference's rescale search (rabitq_impl.hpp:276-333): a min-priority queue of
+    (t, coordinate) increment points, t from t_start = t_end * tight_start[ex] up to
+    t_end = (2^ex - 1 + 10) / max|o|; each pop increments the coordinate's code, updates
+    <code + 1/2, |o|> and ||code + 1/2||^2 in double, and keeps the first t of the largest
+    ratio; the coordinate's next point is pushed while its code is below 2^ex - 1 and the
+    point is below t_end."""
+    import heapq
+    import math
+    eps, n_enum = 1e-5, 10
+    cap = (1 << ex_bits) - 1
+    oa = [float(v) for v in o_abs]
+    max_o = max(oa)
+    t_end = (cap + n_enum) / max_o
+    t_start = t_end * _TIGHT_START[ex_bits]
+    cur = [int(t_start * v + eps) for v in oa]
+    sqr_den = len(oa) * 0.25
+    num = 0.0
+    for c, v in zip(cur, oa):
+        sqr_den += c * c + c
+        num += (c + 0.5) * v
+    heap = [((c + 1) / v if v != 0 else math.inf, i) for i, (c, v) in enumerate(zip(cur, oa))]
+    heapq.heapify(heap)
+    best_ip, best_t = 0.0, 0.0
+    while heap:
+        t, i = heapq.heappop(heap)
+        cur[i] += 1
+        v = cur[i]
+        sqr_den += 2 * v
+        num += oa[i]
+        ip = num / math.sqrt(sqr_den)
+        if ip > best_ip:
+            best_ip, best_t = ip, t
+        if v < cap:
+            tn = (v + 1) / oa[i] if oa[i] != 0 else math.inf
+            if tn < t_end:
+                heapq.heappush(heap, (tn, i))
+    return best_t
+
+
+def quantize_excode(x: np.ndarray, c: np.ndarray, ex_bits: int) -> np.ndarray:
+    """7-bit ex-code of one vector (rabitq_impl.hpp:336-360, 423-429): floor(t |o_i| + eps)
+    capped, bitwise complement on negative residual coordinates."""
+    o, oa = excode_residual_abs(x, c)
+    t = best_rescale_factor(oa, ex_bits)
+    cap = (1 << ex_bits) - 1
+    code = np.array([min(int(t * float(v) + 1e-5), cap) for v in oa], np.int64)
+    code = np.where(o < 0, (~code) & cap, code)
+    return code.astype(np.uint8)
+
+
 PINNED = {
     "read_ivf": "golden: ref_dump meta/ids/centroids/rotator (reference IVF::load)",
     "search_data": "golden: ref_dump short_data/short_factors/long_codes/ex_factors (reference SearchData)",
@@ -556,4 +621,8 @@ PINNED = {
     "vanguard_seeds": "brute force: equals the first min(keep, #valid) of a full stable sort of valid lows",
     "refine_error_bound": "property: bounds |f32 refine - f64 refine| of refine_dist on golden ex-codes",
     "seed_threshold": "properties: >= topk seeds strictly below it with lows below it; >= true topk-th",
+    "excode_residual_abs": "golden: quantize_excode reproduces the reference builder's ex-codes (quant_d128)",
+    "best_rescale_factor": "golden: quantize_excode reproduces the reference builder's ex-codes (quant_d128); "
+                           "brute force over every increment point on small dims",
+    "quantize_excode": "golden: the reference builder's ex-codes of quant_d128 (rows vs centroid row 0)",
 }

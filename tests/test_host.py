@@ -242,3 +242,17 @@ def test_excode_ip7_avx2_and_dispatched_paths_agree(golden, tmp_path):
     want = orc.excode_ip(q, packed, 128)
     for isa, (width, ip) in outs.items():
         assert np.all(np.abs(ip - want) <= 1e-6 * np.abs(q).sum() * 127), isa
+
+
+@pytest.mark.parametrize("P", [64, 128, 256])
+def test_builder_excodes_equal_reference_rescale_search(P):
+    """The builder's rescale search (events bucket-sorted on t, then swept) gives exactly the
+    ex-codes of the oracle's priority-queue restatement of the reference's search."""
+    import cora_oracle as orc
+    rng = np.random.default_rng(P)
+    rows = rng.normal(size=(24, P)).astype(np.float32)
+    cent = (0.2 * rng.normal(size=P)).astype(np.float32)
+    rows[3, :5] = cent[:5]  # a few zero residual coordinates
+    _, _, ex, _ = ca.quantize_rows(rows, cent, metric=0)
+    want = np.stack([orc.quantize_excode(r, cent, 7) for r in rows])
+    assert np.array_equal(ex, want)

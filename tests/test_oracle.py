@@ -310,3 +310,48 @@ def test_seed_threshold_properties():
     lows[3] = 50.0
     assert orc.seed_threshold(d, lows, np.zeros(20, np.float32), 10) > 50.0
     assert orc.seed_threshold(d[:5], lows[:5], np.zeros(5, np.float32), 10) is None
+
+
+def test_quantize_excode_reproduces_reference_builder(golden):
+    """The oracle's restatement of the rescale search reproduces the reference builder's
+    ex-codes (rows 1.. against row 0 as centroid, L2)."""
+    g = golden("quant_d128")
+    rows = np.fromfile(GOLDEN / "quant_d128" / "rows.f32", dtype=np.float32).reshape(-1, 128)
+    codes = np.stack([orc.quantize_excode(r, rows[0], 7) for r in rows[1:]])
+    mism = (codes != g["excode_l2"]).mean()
+    assert mism <= 0.002, mism
+
+
+def test_best_rescale_factor_brute_force():
+    """The priority-queue sweep equals a brute force that evaluates the ratio after every
+    increment point in (t, coordinate) order."""
+    import math
+    rng = np.random.default_rng(31)
+    for dim, ex in ((8, 7), (16, 3), (12, 5)):
+        for _ in range(20):
+            oa = np.abs(rng.normal(size=dim)).astype(np.float32)
+            oa /= np.float32(np.linalg.norm(oa))
+            cap = (1 << ex) - 1
+            t_end = (cap + 10) / float(oa.max())
+            t_start = t_end * orc._TIGHT_START[ex]
+            c0 = [int(t_start * float(v) + 1e-5) for v in oa]
+            pts = []
+            for i, v in enumerate(oa.tolist()):
+                k, c = 1, c0[i]
+                pts.append(((c + 1) / v, i))
+                while c + k < cap and (c + k + 1) / v < t_end:
+                    pts.append(((c + k + 1) / v, i))
+                    k += 1
+            pts.sort()
+            cur = list(c0)
+            num = sum((c + 0.5) * v for c, v in zip(c0, oa.tolist()))
+            den = dim * 0.25 + sum(c * c + c for c in c0)
+            best, bt = 0.0, 0.0
+            for t, i in pts:
+                cur[i] += 1
+                den += 2 * cur[i]
+                num += float(oa[i])
+                r = num / math.sqrt(den)
+                if r > best:
+                    best, bt = r, t
+            assert orc.best_rescale_factor(oa, ex) == bt
