@@ -182,6 +182,7 @@ HOST_SIGNATURES = {
     "cora_quantize_rows": [_P, _P, _U64, _U64, _U64, _I, _P, _P, _P, _P],
     "cora_excode_ip7": [_P, _P, _U64, _U64, _P],
     "cora_cpu_refine_isa": [],
+    "cora_gaussian_mixture": [_P, _U64, _U64, _P, _U64, _U64, _I, _I, _P, _P],
     "cora_test_ring": [C.POINTER(cora_ring_test), _P, _P],
 }
 
@@ -433,6 +434,20 @@ def quantize_rows(rows, centroid, metric=0, ex_bits=7):
     _host_check(_load()[1].cora_quantize_rows(_ptr(rows), _ptr(centroid), n, P, ex_bits, metric,
                                               _ptr(bits), _ptr(f1), _ptr(ex), _ptr(f2)))
     return bits, f1, ex, f2
+
+
+def gaussian_mixture(centers, sd, n, seed, normalize=False, threads=0):
+    """n rows centers[label] + sd * z (z standard normal), optionally L2-normalised, from
+    counter-based streams: the same output for any thread count."""
+    centers = np.ascontiguousarray(centers, np.float32)
+    sd = np.ascontiguousarray(sd, np.float32)
+    k, dim = centers.shape
+    if dim % 2 or sd.shape != (dim,):
+        raise ValueError("gaussian_mixture: dim must be even and sd of length dim")
+    out = np.empty((n, dim), np.float32)
+    _host_check(_load()[1].cora_gaussian_mixture(_ptr(centers), k, dim, _ptr(sd), n, seed,
+                                                 int(normalize), threads, _ptr(out), None))
+    return out
 
 
 def excode_ip7(q, packed):

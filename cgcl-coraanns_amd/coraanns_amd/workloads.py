@@ -4,7 +4,8 @@ Data generation is numpy (seeded); k-means, nearest-centroid assignment, rotatio
 exhaustive ground truth run on the GPU through the engine's cora_tool_* entry points; the
 IVF-RaBitQ index is written in the reference's on-disk format by the C++ builder.
 Seeds follow the measurement plan: base = cfg, queries = 1000 + cfg, k-means = 2000 + cfg,
-rotation = 3000 + cfg.
+rotation = 3000 + cfg. Configurations of more than 2^31 values (4 and 5) draw base and
+queries from the engine's counter-based generator (cora_gaussian_mixture) in parallel.
 """
 from __future__ import annotations
 
@@ -15,7 +16,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from . import build_ivf, gpu_assign, gpu_kmeans, gpu_rotate, gpu_topk
+from . import build_ivf, gaussian_mixture, gpu_assign, gpu_kmeans, gpu_rotate, gpu_topk
 
 
 @dataclass
@@ -78,15 +79,24 @@ def generate(c: Config, n=None, nq=None, queries_only=False):
         np.ones(c.dim, np.float32)
     centers = (_normal(rng_c, (c.n_centers, c.dim)) * (c.center_scale * np.sqrt(var))).astype(np.float32)
 
-    def draw(rng, m):
+    def draw(rng, m, rows=1 << 18):
         lab = rng.integers(0, c.n_centers, m)
         x = _normal(rng, (m, c.dim))
-        x *= (c.within_sd * np.sqrt(var))[None, :]
-        x += centers[lab]
-        if c.normalize:
-            x /= np.linalg.norm(x, axis=1, keepdims=True)
+        sd = (c.within_sd * np.sqrt(var))[None, :]
+        for s in range(0, m, rows):  # in row blocks: no full-size temporaries
+            blk = x[s:s + rows]
+            blk *= sd
+            blk += centers[lab[s:s + rows]]
+            if c.normalize:
+                blk /= np.linalg.norm(blk, axis=1, keepdims=True)
         return x
 
+    if c.n * c.dim > 1 << 31:
+        # configurations of billions of values: counter-based rows generated in parallel
+        # (the numpy stream runs at ~60 M values/s on one core)
+        sd = (c.within_sd * np.sqrt(var)).astype(np.float32)
+        base = None if queries_only else gaussian_mixture(centers, sd, n, c.cfg + 10_000, c.normalize)
+        return base, gaussian_mixture(centers, sd, nq, 1000 + c.cfg, c.normalize)
     base = None if queries_only else draw(np.random.default_rng(c.cfg + 10_000), n)
     queries = draw(np.random.default_rng(1000 + c.cfg), nq)
     return base, queries

@@ -69,6 +69,21 @@ __global__ void update_kernel(float *__restrict__ cent, const float *__restrict_
         cent[i] = sums[i] / (float)counts[c];
 }
 
+// The k selected of one base block, as (distance, global id) candidates:
+// cd/ci[row][slot0 + t] for t < k, from the block's distances [rows][len].
+__global__ void gather_block_topk_kernel(const float *__restrict__ dist, uint32_t len,
+                                         const int32_t *__restrict__ idx, uint32_t rows, uint32_t k,
+                                         uint32_t base0, uint32_t stride, uint32_t slot0,
+                                         float *__restrict__ cd, uint32_t *__restrict__ ci) {
+    const size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (t >= (size_t)rows * k)
+        return;
+    const size_t r = t / k, j = t % k;
+    const uint32_t i = (uint32_t)idx[t];
+    cd[r * stride + slot0 + j] = dist[r * len + i];
+    ci[r * stride + slot0 + j] = base0 + i;
+}
+
 struct DevBuf {
     void *p = nullptr;
     ~DevBuf() {
@@ -214,33 +229,56 @@ int cora_tool_topk(const float *h_base, uint64_t nb, const float *h_q, uint64_t 
         k > (uint64_t)kSelectMaxProbe || nb > 0x7FFFFFFF)
         return CORA_ERR_INVALID_ARGUMENT;
     TCHK(hipSetDevice(device));
-    const size_t qchunk = std::max<size_t>(1, std::min<size_t>(nq, (size_t)(2ull << 30) / (nb * 4)));
-    DevBuf b, bn, q, qn, dist, ids;
+    // Two levels: the base is cut into nblk blocks of <= 2^20 rows; each (query chunk, block)
+    // distance tile is selected to its k best, and the nblk * k candidates of a query are
+    // merged on the host by (distance, id), the select's own tie order.
+    const size_t nblk = (nb + (1u << 20) - 1) >> 20, blk = (nb + nblk - 1) / nblk;
+    const size_t qchunk = std::max<size_t>(1, std::min<size_t>(nq, (size_t)(1ull << 30) / blk));
+    const size_t stride = nblk * k;
+    DevBuf b, bn, q, qn, dist, ids, cd, ci;
     if (dev<float>(b, nb * dim) || dev<float>(bn, nb) || dev<float>(q, qchunk * dim) ||
-        dev<float>(qn, qchunk) || dev<float>(dist, qchunk * nb) || dev<int32_t>(ids, qchunk * k))
+        dev<float>(qn, qchunk) || dev<float>(dist, qchunk * blk) || dev<int32_t>(ids, qchunk * k) ||
+        dev<float>(cd, qchunk * stride) || dev<uint32_t>(ci, qchunk * stride))
         return CORA_ERR_RUNTIME;
     TCHK(hipMemcpy(b.p, h_base, nb * dim * 4, hipMemcpyHostToDevice));
     if (metric == 0)
         launch_row_norms((float *)b.p, (uint32_t)nb, (uint32_t)dim, (float *)bn.p, nullptr);
     else
         TCHK(hipMemset(bn.p, 0, nb * 4));
+    std::vector<float> hd(qchunk * stride);
+    std::vector<uint32_t> hi(qchunk * stride), order(stride);
     for (size_t s = 0; s < nq; s += qchunk) {
         const size_t rows = std::min(qchunk, nq - s);
         TCHK(hipMemcpy(q.p, h_q + s * dim, rows * dim * 4, hipMemcpyHostToDevice));
-        if (metric == 0) {
+        if (metric == 0)
             launch_row_norms((float *)q.p, (uint32_t)rows, (uint32_t)dim, (float *)qn.p, nullptr);
-            launch_dist_gemm((float *)q.p, (float *)qn.p, (float *)b.p, (float *)bn.p,
-                             (uint32_t)rows, (uint32_t)nb, (uint32_t)dim, (float *)dist.p, nullptr);
-        } else {
-            // an[m] + bn[n] - 2 * ip with zero norms = -2 ip: same order as -ip
+        else  // an[m] + bn[n] - 2 * ip with zero norms = -2 ip: same order as -ip
             TCHK(hipMemset(qn.p, 0, rows * 4));
-            launch_dist_gemm((float *)q.p, (float *)qn.p, (float *)b.p, (float *)bn.p,
-                             (uint32_t)rows, (uint32_t)nb, (uint32_t)dim, (float *)dist.p, nullptr);
+        for (size_t j = 0; j < nblk; ++j) {
+            const size_t b0 = j * blk, len = std::min(blk, nb - b0);
+            launch_dist_gemm((float *)q.p, (float *)qn.p, (float *)b.p + b0 * dim, (float *)bn.p + b0,
+                             (uint32_t)rows, (uint32_t)len, (uint32_t)dim, (float *)dist.p, nullptr);
+            launch_select((float *)dist.p, (uint32_t)rows, (uint32_t)len, (uint32_t)k, (int32_t *)ids.p,
+                          nullptr);
+            const size_t n = rows * k;
+            gather_block_topk_kernel<<<(unsigned)((n + 255) / 256), 256>>>(
+                (float *)dist.p, (uint32_t)len, (int32_t *)ids.p, (uint32_t)rows, (uint32_t)k, (uint32_t)b0,
+                (uint32_t)stride, (uint32_t)(j * k), (float *)cd.p, (uint32_t *)ci.p);
         }
-        launch_select((float *)dist.p, (uint32_t)rows, (uint32_t)nb, (uint32_t)k, (int32_t *)ids.p,
-                      nullptr);
         TCHK(hipGetLastError());
-        TCHK(hipMemcpy(h_ids + s * k, ids.p, rows * k * 4, hipMemcpyDeviceToHost));
+        TCHK(hipMemcpy(hd.data(), cd.p, rows * stride * 4, hipMemcpyDeviceToHost));
+        TCHK(hipMemcpy(hi.data(), ci.p, rows * stride * 4, hipMemcpyDeviceToHost));
+        for (size_t r = 0; r < rows; ++r) {
+            const float *d = hd.data() + r * stride;
+            const uint32_t *id = hi.data() + r * stride;
+            for (size_t t = 0; t < stride; ++t)
+                order[t] = (uint32_t)t;
+            std::partial_sort(order.begin(), order.begin() + k, order.end(), [&](uint32_t a, uint32_t c) {
+                return d[a] < d[c] || (d[a] == d[c] && id[a] < id[c]);
+            });
+            for (size_t t = 0; t < k; ++t)
+                h_ids[(s + r) * k + t] = id[order[t]];
+        }
     }
     return CORA_OK;
 }

@@ -3,7 +3,9 @@
 #include <omp.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <fstream>
 #include <limits>
@@ -458,6 +460,9 @@ IvfFile build_ivf(const BuildInput &in, int threads) {
     f.batch_data.assign(block0[in.nlist] * block_bytes, 0);
     f.ex_data.assign(in.n * stride, 0);
     const int nt = threads > 0 ? threads : omp_get_max_threads();
+    // large builds report every tenth of the vectors quantised on stderr
+    const std::size_t report = in.n >= (std::size_t{1} << 22) ? in.n / 10 : 0;
+    std::atomic<std::size_t> done{0};
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
     for (long long cl = 0; cl < static_cast<long long>(in.nlist); ++cl) {
         const std::size_t c = static_cast<std::size_t>(cl);
@@ -485,6 +490,11 @@ IvfFile build_ivf(const BuildInput &in, int threads) {
                 std::memcpy(rec + lc, f2, sizeof(f2));
             }
             fastscan_pack(compact.data(), len, P, blk);
+        }
+        if (report) {
+            const std::size_t before = done.fetch_add(n, std::memory_order_relaxed);
+            if (before / report != (before + n) / report)
+                std::fprintf(stderr, "[build_ivf] quantised %zu / %zu vectors\n", before + n, in.n);
         }
     }
     return f;

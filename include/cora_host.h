@@ -123,6 +123,13 @@ int cora_quantize_rows(const float *rows, const float *centroid, uint64_t n, uin
                        float *f2);
 /* <q', ex_code> of n packed 7-bit codes (the CPU refinement's inner product). */
 int cora_excode_ip7(const float *q, const uint8_t *packed, uint64_t n, uint64_t P, float *out);
+/* Benchmark data: n rows of a Gaussian mixture, row r = centers[label_r] + sd * z_r
+ * (z standard normal), L2-normalised when normalize != 0. Each value is a function of
+ * (seed, row, column) only (SplitMix64-hashed counters, Box-Muller), so the output does not
+ * depend on threads. dim must be even; labels (u32 [n]) may be NULL. */
+int cora_gaussian_mixture(const float *centers, uint64_t n_centers, uint64_t dim, const float *sd,
+                          uint64_t n, uint64_t seed, int normalize, int threads, float *out,
+                          uint32_t *labels);
 /* Vector width of the CPU refinement's inner product: 512 (AVX-512) or 256 (AVX2;
  * forced with CORA_CPU_ISA=avx2 in the environment). */
 int cora_cpu_refine_isa(void);

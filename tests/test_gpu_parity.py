@@ -89,6 +89,26 @@ def synth(tmp_path_factory):
     return Case(path, q, x)
 
 
+@pytest.fixture(scope="module")
+def synth_ip768(tmp_path_factory):
+    """6,000 x 768 unit vectors (P = 768, 24 words per code), 24 clusters, inner product,
+    48 queries: the embedding shape of the 20M x 768 configuration."""
+    rng = np.random.default_rng(768)
+    n, dim, nl, nq = 6000, 768, 24, 48
+    centers = rng.normal(0, 1, (nl, dim))
+    x = centers[rng.integers(0, nl, n)] + rng.normal(0, 0.5, (n, dim))
+    x = (x / np.linalg.norm(x, axis=1, keepdims=True)).astype(np.float32)
+    q = centers[rng.integers(0, nl, nq)] + rng.normal(0, 0.5, (nq, dim))
+    q = (q / np.linalg.norm(q, axis=1, keepdims=True)).astype(np.float32)
+    assign = (x @ centers.T).argmax(1).astype(np.uint32)
+    cent = np.stack([x[assign == c].mean(0) for c in range(nl)])
+    R = np.linalg.qr(rng.normal(size=(dim, dim)))[0].T.astype(np.float32)
+    path = tmp_path_factory.mktemp("synth768") / "synth768.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32),
+                 (cent @ R).astype(np.float32), assign, R, metric=1)
+    return Case(path, q, x)
+
+
 def run_frozen(case, nprobe, topk, thresholds=None, **kw):
     eng = make_engine(case, nprobe, topk, **kw)
     nq = case.queries.shape[0]
@@ -116,7 +136,7 @@ def gpu_intermediates(eng, case, nprobe):
     return g
 
 
-CASES = ["golden_l2", "golden_ip", "synth"]
+CASES = ["golden_l2", "golden_ip", "synth", "synth_ip768"]
 
 
 @pytest.mark.parametrize("case_name", CASES)
@@ -597,15 +617,17 @@ REF_DUMP = Path(__file__).resolve().parent.parent / "oracle" / "_ref" / "ref_dum
 
 
 @pytest.mark.skipif(not REF_DUMP.exists(), reason="oracle/_ref/ref_dump not built (needs /root/reference)")
-def test_topk_and_recall_match_reference_cpu_path(synth, tmp_path):
+@pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
+def test_topk_and_recall_match_reference_cpu_path(case_name, request, tmp_path):
     """Final top-k ids and recall against the reference's own CPU search (rabitqlib
     IVF::search with the FastScan-hacc estimator, ivf.hpp:670-732, run by the ref_dump
     checker built from the reference sources) on the same index file, same queries and
     same nprobe; production mode (live thresholds, vanguard 5, secondary filter)."""
     from coraanns_amd.workloads import write_fbin
 
+    synth = request.getfixturevalue(case_name)
     nprobes, topk = [4, 8, 16], 10
-    say("[gpu] top-k vs reference IVF::search")
+    say(f"[gpu] top-k vs reference IVF::search on {case_name}")
     qf = tmp_path / "q.fbin"
     write_fbin(qf, synth.queries)
     out = tmp_path / "ref"
@@ -613,7 +635,7 @@ def test_topk_and_recall_match_reference_cpu_path(synth, tmp_path):
     subprocess.run([str(REF_DUMP), "index", str(synth.path), str(qf), str(out), str(topk)] +
                    [str(n) for n in nprobes], check=True, capture_output=True, timeout=300)
     ref_ids = np.fromfile(out / "search_ids.bin", np.uint32).reshape(len(nprobes), -1, topk)
-    gt = orc.brute_force_gt(synth.base, synth.queries, topk, 0)
+    gt = orc.brute_force_gt(synth.base, synth.queries, topk, synth.file.metric)
     eng = make_engine(synth, max(nprobes), topk, vanguard=5, frozen=False, secondary=True)
     for li, nprobe in enumerate(nprobes):
         _, ids = eng.search_all(synth.queries, topk, nprobe)

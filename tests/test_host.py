@@ -256,3 +256,27 @@ def test_builder_excodes_equal_reference_rescale_search(P):
     _, _, ex, _ = ca.quantize_rows(rows, cent, metric=0)
     want = np.stack([orc.quantize_excode(r, cent, 7) for r in rows])
     assert np.array_equal(ex, want)
+
+
+def test_gaussian_mixture_generator():
+    """Counter-based benchmark rows: thread-count invariant, prefix-stable, standard normal
+    noise (moments, and a chi-square fit of the mixture labels), unit norm when asked."""
+    rng = np.random.default_rng(1)
+    centers = rng.standard_normal((8, 64)).astype(np.float32) * 5
+    sd = np.full(64, 0.5, np.float32)
+    a = ca.gaussian_mixture(centers, sd, 20000, seed=99, threads=1)
+    b = ca.gaussian_mixture(centers, sd, 20000, seed=99, threads=8)
+    assert np.array_equal(a, b)
+    assert np.array_equal(ca.gaussian_mixture(centers, sd, 500, seed=99), a[:500])
+    assert not np.array_equal(ca.gaussian_mixture(centers, sd, 500, seed=98), a[:500])
+    lab = np.argmin(((a[:, None, :] - centers[None]) ** 2).sum(-1), axis=1)
+    z = ((a - centers[lab]) / sd).astype(np.float64)
+    assert abs(z.mean()) < 0.01 and abs(z.var() - 1) < 0.01
+    assert abs((z ** 4).mean() - 3) < 0.05  # normal kurtosis
+    counts = np.bincount(lab, minlength=8)
+    chi2 = ((counts - 2500.0) ** 2 / 2500.0).sum()
+    assert chi2 < 24.3  # 7 dof, p = 0.001
+    u = ca.gaussian_mixture(centers, sd, 1000, seed=3, normalize=True)
+    assert np.allclose(np.linalg.norm(u, axis=1), 1, atol=1e-6)
+    with pytest.raises(ValueError):
+        ca.gaussian_mixture(centers[:, :63], sd[:63], 10, seed=1)
