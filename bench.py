@@ -43,10 +43,13 @@ def recall_at_k(ids, gt, k):
     return hits / (ids.shape[0] * k)
 
 
-def cpu_baseline(index_path, queries, gt, topk, nprobe, threads, workdir):
+def cpu_baseline(index_path, queries, gt, topk, nprobe, threads, workdir, sample):
+    """rabitq_cpu (the reference CPU path) on the first `sample` queries, 1 warmup + 3
+    rounds; None when it is not built, fails or exceeds its time limit."""
     exe = REPO / "oracle" / "_ref" / "rabitq_cpu"
     if not exe.exists():
         return None
+    queries, gt = queries[:sample], gt[:sample]
     from coraanns_amd.workloads import write_fbin
     qf, gf = Path(workdir) / "bq.fbin", Path(workdir) / "bgt.ibin"
     write_fbin(qf, queries)
@@ -55,7 +58,11 @@ def cpu_baseline(index_path, queries, gt, topk, nprobe, threads, workdir):
     cmd = [str(exe), str(index_path), str(qf), str(gf), "--topk", str(topk), "--nprobes", str(nprobe),
            "--threads", str(threads), "--warmup", "1", "--rounds", "3", "--hacc", "true"]
     t = time.time()
-    out = subprocess.run(cmd, capture_output=True, text=True, env=env, timeout=600)
+    try:
+        out = subprocess.run(cmd, capture_output=True, text=True, env=env, timeout=600)
+    except subprocess.TimeoutExpired:
+        log("[cpu_baseline] rabitq_cpu exceeded 600 s; no baseline")
+        return None
     if out.returncode != 0:
         log(f"[cpu_baseline] rabitq_cpu failed: {out.stderr[-500:]}")
         return None
@@ -103,12 +110,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--config", type=int, default=4,
+                    help="BASELINE configuration (default 4: 20M x 768 inner product, the headline workload)")
     ap.add_argument("--nprobe", type=int, default=0, help="0: smallest grid nprobe reaching the recall target")
     ap.add_argument("--recall-target", type=float, default=0.9)
     ap.add_argument("--batch-q", type=int, default=0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-queries", type=int, default=0,
+                    help="queries in the CPU baseline sample (0: all at P <= 128, 2,000 above)")
     ap.add_argument("--n", type=int, default=0, help="override base size (testing only)")
     ap.add_argument("--nq", type=int, default=0, help="override query count (testing only)")
     ap.add_argument("--no-gpu-seed", action="store_true",
@@ -252,7 +262,8 @@ def main():
 
     baseline = None
     if not args.no_cpu_baseline:
-        baseline = cpu_baseline(index_path, queries, gt, c.topk, nprobe, threads, workdir)
+        sample = args.cpu_queries or (queries.shape[0] if c.padded_dim <= 128 else 2000)
+        baseline = cpu_baseline(index_path, queries, gt, c.topk, nprobe, threads, workdir, sample)
 
     line = {
         "metric": "QPS at recall@10>=0.9 (1 GPU)",

@@ -149,8 +149,59 @@ int cora_tool_rotate(const float *h_x, uint64_t n, uint64_t dim, const float *h_
     return CORA_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Re-seed every empty cluster by splitting a populated one, as Faiss's Lloyd k-means does
+// after each update (the k-means the reference's index recipe trains with): cluster j is
+// chosen with probability proportional to (size_j - 1), its centroid is copied, the two
+// copies are pushed apart by a relative 1/1024 in alternating directions per dimension,
+// and the size is assumed to split evenly. Without it a centroid left empty stays where it
+// was; on well-separated data such centroids drift towards the origin and end up closer
+// to every query than any populated cluster, so probe lists fill with empty clusters.
+// Returns the number of clusters re-seeded; cent [k][dim] and counts are host copies.
+uint32_t split_empty_clusters(std::vector<float> &cent, std::vector<uint32_t> &counts, uint32_t dim,
+                              std::mt19937_64 &gen) {
+    const uint32_t k = (uint32_t)counts.size();
+    constexpr float kEps = 1.0f / 1024.0f;
+    uint32_t split = 0;
+    for (uint32_t ci = 0; ci < k; ++ci) {
+        if (counts[ci])
+            continue;
+        uint64_t total = 0;
+        for (uint32_t j = 0; j < k; ++j)
+            total += counts[j] > 1 ? counts[j] - 1 : 0;
+        if (!total)
+            break;  // nothing left to split
+        uint64_t r = std::uniform_int_distribution<uint64_t>(0, total - 1)(gen);
+        uint32_t cj = 0;
+        for (; cj < k; ++cj) {
+            const uint64_t w = counts[cj] > 1 ? counts[cj] - 1 : 0;
+            if (r < w)
+                break;
+            r -= w;
+        }
+        float *a = &cent[(size_t)ci * dim], *b = &cent[(size_t)cj * dim];
+        for (uint32_t d = 0; d < dim; ++d) {
+            const float v = b[d];
+            a[d] = v * (d % 2 == 0 ? 1 + kEps : 1 - kEps);
+            b[d] = v * (d % 2 == 0 ? 1 - kEps : 1 + kEps);
+        }
+        counts[ci] = counts[cj] / 2;
+        counts[cj] -= counts[ci];
+        ++split;
+    }
+    return split;
+}
+
+}  // namespace
+
+extern "C" {
+
 // Lloyd k-means on n rows (FP32 squared L2), initial centroids = k distinct rows chosen
-// with a seeded generator; an empty cluster keeps its previous centroid.
+// with a seeded generator; after each update, empty clusters are re-seeded by splitting
+// populated ones (split_empty_clusters).
 int cora_tool_kmeans(const float *h_x, uint64_t n, uint64_t dim, uint64_t k, uint32_t iters,
                      uint64_t seed, float *h_centroids, int device) {
     if (!h_x || !h_centroids || !n || !dim || !k || k > n || k > 0x7FFFFFFF)
@@ -175,6 +226,8 @@ int cora_tool_kmeans(const float *h_x, uint64_t n, uint64_t dim, uint64_t k, uin
         return CORA_ERR_RUNTIME;
     TCHK(hipMemcpy(x.p, h_x, n * dim * 4, hipMemcpyHostToDevice));
     TCHK(hipMemcpy(c.p, init.data(), k * dim * 4, hipMemcpyHostToDevice));
+    std::vector<uint32_t> counts(k);
+    std::mt19937_64 split_gen(seed ^ 0x9E3779B97F4A7C15ull);
     for (uint32_t it = 0; it < iters; ++it) {
         launch_row_norms((float *)c.p, (uint32_t)k, (uint32_t)dim, (float *)cn.p, nullptr);
         if (int rc = assign_rows((float *)x.p, n, (uint32_t)dim, (float *)c.p, (float *)cn.p,
@@ -189,6 +242,12 @@ int cora_tool_kmeans(const float *h_x, uint64_t n, uint64_t dim, uint64_t k, uin
                                                                    (uint32_t *)cnt.p, (uint32_t)k,
                                                                    (uint32_t)dim);
         TCHK(hipGetLastError());
+        TCHK(hipMemcpy(counts.data(), cnt.p, k * 4, hipMemcpyDeviceToHost));
+        if (std::find(counts.begin(), counts.end(), 0u) != counts.end()) {
+            TCHK(hipMemcpy(init.data(), c.p, k * dim * 4, hipMemcpyDeviceToHost));
+            if (split_empty_clusters(init, counts, (uint32_t)dim, split_gen))
+                TCHK(hipMemcpy(c.p, init.data(), k * dim * 4, hipMemcpyHostToDevice));
+        }
     }
     TCHK(hipDeviceSynchronize());
     TCHK(hipMemcpy(h_centroids, c.p, k * dim * 4, hipMemcpyDeviceToHost));

@@ -645,3 +645,52 @@ def test_topk_and_recall_match_reference_cpu_path(case_name, request, tmp_path):
         say(f"[gpu]   nprobe={nprobe}: id agreement {agree:.4f}, recall gpu {r_gpu:.4f} ref {r_ref:.4f}")
         assert agree >= 0.98, (nprobe, agree)
         assert abs(r_gpu - r_ref) <= 0.01, (nprobe, r_gpu, r_ref)
+
+
+@pytest.mark.parametrize("dim,metric", [(128, 0), (768, 1)])
+def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, tmp_path):
+    """Pair scheduling at nlist 16,384 (the 10M/20M configurations' nlist: global-atomic
+    bucket counting) and the scan statistics the benchmark's roofline is computed from:
+    the scheduled pairs are exactly the probe lists, vanguard pairs first; the far-pass
+    bytes are sum over clusters of ceil(m_c / unit) * n_c * (P/8 + 12), the vanguard bytes
+    sum m_c * n_c * (P/8 + 12) plus the refined vectors' (P + 8)."""
+    rng = np.random.default_rng(dim)
+    nlist, n, nq, nprobe, vanguard = 16384, 40000, 192, 32, 5
+    cent = rng.normal(0, 1, (nlist, dim)).astype(np.float32)
+    assign = rng.integers(0, nlist, n).astype(np.uint32)
+    x = (cent[assign] + rng.normal(0, 0.3, (n, dim))).astype(np.float32)
+    q = (cent[rng.integers(0, nlist, nq)] + rng.normal(0, 0.3, (nq, dim))).astype(np.float32)
+    if metric == 1:
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+    R = np.linalg.qr(rng.normal(size=(dim, dim)))[0].T.astype(np.float32)
+    path = tmp_path / "sched.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32),
+                 (cent.astype(np.float64) @ R).astype(np.float32), assign, R, metric=metric)
+    case = Case(path, q)
+    P = case.file.padded_dim
+    say(f"[gpu] pair schedule + scan bytes, nlist={nlist} P={P}")
+    eng = make_engine(case, nprobe, 10, vanguard=vanguard, frozen=False, secondary=True,
+                      gpu_seed_refine=True, gpu_refine_filter=True)
+    eng.reset_buffer(q)
+    eng.search(q, 10, nprobe)
+    st = eng.stats()
+    pidx = eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32)
+    pairs = eng.debug_read(ca.DBG_PAIRS, (nq * nprobe, 3), np.int32)
+    assert pidx.min() >= 0 and pidx.max() < nlist
+    # the scheduled pairs are the probe lists (as a multiset), vanguard pairs first
+    want = np.stack([pidx.reshape(-1), np.repeat(np.arange(nq), nprobe), np.tile(np.arange(nprobe), nq)], 1)
+    key = lambda a: np.lexsort((a[:, 2], a[:, 1], a[:, 0]))
+    assert np.array_equal(pairs[key(pairs)], want[key(want)])
+    nvan = nq * vanguard
+    assert np.all(pairs[:nvan, 2] < vanguard) and np.all(pairs[nvan:, 2] >= vanguard)
+    assert np.all(np.diff(pairs[nvan:, 0]) >= 0)  # far pairs grouped by cluster
+    sizes = case.sd.cluster_sizes.astype(np.int64)
+    bpv = P // 8 + 12
+    far_m = np.bincount(pidx[:, vanguard:].reshape(-1), minlength=nlist)
+    van_m = np.bincount(pidx[:, :vanguard].reshape(-1), minlength=nlist)
+    unit = 16 if (P // 32) in (2, 4, 6, 8) else 4  # matrix-core far scan, else batch-q 4
+    assert st["scan_vectors"] == int((far_m * sizes).sum())
+    assert st["scan_bytes"] == int((-(-far_m // unit) * sizes).sum()) * bpv
+    assert st["vanguard_bytes"] == int((van_m * sizes).sum()) * bpv + st["gpu_refined"] * (P + 8)
+    eng.close()

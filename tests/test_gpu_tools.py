@@ -112,3 +112,23 @@ def test_kmeans_reduces_inertia():
 
     assert np.isfinite(c20).all()
     assert inertia(c20) <= inertia(c1) * (1 + 1e-6)
+
+
+def test_kmeans_reseeds_empty_clusters():
+    """Well-separated unit-norm clusters (the 20M x 768 configuration's shape, scaled down)
+    with twice as many centroids as true clusters: random initialisation leaves some true
+    clusters without a centroid and the absorbing centroids drift to the origin, emptying
+    others. Empty clusters are re-seeded by splitting populated ones, so at the end every
+    centroid owns training rows and none sits near the origin."""
+    rng = np.random.default_rng(9)
+    ntrue, k, dim, n = 64, 128, 256, 32768
+    centers = rng.standard_normal((ntrue, dim)).astype(np.float32)
+    x = centers[rng.integers(0, ntrue, n)] + 0.5 * rng.standard_normal((n, dim)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    say("[tools] kmeans re-seeds empty clusters")
+    c = ca.gpu_kmeans(x, k, 20, seed=5)
+    a = ca.gpu_assign(x, c)
+    sizes = np.bincount(a, minlength=k)
+    assert sizes.min() >= 1, np.sort(sizes)[:8]
+    # a populated centroid is the mean of one true cluster's unit vectors (norm ~0.9)
+    assert np.linalg.norm(c, axis=1).min() > 0.5
