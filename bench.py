@@ -239,15 +239,17 @@ def main():
 
     # the dominant scan kernel of the step (HIP events on the engine stream around it)
     W = c.padded_dim // 32
-    mfma_far = W in (2, 4, 6, 8)  # the engine's matrix-core far scan (cross-query reuse is on)
+    mfma_far = W in (2, 4, 6, 8, 16, 24, 32)  # the engine's matrix-core far scan (cross-query reuse is on)
+    far_name = (f"far_mfma_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA ip_int/ip_res" if W <= 8 else
+                f"far_mfma_wide_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA 16x16x64 ip_int, popcount "
+                "ip_res for survivors")
     kernels = {
         "vanguard_query_kernel": {
             "kernel": f"vanguard_query_kernel<{W}> (fused per-query vanguard pass: popcount lower bounds, "
                       "GPU refinement, top-k threshold)",
             "avg_launch_ms": round(avg_van_ms, 4), "bytes_per_launch": int(van_bpl), "achieved": van_achieved},
         "far_mfma_kernel" if mfma_far else "scan_kernel": {
-            "kernel": (f"far_mfma_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA ip_int/ip_res, units of "
-                       "16 same-cluster pairs)") if mfma_far else
+            "kernel": f"{far_name}, units of 16 same-cluster pairs)" if mfma_far else
                       f"scan_kernel<{W}, {8 if batch_q > 1 else 1}, 0> (far-pair RaBitQ popcount scan)",
             "avg_launch_ms": round(avg_scan_ms, 4), "bytes_per_launch": int(bytes_per_launch),
             "achieved": achieved},

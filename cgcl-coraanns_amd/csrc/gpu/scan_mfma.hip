@@ -246,6 +246,194 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
     }
 }
 
+// Residual inner product <b, qres> of vector v (0..63) of a tile, by popcount over the
+// query's residual planes: the wide kernel evaluates it for survivors only (and in the
+// dense debug mode), since the lower bound needs ip_int alone.
+template <int W>
+__device__ __forceinline__ int tile_ip_res(const uint8_t *__restrict__ tile, uint32_t v,
+                                           const uint32_t *__restrict__ rplanes) {
+    uint32_t x[W];
+#pragma unroll
+    for (int g = 0; g < W / 4; ++g) {
+        const uint4 c = *reinterpret_cast<const uint4 *>(tile + (size_t)g * 1024 + v * 16);
+        x[4 * g] = c.x;
+        x[4 * g + 1] = c.y;
+        x[4 * g + 2] = c.z;
+        x[4 * g + 3] = c.w;
+    }
+    return popc_ip<W>(x, rplanes, W);
+}
+
+// Sixteen bits as sixteen int8 0/1 values (bit e in byte e): one 128-bit MFMA operand.
+// Each nibble spreads over four bytes with one 24-bit multiply (copies 7 bits apart).
+__device__ __forceinline__ v4i32 spread16(uint32_t h) {
+    v4i32 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r[i] = (int)(__umul24((h >> (4 * i)) & 15u, 0x00204081u) & 0x01010101u);
+    return r;
+}
+
+// Survivors staged with their ip_int and tile position get their two-stage exact_ip.
+template <int W>
+__device__ void finalize_records(const ScanParams &p, uint32_t n, uint4 *s_rec, const uint32_t *s_loc,
+                                 uint32_t lane) {
+    __syncthreads();
+    for (uint32_t i = lane; i < n; i += 64) {
+        uint4 rec = s_rec[i];
+        const uint32_t query = rec.x & 0xFFFFu, loc = s_loc[i];
+        const int ipr = tile_ip_res<W>(p.tiles + (size_t)(loc >> 6) * p.tile_bytes, loc & 63u,
+                                       p.qplanes + ((size_t)query * 16 + 8) * W);
+        rec.z = __float_as_uint(two_stage_ip(p.qwidth[query], (int)rec.z, p.qwidth2[query], ipr));
+        s_rec[i] = rec;
+    }
+}
+
+// Finalize and publish the wide kernel's staged survivors; out of line, so the unrolled
+// scan loop carries one call instead of the refinement and publication code.
+template <int W>
+__device__ __noinline__ void flush_wide(const ScanParams &p, uint32_t n, uint4 *s_rec, const float *s_cut,
+                                        const uint32_t *s_loc, unsigned long long &limit, uint32_t lane) {
+    finalize_records<W>(p, n, s_rec, s_loc, lane);
+    flush_records(p, p.queue, n, s_rec, s_cut, limit, lane);
+}
+
+constexpr int kStageWide = 384;  // wide kernel: flushed when a row block could overflow it
+
+// Wide codes (W = 16, 24, 32: P = 512, 768, 1024) on v_mfma_i32_16x16x64_i8. Lane-group
+// g = lane / 16 owns code words [g W/4, (g+1) W/4) of every vector: K-step s (64
+// dimensions) takes the 16-bit half s % 2 of word g W/4 + s / 2, i.e. dimensions
+// 8 W g + 16 s + e, e = 0..15, and the query operand the same 16 bytes of qint, so
+// each lane loads W/8 aligned 8-byte pairs per row block and the unit's qint operands
+// (W/2 x 16 bytes) stay in VGPRs. Only the dimension pairing between the two operands
+// matters to the sum, so ip_int is exact. The lower bound uses the popcount kernels'
+// expression; ip_res is evaluated for survivors when they are published.
+template <int W, bool kDense>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void far_mfma_wide_kernel(const ScanParams p) {
+    static_assert(W % 8 == 0 && W >= 16 && W <= 32, "lane-group word ranges of even length");
+    constexpr int WQ = W / 4;  // code words per lane-group
+    constexpr int S = W / 2;   // K-steps of 64 dimensions
+    constexpr uint32_t P = 32u * W;
+    __shared__ uint4 s_rec[kDense ? 1 : kStageWide];
+    __shared__ float s_cut[kDense ? 1 : kStageWide];
+    __shared__ uint32_t s_loc[kDense ? 1 : kStageWide];
+    const uint32_t lane = threadIdx.x, col = lane & 15, quad = lane >> 4;
+    const QueueDev q = p.queue;
+    const uint32_t U = p.num_units[1];
+    const uint32_t ubase = p.num_units[0];
+    uint32_t range = blockIdx.x % kNumXcd, tries = 0;
+    uint32_t staged = 0;
+    unsigned long long limit =
+        kDense ? 0ull : __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+        const uint32_t u = next_far_unit(p.unit_cursor, U, range, tries, lane);
+        if (u >= U)
+            break;
+        const Unit un = p.units[ubase + u];
+        const uint32_t cluster = uniform(un.cluster), count = uniform(un.count);
+        const ClusterMeta cm = p.meta[cluster];
+        const uint32_t n = uniform(cm.n), start = uniform(cm.start), tbase = uniform(cm.tile_base);
+        const uint32_t t_begin = uniform(un.tiles) >> 8, t_end = t_begin + (uniform(un.tiles) & 255u);
+        if (n == 0 || t_begin >= t_end)
+            continue;
+        const bool slot = col < count;
+        const uint32_t w0 = slot ? p.pairs[uniform(un.pair_begin) + col].word0 : 0u;
+        const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
+        float width = 0.0f, k1 = 0.0f, gadd = 0.0f, gerr = 0.0f, cutoff = -FLT_MAX;
+        v4i32 bq[S];
+        if (slot) {
+            width = p.qwidth[query];
+            k1 = p.k1[query];
+            const size_t pi = (size_t)query * p.nprobe + probe;
+            gadd = p.pgadd[pi];
+            gerr = p.pgerr[pi];
+            cutoff = kDense ? FLT_MAX : p.thresholds[query];
+            const v4i32 *qb = reinterpret_cast<const v4i32 *>(p.qbytes + (size_t)query * 2 * P + 8 * W * quad);
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+                bq[s] = qb[s];
+        } else {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+                bq[s] = v4i32{0, 0, 0, 0};
+        }
+        for (uint32_t t = t_begin; t < t_end; ++t) {
+            const uint8_t *tile = p.tiles + (size_t)(tbase + t) * p.tile_bytes;
+            const float *fac = reinterpret_cast<const float *>(tile + 256u * W);
+            // one row block of 16 vectors at a time: its code words, its 12 K-steps, its
+            // lower bounds (keeps one block's operands live, not the tile's)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t v = 16 * m + col;
+                uint32_t xw[WQ];
+#pragma unroll
+                for (int j = 0; j < WQ; j += 2) {
+                    const uint32_t w = WQ * quad + j;  // even: the pair lies in one 4-word group
+                    const uint2 c = *reinterpret_cast<const uint2 *>(tile + (size_t)(w >> 2) * 1024 + v * 16 +
+                                                                     (w & 3u) * 4);
+                    xw[j] = c.x;
+                    xw[j + 1] = c.y;
+                }
+                // two accumulator chains (low and high halves of the words)
+                v4i32 acc = v4i32{0, 0, 0, 0}, acc1 = v4i32{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < WQ; ++j) {
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16(xw[j] & 0xFFFFu), bq[2 * j], acc, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16(xw[j] >> 16), bq[2 * j + 1], acc1, 0, 0, 0);
+                }
+                acc += acc1;
+                const uint32_t o = 16 * m + 4 * quad;
+                const float4 fa = *reinterpret_cast<const float4 *>(fac + o);
+                const float4 fr = *reinterpret_cast<const float4 *>(fac + 64 + o);
+                const float4 fe = *reinterpret_cast<const float4 *>(fac + 128 + o);
+                const float fav[4] = {fa.x, fa.y, fa.z, fa.w};
+                const float frv[4] = {fr.x, fr.y, fr.z, fr.w};
+                const float fev[4] = {fe.x, fe.y, fe.z, fe.w};
+                if constexpr (!kDense) {
+                    // a row block stages at most 4 x 64 records
+                    if (staged + 4 * 64 > (uint32_t)kStageWide) {
+                        flush_wide<W>(p, staged, s_rec, s_cut, s_loc, limit, lane);
+                        staged = 0;
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t local = t * kTileVectors + o + r;
+                    const bool valid = slot && local < n;
+                    const int ip = acc[r];
+                    const float ex = width * (float)ip;
+                    const float low = fav[r] + gadd + frv[r] * (ex + k1) - fev[r] * gerr;
+                    if constexpr (kDense) {
+                        if (valid) {
+                            const size_t od = ((size_t)query * p.nprobe + probe) * p.dbg_stride + local;
+                            p.dbg_ip[od] = ip;
+                            p.dbg_ip2[od] = tile_ip_res<W>(tile, o + r, p.qplanes + ((size_t)query * 16 + 8) * W);
+                            p.dbg_low[od] = low;
+                        }
+                    } else {
+                        const bool survive = valid && low < cutoff;
+                        const unsigned long long mask = __ballot(survive);
+                        if (mask == 0)
+                            continue;
+                        const uint32_t cnt = (uint32_t)__popcll(mask);
+                        if (survive) {
+                            const uint32_t k = staged + lane_rank(mask);
+                            s_rec[k] = make_uint4(w0, start + local, (uint32_t)ip, __float_as_uint(low));
+                            s_cut[k] = cutoff;
+                            s_loc[k] = (tbase + t) * kTileVectors + o + r;
+                        }
+                        staged += cnt;
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (!kDense) {
+        if (staged)
+            flush_wide<W>(p, staged, s_rec, s_cut, s_loc, limit, lane);
+    }
+}
+
 template <class F>
 uint32_t resident_grid_mfma(F kernel) {
     static std::mutex mu;
@@ -270,13 +458,20 @@ uint32_t resident_grid_mfma(F kernel) {
 
 template <int W, bool kDense>
 void launch_w(const ScanParams &p, hipStream_t s) {
-    auto *k = far_mfma_kernel<W, kDense>;
-    k<<<resident_grid_mfma(k), 64, 0, s>>>(p);
+    if constexpr (W <= 8) {
+        auto *k = far_mfma_kernel<W, kDense>;
+        k<<<resident_grid_mfma(k), 64, 0, s>>>(p);
+    } else {
+        auto *k = far_mfma_wide_kernel<W, kDense>;
+        k<<<resident_grid_mfma(k), 64, 0, s>>>(p);
+    }
 }
 
 }  // namespace
 
-bool far_mfma_supported(uint32_t W) { return W == 2 || W == 4 || W == 6 || W == 8; }
+bool far_mfma_supported(uint32_t W) {
+    return W == 2 || W == 4 || W == 6 || W == 8 || W == 16 || W == 24 || W == 32;
+}
 
 void launch_far_mfma(const ScanParams &p, uint32_t W, bool dense, hipStream_t s) {
     switch (W) {
@@ -284,6 +479,9 @@ void launch_far_mfma(const ScanParams &p, uint32_t W, bool dense, hipStream_t s)
     case 4: dense ? launch_w<4, true>(p, s) : launch_w<4, false>(p, s); break;
     case 6: dense ? launch_w<6, true>(p, s) : launch_w<6, false>(p, s); break;
     case 8: dense ? launch_w<8, true>(p, s) : launch_w<8, false>(p, s); break;
+    case 16: dense ? launch_w<16, true>(p, s) : launch_w<16, false>(p, s); break;
+    case 24: dense ? launch_w<24, true>(p, s) : launch_w<24, false>(p, s); break;
+    case 32: dense ? launch_w<32, true>(p, s) : launch_w<32, false>(p, s); break;
     default: break;
     }
 }

@@ -689,7 +689,7 @@ def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, tmp_path):
     bpv = P // 8 + 12
     far_m = np.bincount(pidx[:, vanguard:].reshape(-1), minlength=nlist)
     van_m = np.bincount(pidx[:, :vanguard].reshape(-1), minlength=nlist)
-    unit = 16 if (P // 32) in (2, 4, 6, 8) else 4  # matrix-core far scan, else batch-q 4
+    unit = 16 if (P // 32) in (2, 4, 6, 8, 16, 24, 32) else 4  # matrix-core far scan, else batch-q 4
     assert st["scan_vectors"] == int((far_m * sizes).sum())
     assert st["scan_bytes"] == int((-(-far_m // unit) * sizes).sum()) * bpv
     assert st["vanguard_bytes"] == int((van_m * sizes).sum()) * bpv + st["gpu_refined"] * (P + 8)
