@@ -235,10 +235,39 @@ __device__ void publish_held(VqShared &S, const QueueDev &q, uint32_t &dropped) 
     __syncthreads();
 }
 
-// P <= 128: at most 168 VGPRs so three workgroups (12 waves) share a CU, which the LDS
-// footprint also allows
+// The query's Bq=8 planes [kBq][W] in the constant address space: wave-uniform reads
+// become scalar loads whose words feed the AND as scalar operands.
+typedef __attribute__((address_space(4))) const uint32_t *ConstWords;
+
+// ip_int of one vector (words x) for W >= 16: the planes are read one 4-word group at a
+// time (8 x 4 scalar words), so they never occupy vector registers.
 template <int W>
-__global__ __launch_bounds__(kVqThreads, W > 0 && W <= 4 ? 3 : 1) void vanguard_query_kernel(
+__device__ __forceinline__ int popc_ip_scalar(const uint32_t (&x)[Words<W>::kMax], ConstWords planes) {
+    int a[kBq];
+#pragma unroll
+    for (int j = 0; j < kBq; ++j)
+        a[j] = 0;
+#pragma unroll
+    for (int g = 0; g < W / 4; ++g) {
+#pragma unroll
+        for (int j = 0; j < kBq; ++j) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                a[j] += __popc(x[4 * g + k] & planes[j * W + 4 * g + k]);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one group's 32 plane words live at a time
+    }
+    int ip = -(a[kBq - 1] << (kBq - 1));
+#pragma unroll
+    for (int j = 0; j < kBq - 1; ++j)
+        ip += a[j] << j;
+    return ip;
+}
+
+// P <= 128 and P >= 512: at most 168 VGPRs so three workgroups (12 waves) share a CU,
+// which the LDS footprint also allows
+template <int W>
+__global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) void vanguard_query_kernel(
     const ScanParams p, const VanguardArgs va) {
     extern __shared__ __align__(16) float s_dyn[];  // q' [P]
     __shared__ VqShared S;
@@ -317,6 +346,7 @@ __global__ __launch_bounds__(kVqThreads, W > 0 && W <= 4 ? 3 : 1) void vanguard_
     // lane; as SGPRs they would be spilled and re-read per tile), reloaded from LDS for
     // every segment so they are not live across the list refinement
     uint32_t preg[W > 0 && W <= 4 ? kBq * W : 1];
+    const ConstWords cplanes = (ConstWords)(p.qplanes + (size_t)qi * 2 * kBq * nw);
     const size_t lc = (size_t)P * 7 / 8;
     uint32_t dropped = 0, refined = 0;
     auto process_list = [&]() {
@@ -378,13 +408,22 @@ __global__ __launch_bounds__(kVqThreads, W > 0 && W <= 4 ? 3 : 1) void vanguard_
                     const uint8_t *code = p.ex_codes + gid * lc;
                     int ipa = 0, ipb = 0;
                     float ipx = 0.0f, fa = 0.0f, fr = 0.0f;
+                    // an opaque zero: plane and q' reads indexed with it stay in the chunk
+                    // instead of being hoisted into registers (half of q' alone would take
+                    // 384 per lane at P = 768)
+                    uint32_t pz = 0;
+                    asm volatile("" : "+s"(pz));
+                    const uint32_t *planes = S.planes + pz;
+                    const float *qv = s_q + pz;
                     if (have) {
                         if (sub == 0) {
                             fa = p.ex_factors[2 * gid];
                             fr = p.ex_factors[2 * gid + 1];
                         }
                         constexpr int kWl = W > 0 ? (W + 1) / 2 : kVqMaxW / 2;
-#pragma unroll
+                        // two words per iteration: unrolled fully, the 16 plane reads per
+                        // word would all be scheduled ahead (192 registers at P = 768)
+#pragma unroll 2
                         for (int i = 0; i < kWl; ++i) {
                             const uint32_t w = sub + 2 * i;
                             if (w < nw) {
@@ -397,11 +436,11 @@ __global__ __launch_bounds__(kVqThreads, W > 0 && W <= 4 ? 3 : 1) void vanguard_
                                 const uint32_t xw = *wp;
 #pragma unroll
                                 for (int b = 0; b < kBq - 1; ++b) {
-                                    ipa += __popc(xw & S.planes[b * nw + w]) << b;
-                                    ipb += __popc(xw & S.planes[(kBq + b) * nw + w]) << b;
+                                    ipa += __popc(xw & planes[b * nw + w]) << b;
+                                    ipb += __popc(xw & planes[(kBq + b) * nw + w]) << b;
                                 }
-                                ipa -= __popc(xw & S.planes[(kBq - 1) * nw + w]) << (kBq - 1);
-                                ipb -= __popc(xw & S.planes[(2 * kBq - 1) * nw + w]) << (kBq - 1);
+                                ipa -= __popc(xw & planes[(kBq - 1) * nw + w]) << (kBq - 1);
+                                ipb -= __popc(xw & planes[(2 * kBq - 1) * nw + w]) << (kBq - 1);
                             }
                         }
                         constexpr int kCl = W > 0 ? 2 * W : 2 * kVqMaxW;  // P/8 chunks over 2 lanes
@@ -409,7 +448,7 @@ __global__ __launch_bounds__(kVqThreads, W > 0 && W <= 4 ? 3 : 1) void vanguard_
                         for (int i = 0; i < kCl; ++i) {
                             const uint32_t c = sub + 2 * i;
                             if (c < P / 8)
-                                ipx += excode_chunk_ip<false>(code, s_q, c);
+                                ipx += excode_chunk_ip<false>(code, qv, c);
                         }
                     }
                     ipa += __shfl_xor(ipa, 1, 2);
@@ -588,10 +627,17 @@ __global__ __launch_bounds__(kVqThreads, W > 0 && W <= 4 ? 3 : 1) void vanguard_
             fetch(t + b * kVqWaves, bufs[b]);
     auto step = [&](TileRegs &cur, float cut) {
         int ip;
-        if constexpr (W > 0 && W <= 4)
+        if constexpr (W > 0 && W <= 4) {
             ip = popc_ip<W>(cur.x, preg, nw);
-        else
+        } else if constexpr (W >= 16) {
+            // re-read per tile: an opaque copy of the pointer keeps the scalar loads in
+            // the loop instead of hoisting all 8 W words out of it
+            ConstWords pl = cplanes;
+            asm volatile("" : "+s"(pl));
+            ip = popc_ip_scalar<W>(cur.x, pl);
+        } else {
             ip = popc_ip<W>(cur.x, S.planes, nw);
+        }
         const float ex = width * (float)ip;
         const float low = cur.fa + cur.gadd + cur.fr * (ex + k1) - cur.fe * cur.gerr;
         const bool pass = lane < cur.lim && low < cut;
