@@ -137,6 +137,38 @@ __device__ __forceinline__ float excode_chunk_ip(const uint8_t *__restrict__ cod
     return sum;
 }
 
+// <q', ex_code> over one whole 64-dimension group whose 56 bytes (seven 8-byte words, the
+// layout above) are already in registers; q64 points at the group's 64 values of q'.
+__device__ __forceinline__ float excode_group_ip(const uint2 (&grp)[7], const float *__restrict__ q64) {
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) {
+        uint32_t lo, hi;
+        if (k < 6) {
+            lo = grp[k].x & 0x3F3F3F3Fu;
+            hi = grp[k].y & 0x3F3F3F3Fu;
+        } else {
+            const uint32_t o = k - 6;
+            const uint2 a = grp[o], b = grp[2 + o], d = grp[4 + o];
+            lo = ((a.x >> 6) & 0x03030303u) | ((b.x >> 4) & 0x0C0C0C0Cu) | ((d.x >> 2) & 0x30303030u);
+            hi = ((a.y >> 6) & 0x03030303u) | ((b.y >> 4) & 0x0C0C0C0Cu) | ((d.y >> 2) & 0x30303030u);
+        }
+        lo |= ((grp[6].x >> k) & 0x01010101u) << 6;
+        hi |= ((grp[6].y >> k) & 0x01010101u) << 6;
+        const float4 q0 = *reinterpret_cast<const float4 *>(q64 + 8 * k);
+        const float4 q1 = *reinterpret_cast<const float4 *>(q64 + 8 * k + 4);
+        sum = fmaf((float)(lo & 0xFFu), q0.x, sum);
+        sum = fmaf((float)((lo >> 8) & 0xFFu), q0.y, sum);
+        sum = fmaf((float)((lo >> 16) & 0xFFu), q0.z, sum);
+        sum = fmaf((float)(lo >> 24), q0.w, sum);
+        sum = fmaf((float)(hi & 0xFFu), q1.x, sum);
+        sum = fmaf((float)((hi >> 8) & 0xFFu), q1.y, sum);
+        sum = fmaf((float)((hi >> 16) & 0xFFu), q1.z, sum);
+        sum = fmaf((float)(hi >> 24), q1.w, sum);
+    }
+    return sum;
+}
+
 // Refined distance of a candidate (cpu_refinement.cpp:183-192) from the HBM copy of the
 // ex-codes, evaluated by one lane, and a bound on its rounding difference from the CPU
 // consumer's evaluation (1e-4 of the magnitude of the terms).

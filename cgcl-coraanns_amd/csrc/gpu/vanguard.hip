@@ -388,6 +388,106 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
                     publish_held(S, q, dropped);
                 const uint32_t cn = min(kVqChunk, nwin - c0);
                 const uint32_t held0 = S.nheld;
+                // the refined distance of chunk vector e (lane sub == 0 of its group) into the
+                // chunk results and the held records
+                auto emit = [&](uint32_t e, bool have, uint32_t j, uint32_t pos, size_t gid, float low,
+                                int ipa, int ipb, float ipx, float fa, float fr) {
+                    if (!have) {
+                        S.c_key[e] = ~0ull;
+                        if (e < cn)
+                            S.h_rd[held0 + e] = processed_mark();
+                        return;
+                    }
+                    const float ex = two_stage_ip(width, ipa, width2, ipb);
+                    const float gadd = S.gadd[j];
+                    const float rd = fa + gadd + fr * (128.0f * ex + ipx + kbq);
+                    const float err = 1e-4f * (fabsf(fa) + fabsf(gadd) +
+                                               fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
+                    S.c_key[e] = ((unsigned long long)order_key(rd) << 32) | pos;
+                    S.c_err[e] = err;
+                    S.c_low[e] = low;
+                    const uint32_t h = held0 + e;
+                    S.h_word0[h] = (j << 16) | qi;
+                    S.h_gid[h] = (uint32_t)gid;
+                    S.h_ex[h] = ex;
+                    S.h_low[h] = low;
+                    S.h_rd[h] = rd;
+                    S.h_err[h] = err;
+                };
+                if constexpr (W >= 16) {
+                    // P >= 512: four lanes per vector, the chunk in two halves of 64 vectors;
+                    // each lane issues all of its loads (W/4 code words, W/8 ex-code groups of
+                    // 56 bytes, the ex-factors) before any arithmetic, so a half costs one
+                    // memory round trip instead of one per loop iteration
+                    constexpr int kWq = W / 4, kG = W / 8;
+#pragma unroll 1
+                    for (uint32_t half = 0; half < 2; ++half) {
+                        const uint32_t e = half * 64 + (tid >> 2), sub = tid & 3;
+                        const uint32_t li = e < cn ? S.win[c0 + e] : 0u;
+                        const float low = e < cn ? S.l_low[li] : processed_mark();
+                        const bool have = low < thr;
+                        const uint32_t pos = have ? S.l_pos[li] : 0u;
+                        uint32_t j = 0;
+                        while (have && pos >= S.off[j + 1])
+                            ++j;
+                        const uint32_t local = pos - S.off[j];
+                        const uint8_t *tile =
+                            p.tiles + (size_t)(S.tbase[j] + local / kTileVectors) * p.tile_bytes;
+                        const uint32_t vl = local % kTileVectors;
+                        const size_t gid = (size_t)S.start[j] + local;
+                        uint32_t pz = 0;  // opaque zero, as below
+                        asm volatile("" : "+s"(pz));
+                        const uint32_t *planes = S.planes + pz;
+                        const float *qv = s_q + pz;
+                        uint32_t xw[kWq];
+                        uint2 grp[kG][7];
+                        float fa = 0.0f, fr = 0.0f;
+                        if (have) {
+#pragma unroll
+                            for (int i = 0; i < kWq; ++i)  // word sub + 4 i: group i, component sub
+                                xw[i] = *reinterpret_cast<const uint32_t *>(tile + (size_t)i * 1024 + vl * 16 +
+                                                                            sub * 4);
+#pragma unroll
+                            for (int gi = 0; gi < kG; ++gi) {
+                                const uint2 *gp = reinterpret_cast<const uint2 *>(
+                                    p.ex_codes + gid * lc + (size_t)(sub + 4 * gi) * 56);
+#pragma unroll
+                                for (int k = 0; k < 7; ++k)
+                                    grp[gi][k] = gp[k];
+                            }
+                            if (sub == 0) {
+                                fa = p.ex_factors[2 * gid];
+                                fr = p.ex_factors[2 * gid + 1];
+                            }
+                        }
+                        int ipa = 0, ipb = 0;
+                        float ipx = 0.0f;
+                        if (have) {
+#pragma unroll
+                            for (int i = 0; i < kWq; ++i) {
+                                const uint32_t w = sub + 4 * i;
+#pragma unroll
+                                for (int b = 0; b < kBq - 1; ++b) {
+                                    ipa += __popc(xw[i] & planes[b * W + w]) << b;
+                                    ipb += __popc(xw[i] & planes[(kBq + b) * W + w]) << b;
+                                }
+                                ipa -= __popc(xw[i] & planes[(kBq - 1) * W + w]) << (kBq - 1);
+                                ipb -= __popc(xw[i] & planes[(2 * kBq - 1) * W + w]) << (kBq - 1);
+                            }
+#pragma unroll
+                            for (int gi = 0; gi < kG; ++gi)
+                                ipx += excode_group_ip(grp[gi], qv + 64 * (sub + 4 * gi));
+                        }
+#pragma unroll
+                        for (int o = 1; o < 4; o <<= 1) {
+                            ipa += __shfl_xor(ipa, o, 4);
+                            ipb += __shfl_xor(ipb, o, 4);
+                            ipx += __shfl_xor(ipx, o, 4);
+                        }
+                        if (sub == 0)
+                            emit(e, have, j, pos, gid, low, ipa, ipb, ipx, fa, fr);
+                    }
+                } else {
                 {
                     // vector e of the chunk on lanes 2e, 2e+1; each lane takes every other code
                     // word and every other 8-dimension ex-code chunk, so all loads of the chunk
@@ -454,30 +554,9 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
                     ipa += __shfl_xor(ipa, 1, 2);
                     ipb += __shfl_xor(ipb, 1, 2);
                     ipx += __shfl_xor(ipx, 1, 2);
-                    if (sub == 0 && e < kVqChunk) {
-                        if (!have) {
-                            S.c_key[e] = ~0ull;
-                            if (e < cn)
-                                S.h_rd[held0 + e] = processed_mark();
-                        } else {
-                            const float ex = two_stage_ip(width, ipa, width2, ipb);
-                            const float gadd = S.gadd[j];
-                            const float rd = fa + gadd + fr * (128.0f * ex + ipx + kbq);
-                            const float err =
-                                1e-4f * (fabsf(fa) + fabsf(gadd) +
-                                         fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
-                            S.c_key[e] = ((unsigned long long)order_key(rd) << 32) | pos;
-                            S.c_err[e] = err;
-                            S.c_low[e] = low;
-                            const uint32_t h = held0 + e;
-                            S.h_word0[h] = (j << 16) | qi;
-                            S.h_gid[h] = (uint32_t)gid;
-                            S.h_ex[h] = ex;
-                            S.h_low[h] = low;
-                            S.h_rd[h] = rd;
-                            S.h_err[h] = err;
-                        }
-                    }
+                    if (sub == 0 && e < kVqChunk)
+                        emit(e, have, j, pos, gid, low, ipa, ipb, ipx, fa, fr);
+                }
                 }
                 __syncthreads();
                 // merge the chunk's entering vectors (refined, below the current k-th key) into

@@ -529,8 +529,9 @@ def probed_vectors(case, g, q, nprobe):
     return out
 
 
+@pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
 @pytest.mark.parametrize("vanguard", [3, 8])
-def test_fused_vanguard_frozen_parity(synth, vanguard):
+def test_fused_vanguard_frozen_parity(case_name, vanguard, request):
     """Fused per-query vanguard pass in its deterministic test mode (frozen snapshot,
     lowered by the pass): the threshold is backed by topk published vanguard vectors below
     it; the vanguard pass publishes every vector with low and refined distance below the
@@ -538,9 +539,9 @@ def test_fused_vanguard_frozen_parity(synth, vanguard):
     vectors with low < threshold and refined distance within the bound; the final top-k is
     the top-k of that candidate set by the CPU consumer's distance."""
     nprobe, topk = 8, 10
-    case = synth
+    case = request.getfixturevalue(case_name)
     nq = case.queries.shape[0]
-    say(f"[gpu] fused vanguard pass, frozen parity, vanguard={vanguard}")
+    say(f"[gpu] fused vanguard pass, frozen parity, {case_name} vanguard={vanguard}")
     eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True,
                       extra_flags=ca.FLAG_GPU_SEED_FROZEN)
     eng.reset_buffer(case.queries)
