@@ -287,7 +287,7 @@ def main():
                    "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
                    "query_chunk": chunk, "sweep": sweep},
         "roofline": roofline,
-        "probe_mfma": {"kernel": "gemm_kernel<true> (coarse-probe L2 distances, v_mfma_f32_16x16x4f32)",
+        "probe_mfma": {"kernel": "dist_gemm_kernel (coarse-probe L2 distances, 128x128 tiles, v_mfma_f32_16x16x4f32)",
                        "flops_per_launch": int(np.mean(probe_flops)), "avg_launch_ms": round(avg_probe_ms, 4),
                        "achieved": round(probe_tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                        "frac": round(probe_tflops / FP32_MFMA_PEAK_TFLOPS, 4)},
