@@ -153,6 +153,7 @@ GPU_SIGNATURES = {
     "cora_gpu_debug_dense": [_P, _P, _P, _P, _U64],
     "cora_tool_last_error": [],
     "cora_tool_rotate": [_P, _U64, _U64, _P, _U64, _P, _I],
+    "cora_tool_quantize": [_P, _U64, _U64, _P, _U64, _P, _U64, _P, _I, _P, _P, _P, _P, _I],
     "cora_tool_kmeans": [_P, _U64, _U64, _U64, C.c_uint32, _U64, _P, _I],
     "cora_tool_assign": [_P, _U64, _U64, _P, _U64, _P, _I],
     "cora_tool_topk": [_P, _U64, _P, _U64, _U64, _U64, _I, _P, _I],
@@ -179,6 +180,7 @@ HOST_SIGNATURES = {
     "cora_ivf_arrays_get": [_P, C.POINTER(cora_ivf_arrays)],
     "cora_ivf_free": [_P],
     "cora_build_ivf": [_P, _P, _P, _P, _U64, _U64, _U64, _U64, _U64, _I, _I, C.c_char_p],
+    "cora_build_ivf_gpu": [_P, _P, _P, _P, _U64, _U64, _U64, _U64, _U64, _I, _I, _I, C.c_char_p],
     "cora_quantize_rows": [_P, _P, _U64, _U64, _U64, _I, _P, _P, _P, _P],
     "cora_excode_ip7": [_P, _P, _U64, _U64, _P],
     "cora_cpu_refine_isa": [],
@@ -421,6 +423,18 @@ def build_ivf(path, rotated_data, rotated_centroids, assignments, rotator, metri
     r = np.ascontiguousarray(rotator, np.float32)
     _host_check(_load()[1].cora_build_ivf(_ptr(x), _ptr(c), _ptr(a), _ptr(r), x.shape[0], r.shape[0],
                                           x.shape[1], c.shape[0], 7, metric, threads, str(path).encode()))
+
+
+def build_ivf_gpu(path, data, rotated_centroids, assignments, rotator, metric=0, device=0, threads=0):
+    """The same index as build_ivf(path, data @ rotator, ...) with the rotation and the RaBitQ
+    quantisation on the GPU (bit-identical to build_ivf on the GPU-rotated rows)."""
+    x = np.ascontiguousarray(data, np.float32)
+    c = np.ascontiguousarray(rotated_centroids, np.float32)
+    a = np.ascontiguousarray(assignments, np.uint32)
+    r = np.ascontiguousarray(rotator, np.float32)
+    _host_check(_load()[1].cora_build_ivf_gpu(_ptr(x), _ptr(c), _ptr(a), _ptr(r), x.shape[0], x.shape[1],
+                                              r.shape[1], c.shape[0], 7, metric, device, threads,
+                                              str(path).encode()))
 
 
 def quantize_rows(rows, centroid, metric=0, ex_bits=7):

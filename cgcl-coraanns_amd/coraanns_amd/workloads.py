@@ -16,7 +16,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from . import build_ivf, gaussian_mixture, gpu_assign, gpu_kmeans, gpu_rotate, gpu_topk
+from . import build_ivf, build_ivf_gpu, gaussian_mixture, gpu_assign, gpu_kmeans, gpu_rotate, gpu_topk
 
 
 @dataclass
@@ -126,7 +126,7 @@ def ground_truth(base, queries, k, metric, device=0, extra=16):
     return out
 
 
-def build_index(c: Config, base, path, device=0, log=print, kmeans_iters=20, threads=0):
+def build_index(c: Config, base, path, device=0, log=print, kmeans_iters=20, threads=0, gpu_quantize=True):
     P = c.padded_dim
     R = rotation(c.dim, P, 3000 + c.cfg)
     t = time.time()
@@ -138,11 +138,14 @@ def build_index(c: Config, base, path, device=0, log=print, kmeans_iters=20, thr
     log(f"[build] k-means {c.nlist} x {kmeans_iters} it on {sample_n:,} + assign {base.shape[0]:,}: "
         f"{time.time() - t:.1f}s")
     t = time.time()
-    xr = gpu_rotate(base, R, device)
     cr = (cent.astype(np.float64) @ R.astype(np.float64)).astype(np.float32)
-    build_ivf(path, xr, cr, assign, R, metric=c.metric, threads=threads)
-    log(f"[build] rotate + RaBitQ quantise + write {path}: {time.time() - t:.1f}s")
-    del xr
+    if gpu_quantize:
+        # rotation and RaBitQ quantisation on the GPU, packing on the host
+        build_ivf_gpu(path, base, cr, assign, R, metric=c.metric, device=device, threads=threads)
+    else:
+        build_ivf(path, gpu_rotate(base, R, device), cr, assign, R, metric=c.metric, threads=threads)
+    log(f"[build] rotate + RaBitQ quantise ({'GPU' if gpu_quantize else 'host'}) + write {path}: "
+        f"{time.time() - t:.1f}s")
     return R, cent, assign
 
 

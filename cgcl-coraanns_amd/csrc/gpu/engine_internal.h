@@ -161,6 +161,8 @@ struct VanguardArgs {
 void launch_repack(const uint32_t *ref_words, const float *ref_factors, const ClusterMeta *meta,
                    uint32_t nlist, uint32_t W, uint8_t *tiles, uint32_t tile_bytes,
                    hipStream_t s);
+// message returned by cora_tool_last_error() (tools.hip; thread-local)
+void set_tool_error(const char *msg);
 void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint32_t dim,
                    uint32_t P, hipStream_t s);
 void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,

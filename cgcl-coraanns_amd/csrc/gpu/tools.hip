@@ -123,6 +123,8 @@ int assign_rows(const float *d_x, size_t n, uint32_t dim, const float *d_c, cons
 
 }  // namespace
 
+void cora::set_tool_error(const char *msg) { g_tool_error = msg; }
+
 extern "C" {
 
 const char *cora_tool_last_error(void) { return g_tool_error.c_str(); }

@@ -268,6 +268,26 @@ int cora_build_ivf(const float *rotated_data, const float *rotated_centroids,
     });
 }
 
+int cora_build_ivf_gpu(const float *data, const float *rotated_centroids, const uint32_t *assignments,
+                       const float *rotator, uint64_t n, uint64_t dim, uint64_t padded_dim, uint64_t nlist,
+                       uint64_t ex_bits, int metric, int device, int threads, const char *out_path) {
+    NEED(out_path);
+    return guarded([&] {
+        index::GpuBuildInput in;
+        in.data = data;
+        in.rotated_centroids = rotated_centroids;
+        in.assignments = assignments;
+        in.rotator = rotator;
+        in.n = n;
+        in.dim = dim;
+        in.padded_dim = padded_dim;
+        in.nlist = nlist;
+        in.ex_bits = ex_bits;
+        in.metric = metric;
+        index::build_ivf_gpu(in, device, threads).save(out_path);
+    });
+}
+
 int cora_quantize_rows(const float *rows, const float *centroid, uint64_t n, uint64_t P,
                        uint64_t ex_bits, int metric, uint8_t *bits, float *f1, uint8_t *excode,
                        float *f2) {

@@ -12,9 +12,11 @@
 #include <numeric>
 #include <queue>
 #include <stdexcept>
+#include <string>
 #include <utility>
 #include <vector>
 
+#include "cora_gpu.h"
 #include "coraanns/index/ivf_builder.hpp"
 #include "coraanns/index/ivf_file.hpp"
 #include "coraanns/index/search_data.hpp"
@@ -223,7 +225,7 @@ double best_rescale_factor(const float *o_abs, std::size_t dim, std::size_t ex_b
     double sqr_den = static_cast<double>(dim) * 0.25;
     double num = 0;
     for (std::size_t i = 0; i < dim; ++i) {
-        const int c = static_cast<int>((t_start * o_abs[i]) + kEps);
+        const int c = static_cast<int>(std::fma(t_start, static_cast<double>(o_abs[i]), kEps));
         sqr_den += c * c + c;
         num += (c + 0.5) * o_abs[i];
         const double oi = o_abs[i];
@@ -288,7 +290,7 @@ double best_rescale_factor(const float *o_abs, std::size_t dim, std::size_t ex_b
     thread_local std::vector<int> cur;
     cur.resize(dim);
     for (std::size_t i = 0; i < dim; ++i)
-        cur[i] = static_cast<int>((t_start * o_abs[i]) + kEps);
+        cur[i] = static_cast<int>(std::fma(t_start, static_cast<double>(o_abs[i]), kEps));
     double best_ip = 0, best_t = 0;
     for (const Event &e : sorted) {
         const int v = ++cur[e.dim];
@@ -354,7 +356,7 @@ void quantize_ex_bits(const float *x, const float *c, std::size_t P, std::size_t
     const int cap = (1 << ex_bits) - 1;
     double ipnorm = 0;
     for (std::size_t i = 0; i < P; ++i) {
-        int v = static_cast<int>((t * o_abs[i]) + kEps);
+        int v = static_cast<int>(std::fma(t, static_cast<double>(o_abs[i]), kEps));
         v = std::min(v, cap);
         code[i] = static_cast<uint8_t>(v);
         ipnorm += (v + 0.5) * o_abs[i];
@@ -424,67 +426,77 @@ void fastscan_pack(const uint8_t *compact, std::size_t n, std::size_t P, uint8_t
     }
 }
 
-IvfFile build_ivf(const BuildInput &in, int threads) {
-    if (!in.rotated_data || !in.rotated_centroids || !in.assignments || !in.rotator || !in.n ||
-        !in.dim || in.padded_dim % 64 || in.padded_dim < in.dim || !in.nlist || in.ex_bits != 7)
-        throw std::invalid_argument("build_ivf: invalid input (ex_bits must be 7)");
-    const std::size_t P = in.padded_dim;
-    IvfFile f;
-    f.num = in.n;
-    f.dim = in.dim;
+namespace {
+
+// Cluster order of the rows and the 32-row block of each cluster's first row.
+struct ClusterLayout {
+    std::vector<std::size_t> start, block0;
+};
+
+// Header, rotator, centroids, cluster sizes and ids (cluster order) of an index over
+// `assign`, with zeroed code arrays.
+ClusterLayout layout_index(IvfFile &f, const float *rotated_centroids, const float *rotator,
+                           const uint32_t *assign, std::size_t n, std::size_t dim, std::size_t P,
+                           std::size_t nlist, std::size_t ex_bits, int metric) {
+    f.num = n;
+    f.dim = dim;
     f.padded_dim = P;
-    f.nlist = in.nlist;
-    f.ex_bits = in.ex_bits;
-    f.metric = static_cast<uint8_t>(in.metric);
-    f.rotator.assign(in.rotator, in.rotator + in.dim * P);
-    f.centroids.assign(in.rotated_centroids, in.rotated_centroids + in.nlist * P);
-    f.cluster_sizes.assign(in.nlist, 0);
-    for (std::size_t i = 0; i < in.n; ++i) {
-        if (in.assignments[i] >= in.nlist)
+    f.nlist = nlist;
+    f.ex_bits = ex_bits;
+    f.metric = static_cast<uint8_t>(metric);
+    f.rotator.assign(rotator, rotator + dim * P);
+    f.centroids.assign(rotated_centroids, rotated_centroids + nlist * P);
+    f.cluster_sizes.assign(nlist, 0);
+    for (std::size_t i = 0; i < n; ++i) {
+        if (assign[i] >= nlist)
             throw std::invalid_argument("build_ivf: bad cluster id");
-        ++f.cluster_sizes[in.assignments[i]];
+        ++f.cluster_sizes[assign[i]];
     }
-    std::vector<std::size_t> start(in.nlist + 1, 0), block0(in.nlist + 1, 0);
-    for (std::size_t c = 0; c < in.nlist; ++c) {
-        start[c + 1] = start[c] + f.cluster_sizes[c];
-        block0[c + 1] = block0[c] + (f.cluster_sizes[c] + 31) / 32;
+    ClusterLayout L;
+    L.start.assign(nlist + 1, 0);
+    L.block0.assign(nlist + 1, 0);
+    for (std::size_t c = 0; c < nlist; ++c) {
+        L.start[c + 1] = L.start[c] + f.cluster_sizes[c];
+        L.block0[c + 1] = L.block0[c] + (f.cluster_sizes[c] + 31) / 32;
     }
-    f.ids.resize(in.n);
-    {
-        std::vector<std::size_t> fill(start.begin(), start.end() - 1);
-        for (std::size_t i = 0; i < in.n; ++i)
-            f.ids[fill[in.assignments[i]]++] = static_cast<uint32_t>(i);
-    }
+    f.ids.resize(n);
+    std::vector<std::size_t> fill(L.start.begin(), L.start.end() - 1);
+    for (std::size_t i = 0; i < n; ++i)
+        f.ids[fill[assign[i]]++] = static_cast<uint32_t>(i);
+    f.batch_data.assign(L.block0[nlist] * f.batch_block_bytes(), 0);
+    f.ex_data.assign(n * f.ex_stride(), 0);
+    return L;
+}
+
+// Every cluster's 32-row FastScan blocks and every row's ex-code record. quant(c, id,
+// compact, f1, code, f2) gives row `id` of cluster c: its sign bits as big-endian bytes
+// [P/8], f_add / f_rescale / f_error, its ex-code values [P] and f_add_ex / f_rescale_ex.
+template <class Quant>
+void fill_index(IvfFile &f, const ClusterLayout &L, int threads, Quant quant) {
+    const std::size_t P = f.padded_dim, n_all = f.num;
     const std::size_t block_bytes = f.batch_block_bytes(), stride = f.ex_stride();
     const std::size_t lc = f.ex_code_bytes();
-    f.batch_data.assign(block0[in.nlist] * block_bytes, 0);
-    f.ex_data.assign(in.n * stride, 0);
     const int nt = threads > 0 ? threads : omp_get_max_threads();
     // large builds report every tenth of the vectors quantised on stderr
-    const std::size_t report = in.n >= (std::size_t{1} << 22) ? in.n / 10 : 0;
+    const std::size_t report = n_all >= (std::size_t{1} << 22) ? n_all / 10 : 0;
     std::atomic<std::size_t> done{0};
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
-    for (long long cl = 0; cl < static_cast<long long>(in.nlist); ++cl) {
+    for (long long cl = 0; cl < static_cast<long long>(f.nlist); ++cl) {
         const std::size_t c = static_cast<std::size_t>(cl);
         const std::size_t n = f.cluster_sizes[c];
-        const float *cent = in.rotated_centroids + c * P;
-        std::vector<uint8_t> bits(P), compact(32 * P / 8), code(P);
+        std::vector<uint8_t> compact(32 * P / 8), code(P);
         for (std::size_t i0 = 0; i0 < n; i0 += 32) {
             const std::size_t len = std::min<std::size_t>(32, n - i0);
-            uint8_t *blk = f.batch_data.data() + (block0[c] + i0 / 32) * block_bytes;
+            uint8_t *blk = f.batch_data.data() + (L.block0[c] + i0 / 32) * block_bytes;
             float *fl = reinterpret_cast<float *>(blk + P * 4);
             std::fill(compact.begin(), compact.end(), 0);
             for (std::size_t v = 0; v < len; ++v) {
-                const std::size_t gi = start[c] + i0 + v;
-                const float *x = in.rotated_data + static_cast<std::size_t>(f.ids[gi]) * P;
+                const std::size_t gi = L.start[c] + i0 + v;
                 float f1[3], f2[2];
-                quantize_one_bit(x, cent, P, bits.data(), f1, in.metric);
-                for (std::size_t d = 0; d < P; ++d)
-                    compact[v * (P / 8) + d / 8] |= static_cast<uint8_t>(bits[d] << (7 - d % 8));
+                quant(c, f.ids[gi], compact.data() + v * (P / 8), f1, code.data(), f2);
                 fl[v] = f1[0];
                 fl[32 + v] = f1[1];
                 fl[64 + v] = f1[2];
-                quantize_ex_bits(x, cent, P, in.ex_bits, code.data(), f2, in.metric);
                 uint8_t *rec = f.ex_data.data() + gi * stride;
                 pack_excode7(code.data(), P, rec);
                 std::memcpy(rec + lc, f2, sizeof(f2));
@@ -494,9 +506,57 @@ IvfFile build_ivf(const BuildInput &in, int threads) {
         if (report) {
             const std::size_t before = done.fetch_add(n, std::memory_order_relaxed);
             if (before / report != (before + n) / report)
-                std::fprintf(stderr, "[build_ivf] quantised %zu / %zu vectors\n", before + n, in.n);
+                std::fprintf(stderr, "[build_ivf] packed %zu / %zu vectors\n", before + n, n_all);
         }
     }
+}
+
+}  // namespace
+
+IvfFile build_ivf(const BuildInput &in, int threads) {
+    if (!in.rotated_data || !in.rotated_centroids || !in.assignments || !in.rotator || !in.n ||
+        !in.dim || in.padded_dim % 64 || in.padded_dim < in.dim || !in.nlist || in.ex_bits != 7)
+        throw std::invalid_argument("build_ivf: invalid input (ex_bits must be 7)");
+    const std::size_t P = in.padded_dim;
+    IvfFile f;
+    const ClusterLayout L = layout_index(f, in.rotated_centroids, in.rotator, in.assignments, in.n, in.dim, P,
+                                         in.nlist, in.ex_bits, in.metric);
+    fill_index(f, L, threads,
+               [&](std::size_t c, uint32_t id, uint8_t *compact, float *f1, uint8_t *code, float *f2) {
+                   thread_local std::vector<uint8_t> bits;
+                   bits.resize(P);
+                   const float *x = in.rotated_data + static_cast<std::size_t>(id) * P;
+                   const float *cent = in.rotated_centroids + c * P;
+                   quantize_one_bit(x, cent, P, bits.data(), f1, in.metric);
+                   for (std::size_t d = 0; d < P; ++d)
+                       compact[d / 8] |= static_cast<uint8_t>(bits[d] << (7 - d % 8));
+                   quantize_ex_bits(x, cent, P, in.ex_bits, code, f2, in.metric);
+               });
+    return f;
+}
+
+IvfFile build_ivf_gpu(const GpuBuildInput &in, int device, int threads) {
+    if (!in.data || !in.rotated_centroids || !in.assignments || !in.rotator || !in.n || !in.dim ||
+        in.padded_dim % 64 || in.padded_dim < in.dim || in.padded_dim > 1024 || !in.nlist || in.ex_bits != 7)
+        throw std::invalid_argument("build_ivf_gpu: invalid input (ex_bits must be 7, P <= 1024)");
+    const std::size_t P = in.padded_dim, n = in.n;
+    IvfFile f;
+    const ClusterLayout L = layout_index(f, in.rotated_centroids, in.rotator, in.assignments, n, in.dim, P,
+                                         in.nlist, in.ex_bits, in.metric);
+    std::vector<uint8_t> bits(n * (P / 8)), code(n * P);
+    std::vector<float> f1(n * 3), f2(n * 2);
+    if (int rc = cora_tool_quantize(in.data, n, in.dim, in.rotator, P, in.rotated_centroids, in.nlist,
+                                    in.assignments, in.metric, bits.data(), f1.data(), code.data(), f2.data(),
+                                    device))
+        throw std::runtime_error(std::string("build_ivf_gpu: ") + cora_tool_last_error() + " (status " +
+                                 std::to_string(rc) + ")");
+    fill_index(f, L, threads,
+               [&](std::size_t, uint32_t id, uint8_t *compact, float *g1, uint8_t *cd, float *g2) {
+                   std::memcpy(compact, bits.data() + static_cast<std::size_t>(id) * (P / 8), P / 8);
+                   std::memcpy(g1, f1.data() + static_cast<std::size_t>(id) * 3, 12);
+                   std::memcpy(cd, code.data() + static_cast<std::size_t>(id) * P, P);
+                   std::memcpy(g2, f2.data() + static_cast<std::size_t>(id) * 2, 8);
+               });
     return f;
 }
 

@@ -237,6 +237,16 @@ int cora_tool_assign(const float *x, uint64_t n, uint64_t dim, const float *cent
 /* exhaustive top-k ids by FP32 distance (metric 0: L2, 1: IP), ascending */
 int cora_tool_topk(const float *base, uint64_t nb, const float *queries, uint64_t nq, uint64_t dim,
                    uint64_t k, int metric, uint32_t *ids, int device);
+/* RaBitQ quantisation of index rows on the GPU (the index builder's per-row step,
+ * rabitq_impl.hpp:76-137 and 276-500 as restated by the host builder, bit-identical to it):
+ * rows x [n][dim] are rotated by R [dim][P] on the GPU and quantised against their cluster's
+ * rotated centroid (centroids [nlist][P], assign [n]) with 1 sign bit + 7 ex-bits.
+ * Outputs per row, in input order: bits [n][P/8] (dimension 8b + j at bit 7 - j of byte b),
+ * f1 [n][3] (f_add, f_rescale, f_error), code [n][P] (7-bit ex-code values, complemented
+ * for negative residuals), f2 [n][2] (f_add_ex, f_rescale_ex). P % 64 == 0, P <= 1024. */
+int cora_tool_quantize(const float *x, uint64_t n, uint64_t dim, const float *R, uint64_t P,
+                       const float *centroids, uint64_t nlist, const uint32_t *assign, int metric,
+                       uint8_t *bits, float *f1, uint8_t *code, float *f2, int device);
 
 #ifdef __cplusplus
 }

@@ -116,6 +116,12 @@ int cora_build_ivf(const float *rotated_data, const float *rotated_centroids,
                    const uint32_t *assignments, const float *rotator, uint64_t n, uint64_t dim,
                    uint64_t padded_dim, uint64_t nlist, uint64_t ex_bits, int metric, int threads,
                    const char *out_path);
+/* The same index from raw rows [n][dim]: rotation and RaBitQ quantisation on GPU `device`
+ * (cora_tool_quantize), code packing on the host; bit-identical to cora_build_ivf on the
+ * GPU-rotated rows (cora_tool_rotate). P <= 1024. */
+int cora_build_ivf_gpu(const float *data, const float *rotated_centroids, const uint32_t *assignments,
+                       const float *rotator, uint64_t n, uint64_t dim, uint64_t padded_dim, uint64_t nlist,
+                       uint64_t ex_bits, int metric, int device, int threads, const char *out_path);
 /* RaBitQ codes and factors of n rows against one centroid (for quantizer parity tests):
  * bits u8 [n][P], f1 f32 [n][3], excode u8 [n][P], f2 f32 [n][2]. */
 int cora_quantize_rows(const float *rows, const float *centroid, uint64_t n, uint64_t P,

@@ -24,6 +24,19 @@ struct BuildInput {
 
 IvfFile build_ivf(const BuildInput &in, int threads = 0);
 
+// The same index from raw rows, rotated and quantised on GPU `device` (cora_tool_quantize,
+// bit-identical to build_ivf on the GPU-rotated rows); the host packs the codes.
+struct GpuBuildInput {
+    const float *data = nullptr;               // [n][dim] raw rows
+    const float *rotated_centroids = nullptr;  // [nlist][padded_dim]
+    const uint32_t *assignments = nullptr;     // [n]
+    const float *rotator = nullptr;            // [dim][padded_dim]
+    std::size_t n = 0, dim = 0, padded_dim = 0, nlist = 0, ex_bits = 7;
+    int metric = 0;
+};
+
+IvfFile build_ivf_gpu(const GpuBuildInput &in, int device = 0, int threads = 0);
+
 // bits: u8 {0,1} [P]; factors: f_add, f_rescale, f_error.
 void quantize_one_bit(const float *x, const float *c, std::size_t P, uint8_t *bits,
                       float *factors, int metric);

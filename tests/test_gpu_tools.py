@@ -132,3 +132,33 @@ def test_kmeans_reseeds_empty_clusters():
     assert sizes.min() >= 1, np.sort(sizes)[:8]
     # a populated centroid is the mean of one true cluster's unit vectors (norm ~0.9)
     assert np.linalg.norm(c, axis=1).min() > 0.5
+
+
+@pytest.mark.parametrize("dim,P,metric", [(128, 128, 0), (128, 128, 1), (250, 256, 0), (768, 768, 1)])
+def test_gpu_builder_matches_host_builder(dim, P, metric, tmp_path):
+    """The GPU quantiser (cora_build_ivf_gpu) writes the same index file, byte for byte, as
+    the host builder (cora_build_ivf, itself pinned to the reference builder's codes) on the
+    GPU-rotated rows: sign codes, all factors, ex-codes, ids."""
+    rng = np.random.default_rng(dim + metric)
+    n, nl = 3000, 12
+    centers = rng.standard_normal((nl, dim)).astype(np.float32)
+    x = (centers[rng.integers(0, nl, n)] + 0.6 * rng.standard_normal((n, dim))).astype(np.float32)
+    if metric == 1:
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+    x[7] = centers[0]  # a row equal to its centre's neighbourhood, ties in |o|
+    R = np.linalg.qr(rng.standard_normal((P, P)))[0][:dim].astype(np.float32)
+    cent = ca.gpu_kmeans(x, nl, 5, seed=3)
+    assign = ca.gpu_assign(x, cent)
+    cr = (cent.astype(np.float64) @ R.astype(np.float64)).astype(np.float32)
+    say(f"[tools] GPU builder vs host builder, dim {dim} P {P} metric {metric}")
+    ca.build_ivf(tmp_path / "host.index", ca.gpu_rotate(x, R), cr, assign, R, metric=metric)
+    ca.build_ivf_gpu(tmp_path / "gpu.index", x, cr, assign, R, metric=metric)
+    a, b = (tmp_path / "host.index").read_bytes(), (tmp_path / "gpu.index").read_bytes()
+    assert len(a) == len(b)
+    if a != b:
+        ha, hb = ca.IvfIndex(tmp_path / "host.index"), ca.IvfIndex(tmp_path / "gpu.index")
+        for name in ("short_data", "short_factors", "long_codes", "ex_factors", "ids"):
+            u, v = getattr(ha, name), getattr(hb, name)
+            bad = np.nonzero((u != v).reshape(u.shape[0], -1).any(1))[0]
+            assert bad.size == 0, (name, bad[:8], bad.size)
+        assert a == b
