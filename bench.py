@@ -115,6 +115,7 @@ def main():
     ap.add_argument("--nprobe", type=int, default=0, help="0: smallest grid nprobe reaching the recall target")
     ap.add_argument("--recall-target", type=float, default=0.9)
     ap.add_argument("--batch-q", type=int, default=0)
+    ap.add_argument("--vanguard", type=int, default=-1, help="vanguard size (default: the configuration's)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-queries", type=int, default=0,
@@ -164,7 +165,8 @@ def main():
             np.save(gt_path, gt)
 
     ivf = ca.IvfIndex(index_path)
-    eng = ca.HybridIndex(0, vanguard_size=c.vanguard, cpu_secondary_filter=c.secondary_filter,
+    vanguard = c.vanguard if args.vanguard < 0 else args.vanguard
+    eng = ca.HybridIndex(0, vanguard_size=vanguard, cpu_secondary_filter=c.secondary_filter,
                          cross_query_reuse=True, gpu_filter_timing=True, metric=c.metric,
                          cpu_threads=threads, gpu_seed_refine=not args.no_gpu_seed,
                          gpu_refine_filter=not args.no_gpu_prefilter)
@@ -189,13 +191,15 @@ def main():
     for nprobe in ([] if args.nprobe else c.nprobes):  # --nprobe: measure that one only
         step(nprobe)
         dt, ids, st = step(nprobe)
-        r = recall_at_k(ids, gt, c.topk)
+        r = recall_at_k(ids, gt, 10)
         sweep.append({"nprobe": nprobe, "qps": round(queries.shape[0] / dt, 1), "recall": round(r, 4),
+                      f"recall_at_{c.topk}": round(recall_at_k(ids, gt, c.topk), 4),
                       "candidates_per_query": round(st["submitted"] / queries.shape[0], 1),
                       "seed_ms": round(st["seed_ms"], 3), "scan_ms": round(st["scan_ms"], 3),
                       "recovery_ms": round(st["recovery_ms"], 3), "filter_ms": round(st["gpu_filter_ms"], 3)})
         pp = st["pass_produced"]
-        log(f"[sweep] nprobe={nprobe} QPS={queries.shape[0] / dt:.1f} recall={r:.4f} "
+        log(f"[sweep] nprobe={nprobe} QPS={queries.shape[0] / dt:.1f} recall@10={r:.4f} "
+            f"recall@{c.topk}={recall_at_k(ids, gt, c.topk):.4f} "
             f"cand/q={st['submitted'] / queries.shape[0]:.1f} (seed {pp[0] / queries.shape[0]:.1f}, "
             f"far {(pp[1] - pp[0]) / queries.shape[0]:.1f}, recovery {(pp[2] - pp[1]) / queries.shape[0]:.1f}; "
             f"gpu-seeded queries {st['seeded_queries']}, pre-filter dropped "
@@ -209,6 +213,7 @@ def main():
     for _ in range(args.warmup):
         step(nprobe)
     times, times_up, scan_ms, scan_bytes, recalls, probe_ms, probe_flops = [], [], [], [], [], [], []
+    recalls_k = []
     van_ms, van_bytes = [], []
     for _ in range(args.steps):
         dt, ids, st = step(nprobe)
@@ -220,7 +225,8 @@ def main():
         scan_bytes.append(st["scan_bytes"])
         van_ms.append(st["vanguard_ms"])
         van_bytes.append(st["vanguard_bytes"])
-        recalls.append(recall_at_k(ids, gt, c.topk))
+        recalls.append(recall_at_k(ids, gt, 10))
+        recalls_k.append(recall_at_k(ids, gt, c.topk))
     total = sum(times)
     qps = queries.shape[0] * args.steps / total
     ms_step = 1000.0 * total / args.steps
@@ -281,8 +287,9 @@ def main():
         "dtype": "u32",
         "data": "synthetic",
         "config": {"workload": c.describe(), "nprobe": nprobe, "recall_at_10": round(float(np.mean(recalls)), 4),
+                   f"recall_at_{c.topk}": round(float(np.mean(recalls_k)), 4),
                    "qps_with_upload": round(queries.shape[0] * args.steps / sum(times_up), 1),
-                   "batch_q": batch_q, "vanguard": c.vanguard, "cpu_secondary_filter": c.secondary_filter,
+                   "batch_q": batch_q, "vanguard": vanguard, "cpu_secondary_filter": c.secondary_filter,
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
                    "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
                    "query_chunk": chunk, "sweep": sweep},

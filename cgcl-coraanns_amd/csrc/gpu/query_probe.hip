@@ -317,15 +317,19 @@ __global__ __launch_bounds__(64) void query_prep_kernel(const float *__restrict_
     }
 }
 
-__global__ __launch_bounds__(64) void row_norms_kernel(const float *__restrict__ x, uint32_t P,
-                                                       float *__restrict__ out) {
-    const float *row = x + (size_t)blockIdx.x * P;
-    float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < P; i += 64)
-        s = fmaf(row[i], row[i], s);
-    s = wave_sum(s);
-    if (threadIdx.x == 0)
-        out[blockIdx.x] = s;
+// one wave per row, grid-stride over rows: a dispatch counts its work-items in 32 bits, so
+// one workgroup per row would silently drop rows beyond 2^32 / 64 (67M rows)
+__global__ __launch_bounds__(64) void row_norms_kernel(const float *__restrict__ x, uint32_t rows,
+                                                       uint32_t P, float *__restrict__ out) {
+    for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float *row = x + (size_t)r * P;
+        float s = 0.0f;
+        for (uint32_t i = threadIdx.x; i < P; i += 64)
+            s = fmaf(row[i], row[i], s);
+        s = wave_sum(s);
+        if (threadIdx.x == 0)
+            out[r] = s;
+    }
 }
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -844,7 +848,7 @@ void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_b
 
 void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s) {
     if (rows)
-        row_norms_kernel<<<rows, 64, 0, s>>>(x, P, out);
+        row_norms_kernel<<<rows < (1u << 20) ? rows : (1u << 20), 64, 0, s>>>(x, rows, P, out);
 }
 
 void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,

@@ -46,17 +46,17 @@ __global__ __launch_bounds__(64) void row_argmin_kernel(const float *__restrict_
         out[blockIdx.x] = bi == 0xFFFFFFFFu ? 0u : bi;
 }
 
+// grid-stride over rows (a dispatch counts its work-items in 32 bits)
 __global__ void accumulate_kernel(const float *__restrict__ x, const uint32_t *__restrict__ assign,
                                   uint32_t rows, uint32_t dim, float *__restrict__ sums,
                                   uint32_t *__restrict__ counts) {
-    const uint32_t r = blockIdx.x;
-    if (r >= rows)
-        return;
-    const uint32_t c = assign[r];
-    for (uint32_t d = threadIdx.x; d < dim; d += blockDim.x)
-        atomicAdd(&sums[(size_t)c * dim + d], x[(size_t)r * dim + d]);
-    if (threadIdx.x == 0)
-        atomicAdd(&counts[c], 1u);
+    for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const uint32_t c = assign[r];
+        for (uint32_t d = threadIdx.x; d < dim; d += blockDim.x)
+            atomicAdd(&sums[(size_t)c * dim + d], x[(size_t)r * dim + d]);
+        if (threadIdx.x == 0)
+            atomicAdd(&counts[c], 1u);
+    }
 }
 
 __global__ void update_kernel(float *__restrict__ cent, const float *__restrict__ sums,
@@ -238,7 +238,7 @@ int cora_tool_kmeans(const float *h_x, uint64_t n, uint64_t dim, uint64_t k, uin
             return rc;
         TCHK(hipMemset(sums.p, 0, k * dim * 4));
         TCHK(hipMemset(cnt.p, 0, k * 4));
-        accumulate_kernel<<<(uint32_t)n, 64>>>((float *)x.p, (uint32_t *)asg.p, (uint32_t)n,
+        accumulate_kernel<<<(uint32_t)std::min<uint64_t>(n, 1u << 20), 64>>>((float *)x.p, (uint32_t *)asg.p, (uint32_t)n,
                                                 (uint32_t)dim, (float *)sums.p, (uint32_t *)cnt.p);
         update_kernel<<<(uint32_t)((k * dim + 255) / 256), 256>>>((float *)c.p, (float *)sums.p,
                                                                    (uint32_t *)cnt.p, (uint32_t)k,

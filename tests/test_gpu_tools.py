@@ -162,3 +162,24 @@ def test_gpu_builder_matches_host_builder(dim, P, metric, tmp_path):
             bad = np.nonzero((u != v).reshape(u.shape[0], -1).any(1))[0]
             assert bad.size == 0, (name, bad[:8], bad.size)
         assert a == b
+
+
+def test_topk_l2_beyond_2_32_work_items():
+    """More than 2^32 / 64 base rows (70M x 4, L2): every row's norm takes part (a launch of
+    one 64-lane workgroup per row would exceed the dispatch's 32-bit work-item count and
+    leave the last rows without norms, which then look nearest)."""
+    rng = np.random.default_rng(70)
+    nb, dim, nq, k = 70_000_000, 4, 4, 10
+    base = rng.standard_normal((nb, dim), dtype=np.float32)
+    q = rng.standard_normal((nq, dim), dtype=np.float32)
+    plant = [3, 20_000_001, 45_000_007, nb - 2]
+    for i, w in enumerate(plant):
+        base[w] = q[i]
+    say(f"[tools] topk L2 over {nb:,} rows")
+    ids = ca.gpu_topk(base, q, k, 0)
+    for i, w in enumerate(plant):
+        assert ids[i, 0] == w, (i, ids[i, :3])
+        d = ((base.astype(np.float64) - q[i]) ** 2).sum(1) if i == 0 else None
+        if d is not None:
+            want = np.argsort(d, kind="stable")[:k]
+            assert set(want.tolist()) == set(ids[i].tolist())
