@@ -240,7 +240,8 @@ __device__ void publish_held(VqShared &S, const QueueDev &q, uint32_t &dropped) 
 typedef __attribute__((address_space(4))) const uint32_t *ConstWords;
 
 // ip_int of one vector (words x) for W >= 16: the planes are read one 4-word group at a
-// time (8 x 4 scalar words), so they never occupy vector registers.
+// time (8 x 4 scalar words), so they never occupy vector registers; the opaque per-group
+// base also keeps the loads in the caller's loop instead of hoisted out of it.
 template <int W>
 __device__ __forceinline__ int popc_ip_scalar(const uint32_t (&x)[Words<W>::kMax], ConstWords planes) {
     int a[kBq];
@@ -249,13 +250,16 @@ __device__ __forceinline__ int popc_ip_scalar(const uint32_t (&x)[Words<W>::kMax
         a[j] = 0;
 #pragma unroll
     for (int g = 0; g < W / 4; ++g) {
+        // an opaque base per group: its 8 x 4 words load as their own scalar loads, not
+        // merged with the neighbouring groups' (which would hold ~80 scalar registers)
+        ConstWords pg = planes + 4 * g;
+        asm volatile("" : "+s"(pg));
 #pragma unroll
         for (int j = 0; j < kBq; ++j) {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                a[j] += __popc(x[4 * g + k] & planes[j * W + 4 * g + k]);
+                a[j] += __popc(x[4 * g + k] & pg[j * W + k]);
         }
-        __builtin_amdgcn_sched_barrier(0);  // one group's 32 plane words live at a time
     }
     int ip = -(a[kBq - 1] << (kBq - 1));
 #pragma unroll
@@ -709,11 +713,7 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
         if constexpr (W > 0 && W <= 4) {
             ip = popc_ip<W>(cur.x, preg, nw);
         } else if constexpr (W >= 16) {
-            // re-read per tile: an opaque copy of the pointer keeps the scalar loads in
-            // the loop instead of hoisting all 8 W words out of it
-            ConstWords pl = cplanes;
-            asm volatile("" : "+s"(pl));
-            ip = popc_ip_scalar<W>(cur.x, pl);
+            ip = popc_ip_scalar<W>(cur.x, cplanes);
         } else {
             ip = popc_ip<W>(cur.x, S.planes, nw);
         }
