@@ -706,22 +706,33 @@ __global__ __launch_bounds__(kSelWaveThreads) void select_wave_kernel(const floa
 // plus the lowest-index ties in index order, bitonic sort in LDS.
 constexpr int kSelBigThreads = 1024;
 
-template <int R>
-__global__ __launch_bounds__(kSelBigThreads) void select_regs_kernel(const float *__restrict__ dist,
-                                                                     uint32_t nl, uint32_t k,
-                                                                     uint32_t kpow2,
-                                                                     int32_t *__restrict__ out) {
+template <int R, int kThreads = kSelBigThreads>
+__global__ __launch_bounds__(kThreads) void select_regs_kernel(const float *__restrict__ dist,
+                                                               uint32_t nl, uint32_t k,
+                                                               uint32_t kpow2,
+                                                               int32_t *__restrict__ out) {
     __shared__ uint32_t hist[256];
-    __shared__ uint32_t s_red[2 * kSelBigThreads / 64], s_sc[2];
+    __shared__ uint32_t s_red[2 * kThreads / 64], s_sc[2];
     extern __shared__ unsigned long long sel[];  // [kpow2]
     const float *row = dist + (size_t)blockIdx.x * nl;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t begin = t * R;
     uint32_t key[R];
+    if (R % 4 == 0 && (nl & 3u) == 0 && begin + R <= nl) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-        key[r] = begin + r < nl ? order_key(row[begin + r]) : 0xFFFFFFFFu;
-    // inclusive block scan over 1,024 threads (s_red: one word per wave)
+        for (int r = 0; r < R; r += 4) {  // the thread's R keys as 16-byte loads
+            const float4 v = *reinterpret_cast<const float4 *>(row + begin + r);
+            key[r] = order_key(v.x);
+            key[r + 1] = order_key(v.y);
+            key[r + 2] = order_key(v.z);
+            key[r + 3] = order_key(v.w);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            key[r] = begin + r < nl ? order_key(row[begin + r]) : 0xFFFFFFFFu;
+    }
+    // inclusive block scan over the block (s_red: one word per wave)
     auto incl_scan = [&](uint32_t v) -> uint32_t {
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -739,7 +750,7 @@ __global__ __launch_bounds__(kSelBigThreads) void select_regs_kernel(const float
         return v + add;
     };
     uint32_t take_eq = 0;
-    const uint32_t kth = block_kth_key<kSelBigThreads>(
+    const uint32_t kth = block_kth_key<kThreads>(
         [&](auto f) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
@@ -773,12 +784,12 @@ __global__ __launch_bounds__(kSelBigThreads) void select_regs_kernel(const float
             }
         }
     }
-    for (uint32_t i = k + t; i < kpow2; i += kSelBigThreads)
+    for (uint32_t i = k + t; i < kpow2; i += kThreads)
         sel[i] = ~0ull;
     __syncthreads();
     for (uint32_t size = 2; size <= kpow2; size <<= 1) {
         for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t i = t; i < kpow2; i += kSelBigThreads) {
+            for (uint32_t i = t; i < kpow2; i += kThreads) {
                 const uint32_t j = i ^ stride;
                 if (j > i) {
                     const bool asc = (i & size) == 0;
@@ -792,7 +803,7 @@ __global__ __launch_bounds__(kSelBigThreads) void select_regs_kernel(const float
             __syncthreads();
         }
     }
-    for (uint32_t i = t; i < k; i += kSelBigThreads)
+    for (uint32_t i = t; i < k; i += kThreads)
         out[(size_t)blockIdx.x * k + i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
 }
 
@@ -871,7 +882,11 @@ void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
         kp <<= 1;
     const size_t sel_bytes = kp * sizeof(unsigned long long);
     const size_t lds = sel_bytes + (size_t)nl * 4;
-    if (kp <= kSelWaveMaxK) {
+    if (nl > 8192 && nl <= 32u * 512) {
+        // 8,192 < nlist <= 16,384: a 512-thread block per query holds the row in registers
+        // (read once; 0.41 ms against 0.67 ms for the wave kernel at 10,000 x 16,384)
+        select_regs_kernel<32, 512><<<nq, 512, sel_bytes, s>>>(dist, nl, nprobe, kp, idx);
+    } else if (kp <= kSelWaveMaxK) {
         const uint32_t per = kSelWaveThreads / 64;
         select_wave_kernel<<<(nq + per - 1) / per, kSelWaveThreads, per * sel_bytes, s>>>(dist, nq, nl, nprobe,
                                                                                         kp, idx);
