@@ -130,20 +130,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float *__restrict__ A,
 // Distance GEMM D[m][n] = an[m] + bn[n] - 2 <A[m], Bt[n]> for the coarse probe and the
 // k-means assignment, A [M][K] and Bt [N][K] row-major, K % 4 == 0, 16-byte aligned rows.
 // A workgroup of four waves owns a 128 x 128 output tile, each wave a 64 x 64 quarter as
-// 4 x 4 blocks of v_mfma_f32_16x16x4f32. K advances in slices of 16 staged in LDS as
+// 4 x 4 blocks of v_mfma_f32_16x16x4f32. K advances in slices of kDK (32) staged in LDS as
 // [row][k] (double buffered; the next slice is loaded into registers while the current
-// one is multiplied, one barrier per slice). Within a slice, MFMA j takes from lane l
+// one is multiplied, one barrier per slice). Within each 16-wide part, MFMA j takes from lane l
 // k = 4 (l / 16) + j for both operands, so each lane reads its four k values of a row
 // with one 16-byte LDS read; every k meets its own partner, so the sum is the same.
-constexpr int kDT = 128;         // output tile edge
-constexpr int kDK = 16;          // K slice
-constexpr int kDRow = kDK + 4;   // LDS row stride in floats (staggers banks)
+constexpr int kDT = 128;  // output tile edge
 
+template <int kDK>
 __global__ __launch_bounds__(256) void dist_gemm_kernel(const float *__restrict__ A,
                                                         const float *__restrict__ Bt,
                                                         float *__restrict__ C, uint32_t M, uint32_t N,
                                                         uint32_t K, const float *__restrict__ an,
                                                         const float *__restrict__ bn) {
+    constexpr int kDRow = kDK + 4;
     __shared__ __align__(16) float As[2][kDT * kDRow];
     __shared__ __align__(16) float Bs[2][kDT * kDRow];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -157,11 +157,12 @@ __global__ __launch_bounds__(256) void dist_gemm_kernel(const float *__restrict_
             acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     // staging: thread t loads rows (t >> 2) and 64 + (t >> 2) of each operand, k 4 (t & 3)
     const int srow = tid >> 2, sk = (tid & 3) * 4;
-    float4 ra[2], rb[2];
+    constexpr int H = 2 * (kDK / 16);
+    float4 ra[H], rb[H];
     auto load = [&](uint32_t k0) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t gm = m0 + srow + 64 * h, gn = n0 + srow + 64 * h, gk = k0 + sk;
+        for (int h = 0; h < H; ++h) {
+            const uint32_t gm = m0 + srow + 64 * (h & 1), gn = n0 + srow + 64 * (h & 1), gk = k0 + sk + 16 * (h >> 1);
             ra[h] = gm < M && gk < K ? *reinterpret_cast<const float4 *>(A + (size_t)gm * K + gk)
                                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             rb[h] = gn < N && gk < K ? *reinterpret_cast<const float4 *>(Bt + (size_t)gn * K + gk)
@@ -170,9 +171,9 @@ __global__ __launch_bounds__(256) void dist_gemm_kernel(const float *__restrict_
     };
     auto stage = [&](int buf) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            *reinterpret_cast<float4 *>(&As[buf][(srow + 64 * h) * kDRow + sk]) = ra[h];
-            *reinterpret_cast<float4 *>(&Bs[buf][(srow + 64 * h) * kDRow + sk]) = rb[h];
+        for (int h = 0; h < H; ++h) {
+            *reinterpret_cast<float4 *>(&As[buf][(srow + 64 * (h & 1)) * kDRow + sk + 16 * (h >> 1)]) = ra[h];
+            *reinterpret_cast<float4 *>(&Bs[buf][(srow + 64 * (h & 1)) * kDRow + sk + 16 * (h >> 1)]) = rb[h];
         }
     };
     load(0);
@@ -184,11 +185,13 @@ __global__ __launch_bounds__(256) void dist_gemm_kernel(const float *__restrict_
         const bool more = k0 + kDK < K;
         if (more)
             load(k0 + kDK);
+#pragma unroll
+        for (int ss = 0; ss < kDK / 16; ++ss) {
         float4 a[4], b[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            a[t] = *reinterpret_cast<const float4 *>(&As[buf][(wm + 16 * t + i16) * kDRow + kg]);
-            b[t] = *reinterpret_cast<const float4 *>(&Bs[buf][(wn + 16 * t + i16) * kDRow + kg]);
+            a[t] = *reinterpret_cast<const float4 *>(&As[buf][(wm + 16 * t + i16) * kDRow + kg + 16 * ss]);
+            b[t] = *reinterpret_cast<const float4 *>(&Bs[buf][(wn + 16 * t + i16) * kDRow + kg + 16 * ss]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -201,6 +204,7 @@ __global__ __launch_bounds__(256) void dist_gemm_kernel(const float *__restrict_
                     acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[ti][tj], 0, 0, 0);
                 }
             }
+        }
         }
         if (more) {
             stage(buf ^ 1);
@@ -868,9 +872,9 @@ void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const 
     const bool vec = P % 4 == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
                      (reinterpret_cast<uintptr_t>(c) & 15) == 0;
     if (vec) {
-        // a slice reads k0 .. k0 + 15 with bounds per 4-float group, so any K % 4 == 0 works
+        // a slice reads k0 .. k0 + 31 with bounds per 4-float group, so any K % 4 == 0 works
         dim3 g2((nl + kDT - 1) / kDT, (nq + kDT - 1) / kDT);
-        dist_gemm_kernel<<<g2, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
+        dist_gemm_kernel<32><<<g2, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
     } else
         gemm_kernel<true, false><<<grid, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
 }
