@@ -169,6 +169,7 @@ struct VqShared {
     uint32_t l_pos[kVqList];
     float thr;
     uint32_t nheld, kc, tb, nlist;
+    uint32_t ndropped, nrefined;  // statistics of the query
     unsigned long long base, limit;
 };
 
@@ -189,22 +190,26 @@ __device__ __forceinline__ void append_window(VqShared &S, uint32_t i, bool take
 }
 
 // Publish the held refined vectors whose distance is within their rounding bound of the
-// current threshold (one ring reservation per round of 256), count the others as dropped.
-__device__ void publish_held(VqShared &S, const QueueDev &q, uint32_t &dropped) {
+// current threshold (one ring reservation per round of 256), count the others as dropped
+// (S.ndropped).
+__device__ void publish_held(VqShared &S, const QueueDev &q) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float thr = S.thr;
     const uint32_t nheld = S.nheld;
     for (uint32_t r0 = 0; r0 < nheld; r0 += kVqThreads) {
         const uint32_t i = r0 + tid;
-        bool pub = false;
+        bool pub = false, drop = false;
         if (i < nheld) {
             const float rd = S.h_rd[i];
             pub = rd <= thr + S.h_err[i];
-            dropped += (!pub && !isnan(rd)) ? 1u : 0u;
+            drop = !pub && !isnan(rd);
         }
-        const unsigned long long m = __ballot(pub);
-        if (lane == 0)
+        const unsigned long long m = __ballot(pub), dm = __ballot(drop);
+        if (lane == 0) {
             S.red[wave] = (uint32_t)__popcll(m);
+            if (dm)
+                atomicAdd(&S.ndropped, (uint32_t)__popcll(dm));
+        }
         __syncthreads();
         uint32_t before = 0, total = 0;
 #pragma unroll
@@ -314,6 +319,8 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
         S.kc = 0;
         S.tb = 0;
         S.nlist = 0;
+        S.ndropped = 0;
+        S.nrefined = 0;
         S.limit = __hip_atomic_load(q.cached_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
@@ -352,7 +359,6 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
     uint32_t preg[W > 0 && W <= 4 ? kBq * W : 1];
     const ConstWords cplanes = (ConstWords)(p.qplanes + (size_t)qi * 2 * kBq * nw);
     const size_t lc = (size_t)P * 7 / 8;
-    uint32_t dropped = 0, refined = 0;
     auto process_list = [&]() {
         const uint32_t nl = S.nlist;
         for (;;) {
@@ -389,7 +395,7 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
             for (uint32_t c0 = 0; c0 < nwin; c0 += kVqChunk) {
                 const float thr = S.thr;
                 if (S.nheld + kVqChunk > kVqHeld)
-                    publish_held(S, q, dropped);
+                    publish_held(S, q);
                 const uint32_t cn = min(kVqChunk, nwin - c0);
                 const uint32_t held0 = S.nheld;
                 // the refined distance of chunk vector e (lane sub == 0 of its group) into the
@@ -585,7 +591,8 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
                     enter += S.cnt[w][1];
                     before += w < wave ? S.cnt[w][1] : 0u;
                 }
-                refined += valid;
+                if (tid == 0)
+                    S.nrefined += valid;
                 if (enter) {
                     if (wave < kVqChunk / 64 && ((em >> lane) & 1ull)) {
                         const uint32_t o = before + lane_rank(em);
@@ -760,17 +767,37 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
             if (tid == 0)
                 S.nlist = 0;
             __syncthreads();
+            if constexpr (W >= 16) {
+                // P >= 512: the tiles prefetched before the refinement are fetched again
+                // after it (the cursor restarts at the first pair), so they hold no
+                // registers across it; 2 tiles per wave and refinement, ~6% of the
+                // query's tile bytes
+                jf = 0;
+                f_toff = 0;
+                f_next = uniform(S.toff[1]);
+                f_tbase = uniform(S.tbase[0]);
+                f_n = uniform(S.n[0]);
+                f_off = 0;
+                f_gadd = uniformf(S.gadd[0]);
+                f_gerr = uniformf(S.gerr[0]);
+#pragma unroll
+                for (int b = 0; b < kBufs; ++b) {
+                    if (t + b * kVqWaves < T)
+                        fetch(t + b * kVqWaves, bufs[b]);
+                    else
+                        bufs[b] = TileRegs{};
+                }
+            }
         }
     }
 
     // ---- 3. publication and the query's threshold ----
-    publish_held(S, q, dropped);
-    dropped = block_sum(dropped, S.red);
+    publish_held(S, q);
     if (tid == 0) {
-        if (dropped)
-            atomicAdd(p.dropped, (unsigned long long)dropped);
-        if (refined)
-            atomicAdd(va.refined, (unsigned long long)refined);
+        if (S.ndropped)
+            atomicAdd(p.dropped, (unsigned long long)S.ndropped);
+        if (S.nrefined)
+            atomicAdd(va.refined, (unsigned long long)S.nrefined);
         const float thr = S.thr;
         if (S.kc == topk && thr < thr_in) {
             uint32_t *slot = reinterpret_cast<uint32_t *>(va.thr_out) + qi;
