@@ -37,10 +37,11 @@ FLAG_CROSS_QUERY_REUSE = 4
 
 DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range(5)
 DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
-DBG_SEED_DIST, DBG_THRESHOLDS = 10, 11
+DBG_SEED_DIST, DBG_THRESHOLDS, DBG_PROBE_DIST = 10, 11, 12
 FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
 FLAG_PAIR_SEEDS = 1 << 6
 FLAG_NO_MFMA_SCAN = 1 << 7
+FLAG_FP32_PROBE = 1 << 8
 
 
 class EngineUnavailable(RuntimeError):

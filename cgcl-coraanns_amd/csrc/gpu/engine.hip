@@ -50,6 +50,8 @@ struct cora_gpu_engine {
     int metric = 0;
     uint32_t W = 0, tile_bytes = 0;
     float *d_cent = nullptr, *d_cnorm = nullptr, *d_rot = nullptr;
+    uint16_t *d_cent_hl = nullptr;  // split-FP16 centroids [2][nl][P] (coarse-probe GEMM)
+    float *d_cscale = nullptr;      // their row scales [nl]
     uint8_t *d_tiles = nullptr;
     ClusterMeta *d_meta = nullptr;
     uint8_t *d_excodes = nullptr;  // optional HBM copy of the 7-bit ex-codes
@@ -65,6 +67,8 @@ struct cora_gpu_engine {
     uint32_t *d_planes = nullptr, *d_bcount = nullptr, *d_bcursor = nullptr, *d_boff = nullptr,
              *d_uoff = nullptr, *d_nunits = nullptr, *d_cursor = nullptr, *d_seed = nullptr;
     int32_t *d_pidx = nullptr;
+    uint16_t *d_q_hl = nullptr;  // split-FP16 rotated queries [2][max_q][P]
+    float *d_qscale = nullptr;
     uint32_t *d_qorder = nullptr;  // queries by nearest cluster (fused vanguard pass)
     int8_t *d_qbytes = nullptr;    // [max_q][2][P] qint, qres (MFMA far scan operands)
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
@@ -183,8 +187,9 @@ void release_workspace(cora_gpu_engine *E) {
     E->launched = false;
     E->ws_q = E->ws_k = E->ws_np = E->ws_van = E->seed_words = 0;
     for (float **p : {&E->d_raw, &E->d_qrot, &E->d_k1, &E->d_kb, &E->d_qnorm, &E->d_qwidth, &E->d_qwidth2,
-                      &E->d_dist, &E->d_gadd, &E->d_gerr, &E->d_thr_snap})
+                      &E->d_dist, &E->d_gadd, &E->d_gerr, &E->d_thr_snap, &E->d_qscale})
         dfree(*p);
+    dfree(E->d_q_hl);
     for (uint32_t **p : {&E->d_planes, &E->d_bcount, &E->d_bcursor, &E->d_boff, &E->d_uoff,
                          &E->d_nunits, &E->d_cursor, &E->d_seed})
         dfree(*p);
@@ -301,6 +306,8 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
     release_workspace(E);
     dfree(E->d_cent);
     dfree(E->d_cnorm);
+    dfree(E->d_cent_hl);
+    dfree(E->d_cscale);
     dfree(E->d_rot);
     dfree(E->d_tiles);
     dfree(E->d_meta);
@@ -375,6 +382,8 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
             (rc = dalloc(E, E->d_tiles, std::max<uint64_t>(1, tiles) * tile_bytes)) ||
             (rc = dalloc(E, E->d_cent, n_centroids * padded_dim)) ||
             (rc = dalloc(E, E->d_cnorm, n_centroids)) ||
+            (rc = dalloc(E, E->d_cent_hl, 2 * n_centroids * padded_dim)) ||
+            (rc = dalloc(E, E->d_cscale, n_centroids)) ||
             (rc = dalloc(E, E->d_rot, dim * padded_dim)) ||
             (rc = dalloc(E, d_ref, num_vecs * W)) || (rc = dalloc(E, d_reff, num_vecs * 3)))
             break;
@@ -400,6 +409,8 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
                           E->stream);
             launch_row_norms(E->d_cent, (uint32_t)n_centroids, (uint32_t)padded_dim, E->d_cnorm,
                              E->stream);
+            launch_split_f16(E->d_cent, (uint32_t)n_centroids, (uint32_t)padded_dim, E->d_cent_hl,
+                             E->d_cscale, E->stream);
             chk(hipGetLastError(), "repack launch");
             chk(hipStreamSynchronize(E->stream), "index upload");
         }
@@ -412,6 +423,8 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
         dfree(E->d_tiles);
         dfree(E->d_cent);
         dfree(E->d_cnorm);
+        dfree(E->d_cent_hl);
+        dfree(E->d_cscale);
         dfree(E->d_rot);
         return rc;
     }
@@ -497,6 +510,8 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_qwidth2, max_q));
         TRY(dalloc(E, E->d_planes, max_q * 2 * kBq * E->W));
         TRY(dalloc(E, E->d_dist, max_q * E->nl));
+        TRY(dalloc(E, E->d_q_hl, 2 * max_q * E->P));
+        TRY(dalloc(E, E->d_qscale, max_q));
         TRY(dalloc(E, E->d_pidx, np));
         TRY(dalloc(E, E->d_qorder, max_q));
         TRY(dalloc(E, E->d_qbytes, max_q * 2 * E->P));
@@ -661,8 +676,13 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // coarse probing (hybrid.cu:465-498)
     if (timing)
         HIPCHK(hipEventRecord(E->ev_p0, s));
-    launch_dist_gemm(E->d_qrot, E->d_qnorm, E->d_cent, E->d_cnorm, nq, (uint32_t)E->nl, P,
-                     E->d_dist, s);
+    if (!(a->flags & CORA_FLAG_FP32_PROBE) && dist_gemm_f16x3_supported(P)) {
+        launch_split_f16(E->d_qrot, nq, P, E->d_q_hl, E->d_qscale, s);
+        launch_dist_gemm_f16x3(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
+                               nq, (uint32_t)E->nl, P, E->d_dist, s);
+    } else
+        launch_dist_gemm(E->d_qrot, E->d_qnorm, E->d_cent, E->d_cnorm, nq, (uint32_t)E->nl, P,
+                         E->d_dist, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_p1, s));
     launch_select(E->d_dist, nq, (uint32_t)E->nl, np, E->d_pidx, s);
@@ -925,6 +945,7 @@ int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes
     case CORA_DBG_PROBE_IDX: src = E->d_pidx; size = nq * np * 4; break;
     case CORA_DBG_PROBE_GADD: src = E->d_gadd; size = nq * np * 4; break;
     case CORA_DBG_PROBE_GERR: src = E->d_gerr; size = nq * np * 4; break;
+    case CORA_DBG_PROBE_DIST: src = E->d_dist; size = nq * E->nl * 4; break;
     case CORA_DBG_PAIRS: {
         if (bytes != nq * np * 12)
             return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_read: size mismatch");

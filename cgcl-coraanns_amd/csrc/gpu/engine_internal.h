@@ -169,6 +169,13 @@ void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_b
                        float *kb, float *qnorm, float *qwidth, float *qwidth2, uint32_t *qplanes,
                        int8_t *qbytes, hipStream_t s);
 void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s);
+// split-FP16 operand rows: hl = [2][rows][P] (hi rows, then lo rows), scale [rows]
+void launch_split_f16(const float *x, uint32_t rows, uint32_t P, uint16_t *hl, float *scale,
+                      hipStream_t s);
+bool dist_gemm_f16x3_supported(uint32_t P);
+void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const float *qnorm,
+                            const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t nq,
+                            uint32_t nl, uint32_t P, float *dist, hipStream_t s);
 void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,
                       uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s);
 void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,

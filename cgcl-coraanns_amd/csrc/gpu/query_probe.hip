@@ -2,7 +2,8 @@
 //
 //   rotate        Q' = Q . R on MFMA                    (reference hybrid.cu:436-440)
 //   query_prep    k1/kb sums, ||q'||^2, Bq=8 planes     (query_kernels.cuh:73-103,117-197)
-//   dist_gemm     ||q'||^2 + ||c'||^2 - 2 q'.c' on MFMA  (hybrid.cu:465-477, query_kernels.cuh:10-64)
+//   dist_gemm     ||q'||^2 + ||c'||^2 - 2 q'.c' on MFMA  (hybrid.cu:465-477, query_kernels.cuh:10-64):
+//                 split-FP16 operands (three FP16 products per term), or FP32
 //   select        per-query nprobe smallest, ascending, ties by cluster id (hybrid.cu:485-493)
 //   probe_refine  exact ||q'-c'||^2 and <q',c'> of the selected probes -> g_add, g_error
 //                 (query.hpp:537-545: L2 g_add = ||q'-c'||^2, IP g_add = -<q',c'>)
@@ -241,6 +242,155 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1)
         v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
+}
+
+// ---- split-FP16 coarse-probe GEMM ----
+//
+// Each operand row x_r [P] is scaled by 2^e_r, e_r = 14 - floor(log2 max_i |x_ri|) (the
+// largest magnitude lands in [2^14, 2^15), inside FP16's range), and written as two FP16
+// rows hi = fp16(x 2^e), lo = fp16(x 2^e - hi) (the difference is exact in FP32), so
+// x 2^e = hi + lo + d with |d| <= 2^-22 |x 2^e| (2^-25 absolute below FP16's normal range).
+// The inner product is hi.hi' + hi.lo' + lo.hi' on the FP16 matrix cores with FP32
+// accumulation, scaled back by 2^-(e_r + e_r'): per term a relative error of at most
+// 3 * 2^-22 (the omitted lo.lo' and the two d terms), below FP32's own 24-bit rounding of
+// a 768-term sum.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+__global__ __launch_bounds__(64) void split_f16_kernel(const float *__restrict__ x, uint32_t rows,
+                                                       uint32_t P, _Float16 *__restrict__ hi,
+                                                       _Float16 *__restrict__ lo,
+                                                       float *__restrict__ scale) {
+    const int lane = threadIdx.x;
+    for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float *row = x + (size_t)r * P;
+        float amax = 0.0f;
+        for (uint32_t i = lane; i < P; i += 64)
+            amax = fmaxf(amax, fabsf(row[i]));
+        amax = wave_max(amax);
+        // zero rows keep e = 0; the clamp keeps 2^-e a normal float
+        const int e = amax > 0.0f && amax <= FLT_MAX ? min(max(14 - ilogbf(amax), -100), 100) : 0;
+        for (uint32_t i = lane; i < P; i += 64) {
+            const float v = ldexpf(row[i], e);
+            const _Float16 h = (_Float16)v;
+            hi[(size_t)r * P + i] = h;
+            lo[(size_t)r * P + i] = (_Float16)(v - (float)h);
+        }
+        if (lane == 0)
+            scale[r] = ldexpf(1.0f, -e);
+    }
+}
+
+constexpr int kHT = 128;  // output tile edge
+constexpr int kHK = 32;   // K per LDS stage: one v_mfma_f32_16x16x32_f16 step
+
+// LDS slot of the 8-half group g (0..3) of tile row r: the XOR spreads the 16 rows x 4
+// groups of one MFMA operand read over distinct banks
+__device__ __forceinline__ int hslot(int r, int g) { return r * 4 + (g ^ ((r >> 1) & 3)); }
+
+// dist[m][n] = an[m] + bn[n] - 2 <a_m, b_n> for A [M][K] and B [N][K] given as split-FP16
+// rows (Ah/Al, scale as; Bh/Bl, scale bs); K % 32 == 0, rows 16-byte aligned. 128 x 128
+// output tile per workgroup of four waves (64 x 64 each, 4 x 4 MFMA blocks of 16 x 16),
+// K staged in LDS 32 at a time, double buffered. MFMA 16x16x32 operand layout: lane l
+// supplies A[l % 16][8 (l / 16) .. + 7] and B[8 (l / 16) .. + 7][l % 16], and holds
+// D[4 (l / 16) + r][l % 16]. Tile order: XCD x (blockIdx.x % 8) owns column tiles
+// [x ncx, (x + 1) ncx), swept by groups of four row tiles, so the workgroups resident on
+// an XCD share their operand tiles in its L2.
+__global__ __launch_bounds__(256, 2) void dist_gemm_f16x3_kernel(
+    const _Float16 *__restrict__ Ah, const _Float16 *__restrict__ Al, const float *__restrict__ as,
+    const _Float16 *__restrict__ Bh, const _Float16 *__restrict__ Bl, const float *__restrict__ bs,
+    float *__restrict__ C, uint32_t M, uint32_t N, uint32_t K, const float *__restrict__ an,
+    const float *__restrict__ bn, uint32_t ncx) {
+    __shared__ half8_t S[2][4][kHT * 4];  // [buffer][Ah, Al, Bh, Bl][row x group]
+    const uint32_t xcd = blockIdx.x % kNumXcd, bi = blockIdx.x / kNumXcd;
+    const uint32_t grp = bi / (4 * ncx), within = bi % (4 * ncx);
+    const uint32_t m0 = (grp * 4 + within % 4) * kHT, n0 = (xcd * ncx + within / 4) * kHT;
+    if (m0 >= M || n0 >= N)
+        return;  // the whole workgroup: padding of the tile grid
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // staging: thread t moves group t & 3 of rows t >> 2 and 64 + (t >> 2) of each array
+    const int srow = tid >> 2, sg = tid & 3;
+    half8_t st[4][2];
+    auto load = [&](uint32_t k0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t gm = m0 + srow + 64 * h, gn = n0 + srow + 64 * h;
+            const size_t ka = (size_t)gm * K + k0 + 8 * sg, kb = (size_t)gn * K + k0 + 8 * sg;
+            const half8_t z = {};
+            st[0][h] = gm < M ? *reinterpret_cast<const half8_t *>(Ah + ka) : z;
+            st[1][h] = gm < M ? *reinterpret_cast<const half8_t *>(Al + ka) : z;
+            st[2][h] = gn < N ? *reinterpret_cast<const half8_t *>(Bh + kb) : z;
+            st[3][h] = gn < N ? *reinterpret_cast<const half8_t *>(Bl + kb) : z;
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                S[buf][a][hslot(srow + 64 * h, sg)] = st[a][h];
+    };
+    load(0);
+    stage(0);
+    __syncthreads();
+    const int i16 = lane & 15, g = lane >> 4;
+    int buf = 0;
+    for (uint32_t k0 = 0; k0 < K; k0 += kHK) {
+        const bool more = k0 + kHK < K;
+        if (more)
+            load(k0 + kHK);
+        half8_t ah[4], al[4], bh[4], bl[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            ah[t] = S[buf][0][hslot(wm + 16 * t + i16, g)];
+            al[t] = S[buf][1][hslot(wm + 16 * t + i16, g)];
+            bh[t] = S[buf][2][hslot(wn + 16 * t + i16, g)];
+            bl[t] = S[buf][3][hslot(wn + 16 * t + i16, g)];
+        }
+        // the three products in turn over all 16 blocks: an accumulator's dependent MFMAs
+        // are 16 instructions apart
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+            for (int tj = 0; tj < 4; ++tj)
+                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ti], bh[tj], acc[ti][tj], 0, 0, 0);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+            for (int tj = 0; tj < 4; ++tj)
+                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ti], bl[tj], acc[ti][tj], 0, 0, 0);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+            for (int tj = 0; tj < 4; ++tj)
+                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ti], bh[tj], acc[ti][tj], 0, 0, 0);
+        if (more) {
+            stage(buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+        }
+    }
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t gm = m0 + wm + 16 * ti + 4 * g + r;
+            if (gm >= M)
+                continue;
+            const float am = an[gm], sa = as[gm];
+#pragma unroll
+            for (int tj = 0; tj < 4; ++tj) {
+                const uint32_t gn = n0 + wn + 16 * tj + i16;
+                if (gn < N)
+                    C[(size_t)gm * N + gn] = am + bn[gn] - 2.0f * (acc[ti][tj][r] * (sa * bs[gn]));
+            }
+        }
 }
 
 // One wave per query. Each lane owns dimensions lane + 64*i.
@@ -877,6 +1027,30 @@ void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const 
         dist_gemm_kernel<32><<<g2, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
     } else
         gemm_kernel<true, false><<<grid, 256, 0, s>>>(q, c, dist, nq, nl, P, qnorm, cnorm);
+}
+
+void launch_split_f16(const float *x, uint32_t rows, uint32_t P, uint16_t *hl, float *scale,
+                      hipStream_t s) {
+    if (!rows)
+        return;
+    _Float16 *hi = reinterpret_cast<_Float16 *>(hl);
+    split_f16_kernel<<<rows < (1u << 20) ? rows : (1u << 20), 64, 0, s>>>(x, rows, P, hi,
+                                                                          hi + (size_t)rows * P, scale);
+}
+
+bool dist_gemm_f16x3_supported(uint32_t P) { return P % kHK == 0; }
+
+void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const float *qnorm,
+                            const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t nq,
+                            uint32_t nl, uint32_t P, float *dist, hipStream_t s) {
+    if (!nq || !nl)
+        return;
+    const uint32_t nrt = (nq + kHT - 1) / kHT, nct = (nl + kHT - 1) / kHT;
+    const uint32_t ncx = (nct + kNumXcd - 1) / kNumXcd, groups = (nrt + 3) / 4;
+    const _Float16 *qh = reinterpret_cast<const _Float16 *>(qhl);
+    const _Float16 *ch = reinterpret_cast<const _Float16 *>(chl);
+    dist_gemm_f16x3_kernel<<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
+        qh, qh + (size_t)nq * P, qscale, ch, ch + (size_t)nl * P, cscale, dist, nq, nl, P, qnorm, cnorm, ncx);
 }
 
 void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,

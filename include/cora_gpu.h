@@ -68,8 +68,13 @@ enum cora_search_flags {
      * used when the ex-codes are resident in HBM (vanguard depth <= 64, topk <= 128). */
     CORA_FLAG_PAIR_SEEDS = 1u << 6,
     /* Scan the far pairs with the popcount kernel even where the matrix-core kernel
-     * applies (cross-query reuse with padded dimension 64..256). */
-    CORA_FLAG_NO_MFMA_SCAN = 1u << 7
+     * applies (cross-query reuse with padded dimension 64..256, 512, 768 or 1024). */
+    CORA_FLAG_NO_MFMA_SCAN = 1u << 7,
+    /* Coarse-probe distances from the FP32 matrix-core GEMM instead of the split-FP16 one
+     * (each operand row scaled by a power of two and split into two FP16 rows, three FP16
+     * products per term: at most 3 * 2^-22 relative error per term). Either way the
+     * selected probes' g_add / g_error are recomputed in FP32 (hybrid.cu:465-498). */
+    CORA_FLAG_FP32_PROBE = 1u << 8
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -207,8 +212,10 @@ enum cora_debug_array {
     CORA_DBG_Q_WIDTH2 = 9,        /* f32 [nq] residual quantisation step (width / 254) */
     CORA_DBG_SEED_DIST = 10,      /* f32 [nq][vanguard depth][keep] GPU-refined seed distances
                                      (+inf: unused slot); keep = max(topk, 20) */
-    CORA_DBG_THRESHOLDS = 11      /* f32 [nq] thresholds the GPU filter read last (the
+    CORA_DBG_THRESHOLDS = 11,     /* f32 [nq] thresholds the GPU filter read last (the
                                      snapshot in frozen mode, else the live array) */
+    CORA_DBG_PROBE_DIST = 12      /* f32 [nq][nlist] coarse-probe distance matrix
+                                     ||q'||^2 + ||c'||^2 - 2 <q',c'> */
 };
 int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t bytes);
 

@@ -164,11 +164,13 @@ def test_query_preparation(case_name, request):
 
 
 @pytest.mark.parametrize("case_name", CASES)
-def test_coarse_probe(case_name, request):
+@pytest.mark.parametrize("fp32", [False, True])
+def test_coarse_probe(case_name, fp32, request):
+    """Probe selection from the split-FP16 distance GEMM (default) and the FP32 one."""
     case = request.getfixturevalue(case_name)
     nprobe = min(6, case.file.nlist)
-    say(f"[gpu] coarse probe parity on {case_name} nprobe={nprobe}")
-    eng, _, _ = run_frozen(case, nprobe, 10)
+    say(f"[gpu] coarse probe parity on {case_name} nprobe={nprobe} fp32={fp32}")
+    eng, _, _ = run_frozen(case, nprobe, 10, extra_flags=ca.FLAG_FP32_PROBE if fp32 else 0)
     g = gpu_intermediates(eng, case, nprobe)
     idx, gadd, gerr, l2 = orc.coarse_probe(g["qr"], case.sd.centroids, case.file.nlist, case.file.metric)
     for q in range(idx.shape[0]):
@@ -190,6 +192,29 @@ def test_coarse_probe(case_name, request):
         sc = (qq ** 2).sum() + (c ** 2).sum(1)
         assert np.all(np.abs(g["gadd"][q] - want) <= 1e-5 * sc)
         assert np.all(np.abs(g["gerr"][q] - np.sqrt(l2x)) <= 1e-5 * np.sqrt(sc))
+
+
+@pytest.mark.parametrize("case_name", CASES)
+def test_probe_distance_matrix(case_name, request):
+    """The whole coarse-probe distance matrix ||q'||^2 + ||c'||^2 - 2 <q',c'> of the
+    split-FP16 GEMM (default) and of the FP32 one against FP64 from the same rotated
+    queries, relative to ||q'||^2 + ||c'||^2: within 1e-6 (FP32 rounding of the three terms
+    and of the sum, plus at most 3 * 2^-22 per product term for the split operands). A GEMM
+    on plain FP16 operands (the lo halves dropped) errs by ~2^-11 per term, 1e-5 and more
+    here, and fails."""
+    case = request.getfixturevalue(case_name)
+    nprobe = min(4, case.file.nlist)
+    nq, P, nl = case.queries.shape[0], case.file.padded_dim, case.file.nlist
+    c = case.sd.centroids.astype(np.float64)
+    for name, flags in (("split-fp16", 0), ("fp32", ca.FLAG_FP32_PROBE)):
+        say(f"[gpu] probe distance matrix on {case_name}, {name} GEMM")
+        eng, _, _ = run_frozen(case, nprobe, 10, extra_flags=flags)
+        q = eng.debug_read(ca.DBG_ROTATED_QUERIES, (nq, P), np.float32).astype(np.float64)
+        d = eng.debug_read(ca.DBG_PROBE_DIST, (nq, nl), np.float32)
+        qn, cn = (q ** 2).sum(1)[:, None], (c ** 2).sum(1)[None]
+        want = qn + cn - 2 * q @ c.T
+        err = np.abs(d - want) / (qn + cn)
+        assert err.max() <= 1e-6, (name, float(err.max()))
 
 
 @pytest.mark.parametrize("nlist", [9000, 20000, 40000])
