@@ -126,8 +126,8 @@ def main():
     ap.add_argument("--no-gpu-seed", action="store_true",
                     help="CPU-only thresholds (the reference's behaviour), no GPU seed thresholds")
     ap.add_argument("--no-gpu-prefilter", action="store_true", help="no GPU refined pre-filter")
-    ap.add_argument("--fp32-probe", action="store_true",
-                    help="coarse-probe distances from the FP32 matrix-core GEMM instead of the split-FP16 one")
+    ap.add_argument("--fp32-gemm", action="store_true",
+                    help="query rotation and coarse-probe distances from the FP32 matrix-core GEMMs instead of the split-FP16 ones")
     ap.add_argument("--workdir", default="",
                     help="keep the built index and ground truth in this directory and reuse them")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -173,7 +173,7 @@ def main():
                          cross_query_reuse=True, gpu_filter_timing=True, metric=c.metric,
                          cpu_threads=threads, gpu_seed_refine=not args.no_gpu_seed,
                          gpu_refine_filter=not args.no_gpu_prefilter,
-                         extra_flags=ca.FLAG_FP32_PROBE if args.fp32_probe else 0)
+                         extra_flags=ca.FLAG_FP32_GEMM if args.fp32_gemm else 0)
     eng.load_ivf(ivf)
     chunk = min(queries.shape[0], 65535)
     eng.prepare_workspace(chunk, c.topk, max(c.nprobes))
@@ -242,7 +242,7 @@ def main():
     van_achieved = van_bpl / (avg_van_ms * 1e-3) / 1e9 if avg_van_ms > 0 else 0.0
     avg_probe_ms = float(np.mean(probe_ms))
     probe_tflops = float(np.mean(probe_flops)) / (avg_probe_ms * 1e-3) / 1e12 if avg_probe_ms > 0 else 0.0
-    if args.fp32_probe:
+    if args.fp32_gemm:
         probe_line = {"kernel": "dist_gemm_kernel (coarse-probe L2 distances, 128x128 tiles, v_mfma_f32_16x16x4f32)",
                       "flops_per_launch": int(np.mean(probe_flops)), "avg_launch_ms": round(avg_probe_ms, 4),
                       "achieved": round(probe_tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -41,7 +41,7 @@ DBG_SEED_DIST, DBG_THRESHOLDS, DBG_PROBE_DIST = 10, 11, 12
 FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
 FLAG_PAIR_SEEDS = 1 << 6
 FLAG_NO_MFMA_SCAN = 1 << 7
-FLAG_FP32_PROBE = 1 << 8
+FLAG_FP32_GEMM = 1 << 8
 
 
 class EngineUnavailable(RuntimeError):

@@ -52,6 +52,8 @@ struct cora_gpu_engine {
     float *d_cent = nullptr, *d_cnorm = nullptr, *d_rot = nullptr;
     uint16_t *d_cent_hl = nullptr;  // split-FP16 centroids [2][nl][P] (coarse-probe GEMM)
     float *d_cscale = nullptr;      // their row scales [nl]
+    uint16_t *d_rot_hl = nullptr;   // split-FP16 R^T [2][P][dim] (query rotation GEMM)
+    float *d_rtscale = nullptr;     // its row scales [P]
     uint8_t *d_tiles = nullptr;
     ClusterMeta *d_meta = nullptr;
     uint8_t *d_excodes = nullptr;  // optional HBM copy of the 7-bit ex-codes
@@ -69,6 +71,8 @@ struct cora_gpu_engine {
     int32_t *d_pidx = nullptr;
     uint16_t *d_q_hl = nullptr;  // split-FP16 rotated queries [2][max_q][P]
     float *d_qscale = nullptr;
+    uint16_t *d_raw_hl = nullptr;  // split-FP16 raw queries [2][max_q][dim]
+    float *d_rawscale = nullptr;
     uint32_t *d_qorder = nullptr;  // queries by nearest cluster (fused vanguard pass)
     int8_t *d_qbytes = nullptr;    // [max_q][2][P] qint, qres (MFMA far scan operands)
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
@@ -187,9 +191,10 @@ void release_workspace(cora_gpu_engine *E) {
     E->launched = false;
     E->ws_q = E->ws_k = E->ws_np = E->ws_van = E->seed_words = 0;
     for (float **p : {&E->d_raw, &E->d_qrot, &E->d_k1, &E->d_kb, &E->d_qnorm, &E->d_qwidth, &E->d_qwidth2,
-                      &E->d_dist, &E->d_gadd, &E->d_gerr, &E->d_thr_snap, &E->d_qscale})
+                      &E->d_dist, &E->d_gadd, &E->d_gerr, &E->d_thr_snap, &E->d_qscale, &E->d_rawscale})
         dfree(*p);
     dfree(E->d_q_hl);
+    dfree(E->d_raw_hl);
     for (uint32_t **p : {&E->d_planes, &E->d_bcount, &E->d_bcursor, &E->d_boff, &E->d_uoff,
                          &E->d_nunits, &E->d_cursor, &E->d_seed})
         dfree(*p);
@@ -308,6 +313,8 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
     dfree(E->d_cnorm);
     dfree(E->d_cent_hl);
     dfree(E->d_cscale);
+    dfree(E->d_rot_hl);
+    dfree(E->d_rtscale);
     dfree(E->d_rot);
     dfree(E->d_tiles);
     dfree(E->d_meta);
@@ -372,9 +379,11 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
     const uint32_t tile_bytes = 256u * W + 768u;
     uint32_t *d_ref = nullptr;
     float *d_reff = nullptr;
+    float *d_rt = nullptr;  // R^T, FP32, until split
     auto cleanup = [&]() {
         dfree(d_ref);
         dfree(d_reff);
+        dfree(d_rt);
     };
     int rc = CORA_OK;
     do {
@@ -385,6 +394,8 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
             (rc = dalloc(E, E->d_cent_hl, 2 * n_centroids * padded_dim)) ||
             (rc = dalloc(E, E->d_cscale, n_centroids)) ||
             (rc = dalloc(E, E->d_rot, dim * padded_dim)) ||
+            (rc = dalloc(E, E->d_rot_hl, 2 * dim * padded_dim)) ||
+            (rc = dalloc(E, E->d_rtscale, padded_dim)) || (rc = dalloc(E, d_rt, dim * padded_dim)) ||
             (rc = dalloc(E, d_ref, num_vecs * W)) || (rc = dalloc(E, d_reff, num_vecs * 3)))
             break;
         hipError_t r = hipSuccess;
@@ -400,6 +411,12 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
                            hipMemcpyHostToDevice, E->stream), "centroid upload");
         chk(hipMemcpyAsync(E->d_rot, h_rotator, dim * padded_dim * 4, hipMemcpyHostToDevice,
                            E->stream), "rotator upload");
+        std::vector<float> rt(dim * padded_dim);  // R^T [P][dim]: the rotation GEMM's B rows
+        for (uint64_t d = 0; d < dim; ++d)
+            for (uint64_t c = 0; c < padded_dim; ++c)
+                rt[c * dim + d] = h_rotator[d * padded_dim + c];
+        chk(hipMemcpyAsync(d_rt, rt.data(), dim * padded_dim * 4, hipMemcpyHostToDevice, E->stream),
+            "rotator upload");
         chk(hipMemcpyAsync(d_ref, h_short_data, num_vecs * W * 4, hipMemcpyHostToDevice, E->stream),
             "code upload");
         chk(hipMemcpyAsync(d_reff, h_short_factors, num_vecs * 12, hipMemcpyHostToDevice, E->stream),
@@ -411,6 +428,7 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
                              E->stream);
             launch_split_f16(E->d_cent, (uint32_t)n_centroids, (uint32_t)padded_dim, E->d_cent_hl,
                              E->d_cscale, E->stream);
+            launch_split_f16(d_rt, (uint32_t)padded_dim, (uint32_t)dim, E->d_rot_hl, E->d_rtscale, E->stream);
             chk(hipGetLastError(), "repack launch");
             chk(hipStreamSynchronize(E->stream), "index upload");
         }
@@ -425,6 +443,8 @@ int cora_gpu_load_index(cora_gpu_engine *E, uint64_t num_vecs, uint64_t dim, uin
         dfree(E->d_cnorm);
         dfree(E->d_cent_hl);
         dfree(E->d_cscale);
+        dfree(E->d_rot_hl);
+        dfree(E->d_rtscale);
         dfree(E->d_rot);
         return rc;
     }
@@ -511,6 +531,8 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_planes, max_q * 2 * kBq * E->W));
         TRY(dalloc(E, E->d_dist, max_q * E->nl));
         TRY(dalloc(E, E->d_q_hl, 2 * max_q * E->P));
+        TRY(dalloc(E, E->d_raw_hl, 2 * max_q * E->dim));
+        TRY(dalloc(E, E->d_rawscale, max_q));
         TRY(dalloc(E, E->d_qscale, max_q));
         TRY(dalloc(E, E->d_pidx, np));
         TRY(dalloc(E, E->d_qorder, max_q));
@@ -665,7 +687,13 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const uint32_t P = (uint32_t)E->P;
 
     // query preparation (hybrid.cu:436-463)
-    launch_rotate(E->d_raw, E->d_rot, E->d_qrot, nq, (uint32_t)E->dim, P, s);
+    const bool split_gemm = !(a->flags & CORA_FLAG_FP32_GEMM);
+    if (split_gemm && dist_gemm_f16x3_supported((uint32_t)E->dim) && E->dim % 8 == 0) {
+        launch_split_f16(E->d_raw, nq, (uint32_t)E->dim, E->d_raw_hl, E->d_rawscale, s);
+        launch_rotate_f16x3(E->d_raw_hl, E->d_rawscale, E->d_rot_hl, E->d_rtscale, nq, (uint32_t)E->dim,
+                            P, E->d_qrot, s);
+    } else
+        launch_rotate(E->d_raw, E->d_rot, E->d_qrot, nq, (uint32_t)E->dim, P, s);
     launch_query_prep(E->d_qrot, nq, P, (uint32_t)E->ex_bits, E->d_k1, E->d_kb, E->d_qnorm,
                       E->d_qwidth, E->d_qwidth2, E->d_planes, E->d_qbytes, s);
     HIPCHK(hipEventRecord(E->ev_prep, s));
@@ -676,7 +704,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // coarse probing (hybrid.cu:465-498)
     if (timing)
         HIPCHK(hipEventRecord(E->ev_p0, s));
-    if (!(a->flags & CORA_FLAG_FP32_PROBE) && dist_gemm_f16x3_supported(P)) {
+    if (split_gemm && dist_gemm_f16x3_supported(P)) {
         launch_split_f16(E->d_qrot, nq, P, E->d_q_hl, E->d_qscale, s);
         launch_dist_gemm_f16x3(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
                                nq, (uint32_t)E->nl, P, E->d_dist, s);

@@ -1,6 +1,7 @@
 // Query preparation and coarse probing kernels (gfx950, wave64).
 //
-//   rotate        Q' = Q . R on MFMA                    (reference hybrid.cu:436-440)
+//   rotate        Q' = Q . R on MFMA                    (reference hybrid.cu:436-440):
+//                 split-FP16 operands as dist_gemm's, or FP32
 //   query_prep    k1/kb sums, ||q'||^2, Bq=8 planes     (query_kernels.cuh:73-103,117-197)
 //   dist_gemm     ||q'||^2 + ||c'||^2 - 2 q'.c' on MFMA  (hybrid.cu:465-477, query_kernels.cuh:10-64):
 //                 split-FP16 operands (three FP16 products per term), or FP32
@@ -287,14 +288,17 @@ constexpr int kHK = 32;   // K per LDS stage: one v_mfma_f32_16x16x32_f16 step
 // groups of one MFMA operand read over distinct banks
 __device__ __forceinline__ int hslot(int r, int g) { return r * 4 + (g ^ ((r >> 1) & 3)); }
 
-// dist[m][n] = an[m] + bn[n] - 2 <a_m, b_n> for A [M][K] and B [N][K] given as split-FP16
-// rows (Ah/Al, scale as; Bh/Bl, scale bs); K % 32 == 0, rows 16-byte aligned. 128 x 128
+// C[m][n] = <a_m, b_n> for A [M][K] and B [N][K] given as split-FP16 rows (Ah/Al, scale
+// as; Bh/Bl, scale bs), with kDist the L2 distance an[m] + bn[n] - 2 <a_m, b_n> (coarse
+// probe; without it the query rotation Q . R with B = R^T); K % 32 == 0, rows 16-byte
+// aligned. 128 x 128
 // output tile per workgroup of four waves (64 x 64 each, 4 x 4 MFMA blocks of 16 x 16),
 // K staged in LDS 32 at a time, double buffered. MFMA 16x16x32 operand layout: lane l
 // supplies A[l % 16][8 (l / 16) .. + 7] and B[8 (l / 16) .. + 7][l % 16], and holds
 // D[4 (l / 16) + r][l % 16]. Tile order: XCD x (blockIdx.x % 8) owns column tiles
 // [x ncx, (x + 1) ncx), swept by groups of four row tiles, so the workgroups resident on
 // an XCD share their operand tiles in its L2.
+template <bool kDist>
 __global__ __launch_bounds__(256, 2) void dist_gemm_f16x3_kernel(
     const _Float16 *__restrict__ Ah, const _Float16 *__restrict__ Al, const float *__restrict__ as,
     const _Float16 *__restrict__ Bh, const _Float16 *__restrict__ Bl, const float *__restrict__ bs,
@@ -383,12 +387,14 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_f16x3_kernel(
             const uint32_t gm = m0 + wm + 16 * ti + 4 * g + r;
             if (gm >= M)
                 continue;
-            const float am = an[gm], sa = as[gm];
+            const float am = kDist ? an[gm] : 0.0f, sa = as[gm];
 #pragma unroll
             for (int tj = 0; tj < 4; ++tj) {
                 const uint32_t gn = n0 + wn + 16 * tj + i16;
-                if (gn < N)
-                    C[(size_t)gm * N + gn] = am + bn[gn] - 2.0f * (acc[ti][tj][r] * (sa * bs[gn]));
+                if (gn < N) {
+                    const float v = acc[ti][tj][r] * (sa * bs[gn]);
+                    C[(size_t)gm * N + gn] = kDist ? am + bn[gn] - 2.0f * v : v;
+                }
             }
         }
 }
@@ -903,12 +909,28 @@ __global__ __launch_bounds__(kThreads) void select_regs_kernel(const float *__re
         __syncthreads();
         return v + add;
     };
-    uint32_t take_eq = 0;
+    // a bound on the k-th smallest key: the k-th smallest of the threads' minima (k threads
+    // hold a key at or below it, so the k smallest keys all lie at or below it); only the
+    // keys up to the bound enter the radix selection, a few times k instead of nl
+    uint32_t take_eq = 0, bound = 0xFFFFFFFFu;
+    if (k <= (nl + R - 1) / R) {
+        uint32_t tmin = 0xFFFFFFFFu;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (begin + r < nl)
+                tmin = min(tmin, key[r]);
+        bound = block_kth_key<kThreads>(
+            [&](auto f) {
+                if (begin < nl)
+                    f(tmin);
+            },
+            k, hist, s_red, s_sc, take_eq);
+    }
     const uint32_t kth = block_kth_key<kThreads>(
         [&](auto f) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (begin + r < nl)
+                if (begin + r < nl && key[r] <= bound)
                     f(key[r]);
         },
         k, hist, s_red, s_sc, take_eq);
@@ -1038,7 +1060,7 @@ void launch_split_f16(const float *x, uint32_t rows, uint32_t P, uint16_t *hl, f
                                                                           hi + (size_t)rows * P, scale);
 }
 
-bool dist_gemm_f16x3_supported(uint32_t P) { return P % kHK == 0; }
+bool dist_gemm_f16x3_supported(uint32_t K) { return K % kHK == 0; }
 
 void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const float *qnorm,
                             const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t nq,
@@ -1049,8 +1071,22 @@ void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const floa
     const uint32_t ncx = (nct + kNumXcd - 1) / kNumXcd, groups = (nrt + 3) / 4;
     const _Float16 *qh = reinterpret_cast<const _Float16 *>(qhl);
     const _Float16 *ch = reinterpret_cast<const _Float16 *>(chl);
-    dist_gemm_f16x3_kernel<<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
+    dist_gemm_f16x3_kernel<true><<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
         qh, qh + (size_t)nq * P, qscale, ch, ch + (size_t)nl * P, cscale, dist, nq, nl, P, qnorm, cnorm, ncx);
+}
+
+void launch_rotate_f16x3(const uint16_t *xhl, const float *xscale, const uint16_t *rthl,
+                         const float *rtscale, uint32_t nq, uint32_t dim, uint32_t P, float *out,
+                         hipStream_t s) {
+    if (!nq)
+        return;
+    const uint32_t nrt = (nq + kHT - 1) / kHT, nct = (P + kHT - 1) / kHT;
+    const uint32_t ncx = (nct + kNumXcd - 1) / kNumXcd, groups = (nrt + 3) / 4;
+    const _Float16 *xh = reinterpret_cast<const _Float16 *>(xhl);
+    const _Float16 *rh = reinterpret_cast<const _Float16 *>(rthl);
+    dist_gemm_f16x3_kernel<false><<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
+        xh, xh + (size_t)nq * dim, xscale, rh, rh + (size_t)P * dim, rtscale, out, nq, P, dim, nullptr,
+        nullptr, ncx);
 }
 
 void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,

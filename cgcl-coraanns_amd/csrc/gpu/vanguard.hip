@@ -75,22 +75,6 @@ __device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t *s_red)
     return v + add;
 }
 
-__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t *s_red) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-        v += __shfl_xor(v, o);
-    if (lane == 0)
-        s_red[wave] = v;
-    __syncthreads();
-    uint32_t s = 0;
-#pragma unroll
-    for (int w = 0; w < kVqWaves; ++w)
-        s += s_red[w];
-    __syncthreads();
-    return s;
-}
-
 __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t *s_red) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll

@@ -70,11 +70,12 @@ enum cora_search_flags {
     /* Scan the far pairs with the popcount kernel even where the matrix-core kernel
      * applies (cross-query reuse with padded dimension 64..256, 512, 768 or 1024). */
     CORA_FLAG_NO_MFMA_SCAN = 1u << 7,
-    /* Coarse-probe distances from the FP32 matrix-core GEMM instead of the split-FP16 one
-     * (each operand row scaled by a power of two and split into two FP16 rows, three FP16
-     * products per term: at most 3 * 2^-22 relative error per term). Either way the
-     * selected probes' g_add / g_error are recomputed in FP32 (hybrid.cu:465-498). */
-    CORA_FLAG_FP32_PROBE = 1u << 8
+    /* Query rotation and coarse-probe distances from the FP32 matrix-core GEMMs instead of
+     * the split-FP16 ones (each operand row scaled by a power of two and split into two
+     * FP16 rows, three FP16 products per term: at most 3 * 2^-22 relative error per term).
+     * Either way the selected probes' g_add / g_error are recomputed in FP32
+     * (hybrid.cu:436-440, 465-498). */
+    CORA_FLAG_FP32_GEMM = 1u << 8
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
