@@ -492,6 +492,11 @@ __global__ __launch_bounds__(64) void row_norms_kernel(const float *__restrict__
     }
 }
 
+// set bits of mask below this lane
+__device__ __forceinline__ uint32_t lanes_below(unsigned long long mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 __device__ __forceinline__ uint32_t order_key(float f) {
     const uint32_t u = __float_as_uint(f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -866,13 +871,18 @@ __global__ __launch_bounds__(kSelWaveThreads) void select_wave_kernel(const floa
 // plus the lowest-index ties in index order, bitonic sort in LDS.
 constexpr int kSelBigThreads = 1024;
 
+constexpr uint32_t kSelCand = 256;  // per-wave candidates of the fast path
+
 template <int R, int kThreads = kSelBigThreads>
 __global__ __launch_bounds__(kThreads) void select_regs_kernel(const float *__restrict__ dist,
                                                                uint32_t nl, uint32_t k,
                                                                uint32_t kpow2,
                                                                int32_t *__restrict__ out) {
+    constexpr uint32_t kWaves = kThreads / 64;
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_red[2 * kThreads / 64], s_sc[2];
+    __shared__ unsigned long long s_cand[kWaves][kSelCand], s_best[kWaves][64];
+    __shared__ uint32_t s_over;
     extern __shared__ unsigned long long sel[];  // [kpow2]
     const float *row = dist + (size_t)blockIdx.x * nl;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -909,28 +919,84 @@ __global__ __launch_bounds__(kThreads) void select_regs_kernel(const float *__re
         __syncthreads();
         return v + add;
     };
-    // a bound on the k-th smallest key: the k-th smallest of the threads' minima (k threads
-    // hold a key at or below it, so the k smallest keys all lie at or below it); only the
-    // keys up to the bound enter the radix selection, a few times k instead of nl
-    uint32_t take_eq = 0, bound = 0xFFFFFFFFu;
-    if (k <= (nl + R - 1) / R) {
-        uint32_t tmin = 0xFFFFFFFFu;
+    // k <= 64: each wave keeps the keys of its segment up to the k-th smallest of its 64
+    // lane minima (k lanes hold a key at or below it, so the wave's k smallest keys are all
+    // kept; a few times k keys for untied data), ranks them by (key, index) within the wave,
+    // and the block ranks the waves' sorted k best against each other by binary search (two
+    // barriers in all). A wave keeping more than kSelCand keys (heavy ties) sends the block
+    // to the radix selection below.
+    if (k <= 64) {
+        uint32_t m = 0xFFFFFFFFu;
 #pragma unroll
         for (int r = 0; r < R; ++r)
             if (begin + r < nl)
-                tmin = min(tmin, key[r]);
-        bound = block_kth_key<kThreads>(
-            [&](auto f) {
-                if (begin < nl)
-                    f(tmin);
-            },
-            k, hist, s_red, s_sc, take_eq);
+                m = min(m, key[r]);
+        uint32_t mrank = 0;  // rank of this lane's minimum among the wave's (ties by lane)
+        for (int j = 0; j < 64; ++j) {
+            const uint32_t o = (uint32_t)__shfl((int)m, j);
+            mrank += (o < m || (o == m && (uint32_t)j < lane)) ? 1u : 0u;
+        }
+        const unsigned long long bm = __ballot(mrank == k - 1);
+        const uint32_t bound = (uint32_t)__shfl((int)m, __ffsll((long long)bm) - 1);
+        if (t == 0)
+            s_over = 0;
+        uint32_t c = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool take = begin + r < nl && key[r] <= bound;
+            const unsigned long long tm = __ballot(take);
+            const uint32_t pos = c + lanes_below(tm);
+            if (take && pos < kSelCand)
+                s_cand[wave][pos] = ((unsigned long long)key[r] << 32) | (begin + r);
+            c += (uint32_t)__popcll(tm);
+        }
+        __syncthreads();  // s_over cleared before any wave sets it
+        if (c > kSelCand && lane == 0)
+            s_over = 1;
+        __syncthreads();
+        if (!s_over) {
+            for (uint32_t e = lane; e < c; e += 64) {
+                const unsigned long long v = s_cand[wave][e];
+                uint32_t rk = 0;
+                for (uint32_t f = 0; f < c; ++f)
+                    rk += s_cand[wave][f] < v ? 1u : 0u;
+                if (rk < k)
+                    s_best[wave][rk] = v;
+            }
+            for (uint32_t r = c + lane; r < k; r += 64)
+                s_best[wave][r] = ~0ull;  // a segment with fewer than k keys
+            __syncthreads();
+            for (uint32_t i = t; i < kWaves * k; i += kThreads) {
+                const uint32_t w = i / k;
+                const unsigned long long v = s_best[w][i % k];
+                if (v == ~0ull)
+                    continue;
+                uint32_t rk = i % k;
+                for (uint32_t w2 = 0; w2 < kWaves; ++w2) {
+                    if (w2 == w)
+                        continue;
+                    uint32_t lo = 0, hi = k;  // entries of the sorted list w2 below v
+                    while (lo < hi) {
+                        const uint32_t mid = (lo + hi) >> 1;
+                        if (s_best[w2][mid] < v)
+                            lo = mid + 1;
+                        else
+                            hi = mid;
+                    }
+                    rk += lo;
+                }
+                if (rk < k)
+                    out[(size_t)blockIdx.x * k + rk] = (int32_t)(uint32_t)(v & 0xFFFFFFFFull);
+            }
+            return;
+        }
     }
+    uint32_t take_eq = 0;
     const uint32_t kth = block_kth_key<kThreads>(
         [&](auto f) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (begin + r < nl && key[r] <= bound)
+                if (begin + r < nl)
                     f(key[r]);
         },
         k, hist, s_red, s_sc, take_eq);

@@ -217,6 +217,45 @@ def test_probe_distance_matrix(case_name, request):
         assert err.max() <= 1e-6, (name, float(err.max()))
 
 
+def order_keys(d):
+    """The select's total order on FP32 distances: IEEE bits made monotone as unsigned."""
+    u = np.ascontiguousarray(d, dtype=np.float32).view(np.uint32)
+    return np.where(u & 0x80000000, ~u, u | 0x80000000).astype(np.uint32)
+
+
+@pytest.mark.parametrize("nlist,distinct,nprobe", [(12000, 0, 16), (16384, 0, 32), (16384, 0, 64),
+                                                   (16384, 40, 32), (12000, 7, 64)])
+def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
+    """The probe select (8,192 < nlist <= 16,384: per-wave candidates below the k-th lane
+    minimum, ranked by (distance, cluster id); heavy ties fall back to the radix select)
+    against an exact sort of the GPU's own distance matrix by (distance key, cluster id).
+    distinct > 0 repeats that many centroids over the whole list, so every distance is tied
+    nlist / distinct times."""
+    rng = np.random.default_rng(nlist + distinct)
+    dim, nq = 64, 40
+    n = 2 * nlist
+    cent = rng.normal(0, 1, (nlist, dim)).astype(np.float32)
+    if distinct:
+        cent = cent[np.arange(nlist) % distinct]
+    assign = rng.integers(0, nlist, n).astype(np.uint32)
+    x = (cent[assign] + rng.normal(0, 0.1, (n, dim))).astype(np.float32)
+    q = (cent[rng.integers(0, nlist, nq)] + rng.normal(0, 0.1, (nq, dim))).astype(np.float32)
+    R = np.linalg.qr(rng.normal(size=(dim, dim)))[0].T.astype(np.float32)
+    path = tmp_path / "sel.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32), (cent.astype(np.float64) @ R).astype(np.float32),
+                 assign, R, metric=0)
+    case = Case(path, q)
+    say(f"[gpu] select on GPU distances, nlist={nlist} distinct={distinct} nprobe={nprobe}")
+    eng, _, _ = run_frozen(case, nprobe, 10)
+    d = eng.debug_read(ca.DBG_PROBE_DIST, (nq, nlist), np.float32)
+    pidx = eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32)
+    keys = order_keys(d)
+    ids = np.arange(nlist)
+    for qi in range(nq):
+        want = np.lexsort((ids, keys[qi]))[:nprobe]
+        assert np.array_equal(pidx[qi], want), qi
+
+
 @pytest.mark.parametrize("nlist", [9000, 20000, 40000])
 def test_coarse_probe_large_nlist(nlist, tmp_path):
     """Top-nprobe selection over nlist above the LDS-staged select (register-staged select,
