@@ -650,6 +650,9 @@ int cora_gpu_reset(cora_gpu_engine *E, const float *h_queries, uint64_t nq) {
         E->h_thr[i] = FLT_MAX;
     *E->h_abort = 0;
     E->launched = false;
+    // the queries are resident in HBM when reset returns (a pageable upload may still be in
+    // flight after hipMemcpyAsync returns)
+    HIPCHK(hipStreamSynchronize(E->stream));
     return CORA_OK;
 }
 
@@ -688,7 +691,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
 
     // query preparation (hybrid.cu:436-463)
     const bool split_gemm = !(a->flags & CORA_FLAG_FP32_GEMM);
-    if (split_gemm && dist_gemm_f16x3_supported((uint32_t)E->dim) && E->dim % 8 == 0) {
+    if (split_gemm && dist_gemm_f16x3_supported((uint32_t)E->dim, nq, P)) {
         launch_split_f16(E->d_raw, nq, (uint32_t)E->dim, E->d_raw_hl, E->d_rawscale, s);
         launch_rotate_f16x3(E->d_raw_hl, E->d_rawscale, E->d_rot_hl, E->d_rtscale, nq, (uint32_t)E->dim,
                             P, E->d_qrot, s);
@@ -704,7 +707,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // coarse probing (hybrid.cu:465-498)
     if (timing)
         HIPCHK(hipEventRecord(E->ev_p0, s));
-    if (split_gemm && dist_gemm_f16x3_supported(P)) {
+    if (split_gemm && dist_gemm_f16x3_supported(P, nq, E->nl)) {
         launch_split_f16(E->d_qrot, nq, P, E->d_q_hl, E->d_qscale, s);
         launch_dist_gemm_f16x3(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
                                nq, (uint32_t)E->nl, P, E->d_dist, s);

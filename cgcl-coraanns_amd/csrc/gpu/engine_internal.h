@@ -172,7 +172,8 @@ void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hip
 // split-FP16 operand rows: hl = [2][rows][P] (hi rows, then lo rows), scale [rows]
 void launch_split_f16(const float *x, uint32_t rows, uint32_t P, uint16_t *hl, float *scale,
                       hipStream_t s);
-bool dist_gemm_f16x3_supported(uint32_t K);  // inner dimension K % 32 == 0
+// inner dimension K % 32 == 0 and rows * K < 2^31 for both operands
+bool dist_gemm_f16x3_supported(uint32_t K, uint64_t rows_a, uint64_t rows_b);
 // Q' [nq][P] = X [nq][dim] . R from split-FP16 X and R^T [P][dim]
 void launch_rotate_f16x3(const uint16_t *xhl, const float *xscale, const uint16_t *rthl,
                          const float *rtscale, uint32_t nq, uint32_t dim, uint32_t P, float *out,

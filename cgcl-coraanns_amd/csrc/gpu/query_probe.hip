@@ -293,18 +293,20 @@ __device__ __forceinline__ int hslot(int r, int g) { return r * 4 + (g ^ ((r >> 
 // probe; without it the query rotation Q . R with B = R^T); K % 32 == 0, rows 16-byte
 // aligned. 128 x 128
 // output tile per workgroup of four waves (64 x 64 each, 4 x 4 MFMA blocks of 16 x 16),
-// K staged in LDS 32 at a time, double buffered. MFMA 16x16x32 operand layout: lane l
+// K staged in LDS 32 at a time in one buffer (the next stage's loads in registers during
+// the MFMAs; 32 KB of LDS and 158 VGPRs let three workgroups share a CU, which hides the
+// load latency better than two double-buffered ones). MFMA 16x16x32 operand layout: lane l
 // supplies A[l % 16][8 (l / 16) .. + 7] and B[8 (l / 16) .. + 7][l % 16], and holds
 // D[4 (l / 16) + r][l % 16]. Tile order: XCD x (blockIdx.x % 8) owns column tiles
 // [x ncx, (x + 1) ncx), swept by groups of four row tiles, so the workgroups resident on
 // an XCD share their operand tiles in its L2.
 template <bool kDist>
-__global__ __launch_bounds__(256, 2) void dist_gemm_f16x3_kernel(
+__global__ __launch_bounds__(256, 3) void dist_gemm_f16x3_kernel(
     const _Float16 *__restrict__ Ah, const _Float16 *__restrict__ Al, const float *__restrict__ as,
     const _Float16 *__restrict__ Bh, const _Float16 *__restrict__ Bl, const float *__restrict__ bs,
     float *__restrict__ C, uint32_t M, uint32_t N, uint32_t K, const float *__restrict__ an,
     const float *__restrict__ bn, uint32_t ncx) {
-    __shared__ half8_t S[2][4][kHT * 4];  // [buffer][Ah, Al, Bh, Bl][row x group]
+    __shared__ half8_t S[4][kHT * 4];  // [Ah, Al, Bh, Bl][row x group]
     const uint32_t xcd = blockIdx.x % kNumXcd, bi = blockIdx.x / kNumXcd;
     const uint32_t grp = bi / (4 * ncx), within = bi % (4 * ncx);
     const uint32_t m0 = (grp * 4 + within % 4) * kHT, n0 = (xcd * ncx + within / 4) * kHT;
@@ -324,27 +326,27 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_f16x3_kernel(
     auto load = [&](uint32_t k0) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint32_t gm = m0 + srow + 64 * h, gn = n0 + srow + 64 * h;
-            const size_t ka = (size_t)gm * K + k0 + 8 * sg, kb = (size_t)gn * K + k0 + 8 * sg;
-            const half8_t z = {};
-            st[0][h] = gm < M ? *reinterpret_cast<const half8_t *>(Ah + ka) : z;
-            st[1][h] = gm < M ? *reinterpret_cast<const half8_t *>(Al + ka) : z;
-            st[2][h] = gn < N ? *reinterpret_cast<const half8_t *>(Bh + kb) : z;
-            st[3][h] = gn < N ? *reinterpret_cast<const half8_t *>(Bl + kb) : z;
+            // rows past M (N) repeat the last row: they only feed outputs that are not stored;
+            // 32-bit element offsets (M K, N K < 2^31, checked by the launcher) off uniform bases
+            const uint32_t ka = min(m0 + srow + 64 * h, M - 1) * K + k0 + 8 * sg;
+            const uint32_t kb = min(n0 + srow + 64 * h, N - 1) * K + k0 + 8 * sg;
+            st[0][h] = *reinterpret_cast<const half8_t *>(Ah + ka);
+            st[1][h] = *reinterpret_cast<const half8_t *>(Al + ka);
+            st[2][h] = *reinterpret_cast<const half8_t *>(Bh + kb);
+            st[3][h] = *reinterpret_cast<const half8_t *>(Bl + kb);
         }
     };
-    auto stage = [&](int buf) {
+    auto stage = [&]() {
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                S[buf][a][hslot(srow + 64 * h, sg)] = st[a][h];
+                S[a][hslot(srow + 64 * h, sg)] = st[a][h];
     };
     load(0);
-    stage(0);
+    stage();
     __syncthreads();
     const int i16 = lane & 15, g = lane >> 4;
-    int buf = 0;
     for (uint32_t k0 = 0; k0 < K; k0 += kHK) {
         const bool more = k0 + kHK < K;
         if (more)
@@ -352,10 +354,10 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_f16x3_kernel(
         half8_t ah[4], al[4], bh[4], bl[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            ah[t] = S[buf][0][hslot(wm + 16 * t + i16, g)];
-            al[t] = S[buf][1][hslot(wm + 16 * t + i16, g)];
-            bh[t] = S[buf][2][hslot(wn + 16 * t + i16, g)];
-            bl[t] = S[buf][3][hslot(wn + 16 * t + i16, g)];
+            ah[t] = S[0][hslot(wm + 16 * t + i16, g)];
+            al[t] = S[1][hslot(wm + 16 * t + i16, g)];
+            bh[t] = S[2][hslot(wn + 16 * t + i16, g)];
+            bl[t] = S[3][hslot(wn + 16 * t + i16, g)];
         }
         // the three products in turn over all 16 blocks: an accumulator's dependent MFMAs
         // are 16 instructions apart
@@ -375,9 +377,9 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_f16x3_kernel(
             for (int tj = 0; tj < 4; ++tj)
                 acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ti], bh[tj], acc[ti][tj], 0, 0, 0);
         if (more) {
-            stage(buf ^ 1);
+            __syncthreads();  // every wave's operand reads of this stage are done
+            stage();
             __syncthreads();
-            buf ^= 1;
         }
     }
 #pragma unroll
@@ -1126,7 +1128,10 @@ void launch_split_f16(const float *x, uint32_t rows, uint32_t P, uint16_t *hl, f
                                                                           hi + (size_t)rows * P, scale);
 }
 
-bool dist_gemm_f16x3_supported(uint32_t K) { return K % kHK == 0; }
+bool dist_gemm_f16x3_supported(uint32_t K, uint64_t rows_a, uint64_t rows_b) {
+    // K % 32: whole MFMA steps (rows then also 16-byte aligned); 32-bit element offsets
+    return K % kHK == 0 && rows_a * K < (1ull << 31) && rows_b * K < (1ull << 31);
+}
 
 void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const float *qnorm,
                             const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t nq,

@@ -167,8 +167,8 @@ int cora_gpu_free_workspace(cora_gpu_engine *engine);
 int cora_gpu_queue_view(cora_gpu_engine *engine, cora_queue_view *out);
 
 /* Per-chunk reset (HybridIndex::reset_buffer, hybrid.cu:380-396): uploads the raw
- * queries f32 [nq][dim], resets device queue counters and the host Progress, and
- * sets the thresholds of the first nq queries to FLT_MAX. */
+ * queries f32 [nq][dim] (complete when the call returns), resets device queue counters
+ * and the host Progress, and sets the thresholds of the first nq queries to FLT_MAX. */
 int cora_gpu_reset(cora_gpu_engine *engine, const float *h_queries, uint64_t nq);
 
 /* Enqueue the whole GPU side of HybridIndex::search (hybrid.cu:434-660) and return
