@@ -1051,7 +1051,8 @@ __global__ __launch_bounds__(kThreads) void select_regs_kernel(const float *__re
         out[(size_t)blockIdx.x * k + i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
 }
 
-// One block (4 waves) per query; each wave takes probes p = wave, wave + 4, ...
+// One block (4 waves) per query; each wave takes probes p = wave, wave + 4, ..., two at a
+// time with both centroid rows' loads issued together.
 __global__ __launch_bounds__(256) void probe_refine_kernel(const float *__restrict__ qrot,
                                                            const float *__restrict__ cent,
                                                            const int32_t *__restrict__ idx,
@@ -1065,24 +1066,37 @@ __global__ __launch_bounds__(256) void probe_refine_kernel(const float *__restri
 #pragma unroll
     for (int i = 0; i < 16; ++i)
         v[i] = (uint32_t)i < groups ? qrot[(size_t)q * P + lane + 64 * i] : 0.0f;
-    for (uint32_t p = wave; p < nprobe; p += 4) {
-        const int32_t c = idx[(size_t)q * nprobe + p];
-        const float *crow = cent + (size_t)c * P;
-        float l2 = 0.0f, ip = 0.0f;
+    for (uint32_t p0 = wave; p0 < nprobe; p0 += 8) {
+        const bool two = p0 + 4 < nprobe;
+        const float *crow[2];
+        crow[0] = cent + (size_t)idx[(size_t)q * nprobe + p0] * P;
+        crow[1] = cent + (size_t)idx[(size_t)q * nprobe + (two ? p0 + 4 : p0)] * P;
+        float cv[2][16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            if ((uint32_t)i >= groups)
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                cv[h][i] = (uint32_t)i < groups ? crow[h][lane + 64 * i] : 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (h == 1 && !two)
                 break;
-            const float cv = crow[lane + 64 * i];
-            const float d = v[i] - cv;
-            l2 = fmaf(d, d, l2);
-            ip = fmaf(v[i], cv, ip);
-        }
-        l2 = wave_sum(l2);
-        ip = wave_sum(ip);
-        if (lane == 0) {
-            gadd[(size_t)q * nprobe + p] = metric == 0 ? l2 : -ip;
-            gerr[(size_t)q * nprobe + p] = sqrtf(fmaxf(l2, 0.0f));
+            float l2 = 0.0f, ip = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if ((uint32_t)i >= groups)
+                    break;
+                const float d = v[i] - cv[h][i];
+                l2 = fmaf(d, d, l2);
+                ip = fmaf(v[i], cv[h][i], ip);
+            }
+            l2 = wave_sum(l2);
+            ip = wave_sum(ip);
+            const uint32_t p = p0 + 4 * h;
+            if (lane == 0) {
+                gadd[(size_t)q * nprobe + p] = metric == 0 ? l2 : -ip;
+                gerr[(size_t)q * nprobe + p] = sqrtf(fmaxf(l2, 0.0f));
+            }
         }
     }
 }

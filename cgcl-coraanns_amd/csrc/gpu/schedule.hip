@@ -33,8 +33,9 @@ __device__ __forceinline__ uint32_t pair_bucket(const int32_t *__restrict__ prob
 
 // Counting with a per-block LDS histogram over contiguous pair ranges, so a bucket takes
 // one global atomic per block instead of one per pair (popular clusters otherwise
-// serialise thousands of same-address atomics). Needs 2 * nlist <= kLdsBuckets.
-constexpr uint32_t kLdsBuckets = 16384;
+// serialise thousands of same-address atomics). Needs 2 * nlist <= kLdsBuckets (128 KB of
+// LDS at the maximum, beyond the default 64 KB dynamic limit).
+constexpr uint32_t kLdsBuckets = 32768;
 constexpr uint32_t kHistThreads = 1024;
 constexpr uint32_t kHistPairs = 4096;  // pairs per block
 
@@ -109,10 +110,28 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
     const uint32_t b0 = min(nb, t * chunk), b1 = min(nb, b0 + chunk);
     uint32_t pairs = 0, units = 0, van_units = 0;
     unsigned long long bytes = 0, fu = 0, vec = 0, vbytes = 0;
-    for (uint32_t b = b0; b < b1; ++b) {
-        const uint32_t m = count[b];
+    // the thread's buckets 16 at a time: their loads issued together (one round trip per
+    // 16 buckets instead of one per bucket; this single workgroup is latency-bound)
+    constexpr uint32_t kBatch = 16;
+    uint32_t mv[kBatch], nv[kBatch];
+    auto fetch = [&](uint32_t bb) {
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const uint32_t b = bb + j;
+            mv[j] = b < b1 ? count[b] : 0u;
+            nv[j] = b < b1 ? meta[b < nlist ? b : b - nlist].n : 0u;
+        }
+    };
+    for (uint32_t bb = b0; bb < b1; bb += kBatch) {
+        fetch(bb);
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+        const uint32_t b = bb + j;
+        if (b >= b1)
+            break;
+        const uint32_t m = mv[j];
         pairs += m;
-        const uint32_t n = meta[b < nlist ? b : b - nlist].n, sp = unit_splits(n);
+        const uint32_t n = nv[j], sp = unit_splits(n);
         if (b < nlist) {
             units += m * sp;
             van_units += m * sp;
@@ -123,6 +142,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
             bytes += (unsigned long long)u * n * bpv;
             fu += u;
             vec += (unsigned long long)m * n;
+        }
         }
     }
     s_pairs[t] = pairs;
@@ -150,13 +170,20 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
         __syncthreads();
     }
     uint32_t po = s_pairs[t] - pairs, uo = s_units[t] - units;
-    for (uint32_t b = b0; b < b1; ++b) {
-        const uint32_t m = count[b];
-        bucket_offset[b] = po;
-        unit_offset[b] = uo;
-        po += m;
-        const uint32_t sp = unit_splits(meta[b < nlist ? b : b - nlist].n);
-        uo += (b < nlist ? m : (m + batch_q - 1) / batch_q) * sp;
+    for (uint32_t bb = b0; bb < b1; bb += kBatch) {
+        fetch(bb);
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const uint32_t b = bb + j;
+            if (b >= b1)
+                break;
+            const uint32_t m = mv[j];
+            bucket_offset[b] = po;
+            unit_offset[b] = uo;
+            po += m;
+            const uint32_t sp = unit_splits(nv[j]);
+            uo += (b < nlist ? m : (m + batch_q - 1) / batch_q) * sp;
+        }
     }
     if (t == kScanThreads - 1) {
         bucket_offset[nb] = s_pairs[t];
@@ -241,6 +268,15 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
     const bool lds = 2 * (size_t)nlist <= kLdsBuckets;
     const uint32_t hgrid = (uint32_t)((np + kHistPairs - 1) / kHistPairs);
     const size_t hbytes = 2 * (size_t)nlist * sizeof(uint32_t);
+    static bool raised = false;  // dynamic LDS above 64 KB must be allowed explicitly
+    if (lds && hbytes > 65536 && !raised) {
+        for (const void *f : {reinterpret_cast<const void *>(&count_pairs_lds_kernel),
+                              reinterpret_cast<const void *>(&scatter_pairs_lds_kernel)})
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)(kLdsBuckets * sizeof(uint32_t))) != hipSuccess)
+                (void)hipGetLastError();  // leave no sticky error; the launch then reports it
+        raised = true;
+    }
     if (lds)
         count_pairs_lds_kernel<<<hgrid, kHistThreads, hbytes, s>>>(probe_idx, np, nprobe, nlist, vanguard,
                                                                   bucket_count);
