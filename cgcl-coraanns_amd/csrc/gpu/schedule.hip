@@ -126,23 +126,21 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
         fetch(bb);
 #pragma unroll
         for (uint32_t j = 0; j < kBatch; ++j) {
-        const uint32_t b = bb + j;
-        if (b >= b1)
-            break;
-        const uint32_t m = mv[j];
-        pairs += m;
-        const uint32_t n = nv[j], sp = unit_splits(n);
-        if (b < nlist) {
-            units += m * sp;
-            van_units += m * sp;
-            vbytes += (unsigned long long)m * n * bpv;  // vanguard pairs: one pass per pair
-        } else {
-            const uint32_t u = (m + batch_q - 1) / batch_q;
-            units += u * sp;
-            bytes += (unsigned long long)u * n * bpv;
-            fu += u;
-            vec += (unsigned long long)m * n;
-        }
+            const uint32_t b = bb + j;  // past b1: m = 0 and n = 0, which add nothing
+            const uint32_t m = mv[j];
+            pairs += m;
+            const uint32_t n = nv[j], sp = unit_splits(n);
+            if (b < nlist) {
+                units += m * sp;
+                van_units += m * sp;
+                vbytes += (unsigned long long)m * n * bpv;  // vanguard pairs: one pass per pair
+            } else {
+                const uint32_t u = (m + batch_q - 1) / batch_q;
+                units += u * sp;
+                bytes += (unsigned long long)u * n * bpv;
+                fu += u;
+                vec += (unsigned long long)m * n;
+            }
         }
     }
     s_pairs[t] = pairs;
@@ -175,11 +173,11 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
 #pragma unroll
         for (uint32_t j = 0; j < kBatch; ++j) {
             const uint32_t b = bb + j;
-            if (b >= b1)
-                break;
             const uint32_t m = mv[j];
-            bucket_offset[b] = po;
-            unit_offset[b] = uo;
+            if (b < b1) {
+                bucket_offset[b] = po;
+                unit_offset[b] = uo;
+            }
             po += m;
             const uint32_t sp = unit_splits(nv[j]);
             uo += (b < nlist ? m : (m + batch_q - 1) / batch_q) * sp;
