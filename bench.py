@@ -109,8 +109,8 @@ def copy_calibration():
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=4,
                     help="BASELINE configuration (default 4: 20M x 768 inner product, the headline workload)")
     ap.add_argument("--nprobe", type=int, default=0, help="0: smallest grid nprobe reaching the recall target")
@@ -308,6 +308,7 @@ def main():
         "config": {"workload": c.describe(), "nprobe": nprobe, "recall_at_10": round(float(np.mean(recalls)), 4),
                    f"recall_at_{c.topk}": round(float(np.mean(recalls_k)), 4),
                    "qps_with_upload": round(queries.shape[0] * args.steps / sum(times_up), 1),
+                   "step_ms": [round(1000.0 * t, 3) for t in times],
                    "batch_q": batch_q, "vanguard": vanguard, "cpu_secondary_filter": c.secondary_filter,
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
                    "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
