@@ -145,7 +145,10 @@ def main():
     from coraanns_amd import workloads as wl
 
     c = wl.CONFIGS[args.config]
-    threads = args.cpu_threads or min(16, os.cpu_count() or 16)
+    # CPU refinement threads: 12 of the box's 16-CPU share, so the submitting thread and the
+    # HIP runtime's threads are not starved by spinning consumers (with 16, a search now and
+    # then waited a scheduler tick, ~4 ms)
+    threads = args.cpu_threads or min(12, os.cpu_count() or 12)
     batch_q = args.batch_q or c.batch_q
     workdir = args.workdir or tempfile.mkdtemp(prefix="cora_bench_")
     os.makedirs(workdir, exist_ok=True)
@@ -290,7 +293,9 @@ def main():
     baseline = None
     if not args.no_cpu_baseline:
         sample = args.cpu_queries or (queries.shape[0] if c.padded_dim <= 128 else 2000)
-        baseline = cpu_baseline(index_path, queries, gt, c.topk, nprobe, threads, workdir, sample)
+        # the reference CPU path gets the whole 16-CPU share (nothing else runs beside it)
+        baseline = cpu_baseline(index_path, queries, gt, c.topk, nprobe, args.cpu_threads or min(16, os.cpu_count() or 16),
+                                workdir, sample)
 
     line = {
         "metric": "QPS at recall@10>=0.9 (1 GPU)",
