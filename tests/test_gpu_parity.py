@@ -224,13 +224,15 @@ def order_keys(d):
 
 
 @pytest.mark.parametrize("nlist,distinct,nprobe", [(12000, 0, 16), (16384, 0, 32), (16384, 0, 64),
-                                                   (16384, 40, 32), (12000, 7, 64)])
+                                                   (16384, 40, 32), (12000, 7, 64), (20000, 0, 32),
+                                                   (40000, 0, 16), (65536, 0, 64), (65536, 0, 33),
+                                                   (40000, 50, 64)])
 def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
-    """The probe select (8,192 < nlist <= 16,384: per-wave candidates below the k-th lane
-    minimum, ranked by (distance, cluster id); heavy ties fall back to the radix select)
-    against an exact sort of the GPU's own distance matrix by (distance key, cluster id).
-    distinct > 0 repeats that many centroids over the whole list, so every distance is tied
-    nlist / distinct times."""
+    """The probe select (8,192 < nlist <= 16,384: distances in registers; beyond: two
+    streaming passes; either way per-wave candidates below a bound from minima, ranked by
+    (distance, cluster id); heavy ties fall back to the radix select) against an exact sort
+    of the GPU's own distance matrix by (distance key, cluster id). distinct > 0 repeats that
+    many centroids over the whole list, so every distance is tied nlist / distinct times."""
     rng = np.random.default_rng(nlist + distinct)
     dim, nq = 64, 40
     n = 2 * nlist
