@@ -114,6 +114,7 @@ def main():
     ap.add_argument("--config", type=int, default=4,
                     help="BASELINE configuration (default 4: 20M x 768 inner product, the headline workload)")
     ap.add_argument("--nprobe", type=int, default=0, help="0: smallest grid nprobe reaching the recall target")
+    ap.add_argument("--topk", type=int, default=0, help="override the configuration's top-k (config 4: 10 and 100)")
     ap.add_argument("--recall-target", type=float, default=0.9)
     ap.add_argument("--batch-q", type=int, default=0)
     ap.add_argument("--vanguard", type=int, default=-1, help="vanguard size (default: the configuration's)")
@@ -145,15 +146,19 @@ def main():
     from coraanns_amd import workloads as wl
 
     c = wl.CONFIGS[args.config]
-    # CPU refinement threads: 12 of the box's 16-CPU share, so the submitting thread and the
-    # HIP runtime's threads are not starved by spinning consumers (with 16, a search now and
-    # then waited a scheduler tick, ~4 ms)
-    threads = args.cpu_threads or min(12, os.cpu_count() or 12)
+    if args.topk:  # config 4 is specified at top-10 and top-100
+        import dataclasses
+        c = dataclasses.replace(c, topk=args.topk)
+    # CPU refinement threads: at top-10 the GPU bounds the step and 12 of the box's 16-CPU
+    # share leave room for the submitting thread and the HIP runtime's threads (with 16
+    # spinning consumers a search now and then waited a scheduler tick, ~4 ms); at top-100
+    # the CPU refinement of ~190 candidates per query bounds it and takes all 16
+    threads = args.cpu_threads or min(12 if c.topk <= 10 else 16, os.cpu_count() or 16)
     batch_q = args.batch_q or c.batch_q
     workdir = args.workdir or tempfile.mkdtemp(prefix="cora_bench_")
     os.makedirs(workdir, exist_ok=True)
     index_path = Path(workdir) / f"cfg{c.cfg}.index"
-    gt_path = Path(workdir) / f"cfg{c.cfg}_gt.npy"
+    gt_path = Path(workdir) / (f"cfg{c.cfg}_gt.npy" if not args.topk else f"cfg{c.cfg}_gt_top{c.topk}.npy")
     t0 = time.time()
     if args.workdir and index_path.exists() and gt_path.exists():
         _, queries = wl.generate(c, n=args.n or None, nq=args.nq or None, queries_only=True)
