@@ -101,9 +101,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
     uint32_t batch_q, uint32_t bpv, uint32_t *__restrict__ bucket_offset,
     uint32_t *__restrict__ unit_offset, uint32_t *__restrict__ num_units,
     unsigned long long *__restrict__ stats) {
-    __shared__ uint32_t s_pairs[kScanThreads], s_units[kScanThreads], s_van_units[kScanThreads];
-    __shared__ unsigned long long s_bytes[kScanThreads], s_fu[kScanThreads], s_vec[kScanThreads];
-    __shared__ unsigned long long s_vbytes[kScanThreads];
+    constexpr int kWaves = kScanThreads / 64;
+    // per-wave totals of the seven sums (inclusive scans run within each wave by shuffles)
+    __shared__ unsigned long long s_tot[7][kWaves];
     const uint32_t nb = 2 * nlist;
     const int t = threadIdx.x;
     const uint32_t chunk = (nb + kScanThreads - 1) / kScanThreads;
@@ -143,31 +143,27 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
             }
         }
     }
-    s_pairs[t] = pairs;
-    s_units[t] = units;
-    s_van_units[t] = van_units;
-    s_bytes[t] = bytes;
-    s_fu[t] = fu;
-    s_vec[t] = vec;
-    s_vbytes[t] = vbytes;
-    __syncthreads();
-    for (int o = 1; o < kScanThreads; o <<= 1) {
-        const uint32_t xp = t >= o ? s_pairs[t - o] : 0, xu = t >= o ? s_units[t - o] : 0;
-        const uint32_t xv = t >= o ? s_van_units[t - o] : 0;
-        const unsigned long long xb = t >= o ? s_bytes[t - o] : 0, xf = t >= o ? s_fu[t - o] : 0;
-        const unsigned long long xe = t >= o ? s_vec[t - o] : 0;
-        const unsigned long long xvb = t >= o ? s_vbytes[t - o] : 0;
-        __syncthreads();
-        s_pairs[t] += xp;
-        s_units[t] += xu;
-        s_van_units[t] += xv;
-        s_bytes[t] += xb;
-        s_fu[t] += xf;
-        s_vec[t] += xe;
-        s_vbytes[t] += xvb;
-        __syncthreads();
+    // inclusive scans over the block: within each wave by shuffles, then the totals of the
+    // waves before (one barrier)
+    const int lane = t & 63, wave = t >> 6;
+    unsigned long long v[7] = {pairs, units, van_units, bytes, fu, vec, vbytes};
+#pragma unroll
+    for (int a = 0; a < 7; ++a) {
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const unsigned long long y = __shfl_up(v[a], o);
+            if (lane >= o)
+                v[a] += y;
+        }
+        if (lane == 63)
+            s_tot[a][wave] = v[a];
     }
-    uint32_t po = s_pairs[t] - pairs, uo = s_units[t] - units;
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < 7; ++a)
+        for (int w = 0; w < wave; ++w)
+            v[a] += s_tot[a][w];
+    uint32_t po = (uint32_t)v[0] - pairs, uo = (uint32_t)v[1] - units;
     for (uint32_t bb = b0; bb < b1; bb += kBatch) {
         fetch(bb);
 #pragma unroll
@@ -184,14 +180,14 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
         }
     }
     if (t == kScanThreads - 1) {
-        bucket_offset[nb] = s_pairs[t];
-        unit_offset[nb] = s_units[t];
-        num_units[0] = s_van_units[t];
-        num_units[1] = s_units[t] - s_van_units[t];
-        stats[0] = s_bytes[t];
-        stats[1] = s_fu[t];
-        stats[2] = s_vec[t];
-        stats[9] = s_vbytes[t];
+        bucket_offset[nb] = (uint32_t)v[0];
+        unit_offset[nb] = (uint32_t)v[1];
+        num_units[0] = (uint32_t)v[2];
+        num_units[1] = (uint32_t)(v[1] - v[2]);
+        stats[0] = v[3];
+        stats[1] = v[4];
+        stats[2] = v[5];
+        stats[9] = v[6];
     }
 }
 
