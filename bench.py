@@ -3,10 +3,10 @@
 search on one GPU, plus the RaBitQ scan kernel's HBM roofline and the reference CPU path
 (rabitq_cpu) timed on the same host.
 
-A step is one search() over the workload's full query set (one chunk of <= 65,535
-queries) with the index resident in HBM and the queries already uploaded by reset_buffer,
-which runs before the timed call; the rate including that upload (the reference driver's
-search_all_queries, apps/search.cpp:223-241) is reported as config.qps_with_upload. The
+A step is what the reference driver times per query chunk (apps/search.cpp:230,251-253):
+reset_buffer (query upload, queue and threshold reset) followed by search() over the
+workload's full query set (one chunk of <= 65,535 queries), with the index resident in
+HBM. The rate of search() alone is reported as config.qps_search_only. The
 headline nprobe is the smallest of the configuration's nprobe grid whose recall@10 reaches
 the target. Prints one JSON line on stdout; progress goes to stderr.
 
@@ -17,6 +17,7 @@ import argparse
 import json
 import os
 import re
+import shutil
 import subprocess
 import sys
 import tempfile
@@ -56,7 +57,10 @@ def cpu_baseline(index_path, queries, gt, topk, nprobe, threads, workdir, sample
     write_fbin(qf, queries)
     write_fbin(gf, gt[:, :topk], np.uint32)
     env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_DYNAMIC="FALSE")
-    cmd = [str(exe), str(index_path), str(qf), str(gf), "--topk", str(topk), "--nprobes", str(nprobe),
+    # the reference's measurement recipe runs it with memory interleaved over NUMA nodes
+    # (README.md:100, docs/REPRODUCIBILITY.md:71); numactl is used when the host has it
+    numactl = shutil.which("numactl")
+    cmd = ([numactl, "--interleave=all"] if numactl else []) + [str(exe), str(index_path), str(qf), str(gf), "--topk", str(topk), "--nprobes", str(nprobe),
            "--threads", str(threads), "--warmup", "1", "--rounds", "3", "--hacc", "true"]
     t = time.time()
     try:
@@ -75,8 +79,10 @@ def cpu_baseline(index_path, queries, gt, topk, nprobe, threads, workdir, sample
         f"recall={float(rec):.4f} ({time.time() - t:.1f}s)")
     return {"value": round(float(qps), 1), "unit": "queries/s", "cores": threads, "kind": "reference",
             "recall": round(float(rec), 4),
+            "numactl_interleave": bool(numactl),
             "sample": f"{queries.shape[0]} queries x 3 rounds (1 warmup) at nprobe {nprobe}, top-{topk}, "
-                      f"same index file, rabitq_cpu --hacc true built -mavx2 -mfma"}
+                      f"same index file, rabitq_cpu --hacc true built -mavx2 -mfma"
+                      f"{', numactl --interleave=all' if numactl else ' (no numactl on this host)'}"}
 
 
 def hbm_traffic(cfg, nprobe, kernel):
@@ -191,13 +197,14 @@ def main():
     assert queries.shape[0] <= chunk, "one search() per step"
 
     def step(nprobe):
+        # reset_buffer + search, as the reference driver times each chunk
         t0 = time.perf_counter()
-        eng.reset_buffer(queries)  # query upload: outside the timed region
+        eng.reset_buffer(queries)
         t = time.perf_counter()
         d, i = eng.search(queries, c.topk, nprobe, batch_q)
         t1 = time.perf_counter()
-        step.with_upload = t1 - t0
-        return t1 - t, i, eng.stats()
+        step.search_only = t1 - t
+        return t1 - t0, i, eng.stats()
 
     sweep = []
     for nprobe in ([] if args.nprobe else c.nprobes):  # --nprobe: measure that one only
@@ -224,13 +231,15 @@ def main():
 
     for _ in range(args.warmup):
         step(nprobe)
-    times, times_up, scan_ms, scan_bytes, recalls, probe_ms, probe_flops = [], [], [], [], [], [], []
+    times, times_search, scan_ms, scan_bytes, recalls, probe_ms, probe_flops = [], [], [], [], [], [], []
     recalls_k = []
     van_ms, van_bytes = [], []
+    last_ids = None
     for _ in range(args.steps):
         dt, ids, st = step(nprobe)
+        last_ids = ids
         times.append(dt)
-        times_up.append(step.with_upload)
+        times_search.append(step.search_only)
         probe_ms.append(st["probe_ms"])
         probe_flops.append(st["probe_flops"])
         scan_ms.append(st["scan_ms"])
@@ -301,6 +310,11 @@ def main():
         # the reference CPU path gets the whole 16-CPU share (nothing else runs beside it)
         baseline = cpu_baseline(index_path, queries, gt, c.topk, nprobe, args.cpu_threads or min(16, os.cpu_count() or 16),
                                 workdir, sample)
+        if baseline is not None:
+            # the GPU's recall on exactly the queries the CPU baseline ran
+            n_s = min(sample, queries.shape[0])
+            baseline["gpu_recall_same_sample"] = round(recall_at_k(last_ids[:n_s], gt[:n_s], c.topk), 4)
+            baseline["gpu_recall_at_10_same_sample"] = round(recall_at_k(last_ids[:n_s], gt[:n_s], 10), 4)
 
     line = {
         "metric": "QPS at recall@10>=0.9 (1 GPU)",
@@ -317,7 +331,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": c.describe(), "nprobe": nprobe, "recall_at_10": round(float(np.mean(recalls)), 4),
                    f"recall_at_{c.topk}": round(float(np.mean(recalls_k)), 4),
-                   "qps_with_upload": round(queries.shape[0] * args.steps / sum(times_up), 1),
+                   "qps_search_only": round(queries.shape[0] * args.steps / sum(times_search), 1),
                    "step_ms": [round(1000.0 * t, 3) for t in times],
                    "batch_q": batch_q, "vanguard": vanguard, "cpu_secondary_filter": c.secondary_filter,
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",

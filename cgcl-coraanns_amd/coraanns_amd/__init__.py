@@ -72,7 +72,8 @@ def _raise(code, msg):
 
 class cora_search_args(C.Structure):
     _fields_ = [("num_queries", C.c_uint32), ("topk", C.c_uint32), ("nprobe", C.c_uint32),
-                ("batch_q", C.c_uint32), ("vanguard", C.c_uint32), ("flags", C.c_uint32)]
+                ("batch_q", C.c_uint32), ("vanguard", C.c_uint32), ("flags", C.c_uint32),
+                ("bound_scale", C.c_float)]
 
 
 class cora_search_stats(C.Structure):
@@ -96,7 +97,8 @@ class cora_hybrid_config(C.Structure):
                 ("cpu_secondary_filter", C.c_int), ("vanguard_size", C.c_uint64),
                 ("queue_capacity", C.c_uint64), ("queue_spill_capacity", C.c_uint64),
                 ("metric", C.c_int), ("frozen_thresholds", C.c_int), ("cpu_threads", C.c_int),
-                ("gpu_seed_refine", C.c_int), ("gpu_refine_filter", C.c_int), ("extra_flags", C.c_uint32)]
+                ("gpu_seed_refine", C.c_int), ("gpu_refine_filter", C.c_int), ("extra_flags", C.c_uint32),
+                ("lower_bound_scale", C.c_float)]
 
 
 class cora_hybrid_stats(C.Structure):
@@ -285,7 +287,8 @@ class HybridIndex:
     def __init__(self, device=0, *, profiling=False, candidate_stats=False, gpu_filter_timing=False,
                  cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                  queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
-                 cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0):
+                 cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0,
+                 lower_bound_scale=None):
         _, host = _load()
         h = C.c_void_p()
         _host_check(host.cora_hybrid_create(C.byref(h), device))
@@ -297,18 +300,22 @@ class HybridIndex:
                        queue_capacity=queue_capacity, queue_spill_capacity=queue_spill_capacity,
                        metric=metric, frozen_thresholds=frozen_thresholds, cpu_threads=cpu_threads,
                        gpu_seed_refine=gpu_seed_refine, gpu_refine_filter=gpu_refine_filter,
-                       extra_flags=extra_flags)
+                       extra_flags=extra_flags, lower_bound_scale=lower_bound_scale)
 
     def configure(self, *, profiling=False, candidate_stats=False, gpu_filter_timing=False,
                   cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                   queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
-                  cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0):
+                  cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0,
+                  lower_bound_scale=None):
+        """lower_bound_scale: multiplier of the filter's error term (None keeps the
+        engine's default; 1.0 is the reference Bitwise producer's bound)."""
         cfg = cora_hybrid_config(int(profiling), int(candidate_stats), int(gpu_filter_timing),
                                  int(cross_query_reuse), int(cpu_secondary_filter), int(vanguard_size),
                                  int(queue_capacity or 0),
                                  (1 << 64) - 1 if queue_spill_capacity is None else int(queue_spill_capacity),
                                  int(metric), int(frozen_thresholds), int(cpu_threads),
-                                 int(gpu_seed_refine), int(gpu_refine_filter), int(extra_flags))
+                                 int(gpu_seed_refine), int(gpu_refine_filter), int(extra_flags),
+                                 float(lower_bound_scale or 0.0))
         _host_check(_load()[1].cora_hybrid_configure(self._h, C.byref(cfg)))
 
     def load_from_raw_pointers(self, num_vecs, dim, padded_dim, n_centroids, ex_bits, centroids,

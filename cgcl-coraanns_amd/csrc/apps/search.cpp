@@ -27,6 +27,7 @@
 #include <string>
 #include <vector>
 
+#include "coraanns/benchmark/recall.hpp"
 #include "coraanns/index/ivf_file.hpp"
 #include "coraanns/index/search_data.hpp"
 #include "coraanns/search/hybrid.hpp"
@@ -42,7 +43,8 @@ void print_usage(const char *program) {
                  " [--queue-capacity 67108864] [--queue-spill-capacity 16777216]"
                  " [--cross-query-reuse true] [--candidate-stats false]"
                  " [--gpu-filter-timing false] [--profile false]"
-                 " [--exact-base FILE] [--recall-base FILE] [--recall-once false]\n";
+                 " [--exact-base FILE] [--recall-base FILE] [--recall-once false]"
+                 " [--lower-bound-scale 1.5]\n";
 }
 
 class Options {
@@ -194,70 +196,16 @@ class Matrix {
     std::size_t size_ = 0, rows_ = 0, cols_ = 0, stride_ = 0, offset_ = 0;
 };
 
-// Recall@k (reference recall.hpp:74-275): ID hits against the ground-truth top-k; with a
-// base file, a non-GT result also counts when its exact distance is within the k-th
-// ground-truth distance (<= for L2, >= for IP). Duplicate result IDs count once.
-class Recall {
-  public:
-    Recall(const std::vector<float> &q, std::size_t dim, const Matrix &gt, std::size_t topk,
-           const Matrix *base, int metric)
-        : q_(q), dim_(dim), k_(topk), base_(base), metric_(metric) {
-        const std::size_t nq = q.size() / dim;
-        if (gt.rows() != nq || gt.cols() < topk)
-            throw std::invalid_argument("Invalid query/GT shape for recall@k");
-        truth_.resize(nq * topk);
-        thr_.resize(nq);
-        for (std::size_t i = 0; i < nq; ++i) {
-            const uint32_t *g = gt.row<uint32_t>(i);
-            std::copy(g, g + topk, truth_.begin() + i * topk);
-            if (base_)
-                thr_[i] = score(i, g[topk - 1]);
-            std::sort(truth_.begin() + i * topk, truth_.begin() + (i + 1) * topk);
-        }
-        std::cout << "[Recall] mode=" << (base_ ? "distance-aware" : "id")
-                  << " metric=" << (metric == 0 ? "l2" : "ip") << " topk=" << topk << "\n";
-    }
-    double evaluate(const std::vector<uint32_t> &ids) const {
-        const std::size_t nq = thr_.size();
-        std::size_t id_hits = 0, dist_hits = 0;
-#pragma omp parallel for reduction(+ : id_hits, dist_hits) schedule(static)
-        for (std::size_t i = 0; i < nq; ++i) {
-            std::vector<uint32_t> r(ids.begin() + i * k_, ids.begin() + (i + 1) * k_);
-            std::sort(r.begin(), r.end());
-            r.erase(std::unique(r.begin(), r.end()), r.end());
-            for (uint32_t id : r) {
-                if (std::binary_search(truth_.begin() + i * k_, truth_.begin() + (i + 1) * k_, id)) {
-                    ++id_hits;
-                } else if (base_ && id < base_->rows()) {
-                    const double s = score(i, id);
-                    if (std::isfinite(s) && (metric_ == 0 ? s <= thr_[i] : s >= thr_[i]))
-                        ++dist_hits;
-                }
-            }
-        }
-        const double denom = static_cast<double>(nq * k_);
-        std::cout << "[RecallEval] id_recall=" << id_hits / denom
-                  << " recall=" << (id_hits + dist_hits) / denom << " distance_hits=" << dist_hits
-                  << "\n";
-        return (id_hits + dist_hits) / denom;
-    }
-
-  private:
-    double score(std::size_t q, uint32_t id) const {
-        const float *a = q_.data() + q * dim_;
-        const float *b = base_->row<float>(id);
-        double s = 0;
-        for (std::size_t d = 0; d < dim_; ++d)
-            s += metric_ == 0 ? (double(a[d]) - b[d]) * (double(a[d]) - b[d]) : double(a[d]) * b[d];
-        return s;
-    }
-    const std::vector<float> &q_;
-    std::size_t dim_, k_;
-    const Matrix *base_;
-    int metric_;
-    std::vector<uint32_t> truth_;
-    std::vector<double> thr_;
-};
+// Distance-aware recall needs the base rows; the mapping above provides them.
+coraanns::benchmark::MatrixView view_of(const Matrix &m) {
+    coraanns::benchmark::MatrixView v;
+    v.data = m.mapping();
+    v.offset = m.offset();
+    v.stride = m.stride();
+    v.rows = m.rows();
+    v.cols = m.cols();
+    return v;
+}
 
 }  // namespace
 
@@ -272,7 +220,7 @@ int main(int argc, char **argv) {
                            "query-chunk", "vanguard-size", "cpu-secondary-filter", "profile",
                            "cross-query-reuse", "candidate-stats", "gpu-filter-timing",
                            "exact-base", "recall-once", "queue-capacity", "queue-spill-capacity",
-                           "recall-base"});
+                           "recall-base", "lower-bound-scale"});
         const std::size_t topk = opt.size("topk", 100);
         const std::size_t rounds = opt.size("rounds", 5);
         const std::size_t warmup = opt.size("warmup", 1);
@@ -314,11 +262,23 @@ int main(int argc, char **argv) {
         if (topk == 0 || rounds == 0 || nq == 0 || gt.rows() != nq || dim != ivf.dim || gt.cols() < topk)
             throw std::invalid_argument("query/ground-truth/index shapes do not match");
         std::unique_ptr<Matrix> base_map;
-        if (!recall_base.empty())
+        coraanns::benchmark::MatrixView base_view;
+        if (!recall_base.empty()) {
             base_map = std::make_unique<Matrix>(recall_base);
-        std::unique_ptr<Recall> evaluator;
+            base_view = view_of(*base_map);
+        }
+        const std::vector<uint32_t> gt_ids = gt.dense<uint32_t>();
+        using Evaluator = coraanns::benchmark::RecallEvaluator;
+        auto make_evaluator = [&] {
+            auto e = std::make_unique<Evaluator>(query.data(), nq, dim, gt_ids.data(), gt.rows(), gt.cols(), topk,
+                                                 base_map ? &base_view : nullptr, metric);
+            std::cout << "[Recall] mode=" << (base_map ? "distance-aware" : "id")
+                      << " metric=" << (metric == 0 ? "l2" : "ip") << " topk=" << topk << "\n";
+            return e;
+        };
+        std::unique_ptr<Evaluator> evaluator;
         if (!recall_once)
-            evaluator = std::make_unique<Recall>(query, dim, gt, topk, base_map.get(), metric);
+            evaluator = make_evaluator();
         std::unique_ptr<Matrix> exact;
         if (!exact_file.empty()) {
             if (metric != 0) {
@@ -343,6 +303,14 @@ int main(int argc, char **argv) {
         engine.set_cross_query_reuse(reuse);
         engine.set_cpu_secondary_filter(secondary);
         engine.set_vanguard_size(vanguard);
+        const std::string lbs = opt.get("lower-bound-scale", "");
+        if (!lbs.empty()) {
+            std::size_t used = 0;
+            const float v = std::stof(lbs, &used);
+            if (used != lbs.size())
+                throw std::invalid_argument("Invalid number for --lower-bound-scale: " + lbs);
+            engine.set_lower_bound_scale(v);
+        }
         engine.set_metric(metric);
         engine.load_from_raw_pointers(ivf.num, ivf.dim, ivf.padded_dim, ivf.nlist, ivf.ex_bits,
                                       packed.h_centroids.data(), packed.host_rotator.data(),
@@ -364,6 +332,7 @@ int main(int argc, char **argv) {
                   << "\nqueue_spill_capacity: " << scap << "\nvanguard_size: " << vanguard
                   << "\ncpu_secondary_filter: " << (secondary ? "true" : "false")
                   << "\ncross_query_reuse: " << (reuse ? "true" : "false")
+                  << "\nlower_bound_scale: " << engine.get_lower_bound_scale()
                   << "\nrounds: " << rounds << "\nwarmup_rounds: " << warmup << "\n";
 
         std::vector<float> dists(nq * topk);
@@ -408,7 +377,7 @@ int main(int argc, char **argv) {
                         saved[l] = result;
                     std::cout << " recall=deferred\n";
                 } else {
-                    const double rr = evaluator->evaluate(result);
+                    const double rr = evaluator->evaluate(result.data(), result.size());
                     rec[l] += rr / rounds;
                     std::cout << " recall=" << rr << '\n';
                 }
@@ -429,9 +398,9 @@ int main(int argc, char **argv) {
             }
         }
         if (recall_once) {
-            evaluator = std::make_unique<Recall>(query, dim, gt, topk, base_map.get(), metric);
+            evaluator = make_evaluator();
             for (std::size_t l = 0; l < nprobes.size(); ++l) {
-                rec[l] = evaluator->evaluate(saved[l]);
+                rec[l] = evaluator->evaluate(saved[l].data(), saved[l].size());
                 std::cout << "[RecallPoint] nprobe=" << nprobes[l] << " source_round=1 recall="
                           << rec[l] << '\n';
             }

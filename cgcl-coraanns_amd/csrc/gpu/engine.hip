@@ -664,6 +664,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     if (a->num_queries == 0 || a->num_queries > E->ws_q || a->topk == 0 || a->topk > E->ws_k ||
         a->nprobe == 0 || a->nprobe > E->ws_np)
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "search shape exceeds the prepared workspace");
+    if (!(a->bound_scale >= 0.0f && a->bound_scale <= 16.0f))
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "invalid bound scale (expected 0..16; 0 means 1)");
     if (a->batch_q < 1 || a->batch_q > (uint32_t)kMaxBatchQ)
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "invalid batch-q (expected 1..8)");
     const uint64_t want_depth = std::min<uint64_t>(a->vanguard, a->nprobe);
@@ -682,6 +684,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool frozen = (a->flags & CORA_FLAG_FROZEN_THRESHOLDS) != 0;
     const bool timing = (a->flags & CORA_FLAG_FILTER_TIMING) != 0;
     E->last = *a;
+    E->ring_dirty = true;  // until cora_gpu_sync sees every produced record released
     E->last_depth = depth;
     E->last_batch = batch;
     E->last_mfma = mfma_far;
@@ -718,7 +721,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         HIPCHK(hipEventRecord(E->ev_p1, s));
     launch_select(E->d_dist, nq, (uint32_t)E->nl, np, E->d_pidx, s);
     launch_probe_refine(E->d_qrot, E->d_cent, E->d_pidx, nq, np, P, E->metric, E->d_gadd,
-                        E->d_gerr, s);
+                        E->d_gerr, a->bound_scale > 0.0f ? a->bound_scale : 1.0f, s);
     HIPCHK(hipEventRecord(E->ev_probe, s));
     HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_probe, 0));
     HIPCHK(hipMemcpyAsync(E->h_gadd, E->d_gadd, (size_t)nq * np * 4, hipMemcpyDeviceToHost,
@@ -883,6 +886,10 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     }
     if (st)
         *st = out;
+    // The ring is clean once the consumer has cleared and released every record the GPU
+    // produced; otherwise (a consumer that stopped early, an abort) the next reset clears it.
+    const unsigned long long released = __atomic_load_n(&E->h_progress->released, __ATOMIC_ACQUIRE);
+    E->ring_dirty = released < out.produced;
     if (overflow || stalled) {
         memset(E->h_items, 0xFF, E->qcap * sizeof(uint4));
         E->ring_dirty = false;

@@ -185,9 +185,11 @@ void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const 
                       uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s);
 void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,
                    hipStream_t s);
+// g_error of the selected probes is written as err_scale * ||q' - c'||: the lower bound's
+// error term f_error * g_error scaled at one place for every pass that forms a bound.
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,
                          uint32_t nprobe, uint32_t P, int metric, float *gadd, float *gerr,
-                         hipStream_t s);
+                         float err_scale, hipStream_t s);
 // max_units: capacity of units (nq * nprobe * unit_splits(largest cluster))
 void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint32_t nq,
                         uint32_t nprobe, uint32_t nlist, uint32_t vanguard, uint32_t batch_q,

@@ -1197,7 +1197,8 @@ __global__ __launch_bounds__(256) void probe_refine_kernel(const float *__restri
                                                            const int32_t *__restrict__ idx,
                                                            uint32_t nprobe, uint32_t P, int metric,
                                                            float *__restrict__ gadd,
-                                                           float *__restrict__ gerr) {
+                                                           float *__restrict__ gerr,
+                                                           float err_scale) {
     const uint32_t q = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t groups = P / 64;
@@ -1234,7 +1235,7 @@ __global__ __launch_bounds__(256) void probe_refine_kernel(const float *__restri
             const uint32_t p = p0 + 4 * h;
             if (lane == 0) {
                 gadd[(size_t)q * nprobe + p] = metric == 0 ? l2 : -ip;
-                gerr[(size_t)q * nprobe + p] = sqrtf(fmaxf(l2, 0.0f));
+                gerr[(size_t)q * nprobe + p] = err_scale * sqrtf(fmaxf(l2, 0.0f));
             }
         }
     }
@@ -1351,8 +1352,8 @@ void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
 
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,
                          uint32_t nprobe, uint32_t P, int metric, float *gadd, float *gerr,
-                         hipStream_t s) {
-    probe_refine_kernel<<<nq, 256, 0, s>>>(qrot, cent, idx, nprobe, P, metric, gadd, gerr);
+                         float err_scale, hipStream_t s) {
+    probe_refine_kernel<<<nq, 256, 0, s>>>(qrot, cent, idx, nprobe, P, metric, gadd, gerr, err_scale);
 }
 
 }  // namespace cora

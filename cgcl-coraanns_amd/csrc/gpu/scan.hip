@@ -661,10 +661,15 @@ __global__ __launch_bounds__(kThrThreads) void seed_threshold_kernel(
         const float thr = nextafterf(fmaxf(key_to_float(kth) + __uint_as_float(s_ekey),
                                            key_to_float(s_lkey)),
                                      FLT_MAX);
+        // atomic minimum: the CPU consumer may lower the same slot concurrently, and a
+        // threshold only ever falls
         uint32_t *slot = reinterpret_cast<uint32_t *>(thresholds) + qi;
-        const float cur = __uint_as_float(__hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM));
-        if (thr < cur)
-            __hip_atomic_store(slot, __float_as_uint(thr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        uint32_t cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        while (thr < __uint_as_float(cur)) {
+            if (__hip_atomic_compare_exchange_strong(slot, &cur, __float_as_uint(thr), __ATOMIC_RELAXED,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM))
+                break;
+        }
         s_thr = thr;
         atomicAdd(seeded, 1ull);
     }

@@ -113,6 +113,8 @@ int cora_hybrid_configure(cora_hybrid *h, const cora_hybrid_config *c) {
         x.set_gpu_seed_refine(c->gpu_seed_refine != 0);
         x.set_gpu_refine_filter(c->gpu_refine_filter != 0);
         x.set_extra_search_flags(c->extra_flags);
+        if (c->lower_bound_scale != 0.0f)
+            x.set_lower_bound_scale(c->lower_bound_scale);
     });
 }
 

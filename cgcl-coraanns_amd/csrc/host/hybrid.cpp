@@ -56,6 +56,12 @@ void HybridIndex::set_metric(int metric) {
     metric_ = metric;
 }
 
+void HybridIndex::set_lower_bound_scale(float scale) {
+    if (!(scale > 0.0f && scale <= max_bound_scale))
+        throw std::invalid_argument("lower-bound scale must be in (0, 16]");
+    bound_scale_ = scale;
+}
+
 void HybridIndex::set_vanguard_size(std::size_t size) {
     if (workspace_ready_ && std::min(size, ws_max_nprobe_) > ws_vanguard_)
         throw std::logic_error("prepare workspace again before increasing vanguard size");
@@ -188,6 +194,7 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
                  (cross_query_reuse_enabled_ ? uint32_t{CORA_FLAG_CROSS_QUERY_REUSE} : 0u) |
                  (gpu_seed_refine_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_SEED}) |
                  (gpu_refine_filter_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_PREFILTER}) | extra_flags_;
+    args.bound_scale = bound_scale_;
     last_gpu_filter_ms_ = 0.0f;
     check(engine_, cora_gpu_launch_search(engine_, &args));
 

@@ -268,8 +268,10 @@ RefineOut cpu_refine(const RefineArgs &a, std::size_t nq, std::size_t topk, floa
                     break;
                 ++consumed;
                 const std::size_t q = rec.query_idx;
-                if (q >= nq)
-                    continue;  // defensive: never produced by the engine
+                // defensive: the engine produces none of these; a record outside the
+                // search's shape would index past the probe and code arrays
+                if (q >= nq || rec.probe_idx >= a.nprobe || rec.gid >= a.num_vectors)
+                    continue;
                 if (a.secondary_filter && rec.low_dist >= load_threshold(a.thresholds, q))
                     continue;
                 float dist;

@@ -99,6 +99,12 @@ typedef struct cora_search_args {
     uint32_t batch_q;  /* 1..8 same-cluster pairs per scan pass (reference accepts 1..6) */
     uint32_t vanguard; /* vanguard depth: pairs with probe rank < vanguard are scanned first */
     uint32_t flags;    /* cora_search_flags */
+    /* Multiplier of the lower bound's error term: low = est - bound_scale * f_error * g_error.
+     * 1 (or 0) is the reference Bitwise producer's bound (filter_kernels.cuh:111-114);
+     * above 1 the filter keeps the vectors whose 1-bit estimate errs beyond the bound's
+     * confidence, which the reference CPU path's running threshold happens to keep
+     * (no counterpart in the reference's GPU interface). Range 0..16. */
+    float bound_scale;
 } cora_search_args;
 
 typedef struct cora_search_stats {

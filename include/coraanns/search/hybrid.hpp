@@ -103,6 +103,14 @@ class HybridIndex {
     // Extra cora_search_flags ORed into every launch (test modes such as
     // CORA_FLAG_GPU_SEED_FROZEN).
     void set_extra_search_flags(uint32_t flags) { extra_flags_ = flags; }
+    // Multiplier of the filter's error term, low = est - scale * f_error * g_error
+    // (cora_search_args.bound_scale). 1 is the reference Bitwise producer's bound
+    // (filter_kernels.cuh:111-114) and gives its candidate sets; the default
+    // default_bound_scale widens it so that the vectors whose 1-bit estimate errs beyond
+    // the bound's confidence are still refined, which the reference CPU path's running
+    // threshold does for the vectors it scans early (ivf.hpp:802-817). Range (0, 16].
+    void set_lower_bound_scale(float scale);
+    float get_lower_bound_scale() const { return bound_scale_; }
     bool get_gpu_seed_refine() const { return gpu_seed_refine_; }
     // CPU refinement threads; 0 = omp_get_max_threads() (the reference always uses the
     // caller's OpenMP setting, cpu_refinement.cpp:110).
@@ -152,6 +160,7 @@ class HybridIndex {
     bool gpu_seed_refine_ = true;
     bool gpu_refine_filter_ = true;
     uint32_t extra_flags_ = 0;
+    float bound_scale_ = default_bound_scale;
     int cpu_threads_ = 0;
     std::size_t vanguard_size_ = default_vanguard_size;
     KernelType ip_kernel_type_ = KernelType::Lut4Bit;

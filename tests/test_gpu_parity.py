@@ -48,10 +48,14 @@ class Case:
         self.ivf = ca.IvfIndex(path)
 
 
-def make_engine(case, nprobe, topk, vanguard=0, frozen=True, secondary=False, reuse=True, **kw):
+def make_engine(case, nprobe, topk, vanguard=0, frozen=True, secondary=False, reuse=True,
+                lower_bound_scale=1.0, **kw):
+    """lower_bound_scale 1.0: the reference Bitwise producer's bound, whose candidate sets
+    the oracle restates."""
     eng = ca.HybridIndex(0, vanguard_size=vanguard, frozen_thresholds=frozen,
                          cpu_secondary_filter=secondary, cross_query_reuse=reuse,
-                         metric=case.file.metric, gpu_filter_timing=True, **kw)
+                         metric=case.file.metric, gpu_filter_timing=True,
+                         lower_bound_scale=lower_bound_scale, **kw)
     eng.load_ivf(case.ivf)
     eng.prepare_workspace(case.queries.shape[0], topk, nprobe)
     return eng
@@ -714,6 +718,71 @@ def test_topk_and_recall_match_reference_cpu_path(case_name, request, tmp_path):
         say(f"[gpu]   nprobe={nprobe}: id agreement {agree:.4f}, recall gpu {r_gpu:.4f} ref {r_ref:.4f}")
         assert agree >= 0.98, (nprobe, agree)
         assert abs(r_gpu - r_ref) <= 0.01, (nprobe, r_gpu, r_ref)
+
+
+def _mixture_index(tmp_path, n, dim, n_centers, nlist, nq, metric, sd, seed):
+    """A Gaussian-mixture index of the benchmark configurations' kind, built here (GPU
+    k-means and assignment, host RaBitQ builder) with exact ground truth."""
+    from coraanns_amd import workloads as wl
+
+    rng = np.random.default_rng(seed)
+    centers = rng.normal(0, 1, (n_centers, dim)).astype(np.float32)
+
+    def draw(m):
+        x = centers[rng.integers(0, n_centers, m)] + rng.normal(0, sd, (m, dim)).astype(np.float32)
+        if metric == 1:
+            x /= np.linalg.norm(x, axis=1, keepdims=True)
+        return np.ascontiguousarray(x, np.float32)
+
+    x, q = draw(n), draw(nq)
+    sample = x[rng.choice(n, min(n, 256 * nlist), replace=False)]
+    cent = ca.gpu_kmeans(sample, nlist, 20, seed)
+    assign = ca.gpu_assign(x, cent)
+    R = wl.rotation(dim, (dim + 63) // 64 * 64, seed + 1)
+    path = tmp_path / "mix.index"
+    ca.build_ivf(path, ca.gpu_rotate(x, R), (cent.astype(np.float64) @ R.astype(np.float64)).astype(np.float32),
+                 assign, R, metric=metric)
+    gt = wl.ground_truth(x, q, 10, metric)
+    return path, q, gt
+
+
+@pytest.mark.skipif(not REF_DUMP.exists(), reason="oracle/_ref/ref_dump not built (needs /root/reference)")
+@pytest.mark.parametrize("n,dim,n_centers,nlist,nq,metric,sd", [
+    (200_000, 128, 256, 256, 2000, 0, 0.3),   # config 2's kind (1M x 128 L2) at a fifth of its size
+    (100_000, 768, 512, 128, 1000, 1, 0.5),   # config 4's kind (20M x 768 IP, unit norm)
+])
+def test_recall_at_least_reference_cpu_path(n, dim, n_centers, nlist, nq, metric, sd, tmp_path):
+    """Production mode (live thresholds, vanguard 5, secondary filter, the default lower-bound
+    scale): recall@10 at least the reference CPU search's (rabitqlib IVF::search, FastScan
+    hacc, ivf.hpp:670-732, run by ref_dump from the reference sources) minus 0.001, at every
+    nprobe, on the same index file and queries. With the reference Bitwise bound (scale 1)
+    the GPU filter tests every vector against a nearly final threshold, where the CPU
+    search tests early vectors against a looser running one, and recall trails by ~0.004."""
+    from coraanns_amd.workloads import write_fbin
+
+    say(f"[gpu] recall vs reference CPU path, {n} x {dim} {'IP' if metric else 'L2'}, nlist {nlist}")
+    path, q, gt = _mixture_index(tmp_path, n, dim, n_centers, nlist, nq, metric, sd, 11 + dim)
+    nprobes, topk = [4, 8, 16], 10
+    qf = tmp_path / "q.fbin"
+    write_fbin(qf, q)
+    out = tmp_path / "ref"
+    out.mkdir()
+    subprocess.run([str(REF_DUMP), "index", str(path), str(qf), str(out), str(topk)] +
+                   [str(v) for v in nprobes], check=True, capture_output=True, timeout=600)
+    ref_ids = np.fromfile(out / "search_ids.bin", np.uint32).reshape(len(nprobes), -1, topk)
+    ivf = ca.IvfIndex(path)
+    eng = ca.HybridIndex(0, vanguard_size=5, cpu_secondary_filter=True, metric=metric)
+    eng.load_ivf(ivf)
+    eng.prepare_workspace(nq, topk, max(nprobes))
+    for li, nprobe in enumerate(nprobes):
+        eng.reset_buffer(q)
+        _, ids = eng.search(q, topk, nprobe)
+        r_gpu = orc.recall_at_k(ids, gt, topk)
+        r_ref = orc.recall_at_k(ref_ids[li], gt, topk)
+        agree = np.mean([len(set(a) & set(b)) / topk for a, b in zip(ids.tolist(), ref_ids[li].tolist())])
+        say(f"[gpu]   nprobe={nprobe}: recall gpu {r_gpu:.4f} ref {r_ref:.4f}, id agreement {agree:.4f}")
+        assert r_gpu >= r_ref - 0.001, (nprobe, r_gpu, r_ref)
+    eng.close()
 
 
 @pytest.mark.parametrize("dim,metric", [(128, 0), (768, 1)])

@@ -237,3 +237,22 @@ def test_lifecycle_and_shape_errors():
             e.reset_buffer(q)
         e.set_vanguard_size(1 if it == 0 else 0)
         e.prepare_workspace(nq, 10, 1)
+
+
+def test_unconsumed_ring_is_cleared_before_the_next_search(allpass):
+    """A search whose records the CPU never consumed (the host stopped after the GPU side
+    finished) leaves complete records in the ring. The next reset must clear them: else
+    the next consumer takes them for its own search's records at the same positions."""
+    say("[gpu] unconsumed ring, then a full search")
+    e = allpass.engine(262144, 262144, 0)
+    gpu, lib = e.gpu, ca._load()[0]
+    e.reset_buffer(allpass.query)
+    # GPU side only: 2 of the 8 clusters per query (positions the next search reuses)
+    flags = ca.FLAG_CROSS_QUERY_REUSE | ca.FLAG_NO_GPU_SEED | ca.FLAG_NO_GPU_PREFILTER
+    args = ca.cora_search_args(allpass.queries, allpass.k, 2, 4, 0, flags, 1.0)
+    ca._gpu_check(gpu, lib.cora_gpu_launch_search(gpu, ca.C.byref(args)))
+    st = ca.cora_search_stats()
+    ca._gpu_check(gpu, lib.cora_gpu_sync(gpu, ca.C.byref(st)))
+    assert st.produced == allpass.queries * 2 * (allpass.count // allpass.clusters)
+    for _ in range(2):
+        allpass.check(e, allpass.queries, 4)
