@@ -133,6 +133,11 @@ def main():
     ap.add_argument("--no-gpu-seed", action="store_true",
                     help="CPU-only thresholds (the reference's behaviour), no GPU seed thresholds")
     ap.add_argument("--no-gpu-prefilter", action="store_true", help="no GPU refined pre-filter")
+    ap.add_argument("--lower-bound-scale", type=float, default=0.0,
+                    help="multiplier of the filter's error term (0: the engine's default; 1: the "
+                         "reference Bitwise producer's bound)")
+    ap.add_argument("--no-vanguard-mfma", action="store_true",
+                    help="vanguard lower bounds inside the per-query pass instead of the matrix-core lows pass")
     ap.add_argument("--fp32-gemm", action="store_true",
                     help="query rotation and coarse-probe distances from the FP32 matrix-core GEMMs instead of the split-FP16 ones")
     ap.add_argument("--workdir", default="",
@@ -187,7 +192,9 @@ def main():
                          cross_query_reuse=True, gpu_filter_timing=True, metric=c.metric,
                          cpu_threads=threads, gpu_seed_refine=not args.no_gpu_seed,
                          gpu_refine_filter=not args.no_gpu_prefilter,
-                         extra_flags=ca.FLAG_FP32_GEMM if args.fp32_gemm else 0)
+                         extra_flags=(ca.FLAG_FP32_GEMM if args.fp32_gemm else 0) |
+                                     (ca.FLAG_NO_VANGUARD_MFMA if args.no_vanguard_mfma else 0),
+                         lower_bound_scale=args.lower_bound_scale or None)
     eng.load_ivf(ivf)
     chunk = min(queries.shape[0], 65535)
     eng.prepare_workspace(chunk, c.topk, max(c.nprobes))
@@ -233,7 +240,7 @@ def main():
         step(nprobe)
     times, times_search, scan_ms, scan_bytes, recalls, probe_ms, probe_flops = [], [], [], [], [], [], []
     recalls_k = []
-    van_ms, van_bytes = [], []
+    van_ms, van_bytes, lows_ms, lows_bytes = [], [], [], []
     last_ids = None
     for _ in range(args.steps):
         dt, ids, st = step(nprobe)
@@ -246,6 +253,8 @@ def main():
         scan_bytes.append(st["scan_bytes"])
         van_ms.append(st["vanguard_ms"])
         van_bytes.append(st["vanguard_bytes"])
+        lows_ms.append(st["vanguard_lows_ms"])
+        lows_bytes.append(st["vanguard_lows_bytes"])
         recalls.append(recall_at_k(ids, gt, 10))
         recalls_k.append(recall_at_k(ids, gt, c.topk))
     total = sum(times)
@@ -257,6 +266,9 @@ def main():
     avg_van_ms = float(np.mean(van_ms))
     van_bpl = float(np.mean(van_bytes))
     van_achieved = van_bpl / (avg_van_ms * 1e-3) / 1e9 if avg_van_ms > 0 else 0.0
+    avg_lows_ms = float(np.mean(lows_ms))
+    lows_bpl = float(np.mean(lows_bytes))
+    lows_achieved = lows_bpl / (avg_lows_ms * 1e-3) / 1e9 if avg_lows_ms > 0 else 0.0
     avg_probe_ms = float(np.mean(probe_ms))
     probe_tflops = float(np.mean(probe_flops)) / (avg_probe_ms * 1e-3) / 1e12 if avg_probe_ms > 0 else 0.0
     if args.fp32_gemm:
@@ -275,6 +287,7 @@ def main():
                       "frac": round(3 * probe_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
                       "fp32_equivalent_tflops": round(probe_tflops, 3)}
     log(f"[timed] nprobe={nprobe} steps={args.steps} QPS={qps:.1f} recall={np.mean(recalls):.4f} "
+        f"vanguard lows={avg_lows_ms:.3f}ms {lows_bpl / 1e6:.1f}MB -> {lows_achieved:.1f} GB/s; "
         f"vanguard={avg_van_ms:.3f}ms {van_bpl / 1e6:.1f}MB -> {van_achieved:.1f} GB/s; "
         f"far scan={avg_scan_ms:.3f}ms {bytes_per_launch / 1e6:.1f}MB -> {achieved:.1f} GB/s; "
         f"probe GEMM {avg_probe_ms:.3f}ms -> {probe_tflops:.2f} TFLOP/s")
@@ -285,11 +298,17 @@ def main():
     far_name = (f"far_mfma_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA ip_int/ip_res" if W <= 8 else
                 f"far_mfma_wide_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA 16x16x64 ip_int, popcount "
                 "ip_res for survivors")
+    lows_name = (f"far_mfma_kernel<{W}, 2>" if W <= 8 else f"far_mfma_wide_kernel<{W}, 2>")
     kernels = {
         "vanguard_query_kernel": {
-            "kernel": f"vanguard_query_kernel<{W}> (fused per-query vanguard pass: popcount lower bounds, "
+            "kernel": f"vanguard_query_kernel<{W}, {'true' if avg_lows_ms > 0 else 'false'}> (fused per-query "
+                      f"vanguard pass: {'streamed lower bounds' if avg_lows_ms > 0 else 'popcount lower bounds'}, "
                       "GPU refinement, top-k threshold)",
             "avg_launch_ms": round(avg_van_ms, 4), "bytes_per_launch": int(van_bpl), "achieved": van_achieved},
+        "vanguard_lows": {
+            "kernel": f"{lows_name} (vanguard lower bounds on the matrix cores, cluster-major, units of 16 "
+                      "same-cluster pairs)",
+            "avg_launch_ms": round(avg_lows_ms, 4), "bytes_per_launch": int(lows_bpl), "achieved": lows_achieved},
         "far_mfma_kernel" if mfma_far else "scan_kernel": {
             "kernel": f"{far_name}, units of 16 same-cluster pairs)" if mfma_far else
                       f"scan_kernel<{W}, {8 if batch_q > 1 else 1}, 0> (far-pair RaBitQ popcount scan)",
@@ -334,6 +353,7 @@ def main():
                    "qps_search_only": round(queries.shape[0] * args.steps / sum(times_search), 1),
                    "step_ms": [round(1000.0 * t, 3) for t in times],
                    "batch_q": batch_q, "vanguard": vanguard, "cpu_secondary_filter": c.secondary_filter,
+                   "lower_bound_scale": eng.lower_bound_scale,
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
                    "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
                    "query_chunk": chunk, "sweep": sweep},

@@ -37,11 +37,13 @@ FLAG_CROSS_QUERY_REUSE = 4
 
 DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range(5)
 DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
-DBG_SEED_DIST, DBG_THRESHOLDS, DBG_PROBE_DIST = 10, 11, 12
+DBG_SEED_DIST, DBG_THRESHOLDS, DBG_PROBE_DIST, DBG_VANGUARD_LOWS = 10, 11, 12, 13
 FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
 FLAG_PAIR_SEEDS = 1 << 6
 FLAG_NO_MFMA_SCAN = 1 << 7
 FLAG_FP32_GEMM = 1 << 8
+FLAG_NO_VANGUARD_MFMA = 1 << 9
+FLAG_VANGUARD_MFMA = 1 << 10
 
 
 class EngineUnavailable(RuntimeError):
@@ -83,7 +85,8 @@ class cora_search_stats(C.Structure):
                 ("scan_vectors", C.c_uint64), ("probe_ms", C.c_float), ("probe_flops", C.c_uint64),
                 ("pass_produced", C.c_uint64 * 3), ("seeded_queries", C.c_uint64),
                 ("prefilter_dropped", C.c_uint64), ("seed_ms", C.c_float), ("recovery_ms", C.c_float),
-                ("gpu_refined", C.c_uint64), ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64)]
+                ("gpu_refined", C.c_uint64), ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64),
+                ("vanguard_lows_ms", C.c_float), ("vanguard_lows_bytes", C.c_uint64)]
 
 
 class cora_queue_view(C.Structure):
@@ -108,7 +111,8 @@ class cora_hybrid_stats(C.Structure):
                 ("probe_flops", C.c_uint64), ("pass_produced", C.c_uint64 * 3),
                 ("seeded_queries", C.c_uint64), ("prefilter_dropped", C.c_uint64),
                 ("seed_ms", C.c_float), ("recovery_ms", C.c_float), ("gpu_refined", C.c_uint64),
-                ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64)]
+                ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64),
+                ("vanguard_lows_ms", C.c_float), ("vanguard_lows_bytes", C.c_uint64)]
 
 
 class cora_ivf_info(C.Structure):
@@ -178,6 +182,7 @@ HOST_SIGNATURES = {
     "cora_hybrid_seed_thresholds": [_P, _P, _U64],
     "cora_hybrid_set_vanguard_size": [_P, _U64],
     "cora_hybrid_gpu": [_P],
+    "cora_hybrid_lower_bound_scale": [_P],
     "cora_ivf_load": [C.c_char_p, _I, C.POINTER(C.c_void_p)],
     "cora_ivf_info_get": [_P, C.POINTER(cora_ivf_info)],
     "cora_ivf_arrays_get": [_P, C.POINTER(cora_ivf_arrays)],
@@ -212,6 +217,7 @@ def _load():
     host.cora_host_last_error.restype = C.c_char_p
     gpu.cora_tool_last_error.restype = C.c_char_p
     host.cora_hybrid_gpu.restype = C.c_void_p
+    host.cora_hybrid_lower_bound_scale.restype = C.c_float
     _gpu, _host = gpu, host
     return gpu, host
 
@@ -390,6 +396,10 @@ class HybridIndex:
     def seed_thresholds(self, thr):
         t = np.ascontiguousarray(thr, np.float32)
         _host_check(_load()[1].cora_hybrid_seed_thresholds(self._h, _ptr(t), t.shape[0]))
+
+    @property
+    def lower_bound_scale(self):
+        return float(_load()[1].cora_hybrid_lower_bound_scale(self._h))
 
     @property
     def gpu(self):

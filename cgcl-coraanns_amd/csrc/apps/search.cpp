@@ -44,7 +44,7 @@ void print_usage(const char *program) {
                  " [--cross-query-reuse true] [--candidate-stats false]"
                  " [--gpu-filter-timing false] [--profile false]"
                  " [--exact-base FILE] [--recall-base FILE] [--recall-once false]"
-                 " [--lower-bound-scale 1.5]\n";
+                 " [--lower-bound-scale 1.3]\n";
 }
 
 class Options {
@@ -371,16 +371,22 @@ int main(int argc, char **argv) {
                                       std::chrono::steady_clock::now() - t0).count();
                 const double v = nq / (us / 1e6);
                 qps[l] += v / rounds;
-                std::cout << "[Run] round=" << (r + 1) << " nprobe=" << np << " QPS=" << v;
+                // recall first (its [RecallEval] line precedes the [Run] line, as in the
+                // reference driver, apps/search.cpp:256-271)
+                double rr = 0.0;
                 if (recall_once) {
                     if (r == 0)
                         saved[l] = result;
-                    std::cout << " recall=deferred\n";
                 } else {
-                    const double rr = evaluator->evaluate(result.data(), result.size());
+                    rr = evaluator->evaluate(result.data(), result.size());
                     rec[l] += rr / rounds;
-                    std::cout << " recall=" << rr << '\n';
                 }
+                std::cout << "[Run] round=" << (r + 1) << " nprobe=" << np << " QPS=" << v;
+                if (recall_once)
+                    std::cout << " recall=deferred\n";
+                else
+                    std::cout << " recall=" << rr << '\n';
+                std::cout.flush();
                 std::printf("[QueueStats] round=%zu nprobe=%zu submitted=%llu spilled=%llu wraps=%llu\n",
                             r + 1, np, (unsigned long long)s.submitted, (unsigned long long)s.spilled,
                             (unsigned long long)s.wraps);

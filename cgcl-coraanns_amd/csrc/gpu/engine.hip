@@ -43,7 +43,7 @@ struct cora_gpu_engine {
     hipStream_t stream = nullptr, stream_d2h = nullptr;
     hipEvent_t ev_prep = nullptr, ev_probe = nullptr, ev_f0 = nullptr, ev_f1 = nullptr,
                ev_s0 = nullptr, ev_s1 = nullptr, ev_p0 = nullptr, ev_p1 = nullptr, ev_v0 = nullptr,
-               ev_v1 = nullptr;
+               ev_v1 = nullptr, ev_a0 = nullptr, ev_a1 = nullptr;
     // index
     bool loaded = false;
     uint64_t N = 0, dim = 0, P = 0, nl = 0, ex_bits = 0, max_cluster = 0, total_tiles = 0;
@@ -97,7 +97,7 @@ struct cora_gpu_engine {
     bool launched = false;
     cora_search_args last{};
     uint32_t last_depth = 0, last_batch = 1;
-    bool last_timing = false, last_fused = false, last_mfma = false;
+    bool last_timing = false, last_fused = false, last_mfma = false, last_van_lows = false;
 };
 
 namespace {
@@ -289,7 +289,7 @@ int cora_gpu_create(cora_gpu_engine **out, int device) {
         HIPCHK(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
         HIPCHK(hipStreamCreateWithFlags(&E->stream_d2h, hipStreamNonBlocking));
         for (hipEvent_t *ev : {&E->ev_prep, &E->ev_probe, &E->ev_f0, &E->ev_f1, &E->ev_s0, &E->ev_s1,
-                               &E->ev_p0, &E->ev_p1, &E->ev_v0, &E->ev_v1})
+                               &E->ev_p0, &E->ev_p1, &E->ev_v0, &E->ev_v1, &E->ev_a0, &E->ev_a1})
             HIPCHK(hipEventCreate(ev));
         return CORA_OK;
     };
@@ -321,7 +321,7 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
     dfree(E->d_excodes);
     dfree(E->d_exfac);
     for (hipEvent_t ev : {E->ev_prep, E->ev_probe, E->ev_f0, E->ev_f1, E->ev_s0, E->ev_s1, E->ev_p0,
-                          E->ev_p1, E->ev_v0, E->ev_v1})
+                          E->ev_p1, E->ev_v0, E->ev_v1, E->ev_a0, E->ev_a1})
         if (ev)
             (void)hipEventDestroy(ev);
     if (E->stream)
@@ -545,13 +545,14 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_uoff, nb + 1));
         TRY(dalloc(E, E->d_nunits, 2));
         TRY(dalloc(E, E->d_cursor, kNumXcd));
-        TRY(dalloc(E, E->d_stats, 10));
+        TRY(dalloc(E, E->d_stats, 11));
         TRY(dalloc(E, E->d_pairs, np));
         TRY(dalloc(E, E->d_units, np * unit_splits((uint32_t)E->max_cluster)));
         TRY(dalloc(E, E->d_thr_snap, max_q));
         TRY(dalloc(E, E->d_seed, std::max<uint64_t>(1, max_q * depth * seed_words)));
         if (depth > 0) {
-            E->van_stride = (E->max_cluster + kTileVectors - 1) / kTileVectors * kTileVectors;
+            // a multiple of 256: the fused pass streams a pair's bounds 256 at a time
+            E->van_stride = (E->max_cluster + 255) / 256 * 256;
             TRY(dalloc(E, E->d_van_lows, max_q * depth * std::max<uint64_t>(E->van_stride, 1)));
         }
         if (E->d_excodes) {
@@ -726,22 +727,35 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_probe, 0));
     HIPCHK(hipMemcpyAsync(E->h_gadd, E->d_gadd, (size_t)nq * np * 4, hipMemcpyDeviceToHost,
                           E->stream_d2h));
-    // pair scheduling (hybrid.cu:504-508)
-    launch_build_pairs(E->d_pidx, E->d_meta, nq, np, (uint32_t)E->nl, depth, batch,
-                       P / 8 + 12, E->d_bcount, E->d_bcursor, E->d_boff, E->d_uoff, E->d_pairs,
-                       E->d_units, (uint64_t)nq * np * unit_splits((uint32_t)E->max_cluster),
-                       E->d_nunits, E->d_stats, s);
-    if (frozen) {
-        memcpy(E->h_thr_stage, E->h_thr, (size_t)nq * 4);
-        HIPCHK(hipMemcpyAsync(E->d_thr_snap, E->h_thr_stage, (size_t)nq * 4, hipMemcpyHostToDevice, s));
-    }
-    ScanParams p = scan_params(E, depth, keep, frozen);
     // GPU ex-code stages (seed thresholds, refined pre-filter): live thresholds only, or
     // the frozen snapshot in the GPU_SEED_FROZEN test mode
     const bool ex_stage_mode = !frozen || (a->flags & CORA_FLAG_GPU_SEED_FROZEN);
     const bool gpu_seed = depth > 0 && E->d_excodes && E->d_seed_dist && ex_stage_mode &&
                           !(a->flags & CORA_FLAG_NO_GPU_SEED);
     const bool prefilter = E->d_excodes && ex_stage_mode && !(a->flags & CORA_FLAG_NO_GPU_PREFILTER);
+    // fused per-query vanguard pass (vanguard.hip) unless the reference's per-pair passes
+    // are asked for or the shape exceeds its limits
+    const bool fused = gpu_seed && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
+                       a->topk <= kVanguardMaxTopk;
+    // its lower bounds first on the matrix cores, cluster-major, into the per-pair lows
+    // array [nq][depth][van_stride] of the workspace
+    // (by default only when the sign codes and factors exceed the last-level cache: a
+    // cache-resident index is re-read cheaply by each query's own pass)
+    const bool lows_by_size = (uint64_t)E->N * (E->P / 8 + 12) > kLowsMinIndexBytes;
+    const bool van_lows = fused && depth > 0 && far_mfma_supported(E->W) && E->d_van_lows &&
+                          !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA) &&
+                          (lows_by_size || (a->flags & CORA_FLAG_VANGUARD_MFMA));
+    // pair scheduling (hybrid.cu:504-508)
+    launch_build_pairs(E->d_pidx, E->d_meta, nq, np, (uint32_t)E->nl, depth, batch,
+                       van_lows ? kMfmaBatchQ : 1u, P / 8 + 12, E->d_bcount, E->d_bcursor, E->d_boff,
+                       E->d_uoff, E->d_pairs, E->d_units,
+                       (uint64_t)nq * np * unit_splits((uint32_t)E->max_cluster), E->d_nunits, E->d_stats,
+                       s);
+    if (frozen) {
+        memcpy(E->h_thr_stage, E->h_thr, (size_t)nq * 4);
+        HIPCHK(hipMemcpyAsync(E->d_thr_snap, E->h_thr_stage, (size_t)nq * 4, hipMemcpyHostToDevice, s));
+    }
+    ScanParams p = scan_params(E, depth, keep, frozen);
     if (gpu_seed || prefilter) {
         p.ex_codes = E->d_excodes;
         p.ex_factors = E->d_exfac;
@@ -756,12 +770,9 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     }
     p.prefilter = prefilter ? 1 : 0;
     p.dropped = E->d_stats + 7;
-    // fused per-query vanguard pass (vanguard.hip) unless the reference's per-pair passes
-    // are asked for or the shape exceeds its limits
-    const bool fused = gpu_seed && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
-                       a->topk <= kVanguardMaxTopk;
     VanguardArgs va{};
     E->last_fused = fused && depth > 0;
+    E->last_van_lows = van_lows;
     if (fused) {
         va.probe_idx = E->d_pidx;
         va.nq = nq;
@@ -772,6 +783,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         va.thr_out = frozen ? E->d_thr_snap : E->h_thr;
         va.seeded = E->d_stats + 6;
         va.refined = E->d_stats + 8;
+        va.lows_ready = van_lows ? 1 : 0;
     }
     launch_fill_u64(E->d_stats + 3, 0ull, 6, s);  // per-pass counters of this launch
     if (timing)
@@ -782,6 +794,14 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
             launch_snapshot_thresholds(E->h_thr, E->d_thr_snap, nq, s);
     };
     if (depth > 0 && fused) {
+        if (van_lows) {
+            launch_cursor_init(E->d_cursor, E->d_nunits, 0, s);
+            if (timing)
+                HIPCHK(hipEventRecord(E->ev_a0, s));
+            launch_vanguard_lows(p, E->W, s);
+            if (timing)
+                HIPCHK(hipEventRecord(E->ev_a1, s));
+        }
         snapshot();
         if (timing)
             HIPCHK(hipEventRecord(E->ev_v0, s));
@@ -852,7 +872,7 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     HIPCHK(hipSetDevice(E->device));
     HIPCHK(hipStreamSynchronize(E->stream));
     HIPCHK(hipStreamSynchronize(E->stream_d2h));
-    unsigned long long stats[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    unsigned long long stats[11] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     int stalled = 0;
     HIPCHK(hipMemcpy(stats, E->d_stats, sizeof(stats), hipMemcpyDeviceToHost));
     HIPCHK(hipMemcpy(&stalled, E->d_stalled, sizeof(int), hipMemcpyDeviceToHost));
@@ -871,8 +891,15 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     out.seeded_queries = stats[6];
     out.prefilter_dropped = stats[7];
     out.gpu_refined = stats[8];
-    if (E->last_fused)  // code + factors of every vanguard vector, then P/8 + 7P/8 + 8 per refined one
+    // the per-query pass: code + factors of every vanguard vector (or its 4-byte lower bound
+    // when the lows pass ran), then P/8 + 7P/8 + 8 per refined one; the lows pass: code +
+    // factors of the cluster once per unit
+    if (E->last_fused && E->last_van_lows) {
+        out.vanguard_bytes = 4 * stats[10] + stats[8] * (E->P + 8);
+        out.vanguard_lows_bytes = stats[9];
+    } else if (E->last_fused) {
         out.vanguard_bytes = stats[9] + stats[8] * (E->P + 8);
+    }
     if (E->last_timing) {
         HIPCHK(hipEventElapsedTime(&out.filter_ms, E->ev_f0, E->ev_f1));
         HIPCHK(hipEventElapsedTime(&out.scan_ms, E->ev_s0, E->ev_s1));
@@ -883,6 +910,8 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
             out.recovery_ms = 0.0f;  // no recovery pass
             HIPCHK(hipEventElapsedTime(&out.vanguard_ms, E->ev_v0, E->ev_v1));
         }
+        if (E->last_fused && E->last_van_lows)
+            HIPCHK(hipEventElapsedTime(&out.vanguard_lows_ms, E->ev_a0, E->ev_a1));
     }
     if (st)
         *st = out;
@@ -971,6 +1000,12 @@ int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes
         size = nq * E->last_depth * keep * 4;
         break;
     }
+    case CORA_DBG_VANGUARD_LOWS:
+        if (!E->last_van_lows)
+            return fail(E, CORA_ERR_LOGIC, "debug_read: the last search ran no vanguard lows pass");
+        src = E->d_van_lows;
+        size = nq * E->last_depth * E->van_stride * 4;
+        break;
     case CORA_DBG_THRESHOLDS: {
         if (bytes != nq * 4)
             return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_read: size mismatch");
@@ -1037,7 +1072,10 @@ int cora_gpu_debug_dense(cora_gpu_engine *E, int32_t *out_ip, int32_t *out_ip2, 
         for (uint32_t set = 0; set < 2 && r == hipSuccess; ++set) {
             // the kernel the search ran: the matrix-core far scan for the far units
             launch_cursor_init(E->d_cursor, E->d_nunits, set, E->stream);
-            if (set == 1 && E->last_mfma)
+            // the matrix-core kernel for the units it scanned in the search (far units with
+            // the matrix-core far scan; vanguard units, of up to 16 pairs, with the lows pass)
+            p.dbg_set = set;
+            if ((set == 1 && E->last_mfma) || (set == 0 && E->last_van_lows))
                 launch_far_mfma(p, E->W, true, E->stream);
             else
                 launch_scan_set(p, E->W, 2, set, E->stream);

@@ -24,6 +24,9 @@ constexpr int kSelectMaxProbe = 4096;       // top-nprobe select held in LDS
 constexpr uint32_t kNumXcd = 8;
 constexpr uint32_t kVanguardMaxPairs = 64;  // fused vanguard pass: vanguard depth limit
 constexpr uint32_t kVanguardMaxTopk = 128;  // fused vanguard pass: top-k limit
+// sign codes + factors beyond which the vanguard lows pass runs by default (MI355X's
+// 256 MB last-level cache)
+constexpr uint64_t kLowsMinIndexBytes = 256ull << 20;
 
 struct ClusterMeta {
     uint32_t start;      // first global (cluster-order) vector index
@@ -142,9 +145,12 @@ struct ScanParams {
     int32_t *dbg_ip2;            // residual inner product <b, qres>
     float *dbg_low;
     uint32_t dbg_stride;         // max cluster size
+    uint32_t dbg_set;            // matrix-core dense debug: unit set (0 = vanguard, 1 = far)
 };
 
 // Fused vanguard pass (vanguard.hip): one workgroup per query over its vanguard pairs.
+// With lows_ready the pass streams the lower bounds the matrix-core pass wrote to
+// ScanParams::van_lows instead of evaluating them from the tiles.
 struct VanguardArgs {
     const int32_t *probe_idx;      // [nq][nprobe] probed clusters, nearest first
     const uint32_t *order;         // [nq] queries by nearest cluster (nullptr: identity)
@@ -155,6 +161,7 @@ struct VanguardArgs {
                                    // frozen snapshot in the test mode)
     unsigned long long *seeded;    // queries whose threshold the pass lowered
     unsigned long long *refined;   // vectors refined on the GPU
+    int lows_ready;
 };
 
 // ---- launchers (each defined in the translation unit holding its kernel) ----
@@ -190,13 +197,15 @@ void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,
                          uint32_t nprobe, uint32_t P, int metric, float *gadd, float *gerr,
                          float err_scale, hipStream_t s);
-// max_units: capacity of units (nq * nprobe * unit_splits(largest cluster))
+// max_units: capacity of units (nq * nprobe * unit_splits(largest cluster)); van_batch:
+// pairs per vanguard unit (1, or kMfmaBatchQ for the vanguard lows pass)
 void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint32_t nq,
                         uint32_t nprobe, uint32_t nlist, uint32_t vanguard, uint32_t batch_q,
-                        uint32_t bytes_per_vector, uint32_t *bucket_count, uint32_t *bucket_cursor,
+                        uint32_t van_batch, uint32_t bytes_per_vector, uint32_t *bucket_count,
+                        uint32_t *bucket_cursor,
                         uint32_t *bucket_offset, uint32_t *unit_offset, Pair *pairs, Unit *units,
                         uint64_t max_units, uint32_t *num_units /*[2]: vanguard, far*/,
-                        unsigned long long *scan_stats /*[0..2], [9]*/, hipStream_t s);
+                        unsigned long long *scan_stats /*[0..2], [9], [10]*/, hipStream_t s);
 void launch_fill_u32(uint32_t *p, uint32_t value, size_t n, hipStream_t s);
 void launch_fill_u64(unsigned long long *p, unsigned long long value, size_t n, hipStream_t s);
 void launch_queue_reset(QueueDev q, hipStream_t s);
@@ -226,6 +235,12 @@ void launch_vanguard_query(const ScanParams &p, const VanguardArgs &va, uint32_t
 constexpr uint32_t kMfmaBatchQ = 16;
 bool far_mfma_supported(uint32_t W);
 void launch_far_mfma(const ScanParams &p, uint32_t W, bool dense, hipStream_t s);
+// The vanguard units (units of up to kMfmaBatchQ pairs, set 0) on the matrix cores: the lower
+// bound of every (vector, pair) to p.van_lows[(query * p.vanguard + probe) * p.van_stride + v]
+// (van_stride a multiple of 256).
+void launch_vanguard_lows(const ScanParams &p, uint32_t W, hipStream_t s);
+// mode: 0 = far units, publish; 1 = far units, dense debug output; 2 = vanguard lows
+void launch_mfma_units(const ScanParams &p, uint32_t W, int mode, hipStream_t s);
 // dev[0..n) = the host-coherent thresholds, read with system scope (the per-pass copy the
 // scan kernels read, so no unit waits on a host-memory round trip)
 void launch_snapshot_thresholds(const float *host, float *dev, uint32_t n, hipStream_t s);

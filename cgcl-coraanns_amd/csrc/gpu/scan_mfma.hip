@@ -16,6 +16,11 @@
 // vectors (16 m + ...) and columns are the unit's pair slots, so lane l evaluates pair slot
 // l % 16 for vectors 16 m + 4 (l / 16) + r.
 //
+// The same kernels also evaluate the vanguard pairs cluster-major (MfmaMode::kLows): every
+// (vector, pair) lower bound of the vanguard units is written to the per-pair lows array,
+// which the per-query vanguard pass (vanguard.hip) then streams instead of re-reading each
+// query's clusters on its own.
+//
 // Work distribution, thresholds, staging and publication follow the popcount far scan:
 // one wave per workgroup, persistent grid, per-XCD unit cursors, per-pass threshold
 // snapshot, survivors staged in LDS and flushed 64 at a time (refined pre-filter with the
@@ -33,6 +38,10 @@ namespace {
 
 typedef int32_t v4i32 __attribute__((ext_vector_type(4)));
 constexpr int kStage = 256;  // staged survivor records per wave
+
+// What a unit's lower bounds are used for: published below the cutoff (far pairs),
+// written with ip_int and ip_res to the debug arrays, or written to the vanguard lows.
+enum MfmaMode : int { kPublish = 0, kDenseDbg = 1, kLows = 2 };
 
 // Bits 0..7 of b as eight int8 0/1 values (bit e in byte e), the 64-bit MFMA operand.
 __device__ __forceinline__ long spread_byte(uint32_t b) {
@@ -105,10 +114,12 @@ __device__ void flush_records(const ScanParams &p, const QueueDev &q, uint32_t n
 }
 
 // W = P / 32 words per vector (W even, W <= 8: the unit's query operands stay in VGPRs).
-// kDense: write ip_int, ip_res and the lower bound of every (vector, pair) to the debug
+// kDenseDbg: write ip_int, ip_res and the lower bound of every (vector, pair) to the debug
 // arrays instead of publishing (the estimator parity test of the kernel the search runs).
-template <int W, bool kDense>
+// kLows: the vanguard units; every lower bound goes to van_lows, ip_res is not formed.
+template <int W, int kMode>
 __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
+    constexpr bool kDense = kMode != kPublish;
     static_assert(W % 2 == 0 && W >= 2 && W <= 8, "query operands in registers");
     constexpr int G = (W + 3) / 4;  // code word groups of a tile
     __shared__ uint4 s_rec[kDense ? 1 : kStage];
@@ -116,8 +127,11 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
     const uint32_t lane = threadIdx.x, col = lane & 15, quad = lane >> 4;
     const uint32_t P = 32u * W;
     const QueueDev q = p.queue;
-    const uint32_t U = p.num_units[1];
-    const uint32_t ubase = p.num_units[0];
+    // kLows runs over the vanguard unit set, kPublish over the far units, the dense debug
+    // output over either
+    const uint32_t set = kMode == kLows ? 0u : kMode == kPublish ? 1u : p.dbg_set;
+    const uint32_t U = p.num_units[set];
+    const uint32_t ubase = set ? p.num_units[0] : 0u;
     uint32_t range = blockIdx.x % kNumXcd, tries = 0;
     uint32_t staged = 0;
     unsigned long long limit =
@@ -151,7 +165,7 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
 #pragma unroll
             for (int kc = 0; kc < W; ++kc) {
                 bq[kc] = *reinterpret_cast<const long *>(qb + 32 * kc);
-                br[kc] = *reinterpret_cast<const long *>(qb + P + 32 * kc);
+                br[kc] = kMode == kLows ? 0 : *reinterpret_cast<const long *>(qb + P + 32 * kc);
             }
         } else {
 #pragma unroll
@@ -196,7 +210,8 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
                 for (int kc = 0; kc < W; ++kc) {
                     const long a = spread_byte((xw[m][kc] >> (8 * quad)) & 0xFFu);
                     acc[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq[kc], acc[m], 0, 0, 0);
-                    accr[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, br[kc], accr[m], 0, 0, 0);
+                    if constexpr (kMode != kLows)
+                        accr[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, br[kc], accr[m], 0, 0, 0);
                 }
             }
 #pragma unroll
@@ -204,6 +219,20 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
                 const float fav[4] = {fa[m].x, fa[m].y, fa[m].z, fa[m].w};
                 const float frv[4] = {fr[m].x, fr[m].y, fr[m].z, fr[m].w};
                 const float fev[4] = {fe[m].x, fe[m].y, fe[m].z, fe[m].w};
+                if constexpr (kMode == kLows) {
+                    // rows 16 m + 4 quad + r of the pair's tile-padded slice (lanes past the
+                    // cluster's end write values nobody reads)
+                    if (slot) {
+                        float lw[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            lw[r] = fav[r] + gadd + frv[r] * (width * (float)acc[m][r] + k1) - fev[r] * gerr;
+                        *reinterpret_cast<float4 *>(p.van_lows + ((size_t)query * p.vanguard + probe) * p.van_stride +
+                                                    t * kTileVectors + 16 * m + 4 * quad) =
+                            make_float4(lw[0], lw[1], lw[2], lw[3]);
+                    }
+                    continue;
+                }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t local = t * kTileVectors + 16 * m + 4 * quad + r;
@@ -308,8 +337,9 @@ constexpr int kStageWide = 384;  // wide kernel: flushed when a row block could 
 // (W/2 x 16 bytes) stay in VGPRs. Only the dimension pairing between the two operands
 // matters to the sum, so ip_int is exact. The lower bound uses the popcount kernels'
 // expression; ip_res is evaluated for survivors when they are published.
-template <int W, bool kDense>
+template <int W, int kMode>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void far_mfma_wide_kernel(const ScanParams p) {
+    constexpr bool kDense = kMode != kPublish;
     static_assert(W % 8 == 0 && W >= 16 && W <= 32, "lane-group word ranges of even length");
     constexpr int WQ = W / 4;  // code words per lane-group
     constexpr int S = W / 2;   // K-steps of 64 dimensions
@@ -319,8 +349,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
     __shared__ uint32_t s_loc[kDense ? 1 : kStageWide];
     const uint32_t lane = threadIdx.x, col = lane & 15, quad = lane >> 4;
     const QueueDev q = p.queue;
-    const uint32_t U = p.num_units[1];
-    const uint32_t ubase = p.num_units[0];
+    // kLows runs over the vanguard unit set, kPublish over the far units, the dense debug
+    // output over either
+    const uint32_t set = kMode == kLows ? 0u : kMode == kPublish ? 1u : p.dbg_set;
+    const uint32_t U = p.num_units[set];
+    const uint32_t ubase = set ? p.num_units[0] : 0u;
     uint32_t range = blockIdx.x % kNumXcd, tries = 0;
     uint32_t staged = 0;
     unsigned long long limit =
@@ -397,6 +430,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                 const float fav[4] = {fa.x, fa.y, fa.z, fa.w};
                 const float frv[4] = {fr.x, fr.y, fr.z, fr.w};
                 const float fev[4] = {fe.x, fe.y, fe.z, fe.w};
+                if constexpr (kMode == kLows) {
+                    // rows o + r of the pair's tile-padded slice (lanes past the cluster's
+                    // end write values nobody reads)
+                    if (slot) {
+                        float lw[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float ex = width * (float)acc[r];
+                            lw[r] = fav[r] + gadd + frv[r] * (ex + k1) - fev[r] * gerr;
+                        }
+                        *reinterpret_cast<float4 *>(p.van_lows + ((size_t)query * p.vanguard + probe) * p.van_stride +
+                                                    t * kTileVectors + o) = make_float4(lw[0], lw[1], lw[2], lw[3]);
+                    }
+                    continue;
+                }
                 if constexpr (!kDense) {
                     // a row block stages at most 4 x 64 records
                     if (staged + 4 * 64 > (uint32_t)kStageWide) {
@@ -464,15 +512,25 @@ uint32_t resident_grid_mfma(F kernel) {
     return grid;
 }
 
-template <int W, bool kDense>
+template <int W, int kMode>
 void launch_w(const ScanParams &p, hipStream_t s) {
     if constexpr (W <= 8) {
-        auto *k = far_mfma_kernel<W, kDense>;
+        auto *k = far_mfma_kernel<W, kMode>;
         k<<<resident_grid_mfma(k), 64, 0, s>>>(p);
     } else {
-        auto *k = far_mfma_wide_kernel<W, kDense>;
+        auto *k = far_mfma_wide_kernel<W, kMode>;
         k<<<resident_grid_mfma(k), 64, 0, s>>>(p);
     }
+}
+
+template <int W>
+void launch_mode(const ScanParams &p, int mode, hipStream_t s) {
+    if (mode == kLows)
+        launch_w<W, kLows>(p, s);
+    else if (mode == kDenseDbg)
+        launch_w<W, kDenseDbg>(p, s);
+    else
+        launch_w<W, kPublish>(p, s);
 }
 
 }  // namespace
@@ -482,14 +540,22 @@ bool far_mfma_supported(uint32_t W) {
 }
 
 void launch_far_mfma(const ScanParams &p, uint32_t W, bool dense, hipStream_t s) {
+    launch_mfma_units(p, W, dense ? kDenseDbg : kPublish, s);
+}
+
+void launch_vanguard_lows(const ScanParams &p, uint32_t W, hipStream_t s) {
+    launch_mfma_units(p, W, kLows, s);
+}
+
+void launch_mfma_units(const ScanParams &p, uint32_t W, int mode, hipStream_t s) {
     switch (W) {
-    case 2: dense ? launch_w<2, true>(p, s) : launch_w<2, false>(p, s); break;
-    case 4: dense ? launch_w<4, true>(p, s) : launch_w<4, false>(p, s); break;
-    case 6: dense ? launch_w<6, true>(p, s) : launch_w<6, false>(p, s); break;
-    case 8: dense ? launch_w<8, true>(p, s) : launch_w<8, false>(p, s); break;
-    case 16: dense ? launch_w<16, true>(p, s) : launch_w<16, false>(p, s); break;
-    case 24: dense ? launch_w<24, true>(p, s) : launch_w<24, false>(p, s); break;
-    case 32: dense ? launch_w<32, true>(p, s) : launch_w<32, false>(p, s); break;
+    case 2: launch_mode<2>(p, mode, s); break;
+    case 4: launch_mode<4>(p, mode, s); break;
+    case 6: launch_mode<6>(p, mode, s); break;
+    case 8: launch_mode<8>(p, mode, s); break;
+    case 16: launch_mode<16>(p, mode, s); break;
+    case 24: launch_mode<24>(p, mode, s); break;
+    case 32: launch_mode<32>(p, mode, s); break;
     default: break;
     }
 }

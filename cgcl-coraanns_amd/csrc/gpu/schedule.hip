@@ -3,7 +3,8 @@
 // (query_kernels.cuh:105-113, kernel_types.cuh:34-60, hybrid.cu:504-508). Here the
 // same grouping is a counting sort into 2*nlist buckets (bucket = cluster for vanguard
 // pairs, nlist + cluster for the rest) followed by cutting every bucket into scan
-// units of at most batch_q pairs (1 for vanguard buckets), each split further into
+// units of at most batch_q pairs (van_batch for vanguard buckets: 1 for the per-pair
+// passes, the matrix-core unit size for the vanguard lows pass), each split further into
 // ranges of at most kUnitTiles tiles of the cluster. Pair order inside a bucket is not
 // fixed; every pair's results are independent of it.
 #include "engine_internal.h"
@@ -98,18 +99,18 @@ constexpr int kScanThreads = 1024;
 // algorithmic traffic of the far-pair scan.
 __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
     const uint32_t *__restrict__ count, const ClusterMeta *__restrict__ meta, uint32_t nlist,
-    uint32_t batch_q, uint32_t bpv, uint32_t *__restrict__ bucket_offset,
+    uint32_t batch_q, uint32_t van_batch, uint32_t bpv, uint32_t *__restrict__ bucket_offset,
     uint32_t *__restrict__ unit_offset, uint32_t *__restrict__ num_units,
     unsigned long long *__restrict__ stats) {
     constexpr int kWaves = kScanThreads / 64;
-    // per-wave totals of the seven sums (inclusive scans run within each wave by shuffles)
-    __shared__ unsigned long long s_tot[7][kWaves];
+    // per-wave totals of the eight sums (inclusive scans run within each wave by shuffles)
+    __shared__ unsigned long long s_tot[8][kWaves];
     const uint32_t nb = 2 * nlist;
     const int t = threadIdx.x;
     const uint32_t chunk = (nb + kScanThreads - 1) / kScanThreads;
     const uint32_t b0 = min(nb, t * chunk), b1 = min(nb, b0 + chunk);
     uint32_t pairs = 0, units = 0, van_units = 0;
-    unsigned long long bytes = 0, fu = 0, vec = 0, vbytes = 0;
+    unsigned long long bytes = 0, fu = 0, vec = 0, vbytes = 0, vvec = 0;
     // the thread's buckets 16 at a time: their loads issued together (one round trip per
     // 16 buckets instead of one per bucket; this single workgroup is latency-bound)
     constexpr uint32_t kBatch = 16;
@@ -131,9 +132,11 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
             pairs += m;
             const uint32_t n = nv[j], sp = unit_splits(n);
             if (b < nlist) {
-                units += m * sp;
-                van_units += m * sp;
-                vbytes += (unsigned long long)m * n * bpv;  // vanguard pairs: one pass per pair
+                const uint32_t u = (m + van_batch - 1) / van_batch;
+                units += u * sp;
+                van_units += u * sp;
+                vbytes += (unsigned long long)u * n * bpv;  // one pass per vanguard unit
+                vvec += (unsigned long long)m * n;
             } else {
                 const uint32_t u = (m + batch_q - 1) / batch_q;
                 units += u * sp;
@@ -146,9 +149,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
     // inclusive scans over the block: within each wave by shuffles, then the totals of the
     // waves before (one barrier)
     const int lane = t & 63, wave = t >> 6;
-    unsigned long long v[7] = {pairs, units, van_units, bytes, fu, vec, vbytes};
+    unsigned long long v[8] = {pairs, units, van_units, bytes, fu, vec, vbytes, vvec};
 #pragma unroll
-    for (int a = 0; a < 7; ++a) {
+    for (int a = 0; a < 8; ++a) {
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const unsigned long long y = __shfl_up(v[a], o);
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
     }
     __syncthreads();
 #pragma unroll
-    for (int a = 0; a < 7; ++a)
+    for (int a = 0; a < 8; ++a)
         for (int w = 0; w < wave; ++w)
             v[a] += s_tot[a][w];
     uint32_t po = (uint32_t)v[0] - pairs, uo = (uint32_t)v[1] - units;
@@ -176,7 +179,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
             }
             po += m;
             const uint32_t sp = unit_splits(nv[j]);
-            uo += (b < nlist ? m : (m + batch_q - 1) / batch_q) * sp;
+            uo += (b < nlist ? (m + van_batch - 1) / van_batch : (m + batch_q - 1) / batch_q) * sp;
         }
     }
     if (t == kScanThreads - 1) {
@@ -188,6 +191,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
         stats[1] = v[4];
         stats[2] = v[5];
         stats[9] = v[6];
+        stats[10] = v[7];
     }
 }
 
@@ -209,7 +213,8 @@ __global__ void build_units_kernel(const uint32_t *__restrict__ bucket_offset,
                                    const uint32_t *__restrict__ unit_offset,
                                    const uint32_t *__restrict__ num_units,
                                    const ClusterMeta *__restrict__ meta, uint32_t nlist,
-                                   uint32_t batch_q, uint64_t max_units, Unit *__restrict__ units) {
+                                   uint32_t batch_q, uint32_t van_batch, uint64_t max_units,
+                                   Unit *__restrict__ units) {
     const uint64_t u64 = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x;
     if (u64 >= max_units || u64 >= (uint64_t)num_units[0] + num_units[1])
         return;
@@ -224,7 +229,7 @@ __global__ void build_units_kernel(const uint32_t *__restrict__ bucket_offset,
             hi = mid;
     }
     const uint32_t b = lo, c = b % nlist;
-    const uint32_t q = b < nlist ? 1u : batch_q;
+    const uint32_t q = b < nlist ? van_batch : batch_q;
     const uint32_t n = meta[c].n, sp = unit_splits(n), ntiles = (n + kTileVectors - 1) / kTileVectors;
     const uint32_t local = u - unit_offset[b];
     const uint32_t group = local / sp, split = local % sp;
@@ -251,7 +256,8 @@ void launch_fill_u64(unsigned long long *p, unsigned long long value, size_t n, 
 
 void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint32_t nq,
                         uint32_t nprobe, uint32_t nlist, uint32_t vanguard, uint32_t batch_q,
-                        uint32_t bytes_per_vector, uint32_t *bucket_count, uint32_t *bucket_cursor,
+                        uint32_t van_batch, uint32_t bytes_per_vector, uint32_t *bucket_count,
+                        uint32_t *bucket_cursor,
                         uint32_t *bucket_offset, uint32_t *unit_offset, Pair *pairs, Unit *units,
                         uint64_t max_units, uint32_t *num_units, unsigned long long *scan_stats,
                         hipStream_t s) {
@@ -276,7 +282,7 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
                                                                   bucket_count);
     else
         count_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard, bucket_count);
-    scan_buckets_kernel<<<1, kScanThreads, 0, s>>>(bucket_count, meta, nlist, batch_q,
+    scan_buckets_kernel<<<1, kScanThreads, 0, s>>>(bucket_count, meta, nlist, batch_q, van_batch,
                                                    bytes_per_vector, bucket_offset, unit_offset,
                                                    num_units, scan_stats);
     if (lds)
@@ -286,7 +292,7 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
         scatter_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard,
                                                   bucket_offset, bucket_cursor, pairs);
     build_units_kernel<<<(uint32_t)((max_units + 255) / 256), 256, 0, s>>>(
-        bucket_offset, unit_offset, num_units, meta, nlist, batch_q, max_units, units);
+        bucket_offset, unit_offset, num_units, meta, nlist, batch_q, van_batch, max_units, units);
 }
 
 }  // namespace cora

@@ -9,9 +9,12 @@
 // consumer from the refined distances. Here the whole query is handled in one place:
 //
 //   1. the four waves stream the tiles of the query's vanguard clusters (nearest first)
-//      and evaluate the Bitwise lower bound of the scan kernels (same expression); a
-//      vector whose bound is below the query's current threshold joins an LDS candidate
-//      list (lower bound, position), compacted per wave with a ballot;
+//      and evaluate the Bitwise lower bound of the scan kernels (same expression) — or,
+//      when the matrix-core pass has already written every vanguard lower bound
+//      cluster-major (launch_vanguard_lows: each cluster read once per unit of up to 16
+//      pairs instead of once per query), stream those 4-byte bounds; a vector whose bound
+//      is below the query's current threshold joins an LDS candidate list (lower bound,
+//      position), compacted per wave with a ballot;
 //   2. every 8 tiles per wave, once the list holds 1,024 entries (and at the end), the
 //      list is refined: while fewer than topk vectors are refined, the 128 smallest
 //      bounds first (radix select), then every remaining bound below the threshold, in
@@ -52,6 +55,12 @@ constexpr uint32_t kVqMaxW = 32;     // P <= 1024
 constexpr uint32_t kVqSegTiles = 8;  // tiles per wave between list checks
 constexpr uint32_t kVqHigh = 1024;   // list entries that trigger a refinement round
 constexpr uint32_t kVqList = kVqHigh + kVqWaves * kVqSegTiles * kTileVectors;  // list capacity
+// precomputed bounds: chunks of 256 (one 16-byte load per lane), two per wave per segment
+// (the same 512 list entries per wave and segment as kVqSegTiles tiles), the next
+// segment's two in flight meanwhile
+constexpr uint32_t kPreChunk = 256;
+constexpr uint32_t kPreSegChunks = 2;
+static_assert(kPreSegChunks * kPreChunk == kVqSegTiles * kTileVectors, "list capacity per segment");
 static_assert(kVqChunk * 2 == kVqThreads, "one chunk vector per two lanes");
 
 __device__ __forceinline__ float processed_mark() { return __uint_as_float(0x7FC00000u); }
@@ -258,9 +267,9 @@ __device__ __forceinline__ int popc_ip_scalar(const uint32_t (&x)[Words<W>::kMax
 }
 
 // P <= 128 and P >= 512: at most 168 VGPRs so three workgroups (12 waves) share a CU,
-// which the LDS footprint also allows
-template <int W>
-__global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) void vanguard_query_kernel(
+// which the LDS footprint also allows. kPre: the lower bounds come from p.van_lows.
+template <int W, bool kPre>
+__global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4) || W >= 16 || kPre ? 3 : 1) void vanguard_query_kernel(
     const ScanParams p, const VanguardArgs va) {
     extern __shared__ __align__(16) float s_dyn[];  // q' [P]
     __shared__ VqShared S;
@@ -278,6 +287,8 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
     const uint32_t P = p.P, nw = W > 0 ? (uint32_t)W : P / 32;
     const QueueDev q = p.queue;
     float *s_q = s_dyn;
+    // vectors per streamed unit: a tile of codes, or a chunk of 256 precomputed bounds
+    constexpr uint32_t kStreamVectors = kPre ? kPreChunk : (uint32_t)kTileVectors;
 
     // ---- set-up: pair metadata, q-planes and q' in LDS ----
     if (tid < V) {
@@ -314,7 +325,7 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
             S.off[j] = o;
             S.toff[j] = to;
             o += S.n[j];
-            to += (S.n[j] + kTileVectors - 1) / kTileVectors;
+            to += (S.n[j] + kStreamVectors - 1) / kStreamVectors;
         }
         S.off[V] = o;
         S.toff[V] = to;
@@ -652,124 +663,228 @@ __global__ __launch_bounds__(kVqThreads, (W > 0 && W <= 4) || W >= 16 ? 3 : 1) v
         }
 
     };
-    // kBufs tile buffers per wave in turn: tile t is evaluated from one while tiles
-    // t + 4, ..., t + 4 (kBufs - 1) are in flight into the others, then t + 4 kBufs is
-    // fetched into the first; every kVqSegTiles tiles per wave the list is refined once
-    // it holds kVqHigh entries
-    constexpr int kBufs = W > 0 && W <= 8 ? 4 : 2;
-    struct TileRegs {
-        uint32_t x[K];
-        float fa, fr, fe;
-        // wave-uniform: the pair's g_add / g_error, the valid lanes of the tile and the
-        // list position of its lane 0
-        float gadd, gerr;
-        uint32_t lim, posbase;
-    };
-    TileRegs bufs[kBufs];
-    // pair of the fetch cursor and its constants, wave-uniform (scalar registers); the
-    // fetches are in increasing tile order
-    uint32_t jf = 0, f_next = uniform(S.toff[1]), f_toff = 0, f_tbase = uniform(S.tbase[0]);
-    uint32_t f_n = uniform(S.n[0]), f_off = 0;
-    float f_gadd = uniformf(S.gadd[0]), f_gerr = uniformf(S.gerr[0]);
-    auto fetch = [&](uint32_t tt, TileRegs &r) {
-        while (tt >= f_next) {
-            ++jf;
-            f_toff = f_next;
-            f_next = uniform(S.toff[jf + 1]);
-            f_tbase = uniform(S.tbase[jf]);
-            f_n = uniform(S.n[jf]);
-            f_off = uniform(S.off[jf]);
-            f_gadd = uniformf(S.gadd[jf]);
-            f_gerr = uniformf(S.gerr[jf]);
-        }
-        const uint32_t lt = tt - f_toff;
-        const uint8_t *tile = p.tiles + (size_t)(f_tbase + lt) * p.tile_bytes;
-        load_codes<W>(tile, lane, nw, r.x);
-        const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
-        r.fa = fac[lane];
-        r.fr = fac[64 + lane];
-        r.fe = fac[128 + lane];
-        r.gadd = f_gadd;
-        r.gerr = f_gerr;
-        r.lim = f_n - lt * kTileVectors;
-        r.posbase = f_off + lt * kTileVectors;
-    };
-    uint32_t t = wave;
-#pragma unroll
-    for (int b = 0; b < kBufs; ++b)
-        if (t + b * kVqWaves < T)
-            fetch(t + b * kVqWaves, bufs[b]);
-    auto step = [&](TileRegs &cur, float cut) {
-        int ip;
-        if constexpr (W > 0 && W <= 4) {
-            ip = popc_ip<W>(cur.x, preg, nw);
-        } else if constexpr (W >= 16) {
-            ip = popc_ip_scalar<W>(cur.x, cplanes);
-        } else {
-            ip = popc_ip<W>(cur.x, S.planes, nw);
-        }
-        const float ex = width * (float)ip;
-        const float low = cur.fa + cur.gadd + cur.fr * (ex + k1) - cur.fe * cur.gerr;
-        const bool pass = lane < cur.lim && low < cut;
-        const unsigned long long m = __ballot(pass);
-        if (m) {
-            uint32_t base = 0;
-            if (lane == 0)
-                base = atomicAdd(&S.nlist, (uint32_t)__popcll(m));
-            base = uniform(base);
-            if (pass) {
-                const uint32_t k = base + lane_rank(m);
-                S.l_low[k] = low;
-                S.l_pos[k] = cur.posbase + lane;
+    if constexpr (kPre) {
+        // ---- precomputed bounds: wave w takes chunks w, w + 4, ... of the query (pairs in
+        // probe order); four chunk buffers per wave, the current segment's two and the next
+        // segment's two. A segment that refines the list fetches the next segment's chunks
+        // again afterwards, so no chunk is held across the refinement ----
+        struct Chunk {
+            float4 v;                // bounds of vectors 4 lane .. 4 lane + 3 of the chunk
+            uint32_t lim, posbase;   // wave-uniform: valid vectors, list position of vector 0
+        };
+        // pair cursor, advanced by fetches in increasing chunk order (reset to refetch)
+        uint32_t jf = 0, f_next = 0, f_toff = 0, f_n = 0, f_off = 0;
+        auto reset_cursor = [&]() {
+            jf = 0;
+            f_toff = 0;
+            f_next = uniform(S.toff[1]);
+            f_n = uniform(S.n[0]);
+            f_off = 0;
+        };
+        auto fetch = [&](uint32_t gg, Chunk &c) {
+            while (gg >= f_next) {
+                ++jf;
+                f_toff = f_next;
+                f_next = uniform(S.toff[jf + 1]);
+                f_n = uniform(S.n[jf]);
+                f_off = uniform(S.off[jf]);
             }
-        }
-        if (t + kBufs * kVqWaves < T)
-            fetch(t + kBufs * kVqWaves, cur);
-        t += kVqWaves;
-    };
-    // a segment is kVqSegTiles (a multiple of kBufs) tiles per wave, so every segment
-    // starts on buffer 0 and the buffer of each step is a constant
-    static_assert(kVqSegTiles % kBufs == 0, "segments start on the first buffer");
-    const uint32_t nseg = (T + kVqWaves * kVqSegTiles - 1) / (kVqWaves * kVqSegTiles);
-    for (uint32_t seg = 0; seg < nseg; ++seg) {
-        const float cut = S.thr;
-        const uint32_t seg_end = min(T, (seg + 1) * kVqWaves * kVqSegTiles);
-        if constexpr (W > 0 && W <= 4) {
+            const uint32_t lc = gg - f_toff;
+            // the pair's slice is padded to whole chunks: lanes past the cluster read values
+            // that lim masks
+            c.v = *reinterpret_cast<const float4 *>(p.van_lows + ((size_t)qi * V + jf) * p.van_stride +
+                                                    lc * kPreChunk + 4 * lane);
+            c.lim = f_n - lc * kPreChunk;
+            c.posbase = f_off + lc * kPreChunk;
+        };
+        auto scan = [&](const Chunk &c, float cut) {
+            const float lv[4] = {c.v.x, c.v.y, c.v.z, c.v.w};
 #pragma unroll
-            for (int i = 0; i < kBq * W; ++i)
-                preg[i] = S.planes[i];
-        }
-        for (uint32_t r = 0; r < kVqSegTiles / kBufs; ++r) {
-#pragma unroll
-            for (int b = 0; b < kBufs; ++b)
-                if (t < seg_end)
-                    step(bufs[b], cut);
-        }
-        __syncthreads();
-        if (S.nlist >= kVqHigh || seg + 1 == nseg) {
-            process_list();
-            if (tid == 0)
-                S.nlist = 0;
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t i = 4 * lane + (uint32_t)r;
+                const bool pass = i < c.lim && lv[r] < cut;
+                const unsigned long long m = __ballot(pass);
+                if (m) {
+                    uint32_t base = 0;
+                    if (lane == 0)
+                        base = atomicAdd(&S.nlist, (uint32_t)__popcll(m));
+                    base = uniform(base);
+                    if (pass) {
+                        const uint32_t k = base + lane_rank(m);
+                        S.l_low[k] = lv[r];
+                        S.l_pos[k] = c.posbase + i;
+                    }
+                }
+            }
+        };
+        const uint32_t per_seg = kPreSegChunks * kVqWaves;
+        const uint32_t nseg = (T + per_seg - 1) / per_seg;
+        Chunk c0{}, c1{}, c2{}, c3{};
+        reset_cursor();
+        if (wave < T)
+            fetch(wave, c0);
+        if (wave + kVqWaves < T)
+            fetch(wave + kVqWaves, c1);
+        if (wave + per_seg < T)
+            fetch(wave + per_seg, c2);
+        if (wave + per_seg + kVqWaves < T)
+            fetch(wave + per_seg + kVqWaves, c3);
+        // segment seg scans a, b (chunks g0, g0 + 4 of this wave); na, nb hold segment seg + 1;
+        // a, b are refilled with segment seg + 2
+        auto segment = [&](uint32_t seg, Chunk &a, Chunk &b, Chunk &na, Chunk &nb) {
+            const float cut = S.thr;
+            const uint32_t g0 = seg * per_seg + wave;
+            if (g0 < T)
+                scan(a, cut);
+            if (g0 + kVqWaves < T)
+                scan(b, cut);
             __syncthreads();
-            if constexpr (W >= 16) {
-                // P >= 512: the tiles prefetched before the refinement are fetched again
-                // after it (the cursor restarts at the first pair), so they hold no
-                // registers across it; 2 tiles per wave and refinement, ~6% of the
-                // query's tile bytes
-                jf = 0;
-                f_toff = 0;
-                f_next = uniform(S.toff[1]);
-                f_tbase = uniform(S.tbase[0]);
-                f_n = uniform(S.n[0]);
-                f_off = 0;
-                f_gadd = uniformf(S.gadd[0]);
-                f_gerr = uniformf(S.gerr[0]);
-#pragma unroll
-                for (int b = 0; b < kBufs; ++b) {
-                    if (t + b * kVqWaves < T)
-                        fetch(t + b * kVqWaves, bufs[b]);
-                    else
-                        bufs[b] = TileRegs{};
+            const uint32_t g1 = g0 + per_seg, g2 = g1 + per_seg;
+            if (S.nlist >= kVqHigh || seg + 1 == nseg) {
+                process_list();
+                if (tid == 0)
+                    S.nlist = 0;
+                __syncthreads();
+                reset_cursor();
+                if (g1 < T)
+                    fetch(g1, na);
+                if (g1 + kVqWaves < T)
+                    fetch(g1 + kVqWaves, nb);
+            }
+            if (g2 < T)
+                fetch(g2, a);
+            if (g2 + kVqWaves < T)
+                fetch(g2 + kVqWaves, b);
+        };
+        // one call site (the refinement code is inlined once); the buffers rotate by value
+        for (uint32_t seg = 0; seg < nseg; ++seg) {
+            segment(seg, c0, c1, c2, c3);
+            const Chunk t0 = c0, t1 = c1;
+            c0 = c2;
+            c1 = c3;
+            c2 = t0;
+            c3 = t1;
+        }
+    } else {
+        // kBufs tile buffers per wave in turn: tile t is evaluated from one while tiles
+        // t + 4, ..., t + 4 (kBufs - 1) are in flight into the others, then t + 4 kBufs is
+        // fetched into the first; every kVqSegTiles tiles per wave the list is refined once
+        // it holds kVqHigh entries
+        constexpr int kBufs = W > 0 && W <= 8 ? 4 : 2;
+        struct TileRegs {
+            uint32_t x[K];
+            float fa, fr, fe;
+            // wave-uniform: the pair's g_add / g_error, the valid lanes of the tile and the
+            // list position of its lane 0
+            float gadd, gerr;
+            uint32_t lim, posbase;
+        };
+        TileRegs bufs[kBufs];
+        // pair of the fetch cursor and its constants, wave-uniform (scalar registers); the
+        // fetches are in increasing tile order
+        uint32_t jf = 0, f_next = uniform(S.toff[1]), f_toff = 0, f_tbase = uniform(S.tbase[0]);
+        uint32_t f_n = uniform(S.n[0]), f_off = 0;
+        float f_gadd = uniformf(S.gadd[0]), f_gerr = uniformf(S.gerr[0]);
+        auto fetch = [&](uint32_t tt, TileRegs &r) {
+            while (tt >= f_next) {
+                ++jf;
+                f_toff = f_next;
+                f_next = uniform(S.toff[jf + 1]);
+                f_tbase = uniform(S.tbase[jf]);
+                f_n = uniform(S.n[jf]);
+                f_off = uniform(S.off[jf]);
+                f_gadd = uniformf(S.gadd[jf]);
+                f_gerr = uniformf(S.gerr[jf]);
+            }
+            const uint32_t lt = tt - f_toff;
+            const uint8_t *tile = p.tiles + (size_t)(f_tbase + lt) * p.tile_bytes;
+            load_codes<W>(tile, lane, nw, r.x);
+            const float *fac = reinterpret_cast<const float *>(tile + 256u * nw);
+            r.fa = fac[lane];
+            r.fr = fac[64 + lane];
+            r.fe = fac[128 + lane];
+            r.gadd = f_gadd;
+            r.gerr = f_gerr;
+            r.lim = f_n - lt * kTileVectors;
+            r.posbase = f_off + lt * kTileVectors;
+        };
+        uint32_t t = wave;
+    #pragma unroll
+        for (int b = 0; b < kBufs; ++b)
+            if (t + b * kVqWaves < T)
+                fetch(t + b * kVqWaves, bufs[b]);
+        auto step = [&](TileRegs &cur, float cut) {
+            int ip;
+            if constexpr (W > 0 && W <= 4) {
+                ip = popc_ip<W>(cur.x, preg, nw);
+            } else if constexpr (W >= 16) {
+                ip = popc_ip_scalar<W>(cur.x, cplanes);
+            } else {
+                ip = popc_ip<W>(cur.x, S.planes, nw);
+            }
+            const float ex = width * (float)ip;
+            const float low = cur.fa + cur.gadd + cur.fr * (ex + k1) - cur.fe * cur.gerr;
+            const bool pass = lane < cur.lim && low < cut;
+            const unsigned long long m = __ballot(pass);
+            if (m) {
+                uint32_t base = 0;
+                if (lane == 0)
+                    base = atomicAdd(&S.nlist, (uint32_t)__popcll(m));
+                base = uniform(base);
+                if (pass) {
+                    const uint32_t k = base + lane_rank(m);
+                    S.l_low[k] = low;
+                    S.l_pos[k] = cur.posbase + lane;
+                }
+            }
+            if (t + kBufs * kVqWaves < T)
+                fetch(t + kBufs * kVqWaves, cur);
+            t += kVqWaves;
+        };
+        // a segment is kVqSegTiles (a multiple of kBufs) tiles per wave, so every segment
+        // starts on buffer 0 and the buffer of each step is a constant
+        static_assert(kVqSegTiles % kBufs == 0, "segments start on the first buffer");
+        const uint32_t nseg = (T + kVqWaves * kVqSegTiles - 1) / (kVqWaves * kVqSegTiles);
+        for (uint32_t seg = 0; seg < nseg; ++seg) {
+            const float cut = S.thr;
+            const uint32_t seg_end = min(T, (seg + 1) * kVqWaves * kVqSegTiles);
+            if constexpr (W > 0 && W <= 4) {
+    #pragma unroll
+                for (int i = 0; i < kBq * W; ++i)
+                    preg[i] = S.planes[i];
+            }
+            for (uint32_t r = 0; r < kVqSegTiles / kBufs; ++r) {
+    #pragma unroll
+                for (int b = 0; b < kBufs; ++b)
+                    if (t < seg_end)
+                        step(bufs[b], cut);
+            }
+            __syncthreads();
+            if (S.nlist >= kVqHigh || seg + 1 == nseg) {
+                process_list();
+                if (tid == 0)
+                    S.nlist = 0;
+                __syncthreads();
+                if constexpr (W >= 16) {
+                    // P >= 512: the tiles prefetched before the refinement are fetched again
+                    // after it (the cursor restarts at the first pair), so they hold no
+                    // registers across it; 2 tiles per wave and refinement, ~6% of the
+                    // query's tile bytes
+                    jf = 0;
+                    f_toff = 0;
+                    f_next = uniform(S.toff[1]);
+                    f_tbase = uniform(S.tbase[0]);
+                    f_n = uniform(S.n[0]);
+                    f_off = 0;
+                    f_gadd = uniformf(S.gadd[0]);
+                    f_gerr = uniformf(S.gerr[0]);
+    #pragma unroll
+                    for (int b = 0; b < kBufs; ++b) {
+                        if (t + b * kVqWaves < T)
+                            fetch(t + b * kVqWaves, bufs[b]);
+                        else
+                            bufs[b] = TileRegs{};
+                    }
                 }
             }
         }
@@ -801,7 +916,10 @@ template <int W>
 void launch_vq_w(const ScanParams &p, const VanguardArgs &va, uint32_t nq, hipStream_t s) {
     const size_t dyn = (size_t)p.P * sizeof(float);
     const uint32_t grid = (nq + kNumXcd - 1) / kNumXcd * kNumXcd;
-    vanguard_query_kernel<W><<<grid, kVqThreads, dyn, s>>>(p, va);
+    if (va.lows_ready)
+        vanguard_query_kernel<W, true><<<grid, kVqThreads, dyn, s>>>(p, va);
+    else
+        vanguard_query_kernel<W, false><<<grid, kVqThreads, dyn, s>>>(p, va);
 }
 
 // Queries ordered by nearest probed cluster (counting sort in one workgroup; the order

@@ -183,6 +183,8 @@ int cora_hybrid_stats_get(cora_hybrid *h, cora_hybrid_stats *out) {
     out->gpu_refined = x.get_last_gpu_refined();
     out->vanguard_ms = x.get_last_vanguard_ms();
     out->vanguard_bytes = x.get_last_vanguard_bytes();
+    out->vanguard_lows_ms = x.get_last_vanguard_lows_ms();
+    out->vanguard_lows_bytes = x.get_last_vanguard_lows_bytes();
     return CORA_OK;
 }
 
@@ -202,6 +204,8 @@ int cora_hybrid_set_vanguard_size(cora_hybrid *h, uint64_t size) {
 }
 
 cora_gpu_engine *cora_hybrid_gpu(cora_hybrid *h) { return h ? h->index->gpu_engine() : nullptr; }
+
+float cora_hybrid_lower_bound_scale(cora_hybrid *h) { return h ? h->index->get_lower_bound_scale() : 0.0f; }
 
 int cora_ivf_load(const char *path, int include_extended, cora_ivf **out) {
     NEED(path);

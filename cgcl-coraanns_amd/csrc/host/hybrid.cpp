@@ -258,6 +258,8 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
     last_gpu_refined_ = st.gpu_refined;
     last_vanguard_ms_ = st.vanguard_ms;
     last_vanguard_bytes_ = st.vanguard_bytes;
+    last_vanguard_lows_ms_ = st.vanguard_lows_ms;
+    last_vanguard_lows_bytes_ = st.vanguard_lows_bytes;
     if (rc != CORA_OK)
         throw std::runtime_error(engine_error(engine_));
     if (profiling_enabled_) {

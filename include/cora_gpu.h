@@ -75,7 +75,16 @@ enum cora_search_flags {
      * FP16 rows, three FP16 products per term: at most 3 * 2^-22 relative error per term).
      * Either way the selected probes' g_add / g_error are recomputed in FP32
      * (hybrid.cu:436-440, 465-498). */
-    CORA_FLAG_FP32_GEMM = 1u << 8
+    CORA_FLAG_FP32_GEMM = 1u << 8,
+    /* Fused vanguard pass: where its lower bounds come from (same candidates either way).
+     * By default, when the index's sign codes and factors exceed the last-level cache
+     * (256 MB), they are evaluated first on the matrix cores, cluster-major, in units of
+     * up to 16 same-cluster pairs (each cluster read once per unit), and the per-query pass
+     * streams them; a smaller index stays cache-resident, and each query evaluating its own
+     * clusters inside the per-query pass is faster. NO_VANGUARD_MFMA forces the latter,
+     * VANGUARD_MFMA the former. */
+    CORA_FLAG_NO_VANGUARD_MFMA = 1u << 9,
+    CORA_FLAG_VANGUARD_MFMA = 1u << 10
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -129,8 +138,12 @@ typedef struct cora_search_stats {
     uint64_t gpu_refined;   /* vectors the fused vanguard pass refined on the GPU */
     float vanguard_ms;      /* the fused vanguard pass kernel alone (FILTER_TIMING only) */
     uint64_t vanguard_bytes; /* its algorithmic bytes: code + factor bytes of every vector of
-                                every vanguard pair, plus sign code, ex-code and ex-factor
-                                bytes of every vector it refined */
+                                every vanguard pair (4 bytes of lower bound each when the
+                                matrix-core lows pass ran), plus sign code, ex-code and
+                                ex-factor bytes of every vector it refined */
+    float vanguard_lows_ms;  /* the matrix-core vanguard lows pass alone (0 when it did not run) */
+    uint64_t vanguard_lows_bytes; /* its algorithmic bytes: code + factor bytes of every vector
+                                     of the cluster, once per unit of up to 16 pairs */
 } cora_search_stats;
 
 /* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */
@@ -221,8 +234,12 @@ enum cora_debug_array {
                                      (+inf: unused slot); keep = max(topk, 20) */
     CORA_DBG_THRESHOLDS = 11,     /* f32 [nq] thresholds the GPU filter read last (the
                                      snapshot in frozen mode, else the live array) */
-    CORA_DBG_PROBE_DIST = 12      /* f32 [nq][nlist] coarse-probe distance matrix
+    CORA_DBG_PROBE_DIST = 12,     /* f32 [nq][nlist] coarse-probe distance matrix
                                      ||q'||^2 + ||c'||^2 - 2 <q',c'> */
+    CORA_DBG_VANGUARD_LOWS = 13   /* f32 [nq][vanguard depth][stride] lower bounds the
+                                     matrix-core lows pass wrote (stride = the largest
+                                     cluster rounded up to 256; entries past a cluster's
+                                     size are undefined) */
 };
 int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t bytes);
 

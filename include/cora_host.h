@@ -65,6 +65,8 @@ typedef struct cora_hybrid_stats {
     uint64_t gpu_refined; /* vectors the fused vanguard pass refined on the GPU */
     float vanguard_ms;    /* fused vanguard pass kernel alone */
     uint64_t vanguard_bytes; /* its algorithmic bytes */
+    float vanguard_lows_ms;  /* matrix-core vanguard lows pass alone */
+    uint64_t vanguard_lows_bytes; /* its algorithmic bytes */
 } cora_hybrid_stats;
 
 int cora_hybrid_create(cora_hybrid **out, int device);                 /* HybridIndex() */
@@ -91,6 +93,8 @@ int cora_hybrid_capture_thresholds(cora_hybrid *h, float *out, uint64_t nq);
 int cora_hybrid_seed_thresholds(cora_hybrid *h, const float *in, uint64_t nq);
 int cora_hybrid_set_vanguard_size(cora_hybrid *h, uint64_t size);
 cora_gpu_engine *cora_hybrid_gpu(cora_hybrid *h);
+/* get_lower_bound_scale (0 for a null handle). */
+float cora_hybrid_lower_bound_scale(cora_hybrid *h);
 
 /* IVF file + SearchData adaptation. */
 typedef struct cora_ivf_info {

@@ -130,6 +130,8 @@ class HybridIndex {
     uint64_t get_last_gpu_refined() const { return last_gpu_refined_; }
     float get_last_vanguard_ms() const { return last_vanguard_ms_; }
     uint64_t get_last_vanguard_bytes() const { return last_vanguard_bytes_; }
+    float get_last_vanguard_lows_ms() const { return last_vanguard_lows_ms_; }
+    uint64_t get_last_vanguard_lows_bytes() const { return last_vanguard_lows_bytes_; }
     cora_gpu_engine *gpu_engine() const { return engine_; }
 
   private:
@@ -181,6 +183,8 @@ class HybridIndex {
     float last_seed_ms_ = 0.0f, last_recovery_ms_ = 0.0f;
     uint64_t last_gpu_refined_ = 0, last_vanguard_bytes_ = 0;
     float last_vanguard_ms_ = 0.0f;
+    uint64_t last_vanguard_lows_bytes_ = 0;
+    float last_vanguard_lows_ms_ = 0.0f;
 };
 
 }  // namespace coraanns

@@ -12,7 +12,7 @@ namespace coraanns {
 inline constexpr std::size_t default_vanguard_size = 5;
 inline constexpr int default_batch_q = 4;
 // Default multiplier of the GPU filter's error term (HybridIndex::set_lower_bound_scale).
-inline constexpr float default_bound_scale = 1.5f;
+inline constexpr float default_bound_scale = 1.3f;
 inline constexpr float max_bound_scale = 16.0f;
 inline constexpr std::size_t max_query_chunk = 65535;
 inline constexpr std::size_t max_probe_count = 65536;

@@ -297,15 +297,19 @@ def test_coarse_probe_large_nlist(nlist, tmp_path):
 
 
 @pytest.mark.parametrize("case_name", CASES)
-@pytest.mark.parametrize("mfma", [True, False])
-def test_popcount_estimator_bit_exact(case_name, mfma, request):
+@pytest.mark.parametrize("mfma,vanguard", [(True, 0), (False, 0), (True, 4)])
+def test_popcount_estimator_bit_exact(case_name, mfma, vanguard, request):
     """ip_int and ip_res of every (vector, probe) bit-exact, the lower bound within 1e-5,
-    from the far-scan kernel the search ran: the matrix-core one (int8 MFMA) or the
-    popcount one."""
+    from the scan kernels the search ran: the matrix-core one (int8 MFMA) or the popcount
+    one; with vanguard pairs, the matrix-core kernel over the vanguard units of up to 16
+    pairs that the vanguard lows pass scanned."""
     case = request.getfixturevalue(case_name)
     nprobe = min(8, case.file.nlist)
-    say(f"[gpu] dense estimator parity on {case_name} nprobe={nprobe} mfma={mfma}")
-    eng, _, _ = run_frozen(case, nprobe, 10, extra_flags=0 if mfma else ca.FLAG_NO_MFMA_SCAN)
+    vanguard = min(vanguard, nprobe - 1)
+    say(f"[gpu] dense estimator parity on {case_name} nprobe={nprobe} mfma={mfma} vanguard={vanguard}")
+    flags = (0 if mfma else ca.FLAG_NO_MFMA_SCAN) | \
+        (ca.FLAG_GPU_SEED_FROZEN | ca.FLAG_VANGUARD_MFMA if vanguard else 0)
+    eng, _, _ = run_frozen(case, nprobe, 10, extra_flags=flags, vanguard=vanguard)
     g = gpu_intermediates(eng, case, nprobe)
     maxc = case.ivf.max_cluster
     ip, ipr, low = eng.debug_dense(case.queries.shape[0], nprobe, maxc)
@@ -436,7 +440,7 @@ def test_batch_q_and_reuse_do_not_change_results(synth, batch_q):
     assert np.allclose(d, d0, rtol=1e-6)
 
 
-@pytest.mark.parametrize("mode", ["fused", "pair", "none"])
+@pytest.mark.parametrize("mode", ["fused", "fused_lows", "pair", "none"])
 def test_live_thresholds_match_frozen_results(synth, mode):
     """Default production mode (live thresholds, secondary filter, vanguard 5; the fused
     vanguard pass, the per-pair seed and recovery passes, or no GPU seed thresholds)
@@ -447,7 +451,7 @@ def test_live_thresholds_match_frozen_results(synth, mode):
     _, d0, i0 = run_frozen(synth, nprobe, topk, vanguard=0)
     eng = make_engine(synth, nprobe, topk, vanguard=5, frozen=False, secondary=True,
                       gpu_seed_refine=mode != "none",
-                      extra_flags=ca.FLAG_PAIR_SEEDS if mode == "pair" else 0)
+                      extra_flags={"pair": ca.FLAG_PAIR_SEEDS, "fused_lows": ca.FLAG_VANGUARD_MFMA}.get(mode, 0))
     eng.reset_buffer(synth.queries)
     d, i = eng.search(synth.queries, topk, nprobe, 4)
     st = eng.stats()
@@ -600,20 +604,64 @@ def probed_vectors(case, g, q, nprobe):
 
 
 @pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
+@pytest.mark.parametrize("vanguard", [5, 16])
+def test_vanguard_lows_pass_matches_oracle(case_name, vanguard, request):
+    """The matrix-core vanguard lows pass (vanguard units of up to 16 same-cluster pairs):
+    every (vector, vanguard pair) lower bound it writes equals the oracle's Bitwise bound
+    (filter_kernels.cuh:79-114) within 1e-5 of the magnitude of its terms."""
+    nprobe, topk = 16, 10
+    case = request.getfixturevalue(case_name)
+    nq = case.queries.shape[0]
+    say(f"[gpu] vanguard lows pass vs oracle, {case_name} vanguard={vanguard}")
+    eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True,
+                      extra_flags=ca.FLAG_GPU_SEED_FROZEN | ca.FLAG_VANGUARD_MFMA)
+    eng.reset_buffer(case.queries)
+    eng.search(case.queries, topk, nprobe)
+    st = eng.stats()
+    assert st["vanguard_lows_bytes"] > 0
+    g = gpu_intermediates(eng, case, nprobe)
+    stride = (case.ivf.max_cluster + 255) // 256 * 256
+    lows = eng.debug_read(ca.DBG_VANGUARD_LOWS, (nq, vanguard, stride), np.float32)
+    sd = case.sd
+    qint = qint_from_planes(g["planes"][:, :8])
+    checked = 0
+    for q in range(nq):
+        for p in range(vanguard):
+            c = int(g["pidx"][q, p])
+            s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+            ex = orc.exact_ip_bitwise(orc.ip_int_direct(sd.bits[s:s + n], qint[q]), g["width"][q])
+            f = sd.short_factors[s:s + n]
+            want = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p], ex, g["k1"][q])
+            sc = np.abs(f[:, 0]) + abs(g["gadd"][q, p]) + np.abs(f[:, 1] * (ex + g["k1"][q])) + \
+                np.abs(f[:, 2] * g["gerr"][q, p])
+            assert np.all(np.abs(lows[q, p, :n] - want) <= 1e-5 * sc), (q, p, c)
+            checked += n
+    assert checked > 0
+    # the lows pass reads each cluster once per unit of up to 16 of its vanguard pairs
+    P = case.file.padded_dim
+    m = np.bincount(g["pidx"][:, :vanguard].reshape(-1), minlength=case.file.nlist)
+    sizes = sd.cluster_sizes.astype(np.int64)
+    assert st["vanguard_lows_bytes"] == int((-(-m // 16) * sizes).sum()) * (P // 8 + 12)
+    eng.close()
+
+
+@pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
 @pytest.mark.parametrize("vanguard", [3, 8])
-def test_fused_vanguard_frozen_parity(case_name, vanguard, request):
+@pytest.mark.parametrize("lows", [True, False])
+def test_fused_vanguard_frozen_parity(case_name, vanguard, lows, request):
     """Fused per-query vanguard pass in its deterministic test mode (frozen snapshot,
     lowered by the pass): the threshold is backed by topk published vanguard vectors below
     it; the vanguard pass publishes every vector with low and refined distance below the
     threshold and nothing beyond its rounding bound; the far pass publishes exactly the
     vectors with low < threshold and refined distance within the bound; the final top-k is
-    the top-k of that candidate set by the CPU consumer's distance."""
+    the top-k of that candidate set by the CPU consumer's distance. lows: the bounds come
+    from the matrix-core lows pass, else from the per-query pass itself."""
     nprobe, topk = 8, 10
     case = request.getfixturevalue(case_name)
     nq = case.queries.shape[0]
-    say(f"[gpu] fused vanguard pass, frozen parity, {case_name} vanguard={vanguard}")
+    say(f"[gpu] fused vanguard pass, frozen parity, {case_name} vanguard={vanguard} lows={lows}")
     eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True,
-                      extra_flags=ca.FLAG_GPU_SEED_FROZEN)
+                      extra_flags=ca.FLAG_GPU_SEED_FROZEN | (ca.FLAG_VANGUARD_MFMA if lows else ca.FLAG_NO_VANGUARD_MFMA))
     eng.reset_buffer(case.queries)
     d, i = eng.search(case.queries, topk, nprobe)
     st = eng.stats()
@@ -791,7 +839,8 @@ def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, tmp_path):
     bucket counting) and the scan statistics the benchmark's roofline is computed from:
     the scheduled pairs are exactly the probe lists, vanguard pairs first; the far-pass
     bytes are sum over clusters of ceil(m_c / unit) * n_c * (P/8 + 12), the vanguard bytes
-    sum m_c * n_c * (P/8 + 12) plus the refined vectors' (P + 8)."""
+    ceil(m_c / 16) * n_c * (P/8 + 12) for the vanguard lows pass and 4 m_c n_c plus the
+    refined vectors' (P + 8) for the per-query vanguard pass."""
     rng = np.random.default_rng(dim)
     nlist, n, nq, nprobe, vanguard = 16384, 40000, 192, 32, 5
     cent = rng.normal(0, 1, (nlist, dim)).astype(np.float32)
@@ -809,7 +858,7 @@ def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, tmp_path):
     P = case.file.padded_dim
     say(f"[gpu] pair schedule + scan bytes, nlist={nlist} P={P}")
     eng = make_engine(case, nprobe, 10, vanguard=vanguard, frozen=False, secondary=True,
-                      gpu_seed_refine=True, gpu_refine_filter=True)
+                      gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=ca.FLAG_VANGUARD_MFMA)
     eng.reset_buffer(q)
     eng.search(q, 10, nprobe)
     st = eng.stats()
@@ -830,5 +879,9 @@ def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, tmp_path):
     unit = 16 if (P // 32) in (2, 4, 6, 8, 16, 24, 32) else 4  # matrix-core far scan, else batch-q 4
     assert st["scan_vectors"] == int((far_m * sizes).sum())
     assert st["scan_bytes"] == int((-(-far_m // unit) * sizes).sum()) * bpv
-    assert st["vanguard_bytes"] == int((van_m * sizes).sum()) * bpv + st["gpu_refined"] * (P + 8)
+    # the vanguard lows pass reads each cluster once per unit of up to 16 vanguard pairs; the
+    # per-query pass streams one 4-byte bound per (vector, pair), plus the refined vectors'
+    # sign code, ex-code and ex-factors
+    assert st["vanguard_lows_bytes"] == int((-(-van_m // 16) * sizes).sum()) * bpv
+    assert st["vanguard_bytes"] == 4 * int((van_m * sizes).sum()) + st["gpu_refined"] * (P + 8)
     eng.close()
