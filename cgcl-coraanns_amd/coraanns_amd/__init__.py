@@ -164,6 +164,7 @@ GPU_SIGNATURES = {
     "cora_tool_kmeans": [_P, _U64, _U64, _U64, C.c_uint32, _U64, _P, _I],
     "cora_tool_assign": [_P, _U64, _U64, _P, _U64, _P, _I],
     "cora_tool_topk": [_P, _U64, _P, _U64, _U64, _U64, _I, _P, _I],
+    "cora_tool_assign_noalloc": [_P, _U64, _U64, _P, _U64, _P, _I],
 }
 
 HOST_SIGNATURES = {

@@ -7,6 +7,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <random>
 #include <string>
 #include <vector>
@@ -120,6 +122,38 @@ int assign_rows(const float *d_x, size_t n, uint32_t dim, const float *d_c, cons
     TCHK(hipGetLastError());
     return CORA_OK;
 }
+
+// ---- scratch of the allocation-free assignment (cora_tool_assign_noalloc) ----
+// Centroid norms, row norms and one block of distances live in this static device array;
+// every GPU the library runs on holds its own copy until the process ends. Its host-side
+// name is not a device address: host code uses the per-device address that
+// hipGetSymbolAddress returns (scratch_address) for kernel arguments.
+constexpr size_t kScratchFloats = size_t{4} << 20;  // 16 MiB
+static_assert(CORA_NOALLOC_MAX_CENTROIDS * 3 + 192 <= kScratchFloats,
+              "the scratch holds the centroid norms and at least one row of distances");
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+std::mutex g_scratch_mu;
+std::map<int, float *> g_scratch_addr;  // device ordinal -> address of its scratch
+
+// The calling device's scratch address, resolved once per device (the device is current).
+int scratch_address(int device, float **out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch_addr.find(device);
+    if (it == g_scratch_addr.end()) {
+        float *ptr = nullptr;
+        TCHK(hipGetSymbolAddress(reinterpret_cast<void **>(&ptr), HIP_SYMBOL(scratch)));
+        if (!ptr) {
+            g_tool_error = "hipGetSymbolAddress returned no address for the scratch array";
+            return CORA_ERR_RUNTIME;
+        }
+        it = g_scratch_addr.emplace(device, ptr).first;
+    }
+    *out = it->second;
+    return CORA_OK;
+}
+
+constexpr size_t round_floats(size_t n) { return (n + 63) / 64 * 64; }  // 256-byte slots
 
 }  // namespace
 
@@ -278,6 +312,43 @@ int cora_tool_assign(const float *h_x, uint64_t n, uint64_t dim, const float *h_
             return rc;
         TCHK(hipMemcpy(h_assign + b, asg.p, rows * 4, hipMemcpyDeviceToHost));
     }
+    return CORA_OK;
+}
+
+// The same assignment on device arrays the caller owns, with no allocation: centroid norms,
+// row norms and distance blocks in the static scratch array (nothing in it has to start at
+// zero: every value is written before it is read). Calls that overlap on one GPU (two host
+// threads) share that array and race; a call returns once its kernels have finished.
+int cora_tool_assign_noalloc(const float *d_x, uint64_t n, uint64_t dim, const float *d_centroids,
+                             uint64_t k, uint32_t *d_assign, int device) {
+    if (!d_x || !d_centroids || !d_assign || !n || !dim || !k) {
+        g_tool_error = "assign_noalloc: null array or zero size";
+        return CORA_ERR_INVALID_ARGUMENT;
+    }
+    if (k > CORA_NOALLOC_MAX_CENTROIDS || dim > CORA_NOALLOC_MAX_DIM || n > 0xFFFFFFFFull) {
+        g_tool_error = "assign_noalloc: at most " + std::to_string(CORA_NOALLOC_MAX_CENTROIDS) +
+                       " centroids, dimension " + std::to_string(CORA_NOALLOC_MAX_DIM) +
+                       " and 2^32 - 1 rows (the scratch holds " + std::to_string(kScratchFloats * 4 >> 20) + " MiB)";
+        return CORA_ERR_INVALID_ARGUMENT;
+    }
+    TCHK(hipSetDevice(device));
+    float *base = nullptr;
+    if (int rc = scratch_address(device, &base))
+        return rc;
+    // layout: centroid norms [k], then per block row norms [chunk] and distances [chunk][k]
+    const size_t cn_slot = round_floats(k);
+    // rows per block: what the scratch holds, and row offsets of a block within 2^31 elements
+    const size_t chunk = std::min<size_t>({n, (kScratchFloats - cn_slot - 64) / (k + 1), ((1ull << 31) - 1) / dim});
+    float *cn = base, *xn = base + cn_slot, *dist = xn + round_floats(chunk);
+    if (chunk == 0 || (size_t)(dist - base) + chunk * k > kScratchFloats) {
+        g_tool_error = "assign_noalloc: the scratch cannot hold one row of distances";
+        return CORA_ERR_INVALID_ARGUMENT;
+    }
+    launch_row_norms(d_centroids, (uint32_t)k, (uint32_t)dim, cn, nullptr);
+    if (int rc = assign_rows(d_x, n, (uint32_t)dim, d_centroids, cn, (uint32_t)k, d_assign, xn, dist, chunk,
+                             nullptr))
+        return rc;
+    TCHK(hipStreamSynchronize(nullptr));
     return CORA_OK;
 }
 

@@ -279,6 +279,20 @@ int cora_tool_quantize(const float *x, uint64_t n, uint64_t dim, const float *R,
                        const float *centroids, uint64_t nlist, const uint32_t *assign, int metric,
                        uint8_t *bits, float *f1, uint8_t *code, float *f2, int device);
 
+/* cora_tool_assign without any allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops that assign new vectors to clusters, harnesses that forbid hipMalloc). x [n][dim],
+ * centroids [k][dim] and assign [n] are DEVICE arrays on `device`, owned by the caller; the
+ * norms and distance blocks go to a 16 MiB static device array that each GPU holds until the
+ * process ends. Same result as cora_tool_assign (nearest centroid, ties -> lower id). At most
+ * CORA_NOALLOC_MAX_CENTROIDS centroids and dimension CORA_NOALLOC_MAX_DIM (else
+ * CORA_ERR_INVALID_ARGUMENT). Runs on the null stream and returns when done; calls that
+ * overlap on one GPU share the scratch array and race. */
+#define CORA_NOALLOC_MAX_CENTROIDS 1048576
+#define CORA_NOALLOC_MAX_DIM 4096
+int cora_tool_assign_noalloc(const float *x, uint64_t n, uint64_t dim, const float *centroids, uint64_t k,
+                             uint32_t *assign, int device);
+
 #ifdef __cplusplus
 }
 #endif
