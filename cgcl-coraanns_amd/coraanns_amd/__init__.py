@@ -150,6 +150,7 @@ GPU_SIGNATURES = {
     "cora_gpu_free_workspace": [_P],
     "cora_gpu_queue_view": [_P, C.POINTER(cora_queue_view)],
     "cora_gpu_reset": [_P, _P, _U64],
+    "cora_gpu_query_staging": [_P, C.POINTER(_P)],
     "cora_gpu_launch_search": [_P, C.POINTER(cora_search_args)],
     "cora_gpu_wait_host_inputs": [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P)],
     "cora_gpu_sync": [_P, C.POINTER(cora_search_stats)],

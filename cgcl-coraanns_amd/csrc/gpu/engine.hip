@@ -86,6 +86,7 @@ struct cora_gpu_engine {
     uint4 *h_items = nullptr;
     ProgressDev *h_progress = nullptr;
     float *h_thr = nullptr, *h_thr_stage = nullptr;
+    float *h_qstage = nullptr;  // pinned query staging [max_q][dim] (cora_gpu_query_staging)
     int *h_abort = nullptr;
     unsigned long long *d_produced = nullptr, *d_cached_limit = nullptr, *d_spill_count = nullptr;
     int *d_refresh = nullptr, *d_overflow = nullptr, *d_stalled = nullptr;
@@ -172,6 +173,7 @@ void release_queue(cora_gpu_engine *E) {
     hfree(E->h_progress);
     hfree(E->h_thr);
     hfree(E->h_thr_stage);
+    hfree(E->h_qstage);
     hfree(E->h_abort);
     dfree(E->d_produced);
     dfree(E->d_cached_limit);
@@ -572,6 +574,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(halloc(E, E->h_progress, 1, coherent));
         TRY(halloc(E, E->h_thr, max_q, coherent));
         TRY(halloc(E, E->h_thr_stage, max_q, hipHostMallocDefault));
+        TRY(halloc(E, E->h_qstage, max_q * E->dim, hipHostMallocDefault));
         TRY(halloc(E, E->h_abort, 1, coherent));
         TRY(dalloc(E, E->d_produced, 1));
         TRY(dalloc(E, E->d_cached_limit, 1));
@@ -625,6 +628,15 @@ int cora_gpu_queue_view(cora_gpu_engine *E, cora_queue_view *out) {
     out->capacity = E->qcap;
     out->thresholds = E->h_thr;
     out->abort_flag = E->h_abort;
+    return CORA_OK;
+}
+
+int cora_gpu_query_staging(cora_gpu_engine *E, float **out) {
+    if (!E || !out)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->ws)
+        return fail(E, CORA_ERR_LOGIC, "prepare workspace before searching");
+    *out = E->h_qstage;
     return CORA_OK;
 }
 

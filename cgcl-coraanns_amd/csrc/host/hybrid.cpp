@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstring>
 #include <iostream>
 #include <stdexcept>
 #include <string>
@@ -150,7 +151,23 @@ void HybridIndex::reset_buffer(const float *h_queries, std::size_t num_queries) 
     validate_workspace(num_queries, 1, 1);
     if (!h_queries)
         throw std::invalid_argument("missing queries");
-    check(engine_, cora_gpu_reset(engine_, h_queries, num_queries));
+    // The queries go to the engine's pinned staging buffer first, copied by the OpenMP team
+    // in parallel, so the upload is one DMA from page-locked memory rather than the runtime's
+    // pageable path (~1 MB staged copies with the host copying in between).
+    float *stage = nullptr;
+    check(engine_, cora_gpu_query_staging(engine_, &stage));
+    const std::size_t count = num_queries * dim_;
+    if (stage != h_queries) {
+        const int threads = cpu_threads_ > 0 ? cpu_threads_ : omp_get_max_threads();
+        const std::size_t block = 1u << 16;  // floats per task (256 KiB)
+        const std::size_t blocks = (count + block - 1) / block;
+#pragma omp parallel for num_threads(threads) schedule(static)
+        for (std::size_t b = 0; b < blocks; ++b) {
+            const std::size_t o = b * block;
+            std::memcpy(stage + o, h_queries + o, std::min(block, count - o) * sizeof(float));
+        }
+    }
+    check(engine_, cora_gpu_reset(engine_, stage, num_queries));
     last_spilled_count_ = 0;
 }
 

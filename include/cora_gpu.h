@@ -187,8 +187,14 @@ int cora_gpu_queue_view(cora_gpu_engine *engine, cora_queue_view *out);
 
 /* Per-chunk reset (HybridIndex::reset_buffer, hybrid.cu:380-396): uploads the raw
  * queries f32 [nq][dim] (complete when the call returns), resets device queue counters
- * and the host Progress, and sets the thresholds of the first nq queries to FLT_MAX. */
+ * and the host Progress, and sets the thresholds of the first nq queries to FLT_MAX.
+ * Queries already placed in the pinned staging buffer (cora_gpu_query_staging) upload in
+ * one DMA; any other host array goes through the runtime's pageable-copy path. */
 int cora_gpu_reset(cora_gpu_engine *engine, const float *h_queries, uint64_t nq);
+/* Pinned host buffer of [max_q][dim] floats for the queries of the next reset (valid from
+ * prepare_workspace to free_workspace). No counterpart in the reference, which uploads
+ * from the caller's pageable array. */
+int cora_gpu_query_staging(cora_gpu_engine *engine, float **staging);
 
 /* Enqueue the whole GPU side of HybridIndex::search (hybrid.cu:434-660) and return
  * without waiting: rotation, query factors and Bq=8 quantisation, coarse probing,
