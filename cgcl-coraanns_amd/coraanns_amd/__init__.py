@@ -86,7 +86,8 @@ class cora_search_stats(C.Structure):
                 ("pass_produced", C.c_uint64 * 3), ("seeded_queries", C.c_uint64),
                 ("prefilter_dropped", C.c_uint64), ("seed_ms", C.c_float), ("recovery_ms", C.c_float),
                 ("gpu_refined", C.c_uint64), ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64),
-                ("vanguard_lows_ms", C.c_float), ("vanguard_lows_bytes", C.c_uint64)]
+                ("vanguard_lows_ms", C.c_float), ("vanguard_lows_bytes", C.c_uint64),
+                ("vanguard_mode", C.c_int32), ("phase_ms", C.c_float * 4)]
 
 
 class cora_queue_view(C.Structure):
@@ -112,7 +113,8 @@ class cora_hybrid_stats(C.Structure):
                 ("seeded_queries", C.c_uint64), ("prefilter_dropped", C.c_uint64),
                 ("seed_ms", C.c_float), ("recovery_ms", C.c_float), ("gpu_refined", C.c_uint64),
                 ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64),
-                ("vanguard_lows_ms", C.c_float), ("vanguard_lows_bytes", C.c_uint64)]
+                ("vanguard_lows_ms", C.c_float), ("vanguard_lows_bytes", C.c_uint64),
+                ("vanguard_mode", C.c_int32), ("phase_ms", C.c_float * 4)]
 
 
 class cora_ivf_info(C.Structure):
@@ -388,6 +390,7 @@ class HybridIndex:
         _load()[1].cora_hybrid_stats_get(self._h, C.byref(s))
         out = {k: getattr(s, k) for k, _ in cora_hybrid_stats._fields_}
         out["pass_produced"] = list(out["pass_produced"])
+        out["phase_ms"] = list(out["phase_ms"])
         return out
 
     def capture_thresholds(self, nq):

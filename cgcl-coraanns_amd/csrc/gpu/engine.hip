@@ -43,7 +43,8 @@ struct cora_gpu_engine {
     hipStream_t stream = nullptr, stream_d2h = nullptr;
     hipEvent_t ev_prep = nullptr, ev_probe = nullptr, ev_f0 = nullptr, ev_f1 = nullptr,
                ev_s0 = nullptr, ev_s1 = nullptr, ev_p0 = nullptr, ev_p1 = nullptr, ev_v0 = nullptr,
-               ev_v1 = nullptr, ev_a0 = nullptr, ev_a1 = nullptr;
+               ev_v1 = nullptr, ev_a0 = nullptr, ev_a1 = nullptr, ev_q0 = nullptr, ev_sched = nullptr,
+               ev_done = nullptr;
     // index
     bool loaded = false;
     uint64_t N = 0, dim = 0, P = 0, nl = 0, ex_bits = 0, max_cluster = 0, total_tiles = 0;
@@ -78,6 +79,7 @@ struct cora_gpu_engine {
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
     uint4 *d_seed_rec = nullptr;
     float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
+    unsigned long long *d_selbig = nullptr;  // [max_q][2][max_nprobe] probe select scratch, nprobe > 4096
     uint64_t van_stride = 0;
     Pair *d_pairs = nullptr;
     Unit *d_units = nullptr;
@@ -99,6 +101,7 @@ struct cora_gpu_engine {
     cora_search_args last{};
     uint32_t last_depth = 0, last_batch = 1;
     bool last_timing = false, last_fused = false, last_mfma = false, last_van_lows = false;
+    int last_vanguard_mode = 0;  // cora_search_stats::vanguard_mode
 };
 
 namespace {
@@ -208,6 +211,7 @@ void release_workspace(cora_gpu_engine *E) {
     dfree(E->d_seed_err);
     dfree(E->d_seed_rec);
     dfree(E->d_van_lows);
+    dfree(E->d_selbig);
     E->van_stride = 0;
     dfree(E->d_pairs);
     dfree(E->d_units);
@@ -263,9 +267,8 @@ int validate_shape(cora_gpu_engine *E, uint64_t q, uint64_t k, uint64_t np) {
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "nprobe must be in [1, min(nlist, 65536)]");
     if (E->nl > (uint64_t)INT32_MAX / q || E->P == 0 || E->P > (uint64_t)INT32_MAX / (q * 4))
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "query workspace exceeds kernel indexing limits");
-    if (np > (uint64_t)kSelectMaxProbe)
-        return fail(E, CORA_ERR_INVALID_ARGUMENT,
-                    "nprobe above 4096 is not supported by the LDS probe select");
+    if (np > 65536)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "nprobe must be in [1, min(nlist, 65536)]");
     return CORA_OK;
 }
 
@@ -291,7 +294,8 @@ int cora_gpu_create(cora_gpu_engine **out, int device) {
         HIPCHK(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
         HIPCHK(hipStreamCreateWithFlags(&E->stream_d2h, hipStreamNonBlocking));
         for (hipEvent_t *ev : {&E->ev_prep, &E->ev_probe, &E->ev_f0, &E->ev_f1, &E->ev_s0, &E->ev_s1,
-                               &E->ev_p0, &E->ev_p1, &E->ev_v0, &E->ev_v1, &E->ev_a0, &E->ev_a1})
+                               &E->ev_p0, &E->ev_p1, &E->ev_v0, &E->ev_v1, &E->ev_a0, &E->ev_a1, &E->ev_q0,
+                               &E->ev_sched, &E->ev_done})
             HIPCHK(hipEventCreate(ev));
         return CORA_OK;
     };
@@ -323,7 +327,7 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
     dfree(E->d_excodes);
     dfree(E->d_exfac);
     for (hipEvent_t ev : {E->ev_prep, E->ev_probe, E->ev_f0, E->ev_f1, E->ev_s0, E->ev_s1, E->ev_p0,
-                          E->ev_p1, E->ev_v0, E->ev_v1, E->ev_a0, E->ev_a1})
+                          E->ev_p1, E->ev_v0, E->ev_v1, E->ev_a0, E->ev_a1, E->ev_q0, E->ev_sched, E->ev_done})
         if (ev)
             (void)hipEventDestroy(ev);
     if (E->stream)
@@ -552,6 +556,8 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_units, np * unit_splits((uint32_t)E->max_cluster)));
         TRY(dalloc(E, E->d_thr_snap, max_q));
         TRY(dalloc(E, E->d_seed, std::max<uint64_t>(1, max_q * depth * seed_words)));
+        if (max_nprobe > (uint64_t)kSelectMaxProbe)
+            TRY(dalloc(E, E->d_selbig, max_q * 2 * max_nprobe));
         if (depth > 0) {
             // a multiple of 256: the fused pass streams a pair's bounds 256 at a time
             E->van_stride = (E->max_cluster + 255) / 256 * 256;
@@ -706,6 +712,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const uint32_t P = (uint32_t)E->P;
 
     // query preparation (hybrid.cu:436-463)
+    if (timing)
+        HIPCHK(hipEventRecord(E->ev_q0, s));
     const bool split_gemm = !(a->flags & CORA_FLAG_FP32_GEMM);
     if (split_gemm && dist_gemm_f16x3_supported((uint32_t)E->dim, nq, P)) {
         launch_split_f16(E->d_raw, nq, (uint32_t)E->dim, E->d_raw_hl, E->d_rawscale, s);
@@ -732,7 +740,10 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
                          E->d_dist, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_p1, s));
-    launch_select(E->d_dist, nq, (uint32_t)E->nl, np, E->d_pidx, s);
+    if (np > (uint32_t)kSelectMaxProbe)
+        launch_select_big(E->d_dist, nq, (uint32_t)E->nl, np, E->d_selbig, E->d_pidx, s);
+    else
+        launch_select(E->d_dist, nq, (uint32_t)E->nl, np, E->d_pidx, s);
     launch_probe_refine(E->d_qrot, E->d_cent, E->d_pidx, nq, np, P, E->metric, E->d_gadd,
                         E->d_gerr, a->bound_scale > 0.0f ? a->bound_scale : 1.0f, s);
     HIPCHK(hipEventRecord(E->ev_probe, s));
@@ -763,6 +774,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
                        E->d_uoff, E->d_pairs, E->d_units,
                        (uint64_t)nq * np * unit_splits((uint32_t)E->max_cluster), E->d_nunits, E->d_stats,
                        s);
+    if (timing)
+        HIPCHK(hipEventRecord(E->ev_sched, s));
     if (frozen) {
         memcpy(E->h_thr_stage, E->h_thr, (size_t)nq * 4);
         HIPCHK(hipMemcpyAsync(E->d_thr_snap, E->h_thr_stage, (size_t)nq * 4, hipMemcpyHostToDevice, s));
@@ -785,6 +798,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     VanguardArgs va{};
     E->last_fused = fused && depth > 0;
     E->last_van_lows = van_lows;
+    E->last_vanguard_mode = depth == 0 ? 0 : !fused ? 1 : van_lows ? 3 : 2;
     if (fused) {
         va.probe_idx = E->d_pidx;
         va.nq = nq;
@@ -894,6 +908,7 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     const int overflow = __atomic_load_n(&E->h_progress->overflow, __ATOMIC_ACQUIRE);
     out.stalled = stalled;
     out.overflow = overflow && !stalled;
+    out.vanguard_mode = E->last_vanguard_mode;
     out.scan_bytes = stats[0];
     out.scan_units = stats[1];
     out.scan_vectors = stats[2];
@@ -924,6 +939,14 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
         }
         if (E->last_fused && E->last_van_lows)
             HIPCHK(hipEventElapsedTime(&out.vanguard_lows_ms, E->ev_a0, E->ev_a1));
+        // the reference's profile phases (hybrid.cu:434-516, 679-681); the last ends now,
+        // after the host's refinement, as the reference's stop event does
+        HIPCHK(hipEventRecord(E->ev_done, E->stream));
+        HIPCHK(hipEventSynchronize(E->ev_done));
+        HIPCHK(hipEventElapsedTime(&out.phase_ms[0], E->ev_q0, E->ev_p1));
+        HIPCHK(hipEventElapsedTime(&out.phase_ms[1], E->ev_p1, E->ev_probe));
+        HIPCHK(hipEventElapsedTime(&out.phase_ms[2], E->ev_probe, E->ev_sched));
+        HIPCHK(hipEventElapsedTime(&out.phase_ms[3], E->ev_sched, E->ev_done));
     }
     if (st)
         *st = out;

@@ -190,8 +190,12 @@ void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const floa
                             uint32_t nl, uint32_t P, float *dist, hipStream_t s);
 void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,
                       uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s);
+// nprobe <= kSelectMaxProbe (selection held in LDS)
 void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,
                    hipStream_t s);
+// any nprobe <= nl (up to 65,536): selection in scratch [nq][2][nprobe] u64
+void launch_select_big(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
+                       unsigned long long *scratch, int32_t *idx, hipStream_t s);
 // g_error of the selected probes is written as err_scale * ||q' - c'||: the lower bound's
 // error term f_error * g_error scaled at one place for every pass that forms a bound.
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,

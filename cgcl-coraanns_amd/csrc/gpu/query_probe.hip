@@ -1314,8 +1314,161 @@ void launch_rotate_f16x3(const uint16_t *xhl, const float *xscale, const uint16_
         nullptr, ncx);
 }
 
+// ---- big-k select (nprobe > kSelectMaxProbe, up to 65,536): one 1024-thread block per
+// query, with the selection in global scratch [k] instead of LDS ----
+constexpr int kBigT = 1024;
+
+// exclusive prefix of v over the block (thread order); s_w holds kBigT / 64 words
+__device__ __forceinline__ uint32_t big_exclusive_scan(uint32_t v, uint32_t *s_w, uint32_t &total) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o);
+        if (lane >= (uint32_t)o)
+            x += y;
+    }
+    if (lane == 63)
+        s_w[wave] = x;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kBigT / 64; ++w) {
+        before += (uint32_t)w < wave ? s_w[w] : 0u;
+        all += s_w[w];
+    }
+    __syncthreads();
+    total = all;
+    return x - v + before;
+}
+
+// 1. the k-th smallest order key of the row (radix select, four 8-bit passes over the row);
+// 2. compaction in cluster-id order of the keys below it and of the first ties (lowest ids)
+//    as (key << 32 | id) into a[0, k);
+// 3. a stable LSD radix sort of a by key, 4 bits per pass through b (ties keep id order);
+// 4. the sorted ids to idx.
+__global__ __launch_bounds__(kBigT) void select_big_kernel(const float *__restrict__ dist, uint32_t nl, uint32_t k,
+                                                           unsigned long long *__restrict__ scratch,
+                                                           int32_t *__restrict__ idx) {
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_w[kBigT / 64];
+    __shared__ uint32_t s_sel[2];
+    __shared__ uint32_t s_cnt[16 * kBigT];
+    const uint32_t t = threadIdx.x, q = blockIdx.x;
+    const float *row = dist + (size_t)q * nl;
+    unsigned long long *a = scratch + (size_t)q * 2 * k, *b = a + k;
+    // 1. radix select
+    uint32_t prefix = 0, pmask = 0, need = k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (uint32_t i = t; i < 256; i += kBigT)
+            s_hist[i] = 0;
+        __syncthreads();
+        for (uint32_t i = t; i < nl; i += kBigT) {
+            const uint32_t key = order_key(row[i]);
+            if ((key & pmask) == prefix)
+                atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (t == 0) {
+            uint32_t acc = 0, d = 0;
+            while (acc + s_hist[d] < need)
+                acc += s_hist[d++];
+            s_sel[0] = d;
+            s_sel[1] = need - acc;
+        }
+        __syncthreads();
+        prefix |= s_sel[0] << shift;
+        pmask |= 255u << shift;
+        need = s_sel[1];  // keys equal to the k-th that are taken (ties: the lowest ids)
+        __syncthreads();
+    }
+    const uint32_t kth = prefix;
+    // 2. ordered compaction: thread t owns ids [t * per, (t + 1) * per)
+    const uint32_t per = (nl + kBigT - 1) / kBigT;
+    const uint32_t i0 = min(nl, t * per), i1 = min(nl, i0 + per);
+    uint32_t nless = 0, neq = 0;
+    for (uint32_t i = i0; i < i1; ++i) {
+        const uint32_t key = order_key(row[i]);
+        nless += key < kth;
+        neq += key == kth;
+    }
+    uint32_t tot_less = 0, tot_eq = 0;
+    uint32_t o_less = big_exclusive_scan(nless, s_w, tot_less);
+    uint32_t o_eq = big_exclusive_scan(neq, s_w, tot_eq);
+    for (uint32_t i = i0; i < i1; ++i) {
+        const uint32_t key = order_key(row[i]);
+        const unsigned long long v = ((unsigned long long)key << 32) | i;
+        if (key < kth)
+            a[o_less++] = v;
+        else if (key == kth) {
+            if (o_eq < need)
+                a[tot_less + o_eq] = v;
+            ++o_eq;
+        }
+    }
+    __syncthreads();
+    // 3. stable LSD radix sort of a[0, k) by key: thread t owns elements [t * kper, ...)
+    const uint32_t kper = (k + kBigT - 1) / kBigT;
+    const uint32_t e0 = min(k, t * kper), e1 = min(k, e0 + kper);
+    unsigned long long *src = a, *dst = b;
+    for (int shift = 32; shift < 64; shift += 4) {
+        uint32_t c[16];
+#pragma unroll
+        for (int d = 0; d < 16; ++d)
+            c[d] = 0;
+        for (uint32_t e = e0; e < e1; ++e) {
+            const uint32_t d = (uint32_t)(src[e] >> shift) & 15u;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                c[j] += d == (uint32_t)j;
+        }
+#pragma unroll
+        for (int d = 0; d < 16; ++d)
+            s_cnt[d * kBigT + t] = c[d];
+        __syncthreads();
+        // exclusive scan over s_cnt in (digit, thread) order: thread t sums 16 consecutive entries
+        uint32_t part = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            part += s_cnt[t * 16 + j];
+        uint32_t total = 0;
+        uint32_t run = big_exclusive_scan(part, s_w, total);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t v = s_cnt[t * 16 + j];
+            s_cnt[t * 16 + j] = run;
+            run += v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int d = 0; d < 16; ++d)
+            c[d] = s_cnt[d * kBigT + t];
+        for (uint32_t e = e0; e < e1; ++e) {
+            const unsigned long long v = src[e];
+            const uint32_t d = (uint32_t)(v >> shift) & 15u;
+            uint32_t pos = 0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (d == (uint32_t)j)
+                    pos = c[j]++;
+            dst[pos] = v;
+        }
+        __syncthreads();
+        unsigned long long *tmp = src;
+        src = dst;
+        dst = tmp;
+    }
+    // eight passes: the sorted keys are back in a
+    for (uint32_t e = t; e < k; e += kBigT)
+        idx[(size_t)q * k + e] = (int32_t)(uint32_t)(a[e] & 0xFFFFFFFFull);
+}
+
 void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe, int32_t *idx,
                    hipStream_t s) {
+    if (nprobe > (uint32_t)kSelectMaxProbe) {
+        // (launch_select_big, with its scratch, is the caller's path for this size)
+        return;
+    }
     uint32_t kp = 1;
     while (kp < nprobe)
         kp <<= 1;
@@ -1348,6 +1501,11 @@ void launch_select(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
         select_regs_kernel<64><<<nq, kSelBigThreads, sel_bytes, s>>>(dist, nl, nprobe, kp, idx);
     else
         select_kernel<false><<<nq, kSelThreads, sel_bytes, s>>>(dist, nl, nprobe, kp, idx);
+}
+
+void launch_select_big(const float *dist, uint32_t nq, uint32_t nl, uint32_t nprobe,
+                       unsigned long long *scratch, int32_t *idx, hipStream_t s) {
+    select_big_kernel<<<nq, kBigT, 0, s>>>(dist, nl, nprobe, scratch, idx);
 }
 
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,

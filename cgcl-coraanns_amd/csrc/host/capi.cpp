@@ -185,6 +185,9 @@ int cora_hybrid_stats_get(cora_hybrid *h, cora_hybrid_stats *out) {
     out->vanguard_bytes = x.get_last_vanguard_bytes();
     out->vanguard_lows_ms = x.get_last_vanguard_lows_ms();
     out->vanguard_lows_bytes = x.get_last_vanguard_lows_bytes();
+    out->vanguard_mode = x.get_last_vanguard_mode();
+    for (int i = 0; i < 4; ++i)
+        out->phase_ms[i] = x.get_last_phase_ms(i);
     return CORA_OK;
 }
 

@@ -277,10 +277,25 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
     last_vanguard_bytes_ = st.vanguard_bytes;
     last_vanguard_lows_ms_ = st.vanguard_lows_ms;
     last_vanguard_lows_bytes_ = st.vanguard_lows_bytes;
+    last_vanguard_mode_ = st.vanguard_mode;
+    for (int i = 0; i < 4; ++i)
+        last_phase_ms_[i] = st.phase_ms[i];
     if (rc != CORA_OK)
         throw std::runtime_error(engine_error(engine_));
     if (profiling_enabled_) {
-        std::printf("[Profile] 7~9. GPU filter (popcount scan) time: %g ms\n", st.filter_ms);
+        // the reference's phases (hybrid.cu:479, 500, 516, 679-685)
+        static const char *const kVanguardMode[] = {"none", "per-pair seed and recovery passes",
+                                                     "fused per-query pass",
+                                                     "matrix-core lows pass + fused per-query pass"};
+        std::printf("[Profile] 0~2. Initial Matrix Math time: %g ms\n", st.phase_ms[0]);
+        std::printf("[Profile] 3. Select Top-nprobe Clusters time: %g ms\n", st.phase_ms[1]);
+        std::printf("[Profile] 4. Flatten Pairs time: %g ms\n", st.phase_ms[2]);
+        std::printf("[Profile] 7~9. Single-Stage Global Task Pool Pipeline (BITWISE_DECOMP) time: %g ms\n",
+                    st.phase_ms[3]);
+        std::printf("[Profile] vanguard: %s; GPU filter kernels %g ms\n",
+                    kVanguardMode[st.vanguard_mode >= 0 && st.vanguard_mode < 4 ? st.vanguard_mode : 0],
+                    st.filter_ms);
+        std::printf("------------------------------------------\n");
         std::printf("[Cora-Refine] candidates=%llu refined=%zu refinement_ratio=%.6f\n",
                     static_cast<unsigned long long>(st.produced), out.refined,
                     st.produced ? static_cast<double>(out.refined) / static_cast<double>(st.produced)

@@ -144,6 +144,14 @@ typedef struct cora_search_stats {
     float vanguard_lows_ms;  /* the matrix-core vanguard lows pass alone (0 when it did not run) */
     uint64_t vanguard_lows_bytes; /* its algorithmic bytes: code + factor bytes of every vector
                                      of the cluster, once per unit of up to 16 pairs */
+    /* how the vanguard pairs ran: 0 none, 1 the per-pair seed and recovery passes (asked
+     * for, no ex-codes in HBM, or beyond the fused pass's limits of 64 vanguard pairs and
+     * top-128), 2 the fused per-query pass, 3 the fused pass after the matrix-core lows pass */
+    int32_t vanguard_mode;
+    /* the reference's [Profile] phases (FILTER_TIMING only): query preparation and coarse
+     * GEMM, probe selection, pair scheduling, then the scan pipeline up to cora_gpu_sync
+     * (including the host's refinement) */
+    float phase_ms[4];
 } cora_search_stats;
 
 /* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */

@@ -67,6 +67,8 @@ typedef struct cora_hybrid_stats {
     uint64_t vanguard_bytes; /* its algorithmic bytes */
     float vanguard_lows_ms;  /* matrix-core vanguard lows pass alone */
     uint64_t vanguard_lows_bytes; /* its algorithmic bytes */
+    int32_t vanguard_mode;   /* get_last_vanguard_mode */
+    float phase_ms[4];       /* get_last_phase_ms */
 } cora_hybrid_stats;
 
 int cora_hybrid_create(cora_hybrid **out, int device);                 /* HybridIndex() */

@@ -16,10 +16,8 @@ inline constexpr float default_bound_scale = 1.3f;
 inline constexpr float max_bound_scale = 16.0f;
 inline constexpr std::size_t max_query_chunk = 65535;
 inline constexpr std::size_t max_probe_count = 65536;
-// This engine additionally batches up to 8 same-cluster pairs per scan pass and selects
-// at most 4096 probes per query in LDS.
+// This engine additionally batches up to 8 same-cluster pairs per scan pass.
 inline constexpr int max_batch_q = 8;
-inline constexpr std::size_t max_engine_nprobe = 4096;
 
 inline void validate_search_shape(std::size_t queries, std::size_t topk, std::size_t nprobe,
                                   std::size_t centroids, std::size_t padded_dim) {

@@ -113,7 +113,12 @@ def test_driver_multiple_nprobes_and_recall_once(known_neighbours):
     assert rows[-1][2] == 1.0
     assert len(re.findall(r"^\[RecallPoint\] nprobe=\d+ source_round=1 recall=", r.stdout, re.M)) == 3
     assert len(re.findall(r"^\[GPUFilter\] round=\d+ nprobe=\d+ ", r.stdout, re.M)) == 6
-    assert "[Profile]" in r.stdout
+    # the reference's per-search profile phases (hybrid.cu:479, 500, 516, 679-685)
+    for phase in ["0~2. Initial Matrix Math", "3. Select Top-nprobe Clusters", "4. Flatten Pairs",
+                  "7~9. Single-Stage Global Task Pool Pipeline (BITWISE_DECOMP)"]:
+        times = re.findall(r"^\[Profile\] " + re.escape(phase) + r" time: ([\d.eE+-]+) ms$", r.stdout, re.M)
+        assert len(times) == 9 and all(float(t) >= 0 for t in times), (phase, len(times))
+    assert r.stdout.count("------------------------------------------") == 9
 
 
 @pytest.mark.parametrize("bad", [

@@ -230,13 +230,18 @@ def order_keys(d):
 @pytest.mark.parametrize("nlist,distinct,nprobe", [(12000, 0, 16), (16384, 0, 32), (16384, 0, 64),
                                                    (16384, 40, 32), (12000, 7, 64), (20000, 0, 32),
                                                    (40000, 0, 16), (65536, 0, 64), (65536, 0, 33),
-                                                   (40000, 50, 64)])
+                                                   (40000, 50, 64),
+                                                   # beyond the LDS-held selects: up to the reference's 65,536
+                                                   (16384, 0, 8192), (12000, 7, 5000), (40000, 50, 20000),
+                                                   (65536, 0, 65536)])
 def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
     """The probe select (8,192 < nlist <= 16,384: distances in registers; beyond: two
     streaming passes; either way per-wave candidates below a bound from minima, ranked by
-    (distance, cluster id); heavy ties fall back to the radix select) against an exact sort
-    of the GPU's own distance matrix by (distance key, cluster id). distinct > 0 repeats that
-    many centroids over the whole list, so every distance is tied nlist / distinct times."""
+    (distance, cluster id); heavy ties fall back to the radix select; nprobe > 4,096: radix
+    select of the k-th key, ordered compaction, stable radix sort in global scratch)
+    against an exact sort of the GPU's own distance matrix by (distance key, cluster id).
+    distinct > 0 repeats that many centroids over the whole list, so every distance is
+    tied nlist / distinct times."""
     rng = np.random.default_rng(nlist + distinct)
     dim, nq = 64, 40
     n = 2 * nlist
@@ -260,6 +265,41 @@ def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
     for qi in range(nq):
         want = np.lexsort((ids, keys[qi]))[:nprobe]
         assert np.array_equal(pidx[qi], want), qi
+
+
+def test_end_to_end_nprobe_8192(tmp_path):
+    """nprobe 8,192 (beyond the LDS-held selects) end to end with frozen infinite thresholds:
+    probe lists against the oracle's FP64 coarse probe, every vector of every probed
+    cluster a candidate exactly once, and the top-k of the oracle's restatement."""
+    rng = np.random.default_rng(8192)
+    nlist, dim, n, nq, nprobe, topk = 16384, 128, 60000, 24, 8192, 10
+    cent = rng.normal(0, 1, (nlist, dim)).astype(np.float32)
+    assign = rng.integers(0, nlist, n).astype(np.uint32)
+    x = (cent[assign] + rng.normal(0, 0.3, (n, dim))).astype(np.float32)
+    q = (cent[rng.integers(0, nlist, nq)] + rng.normal(0, 0.3, (nq, dim))).astype(np.float32)
+    R = np.linalg.qr(rng.normal(size=(dim, dim)))[0].T.astype(np.float32)
+    path = tmp_path / "np8192.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32), (cent.astype(np.float64) @ R).astype(np.float32),
+                 assign, R, metric=0)
+    case = Case(path, q)
+    say(f"[gpu] end-to-end at nprobe {nprobe}, nlist {nlist}")
+    eng, d, i = run_frozen(case, nprobe, topk, vanguard=5)
+    st = eng.stats()
+    g = gpu_intermediates(eng, case, nprobe)
+    idx, _, _, l2 = orc.coarse_probe(g["qr"], case.sd.centroids, nprobe, case.file.metric)
+    for qi in range(nq):
+        got = g["pidx"][qi]
+        assert len(set(got.tolist())) == nprobe
+        kth = float(l2[qi][-1])
+        band = 1e-5 * (abs(kth) + 1)
+        # every cluster clearly inside the oracle's top-nprobe is probed, ascending order
+        assert set(idx[qi][l2[qi] < kth - band].tolist()) <= set(got.tolist()), qi
+        cd = ((g["qr"][qi].astype(np.float64) - case.sd.centroids[got].astype(np.float64)) ** 2).sum(1)
+        assert np.all(np.diff(cd) >= -band), qi
+    od, oi, cands = oracle_topk_from_gpu(case, g, nprobe, topk)
+    assert st["submitted"] == sum(len(c) for c in cands)
+    assert_topk_equal(d, i, od, oi)
+    eng.close()
 
 
 @pytest.mark.parametrize("nlist", [9000, 20000, 40000])
@@ -459,6 +499,26 @@ def test_live_thresholds_match_frozen_results(synth, mode):
     assert st["submitted"] < synth.queries.shape[0] * 20000  # the filter prunes
     same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), i0.tolist())])
     assert same >= 0.99, same
+
+
+def test_vanguard_mode_reported(synth):
+    """Which vanguard passes ran is reported, including the fallback to the per-pair passes
+    beyond the fused pass's limits (top-k above 128)."""
+    nprobe = 16
+    eng = make_engine(synth, nprobe, 129, vanguard=5, frozen=False, secondary=True)
+    for topk, flags, mode in [(10, 0, 2), (10, ca.FLAG_VANGUARD_MFMA, 3), (129, 0, 1), (10, ca.FLAG_PAIR_SEEDS, 1)]:
+        eng.configure(vanguard_size=5, cpu_secondary_filter=True, metric=synth.file.metric, gpu_filter_timing=True,
+                      extra_flags=flags, lower_bound_scale=1.0)
+        eng.reset_buffer(synth.queries)
+        eng.search(synth.queries, topk, nprobe)
+        st = eng.stats()
+        assert st["vanguard_mode"] == mode, (topk, flags, st["vanguard_mode"])
+        assert all(t > 0 for t in st["phase_ms"]), st["phase_ms"]
+    eng.configure(vanguard_size=0, metric=synth.file.metric)
+    eng.reset_buffer(synth.queries)
+    eng.search(synth.queries, 10, nprobe)
+    assert eng.stats()["vanguard_mode"] == 0
+    eng.close()
 
 
 @pytest.mark.parametrize("prefilter", [False, True])
