@@ -181,6 +181,82 @@ def search_data(ivf: IVFFile) -> SearchData:
                       ivf.cluster_sizes, starts, bits)
 
 
+@dataclass
+class LazyIVF:
+    """An IVF file mapped, not read: header arrays in memory, batch data, ex data and ids as
+    memory maps, with the per-cluster offsets of search_data (for indexes too large to
+    unpack whole in numpy)."""
+    num: int
+    dim: int
+    padded_dim: int
+    nlist: int
+    ex_bits: int
+    metric: int
+    cluster_sizes: np.ndarray
+    rotator: np.ndarray
+    centroids: np.ndarray
+    batch_data: np.ndarray  # memmap u8
+    ex_data: np.ndarray  # memmap u8 [num, stride]
+    ids: np.ndarray  # memmap u32
+    cluster_start: np.ndarray  # i64 [nlist]: first vector (cluster order)
+    block_start: np.ndarray  # i64 [nlist]: first 32-vector FastScan block
+
+
+def open_ivf_lazy(path) -> LazyIVF:
+    """The layout read_ivf follows (ivf.hpp:403-539), memory-mapped."""
+    raw = np.memmap(path, dtype=np.uint8, mode="r")
+    num, dim, nlist, ex_bits = struct.unpack_from("<4Q", raw[:32].tobytes(), 0)
+    metric = int(raw[33])
+    off = 34
+    sizes = np.frombuffer(raw[off:off + 8 * nlist].tobytes(), dtype=np.uint64).copy()
+    off += 8 * nlist
+    P = round_up(dim, 64)
+    rot = np.frombuffer(raw[off:off + 4 * dim * P].tobytes(), dtype=np.float32).reshape(dim, P).copy()
+    off += 4 * dim * P
+    nblk = (sizes.astype(np.int64) + 31) // 32
+    blocks = int(nblk.sum())
+    batch_bytes = blocks * (P * 32 // 8 + 32 * 12)
+    ex_stride = P * ex_bits // 8 + 8
+    if raw.size - off != batch_bytes + ex_stride * num + 4 * num + 4 * P * nlist:
+        raise ValueError("only indexes with embedded flat centroids are supported by the oracle")
+    cent = np.frombuffer(raw[off:off + 4 * P * nlist].tobytes(), dtype=np.float32).reshape(nlist, P).copy()
+    off += 4 * P * nlist
+    batch = raw[off:off + batch_bytes]
+    off += batch_bytes
+    ex = raw[off:off + ex_stride * num].reshape(num, ex_stride)
+    off += ex_stride * num
+    ids = raw[off:off + 4 * num].view(np.uint32)
+    starts = np.concatenate([[0], np.cumsum(sizes.astype(np.int64))[:-1]])
+    bstarts = np.concatenate([[0], np.cumsum(nblk)[:-1]])
+    return LazyIVF(int(num), int(dim), P, int(nlist), int(ex_bits), metric, sizes, rot, cent, batch, ex, ids,
+                   starts, bstarts)
+
+
+def cluster_data(ivf: LazyIVF, c: int):
+    """One cluster's slice of search_data: sign bits u8 [n, P], short factors f32 [n, 3],
+    packed ex-codes u8 [n, P*ex/8], ex factors f32 [n, 2], ids u32 [n] and the global index
+    of its first vector."""
+    P = ivf.padded_dim
+    n = int(ivf.cluster_sizes[c])
+    start = int(ivf.cluster_start[c])
+    block_bytes = P * 4 + 32 * 12
+    bits = np.zeros((n, P), np.uint8)
+    fac = np.zeros((n, 3), np.float32)
+    b0 = int(ivf.block_start[c]) * block_bytes
+    for i in range(0, n, 32):
+        blen = min(32, n - i)
+        blk = np.asarray(ivf.batch_data[b0 + (i // 32) * block_bytes:b0 + (i // 32 + 1) * block_bytes])
+        fl = blk[P * 4:].view(np.float32)
+        bits[i:i + blen] = unpack_fastscan_bits(blk[:P * 4], P, blen)
+        fac[i:i + blen, 0] = fl[0:blen]
+        fac[i:i + blen, 1] = fl[32:32 + blen]
+        fac[i:i + blen, 2] = fl[64:64 + blen]
+    lc = (P * ivf.ex_bits + 7) // 8
+    ex = np.asarray(ivf.ex_data[start:start + n])
+    return (bits, fac, ex[:, :lc].copy(), ex[:, lc:lc + 8].copy().view(np.float32).reshape(n, 2),
+            np.asarray(ivf.ids[start:start + n]).copy(), start)
+
+
 def cluster_bits_from_short(short: np.ndarray, start: int, n: int, W: int) -> np.ndarray:
     """Inverse of the per-cluster word-major layout (filter_kernels.cuh:90-91)."""
     words = short[start * W:(start + n) * W].reshape(W, n).T
@@ -600,6 +676,8 @@ def quantize_excode(x: np.ndarray, c: np.ndarray, ex_bits: int) -> np.ndarray:
 PINNED = {
     "read_ivf": "golden: ref_dump meta/ids/centroids/rotator (reference IVF::load)",
     "search_data": "golden: ref_dump short_data/short_factors/long_codes/ex_factors (reference SearchData)",
+    "open_ivf_lazy": "equals read_ivf on the golden indexes (header arrays, maps, offsets)",
+    "cluster_data": "equals the per-cluster slices of search_data on the golden indexes",
     "fastscan_pack": "golden: ref_dump fastscan_blocks (reference pack_codes) + unpack round trip",
     "unpack_fastscan_bits": "round trip with fastscan_pack on random bits; golden short_data",
     "rotate": "golden: ref_dump rotated_queries (reference MatrixRotator::rotate), 1e-5",

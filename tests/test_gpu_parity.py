@@ -481,12 +481,13 @@ def test_batch_q_and_reuse_do_not_change_results(synth, batch_q):
 
 
 @pytest.mark.parametrize("mode", ["fused", "fused_lows", "pair", "none"])
-def test_live_thresholds_match_frozen_results(synth, mode):
+@pytest.mark.parametrize("topk", [10, 100])
+def test_live_thresholds_match_frozen_results(synth, mode, topk):
     """Default production mode (live thresholds, secondary filter, vanguard 5; the fused
     vanguard pass, the per-pair seed and recovery passes, or no GPU seed thresholds)
     returns the same top-k as the exhaustive frozen search, except where refine distances
     tie."""
-    nprobe, topk = 16, 10
+    nprobe = 16
     say(f"[gpu] live vs frozen, vanguard mode {mode}")
     _, d0, i0 = run_frozen(synth, nprobe, topk, vanguard=0)
     eng = make_engine(synth, nprobe, topk, vanguard=5, frozen=False, secondary=True,
@@ -706,17 +707,19 @@ def test_vanguard_lows_pass_matches_oracle(case_name, vanguard, request):
 
 
 @pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
-@pytest.mark.parametrize("vanguard", [3, 8])
+@pytest.mark.parametrize("vanguard,topk", [(3, 10), (8, 10), (5, 100), (10, 100)])
 @pytest.mark.parametrize("lows", [True, False])
-def test_fused_vanguard_frozen_parity(case_name, vanguard, lows, request):
+def test_fused_vanguard_frozen_parity(case_name, vanguard, topk, lows, request):
     """Fused per-query vanguard pass in its deterministic test mode (frozen snapshot,
     lowered by the pass): the threshold is backed by topk published vanguard vectors below
     it; the vanguard pass publishes every vector with low and refined distance below the
     threshold and nothing beyond its rounding bound; the far pass publishes exactly the
     vectors with low < threshold and refined distance within the bound; the final top-k is
     the top-k of that candidate set by the CPU consumer's distance. lows: the bounds come
-    from the matrix-core lows pass, else from the per-query pass itself."""
-    nprobe, topk = 8, 10
+    from the matrix-core lows pass, else from the per-query pass itself. Top-100 with
+    vanguard 10 is the 100M configuration's mode (top-k window, held list and threshold
+    over many refinement rounds)."""
+    nprobe = 16
     case = request.getfixturevalue(case_name)
     nq = case.queries.shape[0]
     say(f"[gpu] fused vanguard pass, frozen parity, {case_name} vanguard={vanguard} lows={lows}")

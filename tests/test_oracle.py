@@ -50,6 +50,26 @@ def test_search_data_unpack_bit_exact(fx):
         assert np.array_equal(orc.cluster_bits_from_short(sd.short_data, s, n, W), sd.bits[s:s + n])
 
 
+def test_lazy_reader_matches_search_data(fx):
+    """The memory-mapped per-cluster reader (for indexes too large to unpack whole) gives
+    exactly the search_data slices of every cluster."""
+    name, _, ivf, sd, _ = fx
+    lz = orc.open_ivf_lazy(GOLDEN / name / "ivf.index")
+    assert (lz.num, lz.dim, lz.padded_dim, lz.nlist, lz.ex_bits, lz.metric) == \
+        (ivf.num, ivf.dim, ivf.padded_dim, ivf.nlist, ivf.ex_bits, ivf.metric)
+    assert np.array_equal(lz.rotator, ivf.rotator) and np.array_equal(lz.centroids, ivf.centroids)
+    assert np.array_equal(lz.cluster_start, sd.cluster_start)
+    for c in range(ivf.nlist):
+        bits, fac, lc, exf, ids, start = orc.cluster_data(lz, c)
+        s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+        assert start == s
+        assert np.array_equal(bits, sd.bits[s:s + n])
+        assert np.array_equal(fac.view(np.uint32), sd.short_factors[s:s + n].view(np.uint32))
+        assert np.array_equal(lc, sd.long_codes[s:s + n])
+        assert np.array_equal(exf.view(np.uint32), sd.ex_factors[s:s + n].view(np.uint32))
+        assert np.array_equal(ids, sd.ids[s:s + n])
+
+
 def test_fastscan_pack_golden_and_round_trip(golden):
     g = golden("quant_d128")
     compact = g["compact_bits"]
