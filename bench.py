@@ -136,6 +136,8 @@ def main():
     ap.add_argument("--lower-bound-scale", type=float, default=0.0,
                     help="multiplier of the filter's error term (0: the engine's default; 1: the "
                          "reference Bitwise producer's bound)")
+    ap.add_argument("--gpu-final", action="store_true",
+                    help="GPU-final top-k: the GPU forms the final top-k from its refined distances, no CPU refinement")
     ap.add_argument("--no-vanguard-mfma", action="store_true",
                     help="vanguard lower bounds inside the per-query pass instead of the matrix-core lows pass")
     ap.add_argument("--fp32-gemm", action="store_true",
@@ -194,7 +196,7 @@ def main():
                          gpu_refine_filter=not args.no_gpu_prefilter,
                          extra_flags=(ca.FLAG_FP32_GEMM if args.fp32_gemm else 0) |
                                      (ca.FLAG_NO_VANGUARD_MFMA if args.no_vanguard_mfma else 0),
-                         lower_bound_scale=args.lower_bound_scale or None)
+                         lower_bound_scale=args.lower_bound_scale or None, gpu_final_topk=args.gpu_final)
     eng.load_ivf(ivf)
     chunk = min(queries.shape[0], 65535)
     eng.prepare_workspace(chunk, c.topk, max(c.nprobes))
@@ -353,7 +355,7 @@ def main():
                    "qps_search_only": round(queries.shape[0] * args.steps / sum(times_search), 1),
                    "step_ms": [round(1000.0 * t, 3) for t in times],
                    "batch_q": batch_q, "vanguard": vanguard, "cpu_secondary_filter": c.secondary_filter,
-                   "lower_bound_scale": eng.lower_bound_scale,
+                   "lower_bound_scale": eng.lower_bound_scale, "gpu_final_topk": args.gpu_final,
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
                    "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
                    "query_chunk": chunk, "sweep": sweep},

@@ -44,6 +44,7 @@ FLAG_NO_MFMA_SCAN = 1 << 7
 FLAG_FP32_GEMM = 1 << 8
 FLAG_NO_VANGUARD_MFMA = 1 << 9
 FLAG_VANGUARD_MFMA = 1 << 10
+FLAG_GPU_FINAL = 1 << 11
 
 
 class EngineUnavailable(RuntimeError):
@@ -102,7 +103,7 @@ class cora_hybrid_config(C.Structure):
                 ("queue_capacity", C.c_uint64), ("queue_spill_capacity", C.c_uint64),
                 ("metric", C.c_int), ("frozen_thresholds", C.c_int), ("cpu_threads", C.c_int),
                 ("gpu_seed_refine", C.c_int), ("gpu_refine_filter", C.c_int), ("extra_flags", C.c_uint32),
-                ("lower_bound_scale", C.c_float)]
+                ("lower_bound_scale", C.c_float), ("gpu_final_topk", C.c_int)]
 
 
 class cora_hybrid_stats(C.Structure):
@@ -153,6 +154,7 @@ GPU_SIGNATURES = {
     "cora_gpu_queue_view": [_P, C.POINTER(cora_queue_view)],
     "cora_gpu_reset": [_P, _P, _U64],
     "cora_gpu_query_staging": [_P, C.POINTER(_P)],
+    "cora_gpu_final_results": [_P, _P, _P],
     "cora_gpu_launch_search": [_P, C.POINTER(cora_search_args)],
     "cora_gpu_wait_host_inputs": [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P)],
     "cora_gpu_sync": [_P, C.POINTER(cora_search_stats)],
@@ -298,7 +300,7 @@ class HybridIndex:
                  cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                  queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
                  cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0,
-                 lower_bound_scale=None):
+                 lower_bound_scale=None, gpu_final_topk=False):
         _, host = _load()
         h = C.c_void_p()
         _host_check(host.cora_hybrid_create(C.byref(h), device))
@@ -310,13 +312,14 @@ class HybridIndex:
                        queue_capacity=queue_capacity, queue_spill_capacity=queue_spill_capacity,
                        metric=metric, frozen_thresholds=frozen_thresholds, cpu_threads=cpu_threads,
                        gpu_seed_refine=gpu_seed_refine, gpu_refine_filter=gpu_refine_filter,
-                       extra_flags=extra_flags, lower_bound_scale=lower_bound_scale)
+                       extra_flags=extra_flags, lower_bound_scale=lower_bound_scale,
+                       gpu_final_topk=gpu_final_topk)
 
     def configure(self, *, profiling=False, candidate_stats=False, gpu_filter_timing=False,
                   cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                   queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
                   cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0,
-                  lower_bound_scale=None):
+                  lower_bound_scale=None, gpu_final_topk=False):
         """lower_bound_scale: multiplier of the filter's error term (None keeps the
         engine's default; 1.0 is the reference Bitwise producer's bound)."""
         cfg = cora_hybrid_config(int(profiling), int(candidate_stats), int(gpu_filter_timing),
@@ -325,7 +328,7 @@ class HybridIndex:
                                  (1 << 64) - 1 if queue_spill_capacity is None else int(queue_spill_capacity),
                                  int(metric), int(frozen_thresholds), int(cpu_threads),
                                  int(gpu_seed_refine), int(gpu_refine_filter), int(extra_flags),
-                                 float(lower_bound_scale or 0.0))
+                                 float(lower_bound_scale or 0.0), int(gpu_final_topk))
         _host_check(_load()[1].cora_hybrid_configure(self._h, C.byref(cfg)))
 
     def load_from_raw_pointers(self, num_vecs, dim, padded_dim, n_centroids, ex_bits, centroids,

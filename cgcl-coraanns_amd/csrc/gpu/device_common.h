@@ -220,9 +220,17 @@ __device__ __noinline__ unsigned long long refresh_limit(unsigned long long *cac
     return lim;
 }
 
-// Ring slot when pos is below the write limit, otherwise the HBM spill buffer.
+// Ring slot when pos is below the write limit, otherwise the HBM spill buffer; in the
+// GPU-final mode, the record's own slot of the HBM array (no ring).
 __device__ __forceinline__ void place_record(const QueueDev &q, unsigned long long pos,
                                              unsigned long long limit, uint4 rec) {
+    if (q.final_mode) {
+        if (pos < q.spill_capacity)
+            q.spill[pos].item = rec;
+        else
+            atomicExch(q.spill_overflow, 1);
+        return;
+    }
     if (pos < limit) {
         store_ring(&q.items[pos & q.mask], rec);
     } else {

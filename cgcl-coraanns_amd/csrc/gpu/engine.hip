@@ -80,6 +80,10 @@ struct cora_gpu_engine {
     uint4 *d_seed_rec = nullptr;
     float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
     unsigned long long *d_selbig = nullptr;  // [max_q][2][max_nprobe] probe select scratch, nprobe > 4096
+    // GPU-final top-k: per-query counts/offsets/cursor, grouped keys [spill_cap], results
+    uint32_t *d_fcount = nullptr, *d_foff = nullptr, *d_fcur = nullptr, *d_fidx = nullptr;
+    unsigned long long *d_fkeys = nullptr;
+    float *d_fdist = nullptr;
     uint64_t van_stride = 0;
     Pair *d_pairs = nullptr;
     Unit *d_units = nullptr;
@@ -94,13 +98,14 @@ struct cora_gpu_engine {
     int *d_refresh = nullptr, *d_overflow = nullptr, *d_stalled = nullptr;
     SpillRecord *d_spill = nullptr;
     bool ring_dirty = false;
+    bool final_mode = false;  // the launch in flight publishes to HBM (CORA_FLAG_GPU_FINAL)
     // pinned host copies for CPU refinement
     float *h_qrot = nullptr, *h_kb = nullptr, *h_gadd = nullptr;
     // last launch
     bool launched = false;
     cora_search_args last{};
     uint32_t last_depth = 0, last_batch = 1;
-    bool last_timing = false, last_fused = false, last_mfma = false, last_van_lows = false;
+    bool last_timing = false, last_fused = false, last_mfma = false, last_van_lows = false, last_final = false;
     int last_vanguard_mode = 0;  // cora_search_stats::vanguard_mode
 };
 
@@ -134,6 +139,7 @@ QueueDev queue_dev(cora_gpu_engine *E) {
     q.spill_overflow = E->d_overflow;
     q.abort_flag = E->h_abort;
     q.stalled = E->d_stalled;
+    q.final_mode = E->final_mode ? 1 : 0;
     return q;
 }
 
@@ -212,6 +218,12 @@ void release_workspace(cora_gpu_engine *E) {
     dfree(E->d_seed_rec);
     dfree(E->d_van_lows);
     dfree(E->d_selbig);
+    dfree(E->d_fcount);
+    dfree(E->d_foff);
+    dfree(E->d_fcur);
+    dfree(E->d_fidx);
+    dfree(E->d_fkeys);
+    dfree(E->d_fdist);
     E->van_stride = 0;
     dfree(E->d_pairs);
     dfree(E->d_units);
@@ -564,6 +576,12 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
             TRY(dalloc(E, E->d_van_lows, max_q * depth * std::max<uint64_t>(E->van_stride, 1)));
         }
         if (E->d_excodes) {
+            TRY(dalloc(E, E->d_fcount, max_q));
+            TRY(dalloc(E, E->d_foff, max_q + 1));
+            TRY(dalloc(E, E->d_fcur, max_q));
+            TRY(dalloc(E, E->d_fidx, max_q * max_topk));
+            TRY(dalloc(E, E->d_fdist, max_q * max_topk));
+            TRY(dalloc(E, E->d_fkeys, std::max<uint64_t>(1, E->spill_cap)));
             const uint64_t slots = max_q * depth * std::max<uint64_t>(max_topk, 20);
             TRY(dalloc(E, E->d_seed_dist, slots));
             TRY(dalloc(E, E->d_seed_low, slots));
@@ -637,6 +655,19 @@ int cora_gpu_queue_view(cora_gpu_engine *E, cora_queue_view *out) {
     return CORA_OK;
 }
 
+int cora_gpu_final_results(cora_gpu_engine *E, float *dists, uint32_t *idx) {
+    if (!E || !dists || !idx)
+        return CORA_ERR_INVALID_ARGUMENT;
+    if (!E->launched || !E->last_final)
+        return fail(E, CORA_ERR_LOGIC, "no GPU-final search launched");
+    HIPCHK(hipSetDevice(E->device));
+    HIPCHK(hipStreamSynchronize(E->stream));
+    const size_t n = (size_t)E->last.num_queries * E->last.topk;
+    HIPCHK(hipMemcpy(dists, E->d_fdist, n * 4, hipMemcpyDeviceToHost));
+    HIPCHK(hipMemcpy(idx, E->d_fidx, n * 4, hipMemcpyDeviceToHost));
+    return CORA_OK;
+}
+
 int cora_gpu_query_staging(cora_gpu_engine *E, float **out) {
     if (!E || !out)
         return CORA_ERR_INVALID_ARGUMENT;
@@ -690,7 +721,21 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const uint64_t want_depth = std::min<uint64_t>(a->vanguard, a->nprobe);
     if (want_depth > E->ws_van)
         return fail(E, CORA_ERR_LOGIC, "prepare workspace again before increasing vanguard size");
+    // GPU-final top-k: every published record must carry its refined distance, which the
+    // fused vanguard pass and the refined pre-filter compute (live thresholds, or the
+    // frozen snapshot in its GPU-seeded test mode)
+    const bool want_final = (a->flags & CORA_FLAG_GPU_FINAL) != 0;
+    if (want_final &&
+        (!E->d_excodes || !E->d_fkeys || (a->flags & (CORA_FLAG_NO_GPU_SEED | CORA_FLAG_NO_GPU_PREFILTER |
+                                                       CORA_FLAG_PAIR_SEEDS)) ||
+         ((a->flags & CORA_FLAG_FROZEN_THRESHOLDS) && !(a->flags & CORA_FLAG_GPU_SEED_FROZEN)) ||
+         std::min<uint64_t>(a->vanguard, a->nprobe) > kVanguardMaxPairs || a->topk > kVanguardMaxTopk))
+        return fail(E, CORA_ERR_LOGIC,
+                    "GPU-final top-k needs the ex-codes in HBM, GPU seed thresholds and the refined "
+                    "pre-filter, the fused vanguard pass (vanguard <= 64, topk <= 128) and live thresholds");
     HIPCHK(hipSetDevice(E->device));
+    E->final_mode = want_final;
+    E->last_final = want_final;
     const uint32_t nq = a->num_queries, np = a->nprobe;
     const uint32_t keep = std::max<uint32_t>(a->topk, 20u);
     const uint32_t depth = keep <= (uint32_t)kMaxVanguardKeep ? (uint32_t)want_depth : 0u;
@@ -711,6 +756,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     hipStream_t s = E->stream;
     const uint32_t P = (uint32_t)E->P;
 
+    if (want_final)  // no ring: the write limit never binds
+        launch_fill_u64(E->d_cached_limit, ~0ull, 1, s);
     // query preparation (hybrid.cu:436-463)
     if (timing)
         HIPCHK(hipEventRecord(E->ev_q0, s));
@@ -868,7 +915,11 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     if (timing)
         HIPCHK(hipEventRecord(E->ev_f1, s));
     launch_finish(queue_dev(E), kDrainMaxSeconds * 1000ull * E->wall_clock_khz, s);
+    if (want_final)
+        launch_final_topk(reinterpret_cast<const SpillRecord *>(E->d_spill), E->d_produced, E->spill_cap, nq,
+                          a->topk, E->d_fcount, E->d_foff, E->d_fcur, E->d_fkeys, E->d_fdist, E->d_fidx, s);
     HIPCHK(hipGetLastError());
+    E->final_mode = false;  // the kernels took their copy of the queue view
     E->launched = true;
     return CORA_OK;
 }
@@ -953,7 +1004,7 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     // The ring is clean once the consumer has cleared and released every record the GPU
     // produced; otherwise (a consumer that stopped early, an abort) the next reset clears it.
     const unsigned long long released = __atomic_load_n(&E->h_progress->released, __ATOMIC_ACQUIRE);
-    E->ring_dirty = released < out.produced;
+    E->ring_dirty = !E->last_final && released < out.produced;  // GPU-final: nothing in the ring
     if (overflow || stalled) {
         memset(E->h_items, 0xFF, E->qcap * sizeof(uint4));
         E->ring_dirty = false;
@@ -961,8 +1012,10 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
             return fail(E, CORA_ERR_QUEUE_STALLED,
                         "candidate queue drain stopped waiting for the CPU consumer");
         return fail(E, CORA_ERR_SPILL_EXHAUSTED,
-                    "HBM queue spill capacity exhausted; increase --queue-capacity or "
-                    "--queue-spill-capacity, or reduce --query-chunk.");
+                    E->last_final ? "GPU-final candidate records exceed the HBM spill capacity; increase "
+                                    "--queue-spill-capacity, or reduce --query-chunk."
+                                  : "HBM queue spill capacity exhausted; increase --queue-capacity or "
+                                    "--queue-spill-capacity, or reduce --query-chunk.");
     }
     return CORA_OK;
 }

@@ -93,6 +93,9 @@ struct QueueDev {
     int *spill_overflow;
     int *abort_flag;                   // host-coherent
     int *stalled;                      // HBM
+    // GPU-final top-k: records go to spill[position].item (not to the ring) and carry the
+    // refined distance in place of exact_ip
+    int final_mode;
 };
 
 struct ScanParams {
@@ -252,5 +255,11 @@ void launch_snapshot_thresholds(const float *host, float *dev, uint32_t n, hipSt
 void launch_copy_u64(const unsigned long long *src, unsigned long long *dst, hipStream_t s);
 // max_ticks: drain wait limit in ticks of the device wall clock (wall_clock64)
 void launch_finish(QueueDev q, unsigned long long max_ticks, hipStream_t s);
+// GPU-final top-k (final.hip) from the first min(*d_n, cap) records of recs: per query the
+// topk smallest (refined distance, cluster-order index), ascending; FLT_MAX / 0xFFFFFFFF pad.
+// counts/cursor [nq], offsets [nq + 1], keys [cap].
+void launch_final_topk(const SpillRecord *recs, const unsigned long long *d_n, unsigned long long cap, uint32_t nq,
+                       uint32_t topk, uint32_t *counts, uint32_t *offsets, uint32_t *cursor, unsigned long long *keys,
+                       float *out_dist, uint32_t *out_idx, hipStream_t s);
 
 }  // namespace cora

@@ -84,6 +84,8 @@ __device__ __forceinline__ void flush_stage(const ScanParams &p, const QueueDev 
                 float err;
                 const float dist = refine_one(p, query, rec.x >> 16, rec.y, ex, err);
                 keep = dist <= s_cut[i] + err;
+                if (q.final_mode)
+                    rec.z = __float_as_uint(dist);
             }
         }
         const unsigned long long m = __ballot(keep);

@@ -85,6 +85,8 @@ __device__ void flush_records(const ScanParams &p, const QueueDev &q, uint32_t n
                 const float dist = refine_one(p, rec.x & 0xFFFFu, rec.x >> 16, rec.y,
                                               __uint_as_float(rec.z), err);
                 keep = dist <= s_cut[i] + err;
+                if (q.final_mode)
+                    rec.z = __float_as_uint(dist);
             }
         }
         const unsigned long long m = __ballot(keep);

@@ -223,7 +223,8 @@ __device__ void publish_held(VqShared &S, const QueueDev &q) {
             __syncthreads();
             if (pub)
                 place_record(q, S.base + before + lane_rank(m), S.limit,
-                             make_uint4(S.h_word0[i], S.h_gid[i], __float_as_uint(S.h_ex[i]),
+                             make_uint4(S.h_word0[i], S.h_gid[i],
+                                        __float_as_uint(q.final_mode ? S.h_rd[i] : S.h_ex[i]),
                                         __float_as_uint(S.h_low[i])));
         }
         __syncthreads();  // S.red / S.base reused by the next round

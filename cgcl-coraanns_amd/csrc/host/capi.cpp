@@ -115,6 +115,7 @@ int cora_hybrid_configure(cora_hybrid *h, const cora_hybrid_config *c) {
         x.set_extra_search_flags(c->extra_flags);
         if (c->lower_bound_scale != 0.0f)
             x.set_lower_bound_scale(c->lower_bound_scale);
+        x.set_gpu_final_topk(c->gpu_final_topk != 0);
     });
 }
 

@@ -185,6 +185,55 @@ void HybridIndex::seed_thresholds(const float *in, std::size_t nq) {
     check(engine_, cora_gpu_seed_thresholds(engine_, in, nq));
 }
 
+void HybridIndex::record_stats(const cora_search_stats &st, std::size_t refined) {
+    last_written_count_ = st.produced;
+    last_spilled_count_ = st.spilled;
+    last_refined_count_ = refined;
+    last_gpu_filter_ms_ = st.filter_ms;
+    last_scan_ms_ = st.scan_ms;
+    last_scan_bytes_ = st.scan_bytes;
+    last_scan_units_ = st.scan_units;
+    last_scan_vectors_ = st.scan_vectors;
+    last_probe_ms_ = st.probe_ms;
+    last_probe_flops_ = st.probe_flops;
+    for (int i = 0; i < 3; ++i)
+        last_pass_produced_[i] = st.pass_produced[i];
+    last_seeded_queries_ = st.seeded_queries;
+    last_prefilter_dropped_ = st.prefilter_dropped;
+    last_seed_ms_ = st.seed_ms;
+    last_recovery_ms_ = st.recovery_ms;
+    last_gpu_refined_ = st.gpu_refined;
+    last_vanguard_ms_ = st.vanguard_ms;
+    last_vanguard_bytes_ = st.vanguard_bytes;
+    last_vanguard_lows_ms_ = st.vanguard_lows_ms;
+    last_vanguard_lows_bytes_ = st.vanguard_lows_bytes;
+    last_vanguard_mode_ = st.vanguard_mode;
+    for (int i = 0; i < 4; ++i)
+        last_phase_ms_[i] = st.phase_ms[i];
+}
+
+void HybridIndex::print_profile(const cora_search_stats &st, std::size_t refined) const {
+    if (profiling_enabled_) {
+        // the reference's phases (hybrid.cu:479, 500, 516, 679-685)
+        static const char *const kVanguardMode[] = {"none", "per-pair seed and recovery passes",
+                                                     "fused per-query pass",
+                                                     "matrix-core lows pass + fused per-query pass"};
+        std::printf("[Profile] 0~2. Initial Matrix Math time: %g ms\n", st.phase_ms[0]);
+        std::printf("[Profile] 3. Select Top-nprobe Clusters time: %g ms\n", st.phase_ms[1]);
+        std::printf("[Profile] 4. Flatten Pairs time: %g ms\n", st.phase_ms[2]);
+        std::printf("[Profile] 7~9. Single-Stage Global Task Pool Pipeline (BITWISE_DECOMP) time: %g ms\n",
+                    st.phase_ms[3]);
+        std::printf("[Profile] vanguard: %s; GPU filter kernels %g ms\n",
+                    kVanguardMode[st.vanguard_mode >= 0 && st.vanguard_mode < 4 ? st.vanguard_mode : 0],
+                    st.filter_ms);
+        std::printf("------------------------------------------\n");
+        std::printf("[Cora-Refine] candidates=%llu refined=%zu refinement_ratio=%.6f\n",
+                    static_cast<unsigned long long>(st.produced), refined,
+                    st.produced ? static_cast<double>(refined) / static_cast<double>(st.produced)
+                                : 0.0);
+    }
+}
+
 void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::size_t topk,
                          std::size_t nprobe, float *h_final_dists, uint32_t *h_final_pids,
                          int batch_q) {
@@ -210,10 +259,24 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
                                                                    : 0u) |
                  (cross_query_reuse_enabled_ ? uint32_t{CORA_FLAG_CROSS_QUERY_REUSE} : 0u) |
                  (gpu_seed_refine_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_SEED}) |
-                 (gpu_refine_filter_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_PREFILTER}) | extra_flags_;
+                 (gpu_refine_filter_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_PREFILTER}) |
+                 (gpu_final_topk_ && !exact ? uint32_t{CORA_FLAG_GPU_FINAL} : 0u) | extra_flags_;
     args.bound_scale = bound_scale_;
     last_gpu_filter_ms_ = 0.0f;
     check(engine_, cora_gpu_launch_search(engine_, &args));
+    if (args.flags & CORA_FLAG_GPU_FINAL) {
+        // the GPU formed the final top-k from its refined distances; no CPU refinement
+        cora_search_stats st{};
+        const int rc = cora_gpu_sync(engine_, &st);
+        record_stats(st, 0);
+        if (rc != CORA_OK)
+            throw std::runtime_error(engine_error(engine_));
+        check(engine_, cora_gpu_final_results(engine_, h_final_dists, h_final_pids));
+        for (std::size_t i = 0; i < num_queries * topk; ++i)
+            h_final_pids[i] = h_final_pids[i] < num_vectors_ ? h_ids_[h_final_pids[i]] : 0u;
+        print_profile(st, 0);
+        return;
+    }
 
     cora_queue_view view{};
     const float *rq = nullptr, *kb = nullptr, *gadd = nullptr;
@@ -256,51 +319,10 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
     }
     cora_search_stats st{};
     const int rc = cora_gpu_sync(engine_, &st);
-    last_written_count_ = st.produced;
-    last_spilled_count_ = st.spilled;
-    last_refined_count_ = out.refined;
-    last_gpu_filter_ms_ = st.filter_ms;
-    last_scan_ms_ = st.scan_ms;
-    last_scan_bytes_ = st.scan_bytes;
-    last_scan_units_ = st.scan_units;
-    last_scan_vectors_ = st.scan_vectors;
-    last_probe_ms_ = st.probe_ms;
-    last_probe_flops_ = st.probe_flops;
-    for (int i = 0; i < 3; ++i)
-        last_pass_produced_[i] = st.pass_produced[i];
-    last_seeded_queries_ = st.seeded_queries;
-    last_prefilter_dropped_ = st.prefilter_dropped;
-    last_seed_ms_ = st.seed_ms;
-    last_recovery_ms_ = st.recovery_ms;
-    last_gpu_refined_ = st.gpu_refined;
-    last_vanguard_ms_ = st.vanguard_ms;
-    last_vanguard_bytes_ = st.vanguard_bytes;
-    last_vanguard_lows_ms_ = st.vanguard_lows_ms;
-    last_vanguard_lows_bytes_ = st.vanguard_lows_bytes;
-    last_vanguard_mode_ = st.vanguard_mode;
-    for (int i = 0; i < 4; ++i)
-        last_phase_ms_[i] = st.phase_ms[i];
+    record_stats(st, out.refined);
     if (rc != CORA_OK)
         throw std::runtime_error(engine_error(engine_));
-    if (profiling_enabled_) {
-        // the reference's phases (hybrid.cu:479, 500, 516, 679-685)
-        static const char *const kVanguardMode[] = {"none", "per-pair seed and recovery passes",
-                                                     "fused per-query pass",
-                                                     "matrix-core lows pass + fused per-query pass"};
-        std::printf("[Profile] 0~2. Initial Matrix Math time: %g ms\n", st.phase_ms[0]);
-        std::printf("[Profile] 3. Select Top-nprobe Clusters time: %g ms\n", st.phase_ms[1]);
-        std::printf("[Profile] 4. Flatten Pairs time: %g ms\n", st.phase_ms[2]);
-        std::printf("[Profile] 7~9. Single-Stage Global Task Pool Pipeline (BITWISE_DECOMP) time: %g ms\n",
-                    st.phase_ms[3]);
-        std::printf("[Profile] vanguard: %s; GPU filter kernels %g ms\n",
-                    kVanguardMode[st.vanguard_mode >= 0 && st.vanguard_mode < 4 ? st.vanguard_mode : 0],
-                    st.filter_ms);
-        std::printf("------------------------------------------\n");
-        std::printf("[Cora-Refine] candidates=%llu refined=%zu refinement_ratio=%.6f\n",
-                    static_cast<unsigned long long>(st.produced), out.refined,
-                    st.produced ? static_cast<double>(out.refined) / static_cast<double>(st.produced)
-                                : 0.0);
-    }
+    print_profile(st, out.refined);
 }
 
 }  // namespace coraanns

@@ -84,7 +84,14 @@ enum cora_search_flags {
      * clusters inside the per-query pass is faster. NO_VANGUARD_MFMA forces the latter,
      * VANGUARD_MFMA the former. */
     CORA_FLAG_NO_VANGUARD_MFMA = 1u << 9,
-    CORA_FLAG_VANGUARD_MFMA = 1u << 10
+    CORA_FLAG_VANGUARD_MFMA = 1u << 10,
+    /* GPU-final top-k: the candidates' refined distances, which the fused vanguard pass and
+     * the refined pre-filter compute on the HBM ex-codes with the CPU consumer's formula,
+     * form the final per-query top-k on the GPU (cora_gpu_final_results); nothing goes to
+     * the ring and no CPU refinement runs (the reference's GPU baseline engine refines on
+     * the GPU likewise, src/baselines/gpu.cu:630-700). Needs the ex-codes in HBM, the fused
+     * vanguard pass (topk <= 128, vanguard <= 64) and the refined pre-filter. */
+    CORA_FLAG_GPU_FINAL = 1u << 11
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -199,6 +206,10 @@ int cora_gpu_queue_view(cora_gpu_engine *engine, cora_queue_view *out);
  * Queries already placed in the pinned staging buffer (cora_gpu_query_staging) upload in
  * one DMA; any other host array goes through the runtime's pageable-copy path. */
 int cora_gpu_reset(cora_gpu_engine *engine, const float *h_queries, uint64_t nq);
+/* The final top-k of a search launched with CORA_FLAG_GPU_FINAL, after cora_gpu_sync:
+ * dists [nq][topk] ascending (FLT_MAX pad) and cluster-order vector indexes idx [nq][topk]
+ * (0xFFFFFFFF pad; the ids array of load_from_raw_pointers maps them to ids); ties by index. */
+int cora_gpu_final_results(cora_gpu_engine *engine, float *dists, uint32_t *idx);
 /* Pinned host buffer of [max_q][dim] floats for the queries of the next reset (valid from
  * prepare_workspace to free_workspace). No counterpart in the reference, which uploads
  * from the caller's pageable array. */

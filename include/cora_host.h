@@ -44,6 +44,7 @@ typedef struct cora_hybrid_config {
     int gpu_refine_filter;    /* set_gpu_refine_filter (GPU refined pre-filter) */
     uint32_t extra_flags;     /* set_extra_search_flags (cora_search_flags test modes) */
     float lower_bound_scale;  /* set_lower_bound_scale (0 = keep) */
+    int gpu_final_topk;       /* set_gpu_final_topk */
 } cora_hybrid_config;
 
 typedef struct cora_hybrid_stats {

@@ -19,6 +19,7 @@
 #include "coraanns/search/parameters.hpp"
 
 struct cora_gpu_engine;
+struct cora_search_stats;
 
 namespace coraanns {
 
@@ -110,6 +111,13 @@ class HybridIndex {
     // the bound's confidence are still refined, which the reference CPU path's running
     // threshold does for the vectors it scans early (ivf.hpp:802-817). Range (0, 16].
     void set_lower_bound_scale(float scale);
+    // GPU-final top-k (default off): the GPU forms each query's final top-k from the refined
+    // distances it computes on the HBM ex-codes (fused vanguard pass, refined pre-filter) and
+    // the CPU refines nothing, for searches the CPU refinement would bound (high top-k).
+    // Needs the GPU ex-code stages on, the fused pass's limits (vanguard <= 64, topk <= 128)
+    // and live thresholds; ties in the final distance go to the lower cluster-order index.
+    void set_gpu_final_topk(bool enabled) { gpu_final_topk_ = enabled; }
+    bool get_gpu_final_topk() const { return gpu_final_topk_; }
     float get_lower_bound_scale() const { return bound_scale_; }
     bool get_gpu_seed_refine() const { return gpu_seed_refine_; }
     // CPU refinement threads; 0 = omp_get_max_threads() (the reference always uses the
@@ -141,6 +149,8 @@ class HybridIndex {
 
   private:
     void validate_workspace(std::size_t queries, std::size_t topk, std::size_t nprobe) const;
+    void record_stats(const cora_search_stats &st, std::size_t refined);
+    void print_profile(const cora_search_stats &st, std::size_t refined) const;
 
     cora_gpu_engine *engine_ = nullptr;
     int metric_ = 0;
@@ -168,6 +178,7 @@ class HybridIndex {
     bool gpu_refine_filter_ = true;
     uint32_t extra_flags_ = 0;
     float bound_scale_ = default_bound_scale;
+    bool gpu_final_topk_ = false;
     int cpu_threads_ = 0;
     std::size_t vanguard_size_ = default_vanguard_size;
     KernelType ip_kernel_type_ = KernelType::Lut4Bit;

@@ -502,6 +502,56 @@ def test_live_thresholds_match_frozen_results(synth, mode, topk):
     assert same >= 0.99, same
 
 
+@pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
+@pytest.mark.parametrize("topk", [10, 100])
+@pytest.mark.parametrize("lows", [False, True])
+def test_gpu_final_topk_matches_cpu_refinement(case_name, topk, lows, request):
+    """GPU-final top-k (the GPU forms the final top-k from the refined distances it computed
+    on the HBM ex-codes; nothing published to the ring) against the CPU consumer's top-k of
+    the same search: distances within the rounding bound of the two evaluations, ids equal
+    except where distances tie within it. Frozen thresholds in the GPU-seeded test mode, so
+    both searches see the same thresholds."""
+    case = request.getfixturevalue(case_name)
+    nprobe, nq = 16, case.queries.shape[0]
+    say(f"[gpu] GPU-final top-{topk} vs CPU refinement on {case_name} lows={lows}")
+    flags = ca.FLAG_GPU_SEED_FROZEN | (ca.FLAG_VANGUARD_MFMA if lows else 0)
+    res = {}
+    for final in (False, True):
+        eng = make_engine(case, nprobe, topk, vanguard=5, frozen=True, extra_flags=flags, gpu_final_topk=final)
+        eng.reset_buffer(case.queries)
+        res[final] = eng.search(case.queries, topk, nprobe)
+        st = eng.stats()
+        if final:
+            assert st["refined"] == 0 and st["submitted"] > 0
+        eng.close()
+    (dc, ic), (dg, ig) = res[False], res[True]
+    for q in range(nq):
+        scale = np.abs(dc[q][dc[q] < F32_MAX]).max() + 1
+        tol = 2e-4 * scale  # both sides' rounding bounds of the refined distance
+        assert np.allclose(dg[q], dc[q], rtol=0, atol=tol), q
+        for r in range(topk):
+            if ig[q, r] != ic[q, r]:
+                close = np.abs(dc[q] - dg[q, r]) <= tol
+                assert ig[q, r] in set(ic[q][close].tolist()), (q, r)
+
+
+def test_gpu_final_topk_rejects_unsupported_modes(synth):
+    eng = make_engine(synth, 8, 10, vanguard=5, frozen=True, gpu_final_topk=True)
+    eng.reset_buffer(synth.queries)
+    with pytest.raises(ca.LogicError):  # frozen thresholds without the GPU-seeded test mode
+        eng.search(synth.queries, 10, 8)
+    eng.configure(vanguard_size=5, frozen_thresholds=False, metric=synth.file.metric, gpu_final_topk=True,
+                  extra_flags=ca.FLAG_PAIR_SEEDS)
+    eng.reset_buffer(synth.queries)
+    with pytest.raises(ca.LogicError):  # the per-pair passes publish unrefined seeds
+        eng.search(synth.queries, 10, 8)
+    eng.configure(vanguard_size=5, metric=synth.file.metric, gpu_final_topk=True)
+    eng.reset_buffer(synth.queries)
+    d, i = eng.search(synth.queries, 10, 8)  # live thresholds: supported
+    assert np.all(d[:, 0] < F32_MAX)
+    eng.close()
+
+
 def test_vanguard_mode_reported(synth):
     """Which vanguard passes ran is reported, including the fallback to the per-pair passes
     beyond the fused pass's limits (top-k above 128)."""
