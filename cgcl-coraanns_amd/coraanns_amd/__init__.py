@@ -121,7 +121,7 @@ class cora_hybrid_stats(C.Structure):
 class cora_ivf_info(C.Structure):
     _fields_ = [("num", C.c_uint64), ("dim", C.c_uint64), ("padded_dim", C.c_uint64),
                 ("nlist", C.c_uint64), ("ex_bits", C.c_uint64), ("max_cluster", C.c_uint64),
-                ("metric", C.c_int)]
+                ("metric", C.c_int), ("centroid_storage", C.c_int)]
 
 
 class cora_ivf_arrays(C.Structure):
@@ -261,6 +261,7 @@ class IvfIndex:
         self.num, self.dim, self.padded_dim = info.num, info.dim, info.padded_dim
         self.nlist, self.ex_bits, self.max_cluster, self.metric = (info.nlist, info.ex_bits,
                                                                    info.max_cluster, info.metric)
+        self.centroid_storage = "hnsw_sidecar" if info.centroid_storage == 1 else "embedded"
         ar = cora_ivf_arrays()
         host.cora_ivf_arrays_get(h, C.byref(ar))
         P, n, nl = self.padded_dim, self.num, self.nlist

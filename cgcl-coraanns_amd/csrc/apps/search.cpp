@@ -257,7 +257,8 @@ int main(int argc, char **argv) {
             throw std::invalid_argument("query-chunk must be positive");
 
         std::cout << "Initializing GPU Index..." << std::endl;
-        coraanns::index::IvfFile ivf = coraanns::index::IvfFile::load(argv[1]);
+        // header first (shape checks before the payload is read), then one streaming pass
+        const coraanns::index::IvfHeader ivf = coraanns::index::IvfReader(argv[1]).header();
         const int metric = ivf.metric;
         if (topk == 0 || rounds == 0 || nq == 0 || gt.rows() != nq || dim != ivf.dim || gt.cols() < topk)
             throw std::invalid_argument("query/ground-truth/index shapes do not match");
@@ -294,8 +295,12 @@ int main(int argc, char **argv) {
         const auto nprobes = parse_nprobes(opt.get("nprobes", ""), ivf.nlist);
         const std::size_t max_nprobe = *std::max_element(nprobes.begin(), nprobes.end());
         coraanns::validate_search_shape(chunk, topk, max_nprobe, ivf.nlist, ivf.padded_dim);
-        const std::vector<uint32_t> ids = ivf.ids;
-        coraanns::index::SearchData packed(ivf, !exact, static_cast<int>(threads));
+        std::vector<uint32_t> ids;
+        const std::unique_ptr<coraanns::index::SearchData> packed_ptr =
+            coraanns::index::SearchData::load(argv[1], !exact, static_cast<int>(threads), nullptr, &ids);
+        const coraanns::index::SearchData &packed = *packed_ptr;
+        if (ivf.centroid_storage == coraanns::index::CentroidStorage::HnswSidecar)
+            std::cout << "Centroids: HNSW sidecar " << argv[1] << ".hnsw" << std::endl;
         coraanns::HybridIndex engine;
         engine.set_profiling(profile);
         engine.set_candidate_stats(cand_stats);

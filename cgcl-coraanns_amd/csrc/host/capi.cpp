@@ -29,9 +29,9 @@ struct cora_hybrid {
 };
 
 struct cora_ivf {
-    index::IvfFile file;
+    index::IvfHeader header;
+    std::vector<uint32_t> ids;
     std::unique_ptr<index::SearchData> data;
-    bool extended = false;
 };
 
 namespace {
@@ -217,9 +217,7 @@ int cora_ivf_load(const char *path, int include_extended, cora_ivf **out) {
     *out = nullptr;
     return guarded([&] {
         auto v = std::make_unique<cora_ivf>();
-        v->file = index::IvfFile::load(path);
-        v->extended = include_extended != 0;
-        v->data = std::make_unique<index::SearchData>(v->file, v->extended, 0);
+        v->data = index::SearchData::load(path, include_extended != 0, 0, &v->header, &v->ids);
         *out = v.release();
     });
 }
@@ -227,13 +225,14 @@ int cora_ivf_load(const char *path, int include_extended, cora_ivf **out) {
 int cora_ivf_info_get(const cora_ivf *v, cora_ivf_info *out) {
     NEED(v);
     NEED(out);
-    out->num = v->file.num;
-    out->dim = v->file.dim;
-    out->padded_dim = v->file.padded_dim;
-    out->nlist = v->file.nlist;
-    out->ex_bits = v->file.ex_bits;
+    out->num = v->header.num;
+    out->dim = v->header.dim;
+    out->padded_dim = v->header.padded_dim;
+    out->nlist = v->header.nlist;
+    out->ex_bits = v->header.ex_bits;
     out->max_cluster = v->data->max_cluster_size;
-    out->metric = v->file.metric;
+    out->metric = v->header.metric;
+    out->centroid_storage = static_cast<int>(v->header.centroid_storage);
     return CORA_OK;
 }
 
@@ -247,7 +246,7 @@ int cora_ivf_arrays_get(const cora_ivf *v, cora_ivf_arrays *out) {
     out->short_factors = d.host_short_factors.data();
     out->long_codes = d.host_long_codes;
     out->ex_factors = d.host_ex_factors.empty() ? nullptr : d.host_ex_factors.data();
-    out->ids = v->file.ids.data();
+    out->ids = v->ids.data();
     out->cluster_sizes = reinterpret_cast<const uint64_t *>(d.cluster_sizes.data());
     return CORA_OK;
 }

@@ -1,13 +1,19 @@
 // IVF file I/O, SearchData adaptation and index construction (host side of the
 // "src/index" layer). See include/coraanns/index/*.hpp for the formats.
+#include <fcntl.h>
 #include <omp.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <atomic>
+#include <cerrno>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <future>
 #include <limits>
 #include <numeric>
 #include <queue>
@@ -27,11 +33,19 @@ namespace {
 // FastScan interleave of 16 vectors in a 32-vector block (fastscan.hpp:40-42).
 constexpr int kPerm0[16] = {0, 8, 1, 9, 2, 10, 3, 11, 4, 12, 5, 13, 6, 14, 7, 15};
 
-template <class T>
-void read_exact(std::ifstream &in, T *dst, std::size_t count, const char *what) {
-    in.read(reinterpret_cast<char *>(dst), static_cast<std::streamsize>(count * sizeof(T)));
-    if (!in)
-        throw std::runtime_error(std::string("truncated IVF index while reading ") + what);
+// Streaming loads read the batch and ex sections in chunks of about this size
+// (CORA_IVF_CHUNK_BYTES in the environment overrides it; a chunk always holds at least one
+// cluster or record).
+constexpr uint64_t kStreamChunkBytes = uint64_t{64} << 20;
+
+uint64_t stream_chunk_bytes() {
+    if (const char *e = std::getenv("CORA_IVF_CHUNK_BYTES")) {
+        char *end = nullptr;
+        const unsigned long long v = std::strtoull(e, &end, 10);
+        if (end != e && *end == '\0' && v > 0)
+            return v;
+    }
+    return kStreamChunkBytes;
 }
 
 template <class T>
@@ -41,57 +55,248 @@ void write_all(std::ofstream &out, const T *src, std::size_t count) {
 
 std::size_t round_up(std::size_t v, std::size_t m) { return (v + m - 1) / m * m; }
 
+// Exactly `bytes` from `offset` (EINTR and short reads retried).
+void pread_exact(int fd, uint64_t offset, uint64_t bytes, void *dst, const std::string &file, const char *what) {
+    char *p = static_cast<char *>(dst);
+    while (bytes) {
+        const std::size_t want = static_cast<std::size_t>(std::min<uint64_t>(bytes, uint64_t{1} << 30));
+        const ssize_t got = ::pread(fd, p, want, static_cast<off_t>(offset));
+        if (got < 0 && errno == EINTR)
+            continue;
+        if (got < 0)
+            throw std::runtime_error(std::string("read error (") + std::strerror(errno) + ") in " + file +
+                                     " while reading " + what);
+        if (got == 0)
+            throw std::runtime_error("truncated file " + file + " while reading " + what);
+        p += got;
+        offset += static_cast<uint64_t>(got);
+        bytes -= static_cast<uint64_t>(got);
+    }
+}
+
+uint64_t file_size(int fd, const std::string &file) {
+    struct stat st;
+    if (::fstat(fd, &st) != 0 || st.st_size < 0)
+        throw std::runtime_error("cannot stat " + file);
+    return static_cast<uint64_t>(st.st_size);
+}
+
+struct FdGuard {
+    int fd;
+    ~FdGuard() {
+        if (fd >= 0)
+            ::close(fd);
+    }
+};
+
+uint64_t batch_blocks(const IvfHeader &h) {
+    uint64_t b = 0;
+    for (uint64_t s : h.cluster_sizes)
+        b += (s + 31) / 32;
+    return b;
+}
+
+// Words and factors of one cluster's FastScan blocks into the SearchData arrays (cluster
+// starts at global vector s; words are word-major within the cluster, search_data.cpp:45-82).
+void unpack_cluster(const uint8_t *blocks, std::size_t n, std::size_t s, std::size_t P, uint32_t *short_data,
+                    float *short_factors, std::vector<uint32_t> &words) {
+    const std::size_t W = P / 32, block_bytes = P * 4 + 32 * 12;
+    words.resize(32 * W);
+    for (std::size_t i = 0; i < n; i += 32) {
+        const uint8_t *blk = blocks + (i / 32) * block_bytes;
+        const std::size_t len = std::min<std::size_t>(32, n - i);
+        unpack_fastscan_block(blk, P, len, words.data());
+        const float *fl = reinterpret_cast<const float *>(blk + P * 4);
+        for (std::size_t v = 0; v < len; ++v) {
+            for (std::size_t w = 0; w < W; ++w)
+                short_data[s * W + w * n + i + v] = words[v * W + w];
+            short_factors[(s + i + v) * 3 + 0] = fl[v];
+            short_factors[(s + i + v) * 3 + 1] = fl[32 + v];
+            short_factors[(s + i + v) * 3 + 2] = fl[64 + v];
+        }
+    }
+}
+
 }  // namespace
 
-IvfFile IvfFile::load(const std::string &path) {
-    std::ifstream in(path, std::ios::binary);
-    if (!in)
+// ------------------------------------------------------------------------------------
+// Reading (IVF::load, ivf.hpp:447-539; HNSWInitializer::load, initializer.hpp:255-279)
+// ------------------------------------------------------------------------------------
+IvfReader::IvfReader(const std::string &path) : path_(path) {
+    fd_ = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd_ < 0)
         throw std::runtime_error("Cannot open IVF index: " + path);
-    IvfFile f;
-    uint64_t hdr[4];
-    read_exact(in, hdr, 4, "header");
-    f.num = hdr[0];
-    f.dim = hdr[1];
-    f.nlist = hdr[2];
-    f.ex_bits = hdr[3];
-    read_exact(in, &f.rotator_type, 1, "rotator type");
-    read_exact(in, &f.metric, 1, "metric");
-    if (f.rotator_type != 0)
-        throw std::runtime_error("only MatrixRotator indexes are supported");
-    if (f.metric > 1 || f.ex_bits > 8 || f.dim == 0 || f.nlist == 0 || f.num == 0)
-        throw std::runtime_error("invalid IVF header");
-    f.padded_dim = round_up(f.dim, 64);
-    f.cluster_sizes.resize(f.nlist);
-    read_exact(in, f.cluster_sizes.data(), f.nlist, "cluster sizes");
-    uint64_t total = 0, blocks = 0;
-    for (uint64_t s : f.cluster_sizes) {
-        total += s;
-        blocks += (s + 31) / 32;
+    try {
+        const uint64_t size = file_size(fd_, path);
+        uint64_t hdr[4];
+        read_at(0, sizeof(hdr), hdr, "header");
+        h_.num = hdr[0];
+        h_.dim = hdr[1];
+        h_.nlist = hdr[2];
+        h_.ex_bits = hdr[3];
+        uint8_t tm[2];
+        read_at(32, 2, tm, "rotator type and metric");
+        h_.rotator_type = tm[0];
+        h_.metric = tm[1];
+        if (h_.rotator_type != 0)
+            throw std::runtime_error("only MatrixRotator indexes are supported");
+        // the reference's ids are u32 (defines.hpp PID); the dimension bound keeps every
+        // byte count below 2^64
+        if (h_.metric > 1 || h_.ex_bits > 8 || h_.dim == 0 || h_.dim > (uint64_t{1} << 20) || h_.nlist == 0 ||
+            h_.num == 0 || h_.num > (uint64_t{1} << 32))
+            throw std::runtime_error("invalid IVF header");
+        h_.padded_dim = round_up(h_.dim, 64);
+        if (h_.nlist > (size - 34) / 8)
+            throw std::runtime_error("truncated IVF index while reading cluster sizes");
+        h_.cluster_sizes.resize(h_.nlist);
+        read_at(34, 8 * h_.nlist, h_.cluster_sizes.data(), "cluster sizes");
+        uint64_t total = 0;
+        for (uint64_t s : h_.cluster_sizes) {
+            if (s > h_.num - total)
+                throw std::runtime_error("The sum of cluster num != total number of points");
+            total += s;
+        }
+        if (total != h_.num)
+            throw std::runtime_error("The sum of cluster num != total number of points");
+        rotator_off_ = 34 + 8 * h_.nlist;
+        const uint64_t rot_bytes = 4 * h_.dim * h_.padded_dim;
+        if (rot_bytes > size - rotator_off_)
+            throw std::runtime_error("truncated IVF index while reading rotator");
+        // the stored representation of the centroids follows from the bytes left
+        // (ivf.hpp:487-520)
+        const uint64_t here = rotator_off_ + rot_bytes, remaining = size - here;
+        const uint64_t batch_bytes = batch_blocks(h_) * h_.batch_block_bytes();
+        const uint64_t payload = batch_bytes + h_.ex_stride() * h_.num + 4 * h_.num;
+        const uint64_t cent_bytes = 4 * h_.padded_dim * h_.nlist;
+        if (remaining == payload + cent_bytes) {
+            h_.centroid_storage = CentroidStorage::Embedded;
+            centroid_off_ = here;
+            batch_off_ = here + cent_bytes;
+        } else if (remaining == payload) {
+            h_.centroid_storage = CentroidStorage::HnswSidecar;
+            batch_off_ = here;
+        } else {
+            throw std::runtime_error("IVF index size does not match a supported centroid layout");
+        }
+        ex_off_ = batch_off_ + batch_bytes;
+        ids_off_ = ex_off_ + h_.ex_stride() * h_.num;
+    } catch (...) {
+        ::close(fd_);
+        fd_ = -1;
+        throw;
     }
-    if (total != f.num)
-        throw std::runtime_error("The sum of cluster num != total number of points");
-    f.rotator.resize(f.dim * f.padded_dim);
-    read_exact(in, f.rotator.data(), f.rotator.size(), "rotator");
-    const std::streampos here = in.tellg();
-    in.seekg(0, std::ios::end);
-    const std::streampos end = in.tellg();
-    in.seekg(here);
-    const uint64_t remaining = static_cast<uint64_t>(end - here);
-    const uint64_t batch_bytes = blocks * f.batch_block_bytes();
-    const uint64_t payload = batch_bytes + f.ex_stride() * f.num + 4 * f.num;
-    const uint64_t cent_bytes = 4 * f.padded_dim * f.nlist;
-    if (remaining == payload)
-        throw std::runtime_error("IVF index keeps its centroids in an HNSW sidecar; unsupported");
-    if (remaining != payload + cent_bytes)
-        throw std::runtime_error("IVF index size does not match a supported centroid layout");
-    f.centroids.resize(f.nlist * f.padded_dim);
-    read_exact(in, f.centroids.data(), f.centroids.size(), "centroids");
-    f.batch_data.resize(batch_bytes);
-    read_exact(in, f.batch_data.data(), batch_bytes, "batch data");
+}
+
+IvfReader::~IvfReader() {
+    if (fd_ >= 0)
+        ::close(fd_);
+}
+
+void IvfReader::read_at(uint64_t offset, uint64_t bytes, void *dst, const char *what) const {
+    pread_exact(fd_, offset, bytes, dst, path_, what);
+}
+
+std::vector<float> IvfReader::read_rotator() const {
+    std::vector<float> r(h_.dim * h_.padded_dim);
+    read_at(rotator_off_, 4 * r.size(), r.data(), "rotator");
+    return r;
+}
+
+std::vector<float> IvfReader::read_centroids() const {
+    if (h_.centroid_storage == CentroidStorage::HnswSidecar)
+        return read_hnsw_centroids(path_ + ".hnsw", h_.nlist, h_.padded_dim);
+    std::vector<float> c(h_.nlist * h_.padded_dim);
+    read_at(centroid_off_, 4 * c.size(), c.data(), "centroids");
+    return c;
+}
+
+void IvfReader::read_batch_blocks(uint64_t first, uint64_t count, uint8_t *dst) const {
+    read_at(batch_off_ + first * h_.batch_block_bytes(), count * h_.batch_block_bytes(), dst, "batch data");
+}
+
+void IvfReader::read_ex_records(uint64_t first, uint64_t count, uint8_t *dst) const {
+    read_at(ex_off_ + first * h_.ex_stride(), count * h_.ex_stride(), dst, "ex data");
+}
+
+void IvfReader::read_ids(uint32_t *dst) const { read_at(ids_off_, 4 * h_.num, dst, "ids"); }
+
+std::vector<float> read_hnsw_centroids(const std::string &sidecar, uint64_t nlist, uint64_t padded_dim) {
+    FdGuard g{::open(sidecar.c_str(), O_RDONLY | O_CLOEXEC)};
+    if (g.fd < 0)
+        throw std::runtime_error("Cannot open HNSW centroid sidecar: " + sidecar);
+    const uint64_t size = file_size(g.fd, sidecar);
+    // saveIndex header (hnswalg.h:689-702): six size_t, int maxlevel_, u32 enterpoint_node_,
+    // size_t maxM_, maxM0_, M_, double mult_, size_t ef_construction_
+    constexpr uint64_t kHeader = 6 * 8 + 4 + 4 + 3 * 8 + 8 + 8;
+    unsigned char hb[kHeader];
+    if (size < kHeader)
+        throw std::runtime_error("Index seems to be corrupted or unsupported: " + sidecar);
+    pread_exact(g.fd, 0, kHeader, hb, sidecar, "HNSW header");
+    uint64_t count, per_element, label_off, data_off;
+    std::memcpy(&count, hb + 16, 8);
+    std::memcpy(&per_element, hb + 24, 8);
+    std::memcpy(&label_off, hb + 32, 8);
+    std::memcpy(&data_off, hb + 40, 8);
+    if (count != nlist)
+        throw std::runtime_error("HNSW centroid count does not match the IVF cluster count");
+    const uint64_t vec_bytes = 4 * padded_dim;
+    if (per_element == 0 || label_off > per_element || per_element - label_off < 8 || data_off > label_off ||
+        label_off - data_off != vec_bytes)
+        throw std::runtime_error("HNSW centroid sidecar does not hold vectors of padded_dim floats: " + sidecar);
+    if (count > (size - kHeader) / per_element)
+        throw std::runtime_error("Index seems to be corrupted or unsupported: " + sidecar);
+    // upper-level link lists: a u32 size and that many bytes per element, ending exactly at
+    // the end of the file (the check of hnswalg.h:754-770)
+    const uint64_t links_off = kHeader + count * per_element;
+    {
+        std::vector<unsigned char> links(size - links_off);
+        if (!links.empty())
+            pread_exact(g.fd, links_off, links.size(), links.data(), sidecar, "HNSW link lists");
+        uint64_t pos = 0;
+        for (uint64_t i = 0; i < count; ++i) {
+            if (pos >= links.size() || links.size() - pos < 4)
+                throw std::runtime_error("Index seems to be corrupted or unsupported: " + sidecar);
+            uint32_t len;
+            std::memcpy(&len, links.data() + pos, 4);
+            pos += 4 + static_cast<uint64_t>(len);
+        }
+        if (pos != links.size())
+            throw std::runtime_error("Index seems to be corrupted or unsupported: " + sidecar);
+    }
+    std::vector<float> cent(nlist * padded_dim);
+    std::vector<uint8_t> seen(nlist, 0);
+    const uint64_t per_chunk = std::max<uint64_t>(1, stream_chunk_bytes() / per_element);
+    std::vector<unsigned char> buf;
+    for (uint64_t e0 = 0; e0 < count; e0 += per_chunk) {
+        const uint64_t m = std::min(per_chunk, count - e0);
+        buf.resize(m * per_element);
+        pread_exact(g.fd, kHeader + e0 * per_element, buf.size(), buf.data(), sidecar, "HNSW level-0 elements");
+        for (uint64_t e = 0; e < m; ++e) {
+            const unsigned char *el = buf.data() + e * per_element;
+            uint64_t label;
+            std::memcpy(&label, el + label_off, 8);
+            if (label >= nlist || seen[label])
+                throw std::runtime_error("Invalid or duplicate HNSW centroid label");
+            seen[label] = 1;
+            std::memcpy(cent.data() + label * padded_dim, el + data_off, vec_bytes);
+        }
+    }
+    return cent;
+}
+
+IvfFile IvfFile::load(const std::string &path) {
+    const IvfReader rd(path);
+    IvfFile f;
+    static_cast<IvfHeader &>(f) = rd.header();
+    f.rotator = rd.read_rotator();
+    f.centroids = rd.read_centroids();
+    uint64_t blocks = batch_blocks(f);
+    f.batch_data.resize(blocks * f.batch_block_bytes());
+    rd.read_batch_blocks(0, blocks, f.batch_data.data());
     f.ex_data.resize(f.ex_stride() * f.num);
-    read_exact(in, f.ex_data.data(), f.ex_data.size(), "ex data");
+    rd.read_ex_records(0, f.ex_stride() ? f.num : 0, f.ex_data.data());
     f.ids.resize(f.num);
-    read_exact(in, f.ids.data(), f.num, "ids");
+    rd.read_ids(f.ids.data());
     return f;
 }
 
@@ -156,23 +361,14 @@ SearchData::SearchData(IvfFile &src, bool include_extended, int cpu_threads) {
     }
     const std::size_t block_bytes = src.batch_block_bytes();
     const int threads = cpu_threads > 0 ? cpu_threads : omp_get_max_threads();
-#pragma omp parallel for schedule(dynamic, 16) num_threads(threads)
-    for (long long cl = 0; cl < static_cast<long long>(src.nlist); ++cl) {
-        const std::size_t c = static_cast<std::size_t>(cl);
-        const std::size_t n = cluster_sizes[c], s = start[c];
-        std::vector<uint32_t> words(32 * W);
-        for (std::size_t i = 0; i < n; i += 32) {
-            const uint8_t *blk = src.batch_data.data() + (block0[c] + i / 32) * block_bytes;
-            const std::size_t len = std::min<std::size_t>(32, n - i);
-            unpack_fastscan_block(blk, P, len, words.data());
-            const float *fl = reinterpret_cast<const float *>(blk + P * 4);
-            for (std::size_t v = 0; v < len; ++v) {
-                for (std::size_t w = 0; w < W; ++w)
-                    host_short_data[s * W + w * n + i + v] = words[v * W + w];
-                host_short_factors[(s + i + v) * 3 + 0] = fl[v];
-                host_short_factors[(s + i + v) * 3 + 1] = fl[32 + v];
-                host_short_factors[(s + i + v) * 3 + 2] = fl[64 + v];
-            }
+#pragma omp parallel num_threads(threads)
+    {
+        std::vector<uint32_t> words;
+#pragma omp for schedule(dynamic, 16)
+        for (long long cl = 0; cl < static_cast<long long>(src.nlist); ++cl) {
+            const std::size_t c = static_cast<std::size_t>(cl);
+            unpack_cluster(src.batch_data.data() + block0[c] * block_bytes, cluster_sizes[c], start[c], P,
+                           host_short_data.data(), host_short_factors.data(), words);
         }
     }
     if (include_extended && src.ex_bits > 0) {
@@ -188,10 +384,120 @@ SearchData::SearchData(IvfFile &src, bool include_extended, int cpu_threads) {
             host_ex_factors[2 * i + 1] = f[1];
             std::memmove(ex + i * lc, rec, lc);  // destination never passes the source
         }
+        // the storage keeps its ex-data capacity (no shrinking copy of a multi-GB array)
         extended_storage_.resize(N * lc);
-        extended_storage_.shrink_to_fit();
         host_long_codes = extended_storage_.data();
     }
+}
+
+std::unique_ptr<SearchData> SearchData::load(const std::string &path, bool include_extended, int cpu_threads,
+                                             IvfHeader *header, std::vector<uint32_t> *ids) {
+    const IvfReader rd(path);
+    const IvfHeader &h = rd.header();
+    const std::size_t P = h.padded_dim, W = P / 32, N = h.num, nl = h.nlist;
+    const int threads = cpu_threads > 0 ? cpu_threads : omp_get_max_threads();
+    std::unique_ptr<SearchData> sd(new SearchData());
+    sd->host_rotator = rd.read_rotator();
+    sd->h_centroids = rd.read_centroids();
+    sd->cluster_sizes.assign(h.cluster_sizes.begin(), h.cluster_sizes.end());
+    for (std::size_t s : sd->cluster_sizes)
+        sd->max_cluster_size = std::max(sd->max_cluster_size, s);
+    sd->host_short_data.assign(N * W, 0u);
+    sd->host_short_factors.assign(N * 3, 0.0f);
+
+    // Chunked pipeline: chunk k+1 is read by a reader thread while chunk k is unpacked.
+    // `plan` gives the item ranges, `read` fills a buffer, `work` consumes it.
+    auto pipeline = [](const std::vector<std::pair<uint64_t, uint64_t>> &plan, auto read, auto work) {
+        std::vector<uint8_t> buf[2];
+        std::future<void> pending;
+        if (!plan.empty())
+            pending = std::async(std::launch::async, [&] { read(plan[0], buf[0]); });
+        for (std::size_t k = 0; k < plan.size(); ++k) {
+            pending.get();
+            if (k + 1 < plan.size())
+                pending = std::async(std::launch::async, [&, k] { read(plan[k + 1], buf[(k + 1) & 1]); });
+            try {
+                work(plan[k], buf[k & 1]);
+            } catch (...) {
+                if (pending.valid())
+                    pending.wait();
+                throw;
+            }
+        }
+    };
+
+    // batch data: whole clusters per chunk (a chunk holds at least one cluster)
+    std::vector<uint64_t> start(nl + 1, 0), block0(nl + 1, 0);
+    for (std::size_t c = 0; c < nl; ++c) {
+        start[c + 1] = start[c] + h.cluster_sizes[c];
+        block0[c + 1] = block0[c] + (h.cluster_sizes[c] + 31) / 32;
+    }
+    const uint64_t block_bytes = h.batch_block_bytes(), chunk = stream_chunk_bytes();
+    std::vector<std::pair<uint64_t, uint64_t>> cplan;  // cluster ranges [c0, c1)
+    for (uint64_t c0 = 0; c0 < nl;) {
+        uint64_t c1 = c0 + 1;
+        while (c1 < nl && (block0[c1 + 1] - block0[c0]) * block_bytes <= chunk)
+            ++c1;
+        cplan.emplace_back(c0, c1);
+        c0 = c1;
+    }
+    pipeline(
+        cplan,
+        [&](std::pair<uint64_t, uint64_t> r, std::vector<uint8_t> &buf) {
+            const uint64_t nb = block0[r.second] - block0[r.first];
+            buf.resize(nb * block_bytes);
+            rd.read_batch_blocks(block0[r.first], nb, buf.data());
+        },
+        [&](std::pair<uint64_t, uint64_t> r, std::vector<uint8_t> &buf) {
+#pragma omp parallel num_threads(threads)
+            {
+                std::vector<uint32_t> words;
+#pragma omp for schedule(dynamic, 16)
+                for (long long cl = static_cast<long long>(r.first); cl < static_cast<long long>(r.second); ++cl) {
+                    const std::size_t c = static_cast<std::size_t>(cl);
+                    unpack_cluster(buf.data() + (block0[c] - block0[r.first]) * block_bytes, h.cluster_sizes[c],
+                                   start[c], P, sd->host_short_data.data(), sd->host_short_factors.data(), words);
+                }
+            }
+        });
+
+    // ex data: records split into the dense code array and the factor pairs
+    // (search_data.cpp:84-123 compacts the same split in place)
+    if (include_extended && h.ex_bits > 0) {
+        const std::size_t lc = h.ex_code_bytes(), stride = h.ex_stride();
+        sd->host_ex_factors.assign(N * 2, 0.0f);
+        sd->extended_storage_.resize(N * lc);
+        const uint64_t per = std::max<uint64_t>(1, chunk / stride);
+        std::vector<std::pair<uint64_t, uint64_t>> vplan;
+        for (uint64_t v0 = 0; v0 < N; v0 += per)
+            vplan.emplace_back(v0, std::min<uint64_t>(N, v0 + per));
+        uint8_t *codes = sd->extended_storage_.data();
+        float *fac = sd->host_ex_factors.data();
+        pipeline(
+            vplan,
+            [&](std::pair<uint64_t, uint64_t> r, std::vector<uint8_t> &buf) {
+                buf.resize((r.second - r.first) * stride);
+                rd.read_ex_records(r.first, r.second - r.first, buf.data());
+            },
+            [&](std::pair<uint64_t, uint64_t> r, std::vector<uint8_t> &buf) {
+                const long long n = static_cast<long long>(r.second - r.first);
+#pragma omp parallel for schedule(static) num_threads(threads)
+                for (long long i = 0; i < n; ++i) {
+                    const uint8_t *rec = buf.data() + static_cast<std::size_t>(i) * stride;
+                    const std::size_t v = r.first + static_cast<std::size_t>(i);
+                    std::memcpy(codes + v * lc, rec, lc);
+                    std::memcpy(fac + 2 * v, rec + lc, 2 * sizeof(float));
+                }
+            });
+        sd->host_long_codes = codes;
+    }
+    if (ids) {
+        ids->resize(N);
+        rd.read_ids(ids->data());
+    }
+    if (header)
+        *header = h;
+    return sd;
 }
 
 // ------------------------------------------------------------------------------------

@@ -103,6 +103,7 @@ float cora_hybrid_lower_bound_scale(cora_hybrid *h);
 typedef struct cora_ivf_info {
     uint64_t num, dim, padded_dim, nlist, ex_bits, max_cluster;
     int metric;
+    int centroid_storage; /* 0 = embedded in the index, 1 = "<index>.hnsw" sidecar (ivf.hpp:487-520) */
 } cora_ivf_info;
 typedef struct cora_ivf_arrays {
     const float *centroids;     /* [nlist][P] */
@@ -114,6 +115,8 @@ typedef struct cora_ivf_arrays {
     const uint32_t *ids;        /* [num] */
     const uint64_t *cluster_sizes; /* [nlist] */
 } cora_ivf_arrays;
+/* IVF::load (ivf.hpp:447-539) + SearchData (search_data.cpp:9-127) in one streaming pass:
+ * centroids embedded or from the HNSW sidecar, batch and ex data read in bounded chunks. */
 int cora_ivf_load(const char *path, int include_extended, cora_ivf **out);
 int cora_ivf_info_get(const cora_ivf *ivf, cora_ivf_info *out);
 int cora_ivf_arrays_get(const cora_ivf *ivf, cora_ivf_arrays *out);

@@ -2,12 +2,14 @@
 // (reference include/coraanns/index/search_data.hpp:14-30, src/index/search_data.cpp:9-127):
 // FastScan-packed sign codes unpacked to per-cluster word-major u32 words (dimension
 // 32w+l at bit 31-l of word w), AoS short factors, ex-codes compacted to a dense
-// [num][padded_dim*ex_bits/8] array (taking over the IVF's ex-data storage), and the
-// rotator. The engine builds its GPU tile layout from these arrays.
+// [num][padded_dim*ex_bits/8] array, and the rotator. The engine builds its GPU tile
+// layout from these arrays.
 #pragma once
 
 #include <cstddef>
 #include <cstdint>
+#include <memory>
+#include <string>
 #include <vector>
 
 #include "coraanns/index/ivf_file.hpp"
@@ -16,8 +18,20 @@ namespace coraanns::index {
 
 class SearchData {
   public:
+    // From an index already in memory (the reference constructor's signature). The
+    // ex-codes are compacted in the IVF's own ex-data storage, which SearchData takes over.
     // include_extended = false keeps only the short codes (exact FP32 refine mode).
     SearchData(IvfFile &source, bool include_extended, int cpu_threads = 0);
+
+    // Streaming load straight from an index file: batch data and ex data are read in
+    // bounded chunks (a reader thread overlaps the next read with the unpacking of the
+    // current chunk), so the peak host memory is the adapted arrays plus two chunks, not
+    // the file plus the arrays. header / ids (may be null) receive the file's header and
+    // the cluster-order ids.
+    static std::unique_ptr<SearchData> load(const std::string &path, bool include_extended,
+                                            int cpu_threads = 0, IvfHeader *header = nullptr,
+                                            std::vector<uint32_t> *ids = nullptr);
+
     std::vector<float> h_centroids, host_rotator, host_short_factors, host_ex_factors;
     std::vector<uint32_t> host_short_data;
     std::vector<std::size_t> cluster_sizes;
@@ -25,6 +39,7 @@ class SearchData {
     std::size_t max_cluster_size = 0;
 
   private:
+    SearchData() = default;
     std::vector<uint8_t> extended_storage_;
 };
 

@@ -49,11 +49,61 @@ def round_up(x, m):
     return (x + m - 1) // m * m
 
 
+HNSW_HEADER = struct.Struct("<6QiI3QdQ")  # hnswlib saveIndex header (hnswalg.h:689-702)
+
+
+def read_hnsw_centroids(path, nlist: int, P: int) -> np.ndarray:
+    """Centroids of an HNSW sidecar ("<index>.hnsw", HNSWInitializer::save/load,
+    initializer.hpp:255-279). hnswlib's saveIndex (hnswalg.h:685-713) writes a header of
+    offsetLevel0_, max_elements_, cur_element_count, size_data_per_element_, label_offset_,
+    offsetData_ (size_t), maxlevel_ (int), enterpoint_node_ (u32), maxM_, maxM0_, M_ (size_t),
+    mult_ (double), ef_construction_ (size_t); then cur_element_count level-0 elements of
+    size_data_per_element_ bytes (vector at offsetData_, size_t label at label_offset_); then
+    per element a u32 byte count and its upper-level links. Centroid c is the vector labelled
+    c (rebuild_label_to_internal, initializer.hpp:181-198)."""
+    raw = np.fromfile(path, dtype=np.uint8)
+    if raw.size < HNSW_HEADER.size:
+        raise ValueError("Index seems to be corrupted or unsupported")
+    (_, _, count, per, label_off, data_off, _, _, _, _, _, _, _) = HNSW_HEADER.unpack_from(raw.tobytes(), 0)
+    if count != nlist:
+        raise ValueError("HNSW centroid count does not match the IVF cluster count")
+    if label_off - data_off != 4 * P or label_off + 8 > per:
+        raise ValueError("HNSW sidecar vectors are not padded_dim floats")
+    off = HNSW_HEADER.size
+    if off + count * per > raw.size:
+        raise ValueError("Index seems to be corrupted or unsupported")
+    # the loadIndex check (hnswalg.h:754-770): the link lists end exactly at the file end
+    pos = off + count * per
+    for _ in range(count):
+        if pos + 4 > raw.size:
+            raise ValueError("Index seems to be corrupted or unsupported")
+        pos += 4 + int(raw[pos:pos + 4].view(np.uint32)[0])
+    if pos != raw.size:
+        raise ValueError("Index seems to be corrupted or unsupported")
+    el = raw[off:off + count * per].reshape(count, per)
+    labels = el[:, label_off:label_off + 8].copy().view(np.uint64).reshape(count)
+    if np.any(labels >= nlist) or np.unique(labels).size != count:
+        raise ValueError("Invalid or duplicate HNSW centroid label")
+    cent = np.empty((nlist, P), np.float32)
+    cent[labels.astype(np.int64)] = el[:, data_off:data_off + 4 * P].copy().view(np.float32).reshape(count, P)
+    return cent
+
+
+def _centroid_layout(remaining: int, payload: int, nlist: int, P: int) -> str:
+    """Stored centroid representation from the bytes left after the rotator
+    (ivf.hpp:487-520)."""
+    if remaining == payload + 4 * P * nlist:
+        return "embedded"
+    if remaining == payload:
+        return "hnsw_sidecar"
+    raise ValueError("IVF index size does not match a supported centroid layout")
+
+
 def read_ivf(path) -> IVFFile:
     """IVF::load (ivf.hpp:447-539): header of four size_t + two u8, cluster sizes,
-    MatrixRotator [dim x P] (rotator.hpp:89-94), embedded flat centroids
-    (initializer.hpp:147-169), batch data, ex data, ids. P = round_up(dim, 64)
-    (ivf.hpp:242, rotator.hpp:375-405)."""
+    MatrixRotator [dim x P] (rotator.hpp:89-94), the centroids (embedded flat centroids,
+    initializer.hpp:147-169, or none here and an HNSW sidecar "<path>.hnsw"), batch data,
+    ex data, ids. P = round_up(dim, 64) (ivf.hpp:242, rotator.hpp:375-405)."""
     raw = np.fromfile(path, dtype=np.uint8)
     num, dim, nlist, ex_bits = struct.unpack_from("<4Q", raw, 0)
     rtype, metric = raw[32], raw[33]
@@ -67,12 +117,11 @@ def read_ivf(path) -> IVFFile:
     batch_bytes = blocks * (P * 32 // 8 + 32 * 12)
     ex_stride = P * ex_bits // 8 + 8 if ex_bits > 0 else 0
     payload = batch_bytes + ex_stride * num + 4 * num
-    remaining = raw.size - off
-    if remaining == payload + 4 * P * nlist:
+    if _centroid_layout(raw.size - off, payload, nlist, P) == "embedded":
         cent = np.frombuffer(raw, dtype=np.float32, count=nlist * P, offset=off).reshape(nlist, P).copy()
         off += 4 * P * nlist
     else:
-        raise ValueError("only indexes with embedded flat centroids are supported by the oracle")
+        cent = read_hnsw_centroids(str(path) + ".hnsw", nlist, P)
     batch = raw[off:off + batch_bytes].copy()
     off += batch_bytes
     ex = raw[off:off + ex_stride * num].reshape(num, ex_stride).copy()
@@ -217,10 +266,11 @@ def open_ivf_lazy(path) -> LazyIVF:
     blocks = int(nblk.sum())
     batch_bytes = blocks * (P * 32 // 8 + 32 * 12)
     ex_stride = P * ex_bits // 8 + 8
-    if raw.size - off != batch_bytes + ex_stride * num + 4 * num + 4 * P * nlist:
-        raise ValueError("only indexes with embedded flat centroids are supported by the oracle")
-    cent = np.frombuffer(raw[off:off + 4 * P * nlist].tobytes(), dtype=np.float32).reshape(nlist, P).copy()
-    off += 4 * P * nlist
+    if _centroid_layout(raw.size - off, batch_bytes + ex_stride * num + 4 * num, nlist, P) == "embedded":
+        cent = np.frombuffer(raw[off:off + 4 * P * nlist].tobytes(), dtype=np.float32).reshape(nlist, P).copy()
+        off += 4 * P * nlist
+    else:
+        cent = read_hnsw_centroids(str(path) + ".hnsw", nlist, P)
     batch = raw[off:off + batch_bytes]
     off += batch_bytes
     ex = raw[off:off + ex_stride * num].reshape(num, ex_stride)
@@ -675,6 +725,9 @@ def quantize_excode(x: np.ndarray, c: np.ndarray, ex_bits: int) -> np.ndarray:
 
 PINNED = {
     "read_ivf": "golden: ref_dump meta/ids/centroids/rotator (reference IVF::load)",
+    "read_hnsw_centroids": "reference-built sidecar index (coraanns_build_index, nlist 20000): centroids "
+                           "equal ref_dump's (reference IVF::load + HNSWInitializer); permuted-label "
+                           "sidecars equal the embedded centroids; corrupt files rejected",
     "search_data": "golden: ref_dump short_data/short_factors/long_codes/ex_factors (reference SearchData)",
     "open_ivf_lazy": "equals read_ivf on the golden indexes (header arrays, maps, offsets)",
     "cluster_data": "equals the per-cluster slices of search_data on the golden indexes",

@@ -129,3 +129,20 @@ def test_driver_rejects_invalid_options(known_neighbours, bad):
     d = known_neighbours
     r = run_driver([d / "ivf.index", d / "queries.fbin", d / "gt.ibin"] + bad)
     assert r.returncode == 1 and "coraanns_search failed" in r.stderr, (bad, r.stdout, r.stderr)
+
+
+def test_driver_reads_hnsw_sidecar_index(known_neighbours, tmp_path):
+    """An index whose centroids live in an hnswlib sidecar (the reference's form for
+    nlist >= 20000, ivf.hpp:487-520), labels stored out of order: at nprobe 1 every query
+    must probe its own cluster, so a wrong label-to-centroid mapping loses the recall."""
+    from test_ivf_storage import write_sidecar
+    d = known_neighbours
+    side = tmp_path / "side.index"
+    write_sidecar(d / "ivf.index", side, np.array([2, 0, 3, 1]))
+    say("[gpu] coraanns_search on an HNSW-sidecar index")
+    r = run_driver([side, d / "queries.fbin", d / "gt.ibin", "--topk", 1, "--nprobes", "1,4", "--warmup", 0,
+                    "--rounds", 1])
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "Centroids: HNSW sidecar" in r.stdout
+    rows = parse_summary(r.stdout, [1, 4])
+    assert rows[0][2] == 1.0 and rows[1][2] == 1.0, r.stdout
