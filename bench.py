@@ -140,6 +140,9 @@ def main():
                     help="GPU-final top-k: the GPU forms the final top-k from its refined distances, no CPU refinement")
     ap.add_argument("--no-vanguard-mfma", action="store_true",
                     help="vanguard lower bounds inside the per-query pass instead of the matrix-core lows pass")
+    ap.add_argument("--ip-kernel", choices=["bitwise", "lut4"], default="bitwise",
+                    help="estimator: bitwise (Bq=8 popcount bound, the default here) or lut4 (the reference's "
+                         "FP16 nibble-LUT estimator, set_ip_kernel_type(Lut4Bit))")
     ap.add_argument("--fp32-gemm", action="store_true",
                     help="query rotation and coarse-probe distances from the FP32 matrix-core GEMMs instead of the split-FP16 ones")
     ap.add_argument("--workdir", default="",
@@ -196,7 +199,8 @@ def main():
                          gpu_refine_filter=not args.no_gpu_prefilter,
                          extra_flags=(ca.FLAG_FP32_GEMM if args.fp32_gemm else 0) |
                                      (ca.FLAG_NO_VANGUARD_MFMA if args.no_vanguard_mfma else 0),
-                         lower_bound_scale=args.lower_bound_scale or None, gpu_final_topk=args.gpu_final)
+                         lower_bound_scale=args.lower_bound_scale or None, gpu_final_topk=args.gpu_final,
+                         ip_kernel_type=args.ip_kernel)
     eng.load_ivf(ivf)
     chunk = min(queries.shape[0], 65535)
     eng.prepare_workspace(chunk, c.topk, max(c.nprobes))
@@ -296,7 +300,9 @@ def main():
 
     # the dominant scan kernel of the step (HIP events on the engine stream around it)
     W = c.padded_dim // 32
-    mfma_far = W in (2, 4, 6, 8, 16, 24, 32)  # the engine's matrix-core far scan (cross-query reuse is on)
+    lut = args.ip_kernel == "lut4"
+    # the engine's matrix-core far scan (cross-query reuse is on; Bitwise estimator only)
+    mfma_far = W in (2, 4, 6, 8, 16, 24, 32) and not lut
     far_name = (f"far_mfma_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA ip_int/ip_res" if W <= 8 else
                 f"far_mfma_wide_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA 16x16x64 ip_int, popcount "
                 "ip_res for survivors")
@@ -313,7 +319,8 @@ def main():
             "avg_launch_ms": round(avg_lows_ms, 4), "bytes_per_launch": int(lows_bpl), "achieved": lows_achieved},
         "far_mfma_kernel" if mfma_far else "scan_kernel": {
             "kernel": f"{far_name}, units of 16 same-cluster pairs)" if mfma_far else
-                      f"scan_kernel<{W}, {8 if batch_q > 1 else 1}, 0> (far-pair RaBitQ popcount scan)",
+                      f"scan_kernel<0, {4 if batch_q > 1 else 1}, 0, 1> (far-pair LUT4 scan, FP16 nibble tables in LDS)"
+                      if lut else f"scan_kernel<{W}, {8 if batch_q > 1 else 1}, 0, 0> (far-pair RaBitQ popcount scan)",
             "avg_launch_ms": round(avg_scan_ms, 4), "bytes_per_launch": int(bytes_per_launch),
             "achieved": achieved},
     }
@@ -356,6 +363,7 @@ def main():
                    "step_ms": [round(1000.0 * t, 3) for t in times],
                    "batch_q": batch_q, "vanguard": vanguard, "cpu_secondary_filter": c.secondary_filter,
                    "lower_bound_scale": eng.lower_bound_scale, "gpu_final_topk": args.gpu_final,
+                   "ip_kernel_type": args.ip_kernel,
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
                    "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
                    "query_chunk": chunk, "sweep": sweep},

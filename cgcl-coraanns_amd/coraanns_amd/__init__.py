@@ -37,7 +37,7 @@ FLAG_CROSS_QUERY_REUSE = 4
 
 DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range(5)
 DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
-DBG_SEED_DIST, DBG_THRESHOLDS, DBG_PROBE_DIST, DBG_VANGUARD_LOWS = 10, 11, 12, 13
+DBG_SEED_DIST, DBG_THRESHOLDS, DBG_PROBE_DIST, DBG_VANGUARD_LOWS, DBG_LUT = 10, 11, 12, 13, 14
 FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
 FLAG_PAIR_SEEDS = 1 << 6
 FLAG_NO_MFMA_SCAN = 1 << 7
@@ -45,6 +45,8 @@ FLAG_FP32_GEMM = 1 << 8
 FLAG_NO_VANGUARD_MFMA = 1 << 9
 FLAG_VANGUARD_MFMA = 1 << 10
 FLAG_GPU_FINAL = 1 << 11
+FLAG_LUT4 = 1 << 12
+KERNEL_TYPES = {None: 0, "lut4": 1, "bitwise": 2}
 
 
 class EngineUnavailable(RuntimeError):
@@ -103,7 +105,7 @@ class cora_hybrid_config(C.Structure):
                 ("queue_capacity", C.c_uint64), ("queue_spill_capacity", C.c_uint64),
                 ("metric", C.c_int), ("frozen_thresholds", C.c_int), ("cpu_threads", C.c_int),
                 ("gpu_seed_refine", C.c_int), ("gpu_refine_filter", C.c_int), ("extra_flags", C.c_uint32),
-                ("lower_bound_scale", C.c_float), ("gpu_final_topk", C.c_int)]
+                ("lower_bound_scale", C.c_float), ("gpu_final_topk", C.c_int), ("ip_kernel_type", C.c_int)]
 
 
 class cora_hybrid_stats(C.Structure):
@@ -301,7 +303,7 @@ class HybridIndex:
                  cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                  queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
                  cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0,
-                 lower_bound_scale=None, gpu_final_topk=False):
+                 lower_bound_scale=None, gpu_final_topk=False, ip_kernel_type=None):
         _, host = _load()
         h = C.c_void_p()
         _host_check(host.cora_hybrid_create(C.byref(h), device))
@@ -314,22 +316,24 @@ class HybridIndex:
                        metric=metric, frozen_thresholds=frozen_thresholds, cpu_threads=cpu_threads,
                        gpu_seed_refine=gpu_seed_refine, gpu_refine_filter=gpu_refine_filter,
                        extra_flags=extra_flags, lower_bound_scale=lower_bound_scale,
-                       gpu_final_topk=gpu_final_topk)
+                       gpu_final_topk=gpu_final_topk, ip_kernel_type=ip_kernel_type)
 
     def configure(self, *, profiling=False, candidate_stats=False, gpu_filter_timing=False,
                   cross_query_reuse=True, cpu_secondary_filter=True, vanguard_size=5,
                   queue_capacity=None, queue_spill_capacity=None, metric=0, frozen_thresholds=False,
                   cpu_threads=0, gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=0,
-                  lower_bound_scale=None, gpu_final_topk=False):
+                  lower_bound_scale=None, gpu_final_topk=False, ip_kernel_type=None):
         """lower_bound_scale: multiplier of the filter's error term (None keeps the
-        engine's default; 1.0 is the reference Bitwise producer's bound)."""
+        engine's default; 1.0 is the reference Bitwise producer's bound). ip_kernel_type:
+        None keeps the current one (Bitwise by default), "lut4" or "bitwise"."""
         cfg = cora_hybrid_config(int(profiling), int(candidate_stats), int(gpu_filter_timing),
                                  int(cross_query_reuse), int(cpu_secondary_filter), int(vanguard_size),
                                  int(queue_capacity or 0),
                                  (1 << 64) - 1 if queue_spill_capacity is None else int(queue_spill_capacity),
                                  int(metric), int(frozen_thresholds), int(cpu_threads),
                                  int(gpu_seed_refine), int(gpu_refine_filter), int(extra_flags),
-                                 float(lower_bound_scale or 0.0), int(gpu_final_topk))
+                                 float(lower_bound_scale or 0.0), int(gpu_final_topk),
+                                 KERNEL_TYPES[ip_kernel_type])
         _host_check(_load()[1].cora_hybrid_configure(self._h, C.byref(cfg)))
 
     def load_from_raw_pointers(self, num_vecs, dim, padded_dim, n_centroids, ex_bits, centroids,

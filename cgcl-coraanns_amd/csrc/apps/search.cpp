@@ -6,7 +6,7 @@
 // the default nprobe grid (options.hpp:94-132), query chunks of at most 65,535, warmup
 // and timed rounds per nprobe with QPS = nq / wall time, recall outside the timer
 // (ID recall, or distance-aware with --recall-base; recall.hpp:74-275), and the final
-// "nprobe\tQPS\trecall" table. --batch-q accepts 1..8 here (the reference 1..6).
+// "nprobe\tQPS\trecall" table. --batch-q accepts 1..64 here (the reference 1..6).
 #include <fcntl.h>
 #include <omp.h>
 #include <sys/mman.h>
@@ -227,7 +227,7 @@ int main(int argc, char **argv) {
         const bool recall_once = opt.flag("recall-once", false);
         const std::size_t batch_q = opt.size("batch-q", coraanns::default_batch_q);
         if (batch_q < 1 || batch_q > static_cast<std::size_t>(coraanns::max_batch_q))
-            throw std::invalid_argument("batch-q must be in [1, 8]");
+            throw std::invalid_argument("batch-q must be in [1, 64]");
         const std::size_t threads = opt.size("threads", static_cast<std::size_t>(omp_get_max_threads()));
         if (threads == 0 || threads > static_cast<std::size_t>(std::numeric_limits<int>::max()))
             throw std::invalid_argument("threads must be a positive int");

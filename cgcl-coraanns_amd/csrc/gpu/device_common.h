@@ -88,6 +88,36 @@ __device__ __forceinline__ int popc_ip(const uint32_t (&x)[Words<W>::kMax],
     return ip;
 }
 
+// Estimator of <q',b> a scan kernel instance evaluates.
+enum EstKind { kEstBitwise = 0, kEstLut4 = 1 };
+
+// FP16 nibble-LUT <q',b> (the reference's Lut4Bit producers, filter_kernels.cuh:283-306,
+// 655-708). The tile words hold dimension 32w+l at bit l; bit-reversed, they are the
+// reference's words, whose nibble j (bits 31-4j..28-4j, top bit the lowest dimension)
+// indexes entry [8w+j][nibble] of the query's table L [P/4][16] of FP16 values (two per u32
+// word, the lower half first). Even nibbles accumulate into a0 and odd ones into a1, each
+// in nibble order in FP32, and the result is a0 + a1.
+template <int W>
+__device__ __forceinline__ float lut4_ip(const uint32_t (&x)[Words<W>::kMax], const uint32_t *__restrict__ L,
+                                         uint32_t rw) {
+    const uint32_t nw = W > 0 ? (uint32_t)W : rw;
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(L);
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < Words<W>::kMax; ++w) {
+        if ((uint32_t)w < nw) {
+            const uint32_t c = __builtin_bitreverse32(x[w]);
+            const uint16_t *t = h + (size_t)w * 128;
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                a0 += (float)__builtin_bit_cast(_Float16, t[j * 16 + ((c >> (28 - 4 * j)) & 15u)]);
+                a1 += (float)__builtin_bit_cast(_Float16, t[(j + 1) * 16 + ((c >> (24 - 4 * j)) & 15u)]);
+            }
+        }
+    }
+    return a0 + a1;
+}
+
 // Two-stage <q',b>: width * ip_int rounded, then width2 * ip_res added with one rounding.
 __device__ __forceinline__ float two_stage_ip(float width, int ip, float width2, int ip_res) {
     return __fmaf_rn(width2, (float)ip_res, __fmul_rn(width, (float)ip));

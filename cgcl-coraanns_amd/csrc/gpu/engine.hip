@@ -76,6 +76,7 @@ struct cora_gpu_engine {
     float *d_rawscale = nullptr;
     uint32_t *d_qorder = nullptr;  // queries by nearest cluster (fused vanguard pass)
     int8_t *d_qbytes = nullptr;    // [max_q][2][P] qint, qres (MFMA far scan operands)
+    uint16_t *d_lut = nullptr;     // [max_q][P/4][16] FP16 nibble tables (LUT4 estimator)
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
     uint4 *d_seed_rec = nullptr;
     float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
@@ -149,6 +150,7 @@ ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool f
     p.meta = E->d_meta;
     p.qplanes = E->d_planes;
     p.qbytes = E->d_qbytes;
+    p.lut = (E->last.flags & CORA_FLAG_LUT4) ? reinterpret_cast<const uint32_t *>(E->d_lut) : nullptr;
     p.qwidth = E->d_qwidth;
     p.qwidth2 = E->d_qwidth2;
     p.k1 = E->d_k1;
@@ -212,6 +214,7 @@ void release_workspace(cora_gpu_engine *E) {
     dfree(E->d_pidx);
     dfree(E->d_qorder);
     dfree(E->d_qbytes);
+    dfree(E->d_lut);
     dfree(E->d_seed_dist);
     dfree(E->d_seed_low);
     dfree(E->d_seed_err);
@@ -555,6 +558,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_pidx, np));
         TRY(dalloc(E, E->d_qorder, max_q));
         TRY(dalloc(E, E->d_qbytes, max_q * 2 * E->P));
+        TRY(dalloc(E, E->d_lut, max_q * 4 * E->P));
         TRY(dalloc(E, E->d_gadd, np));
         TRY(dalloc(E, E->d_gerr, np));
         TRY(dalloc(E, E->d_bcount, nb));
@@ -716,8 +720,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "search shape exceeds the prepared workspace");
     if (!(a->bound_scale >= 0.0f && a->bound_scale <= 16.0f))
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "invalid bound scale (expected 0..16; 0 means 1)");
-    if (a->batch_q < 1 || a->batch_q > (uint32_t)kMaxBatchQ)
-        return fail(E, CORA_ERR_INVALID_ARGUMENT, "invalid batch-q (expected 1..8)");
+    if (a->batch_q < 1 || a->batch_q > kMaxBatchQArg)
+        return fail(E, CORA_ERR_INVALID_ARGUMENT, "invalid batch-q (expected 1..64)");
     const uint64_t want_depth = std::min<uint64_t>(a->vanguard, a->nprobe);
     if (want_depth > E->ws_van)
         return fail(E, CORA_ERR_LOGIC, "prepare workspace again before increasing vanguard size");
@@ -725,14 +729,16 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // fused vanguard pass and the refined pre-filter compute (live thresholds, or the
     // frozen snapshot in its GPU-seeded test mode)
     const bool want_final = (a->flags & CORA_FLAG_GPU_FINAL) != 0;
+    const bool lut = (a->flags & CORA_FLAG_LUT4) != 0;
     if (want_final &&
-        (!E->d_excodes || !E->d_fkeys || (a->flags & (CORA_FLAG_NO_GPU_SEED | CORA_FLAG_NO_GPU_PREFILTER |
-                                                       CORA_FLAG_PAIR_SEEDS)) ||
+        (!E->d_excodes || !E->d_fkeys ||
+         (a->flags & (CORA_FLAG_NO_GPU_SEED | CORA_FLAG_NO_GPU_PREFILTER | CORA_FLAG_PAIR_SEEDS | CORA_FLAG_LUT4)) ||
          ((a->flags & CORA_FLAG_FROZEN_THRESHOLDS) && !(a->flags & CORA_FLAG_GPU_SEED_FROZEN)) ||
          std::min<uint64_t>(a->vanguard, a->nprobe) > kVanguardMaxPairs || a->topk > kVanguardMaxTopk))
         return fail(E, CORA_ERR_LOGIC,
                     "GPU-final top-k needs the ex-codes in HBM, GPU seed thresholds and the refined "
-                    "pre-filter, the fused vanguard pass (vanguard <= 64, topk <= 128) and live thresholds");
+                    "pre-filter, the fused vanguard pass (vanguard <= 64, topk <= 128, Bitwise estimator) "
+                    "and live thresholds");
     HIPCHK(hipSetDevice(E->device));
     E->final_mode = want_final;
     E->last_final = want_final;
@@ -742,9 +748,14 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // Cross-query reuse: the far pairs of one cluster are scanned together, batch_q at a time
     // by the popcount kernel, or kMfmaBatchQ at a time by the matrix-core kernel when the
     // padded dimension allows it (the unit size changes only the speed, never the result).
+    // The LUT4 estimator (the reference's default Lut4Bit producers) runs the per-pair seed,
+    // far and recovery passes of the popcount kernels with the FP16 tables in place of the
+    // q-planes, at most kLutMaxBatchQ pairs per pass.
     const bool reuse = (a->flags & CORA_FLAG_CROSS_QUERY_REUSE) != 0;
-    const bool mfma_far = reuse && far_mfma_supported(E->W) && !(a->flags & CORA_FLAG_NO_MFMA_SCAN);
-    const uint32_t batch = mfma_far ? kMfmaBatchQ : reuse ? a->batch_q : 1u;
+    const bool mfma_far = !lut && reuse && far_mfma_supported(E->W) && !(a->flags & CORA_FLAG_NO_MFMA_SCAN);
+    const uint32_t batch = mfma_far ? kMfmaBatchQ
+                           : reuse  ? std::min<uint32_t>(a->batch_q, lut ? kLutMaxBatchQ : (uint32_t)kMaxBatchQ)
+                                    : 1u;
     const bool frozen = (a->flags & CORA_FLAG_FROZEN_THRESHOLDS) != 0;
     const bool timing = (a->flags & CORA_FLAG_FILTER_TIMING) != 0;
     E->last = *a;
@@ -770,6 +781,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         launch_rotate(E->d_raw, E->d_rot, E->d_qrot, nq, (uint32_t)E->dim, P, s);
     launch_query_prep(E->d_qrot, nq, P, (uint32_t)E->ex_bits, E->d_k1, E->d_kb, E->d_qnorm,
                       E->d_qwidth, E->d_qwidth2, E->d_planes, E->d_qbytes, s);
+    if (lut)
+        launch_lut_build(E->d_qrot, nq, P, E->d_lut, s);
     HIPCHK(hipEventRecord(E->ev_prep, s));
     HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_prep, 0));
     HIPCHK(hipMemcpyAsync(E->h_qrot, E->d_qrot, (size_t)nq * P * 4, hipMemcpyDeviceToHost,
@@ -805,7 +818,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool prefilter = E->d_excodes && ex_stage_mode && !(a->flags & CORA_FLAG_NO_GPU_PREFILTER);
     // fused per-query vanguard pass (vanguard.hip) unless the reference's per-pair passes
     // are asked for or the shape exceeds its limits
-    const bool fused = gpu_seed && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
+    const bool fused = gpu_seed && !lut && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
                        a->topk <= kVanguardMaxTopk;
     // its lower bounds first on the matrix cores, cluster-major, into the per-pair lows
     // array [nq][depth][van_stride] of the workspace
@@ -1080,6 +1093,12 @@ int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes
     case CORA_DBG_Q_WIDTH: src = E->d_qwidth; size = nq * 4; break;
     case CORA_DBG_Q_PLANES: src = E->d_planes; size = nq * 2 * kBq * E->W * 4; break;
     case CORA_DBG_Q_WIDTH2: src = E->d_qwidth2; size = nq * 4; break;
+    case CORA_DBG_LUT:
+        if (!(E->last.flags & CORA_FLAG_LUT4))
+            return fail(E, CORA_ERR_LOGIC, "debug_read: the last search did not use the LUT4 estimator");
+        src = E->d_lut;
+        size = nq * E->P * 8;
+        break;
     case CORA_DBG_SEED_DIST: {
         const uint64_t keep = std::max<uint64_t>(E->last.topk, 20);
         if (!E->d_seed_dist)

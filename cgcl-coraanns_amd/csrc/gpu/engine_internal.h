@@ -18,7 +18,8 @@ namespace cora {
 
 constexpr int kTileVectors = 64;
 constexpr int kBq = 8;             // query quantisation bits (reference RABITQ_BQ)
-constexpr int kMaxBatchQ = 8;      // same-cluster pairs per scan pass
+constexpr int kMaxBatchQ = 8;      // same-cluster pairs per popcount scan pass
+constexpr uint32_t kMaxBatchQArg = 64;  // largest batch-q a search accepts
 constexpr int kMaxVanguardKeep = 1024;
 constexpr int kSelectMaxProbe = 4096;       // top-nprobe select held in LDS
 constexpr uint32_t kNumXcd = 8;
@@ -103,6 +104,9 @@ struct ScanParams {
     const ClusterMeta *meta;
     const uint32_t *qplanes;  // [nq][16][W]: Bq=8 query planes 0..7, residual planes 8..15
     const int8_t *qbytes;     // [nq][2][P]: qint and qres as int8 (MFMA operands)
+    // LUT4 estimator (CORA_FLAG_LUT4): per query the FP16 nibble table [P/4][16], 2P u32
+    // words; nullptr selects the Bitwise estimator
+    const uint32_t *lut;
     const float *qwidth;      // [nq] Bq=8 step
     const float *qwidth2;     // [nq] residual step (qwidth / 254)
     const float *k1;          // [nq]
@@ -178,6 +182,10 @@ void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint
 void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_bits, float *k1,
                        float *kb, float *qnorm, float *qwidth, float *qwidth2, uint32_t *qplanes,
                        int8_t *qbytes, hipStream_t s);
+// FP16 nibble tables of the reference's Lut4Bit estimator (query_kernels.cuh:199-221):
+// lut[q][g][m] = half(sum over the set bits of m, top bit first, of qrot[q][4g..4g+3]),
+// summed in FP32 in dimension order and rounded to nearest even.
+void launch_lut_build(const float *qrot, uint32_t nq, uint32_t P, uint16_t *lut, hipStream_t s);
 void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s);
 // split-FP16 operand rows: hl = [2][rows][P] (hi rows, then lo rows), scale [rows]
 void launch_split_f16(const float *x, uint32_t rows, uint32_t P, uint16_t *hl, float *scale,
@@ -238,6 +246,8 @@ bool launch_order_queries(const int32_t *probe_idx, uint32_t nq, uint32_t nprobe
                           uint32_t *order, hipStream_t s);
 void launch_vanguard_query(const ScanParams &p, const VanguardArgs &va, uint32_t W, uint32_t nq,
                            hipStream_t s);
+// queries per pass of the LUT4 scan (its tables take the LDS of the q-planes)
+constexpr uint32_t kLutMaxBatchQ = 4;
 // far-pair scan on the matrix cores (scan_mfma.hip): units of up to kMfmaBatchQ pairs
 constexpr uint32_t kMfmaBatchQ = 16;
 bool far_mfma_supported(uint32_t W);

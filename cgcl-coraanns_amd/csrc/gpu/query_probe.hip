@@ -481,6 +481,30 @@ __global__ __launch_bounds__(64) void query_prep_kernel(const float *__restrict_
 
 // one wave per row, grid-stride over rows: a dispatch counts its work-items in 32 bits, so
 // one workgroup per row would silently drop rows beyond 2^32 / 64 (67M rows)
+// One table entry per thread: entry m of nibble group g sums, in FP32 and in dimension
+// order, the components 4g + i (i = 0..3) whose bit 3 - i is set in m, starting from 0,
+// then rounds to FP16 (nearest even), as precompute_lut_fp16_kernel does
+// (query_kernels.cuh:199-221).
+__global__ __launch_bounds__(256) void lut_build_kernel(const float *__restrict__ qrot, uint32_t P,
+                                                         uint16_t *__restrict__ lut) {
+    const uint32_t q = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t entries = P * 4;  // P/4 groups of 16
+    if (i >= entries)
+        return;
+    const uint32_t g = i >> 4, m = i & 15u;
+    const float *v = qrot + (size_t)q * P + 4 * g;
+    float sum = 0.0f;
+    if (m & 8u)
+        sum += v[0];
+    if (m & 4u)
+        sum += v[1];
+    if (m & 2u)
+        sum += v[2];
+    if (m & 1u)
+        sum += v[3];
+    lut[(size_t)q * entries + i] = __builtin_bit_cast(uint16_t, (_Float16)sum);
+}
+
 __global__ __launch_bounds__(64) void row_norms_kernel(const float *__restrict__ x, uint32_t rows,
                                                        uint32_t P, float *__restrict__ out) {
     for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
@@ -1253,6 +1277,11 @@ void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_b
                        float *kb, float *qnorm, float *qwidth, float *qwidth2, uint32_t *qplanes,
                        int8_t *qbytes, hipStream_t s) {
     query_prep_kernel<<<nq, 64, 0, s>>>(qrot, P, ex_bits, k1, kb, qnorm, qwidth, qwidth2, qplanes, qbytes);
+}
+
+void launch_lut_build(const float *qrot, uint32_t nq, uint32_t P, uint16_t *lut, hipStream_t s) {
+    if (nq)
+        lut_build_kernel<<<dim3((P * 4 + 255) / 256, nq), 256, 0, s>>>(qrot, P, lut);
 }
 
 void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hipStream_t s) {

@@ -47,6 +47,10 @@ namespace {
 
 enum ScanKind { kFar = 0, kRecovery = 1, kDense = 2 };
 
+// LUT4 tables staged per query in LDS: 64 u32 words (8 nibble groups of 16 FP16 values)
+// per code word.
+constexpr int kLutWordsPerCodeWord = 64;
+
 // Publish the n staged survivors of this wave (n wave-uniform, 0 < n <= kCap), 64 at a
 // time. Must be called by all 64 lanes; the workgroup is this one wave. Staged records
 // carry ip_int in their exact_ip word; it is replaced by the two-stage estimate. With
@@ -55,7 +59,7 @@ enum ScanKind { kFar = 0, kRecovery = 1, kDense = 2 };
 // is backed by at least topk candidates the CPU consumer will refine, so such a record
 // can never enter the top-k and the consumer would discard it. Kept records of each
 // round take one reservation on the ring position counter.
-template <int W>
+template <int W, int EST>
 __device__ __forceinline__ void flush_stage(const ScanParams &p, const QueueDev &q, uint32_t n,
                                             const uint4 *s_rec, const uint32_t *s_code,
                                             const float *s_cut, unsigned long long &limit,
@@ -70,14 +74,19 @@ __device__ __forceinline__ void flush_stage(const ScanParams &p, const QueueDev 
         uint4 rec = make_uint4(0u, 0u, 0u, 0u);
         if (i < n) {
             rec = s_rec[i];
-            uint32_t x[K];
-#pragma unroll
-            for (int w = 0; w < K; ++w)
-                x[w] = (uint32_t)w < nw ? s_code[w * CAP + i] : 0u;
             const uint32_t query = rec.x & 0xFFFFu;
-            const uint32_t *res = p.qplanes + ((size_t)query * 2 + 1) * kBq * nw;
-            const int ip_res = popc_ip<W>(x, res, nw);
-            const float ex = two_stage_ip(p.qwidth[query], (int)rec.z, p.qwidth2[query], ip_res);
+            float ex;
+            if constexpr (EST == kEstLut4) {
+                ex = __uint_as_float(rec.z);  // the LUT estimate is the exact_ip handed on
+            } else {
+                uint32_t x[K];
+#pragma unroll
+                for (int w = 0; w < K; ++w)
+                    x[w] = (uint32_t)w < nw ? s_code[w * CAP + i] : 0u;
+                const uint32_t *res = p.qplanes + ((size_t)query * 2 + 1) * kBq * nw;
+                const int ip_res = popc_ip<W>(x, res, nw);
+                ex = two_stage_ip(p.qwidth[query], (int)rec.z, p.qwidth2[query], ip_res);
+            }
             rec.z = __float_as_uint(ex);
             keep = true;
             if (p.prefilter) {
@@ -145,13 +154,15 @@ struct PlaneStore {
     static constexpr bool kRegs = W > 0 && W <= 4 && QMAX == 1;
 };
 
-template <int W, int QMAX, int KIND>
+template <int W, int QMAX, int KIND, int EST>
 __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t unit_set) {
     constexpr int K = Words<W>::kMax;
     constexpr int CAP = Stage<W>::kCap;
-    constexpr bool kRegs = PlaneStore<W, QMAX>::kRegs;
+    constexpr bool kLut = EST == kEstLut4;
+    constexpr bool kRegs = !kLut && PlaneStore<W, QMAX>::kRegs;
     constexpr bool kStaged = KIND != kDense;
-    __shared__ uint32_t s_planes[kRegs ? 1 : QMAX * kBq * K];
+    // q-planes of the unit's queries (Bitwise), or their LUT4 tables
+    __shared__ uint32_t s_planes[kRegs ? 1 : QMAX * (kLut ? kLutWordsPerCodeWord : kBq) * K];
     __shared__ uint4 s_rec[kStaged ? CAP : 1];
     __shared__ uint32_t s_code[kStaged ? CAP * K : 1];
     __shared__ float s_cut[kStaged ? CAP : 1];
@@ -221,14 +232,16 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
                 preg[i] = uniform(src[i]);
         } else {
             __syncthreads();
-            for (uint32_t i = lane; i < QMAX * kBq * nw; i += 64) {
-                const uint32_t j = i / (kBq * nw), r = i % (kBq * nw);
+            const uint32_t per = (kLut ? kLutWordsPerCodeWord : kBq) * nw;
+            for (uint32_t i = lane; i < QMAX * per; i += 64) {
+                const uint32_t j = i / per, r = i % per;
                 uint32_t wj = word0[0];
 #pragma unroll
                 for (int jj = 1; jj < QMAX; ++jj)
                     if ((uint32_t)jj == j)
                         wj = word0[jj];
-                s_planes[i] = j < count ? qplanes[(size_t)(wj & 0xFFFFu) * 2 * kBq * nw + r] : 0u;
+                const size_t qj = wj & 0xFFFFu;
+                s_planes[i] = j >= count ? 0u : kLut ? p.lut[qj * per + r] : qplanes[qj * 2 * kBq * nw + r];
             }
             __syncthreads();
         }
@@ -263,19 +276,21 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
                     continue;
                 uint32_t xr[K];
                 load_codes<W>(tiles + (size_t)(tbase + t) * tile_bytes, lane, rw, xr);
-                int ip;
-                if constexpr (kRegs)
-                    ip = popc_ip<W>(xr, preg, rw);
+                uint32_t zbits;  // ip_int (Bitwise) or the LUT4 estimate's bits
+                if constexpr (kLut)
+                    zbits = __float_as_uint(lut4_ip<W>(xr, s_planes, rw));
+                else if constexpr (kRegs)
+                    zbits = (uint32_t)popc_ip<W>(xr, preg, rw);
                 else
-                    ip = popc_ip<W>(xr, s_planes, rw);
+                    zbits = (uint32_t)popc_ip<W>(xr, s_planes, rw);
                 const uint32_t cnt = (uint32_t)__popcll(mask);
                 if (staged + cnt > (uint32_t)CAP) {
-                    flush_stage<W>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
+                    flush_stage<W, EST>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
                     staged = 0;
                 }
                 if (survive) {
                     const uint32_t k = staged + lane_rank(mask);
-                    s_rec[k] = make_uint4(word0[0], start + local, (uint32_t)ip, __float_as_uint(low));
+                    s_rec[k] = make_uint4(word0[0], start + local, zbits, __float_as_uint(low));
                     s_cut[k] = cutoff[0];
 #pragma unroll
                     for (int w = 0; w < K; ++w)
@@ -316,20 +331,26 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
             for (int j = 0; j < QMAX; ++j) {
                 if ((uint32_t)j >= count)
                     break;
-                int ip;
-                if constexpr (kRegs)
-                    ip = popc_ip<W>(x, preg, rw);
-                else
-                    ip = popc_ip<W>(x, s_planes + j * kBq * nw, rw);
-                const float ex = width[j] * (float)ip;
+                int ip = 0;
+                float ex;
+                if constexpr (kLut) {
+                    ex = lut4_ip<W>(x, s_planes + j * kLutWordsPerCodeWord * nw, rw);
+                } else {
+                    if constexpr (kRegs)
+                        ip = popc_ip<W>(x, preg, rw);
+                    else
+                        ip = popc_ip<W>(x, s_planes + j * kBq * nw, rw);
+                    ex = width[j] * (float)ip;
+                }
+                const uint32_t zbits = kLut ? __float_as_uint(ex) : (uint32_t)ip;
                 const float low = fa + gadd[j] + fr * (ex + k1[j]) - fe * gerr[j];
                 if constexpr (KIND == kDense) {
                     if (valid) {
                         const uint32_t query = word0[j] & 0xFFFFu, probe = word0[j] >> 16;
                         const uint32_t *res = qplanes + ((size_t)query * 2 + 1) * kBq * nw;
                         const size_t o = ((size_t)query * nprobe + probe) * p.dbg_stride + local;
-                        p.dbg_ip[o] = ip;
-                        p.dbg_ip2[o] = popc_ip<W>(x, res, rw);
+                        p.dbg_ip[o] = (int32_t)zbits;
+                        p.dbg_ip2[o] = kLut ? 0 : popc_ip<W>(x, res, rw);
                         p.dbg_low[o] = low;
                     }
                 } else {
@@ -338,13 +359,12 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
                     if (mask != 0) {
                         const uint32_t cnt = (uint32_t)__popcll(mask);
                         if (staged + cnt > (uint32_t)CAP) {
-                            flush_stage<W>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
+                            flush_stage<W, EST>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
                             staged = 0;
                         }
                         if (survive) {
                             const uint32_t k = staged + lane_rank(mask);
-                            s_rec[k] = make_uint4(word0[j], start + local, (uint32_t)ip,
-                                                  __float_as_uint(low));
+                            s_rec[k] = make_uint4(word0[j], start + local, zbits, __float_as_uint(low));
                             s_cut[k] = cutoff[j];
 #pragma unroll
                             for (int w = 0; w < K; ++w)
@@ -365,7 +385,7 @@ __global__ __launch_bounds__(64) void scan_kernel(const ScanParams p, uint32_t u
     }
     if constexpr (kStaged) {
         if (staged)
-            flush_stage<W>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
+            flush_stage<W, EST>(p, q, staged, s_rec, s_code, s_cut, limit, lane);
     }
 }
 
@@ -408,9 +428,11 @@ __device__ void wave_sort(unsigned long long *buf, uint32_t cap, uint32_t lane) 
 // bound also goes to the pair's slice of the HBM lows buffer, which the recovery pass
 // reads instead of recomputing the estimator. With the HBM ex-codes, the seeds are then
 // refined on the GPU (16 lanes per seed) for the seed thresholds.
-template <int W>
+template <int W, int EST>
 __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
+    constexpr bool kLut = EST == kEstLut4;
     extern __shared__ unsigned long long s_buf[];  // [cap] keys, then [cap] f32 exact_ip
+    __shared__ uint32_t s_lut[kLut ? kLutWordsPerCodeWord * Words<W>::kMax : 1];  // the pair's LUT4 table
     const uint32_t cap = p.seed_buf;
     float *s_exk = reinterpret_cast<float *>(s_buf + cap);
     const uint32_t lane = threadIdx.x;
@@ -439,6 +461,12 @@ __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
         const float gadd = uniformf(p.pgadd[pi]), gerr = uniformf(p.pgerr[pi]);
         const float cutoff = uniformf(read_threshold(p.thresholds, query));
         const uint32_t *planes = p.qplanes + (size_t)query * 2 * kBq * rw;
+        if constexpr (kLut) {
+            __syncthreads();
+            for (uint32_t i = lane; i < kLutWordsPerCodeWord * rw; i += 64)
+                s_lut[i] = p.lut[(size_t)query * kLutWordsPerCodeWord * rw + i];
+            __syncthreads();
+        }
         float *lows_out = p.van_lows ? p.van_lows + ((size_t)query * p.vanguard + probe) * p.van_stride
                                      : nullptr;
         const uint32_t ntiles = (n + kTileVectors - 1) / kTileVectors;
@@ -466,8 +494,7 @@ __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
             }
             const uint32_t local = t * kTileVectors + lane;
             const bool valid = local < n;
-            const int ip = popc_ip<W>(x, planes, rw);
-            const float ex = width * (float)ip;
+            const float ex = kLut ? lut4_ip<W>(x, s_lut, rw) : width * (float)popc_ip<W>(x, planes, rw);
             const float low = fa + gadd + fr * (ex + k1) - fe * gerr;
 #pragma unroll
             for (int w = 0; w < Words<W>::kMax; ++w)
@@ -529,9 +556,9 @@ __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
             const uint8_t *tile = p.tiles + (size_t)(tbase + local / kTileVectors) * p.tile_bytes;
             uint32_t x[Words<W>::kMax];
             load_codes<W>(tile, local % kTileVectors, rw, x);
-            const int ip = popc_ip<W>(x, planes, rw);
-            const int ip_res = popc_ip<W>(x, planes + kBq * rw, rw);
-            const float ex = two_stage_ip(width, ip, width2, ip_res);
+            const float ex = kLut ? lut4_ip<W>(x, s_lut, rw)
+                                  : two_stage_ip(width, popc_ip<W>(x, planes, rw), width2,
+                                                 popc_ip<W>(x, planes + kBq * rw, rw));
             s_exk[sidx] = ex;
             atomicOr(&seed[local >> 5], 1u << (local & 31));
             const uint4 rec = make_uint4(w0, start + local, __float_as_uint(ex),
@@ -837,14 +864,32 @@ uint32_t resident_grid(F kernel, int block, size_t dyn_lds = 0) {
     return grid;
 }
 
-template <int W, int Q, int KIND>
+template <int W, int Q, int KIND, int EST = kEstBitwise>
 void launch_one(const ScanParams &p, uint32_t set, hipStream_t s) {
-    auto *k = scan_kernel<W, Q, KIND>;
+    auto *k = scan_kernel<W, Q, KIND, EST>;
     k<<<resident_grid(k, 64), 64, 0, s>>>(p, set);
+}
+
+// LUT4 estimator: the generic-width kernels only (an A/B mode), up to kLutMaxBatchQ
+// queries per pass
+int launch_scan_lut(const ScanParams &p, uint32_t batch_q, int kind, uint32_t set, hipStream_t s) {
+    if (kind == kFar) {
+        if (batch_q <= 1)
+            launch_one<0, 1, kFar, kEstLut4>(p, set, s);
+        else
+            launch_one<0, kLutMaxBatchQ, kFar, kEstLut4>(p, set, s);
+    } else if (kind == kRecovery) {
+        launch_one<0, 1, kRecovery, kEstLut4>(p, set, s);
+    } else {
+        launch_one<0, kLutMaxBatchQ, kDense, kEstLut4>(p, set, s);
+    }
+    return 0;
 }
 
 template <int W>
 int launch_scan_w(const ScanParams &p, uint32_t batch_q, int kind, uint32_t set, hipStream_t s) {
+    if (p.lut)
+        return launch_scan_lut(p, batch_q, kind, set, s);
     if (kind == kFar) {
         if (batch_q <= 1)
             launch_one<W, 1, kFar>(p, set, s);
@@ -858,9 +903,9 @@ int launch_scan_w(const ScanParams &p, uint32_t batch_q, int kind, uint32_t set,
     return 0;
 }
 
-template <int W>
+template <int W, int EST = kEstBitwise>
 void launch_seed_w(const ScanParams &p, hipStream_t s) {
-    auto *k = seed_kernel<W>;
+    auto *k = seed_kernel<W, EST>;
     const size_t lds = (size_t)p.seed_buf * (sizeof(unsigned long long) + sizeof(float));
     k<<<resident_grid(k, 64, lds), 64, lds, s>>>(p);
 }
@@ -898,6 +943,10 @@ int launch_scan_set(const ScanParams &p, uint32_t W, int kind, uint32_t set, hip
 }
 
 int launch_vanguard_seed(const ScanParams &p, uint32_t W, hipStream_t s) {
+    if (p.lut) {
+        launch_seed_w<0, kEstLut4>(p, s);
+        return 0;
+    }
     switch (W) {
     case 2: launch_seed_w<2>(p, s); break;
     case 4: launch_seed_w<4>(p, s); break;

@@ -116,6 +116,12 @@ int cora_hybrid_configure(cora_hybrid *h, const cora_hybrid_config *c) {
         if (c->lower_bound_scale != 0.0f)
             x.set_lower_bound_scale(c->lower_bound_scale);
         x.set_gpu_final_topk(c->gpu_final_topk != 0);
+        if (c->ip_kernel_type == 1)
+            x.set_ip_kernel_type(KernelType::Lut4Bit);
+        else if (c->ip_kernel_type == 2)
+            x.set_ip_kernel_type(KernelType::Bitwise);
+        else if (c->ip_kernel_type != 0)
+            throw std::invalid_argument("ip_kernel_type must be 0 (keep), 1 (Lut4Bit) or 2 (Bitwise)");
     });
 }
 

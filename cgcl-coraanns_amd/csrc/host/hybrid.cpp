@@ -221,8 +221,8 @@ void HybridIndex::print_profile(const cora_search_stats &st, std::size_t refined
         std::printf("[Profile] 0~2. Initial Matrix Math time: %g ms\n", st.phase_ms[0]);
         std::printf("[Profile] 3. Select Top-nprobe Clusters time: %g ms\n", st.phase_ms[1]);
         std::printf("[Profile] 4. Flatten Pairs time: %g ms\n", st.phase_ms[2]);
-        std::printf("[Profile] 7~9. Single-Stage Global Task Pool Pipeline (BITWISE_DECOMP) time: %g ms\n",
-                    st.phase_ms[3]);
+        std::printf("[Profile] 7~9. Single-Stage Global Task Pool Pipeline (%s) time: %g ms\n",
+                    ip_kernel_type_ == KernelType::Lut4Bit ? "LUT_4BIT" : "BITWISE_DECOMP", st.phase_ms[3]);
         std::printf("[Profile] vanguard: %s; GPU filter kernels %g ms\n",
                     kVanguardMode[st.vanguard_mode >= 0 && st.vanguard_mode < 4 ? st.vanguard_mode : 0],
                     st.filter_ms);
@@ -239,7 +239,7 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
                          int batch_q) {
     validate_workspace(num_queries, topk, nprobe);
     if (!h_queries || !h_final_dists || !h_final_pids || batch_q < 1 || batch_q > max_batch_q)
-        throw std::invalid_argument("invalid search buffers or batch-q (expected 1..8)");
+        throw std::invalid_argument("invalid search buffers or batch-q (expected 1..64)");
     const bool exact = exact_base_mapping_ != nullptr;
     if (!exact && (!h_long_codes_ || !h_ex_factors_))
         throw std::logic_error("extended codes or an exact-refine base are required");
@@ -260,7 +260,8 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
                  (cross_query_reuse_enabled_ ? uint32_t{CORA_FLAG_CROSS_QUERY_REUSE} : 0u) |
                  (gpu_seed_refine_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_SEED}) |
                  (gpu_refine_filter_ && !exact ? 0u : uint32_t{CORA_FLAG_NO_GPU_PREFILTER}) |
-                 (gpu_final_topk_ && !exact ? uint32_t{CORA_FLAG_GPU_FINAL} : 0u) | extra_flags_;
+                 (gpu_final_topk_ && !exact ? uint32_t{CORA_FLAG_GPU_FINAL} : 0u) |
+                 (ip_kernel_type_ == KernelType::Lut4Bit ? uint32_t{CORA_FLAG_LUT4} : 0u) | extra_flags_;
     args.bound_scale = bound_scale_;
     last_gpu_filter_ms_ = 0.0f;
     check(engine_, cora_gpu_launch_search(engine_, &args));

@@ -91,7 +91,14 @@ enum cora_search_flags {
      * the ring and no CPU refinement runs (the reference's GPU baseline engine refines on
      * the GPU likewise, src/baselines/gpu.cu:630-700). Needs the ex-codes in HBM, the fused
      * vanguard pass (topk <= 128, vanguard <= 64) and the refined pre-filter. */
-    CORA_FLAG_GPU_FINAL = 1u << 11
+    CORA_FLAG_GPU_FINAL = 1u << 11,
+    /* LUT4 estimator, the reference's KernelType::Lut4Bit (query_kernels.cuh:199-221,
+     * filter_kernels.cuh:283-306,586-770): <q',b> is the FP32 sum of FP16 nibble-table
+     * entries (even and odd nibbles in two accumulators), used for the lower bound and handed
+     * to refinement as exact_ip. Runs the per-pair seed, far and recovery passes (no fused
+     * vanguard pass, no matrix-core scans) with at most 4 same-cluster pairs per pass.
+     * Without it the Bitwise estimator runs (Bq=8 popcount bound; two-stage exact_ip). */
+    CORA_FLAG_LUT4 = 1u << 12
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -112,7 +119,9 @@ typedef struct cora_search_args {
     uint32_t num_queries;
     uint32_t topk;
     uint32_t nprobe;
-    uint32_t batch_q;  /* 1..8 same-cluster pairs per scan pass (reference accepts 1..6) */
+    uint32_t batch_q;  /* 1..64 same-cluster pairs per cluster pass with cross-query reuse (the
+                          reference accepts 1..6); the popcount scan takes at most 8 per pass
+                          (4 with LUT4), the matrix-core scans 16 whatever the value */
     uint32_t vanguard; /* vanguard depth: pairs with probe rank < vanguard are scanned first */
     uint32_t flags;    /* cora_search_flags */
     /* Multiplier of the lower bound's error term: low = est - bound_scale * f_error * g_error.
@@ -261,10 +270,11 @@ enum cora_debug_array {
                                      snapshot in frozen mode, else the live array) */
     CORA_DBG_PROBE_DIST = 12,     /* f32 [nq][nlist] coarse-probe distance matrix
                                      ||q'||^2 + ||c'||^2 - 2 <q',c'> */
-    CORA_DBG_VANGUARD_LOWS = 13   /* f32 [nq][vanguard depth][stride] lower bounds the
+    CORA_DBG_VANGUARD_LOWS = 13,  /* f32 [nq][vanguard depth][stride] lower bounds the
                                      matrix-core lows pass wrote (stride = the largest
                                      cluster rounded up to 256; entries past a cluster's
                                      size are undefined) */
+    CORA_DBG_LUT = 14             /* f16 [nq][P/4][16] LUT4 tables (CORA_FLAG_LUT4 searches) */
 };
 int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t bytes);
 
@@ -272,7 +282,8 @@ int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t 
  * search, evaluate every vector of the probed cluster with the scan kernel's estimator
  * and write ip_int = <b, qint> (i32), the residual inner product <b, qres> (i32) and the
  * low distance (f32) to out_ip / out_ip2 / out_low, laid out [nq][nprobe][max_cluster]
- * (entries past the cluster size are left untouched). */
+ * (entries past the cluster size are left untouched). After a CORA_FLAG_LUT4 search,
+ * out_ip holds the bits of the f32 LUT4 estimate and out_ip2 zero. */
 int cora_gpu_debug_dense(cora_gpu_engine *engine, int32_t *out_ip, int32_t *out_ip2,
                          float *out_low, uint64_t capacity_elems);
 

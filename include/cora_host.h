@@ -45,6 +45,7 @@ typedef struct cora_hybrid_config {
     uint32_t extra_flags;     /* set_extra_search_flags (cora_search_flags test modes) */
     float lower_bound_scale;  /* set_lower_bound_scale (0 = keep) */
     int gpu_final_topk;       /* set_gpu_final_topk */
+    int ip_kernel_type;       /* set_ip_kernel_type: 0 = keep, 1 = Lut4Bit, 2 = Bitwise */
 } cora_hybrid_config;
 
 typedef struct cora_hybrid_stats {

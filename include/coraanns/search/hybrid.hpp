@@ -49,8 +49,11 @@ class HybridIndex {
     void set_vanguard_size(std::size_t size);
     std::size_t get_vanguard_size() const { return vanguard_size_; }
 
-    // Both kernel types run the same Bq=8 popcount estimator here (the reference's
-    // Bitwise arithmetic, filter_kernels.cuh:79-114); the setting is kept for API parity.
+    // Bitwise (the default here): the Bq=8 popcount lower bound (filter_kernels.cuh:79-114),
+    // the two-stage exact_ip, the fused vanguard pass and the matrix-core scans.
+    // Lut4Bit (the reference's default): its FP16 nibble-LUT estimator
+    // (query_kernels.cuh:199-221, filter_kernels.cuh:283-306,586-770) on the per-pair seed,
+    // far and recovery passes, the LUT value being the exact_ip refinement uses.
     void set_ip_kernel_type(KernelType t) { ip_kernel_type_ = t; }
     KernelType get_ip_kernel_type() const { return ip_kernel_type_; }
 
@@ -181,7 +184,7 @@ class HybridIndex {
     bool gpu_final_topk_ = false;
     int cpu_threads_ = 0;
     std::size_t vanguard_size_ = default_vanguard_size;
-    KernelType ip_kernel_type_ = KernelType::Lut4Bit;
+    KernelType ip_kernel_type_ = KernelType::Bitwise;
 
     std::size_t queue_capacity_ = queue::default_capacity;
     std::size_t queue_spill_capacity_ = queue::default_spill_capacity;

@@ -16,8 +16,10 @@ inline constexpr float default_bound_scale = 1.3f;
 inline constexpr float max_bound_scale = 16.0f;
 inline constexpr std::size_t max_query_chunk = 65535;
 inline constexpr std::size_t max_probe_count = 65536;
-// This engine additionally batches up to 8 same-cluster pairs per scan pass.
-inline constexpr int max_batch_q = 8;
+// Cross-query reuse groups up to batch-q same-cluster pairs (the reference accepts 1..6);
+// larger requests are accepted up to 64 and scanned at most 8 pairs per popcount pass
+// (4 with the LUT4 estimator; the matrix-core scans take 16 at a time whatever batch-q is).
+inline constexpr int max_batch_q = 64;
 
 inline void validate_search_shape(std::size_t queries, std::size_t topk, std::size_t nprobe,
                                   std::size_t centroids, std::size_t padded_dim) {

@@ -415,6 +415,41 @@ def exact_ip_bitwise(ip_int, width):
     return (np.float32(width) * np.asarray(ip_int, dtype=np.float32)).astype(np.float32)
 
 
+def lut4_table(qr: np.ndarray) -> np.ndarray:
+    """FP16 nibble tables of the Lut4Bit estimator, precompute_lut_fp16_kernel
+    (query_kernels.cuh:199-221): for nibble group g and pattern m, start from 0.0f and add
+    in FP32, in this order, q'[4g] if m & 8, q'[4g+1] if m & 4, q'[4g+2] if m & 2,
+    q'[4g+3] if m & 1, then round to FP16 (__float2half: nearest even). [nq, P/4, 16] f16."""
+    qr = np.atleast_2d(np.asarray(qr, np.float32))
+    nq, P = qr.shape
+    v = qr.reshape(nq, P // 4, 4)
+    m = np.arange(16)
+    s = np.zeros((nq, P // 4, 16), np.float32)
+    for i, bit in enumerate((8, 4, 2, 1)):
+        add = np.where((m & bit) != 0, 1, 0).astype(bool)
+        s = np.where(add[None, None, :], (s + v[:, :, i:i + 1]).astype(np.float32), s)
+    with np.errstate(over="ignore"):  # beyond the FP16 range: +-inf, as __float2half gives
+        return s.astype(np.float16)
+
+
+def lut4_ip(words: np.ndarray, lut: np.ndarray) -> np.ndarray:
+    """<q',b> of the Lut4Bit producers (filter_kernels.cuh:283-306, 655-708) for codes in
+    the reference word layout (words [n, P/32], dimension 32w+l at bit 31-l): nibble
+    j = 8w + i of word w is (word >> (28 - 4i)) & 15; FP32 accumulators a0 (even j) and
+    a1 (odd j) each add float(lut[j, nibble]) in increasing j, and the estimate is a0 + a1.
+    Returns f32 [n]."""
+    words = np.atleast_2d(np.asarray(words, np.uint32))
+    n, W = words.shape
+    tab = np.asarray(lut, np.float16).astype(np.float32)  # exact
+    a = [np.zeros(n, np.float32), np.zeros(n, np.float32)]
+    for w in range(W):
+        for i in range(8):
+            j = 8 * w + i
+            nib = (words[:, w] >> np.uint32(28 - 4 * i)) & np.uint32(15)
+            a[j & 1] = (a[j & 1] + tab[j, nib]).astype(np.float32)
+    return (a[0] + a[1]).astype(np.float32)
+
+
 def low_dist(f_add, f_rescale, f_error, g_add, g_error, exact_ip, k1):
     """low = f_add + g_add + f_rescale*(exact_ip + k1) - f_error*g_error
     (filter_kernels.cuh:113-114; estimator.hpp:315-318). float64, rounded once."""
@@ -549,7 +584,10 @@ class HybridResult:
 
 
 def hybrid_search(sd: SearchData, queries: np.ndarray, topk: int, nprobe: int, metric: int,
-                  ex_bits: int, thresholds=None) -> HybridResult:
+                  ex_bits: int, thresholds=None, estimator: str = "bitwise") -> HybridResult:
+    """estimator "bitwise": Bq=8 lower bound, two-stage exact_ip for refinement (this
+    engine's Bitwise mode); "lut4": the FP16 nibble-LUT estimate for both (the reference's
+    Lut4Bit producers)."""
     P = sd.centroids.shape[1]
     W = P // 32
     nq = queries.shape[0]
@@ -558,6 +596,7 @@ def hybrid_search(sd: SearchData, queries: np.ndarray, topk: int, nprobe: int, m
     qint, width = quantize_query_bitwise(qr)
     qres, width2 = quantize_query_residual(qr, qint, width)
     planes = query_planes_msb(qint)
+    luts = lut4_table(qr) if estimator == "lut4" else None
     idx, g_add, g_err, _ = coarse_probe(qr, sd.centroids, nprobe, metric)
     thr = np.full(nq, F32_MAX, np.float32) if thresholds is None else np.asarray(thresholds, np.float32)
     dists = np.full((nq, topk), F32_MAX, np.float32)
@@ -572,17 +611,23 @@ def hybrid_search(sd: SearchData, queries: np.ndarray, topk: int, nprobe: int, m
             s = int(sd.cluster_start[c])
             if n == 0:
                 continue
-            words = sd.short_data[s * W:(s + n) * W].reshape(W, n).T
-            ipi = ip_int_planes(np.ascontiguousarray(words), planes[q])
-            eip = exact_ip_bitwise(ipi, width[q])
+            words = np.ascontiguousarray(sd.short_data[s * W:(s + n) * W].reshape(W, n).T)
+            if luts is not None:
+                eip = lut4_ip(words, luts[q])
+            else:
+                ipi = ip_int_planes(words, planes[q])
+                eip = exact_ip_bitwise(ipi, width[q])
             f = sd.short_factors[s:s + n]
             low = low_dist(f[:, 0], f[:, 1], f[:, 2], g_add[q, p], g_err[q, p], eip, k1[q])
             keep = np.nonzero(low < thr[q])[0]
             if keep.size == 0:
                 continue
             gids = s + keep
-            ipr = ip_int_direct(sd.bits[gids], qres[q])
-            eip2 = exact_ip_two_stage(ipi[keep], ipr, width[q], width2[q])
+            if luts is not None:
+                eip2 = eip[keep]
+            else:
+                ipr = ip_int_direct(sd.bits[gids], qres[q])
+                eip2 = exact_ip_two_stage(ipi[keep], ipr, width[q], width2[q])
             ip2 = excode_ip(qr[q], sd.long_codes[gids], P)
             rd = refine_dist(sd.ex_factors[gids, 0], sd.ex_factors[gids, 1], g_add[q, p], eip2,
                              ip2, kb[q], ex_bits)
@@ -725,6 +770,10 @@ def quantize_excode(x: np.ndarray, c: np.ndarray, ex_bits: int) -> np.ndarray:
 
 PINNED = {
     "read_ivf": "golden: ref_dump meta/ids/centroids/rotator (reference IVF::load)",
+    "lut4_table": "closed forms: single-bit entries, pattern bit 3 = first dimension, FP16 "
+                  "round-half-even and overflow to inf",
+    "lut4_ip": "closed forms: split even/odd FP32 accumulators (1 + n_odd 2^-24 case), one-hot "
+               "nibble layout, exact integer inner products for representable values",
     "read_hnsw_centroids": "reference-built sidecar index (coraanns_build_index, nlist 20000): centroids "
                            "equal ref_dump's (reference IVF::load + HNSWInitializer); permuted-label "
                            "sidecars equal the embedded centroids; corrupt files rejected",
@@ -735,7 +784,9 @@ PINNED = {
     "unpack_fastscan_bits": "round trip with fastscan_pack on random bits; golden short_data",
     "rotate": "golden: ref_dump rotated_queries (reference MatrixRotator::rotate), 1e-5",
     "query_factors": "golden: ref_dump est_qvals k1xsumq/kbxsumq (reference SplitBatchQuery), 1e-5",
-    "quantize_query_bitwise": "closed forms: zero query, +-amax -> +-127, half-even ties, |err|<=width/2",
+    "quantize_query_bitwise": "closed forms: zero query, +-amax -> +-127, half-even ties at width 1 and "
+                              "2^-3, |err|<=width/2; exact rational arithmetic at rounding boundaries "
+                              "where q*(1/width) and q/width round apart",
     "quantize_query_residual": "closed forms: |q' - width*qint - width2*qres| <= width2/2 (+ f32 rounding), "
                                "zero query -> 0, exact multiples of width -> qres 0",
     "exact_ip_two_stage": "bound: |two_stage - <q',b>_f64| <= popc(b)*width2/2 (+ f32 rounding) on random data",

@@ -122,7 +122,7 @@ def test_driver_multiple_nprobes_and_recall_once(known_neighbours):
 
 
 @pytest.mark.parametrize("bad", [
-    ["--topk", "0"], ["--nprobes", "5"], ["--nprobes", "2,2"], ["--batch-q", "9"], ["--rounds", "x"],
+    ["--topk", "0"], ["--nprobes", "5"], ["--nprobes", "2,2"], ["--batch-q", "65"], ["--batch-q", "0"], ["--rounds", "x"],
     ["--unknown", "1"], ["--queue-capacity", "300"], ["--lower-bound-scale", "0"],
 ])
 def test_driver_rejects_invalid_options(known_neighbours, bad):

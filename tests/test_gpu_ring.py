@@ -126,7 +126,7 @@ def test_forced_spill_and_refill():
     assert spilled, "capacity 32 never exercised the HBM spill path"
 
 
-@pytest.mark.parametrize("batch_q", [1, 2, 3, 5, 6, 7, 8])
+@pytest.mark.parametrize("batch_q", [1, 2, 3, 5, 6, 7, 8, 24, 64])
 def test_all_pass_batch_q(allpass, batch_q):
     say(f"[gpu] all-pass batch_q={batch_q}")
     e = allpass.engine(8192, 262144, 5)
@@ -224,7 +224,9 @@ def test_lifecycle_and_shape_errors():
     with pytest.raises(ca.InvalidArgument):
         e.search(q, 10, 2)
     with pytest.raises(ca.InvalidArgument):
-        e.search(q, 10, 1, 9)
+        e.search(q, 10, 1, 65)
+    with pytest.raises(ca.InvalidArgument):
+        e.search(q, 10, 1, 0)
     with pytest.raises(ca.LogicError):
         e.set_vanguard_size(1)
     for it in range(3):

@@ -375,3 +375,143 @@ def test_best_rescale_factor_brute_force():
                 if r > best:
                     best, bt = r, t
             assert orc.best_rescale_factor(oa, ex) == bt
+
+
+# --------------------------------------------------------------------------------------
+# Exact single-precision arithmetic from rationals (independent of numpy's float32 ops):
+# the correctly rounded (nearest, ties to even) float32 of a Fraction.
+# --------------------------------------------------------------------------------------
+from fractions import Fraction  # noqa: E402
+
+
+def f32_round(x: Fraction) -> np.float32:
+    d = np.float32(float(x))  # within one float32 ulp of x
+    best = None
+    for c in (np.nextafter(d, np.float32(-np.inf)), d, np.nextafter(d, np.float32(np.inf))):
+        err = abs(Fraction(float(c)) - x)
+        key = (err, int(np.array(c).view(np.uint32)) & 1)  # ties: even mantissa
+        if best is None or key < best[0]:
+            best = (key, c)
+    return np.float32(best[1])
+
+
+def rint_even(x: Fraction) -> int:
+    f = x.numerator // x.denominator
+    r = x - f
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and f % 2 == 1):
+        f += 1
+    return f
+
+
+def bq8_expected(row):
+    """qint of one row by exact rational arithmetic: width = f32(amax / 127),
+    inv = f32(1 / width), qint = clamp(rint_even(f32(q * inv)), -128, 127)
+    (query_kernels.cuh:158-176)."""
+    amax = max(abs(Fraction(float(v))) for v in row)
+    width = max(f32_round(amax / 127), np.float32(1e-30))
+    inv = f32_round(1 / Fraction(float(width)))
+    out = [min(127, max(-128, rint_even(Fraction(float(f32_round(Fraction(float(v)) * Fraction(float(inv))))))))
+           for v in row]
+    return np.array(out, np.int32), width, inv
+
+
+def test_quantize_query_reciprocal_product_boundaries():
+    """Rows whose components sit next to a rounding boundary of q * (1/width): for each,
+    q * f32(1/width) and q / width round to different integers, and the oracle must give
+    the former (the reference multiplies by the reciprocal, query_kernels.cuh:158-176)."""
+    rng = np.random.default_rng(21)
+    found = 0
+    for _ in range(400):
+        amax = np.float32(rng.uniform(0.1, 50.0))
+        row = np.zeros(64, np.float32)
+        row[0] = amax
+        _, width, inv = bq8_expected(row[:1])
+        cases = []
+        for k in range(-120, 121, 7):
+            c = np.float32((k + 0.5) * float(width))
+            for cand in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+                by_inv = rint_even(Fraction(float(f32_round(Fraction(float(cand)) * Fraction(float(inv))))))
+                by_div = rint_even(Fraction(float(f32_round(Fraction(float(cand)) / Fraction(float(width))))))
+                if by_inv != by_div:
+                    cases.append(cand)
+        if not cases:
+            continue
+        row[1:1 + min(63, len(cases))] = cases[:63]
+        want, w, _ = bq8_expected(row)
+        qint, wo = orc.quantize_query_bitwise(row[None])
+        assert wo[0] == w
+        assert np.array_equal(qint[0], want)
+        found += len(cases)
+    assert found >= 20, found
+
+
+def test_quantize_query_half_even_ties_with_width_not_one():
+    """width = 2^-3 (amax = 127/8): 1/width = 8 exactly, so q = (k + 1/2)/8 gives an exact
+    tie q * inv = k + 1/2, which rounds to the even neighbour."""
+    row = np.zeros(64, np.float32)
+    row[0] = np.float32(127.0 / 8.0)
+    ties = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5]
+    row[1:1 + len(ties)] = np.array(ties, np.float32) / np.float32(8.0)
+    qint, w = orc.quantize_query_bitwise(row[None])
+    assert w[0] == np.float32(0.125)
+    assert list(qint[0, :1 + len(ties)]) == [127, 0, 2, 2, 0, -2, -2, 126, -126]
+
+
+def words_of_bits(bits):
+    return orc.bits_to_words_msb(np.asarray(bits, np.uint8))
+
+
+def test_lut4_table_closed_forms():
+    P = 64
+    q = np.zeros((1, P), np.float32)
+    q[0, :4] = [3.0, -5.0, 0.25, 1024.0]
+    # group 1: 1 + 2^-11 rounds to even (1.0) in FP16; 1 + 2^-10 is representable
+    q[0, 4:8] = [1.0, 2.0 ** -11, 2.0 ** -11, 0.0]
+    # group 2: FP16 overflow (65504 is the largest finite value)
+    q[0, 8:12] = [60000.0, 10000.0, 0.0, 0.0]
+    t = orc.lut4_table(q)[0].astype(np.float64)
+    assert t.shape == (P // 4, 16)
+    # single bits: bit 3 of the pattern is the group's first dimension
+    assert [t[0, 8], t[0, 4], t[0, 2], t[0, 1]] == [3.0, -5.0, 0.25, 1024.0]
+    # all four: 1022.25 is halfway between the FP16 neighbours 1022.0 (even) and 1022.5
+    assert t[0, 0] == 0.0 and t[0, 15] == 1022.0
+    assert t[1, 0b1100] == 1.0 and t[1, 0b1110] == 1.0 + 2.0 ** -10
+    assert np.isinf(t[2, 0b1100]) and t[2, 0b1000] == 60000.0
+
+
+def test_lut4_ip_accumulation_order_and_nibble_layout():
+    """a0 gathers the even nibbles, a1 the odd ones, each in FP32 in nibble order; the
+    estimate is a0 + a1. With nibble 0's entry 1.0 and every other nibble's 2^-24, a0 stays
+    1.0 (1 + 2^-24 rounds back to 1), a1 sums the odd nibbles exactly, so the result is
+    1 + n_odd * 2^-24 rounded once; one accumulator would return 1.0."""
+    P = 128  # 32 nibbles: 16 odd ones
+    q = np.zeros((1, P), np.float32)
+    q[0, 0] = 1.0
+    for g in range(1, P // 4):
+        q[0, 4 * g] = 2.0 ** -24  # FP16's smallest subnormal
+    lut = orc.lut4_table(q)[0]
+    bits = np.zeros((1, P), np.uint8)
+    bits[0, ::4] = 1  # the first dimension of every group: pattern 8 in every nibble
+    got = orc.lut4_ip(words_of_bits(bits), lut)[0]
+    assert got == np.float32(1.0 + 16 * 2.0 ** -24)
+    # bit layout: a single set dimension d selects the entry of its own nibble
+    rng = np.random.default_rng(4)
+    qr = rng.normal(0, 1, (1, P)).astype(np.float32)
+    t = orc.lut4_table(qr)[0]
+    for d in (0, 1, 2, 3, 31, 32, 77, 127):
+        b = np.zeros((1, P), np.uint8)
+        b[0, d] = 1
+        assert orc.lut4_ip(words_of_bits(b), t)[0] == np.float32(np.float16(qr[0, d]))
+
+
+def test_lut4_ip_equals_exact_sum_for_representable_values():
+    """Small integers: every table entry and partial sum is exact in FP16 and FP32, so the
+    estimate equals the integer inner product <b, q>."""
+    rng = np.random.default_rng(5)
+    for P in (64, 128, 768):
+        q = rng.integers(-20, 21, (3, P)).astype(np.float32)
+        bits = rng.integers(0, 2, (40, P), dtype=np.uint8)
+        w = words_of_bits(bits)
+        for i in range(3):
+            got = orc.lut4_ip(w, orc.lut4_table(q[i:i + 1])[0])
+            assert np.array_equal(got, (bits.astype(np.int64) @ q[i].astype(np.int64)).astype(np.float32))
