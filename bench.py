@@ -94,7 +94,7 @@ def hbm_traffic(cfg, nprobe, kernel):
         return None
     data = json.loads(f.read_text())
     for name, v in data.get("kernels", {}).items():
-        if kernel in name:
+        if v.get("role") == kernel:
             return int(v["fetch_bytes"] + v["write_bytes"])
     return None
 

@@ -167,6 +167,55 @@ def test_query_preparation(case_name, request):
     assert np.array_equal(qint_from_planes(g["planes"][:, 8:]), qres)
 
 
+def test_bq8_quantiser_at_rounding_boundaries(tmp_path):
+    """The GPU's Bq=8 query quantisation on rows placed at its rounding boundaries: exact
+    ties with width 2^-3, and components where q * f32(1/width) and q / width round to
+    different integers. The index's rotator is the identity and the FP32 GEMM rotates, so
+    the quantiser sees the rows unchanged; the expected codes come from exact rational
+    arithmetic (query_kernels.cuh:158-176: __float2int_rn(q * inv_width))."""
+    from test_oracle import bq8_expected, f32_round, rint_even
+    from fractions import Fraction
+    dim = 64
+    rng = np.random.default_rng(31)
+    rows = []
+    tie = np.zeros(dim, np.float32)
+    tie[0] = np.float32(127.0 / 8.0)
+    tie[1:9] = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5], np.float32) / np.float32(8.0)
+    rows.append(tie)
+    while len(rows) < 24:
+        row = np.zeros(dim, np.float32)
+        row[0] = np.float32(rng.uniform(0.1, 50.0))
+        _, width, inv = bq8_expected(row[:1])
+        cases = []
+        for k in range(-120, 121, 3):
+            c = np.float32((k + 0.5) * float(width))
+            for cand in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+                a = rint_even(Fraction(float(f32_round(Fraction(float(cand)) * Fraction(float(inv))))))
+                b = rint_even(Fraction(float(f32_round(Fraction(float(cand)) / Fraction(float(width))))))
+                if a != b:
+                    cases.append(cand)
+        if cases:
+            row[1:1 + min(dim - 1, len(cases))] = cases[:dim - 1]
+            rows.append(row)
+    q = np.stack(rows).astype(np.float32)
+    nq = q.shape[0]
+    base = rng.normal(0, 1, (256, dim)).astype(np.float32)
+    R = np.eye(dim, dtype=np.float32)
+    path = tmp_path / "eye.index"
+    ca.build_ivf(path, base, base[:2].copy(), (np.arange(256) % 2).astype(np.uint32), R, metric=0)
+    case = Case(path, q)
+    say(f"[gpu] Bq=8 quantiser on {nq} boundary rows")
+    eng, _, _ = run_frozen(case, 2, 10, extra_flags=ca.FLAG_FP32_GEMM)
+    g = gpu_intermediates(eng, case, 2)
+    assert np.array_equal(g["qr"].view(np.uint32), q.view(np.uint32))  # the identity rotation is exact
+    got = qint_from_planes(g["planes"][:, :8])
+    for r in range(nq):
+        want, width, _ = bq8_expected(q[r])
+        assert g["width"][r] == width, r
+        assert np.array_equal(got[r], want), r
+    eng.close()
+
+
 @pytest.mark.parametrize("case_name", CASES)
 @pytest.mark.parametrize("fp32", [False, True])
 def test_coarse_probe(case_name, fp32, request):
