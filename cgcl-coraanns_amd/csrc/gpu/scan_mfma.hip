@@ -6,8 +6,8 @@
 // to 16 same-cluster pairs, so a 64-vector tile against the unit's queries is a
 // [64 x P] x [P x 16] integer product: four 16x16 output blocks, P/32 K-steps each, plus
 // the same product against the residual query (qres) for the two-stage exact_ip. The
-// code bits are widened to int8 in registers (one multiply spreads a nibble over four
-// bytes); the queries' int8 values come from the query preparation. ip_int and ip_res are
+// code bits are widened to int8 through a 256-entry table in LDS (one 8-byte read per
+// code byte); the queries' int8 values come from the query preparation. ip_int and ip_res are
 // therefore bit-identical to the popcount kernel's (scan.hip), and the lower bound uses
 // the same expression, so the candidate set is the same.
 //
@@ -126,8 +126,13 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
     constexpr int G = (W + 3) / 4;  // code word groups of a tile
     __shared__ uint4 s_rec[kDense ? 1 : kStage];
     __shared__ float s_cut[kDense ? 1 : kStage];
+    // bits 0..7 of a byte b as eight int8 0/1 values (the MFMA operand): s_spread[b]
+    __shared__ long s_spread[256];
     const uint32_t lane = threadIdx.x, col = lane & 15, quad = lane >> 4;
     const uint32_t P = 32u * W;
+    for (uint32_t b = lane; b < 256; b += 64)
+        s_spread[b] = spread_byte(b);
+    __syncthreads();
     const QueueDev q = p.queue;
     // kLows runs over the vanguard unit set, kPublish over the far units, the dense debug
     // output over either
@@ -210,7 +215,7 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
                 accr[m] = v4i32{0, 0, 0, 0};
 #pragma unroll
                 for (int kc = 0; kc < W; ++kc) {
-                    const long a = spread_byte((xw[m][kc] >> (8 * quad)) & 0xFFu);
+                    const long a = s_spread[(xw[m][kc] >> (8 * quad)) & 0xFFu];
                     acc[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq[kc], acc[m], 0, 0, 0);
                     if constexpr (kMode != kLows)
                         accr[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, br[kc], accr[m], 0, 0, 0);
@@ -295,16 +300,6 @@ __device__ __forceinline__ int tile_ip_res(const uint8_t *__restrict__ tile, uin
     return popc_ip<W>(x, rplanes, W);
 }
 
-// Sixteen bits as sixteen int8 0/1 values (bit e in byte e): one 128-bit MFMA operand.
-// Each nibble spreads over four bytes with one 24-bit multiply (copies 7 bits apart).
-__device__ __forceinline__ v4i32 spread16(uint32_t h) {
-    v4i32 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        r[i] = (int)(__umul24((h >> (4 * i)) & 15u, 0x00204081u) & 0x01010101u);
-    return r;
-}
-
 // Survivors staged with their ip_int and tile position get their two-stage exact_ip.
 template <int W>
 __device__ void finalize_records(const ScanParams &p, uint32_t n, uint4 *s_rec, const uint32_t *s_loc,
@@ -339,6 +334,9 @@ constexpr int kStageWide = 384;  // wide kernel: flushed when a row block could 
 // (W/2 x 16 bytes) stay in VGPRs. Only the dimension pairing between the two operands
 // matters to the sum, so ip_int is exact. The lower bound uses the popcount kernels'
 // expression; ip_res is evaluated for survivors when they are published.
+// The sixteen code bits of an operand become sixteen int8 0/1 bytes through a 256-entry
+// table in LDS (two 8-byte reads per operand): widening them arithmetically took 16 VALU
+// instructions per operand and bounded the kernel (10-13% faster at P = 768).
 template <int W, int kMode>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void far_mfma_wide_kernel(const ScanParams p) {
     constexpr bool kDense = kMode != kPublish;
@@ -349,7 +347,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
     __shared__ uint4 s_rec[kDense ? 1 : kStageWide];
     __shared__ float s_cut[kDense ? 1 : kStageWide];
     __shared__ uint32_t s_loc[kDense ? 1 : kStageWide];
+    // bits 0..7 of a byte b as eight int8 0/1 values: s_spread[b]
+    __shared__ uint2 s_spread[256];
     const uint32_t lane = threadIdx.x, col = lane & 15, quad = lane >> 4;
+    for (uint32_t b = lane; b < 256; b += 64) {
+        const long v = spread_byte(b);
+        s_spread[b] = make_uint2((uint32_t)v, (uint32_t)((unsigned long long)v >> 32));
+    }
+    __syncthreads();
+    const auto spread16_lds = [&](uint32_t h) -> v4i32 {
+        const uint2 a = s_spread[h & 255u], b = s_spread[(h >> 8) & 255u];
+        return v4i32{(int)a.x, (int)a.y, (int)b.x, (int)b.y};
+    };
     const QueueDev q = p.queue;
     // kLows runs over the vanguard unit set, kPublish over the far units, the dense debug
     // output over either
@@ -423,8 +432,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                 v4i32 acc = v4i32{0, 0, 0, 0}, acc1 = v4i32{0, 0, 0, 0};
 #pragma unroll
                 for (int j = 0; j < WQ; ++j) {
-                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16(xw[j] & 0xFFFFu), bq[2 * j], acc, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16(xw[j] >> 16), bq[2 * j + 1], acc1, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16_lds(xw[j] & 0xFFFFu), bq[2 * j], acc, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16_lds(xw[j] >> 16), bq[2 * j + 1], acc1, 0, 0, 0);
                 }
                 acc += acc1;
                 const uint32_t o = 16 * m + 4 * quad;

@@ -667,21 +667,14 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
     if constexpr (kPre) {
         // ---- precomputed bounds: wave w takes chunks w, w + 4, ... of the query (pairs in
         // probe order); four chunk buffers per wave, the current segment's two and the next
-        // segment's two. A segment that refines the list fetches the next segment's chunks
-        // again afterwards, so no chunk is held across the refinement ----
+        // segment's two, which stay in flight (or in registers) across a refinement of the
+        // list (six VGPRs per chunk) ----
         struct Chunk {
             float4 v;                // bounds of vectors 4 lane .. 4 lane + 3 of the chunk
             uint32_t lim, posbase;   // wave-uniform: valid vectors, list position of vector 0
         };
-        // pair cursor, advanced by fetches in increasing chunk order (reset to refetch)
-        uint32_t jf = 0, f_next = 0, f_toff = 0, f_n = 0, f_off = 0;
-        auto reset_cursor = [&]() {
-            jf = 0;
-            f_toff = 0;
-            f_next = uniform(S.toff[1]);
-            f_n = uniform(S.n[0]);
-            f_off = 0;
-        };
+        // pair cursor, advanced by fetches in increasing chunk order
+        uint32_t jf = 0, f_next = uniform(S.toff[1]), f_toff = 0, f_n = uniform(S.n[0]), f_off = 0;
         auto fetch = [&](uint32_t gg, Chunk &c) {
             while (gg >= f_next) {
                 ++jf;
@@ -721,7 +714,6 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
         const uint32_t per_seg = kPreSegChunks * kVqWaves;
         const uint32_t nseg = (T + per_seg - 1) / per_seg;
         Chunk c0{}, c1{}, c2{}, c3{};
-        reset_cursor();
         if (wave < T)
             fetch(wave, c0);
         if (wave + kVqWaves < T)
@@ -746,11 +738,6 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                 if (tid == 0)
                     S.nlist = 0;
                 __syncthreads();
-                reset_cursor();
-                if (g1 < T)
-                    fetch(g1, na);
-                if (g1 + kVqWaves < T)
-                    fetch(g1 + kVqWaves, nb);
             }
             if (g2 < T)
                 fetch(g2, a);
