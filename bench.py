@@ -143,6 +143,9 @@ def main():
     ap.add_argument("--ip-kernel", choices=["bitwise", "lut4"], default="bitwise",
                     help="estimator: bitwise (Bq=8 popcount bound, the default here) or lut4 (the reference's "
                          "FP16 nibble-LUT estimator, set_ip_kernel_type(Lut4Bit))")
+    ap.add_argument("--unfused-probe", action="store_true",
+                    help="coarse probe through the whole distance matrix and a select pass over it, instead of "
+                         "the select fused into the GEMM epilogue")
     ap.add_argument("--fp32-gemm", action="store_true",
                     help="query rotation and coarse-probe distances from the FP32 matrix-core GEMMs instead of the split-FP16 ones")
     ap.add_argument("--workdir", default="",
@@ -198,7 +201,8 @@ def main():
                          cpu_threads=threads, gpu_seed_refine=not args.no_gpu_seed,
                          gpu_refine_filter=not args.no_gpu_prefilter,
                          extra_flags=(ca.FLAG_FP32_GEMM if args.fp32_gemm else 0) |
-                                     (ca.FLAG_NO_VANGUARD_MFMA if args.no_vanguard_mfma else 0),
+                                     (ca.FLAG_NO_VANGUARD_MFMA if args.no_vanguard_mfma else 0) |
+                                     (ca.FLAG_UNFUSED_PROBE if args.unfused_probe else 0),
                          lower_bound_scale=args.lower_bound_scale or None, gpu_final_topk=args.gpu_final,
                          ip_kernel_type=args.ip_kernel)
     eng.load_ivf(ivf)
@@ -245,6 +249,7 @@ def main():
     for _ in range(args.warmup):
         step(nprobe)
     times, times_search, scan_ms, scan_bytes, recalls, probe_ms, probe_flops = [], [], [], [], [], [], []
+    select_ms = []
     recalls_k = []
     van_ms, van_bytes, lows_ms, lows_bytes = [], [], [], []
     last_ids = None
@@ -254,6 +259,7 @@ def main():
         times.append(dt)
         times_search.append(step.search_only)
         probe_ms.append(st["probe_ms"])
+        select_ms.append(st["phase_ms"][1])
         probe_flops.append(st["probe_flops"])
         scan_ms.append(st["scan_ms"])
         scan_bytes.append(st["scan_bytes"])
@@ -292,11 +298,13 @@ def main():
                       "achieved": round(3 * probe_tflops, 3), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                       "frac": round(3 * probe_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
                       "fp32_equivalent_tflops": round(probe_tflops, 3)}
+    probe_line["select_and_gadd_ms"] = round(float(np.mean(select_ms)), 4)
     log(f"[timed] nprobe={nprobe} steps={args.steps} QPS={qps:.1f} recall={np.mean(recalls):.4f} "
         f"vanguard lows={avg_lows_ms:.3f}ms {lows_bpl / 1e6:.1f}MB -> {lows_achieved:.1f} GB/s; "
         f"vanguard={avg_van_ms:.3f}ms {van_bpl / 1e6:.1f}MB -> {van_achieved:.1f} GB/s; "
         f"far scan={avg_scan_ms:.3f}ms {bytes_per_launch / 1e6:.1f}MB -> {achieved:.1f} GB/s; "
-        f"probe GEMM {avg_probe_ms:.3f}ms -> {probe_tflops:.2f} TFLOP/s")
+        f"probe GEMM {avg_probe_ms:.3f}ms -> {probe_tflops:.2f} TFLOP/s; "
+        f"probe select + g_add {float(np.mean(select_ms)):.3f}ms")
 
     # the dominant scan kernel of the step (HIP events on the engine stream around it)
     W = c.padded_dim // 32

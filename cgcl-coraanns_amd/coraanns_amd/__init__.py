@@ -38,6 +38,7 @@ FLAG_CROSS_QUERY_REUSE = 4
 DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range(5)
 DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
 DBG_SEED_DIST, DBG_THRESHOLDS, DBG_PROBE_DIST, DBG_VANGUARD_LOWS, DBG_LUT = 10, 11, 12, 13, 14
+DBG_PROBE_FALLBACK = 15
 FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
 FLAG_PAIR_SEEDS = 1 << 6
 FLAG_NO_MFMA_SCAN = 1 << 7
@@ -46,6 +47,7 @@ FLAG_NO_VANGUARD_MFMA = 1 << 9
 FLAG_VANGUARD_MFMA = 1 << 10
 FLAG_GPU_FINAL = 1 << 11
 FLAG_LUT4 = 1 << 12
+FLAG_UNFUSED_PROBE = 1 << 13
 KERNEL_TYPES = {None: 0, "lut4": 1, "bitwise": 2}
 
 

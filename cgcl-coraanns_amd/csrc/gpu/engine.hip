@@ -81,6 +81,7 @@ struct cora_gpu_engine {
     uint4 *d_seed_rec = nullptr;
     float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
     unsigned long long *d_selbig = nullptr;  // [max_q][2][max_nprobe] probe select scratch, nprobe > 4096
+    uint32_t *d_probe_fb = nullptr;          // [1 + max_q] fused probe select: fallback count, rows
     // GPU-final top-k: per-query counts/offsets/cursor, grouped keys [spill_cap], results
     uint32_t *d_fcount = nullptr, *d_foff = nullptr, *d_fcur = nullptr, *d_fidx = nullptr;
     unsigned long long *d_fkeys = nullptr;
@@ -107,6 +108,7 @@ struct cora_gpu_engine {
     cora_search_args last{};
     uint32_t last_depth = 0, last_batch = 1;
     bool last_timing = false, last_fused = false, last_mfma = false, last_van_lows = false, last_final = false;
+    bool last_fused_probe = false;  // the last search selected its probes in the GEMM epilogue + merge
     int last_vanguard_mode = 0;  // cora_search_stats::vanguard_mode
 };
 
@@ -221,6 +223,7 @@ void release_workspace(cora_gpu_engine *E) {
     dfree(E->d_seed_rec);
     dfree(E->d_van_lows);
     dfree(E->d_selbig);
+    dfree(E->d_probe_fb);
     dfree(E->d_fcount);
     dfree(E->d_foff);
     dfree(E->d_fcur);
@@ -574,6 +577,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_seed, std::max<uint64_t>(1, max_q * depth * seed_words)));
         if (max_nprobe > (uint64_t)kSelectMaxProbe)
             TRY(dalloc(E, E->d_selbig, max_q * 2 * max_nprobe));
+        TRY(dalloc(E, E->d_probe_fb, 1 + max_q));
         if (depth > 0) {
             // a multiple of 256: the fused pass streams a pair's bounds 256 at a time
             E->van_stride = (E->max_cluster + 255) / 256 * 256;
@@ -791,16 +795,29 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // coarse probing (hybrid.cu:465-498)
     if (timing)
         HIPCHK(hipEventRecord(E->ev_p0, s));
-    if (split_gemm && dist_gemm_f16x3_supported(P, nq, E->nl)) {
+    const bool split_probe = split_gemm && dist_gemm_f16x3_supported(P, nq, E->nl);
+    // the fused select keeps its candidates in the distance matrix's memory
+    const bool fused_probe = split_probe && !(a->flags & CORA_FLAG_UNFUSED_PROBE) &&
+                             fused_probe_supported((uint32_t)E->nl, np) &&
+                             fused_probe_scratch_bytes(nq, (uint32_t)E->nl) <= (size_t)nq * E->nl * sizeof(float);
+    E->last_fused_probe = fused_probe;
+    if (split_probe) {
         launch_split_f16(E->d_qrot, nq, P, E->d_q_hl, E->d_qscale, s);
-        launch_dist_gemm_f16x3(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
-                               nq, (uint32_t)E->nl, P, E->d_dist, s);
+        if (fused_probe)
+            launch_fused_probe_gemm(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
+                                    nq, (uint32_t)E->nl, P, E->d_dist, E->d_probe_fb, s);
+        else
+            launch_dist_gemm_f16x3(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
+                                   nq, (uint32_t)E->nl, P, E->d_dist, s);
     } else
         launch_dist_gemm(E->d_qrot, E->d_qnorm, E->d_cent, E->d_cnorm, nq, (uint32_t)E->nl, P,
                          E->d_dist, s);
     if (timing)
         HIPCHK(hipEventRecord(E->ev_p1, s));
-    if (np > (uint32_t)kSelectMaxProbe)
+    if (fused_probe)
+        launch_fused_probe_select(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm, nq,
+                                  (uint32_t)E->nl, P, np, E->d_dist, E->d_probe_fb, E->d_pidx, s);
+    else if (np > (uint32_t)kSelectMaxProbe)
         launch_select_big(E->d_dist, nq, (uint32_t)E->nl, np, E->d_selbig, E->d_pidx, s);
     else
         launch_select(E->d_dist, nq, (uint32_t)E->nl, np, E->d_pidx, s);
@@ -1125,7 +1142,24 @@ int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes
     case CORA_DBG_PROBE_IDX: src = E->d_pidx; size = nq * np * 4; break;
     case CORA_DBG_PROBE_GADD: src = E->d_gadd; size = nq * np * 4; break;
     case CORA_DBG_PROBE_GERR: src = E->d_gerr; size = nq * np * 4; break;
-    case CORA_DBG_PROBE_DIST: src = E->d_dist; size = nq * E->nl * 4; break;
+    case CORA_DBG_PROBE_DIST:
+        if (E->last_fused_probe)
+            return fail(E, CORA_ERR_LOGIC,
+                        "debug_read: the last search selected its probes without the distance matrix "
+                        "(CORA_FLAG_UNFUSED_PROBE keeps it)");
+        src = E->d_dist;
+        size = nq * E->nl * 4;
+        break;
+    case CORA_DBG_PROBE_FALLBACK:
+        if (bytes != (1 + nq) * 4)
+            return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_read: size mismatch");
+        if (!E->last_fused_probe) {
+            memset(dst, 0, bytes);
+            return CORA_OK;
+        }
+        src = E->d_probe_fb;
+        size = (1 + nq) * 4;
+        break;
     case CORA_DBG_PAIRS: {
         if (bytes != nq * np * 12)
             return fail(E, CORA_ERR_INVALID_ARGUMENT, "debug_read: size mismatch");

@@ -199,6 +199,21 @@ void launch_rotate_f16x3(const uint16_t *xhl, const float *xscale, const uint16_
 void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const float *qnorm,
                             const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t nq,
                             uint32_t nl, uint32_t P, float *dist, hipStream_t s);
+// Fused coarse-probe select (nl >= 8,192, nprobe <= 64, nl <= kFusedProbeMaxList): the split-FP16
+// distance GEMM keeps 8 candidate keys per query and 128-cluster tile in scratch (the distance
+// matrix's memory: at least fused_probe_scratch_bytes, and nq x nl floats for the fallback);
+// the select part merges them into the top-nprobe idx, and the queries the candidates cannot
+// settle (fb: 1 + nq words, [0] their count, then their rows) are selected again from their
+// distance rows, computed again into the same scratch.
+constexpr uint32_t kFusedProbeMaxList = 65536;
+bool fused_probe_supported(uint32_t nl, uint32_t nprobe);
+size_t fused_probe_scratch_bytes(uint32_t nq, uint32_t nl);
+void launch_fused_probe_gemm(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
+                             const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
+                             void *scratch, uint32_t *fb, hipStream_t s);
+void launch_fused_probe_select(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
+                               const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
+                               uint32_t nprobe, void *scratch, uint32_t *fb, int32_t *idx, hipStream_t s);
 void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const float *cnorm,
                       uint32_t nq, uint32_t nl, uint32_t P, float *dist, hipStream_t s);
 // nprobe <= kSelectMaxProbe (selection held in LDS)

@@ -21,6 +21,16 @@ constexpr int kTileK = 16;  // K slice staged in LDS per step
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+// set bits of mask below this lane
+__device__ __forceinline__ uint32_t lanes_below(unsigned long long mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // C[m][n] = sum_k A[m][k] * B(k, n) on the matrix cores (v_mfma_f32_16x16x4f32: FP32
 // inputs, FP32 accumulation). A is row-major [M][K]. With TRANS_B the second operand is
 // Bt [N][K] (B(k, n) = Bt[n][k]) and the epilogue forms the L2 distance
@@ -283,15 +293,43 @@ __global__ __launch_bounds__(64) void split_f16_kernel(const float *__restrict__
 
 constexpr int kHT = 128;  // output tile edge
 constexpr int kHK = 32;   // K per LDS stage: one v_mfma_f32_16x16x32_f16 step
+constexpr int kFallbackRowTiles = 8;        // row tiles of the fused select's fallback GEMM grid
+constexpr int kFallbackSelectBlocks = 512;  // workgroups of its fallback select
 
 // LDS slot of the 8-half group g (0..3) of tile row r: the XOR spreads the 16 rows x 4
 // groups of one MFMA operand read over distinct banks
 __device__ __forceinline__ int hslot(int r, int g) { return r * 4 + (g ^ ((r >> 1) & 3)); }
 
-// C[m][n] = <a_m, b_n> for A [M][K] and B [N][K] given as split-FP16 rows (Ah/Al, scale
-// as; Bh/Bl, scale bs), with kDist the L2 distance an[m] + bn[n] - 2 <a_m, b_n> (coarse
-// probe; without it the query rotation Q . R with B = R^T); K % 32 == 0, rows 16-byte
-// aligned. 128 x 128
+// The coarse-probe distance of one (query, cluster) pair from the GEMM accumulator: the
+// product scaled back (s is a power of two), then ||q'||^2 + ||c'||^2 - 2 <q',c'> with one
+// rounding of the fused multiply-add; every mode of the GEMM forms it the same way.
+__device__ __forceinline__ float probe_distance(float acc, float s, float an, float bn) {
+    return __fmaf_rn(-2.0f, __fmul_rn(acc, s), __fadd_rn(an, bn));
+}
+
+// The median of three unsigned words (v_med3_u32; the compiler does not form it from min and
+// max of run-time bounds): for a <= b, x clamped to [a, b].
+__device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t x) {
+    uint32_t r;
+    asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(x));
+    return r;
+}
+
+// Fused probe select: the GEMM epilogue keeps, per query row and 128-cluster tile, the
+// kProbeSlots smallest (distance, cluster) keys, compared on the order key with its low 7 bits
+// replaced by the column in the tile (so the 128 keys of a row are distinct 32-bit values
+// and the comparison is one v_med3 per slot); the exact keys of the kept columns are stored.
+constexpr int kProbeSlots = 8;  // a power of two
+constexpr int kEs = kHT + 4;  // LDS row stride (floats) of the epilogue's half tile: no bank conflicts
+
+// kMode 0: C = A . B^T (the query rotation Q . R with B = R^T). kMode 1: the distance matrix
+// an[m] + bn[n] - 2 <a_m, b_n> (coarse probe). kMode 2: the same distances reduced in the
+// epilogue to each row's kProbeSlots smallest keys per 128-column tile, written to
+// cand [M][ntiles][kProbeSlots] as (order key << 32 | column) (the distance matrix is not
+// written). kMode 3: distance rows of selected operand rows: output row m is A's row rmap[m],
+// for m < *mcount (at most M), the grid's row tiles sweeping them mstep rows at a time.
+// A [M][K] and B [N][K] are split-FP16 rows (Ah/Al, scale as; Bh/Bl, scale bs);
+// K % 32 == 0, rows 16-byte aligned. 128 x 128
 // output tile per workgroup of four waves (64 x 64 each, 4 x 4 MFMA blocks of 16 x 16),
 // K staged in LDS 32 at a time in one buffer (the next stage's loads in registers during
 // the MFMAs; 32 KB of LDS and 158 VGPRs let three workgroups share a CU, which hides the
@@ -300,105 +338,204 @@ __device__ __forceinline__ int hslot(int r, int g) { return r * 4 + (g ^ ((r >> 
 // D[4 (l / 16) + r][l % 16]. Tile order: XCD x (blockIdx.x % 8) owns column tiles
 // [x ncx, (x + 1) ncx), swept by groups of four row tiles, so the workgroups resident on
 // an XCD share their operand tiles in its L2.
-template <bool kDist>
+template <int kMode>
 __global__ __launch_bounds__(256, 3) void dist_gemm_f16x3_kernel(
     const _Float16 *__restrict__ Ah, const _Float16 *__restrict__ Al, const float *__restrict__ as,
     const _Float16 *__restrict__ Bh, const _Float16 *__restrict__ Bl, const float *__restrict__ bs,
     float *__restrict__ C, uint32_t M, uint32_t N, uint32_t K, const float *__restrict__ an,
-    const float *__restrict__ bn, uint32_t ncx) {
-    __shared__ half8_t S[4][kHT * 4];  // [Ah, Al, Bh, Bl][row x group]
+    const float *__restrict__ bn, uint32_t ncx, uint32_t mstep, const uint32_t *__restrict__ rmap,
+    const uint32_t *__restrict__ mcount, unsigned long long *__restrict__ cand, uint32_t ntiles) {
+    constexpr size_t kOperandBytes = 4 * kHT * 4 * sizeof(half8_t);
+    constexpr size_t kHalfBytes = 64 * kEs * sizeof(float);
+    constexpr size_t kLdsBytes = kMode == 2 && kHalfBytes > kOperandBytes ? kHalfBytes : kOperandBytes;
+    __shared__ __align__(16) unsigned char s_raw[kLdsBytes];
+    half8_t(*S)[kHT * 4] = reinterpret_cast<half8_t(*)[kHT * 4]>(s_raw);  // [Ah, Al, Bh, Bl][row x group]
     const uint32_t xcd = blockIdx.x % kNumXcd, bi = blockIdx.x / kNumXcd;
     const uint32_t grp = bi / (4 * ncx), within = bi % (4 * ncx);
-    const uint32_t m0 = (grp * 4 + within % 4) * kHT, n0 = (xcd * ncx + within / 4) * kHT;
-    if (m0 >= M || n0 >= N)
+    const uint32_t n0 = (xcd * ncx + within / 4) * kHT;
+    const uint32_t Me = kMode == 3 ? min(M, *mcount) : M;
+    if (n0 >= N)
         return;  // the whole workgroup: padding of the tile grid
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    f32x4_t acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const int i16 = lane & 15, g = lane >> 4;
     // staging: thread t moves group t & 3 of rows t >> 2 and 64 + (t >> 2) of each array
     const int srow = tid >> 2, sg = tid & 3;
-    half8_t st[4][2];
-    auto load = [&](uint32_t k0) {
+    auto row_tile = [&](uint32_t m0) __attribute__((always_inline)) {
+        f32x4_t acc[4][4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            // rows past M (N) repeat the last row: they only feed outputs that are not stored;
-            // 32-bit element offsets (M K, N K < 2^31, checked by the launcher) off uniform bases
-            const uint32_t ka = min(m0 + srow + 64 * h, M - 1) * K + k0 + 8 * sg;
-            const uint32_t kb = min(n0 + srow + 64 * h, N - 1) * K + k0 + 8 * sg;
-            st[0][h] = *reinterpret_cast<const half8_t *>(Ah + ka);
-            st[1][h] = *reinterpret_cast<const half8_t *>(Al + ka);
-            st[2][h] = *reinterpret_cast<const half8_t *>(Bh + kb);
-            st[3][h] = *reinterpret_cast<const half8_t *>(Bl + kb);
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        half8_t st[4][2];
+        auto load = [&](uint32_t k0) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                // rows past the last (M, or *mcount) repeat it: they only feed outputs that are
+                // not stored; 32-bit element offsets (M K, N K < 2^31, checked by the launcher)
+                const uint32_t r = min(m0 + srow + 64 * h, Me - 1);
+                const uint32_t ka = (kMode == 3 ? rmap[r] : r) * K + k0 + 8 * sg;
+                const uint32_t kb = min(n0 + srow + 64 * h, N - 1) * K + k0 + 8 * sg;
+                st[0][h] = *reinterpret_cast<const half8_t *>(Ah + ka);
+                st[1][h] = *reinterpret_cast<const half8_t *>(Al + ka);
+                st[2][h] = *reinterpret_cast<const half8_t *>(Bh + kb);
+                st[3][h] = *reinterpret_cast<const half8_t *>(Bl + kb);
+            }
+        };
+        auto stage = [&]() {
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    S[a][hslot(srow + 64 * h, sg)] = st[a][h];
+        };
+        load(0);
+        stage();
+        __syncthreads();
+        for (uint32_t k0 = 0; k0 < K; k0 += kHK) {
+            const bool more = k0 + kHK < K;
+            if (more)
+                load(k0 + kHK);
+            half8_t ah[4], al[4], bh[4], bl[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                ah[t] = S[0][hslot(wm + 16 * t + i16, g)];
+                al[t] = S[1][hslot(wm + 16 * t + i16, g)];
+                bh[t] = S[2][hslot(wn + 16 * t + i16, g)];
+                bl[t] = S[3][hslot(wn + 16 * t + i16, g)];
+            }
+            // the three products in turn over all 16 blocks: an accumulator's dependent MFMAs
+            // are 16 instructions apart
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 4; ++tj)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ti], bh[tj], acc[ti][tj], 0, 0, 0);
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 4; ++tj)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ti], bl[tj], acc[ti][tj], 0, 0, 0);
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 4; ++tj)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ti], bh[tj], acc[ti][tj], 0, 0, 0);
+            if (more) {
+                __syncthreads();  // every wave's operand reads of this stage are done
+                stage();
+                __syncthreads();
+            }
         }
-    };
-    auto stage = [&]() {
+        if constexpr (kMode != 2) {
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+            for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                S[a][hslot(srow + 64 * h, sg)] = st[a][h];
-    };
-    load(0);
-    stage();
-    __syncthreads();
-    const int i16 = lane & 15, g = lane >> 4;
-    for (uint32_t k0 = 0; k0 < K; k0 += kHK) {
-        const bool more = k0 + kHK < K;
-        if (more)
-            load(k0 + kHK);
-        half8_t ah[4], al[4], bh[4], bl[4];
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t gm = m0 + wm + 16 * ti + 4 * g + r;
+                    if (gm >= Me)
+                        continue;
+                    const uint32_t pm = kMode == 3 ? rmap[gm] : gm;
+                    const float am = kMode != 0 ? an[pm] : 0.0f, sa = as[pm];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            ah[t] = S[0][hslot(wm + 16 * t + i16, g)];
-            al[t] = S[1][hslot(wm + 16 * t + i16, g)];
-            bh[t] = S[2][hslot(wn + 16 * t + i16, g)];
-            bl[t] = S[3][hslot(wn + 16 * t + i16, g)];
-        }
-        // the three products in turn over all 16 blocks: an accumulator's dependent MFMAs
-        // are 16 instructions apart
+                    for (int tj = 0; tj < 4; ++tj) {
+                        const uint32_t gn = n0 + wn + 16 * tj + i16;
+                        if (gn < N)
+                            C[(size_t)gm * N + gn] = kMode != 0 ? probe_distance(acc[ti][tj][r], sa * bs[gn], am, bn[gn])
+                                                                : acc[ti][tj][r] * (sa * bs[gn]);
+                    }
+                }
+        } else {
+            // one half tile (64 rows x 128 columns) at a time through the LDS; four threads per
+            // row each take the columns eq, eq + 4, ... and keep their kProbeSlots smallest
+            // packed keys (sorted, one v_med3 per slot and column), then the row's four
+            // threads merge their lists by shuffles; thread eq stores slots eq, eq + 4, ...
+            float *Et = reinterpret_cast<float *>(s_raw);
+            const uint32_t tile = n0 / kHT;
+            const int er = tid >> 2, eq = tid & 3;
+#pragma unroll 1
+            for (int h = 0; h < 2; ++h) {
+                __syncthreads();  // the LDS's previous readers (operands, or the other half) are done
+                if ((wave >> 1) == h) {
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti)
+                    for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-            for (int tj = 0; tj < 4; ++tj)
-                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ti], bh[tj], acc[ti][tj], 0, 0, 0);
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t gm = m0 + wm + 16 * ti + 4 * g + r;
+                            const uint32_t pm = min(gm, Me - 1);
+                            const float am = an[pm], sa = as[pm];
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti)
+                            for (int tj = 0; tj < 4; ++tj) {
+                                const uint32_t gn = min(n0 + wn + 16 * tj + i16, N - 1);
+                                Et[(16 * ti + 4 * g + r) * kEs + wn + 16 * tj + i16] =
+                                    probe_distance(acc[ti][tj][r], sa * bs[gn], am, bn[gn]);
+                            }
+                        }
+                }
+                __syncthreads();
+                const float *erow = Et + er * kEs;
+                uint32_t t[kProbeSlots];
 #pragma unroll
-            for (int tj = 0; tj < 4; ++tj)
-                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ti], bl[tj], acc[ti][tj], 0, 0, 0);
+                for (int sl = 0; sl < kProbeSlots; ++sl)
+                    t[sl] = ~0u;
+#pragma unroll 2
+                for (int j = 0; j < kHT / 4; ++j) {
+                    const uint32_t col = eq + 4 * j;
+                    const uint32_t x = n0 + col < N ? (order_key(erow[col]) & ~127u) | col : ~0u;
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti)
+                    for (int sl = kProbeSlots - 1; sl > 0; --sl)
+                        t[sl] = med3_u32(t[sl - 1], t[sl], x);
+                    t[0] = min(t[0], x);
+                }
 #pragma unroll
-            for (int tj = 0; tj < 4; ++tj)
-                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ti], bh[tj], acc[ti][tj], 0, 0, 0);
-        if (more) {
-            __syncthreads();  // every wave's operand reads of this stage are done
-            stage();
-            __syncthreads();
-        }
-    }
+                for (int o = 1; o < 4; o <<= 1) {
+                    // the kProbeSlots smallest of two sorted lists: the partner's reversed
+                    // against ours gives a bitonic sequence holding them, which is then sorted
+                    uint32_t p[kProbeSlots];
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+                    for (int sl = 0; sl < kProbeSlots; ++sl)
+                        p[sl] = __shfl_xor(t[sl], o);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t gm = m0 + wm + 16 * ti + 4 * g + r;
-            if (gm >= M)
-                continue;
-            const float am = kDist ? an[gm] : 0.0f, sa = as[gm];
+                    for (int sl = 0; sl < kProbeSlots; ++sl)
+                        t[sl] = min(t[sl], p[kProbeSlots - 1 - sl]);
 #pragma unroll
-            for (int tj = 0; tj < 4; ++tj) {
-                const uint32_t gn = n0 + wn + 16 * tj + i16;
-                if (gn < N) {
-                    const float v = acc[ti][tj][r] * (sa * bs[gn]);
-                    C[(size_t)gm * N + gn] = kDist ? am + bn[gn] - 2.0f * v : v;
+                    for (int st = kProbeSlots / 2; st > 0; st >>= 1)
+#pragma unroll
+                        for (int sl = 0; sl < kProbeSlots; ++sl)
+                            if ((sl & st) == 0) {
+                                const uint32_t a = t[sl], b = t[sl + st];
+                                t[sl] = min(a, b);
+                                t[sl + st] = max(a, b);
+                            }
+                }
+                const uint32_t gm = m0 + h * 64 + er;
+#pragma unroll
+                for (int u = 0; u < kProbeSlots / 4; ++u) {
+                    const int slot = eq + 4 * u;
+                    uint32_t mine = t[0];
+#pragma unroll
+                    for (int sl = 1; sl < kProbeSlots; ++sl)
+                        mine = sl == slot ? t[sl] : mine;
+                    const uint32_t col = mine & 127u;
+                    if (gm < Me)
+                        cand[((size_t)gm * ntiles + tile) * kProbeSlots + slot] =
+                            n0 + col < N ? ((unsigned long long)order_key(erow[col]) << 32) | (n0 + col) : ~0ull;
                 }
             }
         }
+    };
+    const uint32_t m_first = (grp * 4 + within % 4) * kHT;
+    if constexpr (kMode != 3) {
+        if (m_first < M)
+            row_tile(m_first);
+    } else {
+        for (uint32_t m0 = m_first; m0 < Me; m0 += mstep) {
+            row_tile(m0);
+            if (m0 + mstep < Me)
+                __syncthreads();  // the next row tile's staging overwrites the LDS
+        }
+    }
 }
 
 // One wave per query. Each lane owns dimensions lane + 64*i.
@@ -518,15 +655,6 @@ __global__ __launch_bounds__(64) void row_norms_kernel(const float *__restrict__
     }
 }
 
-// set bits of mask below this lane
-__device__ __forceinline__ uint32_t lanes_below(unsigned long long mask) {
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
-__device__ __forceinline__ uint32_t order_key(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
 
 constexpr int kSelThreads = 256;
 
@@ -632,14 +760,13 @@ __device__ uint32_t block_kth_key(EachKey each_key, uint32_t k, uint32_t *hist, 
 // smaller distance and the lowest-index ties in index order, then bitonic sort
 // (key, cluster) ascending in LDS. With kLds the row's order keys are staged in LDS once.
 template <bool kLds>
-__device__ void select_block(const float *__restrict__ dist, uint32_t nl, uint32_t k, uint32_t kpow2,
+__device__ void select_block(const float *__restrict__ row, uint32_t nl, uint32_t k, uint32_t kpow2,
                              int32_t *__restrict__ out) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_red[2 * kSelThreads / 64], s_sc[2];
     __shared__ uint32_t sa[kSelThreads], sb[kSelThreads];
     extern __shared__ unsigned long long sel[];  // [kpow2], then the row's keys with kLds
     uint32_t *keys = reinterpret_cast<uint32_t *>(sel + kpow2);
-    const float *row = dist + (size_t)blockIdx.x * nl;
     const uint32_t t = threadIdx.x;
     auto key_at = [&](uint32_t i) -> uint32_t {
         if constexpr (kLds)
@@ -700,7 +827,7 @@ __device__ void select_block(const float *__restrict__ dist, uint32_t nl, uint32
         }
     }
     for (uint32_t i = t; i < k; i += kSelThreads)
-        out[(size_t)blockIdx.x * k + i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
+        out[i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
 }
 
 template <bool kLds>
@@ -708,7 +835,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float *__rest
                                                              uint32_t nl, uint32_t k,
                                                              uint32_t kpow2,
                                                              int32_t *__restrict__ out) {
-    select_block<kLds>(dist, nl, k, kpow2, out);
+    select_block<kLds>(dist + (size_t)blockIdx.x * nl, nl, k, kpow2, out + (size_t)blockIdx.x * k);
 }
 
 // nlist beyond what registers hold, k <= 64: two streaming passes over the row. Each of the
@@ -806,7 +933,7 @@ __global__ __launch_bounds__(kSelThreads) void select_stream_kernel(const float 
         s_over = 1;
     __syncthreads();
     if (s_over) {
-        select_block<false>(dist, nl, k, kpow2, out);
+        select_block<false>(dist + (size_t)blockIdx.x * nl, nl, k, kpow2, out + (size_t)blockIdx.x * k);
         return;
     }
     for (uint32_t e = lane; e < c; e += 64) {
@@ -841,6 +968,105 @@ __global__ __launch_bounds__(kSelThreads) void select_stream_kernel(const float 
         }
         if (rk < k)
             out[(size_t)blockIdx.x * k + rk] = (int32_t)(uint32_t)(v & 0xFFFFFFFFull);
+    }
+}
+
+// Fused probe select, second half: per query (one wave of four per workgroup) the k smallest
+// of the candidate keys that the distance GEMM kept, kProbeSlots per 128-cluster tile, each
+// (order key << 32 | cluster), so ties fall to the lower cluster id as in the other selects.
+// The k-th smallest of the 64 lanes' minima (the first keys of each lane's tiles) bounds the
+// k-th smallest key, since k distinct keys lie at or below it; the keys up to the bound are
+// compacted in LDS and ranked exactly by counting. The result is proven when no tile can have
+// dropped a key of it: a tile dropped only columns whose packed comparison key, the order key
+// with its low 7 bits cleared, is at least that of its last kept key, so a tile whose last
+// key, so truncated, lies above the k-th key's order key dropped nothing that belongs. A query
+// that fails this (kProbeSlots of its nearest clusters in one tile, or ties within 128 ulps of the
+// k-th distance), or that has more than kMergeCap keys below the bound, goes to the fallback
+// list: its distance row is computed again and selected by the generic select.
+constexpr uint32_t kMergeWaves = 4;
+constexpr uint32_t kMergeCap = 1024;
+
+__global__ __launch_bounds__(64 * kMergeWaves) void probe_merge_kernel(
+    const unsigned long long *__restrict__ cand, uint32_t nq, uint32_t ntiles, uint32_t k,
+    int32_t *__restrict__ idx, uint32_t *__restrict__ fb_count, uint32_t *__restrict__ fb_rows) {
+    __shared__ unsigned long long s_c[kMergeWaves][kMergeCap];
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t q = blockIdx.x * kMergeWaves + w;
+    const bool live = q < nq;  // a wave past the last query still meets every barrier
+    const unsigned long long *cq = cand + (size_t)(live ? q : 0) * ntiles * kProbeSlots;
+    unsigned long long m = ~0ull;
+    if (live)
+        for (uint32_t t = lane; t < ntiles; t += 64)
+            m = min(m, cq[(size_t)t * kProbeSlots]);
+    // bitonic sort of the 64 lane minima, ascending by lane
+    for (uint32_t size = 2; size <= 64; size <<= 1)
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            const unsigned long long o = ((unsigned long long)(uint32_t)__shfl_xor((int)(uint32_t)(m >> 32), (int)stride) << 32) |
+                                         (uint32_t)__shfl_xor((int)(uint32_t)m, (int)stride);
+            const bool take_min = ((lane & stride) == 0) == ((lane & size) == 0);
+            m = take_min ? min(m, o) : max(m, o);
+        }
+    const unsigned long long bound =
+        ((unsigned long long)(uint32_t)__shfl((int)(uint32_t)(m >> 32), (int)(k - 1)) << 32) |
+        (uint32_t)__shfl((int)(uint32_t)m, (int)(k - 1));
+    uint32_t cnt = 0;
+    if (live)
+        for (uint32_t t0 = 0; t0 < ntiles; t0 += 64) {
+            const uint32_t t = t0 + lane;
+#pragma unroll
+            for (int sl = 0; sl < kProbeSlots; ++sl) {
+                const unsigned long long key = t < ntiles ? cq[(size_t)t * kProbeSlots + sl] : ~0ull;
+                const bool take = key <= bound && key != ~0ull;
+                const unsigned long long tm = __ballot(take);
+                const uint32_t pos = cnt + lanes_below(tm);
+                if (take && pos < kMergeCap)
+                    s_c[w][pos] = key;
+                cnt += (uint32_t)__popcll(tm);
+            }
+        }
+    __syncthreads();
+    bool fallback = cnt > kMergeCap;
+    if (live && !fallback) {
+        unsigned long long kth = 0;
+        for (uint32_t i0 = 0; i0 < cnt; i0 += 64) {
+            const uint32_t i = i0 + lane;
+            const unsigned long long key = i < cnt ? s_c[w][i] : ~0ull;
+            uint32_t r = 0;
+            for (uint32_t j = 0; j < cnt; ++j)
+                r += s_c[w][j] < key;
+            if (i < cnt && r < k)
+                idx[(size_t)q * k + r] = (int32_t)(uint32_t)key;
+            if (i < cnt && r == k - 1)
+                kth = key;
+        }
+        // one lane holds the k-th key (cnt >= k: k keys lie at or below the bound)
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+            kth = max(kth, ((unsigned long long)(uint32_t)__shfl_xor((int)(uint32_t)(kth >> 32), o) << 32) |
+                               (uint32_t)__shfl_xor((int)(uint32_t)kth, o));
+        const uint32_t kth_key = (uint32_t)(kth >> 32);
+        bool open = false;
+        for (uint32_t t = lane; t < ntiles; t += 64) {
+            const unsigned long long last = cq[(size_t)t * kProbeSlots + kProbeSlots - 1];
+            open |= last != ~0ull && ((uint32_t)(last >> 32) & ~127u) <= kth_key;
+        }
+        fallback = __ballot(open) != 0;
+    }
+    if (live && fallback && lane == 0)
+        fb_rows[atomicAdd(fb_count, 1u)] = q;
+}
+
+// The fallback rows of the fused select: row r of dist (the distances of query rows[r],
+// computed again) through the generic block select, rows swept by the grid.
+__global__ __launch_bounds__(kSelThreads) void select_rows_kernel(const float *__restrict__ dist, uint32_t nl,
+                                                                  uint32_t k, uint32_t kpow2,
+                                                                  const uint32_t *__restrict__ rows,
+                                                                  const uint32_t *__restrict__ count,
+                                                                  int32_t *__restrict__ out) {
+    const uint32_t n = *count;
+    for (uint32_t r = blockIdx.x; r < n; r += gridDim.x) {
+        select_block<false>(dist + (size_t)r * nl, nl, k, kpow2, out + (size_t)rows[r] * k);
+        __syncthreads();  // the next row reuses the LDS
     }
 }
 
@@ -1325,8 +1551,65 @@ void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const floa
     const uint32_t ncx = (nct + kNumXcd - 1) / kNumXcd, groups = (nrt + 3) / 4;
     const _Float16 *qh = reinterpret_cast<const _Float16 *>(qhl);
     const _Float16 *ch = reinterpret_cast<const _Float16 *>(chl);
-    dist_gemm_f16x3_kernel<true><<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
-        qh, qh + (size_t)nq * P, qscale, ch, ch + (size_t)nl * P, cscale, dist, nq, nl, P, qnorm, cnorm, ncx);
+    dist_gemm_f16x3_kernel<1><<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
+        qh, qh + (size_t)nq * P, qscale, ch, ch + (size_t)nl * P, cscale, dist, nq, nl, P, qnorm, cnorm, ncx,
+        groups * 4 * kHT, nullptr, nullptr, nullptr, 0);
+}
+
+bool fused_probe_supported(uint32_t nl, uint32_t nprobe) {
+    // the merge's bound takes the k-th of 64 lane minima (k <= 64, every lane a tile); the
+    // candidates (nl / 32 keys per query) fit in the distance matrix they replace
+    return nprobe >= 1 && nprobe <= 64 && nl >= 64 * kHT && nl <= kFusedProbeMaxList;
+}
+
+size_t fused_probe_scratch_bytes(uint32_t nq, uint32_t nl) {
+    return (size_t)nq * ((nl + kHT - 1) / kHT) * kProbeSlots * sizeof(unsigned long long);
+}
+
+namespace {
+struct FusedGeometry {
+    uint32_t nct, ncx, groups;
+    const _Float16 *qh, *ch;
+    FusedGeometry(const uint16_t *qhl, const uint16_t *chl, uint32_t nq, uint32_t nl)
+        : nct((nl + kHT - 1) / kHT), ncx((nct + kNumXcd - 1) / kNumXcd),
+          groups(((nq + kHT - 1) / kHT + 3) / 4), qh(reinterpret_cast<const _Float16 *>(qhl)),
+          ch(reinterpret_cast<const _Float16 *>(chl)) {}
+};
+}  // namespace
+
+void launch_fused_probe_gemm(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
+                             const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
+                             void *scratch, uint32_t *fb, hipStream_t s) {
+    if (!nq)
+        return;
+    const FusedGeometry f(qhl, chl, nq, nl);
+    // fb: [0] the fallback count, [1 .. nq] the fallback query rows
+    launch_fill_u32(fb, 0u, 1, s);
+    dist_gemm_f16x3_kernel<2><<<kNumXcd * f.ncx * 4 * f.groups, 256, 0, s>>>(
+        f.qh, f.qh + (size_t)nq * P, qscale, f.ch, f.ch + (size_t)nl * P, cscale, nullptr, nq, nl, P, qnorm, cnorm,
+        f.ncx, f.groups * 4 * kHT, nullptr, nullptr, static_cast<unsigned long long *>(scratch), f.nct);
+}
+
+void launch_fused_probe_select(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
+                               const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
+                               uint32_t nprobe, void *scratch, uint32_t *fb, int32_t *idx, hipStream_t s) {
+    if (!nq)
+        return;
+    const FusedGeometry f(qhl, chl, nq, nl);
+    probe_merge_kernel<<<(nq + kMergeWaves - 1) / kMergeWaves, 64 * kMergeWaves, 0, s>>>(
+        static_cast<const unsigned long long *>(scratch), nq, f.nct, nprobe, idx, fb, fb + 1);
+    // fallback: those rows again as a distance matrix (the candidates are no longer needed, so
+    // it takes their memory), a grid of up to kFallbackRowTiles row tiles sweeping the *fb rows
+    const uint32_t fgroups = min(f.groups, (uint32_t)kFallbackRowTiles / 4);
+    float *dist = static_cast<float *>(scratch);
+    dist_gemm_f16x3_kernel<3><<<kNumXcd * f.ncx * 4 * fgroups, 256, 0, s>>>(
+        f.qh, f.qh + (size_t)nq * P, qscale, f.ch, f.ch + (size_t)nl * P, cscale, dist, nq, nl, P, qnorm, cnorm,
+        f.ncx, fgroups * 4 * kHT, fb + 1, fb, nullptr, 0);
+    uint32_t kp = 1;
+    while (kp < nprobe)
+        kp <<= 1;
+    select_rows_kernel<<<min(nq, (uint32_t)kFallbackSelectBlocks), kSelThreads, kp * sizeof(unsigned long long), s>>>(
+        dist, nl, nprobe, kp, fb + 1, fb, idx);
 }
 
 void launch_rotate_f16x3(const uint16_t *xhl, const float *xscale, const uint16_t *rthl,
@@ -1338,9 +1621,9 @@ void launch_rotate_f16x3(const uint16_t *xhl, const float *xscale, const uint16_
     const uint32_t ncx = (nct + kNumXcd - 1) / kNumXcd, groups = (nrt + 3) / 4;
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(xhl);
     const _Float16 *rh = reinterpret_cast<const _Float16 *>(rthl);
-    dist_gemm_f16x3_kernel<false><<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
+    dist_gemm_f16x3_kernel<0><<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
         xh, xh + (size_t)nq * dim, xscale, rh, rh + (size_t)P * dim, rtscale, out, nq, P, dim, nullptr,
-        nullptr, ncx);
+        nullptr, ncx, groups * 4 * kHT, nullptr, nullptr, nullptr, 0);
 }
 
 // ---- big-k select (nprobe > kSelectMaxProbe, up to 65,536): one 1024-thread block per

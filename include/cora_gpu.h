@@ -98,7 +98,13 @@ enum cora_search_flags {
      * to refinement as exact_ip. Runs the per-pair seed, far and recovery passes (no fused
      * vanguard pass, no matrix-core scans) with at most 4 same-cluster pairs per pass.
      * Without it the Bitwise estimator runs (Bq=8 popcount bound; two-stage exact_ip). */
-    CORA_FLAG_LUT4 = 1u << 12
+    CORA_FLAG_LUT4 = 1u << 12,
+    /* Coarse probe through the whole [nq][nlist] distance matrix and a select pass over it.
+     * Without it, for 8,192 <= nlist <= 65,536 and nprobe <= 64 (split-FP16 GEMM), the GEMM's
+     * epilogue keeps 8 candidate keys per query and 128-cluster tile and a merge selects from
+     * them, with the same result; the distance matrix is then not available to
+     * CORA_DBG_PROBE_DIST (its memory holds the candidates). */
+    CORA_FLAG_UNFUSED_PROBE = 1u << 13
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -269,12 +275,17 @@ enum cora_debug_array {
     CORA_DBG_THRESHOLDS = 11,     /* f32 [nq] thresholds the GPU filter read last (the
                                      snapshot in frozen mode, else the live array) */
     CORA_DBG_PROBE_DIST = 12,     /* f32 [nq][nlist] coarse-probe distance matrix
-                                     ||q'||^2 + ||c'||^2 - 2 <q',c'> */
+                                     ||q'||^2 + ||c'||^2 - 2 <q',c'> (searches that selected
+                                     from it: CORA_FLAG_UNFUSED_PROBE or outside the fused
+                                     select's range) */
     CORA_DBG_VANGUARD_LOWS = 13,  /* f32 [nq][vanguard depth][stride] lower bounds the
                                      matrix-core lows pass wrote (stride = the largest
                                      cluster rounded up to 256; entries past a cluster's
                                      size are undefined) */
-    CORA_DBG_LUT = 14             /* f16 [nq][P/4][16] LUT4 tables (CORA_FLAG_LUT4 searches) */
+    CORA_DBG_LUT = 14,            /* f16 [nq][P/4][16] LUT4 tables (CORA_FLAG_LUT4 searches) */
+    CORA_DBG_PROBE_FALLBACK = 15  /* u32 [1 + nq]: the number of queries whose fused probe
+                                     select fell back to their distance row, then those
+                                     queries (any order); count 0 for an unfused search */
 };
 int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t bytes);
 

@@ -284,13 +284,17 @@ def order_keys(d):
                                                    (16384, 0, 8192), (12000, 7, 5000), (40000, 50, 20000),
                                                    (65536, 0, 65536)])
 def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
-    """The probe select (8,192 < nlist <= 16,384: distances in registers; beyond: two
-    streaming passes; either way per-wave candidates below a bound from minima, ranked by
-    (distance, cluster id); heavy ties fall back to the radix select; nprobe > 4,096: radix
-    select of the k-th key, ordered compaction, stable radix sort in global scratch)
-    against an exact sort of the GPU's own distance matrix by (distance key, cluster id).
-    distinct > 0 repeats that many centroids over the whole list, so every distance is
-    tied nlist / distinct times."""
+    """The probe select over the materialised distance matrix (8,192 < nlist <= 16,384:
+    distances in registers; beyond: two streaming passes; either way per-wave candidates
+    below a bound from minima, ranked by (distance, cluster id); heavy ties fall back to the
+    radix select; nprobe > 4,096: radix select of the k-th key, ordered compaction, stable
+    radix sort in global scratch) against an exact sort of the GPU's own distance matrix by
+    (distance key, cluster id); then, where the fused select applies (nprobe <= 64), the
+    default search, whose GEMM epilogue keeps 8 keys per 128-cluster tile and whose merge
+    selects from them, must give the same probe lists. distinct > 0 repeats that many
+    centroids over the whole list, so every distance is tied nlist / distinct times: the
+    fused select cannot settle such queries from its candidates and sends them to its
+    fallback (the query's distance row computed again, the generic select)."""
     rng = np.random.default_rng(nlist + distinct)
     dim, nq = 64, 40
     n = 2 * nlist
@@ -306,14 +310,66 @@ def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
                  assign, R, metric=0)
     case = Case(path, q)
     say(f"[gpu] select on GPU distances, nlist={nlist} distinct={distinct} nprobe={nprobe}")
-    eng, _, _ = run_frozen(case, nprobe, 10)
+    eng, _, _ = run_frozen(case, nprobe, 10, extra_flags=ca.FLAG_UNFUSED_PROBE)
     d = eng.debug_read(ca.DBG_PROBE_DIST, (nq, nlist), np.float32)
     pidx = eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32)
+    fb = eng.debug_read(ca.DBG_PROBE_FALLBACK, (nq + 1,), np.uint32)
+    eng.close()
+    assert fb[0] == 0
     keys = order_keys(d)
     ids = np.arange(nlist)
+    want = np.stack([np.lexsort((ids, keys[qi]))[:nprobe] for qi in range(nq)])
     for qi in range(nq):
-        want = np.lexsort((ids, keys[qi]))[:nprobe]
-        assert np.array_equal(pidx[qi], want), qi
+        assert np.array_equal(pidx[qi], want[qi]), qi
+    if nprobe > 64:
+        return
+    say(f"[gpu] fused select, nlist={nlist} distinct={distinct} nprobe={nprobe}")
+    eng, _, _ = run_frozen(case, nprobe, 10)
+    fused = eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32)
+    fb = eng.debug_read(ca.DBG_PROBE_FALLBACK, (nq + 1,), np.uint32)
+    with pytest.raises(ca.EngineError):
+        eng.debug_read(ca.DBG_PROBE_DIST, (nq, nlist), np.float32)
+    eng.close()
+    for qi in range(nq):
+        assert np.array_equal(fused[qi], want[qi]), qi
+    rows = fb[1:1 + fb[0]]
+    assert len(set(rows.tolist())) == len(rows) and np.all(rows < nq)
+    if 0 < distinct < 16:
+        # every 128-cluster tile holds 8 or more copies of the nearest centroid: more than the
+        # epilogue keeps
+        assert fb[0] > 0, "tied distances never reached the fallback"
+    elif not distinct:
+        assert fb[0] <= nq // 4, "the merge settled too few queries"
+
+
+def test_fused_probe_fallback_sweep(tmp_path):
+    """More fallback queries than the fallback GEMM's grid holds (1,024 rows per sweep): 10
+    centroids repeated over 10,000 clusters (each 128-cluster tile holds 12 or 13 copies of a
+    query's nearest, more than the 8 keys per tile the epilogue keeps, so no query is settled
+    by the merge), 2,500 queries, against the select over the materialised matrix."""
+    rng = np.random.default_rng(2500)
+    nlist, distinct, dim, nq, nprobe = 10000, 10, 64, 2500, 40
+    cent = rng.normal(0, 1, (distinct, dim)).astype(np.float32)[np.arange(nlist) % distinct]
+    n = 2 * nlist
+    assign = rng.integers(0, nlist, n).astype(np.uint32)
+    x = (cent[assign] + rng.normal(0, 0.1, (n, dim))).astype(np.float32)
+    q = (cent[rng.integers(0, nlist, nq)] + rng.normal(0, 0.1, (nq, dim))).astype(np.float32)
+    R = np.linalg.qr(rng.normal(size=(dim, dim)))[0].T.astype(np.float32)
+    path = tmp_path / "sweep.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32), (cent.astype(np.float64) @ R).astype(np.float32),
+                 assign, R, metric=0)
+    case = Case(path, q)
+    say(f"[gpu] fused select fallback sweep, nq={nq} nlist={nlist}")
+    eng, _, _ = run_frozen(case, nprobe, 10, extra_flags=ca.FLAG_UNFUSED_PROBE)
+    want = eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32)
+    eng.close()
+    eng, _, _ = run_frozen(case, nprobe, 10)
+    got = eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32)
+    fb = eng.debug_read(ca.DBG_PROBE_FALLBACK, (nq + 1,), np.uint32)
+    eng.close()
+    assert fb[0] > 1024, int(fb[0])
+    assert np.array_equal(np.sort(fb[1:1 + fb[0]]), np.unique(fb[1:1 + fb[0]]))
+    assert np.array_equal(got, want)
 
 
 def test_end_to_end_nprobe_8192(tmp_path):
