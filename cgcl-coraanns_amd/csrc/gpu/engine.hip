@@ -839,9 +839,10 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
                        a->topk <= kVanguardMaxTopk;
     // its lower bounds first on the matrix cores, cluster-major, into the per-pair lows
     // array [nq][depth][van_stride] of the workspace
-    // (by default only when the sign codes and factors exceed the last-level cache: a
-    // cache-resident index is re-read cheaply by each query's own pass)
-    const bool lows_by_size = (uint64_t)E->N * (E->P / 8 + 12) > kLowsMinIndexBytes;
+    // (by default only for wide codes whose sign codes and factors exceed the last-level
+    // cache: a cache-resident index, or 28 bytes a vector at P = 128, is read cheaply enough
+    // by each query's own pass)
+    const bool lows_by_size = (uint64_t)E->N * (E->P / 8 + 12) > kLowsMinIndexBytes && E->P >= kLowsMinDim;
     const bool van_lows = fused && depth > 0 && far_mfma_supported(E->W) && E->d_van_lows &&
                           !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA) &&
                           (lows_by_size || (a->flags & CORA_FLAG_VANGUARD_MFMA));

@@ -25,9 +25,13 @@ constexpr int kSelectMaxProbe = 4096;       // top-nprobe select held in LDS
 constexpr uint32_t kNumXcd = 8;
 constexpr uint32_t kVanguardMaxPairs = 64;  // fused vanguard pass: vanguard depth limit
 constexpr uint32_t kVanguardMaxTopk = 128;  // fused vanguard pass: top-k limit
-// sign codes + factors beyond which the vanguard lows pass runs by default (MI355X's
-// 256 MB last-level cache)
+// the vanguard lows pass runs by default for sign codes + factors beyond MI355X's 256 MB
+// last-level cache and at least this padded dimension: a query's own pass reads P/8 + 12
+// bytes per vanguard vector against the lows pass's 4, a saving that pays for the extra
+// pass at P = 768 (config 4: 0.98M -> 1.43M QPS) but not at P = 128 (config 3, 280 MB:
+// 4.05M without it, 3.28M with it; config 5, 2.8 GB: 1.01M against 0.94M)
 constexpr uint64_t kLowsMinIndexBytes = 256ull << 20;
+constexpr uint32_t kLowsMinDim = 512;
 
 struct ClusterMeta {
     uint32_t start;      // first global (cluster-order) vector index

@@ -78,11 +78,12 @@ enum cora_search_flags {
     CORA_FLAG_FP32_GEMM = 1u << 8,
     /* Fused vanguard pass: where its lower bounds come from (same candidates either way).
      * By default, when the index's sign codes and factors exceed the last-level cache
-     * (256 MB), they are evaluated first on the matrix cores, cluster-major, in units of
-     * up to 16 same-cluster pairs (each cluster read once per unit), and the per-query pass
-     * streams them; a smaller index stays cache-resident, and each query evaluating its own
-     * clusters inside the per-query pass is faster. NO_VANGUARD_MFMA forces the latter,
-     * VANGUARD_MFMA the former. */
+     * (256 MB) and the padded dimension is at least 512, they are evaluated first on the
+     * matrix cores, cluster-major, in units of up to 16 same-cluster pairs (each cluster read
+     * once per unit), and the per-query pass streams them; for a cache-resident index, or
+     * narrow codes (P/8 + 12 bytes a vector against 4 bytes of bound), each query evaluating
+     * its own clusters inside the per-query pass is faster. NO_VANGUARD_MFMA forces the
+     * latter, VANGUARD_MFMA the former. */
     CORA_FLAG_NO_VANGUARD_MFMA = 1u << 9,
     CORA_FLAG_VANGUARD_MFMA = 1u << 10,
     /* GPU-final top-k: the candidates' refined distances, which the fused vanguard pass and
