@@ -204,13 +204,13 @@ __device__ __forceinline__ float excode_group_ip(const uint2 (&grp)[7], const fl
 // consumer's evaluation (1e-4 of the magnitude of the terms).
 __device__ __forceinline__ float refine_one(const ScanParams &p, uint32_t query, uint32_t probe,
                                             uint32_t gid, float ex, float &err) {
-    const size_t lc = (size_t)p.P * 7 / 8;
-    const uint8_t *code = p.ex_codes + (size_t)gid * lc;
+    const uint8_t *code = p.ex_rec + (size_t)gid * p.ex_stride;
     const float *qv = p.qrot + (size_t)query * p.P;
     float ip = 0.0f, l1 = 0.0f;
     for (uint32_t c = 0; c < p.P / 8; ++c)
         ip += excode_chunk_ip(code, qv, c, &l1);
-    const float fa = p.ex_factors[2 * (size_t)gid], fr = p.ex_factors[2 * (size_t)gid + 1];
+    const float2 f = *reinterpret_cast<const float2 *>(code + ex_record_factor_offset(p.P));
+    const float fa = f.x, fr = f.y;
     const float gadd = p.pgadd[(size_t)query * p.nprobe + probe], kbq = p.kb[query];
     err = 1e-4f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq)));
     return fa + gadd + fr * (128.0f * ex + ip + kbq);

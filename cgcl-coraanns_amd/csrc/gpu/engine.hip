@@ -57,8 +57,7 @@ struct cora_gpu_engine {
     float *d_rtscale = nullptr;     // its row scales [P]
     uint8_t *d_tiles = nullptr;
     ClusterMeta *d_meta = nullptr;
-    uint8_t *d_excodes = nullptr;  // optional HBM copy of the 7-bit ex-codes
-    float *d_exfac = nullptr;
+    uint8_t *d_exrec = nullptr;  // optional refinement records [N][ex_record_bytes(P)]
     // queue configuration (hybrid.cuh:105-106)
     uint64_t qcap = 1ull << 26, spill_cap = 1ull << 24;
     // workspace
@@ -342,8 +341,7 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
     dfree(E->d_rot);
     dfree(E->d_tiles);
     dfree(E->d_meta);
-    dfree(E->d_excodes);
-    dfree(E->d_exfac);
+    dfree(E->d_exrec);
     for (hipEvent_t ev : {E->ev_prep, E->ev_probe, E->ev_f0, E->ev_f1, E->ev_s0, E->ev_s1, E->ev_p0,
                           E->ev_p1, E->ev_v0, E->ev_v1, E->ev_a0, E->ev_a1, E->ev_q0, E->ev_sched, E->ev_done})
         if (ev)
@@ -492,28 +490,50 @@ int cora_gpu_load_excodes(cora_gpu_engine *E, const uint8_t *h_long_codes,
         return CORA_ERR_INVALID_ARGUMENT;
     if (!E->loaded)
         return fail(E, CORA_ERR_LOGIC, "load the index before its ex-codes");
-    if (E->d_excodes)
+    if (E->d_exrec)
         return fail(E, CORA_ERR_LOGIC, "ex-codes already loaded");
     if (E->ws)
         return fail(E, CORA_ERR_LOGIC, "load ex-codes before prepare_workspace");
     if (!h_long_codes || !h_ex_factors || E->ex_bits != 7)
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "GPU ex-codes need 7 ex-bits and both arrays");
     HIPCHK(hipSetDevice(E->device));
+    // records built on the device: the ex-codes and factors uploaded in bounded chunks
+    // through a staging pair, then the sign codes copied from the tiles
     const uint64_t lc = E->P * 7 / 8;
-    int rc = dalloc(E, E->d_excodes, E->N * lc);
+    const uint64_t chunk = std::max<uint64_t>(1, std::min<uint64_t>(E->N, (256ull << 20) / (lc + 8)));
+    uint8_t *st_codes = nullptr;
+    float *st_fac = nullptr;
+    int rc = dalloc(E, E->d_exrec, E->N * ex_record_bytes((uint32_t)E->P));
     if (rc == CORA_OK)
-        rc = dalloc(E, E->d_exfac, E->N * 2);
+        rc = dalloc(E, st_codes, chunk * lc);
+    if (rc == CORA_OK)
+        rc = dalloc(E, st_fac, chunk * 2);
     hipError_t r = hipSuccess;
-    if (rc == CORA_OK)
-        r = hipMemcpy(E->d_excodes, h_long_codes, E->N * lc, hipMemcpyHostToDevice);
-    if (rc == CORA_OK && r == hipSuccess)
-        r = hipMemcpy(E->d_exfac, h_ex_factors, E->N * 2 * sizeof(float), hipMemcpyHostToDevice);
+    for (uint64_t g0 = 0; rc == CORA_OK && r == hipSuccess && g0 < E->N; g0 += chunk) {
+        const uint64_t n = std::min(chunk, E->N - g0);
+        r = hipMemcpy(st_codes, h_long_codes + g0 * lc, n * lc, hipMemcpyHostToDevice);
+        if (r == hipSuccess)
+            r = hipMemcpy(st_fac, h_ex_factors + 2 * g0, n * 2 * sizeof(float), hipMemcpyHostToDevice);
+        if (r == hipSuccess) {
+            launch_ex_record_fill(st_codes, st_fac, g0, (uint32_t)n, (uint32_t)E->P, E->d_exrec, E->stream);
+            r = hipGetLastError();
+        }
+        if (r == hipSuccess)
+            r = hipStreamSynchronize(E->stream);  // the staging pair is reused
+    }
+    if (rc == CORA_OK && r == hipSuccess) {
+        launch_ex_record_sign(E->d_meta, (uint32_t)E->nl, E->d_tiles, (uint32_t)E->tile_bytes, (uint32_t)E->W,
+                              E->d_exrec, E->stream);
+        r = hipGetLastError();
+        if (r == hipSuccess)
+            r = hipStreamSynchronize(E->stream);
+    }
     if (rc == CORA_OK && r != hipSuccess)
         rc = fail(E, CORA_ERR_RUNTIME, std::string("ex-code upload: ") + hipGetErrorString(r));
-    if (rc != CORA_OK) {
-        dfree(E->d_excodes);
-        dfree(E->d_exfac);
-    }
+    dfree(st_codes);
+    dfree(st_fac);
+    if (rc != CORA_OK)
+        dfree(E->d_exrec);
     return rc;
 }
 
@@ -583,7 +603,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
             E->van_stride = (E->max_cluster + 255) / 256 * 256;
             TRY(dalloc(E, E->d_van_lows, max_q * depth * std::max<uint64_t>(E->van_stride, 1)));
         }
-        if (E->d_excodes) {
+        if (E->d_exrec) {
             TRY(dalloc(E, E->d_fcount, max_q));
             TRY(dalloc(E, E->d_foff, max_q + 1));
             TRY(dalloc(E, E->d_fcur, max_q));
@@ -735,7 +755,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool want_final = (a->flags & CORA_FLAG_GPU_FINAL) != 0;
     const bool lut = (a->flags & CORA_FLAG_LUT4) != 0;
     if (want_final &&
-        (!E->d_excodes || !E->d_fkeys ||
+        (!E->d_exrec || !E->d_fkeys ||
          (a->flags & (CORA_FLAG_NO_GPU_SEED | CORA_FLAG_NO_GPU_PREFILTER | CORA_FLAG_PAIR_SEEDS | CORA_FLAG_LUT4)) ||
          ((a->flags & CORA_FLAG_FROZEN_THRESHOLDS) && !(a->flags & CORA_FLAG_GPU_SEED_FROZEN)) ||
          std::min<uint64_t>(a->vanguard, a->nprobe) > kVanguardMaxPairs || a->topk > kVanguardMaxTopk))
@@ -830,9 +850,9 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // GPU ex-code stages (seed thresholds, refined pre-filter): live thresholds only, or
     // the frozen snapshot in the GPU_SEED_FROZEN test mode
     const bool ex_stage_mode = !frozen || (a->flags & CORA_FLAG_GPU_SEED_FROZEN);
-    const bool gpu_seed = depth > 0 && E->d_excodes && E->d_seed_dist && ex_stage_mode &&
+    const bool gpu_seed = depth > 0 && E->d_exrec && E->d_seed_dist && ex_stage_mode &&
                           !(a->flags & CORA_FLAG_NO_GPU_SEED);
-    const bool prefilter = E->d_excodes && ex_stage_mode && !(a->flags & CORA_FLAG_NO_GPU_PREFILTER);
+    const bool prefilter = E->d_exrec && ex_stage_mode && !(a->flags & CORA_FLAG_NO_GPU_PREFILTER);
     // fused per-query vanguard pass (vanguard.hip) unless the reference's per-pair passes
     // are asked for or the shape exceeds its limits
     const bool fused = gpu_seed && !lut && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
@@ -860,8 +880,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     }
     ScanParams p = scan_params(E, depth, keep, frozen);
     if (gpu_seed || prefilter) {
-        p.ex_codes = E->d_excodes;
-        p.ex_factors = E->d_exfac;
+        p.ex_rec = E->d_exrec;
+        p.ex_stride = ex_record_bytes((uint32_t)E->P);
         p.qrot = E->d_qrot;
         p.kb = E->d_kb;
     }

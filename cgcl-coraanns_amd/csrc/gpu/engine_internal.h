@@ -33,6 +33,15 @@ constexpr uint32_t kVanguardMaxTopk = 128;  // fused vanguard pass: top-k limit
 constexpr uint64_t kLowsMinIndexBytes = 256ull << 20;
 constexpr uint32_t kLowsMinDim = 512;
 
+// Refinement record of one vector (cluster order), ex_record_bytes(P) = P + 16 bytes, so a
+// refined vector is one contiguous read: the packed 7-bit ex-code (P*7/8 bytes, the
+// reference's packing, pack_excode.hpp:216-265), its sign code (P/8 bytes, the tiles' words:
+// dimension 32w+l at bit l of word w), f_add_ex and f_rescale_ex, and 8 bytes of padding
+// (16-byte aligned records).
+__host__ __device__ constexpr uint32_t ex_record_bytes(uint32_t P) { return P + 16; }
+__host__ __device__ constexpr uint32_t ex_record_sign_offset(uint32_t P) { return P * 7 / 8; }
+__host__ __device__ constexpr uint32_t ex_record_factor_offset(uint32_t P) { return P; }
+
 struct ClusterMeta {
     uint32_t start;      // first global (cluster-order) vector index
     uint32_t n;          // vectors in the cluster
@@ -130,13 +139,13 @@ struct ScanParams {
     uint32_t seed_words;         // u32 words of seed bitmask per vanguard pair
     uint32_t *seed_bits;         // [nq * vanguard][seed_words]
     QueueDev queue;
-    // GPU seed refinement (optional: ex_codes == nullptr disables it). The seed pass
+    // GPU seed refinement (optional: ex_rec == nullptr disables it). The seed pass
     // refines each seed with the HBM copy of the ex-codes exactly as the CPU consumer
     // will (cpu_refinement.cpp:183-192) and records, per seed slot
     // [nq][vanguard][keep], its refined distance, its lower bound and a bound on the
     // rounding difference between this and the CPU's evaluation.
-    const uint8_t *ex_codes;     // [N][P*7/8] packed 7-bit ex-codes (pack_excode.hpp:216-265)
-    const float *ex_factors;     // [N][2] f_add_ex, f_rescale_ex
+    const uint8_t *ex_rec;       // [N][ex_stride] refinement records (ex_record_bytes)
+    uint32_t ex_stride;
     const float *qrot;           // [nq][P] rotated queries
     const float *kb;             // [nq] kbxSumq
     float *seed_dist;            // [nq][vanguard][keep], +inf when unused
@@ -148,7 +157,7 @@ struct ScanParams {
     float *van_lows;
     uint32_t van_stride;
     uint32_t seed_buf;           // seed pass LDS buffer entries (power of two >= keep + 64)
-    // refined pre-filter of the far and recovery passes (needs ex_codes)
+    // refined pre-filter of the far and recovery passes (needs ex_rec)
     int prefilter;
     unsigned long long *dropped;  // records the pre-filter dropped
     // dense debug output
@@ -179,6 +188,12 @@ struct VanguardArgs {
 void launch_repack(const uint32_t *ref_words, const float *ref_factors, const ClusterMeta *meta,
                    uint32_t nlist, uint32_t W, uint8_t *tiles, uint32_t tile_bytes,
                    hipStream_t s);
+// Refinement records from the host's packed ex-codes and ex-factors (rows [g0, g0 + n)),
+// then the sign codes of every vector from the tiles.
+void launch_ex_record_fill(const uint8_t *codes, const float *factors, uint64_t g0, uint32_t n, uint32_t P,
+                           uint8_t *rec, hipStream_t s);
+void launch_ex_record_sign(const ClusterMeta *meta, uint32_t nlist, const uint8_t *tiles, uint32_t tile_bytes,
+                           uint32_t W, uint8_t *rec, hipStream_t s);
 // message returned by cora_tool_last_error() (tools.hip; thread-local)
 void set_tool_error(const char *msg);
 void launch_rotate(const float *q, const float *R, float *out, uint32_t nq, uint32_t dim,

@@ -574,14 +574,13 @@ __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
             // with a bound on its rounding difference from the CPU's evaluation.
             __syncthreads();
             const uint32_t sub = lane & 15, chunks = p.P / 8;
-            const size_t lc = (size_t)p.P * 7 / 8;
             const float *qv = p.qrot + (size_t)query * p.P;
             const float kbq = uniformf(p.kb[query]);
             for (uint32_t sidx = lane >> 4; sidx < take; sidx += 4) {
                 const unsigned long long key = s_buf[sidx];
                 const uint32_t local = (uint32_t)key;
                 const size_t gid = (size_t)start + local;
-                const uint8_t *code = p.ex_codes + gid * lc;
+                const uint8_t *code = p.ex_rec + gid * p.ex_stride;
                 float ip = 0.0f, l1 = 0.0f;
                 for (uint32_t c = sub; c < chunks; c += 16)
                     ip += excode_chunk_ip(code, qv, c, &l1);
@@ -591,7 +590,8 @@ __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
                     l1 += __shfl_xor(l1, o, 16);
                 }
                 if (sub == 0) {
-                    const float fa = p.ex_factors[2 * gid], fr = p.ex_factors[2 * gid + 1];
+                    const float2 f = *reinterpret_cast<const float2 *>(code + ex_record_factor_offset(p.P));
+                    const float fa = f.x, fr = f.y;
                     const float ex = s_exk[sidx];
                     const float dist = fa + gadd + fr * (128.0f * ex + ip + kbq);
                     const float mag = fabsf(fa) + fabsf(gadd) +

@@ -422,9 +422,10 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                 };
                 if constexpr (W >= 16) {
                     // P >= 512: four lanes per vector, the chunk in two halves of 64 vectors;
-                    // each lane issues all of its loads (W/4 code words, W/8 ex-code groups of
-                    // 56 bytes, the ex-factors) before any arithmetic, so a half costs one
-                    // memory round trip instead of one per loop iteration
+                    // each lane issues all of its loads from the vector's refinement record
+                    // (W/4 sign-code words, W/8 ex-code groups of 56 bytes, the ex-factors)
+                    // before any arithmetic, so a half costs one memory round trip instead of
+                    // one per loop iteration
                     constexpr int kWq = W / 4, kG = W / 8;
 #pragma unroll 1
                     for (uint32_t half = 0; half < 2; ++half) {
@@ -436,11 +437,8 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                         uint32_t j = 0;
                         while (have && pos >= S.off[j + 1])
                             ++j;
-                        const uint32_t local = pos - S.off[j];
-                        const uint8_t *tile =
-                            p.tiles + (size_t)(S.tbase[j] + local / kTileVectors) * p.tile_bytes;
-                        const uint32_t vl = local % kTileVectors;
-                        const size_t gid = (size_t)S.start[j] + local;
+                        const size_t gid = (size_t)S.start[j] + (pos - S.off[j]);
+                        const uint8_t *rec = p.ex_rec + gid * p.ex_stride;
                         uint32_t pz = 0;  // opaque zero, as below
                         asm volatile("" : "+s"(pz));
                         const uint32_t *planes = S.planes + pz;
@@ -449,21 +447,25 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                         uint2 grp[kG][7];
                         float fa = 0.0f, fr = 0.0f;
                         if (have) {
+                            // sign-code words sub kWq .. sub kWq + kWq - 1, in 8-byte pairs
+                            const uint2 *wp = reinterpret_cast<const uint2 *>(rec + lc) + sub * (kWq / 2);
 #pragma unroll
-                            for (int i = 0; i < kWq; ++i)  // word sub + 4 i: group i, component sub
-                                xw[i] = *reinterpret_cast<const uint32_t *>(tile + (size_t)i * 1024 + vl * 16 +
-                                                                            sub * 4);
+                            for (int i = 0; i < kWq / 2; ++i) {
+                                const uint2 v = wp[i];
+                                xw[2 * i] = v.x;
+                                xw[2 * i + 1] = v.y;
+                            }
 #pragma unroll
                             for (int gi = 0; gi < kG; ++gi) {
-                                const uint2 *gp = reinterpret_cast<const uint2 *>(
-                                    p.ex_codes + gid * lc + (size_t)(sub + 4 * gi) * 56);
+                                const uint2 *gp = reinterpret_cast<const uint2 *>(rec + (size_t)(sub + 4 * gi) * 56);
 #pragma unroll
                                 for (int k = 0; k < 7; ++k)
                                     grp[gi][k] = gp[k];
                             }
                             if (sub == 0) {
-                                fa = p.ex_factors[2 * gid];
-                                fr = p.ex_factors[2 * gid + 1];
+                                const float2 f = *reinterpret_cast<const float2 *>(rec + P);
+                                fa = f.x;
+                                fr = f.y;
                             }
                         }
                         int ipa = 0, ipb = 0;
@@ -471,7 +473,7 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                         if (have) {
 #pragma unroll
                             for (int i = 0; i < kWq; ++i) {
-                                const uint32_t w = sub + 4 * i;
+                                const uint32_t w = sub * kWq + i;
 #pragma unroll
                                 for (int b = 0; b < kBq - 1; ++b) {
                                     ipa += __popc(xw[i] & planes[b * W + w]) << b;
@@ -506,12 +508,9 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                     uint32_t j = 0;
                     while (have && pos >= S.off[j + 1])
                         ++j;
-                    const uint32_t local = pos - S.off[j];
-                    const uint8_t *tile =
-                        p.tiles + (size_t)(S.tbase[j] + local / kTileVectors) * p.tile_bytes;
-                    const uint32_t vl = local % kTileVectors;
-                    const size_t gid = (size_t)S.start[j] + local;
-                    const uint8_t *code = p.ex_codes + gid * lc;
+                    const size_t gid = (size_t)S.start[j] + (pos - S.off[j]);
+                    const uint8_t *code = p.ex_rec + gid * p.ex_stride;  // the ex-code leads the record
+                    const uint32_t *sw = reinterpret_cast<const uint32_t *>(code + lc);
                     int ipa = 0, ipb = 0;
                     float ipx = 0.0f, fa = 0.0f, fr = 0.0f;
                     // an opaque zero: plane and q' reads indexed with it stay in the chunk
@@ -523,23 +522,21 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                     const float *qv = s_q + pz;
                     if (have) {
                         if (sub == 0) {
-                            fa = p.ex_factors[2 * gid];
-                            fr = p.ex_factors[2 * gid + 1];
+                            const float2 f = *reinterpret_cast<const float2 *>(code + P);
+                            fa = f.x;
+                            fr = f.y;
                         }
                         constexpr int kWl = W > 0 ? (W + 1) / 2 : kVqMaxW / 2;
-                        // two words per iteration: unrolled fully, the 16 plane reads per
-                        // word would all be scheduled ahead (192 registers at P = 768)
+                        // lane sub takes the sign-code words sub nw/2 .. (sub + 1) nw/2 - 1 (nw is
+                        // even: P % 64 == 0); two words per iteration: unrolled fully, the 16
+                        // plane reads per word would all be scheduled ahead (192 registers at
+                        // P = 768)
+                        const uint32_t half_w = nw / 2;
 #pragma unroll 2
                         for (int i = 0; i < kWl; ++i) {
-                            const uint32_t w = sub + 2 * i;
-                            if (w < nw) {
-                                const uint32_t *wp =
-                                    (nw & 3u) == 2u && w >= nw - 2
-                                        ? reinterpret_cast<const uint32_t *>(tile + (size_t)(nw / 4) * 1024 +
-                                                                             vl * 8 + (w & 1u) * 4)
-                                        : reinterpret_cast<const uint32_t *>(tile + (size_t)(w / 4) * 1024 +
-                                                                             vl * 16 + (w & 3u) * 4);
-                                const uint32_t xw = *wp;
+                            if ((uint32_t)i < half_w) {
+                                const uint32_t w = sub * half_w + i;
+                                const uint32_t xw = sw[w];
 #pragma unroll
                                 for (int b = 0; b < kBq - 1; ++b) {
                                     ipa += __popc(xw & planes[b * nw + w]) << b;

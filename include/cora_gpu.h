@@ -197,12 +197,12 @@ int cora_gpu_load_index(cora_gpu_engine *engine, uint64_t num_vecs, uint64_t dim
 
 /* Optional HBM copy of the 7-bit ex-codes [num_vecs][padded_dim*7/8] (reference packed
  * layout, pack_excode.hpp:216-265) and ex-factors [num_vecs][2] (no counterpart in the
- * reference, whose ex-codes live on the host only). With them the vanguard seed pass
- * refines its seeds on the GPU with the CPU consumer's formula (cpu_refinement.cpp:
- * 183-192) and, before the far and recovery passes, lowers each query's live threshold
- * to a value the CPU would publish after refining those seeds (see scan.hip). The CPU
- * still refines every published candidate. Requires ex_bits == 7; call after
- * cora_gpu_load_index. */
+ * reference, whose ex-codes live on the host only), kept as one refinement record per
+ * vector (ex-code, sign code, ex-factors: padded_dim + 16 bytes). With them the GPU
+ * refines vanguard vectors with the CPU consumer's formula (cpu_refinement.cpp:183-192),
+ * lowers each query's live threshold to a value the CPU would publish after refining
+ * them, and drops far candidates the CPU would reject. The CPU still refines every
+ * published candidate. Requires ex_bits == 7; call after cora_gpu_load_index. */
 int cora_gpu_load_excodes(cora_gpu_engine *engine, const uint8_t *h_long_codes,
                           const float *h_ex_factors);
 
