@@ -87,8 +87,9 @@ def oracle_topk(lz, g, nprobe, topk, thresholds=None, queries=None):
             ipi = orc.ip_int_direct(bits, qint[q])
             low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p],
                                orc.exact_ip_bitwise(ipi, g["width"][q]), g["k1"][q])
-            lo += int((low < thr - band).sum())
-            hi += int((low < thr + band).sum())
+            low64 = low.astype(np.float64)  # the band around FLT_MAX does not fit FP32
+            lo += int((low64 < thr - band).sum())
+            hi += int((low64 < thr + band).sum())
             keep = np.nonzero(low < thr)[0]
             ex2 = orc.exact_ip_two_stage(ipi[keep], orc.ip_int_direct(bits[keep], qres[q]), g["width"][q],
                                          g["width2"][q])
