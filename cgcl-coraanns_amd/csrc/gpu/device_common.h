@@ -27,6 +27,35 @@ __device__ __forceinline__ uint32_t lane_rank(unsigned long long mask) {
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// A load through a global-memory (address space 1) pointer: a global_load, counted by
+// vmcnt only. A pointer read from a kernel's parameter struct after the struct has escaped
+// to an out-of-line call is generic, and its loads become flat loads, which count against
+// lgkmcnt too: every wait for an LDS read then also waits for the memory loads in flight.
+// HIP's vector classes are copied through a generic reference, which would turn the load
+// flat again, so they are loaded as clang vectors and rebuilt.
+template <class T>
+__device__ __forceinline__ T gload(const void *p) {
+    return *(const __attribute__((address_space(1))) T *)p;
+}
+template <>
+__device__ __forceinline__ float4 gload<float4>(const void *p) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    const v4f v = *(const __attribute__((address_space(1))) v4f *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <>
+__device__ __forceinline__ uint2 gload<uint2>(const void *p) {
+    typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+    const v2u v = *(const __attribute__((address_space(1))) v2u *)p;
+    return make_uint2(v.x, v.y);
+}
+template <>
+__device__ __forceinline__ uint4 gload<uint4>(const void *p) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const v4u v = *(const __attribute__((address_space(1))) v4u *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // W > 0: compile-time word count; W == 0: runtime word count (any P % 64 == 0, P <= 1024).
 template <int W>
 struct Words {

@@ -373,29 +373,32 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
         const uint32_t u = next_far_unit(p.unit_cursor, U, range, tries, lane);
         if (u >= U)
             break;
-        const Unit un = p.units[ubase + u];
-        const uint32_t cluster = uniform(un.cluster), count = uniform(un.count);
-        const ClusterMeta cm = p.meta[cluster];
-        const uint32_t n = uniform(cm.n), start = uniform(cm.start), tbase = uniform(cm.tile_base);
-        const uint32_t t_begin = uniform(un.tiles) >> 8, t_end = t_begin + (uniform(un.tiles) & 255u);
+        // every load of the kernel body through global pointers: p escapes to flush_wide, so
+        // pointers read from it are generic, and flat loads would make each LDS wait of the
+        // widening also wait for the tile loads in flight
+        const uint4 un = gload<uint4>(p.units + ubase + u);  // Unit: cluster, pair_begin, count, tiles
+        const uint32_t cluster = uniform(un.x), count = uniform(un.z);
+        const uint4 cm = gload<uint4>(p.meta + cluster);  // ClusterMeta: start, n, tile_base
+        const uint32_t n = uniform(cm.y), start = uniform(cm.x), tbase = uniform(cm.z);
+        const uint32_t t_begin = uniform(un.w) >> 8, t_end = t_begin + (uniform(un.w) & 255u);
         if (n == 0 || t_begin >= t_end)
             continue;
         const bool slot = col < count;
-        const uint32_t w0 = slot ? p.pairs[uniform(un.pair_begin) + col].word0 : 0u;
+        const uint32_t w0 = slot ? gload<uint32_t>(&p.pairs[uniform(un.y) + col].word0) : 0u;
         const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
         float width = 0.0f, k1 = 0.0f, gadd = 0.0f, gerr = 0.0f, cutoff = -FLT_MAX;
         v4i32 bq[S];
         if (slot) {
-            width = p.qwidth[query];
-            k1 = p.k1[query];
+            width = gload<float>(p.qwidth + query);
+            k1 = gload<float>(p.k1 + query);
             const size_t pi = (size_t)query * p.nprobe + probe;
-            gadd = p.pgadd[pi];
-            gerr = p.pgerr[pi];
-            cutoff = kDense ? FLT_MAX : p.thresholds[query];
+            gadd = gload<float>(p.pgadd + pi);
+            gerr = gload<float>(p.pgerr + pi);
+            cutoff = kDense ? FLT_MAX : gload<float>(p.thresholds + query);
             const v4i32 *qb = reinterpret_cast<const v4i32 *>(p.qbytes + (size_t)query * 2 * P + 8 * W * quad);
 #pragma unroll
             for (int s = 0; s < S; ++s)
-                bq[s] = qb[s];
+                bq[s] = gload<v4i32>(qb + s);
         } else {
 #pragma unroll
             for (int s = 0; s < S; ++s)
@@ -413,14 +416,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 const uint32_t v = 16 * m + col;
-                fat[m] = *reinterpret_cast<const float4 *>(fac + 16 * m + 4 * quad);
-                frt[m] = *reinterpret_cast<const float4 *>(fac + 64 + 16 * m + 4 * quad);
-                fet[m] = *reinterpret_cast<const float4 *>(fac + 128 + 16 * m + 4 * quad);
+                fat[m] = gload<float4>(fac + 16 * m + 4 * quad);
+                frt[m] = gload<float4>(fac + 64 + 16 * m + 4 * quad);
+                fet[m] = gload<float4>(fac + 128 + 16 * m + 4 * quad);
 #pragma unroll
                 for (int j = 0; j < WQ; j += 2) {
                     const uint32_t w = WQ * quad + j;  // even: the pair lies in one 4-word group
-                    const uint2 c = *reinterpret_cast<const uint2 *>(tile + (size_t)(w >> 2) * 1024 + v * 16 +
-                                                                     (w & 3u) * 4);
+                    const uint2 c = gload<uint2>(tile + (size_t)(w >> 2) * 1024 + v * 16 + (w & 3u) * 4);
                     xt[m][j] = c.x;
                     xt[m][j + 1] = c.y;
                 }
