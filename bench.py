@@ -186,7 +186,10 @@ def main():
     else:
         base, queries = wl.generate(c, n=args.n or None, nq=args.nq or None)
         log(f"[data] {c.describe()}: generated {base.shape} + {queries.shape} in {time.time() - t0:.1f}s")
-        wl.build_index(c, base, index_path, log=log)
+        if args.workdir and index_path.exists():
+            log(f"[data] index reused from {workdir}; ground truth for top-{c.topk} computed")
+        else:
+            wl.build_index(c, base, index_path, log=log)
         t = time.time()
         gt = wl.ground_truth(base, queries, c.topk, c.metric)
         log(f"[gt] exact top-{c.topk} (GPU FP32 + FP64 re-rank): {time.time() - t:.1f}s")

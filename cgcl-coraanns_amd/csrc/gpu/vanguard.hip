@@ -84,22 +84,6 @@ __device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t *s_red)
     return v + add;
 }
 
-__device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t *s_red) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-        v = max(v, (uint32_t)__shfl_xor(v, o));
-    if (lane == 0)
-        s_red[wave] = v;
-    __syncthreads();
-    uint32_t s = 0;
-#pragma unroll
-    for (int w = 0; w < kVqWaves; ++w)
-        s = max(s, s_red[w]);
-    __syncthreads();
-    return s;
-}
-
 // The k-th smallest (k >= 1) order key among lows(i) < thr, i < n (4 radix passes of 8
 // bits; the caller guarantees at least k such entries).
 template <class L>
@@ -628,16 +612,20 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                     }
                     __syncthreads();
                     const uint32_t kn = min(topk, kc + enter);
-                    if (kn == topk) {
-                        // threshold backed by the k best: max(d_k + e, l) + 1 ulp
+                    if (kn == topk && wave == 0) {
+                        // threshold backed by the k best: max(d_k + e, l) + 1 ulp (one wave: topk
+                        // <= 128, two entries a lane)
                         uint32_t ekey = 0, lkey = 0;
-                        if (tid < topk) {
-                            ekey = __float_as_uint(S.t_err[tb ^ 1][tid]);  // >= 0: bits order like values
-                            lkey = order_key(S.t_low[tb ^ 1][tid]);
+                        for (uint32_t i = lane; i < topk; i += 64) {
+                            ekey = max(ekey, __float_as_uint(S.t_err[tb ^ 1][i]));  // >= 0: bits order like values
+                            lkey = max(lkey, order_key(S.t_low[tb ^ 1][i]));
                         }
-                        ekey = block_max(ekey, S.red);
-                        lkey = block_max(lkey, S.red);
-                        if (tid == 0) {
+#pragma unroll
+                        for (int o = 32; o > 0; o >>= 1) {
+                            ekey = max(ekey, (uint32_t)__shfl_xor(ekey, o));
+                            lkey = max(lkey, (uint32_t)__shfl_xor(lkey, o));
+                        }
+                        if (lane == 0) {
                             const float dk = key_to_float((uint32_t)(S.t_key[tb ^ 1][topk - 1] >> 32));
                             const float t =
                                 nextafterf(fmaxf(dk + __uint_as_float(ekey), key_to_float(lkey)), FLT_MAX);
