@@ -34,6 +34,11 @@ void hfree(T *&p) {
     p = nullptr;
 }
 
+// Query upload slices: at most kUploadSlices of at least kUploadMinRows rows (a multiple of
+// the GEMMs' 128-row tiles).
+constexpr uint32_t kUploadSlices = 4;
+constexpr uint32_t kUploadMinRows = 1024;
+
 }  // namespace
 
 struct cora_gpu_engine {
@@ -41,6 +46,15 @@ struct cora_gpu_engine {
     std::string err;
     unsigned long long wall_clock_khz = 0;  // device wall_clock64() rate
     hipStream_t stream = nullptr, stream_d2h = nullptr;
+    // query upload from the pinned staging buffer in slices (cora_gpu_reset): each slice's
+    // DMA on stream_h2d signals ev_up[i]; the search prepares and probes a slice's queries as
+    // soon as it has landed, while the later slices are still in flight
+    hipStream_t stream_h2d = nullptr;
+    hipEvent_t ev_up[kUploadSlices] = {};
+    hipEvent_t ev_pg[kUploadSlices][2] = {};  // the probe GEMM of each slice (timing)
+    uint32_t up_slices = 0, up_row[kUploadSlices + 1] = {};
+    uint64_t up_nq = 0;
+    uint32_t last_slices = 0;  // slices of the last launched search (0: one pass)
     hipEvent_t ev_prep = nullptr, ev_probe = nullptr, ev_f0 = nullptr, ev_f1 = nullptr,
                ev_s0 = nullptr, ev_s1 = nullptr, ev_p0 = nullptr, ev_p1 = nullptr, ev_v0 = nullptr,
                ev_v1 = nullptr, ev_a0 = nullptr, ev_a1 = nullptr, ev_q0 = nullptr, ev_sched = nullptr,
@@ -201,6 +215,9 @@ void release_workspace(cora_gpu_engine *E) {
         (void)hipStreamSynchronize(E->stream);
     if (E->stream_d2h)
         (void)hipStreamSynchronize(E->stream_d2h);
+    if (E->stream_h2d)
+        (void)hipStreamSynchronize(E->stream_h2d);
+    E->up_slices = 0;
     E->ws = false;
     E->launched = false;
     E->ws_q = E->ws_k = E->ws_np = E->ws_van = E->seed_words = 0;
@@ -310,6 +327,12 @@ int cora_gpu_create(cora_gpu_engine **out, int device) {
         E->wall_clock_khz = (unsigned long long)khz;
         HIPCHK(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
         HIPCHK(hipStreamCreateWithFlags(&E->stream_d2h, hipStreamNonBlocking));
+        HIPCHK(hipStreamCreateWithFlags(&E->stream_h2d, hipStreamNonBlocking));
+        for (uint32_t i = 0; i < kUploadSlices; ++i) {
+            HIPCHK(hipEventCreateWithFlags(&E->ev_up[i], hipEventDisableTiming));
+            HIPCHK(hipEventCreate(&E->ev_pg[i][0]));
+            HIPCHK(hipEventCreate(&E->ev_pg[i][1]));
+        }
         for (hipEvent_t *ev : {&E->ev_prep, &E->ev_probe, &E->ev_f0, &E->ev_f1, &E->ev_s0, &E->ev_s1,
                                &E->ev_p0, &E->ev_p1, &E->ev_v0, &E->ev_v1, &E->ev_a0, &E->ev_a1, &E->ev_q0,
                                &E->ev_sched, &E->ev_done})
@@ -348,8 +371,14 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
             (void)hipEventDestroy(ev);
     if (E->stream)
         (void)hipStreamDestroy(E->stream);
+    for (uint32_t i = 0; i < kUploadSlices; ++i)
+        for (hipEvent_t ev : {E->ev_up[i], E->ev_pg[i][0], E->ev_pg[i][1]})
+            if (ev)
+                (void)hipEventDestroy(ev);
     if (E->stream_d2h)
         (void)hipStreamDestroy(E->stream_d2h);
+    if (E->stream_h2d)
+        (void)hipStreamDestroy(E->stream_h2d);
     delete E;
     return CORA_OK;
 }
@@ -701,6 +730,9 @@ int cora_gpu_query_staging(cora_gpu_engine *E, float **out) {
         return CORA_ERR_INVALID_ARGUMENT;
     if (!E->ws)
         return fail(E, CORA_ERR_LOGIC, "prepare workspace before searching");
+    // the caller is about to rewrite the buffer: the last reset's upload must be complete
+    HIPCHK(hipSetDevice(E->device));
+    HIPCHK(hipStreamSynchronize(E->stream_h2d));
     *out = E->h_qstage;
     return CORA_OK;
 }
@@ -716,11 +748,31 @@ int cora_gpu_reset(cora_gpu_engine *E, const float *h_queries, uint64_t nq) {
         return fail(E, CORA_ERR_INVALID_ARGUMENT, "missing queries");
     HIPCHK(hipSetDevice(E->device));
     HIPCHK(hipStreamSynchronize(E->stream));
+    HIPCHK(hipStreamSynchronize(E->stream_h2d));
     if (E->ring_dirty) {
         memset(E->h_items, 0xFF, E->qcap * sizeof(uint4));
         E->ring_dirty = false;
     }
-    HIPCHK(hipMemcpyAsync(E->d_raw, h_queries, nq * E->dim * 4, hipMemcpyHostToDevice, E->stream));
+    E->up_slices = 0;
+    E->up_nq = nq;
+    if (h_queries == E->h_qstage && nq >= 2 * kUploadMinRows) {
+        // from the pinned staging buffer: slices of whole 128-row tiles on the H2D stream; the
+        // search waits for each before the kernels that read it (cora_gpu_launch_search)
+        const uint32_t ns = std::min<uint32_t>(kUploadSlices, (uint32_t)(nq / kUploadMinRows));
+        const uint32_t per = (uint32_t)((nq + ns - 1) / ns + 127) / 128 * 128;
+        for (uint32_t i = 0; i < ns; ++i) {
+            const uint64_t r0 = std::min<uint64_t>(nq, (uint64_t)i * per);
+            const uint64_t r1 = i + 1 == ns ? nq : std::min<uint64_t>(nq, r0 + per);
+            E->up_row[i] = (uint32_t)r0;
+            E->up_row[i + 1] = (uint32_t)r1;
+            HIPCHK(hipMemcpyAsync(E->d_raw + r0 * E->dim, h_queries + r0 * E->dim, (r1 - r0) * E->dim * 4,
+                                  hipMemcpyHostToDevice, E->stream_h2d));
+            HIPCHK(hipEventRecord(E->ev_up[i], E->stream_h2d));
+        }
+        E->up_slices = ns;
+    } else {
+        HIPCHK(hipMemcpyAsync(E->d_raw, h_queries, nq * E->dim * 4, hipMemcpyHostToDevice, E->stream));
+    }
     launch_queue_reset(queue_dev(E), E->stream);
     HIPCHK(hipGetLastError());
     new (E->h_progress) ProgressDev{};
@@ -728,9 +780,10 @@ int cora_gpu_reset(cora_gpu_engine *E, const float *h_queries, uint64_t nq) {
         E->h_thr[i] = FLT_MAX;
     *E->h_abort = 0;
     E->launched = false;
-    // the queries are resident in HBM when reset returns (a pageable upload may still be in
-    // flight after hipMemcpyAsync returns)
-    HIPCHK(hipStreamSynchronize(E->stream));
+    // an upload from any other host array is resident in HBM when reset returns (a pageable
+    // upload may still be in flight after hipMemcpyAsync returns)
+    if (!E->up_slices)
+        HIPCHK(hipStreamSynchronize(E->stream));
     return CORA_OK;
 }
 
@@ -793,45 +846,86 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
 
     if (want_final)  // no ring: the write limit never binds
         launch_fill_u64(E->d_cached_limit, ~0ull, 1, s);
-    // query preparation (hybrid.cu:436-463)
-    if (timing)
-        HIPCHK(hipEventRecord(E->ev_q0, s));
+    // query preparation (hybrid.cu:436-463) and coarse probing (hybrid.cu:465-498)
     const bool split_gemm = !(a->flags & CORA_FLAG_FP32_GEMM);
-    if (split_gemm && dist_gemm_f16x3_supported((uint32_t)E->dim, nq, P)) {
-        launch_split_f16(E->d_raw, nq, (uint32_t)E->dim, E->d_raw_hl, E->d_rawscale, s);
-        launch_rotate_f16x3(E->d_raw_hl, E->d_rawscale, E->d_rot_hl, E->d_rtscale, nq, (uint32_t)E->dim,
-                            P, E->d_qrot, s);
-    } else
-        launch_rotate(E->d_raw, E->d_rot, E->d_qrot, nq, (uint32_t)E->dim, P, s);
-    launch_query_prep(E->d_qrot, nq, P, (uint32_t)E->ex_bits, E->d_k1, E->d_kb, E->d_qnorm,
-                      E->d_qwidth, E->d_qwidth2, E->d_planes, E->d_qbytes, s);
-    if (lut)
-        launch_lut_build(E->d_qrot, nq, P, E->d_lut, s);
-    HIPCHK(hipEventRecord(E->ev_prep, s));
-    HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_prep, 0));
-    HIPCHK(hipMemcpyAsync(E->h_qrot, E->d_qrot, (size_t)nq * P * 4, hipMemcpyDeviceToHost,
-                          E->stream_d2h));
-    HIPCHK(hipMemcpyAsync(E->h_kb, E->d_kb, (size_t)nq * 4, hipMemcpyDeviceToHost, E->stream_d2h));
-    // coarse probing (hybrid.cu:465-498)
-    if (timing)
-        HIPCHK(hipEventRecord(E->ev_p0, s));
+    const bool split_rot = split_gemm && dist_gemm_f16x3_supported((uint32_t)E->dim, nq, P);
     const bool split_probe = split_gemm && dist_gemm_f16x3_supported(P, nq, E->nl);
     // the fused select keeps its candidates in the distance matrix's memory
     const bool fused_probe = split_probe && !(a->flags & CORA_FLAG_UNFUSED_PROBE) &&
                              fused_probe_supported((uint32_t)E->nl, np) &&
                              fused_probe_scratch_bytes(nq, (uint32_t)E->nl) <= (size_t)nq * E->nl * sizeof(float);
     E->last_fused_probe = fused_probe;
-    if (split_probe) {
-        launch_split_f16(E->d_qrot, nq, P, E->d_q_hl, E->d_qscale, s);
-        if (fused_probe)
-            launch_fused_probe_gemm(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
-                                    nq, (uint32_t)E->nl, P, E->d_dist, E->d_probe_fb, s);
-        else
-            launch_dist_gemm_f16x3(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
-                                   nq, (uint32_t)E->nl, P, E->d_dist, s);
-    } else
-        launch_dist_gemm(E->d_qrot, E->d_qnorm, E->d_cent, E->d_cnorm, nq, (uint32_t)E->nl, P,
-                         E->d_dist, s);
+    // queries uploaded in slices (cora_gpu_reset): each slice is rotated, prepared and probed
+    // by the fused GEMM as soon as it has landed; every other path waits for the whole upload
+    const uint32_t ns = E->up_slices && E->up_nq == nq && split_rot && fused_probe && !lut ? E->up_slices : 0u;
+    E->last_slices = ns;
+    if (!ns)
+        for (uint32_t i = 0; i < E->up_slices; ++i)
+            HIPCHK(hipStreamWaitEvent(s, E->ev_up[i], 0));
+    if (ns) {
+        const uint64_t D = E->dim;
+        launch_fill_u32(E->d_probe_fb, 0u, 1, s);  // the fallback count (launch_fused_probe_gemm)
+        for (uint32_t i = 0; i < ns; ++i) {
+            const uint32_t r0 = E->up_row[i], rows = E->up_row[i + 1] - r0;
+            HIPCHK(hipStreamWaitEvent(s, E->ev_up[i], 0));
+            if (timing && i == 0)
+                HIPCHK(hipEventRecord(E->ev_q0, s));
+            launch_split_f16_rows(E->d_raw + r0 * D, rows, (uint32_t)D, E->d_raw_hl + r0 * D,
+                                  E->d_raw_hl + (nq + r0) * D, E->d_rawscale + r0, s);
+            launch_rotate_f16x3_rows(E->d_raw_hl + r0 * D, E->d_raw_hl + (nq + r0) * D, E->d_rawscale + r0,
+                                     E->d_rot_hl, E->d_rtscale, rows, (uint32_t)D, P, E->d_qrot + (size_t)r0 * P, s);
+            launch_query_prep(E->d_qrot + (size_t)r0 * P, rows, P, (uint32_t)E->ex_bits, E->d_k1 + r0, E->d_kb + r0,
+                              E->d_qnorm + r0, E->d_qwidth + r0, E->d_qwidth2 + r0,
+                              E->d_planes + (size_t)r0 * 2 * kBq * E->W, E->d_qbytes + (size_t)r0 * 2 * P, s);
+            if (i + 1 == ns) {
+                HIPCHK(hipEventRecord(E->ev_prep, s));
+                HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_prep, 0));
+                HIPCHK(hipMemcpyAsync(E->h_qrot, E->d_qrot, (size_t)nq * P * 4, hipMemcpyDeviceToHost,
+                                      E->stream_d2h));
+                HIPCHK(hipMemcpyAsync(E->h_kb, E->d_kb, (size_t)nq * 4, hipMemcpyDeviceToHost, E->stream_d2h));
+            }
+            launch_split_f16_rows(E->d_qrot + (size_t)r0 * P, rows, P, E->d_q_hl + (size_t)r0 * P,
+                                  E->d_q_hl + (size_t)(nq + r0) * P, E->d_qscale + r0, s);
+            if (timing)
+                HIPCHK(hipEventRecord(E->ev_pg[i][0], s));
+            launch_fused_probe_gemm_rows(E->d_q_hl, E->d_q_hl + (size_t)nq * P, E->d_qscale, E->d_qnorm,
+                                         E->d_cent_hl, E->d_cscale, E->d_cnorm, r0, rows, nq, (uint32_t)E->nl, P,
+                                         E->d_dist, s);
+            if (timing)
+                HIPCHK(hipEventRecord(E->ev_pg[i][1], s));
+        }
+    } else {
+        if (timing)
+            HIPCHK(hipEventRecord(E->ev_q0, s));
+        if (split_rot) {
+            launch_split_f16(E->d_raw, nq, (uint32_t)E->dim, E->d_raw_hl, E->d_rawscale, s);
+            launch_rotate_f16x3(E->d_raw_hl, E->d_rawscale, E->d_rot_hl, E->d_rtscale, nq, (uint32_t)E->dim,
+                                P, E->d_qrot, s);
+        } else
+            launch_rotate(E->d_raw, E->d_rot, E->d_qrot, nq, (uint32_t)E->dim, P, s);
+        launch_query_prep(E->d_qrot, nq, P, (uint32_t)E->ex_bits, E->d_k1, E->d_kb, E->d_qnorm,
+                          E->d_qwidth, E->d_qwidth2, E->d_planes, E->d_qbytes, s);
+        if (lut)
+            launch_lut_build(E->d_qrot, nq, P, E->d_lut, s);
+        HIPCHK(hipEventRecord(E->ev_prep, s));
+        HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_prep, 0));
+        HIPCHK(hipMemcpyAsync(E->h_qrot, E->d_qrot, (size_t)nq * P * 4, hipMemcpyDeviceToHost,
+                              E->stream_d2h));
+        HIPCHK(hipMemcpyAsync(E->h_kb, E->d_kb, (size_t)nq * 4, hipMemcpyDeviceToHost, E->stream_d2h));
+        if (timing)
+            HIPCHK(hipEventRecord(E->ev_p0, s));
+        if (split_probe) {
+            launch_split_f16(E->d_qrot, nq, P, E->d_q_hl, E->d_qscale, s);
+            if (fused_probe)
+                launch_fused_probe_gemm(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
+                                        nq, (uint32_t)E->nl, P, E->d_dist, E->d_probe_fb, s);
+            else
+                launch_dist_gemm_f16x3(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
+                                       nq, (uint32_t)E->nl, P, E->d_dist, s);
+        } else
+            launch_dist_gemm(E->d_qrot, E->d_qnorm, E->d_cent, E->d_cnorm, nq, (uint32_t)E->nl, P,
+                             E->d_dist, s);
+    }
     if (timing)
         HIPCHK(hipEventRecord(E->ev_p1, s));
     if (fused_probe)
@@ -1032,7 +1126,17 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     if (E->last_timing) {
         HIPCHK(hipEventElapsedTime(&out.filter_ms, E->ev_f0, E->ev_f1));
         HIPCHK(hipEventElapsedTime(&out.scan_ms, E->ev_s0, E->ev_s1));
-        HIPCHK(hipEventElapsedTime(&out.probe_ms, E->ev_p0, E->ev_p1));
+        if (E->last_slices) {
+            // the probe GEMM slice by slice (query preparation runs between them)
+            out.probe_ms = 0.0f;
+            for (uint32_t i = 0; i < E->last_slices; ++i) {
+                float ms = 0.0f;
+                HIPCHK(hipEventElapsedTime(&ms, E->ev_pg[i][0], E->ev_pg[i][1]));
+                out.probe_ms += ms;
+            }
+        } else {
+            HIPCHK(hipEventElapsedTime(&out.probe_ms, E->ev_p0, E->ev_p1));
+        }
         HIPCHK(hipEventElapsedTime(&out.seed_ms, E->ev_f0, E->ev_s0));
         HIPCHK(hipEventElapsedTime(&out.recovery_ms, E->ev_s1, E->ev_f1));
         if (E->last_fused) {

@@ -209,12 +209,18 @@ void launch_row_norms(const float *x, uint32_t rows, uint32_t P, float *out, hip
 // split-FP16 operand rows: hl = [2][rows][P] (hi rows, then lo rows), scale [rows]
 void launch_split_f16(const float *x, uint32_t rows, uint32_t P, uint16_t *hl, float *scale,
                       hipStream_t s);
+// the same with the hi and lo rows at separate addresses
+void launch_split_f16_rows(const float *x, uint32_t rows, uint32_t P, uint16_t *hi, uint16_t *lo, float *scale,
+                           hipStream_t s);
 // inner dimension K % 32 == 0 and rows * K < 2^31 for both operands
 bool dist_gemm_f16x3_supported(uint32_t K, uint64_t rows_a, uint64_t rows_b);
 // Q' [nq][P] = X [nq][dim] . R from split-FP16 X and R^T [P][dim]
 void launch_rotate_f16x3(const uint16_t *xhl, const float *xscale, const uint16_t *rthl,
                          const float *rtscale, uint32_t nq, uint32_t dim, uint32_t P, float *out,
                          hipStream_t s);
+void launch_rotate_f16x3_rows(const uint16_t *xhi, const uint16_t *xlo, const float *xscale, const uint16_t *rthl,
+                              const float *rtscale, uint32_t rows, uint32_t dim, uint32_t P, float *out,
+                              hipStream_t s);
 void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const float *qnorm,
                             const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t nq,
                             uint32_t nl, uint32_t P, float *dist, hipStream_t s);
@@ -230,6 +236,11 @@ size_t fused_probe_scratch_bytes(uint32_t nq, uint32_t nl);
 void launch_fused_probe_gemm(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
                              const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
                              void *scratch, uint32_t *fb, hipStream_t s);
+// the GEMM part for query rows [r0, r0 + rows) of qhi / qlo ([nq][P] each); fb is not touched
+void launch_fused_probe_gemm_rows(const uint16_t *qhi, const uint16_t *qlo, const float *qscale, const float *qnorm,
+                                  const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t r0,
+                                  uint32_t rows, uint32_t nq, uint32_t nl, uint32_t P, void *scratch,
+                                  hipStream_t s);
 void launch_fused_probe_select(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
                                const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
                                uint32_t nprobe, void *scratch, uint32_t *fb, int32_t *idx, hipStream_t s);

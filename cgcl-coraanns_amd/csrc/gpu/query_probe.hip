@@ -1530,11 +1530,15 @@ void launch_dist_gemm(const float *q, const float *qnorm, const float *c, const 
 
 void launch_split_f16(const float *x, uint32_t rows, uint32_t P, uint16_t *hl, float *scale,
                       hipStream_t s) {
+    launch_split_f16_rows(x, rows, P, hl, hl + (size_t)rows * P, scale, s);
+}
+
+void launch_split_f16_rows(const float *x, uint32_t rows, uint32_t P, uint16_t *hi, uint16_t *lo, float *scale,
+                           hipStream_t s) {
     if (!rows)
         return;
-    _Float16 *hi = reinterpret_cast<_Float16 *>(hl);
-    split_f16_kernel<<<rows < (1u << 20) ? rows : (1u << 20), 64, 0, s>>>(x, rows, P, hi,
-                                                                          hi + (size_t)rows * P, scale);
+    split_f16_kernel<<<rows < (1u << 20) ? rows : (1u << 20), 64, 0, s>>>(
+        x, rows, P, reinterpret_cast<_Float16 *>(hi), reinterpret_cast<_Float16 *>(lo), scale);
 }
 
 bool dist_gemm_f16x3_supported(uint32_t K, uint64_t rows_a, uint64_t rows_b) {
@@ -1582,12 +1586,27 @@ void launch_fused_probe_gemm(const uint16_t *qhl, const float *qscale, const flo
                              void *scratch, uint32_t *fb, hipStream_t s) {
     if (!nq)
         return;
-    const FusedGeometry f(qhl, chl, nq, nl);
     // fb: [0] the fallback count, [1 .. nq] the fallback query rows
     launch_fill_u32(fb, 0u, 1, s);
+    launch_fused_probe_gemm_rows(qhl, qhl + (size_t)nq * P, qscale, qnorm, chl, cscale, cnorm, 0, nq, nq, nl, P,
+                                 scratch, s);
+}
+
+void launch_fused_probe_gemm_rows(const uint16_t *qhi, const uint16_t *qlo, const float *qscale, const float *qnorm,
+                                  const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t r0,
+                                  uint32_t rows, uint32_t nq, uint32_t nl, uint32_t P, void *scratch,
+                                  hipStream_t s) {
+    if (!rows)
+        return;
+    // rows [r0, r0 + rows) of the [nq] query operands, as a GEMM of its own whose candidate
+    // keys land in those rows of the [nq][nct][kProbeSlots] candidate array
+    const FusedGeometry f(qhi, chl, rows, nl);
+    const _Float16 *lo = reinterpret_cast<const _Float16 *>(qlo);
     dist_gemm_f16x3_kernel<2><<<kNumXcd * f.ncx * 4 * f.groups, 256, 0, s>>>(
-        f.qh, f.qh + (size_t)nq * P, qscale, f.ch, f.ch + (size_t)nl * P, cscale, nullptr, nq, nl, P, qnorm, cnorm,
-        f.ncx, f.groups * 4 * kHT, nullptr, nullptr, static_cast<unsigned long long *>(scratch), f.nct);
+        f.qh + (size_t)r0 * P, lo + (size_t)r0 * P, qscale + r0, f.ch, f.ch + (size_t)nl * P, cscale, nullptr, rows,
+        nl, P, qnorm + r0, cnorm, f.ncx, f.groups * 4 * kHT, nullptr, nullptr,
+        static_cast<unsigned long long *>(scratch) + (size_t)r0 * f.nct * kProbeSlots, f.nct);
+    (void)nq;
 }
 
 void launch_fused_probe_select(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
@@ -1615,15 +1634,21 @@ void launch_fused_probe_select(const uint16_t *qhl, const float *qscale, const f
 void launch_rotate_f16x3(const uint16_t *xhl, const float *xscale, const uint16_t *rthl,
                          const float *rtscale, uint32_t nq, uint32_t dim, uint32_t P, float *out,
                          hipStream_t s) {
-    if (!nq)
+    launch_rotate_f16x3_rows(xhl, xhl + (size_t)nq * dim, xscale, rthl, rtscale, nq, dim, P, out, s);
+}
+
+void launch_rotate_f16x3_rows(const uint16_t *xhi, const uint16_t *xlo, const float *xscale, const uint16_t *rthl,
+                              const float *rtscale, uint32_t rows, uint32_t dim, uint32_t P, float *out,
+                              hipStream_t s) {
+    if (!rows)
         return;
-    const uint32_t nrt = (nq + kHT - 1) / kHT, nct = (P + kHT - 1) / kHT;
+    const uint32_t nrt = (rows + kHT - 1) / kHT, nct = (P + kHT - 1) / kHT;
     const uint32_t ncx = (nct + kNumXcd - 1) / kNumXcd, groups = (nrt + 3) / 4;
-    const _Float16 *xh = reinterpret_cast<const _Float16 *>(xhl);
+    const _Float16 *xh = reinterpret_cast<const _Float16 *>(xhi);
     const _Float16 *rh = reinterpret_cast<const _Float16 *>(rthl);
     dist_gemm_f16x3_kernel<0><<<kNumXcd * ncx * 4 * groups, 256, 0, s>>>(
-        xh, xh + (size_t)nq * dim, xscale, rh, rh + (size_t)P * dim, rtscale, out, nq, P, dim, nullptr,
-        nullptr, ncx, groups * 4 * kHT, nullptr, nullptr, nullptr, 0);
+        xh, reinterpret_cast<const _Float16 *>(xlo), xscale, rh, rh + (size_t)P * dim, rtscale, out, rows, P, dim,
+        nullptr, nullptr, ncx, groups * 4 * kHT, nullptr, nullptr, nullptr, 0);
 }
 
 // ---- big-k select (nprobe > kSelectMaxProbe, up to 65,536): one 1024-thread block per

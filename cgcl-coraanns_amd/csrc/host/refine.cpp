@@ -198,6 +198,9 @@ inline void store_threshold(float *t, std::size_t q, float v) {
     }
 }
 
+constexpr std::size_t kRefineChunk = 1024;
+static_assert(queue::consumer_chunk % kRefineChunk == 0, "a power of two no larger than the reference's chunk");
+
 struct alignas(64) QuerySlot {
     std::atomic_flag lock = ATOMIC_FLAG_INIT;
     int count = 0;
@@ -217,7 +220,12 @@ RefineOut cpu_refine(const RefineArgs &a, std::size_t nq, std::size_t topk, floa
     std::vector<uint32_t> tp(nq * kstride);
     std::unique_ptr<QuerySlot[]> slots(new QuerySlot[nq]);
     const Position capacity = a.capacity, mask = capacity - 1;
-    const Position chunk = std::min<Position>(queue::consumer_chunk, capacity);
+    // Consumer chunks of kRefineChunk records rather than the reference's consumer_chunk
+    // (8,192): at ~170 ns a record, a thread that takes one of the last 8,192-record chunks
+    // would refine for ~1.4 ms after the GPU published its records, the length of the far
+    // scan, and end the search after the GPU; smaller chunks spread the last records over
+    // all threads. Which thread refines a record changes nothing in the results.
+    const Position chunk = std::min<Position>(kRefineChunk, capacity);
     std::atomic<Position> head{0};
     queue::ReleaseTracker tracker(*a.progress, capacity, chunk);
     queue::Progress *pg = a.progress;

@@ -217,18 +217,22 @@ int cora_gpu_free_workspace(cora_gpu_engine *engine);
 int cora_gpu_queue_view(cora_gpu_engine *engine, cora_queue_view *out);
 
 /* Per-chunk reset (HybridIndex::reset_buffer, hybrid.cu:380-396): uploads the raw
- * queries f32 [nq][dim] (complete when the call returns), resets device queue counters
- * and the host Progress, and sets the thresholds of the first nq queries to FLT_MAX.
- * Queries already placed in the pinned staging buffer (cora_gpu_query_staging) upload in
- * one DMA; any other host array goes through the runtime's pageable-copy path. */
+ * queries f32 [nq][dim], resets device queue counters and the host Progress, and sets the
+ * thresholds of the first nq queries to FLT_MAX. Queries already placed in the pinned
+ * staging buffer (cora_gpu_query_staging) upload asynchronously, in up to four slices for
+ * nq >= 2,048, and the next search prepares and probes each slice as soon as it has landed;
+ * the staging buffer is rewritable after the next cora_gpu_query_staging call, which waits
+ * for the upload. Any other host array goes through the runtime's pageable-copy path and
+ * is resident when the call returns. */
 int cora_gpu_reset(cora_gpu_engine *engine, const float *h_queries, uint64_t nq);
 /* The final top-k of a search launched with CORA_FLAG_GPU_FINAL, after cora_gpu_sync:
  * dists [nq][topk] ascending (FLT_MAX pad) and cluster-order vector indexes idx [nq][topk]
  * (0xFFFFFFFF pad; the ids array of load_from_raw_pointers maps them to ids); ties by index. */
 int cora_gpu_final_results(cora_gpu_engine *engine, float *dists, uint32_t *idx);
 /* Pinned host buffer of [max_q][dim] floats for the queries of the next reset (valid from
- * prepare_workspace to free_workspace). No counterpart in the reference, which uploads
- * from the caller's pageable array. */
+ * prepare_workspace to free_workspace); returns once the last reset's upload from it is
+ * complete. No counterpart in the reference, which uploads from the caller's pageable
+ * array. */
 int cora_gpu_query_staging(cora_gpu_engine *engine, float **staging);
 
 /* Enqueue the whole GPU side of HybridIndex::search (hybrid.cu:434-660) and return

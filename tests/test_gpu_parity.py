@@ -372,6 +372,41 @@ def test_fused_probe_fallback_sweep(tmp_path):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("dim,metric", [(96, 0), (768, 1)])
+def test_sliced_upload_matches_one_pass(dim, metric, tmp_path):
+    """Queries uploaded from the staging buffer in slices (4,100 queries: four slices of
+    1,152 / 1,152 / 1,152 / 644 rows, each rotated, prepared and probed as it lands) give the
+    same rotated queries, query factors, Bq=8 planes, probe lists and frozen top-k, bit for
+    bit, as the same queries searched in chunks of 1,400 that upload and run in one pass."""
+    rng = np.random.default_rng(4100 + dim)
+    nlist, n, nq, nprobe, topk = 8192, 40000, 4100, 16, 10
+    cent = rng.normal(0, 1, (nlist, dim)).astype(np.float32)
+    assign = rng.integers(0, nlist, n).astype(np.uint32)
+    x = (cent[assign] + rng.normal(0, 0.3, (n, dim))).astype(np.float32)
+    q = (cent[rng.integers(0, nlist, nq)] + rng.normal(0, 0.3, (nq, dim))).astype(np.float32)
+    if metric == 1:
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+    P = (dim + 63) // 64 * 64  # the rotator is [dim][P]: orthonormal rows, padded to whole 64s
+    R = np.linalg.qr(rng.normal(size=(P, P)))[0][:dim].astype(np.float32)
+    path = tmp_path / "sliced.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32), (cent.astype(np.float64) @ R).astype(np.float32),
+                 assign, R, metric=metric)
+    case = Case(path, q)
+    say(f"[gpu] sliced upload vs one pass, nq={nq} dim={dim} nlist={nlist}")
+    eng, d, i = run_frozen(case, nprobe, topk, vanguard=3)
+    g = gpu_intermediates(eng, case, nprobe)
+    eng.close()
+    for c0 in range(0, nq, 1400):
+        sub = Case(path, q[c0:c0 + 1400])
+        e2, d2, i2 = run_frozen(sub, nprobe, topk, vanguard=3)
+        g2 = gpu_intermediates(e2, sub, nprobe)
+        e2.close()
+        for key, v in g2.items():
+            assert np.array_equal(g[key][c0:c0 + 1400], v), (key, c0)
+        assert np.array_equal(i[c0:c0 + 1400], i2) and np.array_equal(d[c0:c0 + 1400], d2), c0
+
+
 def test_end_to_end_nprobe_8192(tmp_path):
     """nprobe 8,192 (beyond the LDS-held selects) end to end with frozen infinite thresholds:
     probe lists against the oracle's FP64 coarse probe, every vector of every probed
