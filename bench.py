@@ -171,8 +171,10 @@ def main():
     # CPU refinement threads: at top-10 the GPU bounds the step and 12 of the box's 16-CPU
     # share leave room for the submitting thread and the HIP runtime's threads (with 16
     # spinning consumers a search now and then waited a scheduler tick, ~4 ms); at top-100
-    # the CPU refinement of ~190 candidates per query bounds it and takes all 16
-    threads = args.cpu_threads or min(12 if c.topk <= 10 else 16, os.cpu_count() or 16)
+    # the CPU refinement of ~190 candidates per query bounds it and takes all 16; with the
+    # GPU-final top-k the CPU refines nothing (its threads copy the queries and map the
+    # result ids), and 16 threads left 7 of 10 steps 6-9 ms longer
+    threads = args.cpu_threads or min(12 if c.topk <= 10 or args.gpu_final else 16, os.cpu_count() or 16)
     batch_q = args.batch_q or c.batch_q
     workdir = args.workdir or tempfile.mkdtemp(prefix="cora_bench_")
     os.makedirs(workdir, exist_ok=True)

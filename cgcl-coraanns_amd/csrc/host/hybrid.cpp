@@ -273,7 +273,12 @@ void HybridIndex::search(const float *h_queries, std::size_t num_queries, std::s
         if (rc != CORA_OK)
             throw std::runtime_error(engine_error(engine_));
         check(engine_, cora_gpu_final_results(engine_, h_final_dists, h_final_pids));
-        for (std::size_t i = 0; i < num_queries * topk; ++i)
+        // cluster-order indexes to ids: random reads of the ids array (80 MB at 20M vectors),
+        // one cache miss each, spread over the refinement threads (the CPU refines nothing here)
+        const std::size_t n = num_queries * topk;
+        const int threads = cpu_threads_ > 0 ? cpu_threads_ : omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(static)
+        for (std::size_t i = 0; i < n; ++i)
             h_final_pids[i] = h_final_pids[i] < num_vectors_ ? h_ids_[h_final_pids[i]] : 0u;
         print_profile(st, 0);
         return;
