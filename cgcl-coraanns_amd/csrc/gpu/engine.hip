@@ -34,9 +34,9 @@ void hfree(T *&p) {
     p = nullptr;
 }
 
-// Query upload slices: at most kUploadSlices of at least kUploadMinRows rows (a multiple of
-// the GEMMs' 128-row tiles).
-constexpr uint32_t kUploadSlices = 4;
+// Query upload slices (cora_gpu_reset): kUploadSlices of them for 2 kUploadMinRows queries
+// or more.
+constexpr uint32_t kUploadSlices = 3;
 constexpr uint32_t kUploadMinRows = 1024;
 
 }  // namespace
@@ -756,13 +756,16 @@ int cora_gpu_reset(cora_gpu_engine *E, const float *h_queries, uint64_t nq) {
     E->up_slices = 0;
     E->up_nq = nq;
     if (h_queries == E->h_qstage && nq >= 2 * kUploadMinRows) {
-        // from the pinned staging buffer: slices of whole 128-row tiles on the H2D stream; the
-        // search waits for each before the kernels that read it (cora_gpu_launch_search)
-        const uint32_t ns = std::min<uint32_t>(kUploadSlices, (uint32_t)(nq / kUploadMinRows));
-        const uint32_t per = (uint32_t)((nq + ns - 1) / ns + 127) / 128 * 128;
+        // from the pinned staging buffer: three slices of whole 128-row tiles on the H2D
+        // stream, the first an eighth of the queries (it lands soonest, and the GPU starts on
+        // it), the other two halves of the rest (large enough to fill the GPU in the rotation
+        // GEMM); the search waits for each before the kernels that read it
+        const auto up128 = [](uint64_t r) { return (r + 127) / 128 * 128; };
+        const uint64_t s0 = up128(nq / 8), s1 = s0 + up128((nq - s0) / 2);
+        const uint64_t bounds[kUploadSlices + 1] = {0, s0, s1, nq};
+        const uint32_t ns = kUploadSlices;
         for (uint32_t i = 0; i < ns; ++i) {
-            const uint64_t r0 = std::min<uint64_t>(nq, (uint64_t)i * per);
-            const uint64_t r1 = i + 1 == ns ? nq : std::min<uint64_t>(nq, r0 + per);
+            const uint64_t r0 = bounds[i], r1 = bounds[i + 1];
             E->up_row[i] = (uint32_t)r0;
             E->up_row[i + 1] = (uint32_t)r1;
             HIPCHK(hipMemcpyAsync(E->d_raw + r0 * E->dim, h_queries + r0 * E->dim, (r1 - r0) * E->dim * 4,

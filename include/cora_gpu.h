@@ -219,7 +219,7 @@ int cora_gpu_queue_view(cora_gpu_engine *engine, cora_queue_view *out);
 /* Per-chunk reset (HybridIndex::reset_buffer, hybrid.cu:380-396): uploads the raw
  * queries f32 [nq][dim], resets device queue counters and the host Progress, and sets the
  * thresholds of the first nq queries to FLT_MAX. Queries already placed in the pinned
- * staging buffer (cora_gpu_query_staging) upload asynchronously, in up to four slices for
+ * staging buffer (cora_gpu_query_staging) upload asynchronously, in three slices for
  * nq >= 2,048, and the next search prepares and probes each slice as soon as it has landed;
  * the staging buffer is rewritable after the next cora_gpu_query_staging call, which waits
  * for the upload. Any other host array goes through the runtime's pageable-copy path and

@@ -374,8 +374,8 @@ def test_fused_probe_fallback_sweep(tmp_path):
 
 @pytest.mark.parametrize("dim,metric", [(96, 0), (768, 1)])
 def test_sliced_upload_matches_one_pass(dim, metric, tmp_path):
-    """Queries uploaded from the staging buffer in slices (4,100 queries: four slices of
-    1,152 / 1,152 / 1,152 / 644 rows, each rotated, prepared and probed as it lands) give the
+    """Queries uploaded from the staging buffer in slices (4,100 queries: three slices of
+    512 / 1,920 / 1,668 rows, each rotated, prepared and probed as it lands) give the
     same rotated queries, query factors, Bq=8 planes, probe lists and frozen top-k, bit for
     bit, as the same queries searched in chunks of 1,400 that upload and run in one pass."""
     rng = np.random.default_rng(4100 + dim)
