@@ -108,6 +108,7 @@ struct cora_gpu_engine {
     ProgressDev *h_progress = nullptr;
     float *h_thr = nullptr, *h_thr_stage = nullptr;
     float *h_qstage = nullptr;  // pinned query staging [max_q][dim] (cora_gpu_query_staging)
+    unsigned long long *h_sync = nullptr;  // pinned: the search's statistics and stall flag (cora_gpu_sync)
     int *h_abort = nullptr;
     unsigned long long *d_produced = nullptr, *d_cached_limit = nullptr, *d_spill_count = nullptr;
     int *d_refresh = nullptr, *d_overflow = nullptr, *d_stalled = nullptr;
@@ -200,6 +201,7 @@ void release_queue(cora_gpu_engine *E) {
     hfree(E->h_thr);
     hfree(E->h_thr_stage);
     hfree(E->h_qstage);
+    hfree(E->h_sync);
     hfree(E->h_abort);
     dfree(E->d_produced);
     dfree(E->d_cached_limit);
@@ -656,6 +658,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(halloc(E, E->h_thr, max_q, coherent));
         TRY(halloc(E, E->h_thr_stage, max_q, hipHostMallocDefault));
         TRY(halloc(E, E->h_qstage, max_q * E->dim, hipHostMallocDefault));
+        TRY(halloc(E, E->h_sync, 12, hipHostMallocDefault));
         TRY(halloc(E, E->h_abort, 1, coherent));
         TRY(dalloc(E, E->d_produced, 1));
         TRY(dalloc(E, E->d_cached_limit, 1));
@@ -1095,12 +1098,16 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     if (!E->launched)
         return fail(E, CORA_ERR_LOGIC, "no search launched");
     HIPCHK(hipSetDevice(E->device));
+    // the statistics and the stall flag in one round trip: both copies behind the search's
+    // kernels on its stream, into pinned memory, and one synchronisation
+    HIPCHK(hipMemcpyAsync(E->h_sync, E->d_stats, 11 * sizeof(unsigned long long), hipMemcpyDeviceToHost, E->stream));
+    HIPCHK(hipMemcpyAsync(E->h_sync + 11, E->d_stalled, sizeof(int), hipMemcpyDeviceToHost, E->stream));
     HIPCHK(hipStreamSynchronize(E->stream));
     HIPCHK(hipStreamSynchronize(E->stream_d2h));
-    unsigned long long stats[11] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    unsigned long long stats[11];
+    memcpy(stats, E->h_sync, sizeof(stats));
     int stalled = 0;
-    HIPCHK(hipMemcpy(stats, E->d_stats, sizeof(stats), hipMemcpyDeviceToHost));
-    HIPCHK(hipMemcpy(&stalled, E->d_stalled, sizeof(int), hipMemcpyDeviceToHost));
+    memcpy(&stalled, E->h_sync + 11, sizeof(int));
     cora_search_stats out{};
     out.produced = __atomic_load_n(&E->h_progress->produced, __ATOMIC_ACQUIRE);
     out.spilled = __atomic_load_n(&E->h_progress->spilled, __ATOMIC_ACQUIRE);

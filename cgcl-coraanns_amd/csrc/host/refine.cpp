@@ -350,6 +350,9 @@ RefineOut cpu_refine(const RefineArgs &a, std::size_t nq, std::size_t topk, floa
     out.produced = produced();
     out.refined = refined_total.load();
     out.aborted = aborted();
+    // the results, one query per iteration, over the refinement threads (this runs after the
+    // GPU has finished, so it is on the step's critical path)
+#pragma omp parallel for num_threads(threads) schedule(static)
     for (std::size_t q = 0; q < nq; ++q) {
         const int n = slots[q].count;
         for (int i = 0; i < static_cast<int>(topk); ++i) {
