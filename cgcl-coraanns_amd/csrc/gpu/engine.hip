@@ -50,6 +50,11 @@ struct cora_gpu_engine {
     // DMA on stream_h2d signals ev_up[i]; the search prepares and probes a slice's queries as
     // soon as it has landed, while the later slices are still in flight
     hipStream_t stream_h2d = nullptr;
+    // pair scheduling and the query order of the fused pass need only the probe indices: they
+    // run on stream_aux (forked at ev_fork) beside the probes' exact g_add and join the engine
+    // stream at ev_join before the first scan
+    hipStream_t stream_aux = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     hipEvent_t ev_up[kUploadSlices] = {};
     hipEvent_t ev_pg[kUploadSlices][2] = {};  // the probe GEMM of each slice (timing)
     uint32_t up_slices = 0, up_row[kUploadSlices + 1] = {};
@@ -103,6 +108,8 @@ struct cora_gpu_engine {
     Pair *d_pairs = nullptr;
     Unit *d_units = nullptr;
     unsigned long long *d_stats = nullptr;
+    unsigned long long *d_btot = nullptr;  // per-block totals of the bucket scan
+    bool bcount_zero = false;  // d_bcount is all zero: the last pair scheduling's scan cleared it
     // queue
     uint4 *h_items = nullptr;
     ProgressDev *h_progress = nullptr;
@@ -219,6 +226,8 @@ void release_workspace(cora_gpu_engine *E) {
         (void)hipStreamSynchronize(E->stream_d2h);
     if (E->stream_h2d)
         (void)hipStreamSynchronize(E->stream_h2d);
+    if (E->stream_aux)
+        (void)hipStreamSynchronize(E->stream_aux);
     E->up_slices = 0;
     E->ws = false;
     E->launched = false;
@@ -252,6 +261,7 @@ void release_workspace(cora_gpu_engine *E) {
     dfree(E->d_pairs);
     dfree(E->d_units);
     dfree(E->d_stats);
+    dfree(E->d_btot);
     hfree(E->h_qrot);
     hfree(E->h_kb);
     hfree(E->h_gadd);
@@ -330,6 +340,9 @@ int cora_gpu_create(cora_gpu_engine **out, int device) {
         HIPCHK(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
         HIPCHK(hipStreamCreateWithFlags(&E->stream_d2h, hipStreamNonBlocking));
         HIPCHK(hipStreamCreateWithFlags(&E->stream_h2d, hipStreamNonBlocking));
+        HIPCHK(hipStreamCreateWithFlags(&E->stream_aux, hipStreamNonBlocking));
+        HIPCHK(hipEventCreateWithFlags(&E->ev_fork, hipEventDisableTiming));
+        HIPCHK(hipEventCreateWithFlags(&E->ev_join, hipEventDisableTiming));
         for (uint32_t i = 0; i < kUploadSlices; ++i) {
             HIPCHK(hipEventCreateWithFlags(&E->ev_up[i], hipEventDisableTiming));
             HIPCHK(hipEventCreate(&E->ev_pg[i][0]));
@@ -381,6 +394,11 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
         (void)hipStreamDestroy(E->stream_d2h);
     if (E->stream_h2d)
         (void)hipStreamDestroy(E->stream_h2d);
+    for (hipEvent_t ev : {E->ev_fork, E->ev_join})
+        if (ev)
+            (void)hipEventDestroy(ev);
+    if (E->stream_aux)
+        (void)hipStreamDestroy(E->stream_aux);
     delete E;
     return CORA_OK;
 }
@@ -616,12 +634,14 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_gadd, np));
         TRY(dalloc(E, E->d_gerr, np));
         TRY(dalloc(E, E->d_bcount, nb));
+        E->bcount_zero = false;
         TRY(dalloc(E, E->d_bcursor, nb));
         TRY(dalloc(E, E->d_boff, nb + 1));
         TRY(dalloc(E, E->d_uoff, nb + 1));
         TRY(dalloc(E, E->d_nunits, 2));
         TRY(dalloc(E, E->d_cursor, kNumXcd));
         TRY(dalloc(E, E->d_stats, 11));
+        TRY(dalloc(E, E->d_btot, bucket_scan_words((uint32_t)E->nl)));
         TRY(dalloc(E, E->d_pairs, np));
         TRY(dalloc(E, E->d_units, np * unit_splits((uint32_t)E->max_cluster)));
         TRY(dalloc(E, E->d_thr_snap, max_q));
@@ -941,12 +961,6 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         launch_select_big(E->d_dist, nq, (uint32_t)E->nl, np, E->d_selbig, E->d_pidx, s);
     else
         launch_select(E->d_dist, nq, (uint32_t)E->nl, np, E->d_pidx, s);
-    launch_probe_refine(E->d_qrot, E->d_cent, E->d_pidx, nq, np, P, E->metric, E->d_gadd,
-                        E->d_gerr, a->bound_scale > 0.0f ? a->bound_scale : 1.0f, s);
-    HIPCHK(hipEventRecord(E->ev_probe, s));
-    HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_probe, 0));
-    HIPCHK(hipMemcpyAsync(E->h_gadd, E->d_gadd, (size_t)nq * np * 4, hipMemcpyDeviceToHost,
-                          E->stream_d2h));
     // GPU ex-code stages (seed thresholds, refined pre-filter): live thresholds only, or
     // the frozen snapshot in the GPU_SEED_FROZEN test mode
     const bool ex_stage_mode = !frozen || (a->flags & CORA_FLAG_GPU_SEED_FROZEN);
@@ -966,12 +980,26 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool van_lows = fused && depth > 0 && far_mfma_supported(E->W) && E->d_van_lows &&
                           !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA) &&
                           (lows_by_size || (a->flags & CORA_FLAG_VANGUARD_MFMA));
+    // fork: pair scheduling (and the fused pass's query order) on stream_aux
+    HIPCHK(hipEventRecord(E->ev_fork, s));
+    HIPCHK(hipStreamWaitEvent(E->stream_aux, E->ev_fork, 0));
     // pair scheduling (hybrid.cu:504-508)
     launch_build_pairs(E->d_pidx, E->d_meta, nq, np, (uint32_t)E->nl, depth, batch,
                        van_lows ? kMfmaBatchQ : 1u, P / 8 + 12, E->d_bcount, E->d_bcursor, E->d_boff,
                        E->d_uoff, E->d_pairs, E->d_units,
                        (uint64_t)nq * np * unit_splits((uint32_t)E->max_cluster), E->d_nunits, E->d_stats,
-                       s);
+                       E->d_btot, E->bcount_zero, E->stream_aux);
+    E->bcount_zero = true;
+    const bool ordered = fused && launch_order_queries(E->d_pidx, nq, np, (uint32_t)E->nl, E->d_qorder,
+                                                       E->stream_aux);
+    HIPCHK(hipEventRecord(E->ev_join, E->stream_aux));
+    launch_probe_refine(E->d_qrot, E->d_cent, E->d_pidx, nq, np, P, E->metric, E->d_gadd,
+                        E->d_gerr, a->bound_scale > 0.0f ? a->bound_scale : 1.0f, s);
+    HIPCHK(hipEventRecord(E->ev_probe, s));
+    HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_probe, 0));
+    HIPCHK(hipMemcpyAsync(E->h_gadd, E->d_gadd, (size_t)nq * np * 4, hipMemcpyDeviceToHost,
+                          E->stream_d2h));
+    HIPCHK(hipStreamWaitEvent(s, E->ev_join, 0));
     if (timing)
         HIPCHK(hipEventRecord(E->ev_sched, s));
     if (frozen) {
@@ -1000,8 +1028,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     if (fused) {
         va.probe_idx = E->d_pidx;
         va.nq = nq;
-        va.order = launch_order_queries(E->d_pidx, nq, np, (uint32_t)E->nl, E->d_qorder, s) ? E->d_qorder
-                                                                                          : nullptr;
+        va.order = ordered ? E->d_qorder : nullptr;
         va.depth = depth;
         va.topk = a->topk;
         va.thr_out = frozen ? E->d_thr_snap : E->h_thr;

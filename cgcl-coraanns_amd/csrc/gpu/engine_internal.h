@@ -265,7 +265,12 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
                         uint32_t *bucket_cursor,
                         uint32_t *bucket_offset, uint32_t *unit_offset, Pair *pairs, Unit *units,
                         uint64_t max_units, uint32_t *num_units /*[2]: vanguard, far*/,
-                        unsigned long long *scan_stats /*[0..2], [9], [10]*/, hipStream_t s);
+                        unsigned long long *scan_stats /*[0..2], [9], [10]*/,
+                        unsigned long long *block_tot /*[bucket_scan_words(nlist)] scratch*/,
+                        bool counts_zero /*bucket_count is all zero (the last call's scan cleared it)*/,
+                        hipStream_t s);
+// u64 words of the bucket scan's per-block totals
+size_t bucket_scan_words(uint32_t nlist);
 void launch_fill_u32(uint32_t *p, uint32_t value, size_t n, hipStream_t s);
 void launch_fill_u64(unsigned long long *p, unsigned long long value, size_t n, hipStream_t s);
 void launch_queue_reset(QueueDev q, hipStream_t s);

@@ -1440,52 +1440,60 @@ __global__ __launch_bounds__(kThreads) void select_regs_kernel(const float *__re
         out[(size_t)blockIdx.x * k + i] = (int32_t)(uint32_t)(sel[i] & 0xFFFFFFFFull);
 }
 
-// One block (4 waves) per query; each wave takes probes p = wave, wave + 4, ..., two at a
-// time with both centroid rows' loads issued together.
+// 4 blocks of 256 threads a CU, on 256 CUs
+constexpr uint32_t kRefineGrid = 1024;
+
+// A block (4 waves) per query, over a grid of at most kRefineGrid blocks that strides
+// through the queries: once its blocks are dispatched, the hardware places the workgroups of
+// the pair scheduling, which runs beside this kernel on another stream, in the wave slots left
+// free (with a block per query it would hand every freed slot back to this kernel and the
+// scheduling would wait for its end). Each wave takes probes p = wave, wave + 4, ..., two
+// at a time with both centroid rows' loads issued together.
 __global__ __launch_bounds__(256) void probe_refine_kernel(const float *__restrict__ qrot,
                                                            const float *__restrict__ cent,
                                                            const int32_t *__restrict__ idx,
                                                            uint32_t nprobe, uint32_t P, int metric,
                                                            float *__restrict__ gadd,
                                                            float *__restrict__ gerr,
-                                                           float err_scale) {
-    const uint32_t q = blockIdx.x;
+                                                           float err_scale, uint32_t nq) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t groups = P / 64;
-    float v[16];
+    for (uint32_t q = blockIdx.x; q < nq; q += gridDim.x) {
+        float v[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-        v[i] = (uint32_t)i < groups ? qrot[(size_t)q * P + lane + 64 * i] : 0.0f;
-    for (uint32_t p0 = wave; p0 < nprobe; p0 += 8) {
-        const bool two = p0 + 4 < nprobe;
-        const float *crow[2];
-        crow[0] = cent + (size_t)idx[(size_t)q * nprobe + p0] * P;
-        crow[1] = cent + (size_t)idx[(size_t)q * nprobe + (two ? p0 + 4 : p0)] * P;
-        float cv[2][16];
+        for (int i = 0; i < 16; ++i)
+            v[i] = (uint32_t)i < groups ? qrot[(size_t)q * P + lane + 64 * i] : 0.0f;
+        for (uint32_t p0 = wave; p0 < nprobe; p0 += 8) {
+            const bool two = p0 + 4 < nprobe;
+            const float *crow[2];
+            crow[0] = cent + (size_t)idx[(size_t)q * nprobe + p0] * P;
+            crow[1] = cent + (size_t)idx[(size_t)q * nprobe + (two ? p0 + 4 : p0)] * P;
+            float cv[2][16];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                cv[h][i] = (uint32_t)i < groups ? crow[h][lane + 64 * i] : 0.0f;
+                for (int i = 0; i < 16; ++i)
+                    cv[h][i] = (uint32_t)i < groups ? crow[h][lane + 64 * i] : 0.0f;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (h == 1 && !two)
-                break;
-            float l2 = 0.0f, ip = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                if ((uint32_t)i >= groups)
+            for (int h = 0; h < 2; ++h) {
+                if (h == 1 && !two)
                     break;
-                const float d = v[i] - cv[h][i];
-                l2 = fmaf(d, d, l2);
-                ip = fmaf(v[i], cv[h][i], ip);
-            }
-            l2 = wave_sum(l2);
-            ip = wave_sum(ip);
-            const uint32_t p = p0 + 4 * h;
-            if (lane == 0) {
-                gadd[(size_t)q * nprobe + p] = metric == 0 ? l2 : -ip;
-                gerr[(size_t)q * nprobe + p] = err_scale * sqrtf(fmaxf(l2, 0.0f));
+                float l2 = 0.0f, ip = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    if ((uint32_t)i >= groups)
+                        break;
+                    const float d = v[i] - cv[h][i];
+                    l2 = fmaf(d, d, l2);
+                    ip = fmaf(v[i], cv[h][i], ip);
+                }
+                l2 = wave_sum(l2);
+                ip = wave_sum(ip);
+                const uint32_t p = p0 + 4 * h;
+                if (lane == 0) {
+                    gadd[(size_t)q * nprobe + p] = metric == 0 ? l2 : -ip;
+                    gerr[(size_t)q * nprobe + p] = err_scale * sqrtf(fmaxf(l2, 0.0f));
+                }
             }
         }
     }
@@ -1848,7 +1856,10 @@ void launch_select_big(const float *dist, uint32_t nq, uint32_t nl, uint32_t npr
 void launch_probe_refine(const float *qrot, const float *cent, const int32_t *idx, uint32_t nq,
                          uint32_t nprobe, uint32_t P, int metric, float *gadd, float *gerr,
                          float err_scale, hipStream_t s) {
-    probe_refine_kernel<<<nq, 256, 0, s>>>(qrot, cent, idx, nprobe, P, metric, gadd, gerr, err_scale);
+    if (nq == 0)
+        return;
+    probe_refine_kernel<<<std::min(nq, kRefineGrid), 256, 0, s>>>(qrot, cent, idx, nprobe, P, metric, gadd, gerr,
+                                                                  err_scale, nq);
 }
 
 }  // namespace cora

@@ -93,106 +93,131 @@ __global__ void count_pairs_kernel(const int32_t *__restrict__ probe_idx, uint32
     atomicAdd(&count[(p >= vanguard ? nlist : 0u) + c], 1u);
 }
 
-constexpr int kScanThreads = 1024;
+// Bucket scan over many workgroups, kScanBlock buckets each (one a thread): the first
+// kernel writes every block's totals of the eight sums, the second scans its buckets on
+// top of the totals of the blocks before it, and its last block writes the grand totals.
+// The second also clears each bucket's scatter cursor and, once it has read it, its count,
+// so the next search's counting starts from zero without a fill.
+constexpr uint32_t kScanBlock = 1024;
+constexpr int kScanWaves = kScanBlock / 64;
+constexpr int kScanSums = 8;
 
-// Single block: exclusive scans of bucket sizes and unit counts, unit totals and the
-// algorithmic traffic of the far-pair scan.
-__global__ __launch_bounds__(kScanThreads) void scan_buckets_kernel(
+// The eight per-bucket terms: pairs, units, vanguard units, far-scan bytes, far units, far
+// pair-vectors, vanguard-scan bytes, vanguard pair-vectors. Buckets past the end add nothing.
+__device__ __forceinline__ void bucket_terms(uint32_t b, uint32_t nb, const uint32_t *count,
+                                             const ClusterMeta *__restrict__ meta, uint32_t nlist,
+                                             uint32_t batch_q, uint32_t van_batch, uint32_t bpv,
+                                             unsigned long long v[kScanSums]) {
+    const uint32_t m = b < nb ? count[b] : 0u;
+    const uint32_t n = b < nb ? meta[b < nlist ? b : b - nlist].n : 0u;
+    const bool van = b < nlist;
+    const uint32_t u = (m + (van ? van_batch : batch_q) - 1) / (van ? van_batch : batch_q);
+    const unsigned long long scan = (unsigned long long)u * n * bpv, pv = (unsigned long long)m * n;
+    v[0] = m;
+    v[1] = (unsigned long long)u * unit_splits(n);
+    v[2] = van ? v[1] : 0ull;
+    v[3] = van ? 0ull : scan;
+    v[4] = van ? 0ull : u;
+    v[5] = van ? 0ull : pv;
+    v[6] = van ? scan : 0ull;
+    v[7] = van ? pv : 0ull;
+}
+
+__global__ __launch_bounds__(kScanBlock) void bucket_totals_kernel(
     const uint32_t *__restrict__ count, const ClusterMeta *__restrict__ meta, uint32_t nlist,
-    uint32_t batch_q, uint32_t van_batch, uint32_t bpv, uint32_t *__restrict__ bucket_offset,
-    uint32_t *__restrict__ unit_offset, uint32_t *__restrict__ num_units,
-    unsigned long long *__restrict__ stats) {
-    constexpr int kWaves = kScanThreads / 64;
-    // per-wave totals of the eight sums (inclusive scans run within each wave by shuffles)
-    __shared__ unsigned long long s_tot[8][kWaves];
-    const uint32_t nb = 2 * nlist;
-    const int t = threadIdx.x;
-    const uint32_t chunk = (nb + kScanThreads - 1) / kScanThreads;
-    const uint32_t b0 = min(nb, t * chunk), b1 = min(nb, b0 + chunk);
-    uint32_t pairs = 0, units = 0, van_units = 0;
-    unsigned long long bytes = 0, fu = 0, vec = 0, vbytes = 0, vvec = 0;
-    // the thread's buckets 16 at a time: their loads issued together (one round trip per
-    // 16 buckets instead of one per bucket; this single workgroup is latency-bound)
-    constexpr uint32_t kBatch = 16;
-    uint32_t mv[kBatch], nv[kBatch];
-    auto fetch = [&](uint32_t bb) {
+    uint32_t batch_q, uint32_t van_batch, uint32_t bpv, unsigned long long *__restrict__ block_tot) {
+    __shared__ unsigned long long s_w[kScanSums][kScanWaves];
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    unsigned long long v[kScanSums];
+    bucket_terms(blockIdx.x * kScanBlock + t, 2 * nlist, count, meta, nlist, batch_q, van_batch, bpv, v);
 #pragma unroll
-        for (uint32_t j = 0; j < kBatch; ++j) {
-            const uint32_t b = bb + j;
-            mv[j] = b < b1 ? count[b] : 0u;
-            nv[j] = b < b1 ? meta[b < nlist ? b : b - nlist].n : 0u;
-        }
-    };
-    for (uint32_t bb = b0; bb < b1; bb += kBatch) {
-        fetch(bb);
+    for (int a = 0; a < kScanSums; ++a) {
 #pragma unroll
-        for (uint32_t j = 0; j < kBatch; ++j) {
-            const uint32_t b = bb + j;  // past b1: m = 0 and n = 0, which add nothing
-            const uint32_t m = mv[j];
-            pairs += m;
-            const uint32_t n = nv[j], sp = unit_splits(n);
-            if (b < nlist) {
-                const uint32_t u = (m + van_batch - 1) / van_batch;
-                units += u * sp;
-                van_units += u * sp;
-                vbytes += (unsigned long long)u * n * bpv;  // one pass per vanguard unit
-                vvec += (unsigned long long)m * n;
-            } else {
-                const uint32_t u = (m + batch_q - 1) / batch_q;
-                units += u * sp;
-                bytes += (unsigned long long)u * n * bpv;
-                fu += u;
-                vec += (unsigned long long)m * n;
-            }
-        }
-    }
-    // inclusive scans over the block: within each wave by shuffles, then the totals of the
-    // waves before (one barrier)
-    const int lane = t & 63, wave = t >> 6;
-    unsigned long long v[8] = {pairs, units, van_units, bytes, fu, vec, vbytes, vvec};
-#pragma unroll
-    for (int a = 0; a < 8; ++a) {
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const unsigned long long y = __shfl_up(v[a], o);
-            if (lane >= o)
-                v[a] += y;
-        }
-        if (lane == 63)
-            s_tot[a][wave] = v[a];
+        for (int o = 32; o > 0; o >>= 1)
+            v[a] += __shfl_xor(v[a], o);
+        if (lane == 0)
+            s_w[a][wave] = v[a];
     }
     __syncthreads();
-#pragma unroll
-    for (int a = 0; a < 8; ++a)
-        for (int w = 0; w < wave; ++w)
-            v[a] += s_tot[a][w];
-    uint32_t po = (uint32_t)v[0] - pairs, uo = (uint32_t)v[1] - units;
-    for (uint32_t bb = b0; bb < b1; bb += kBatch) {
-        fetch(bb);
-#pragma unroll
-        for (uint32_t j = 0; j < kBatch; ++j) {
-            const uint32_t b = bb + j;
-            const uint32_t m = mv[j];
-            if (b < b1) {
-                bucket_offset[b] = po;
-                unit_offset[b] = uo;
-            }
-            po += m;
-            const uint32_t sp = unit_splits(nv[j]);
-            uo += (b < nlist ? (m + van_batch - 1) / van_batch : (m + batch_q - 1) / batch_q) * sp;
+    if (t < (uint32_t)kScanSums) {
+        unsigned long long x = 0;
+        for (int w = 0; w < kScanWaves; ++w)
+            x += s_w[t][w];
+        block_tot[(size_t)t * gridDim.x + blockIdx.x] = x;
+    }
+}
+
+__global__ __launch_bounds__(kScanBlock) void bucket_scan_kernel(
+    uint32_t *count /*cleared after it is read*/, const ClusterMeta *__restrict__ meta, uint32_t nlist,
+    uint32_t batch_q, uint32_t van_batch, uint32_t bpv, const unsigned long long *__restrict__ block_tot,
+    uint32_t *__restrict__ cursor, uint32_t *__restrict__ bucket_offset, uint32_t *__restrict__ unit_offset, uint32_t *__restrict__ num_units,
+    unsigned long long *__restrict__ stats) {
+    __shared__ uint32_t s_w[2][kScanWaves];
+    __shared__ unsigned long long s_pre[2];
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6, nb = 2 * nlist;
+    const uint32_t b = blockIdx.x * kScanBlock + t;
+    const uint32_t nblk = gridDim.x;
+    // offsets of this block's first bucket: the totals of the blocks before it
+    if (t < 2) {
+        unsigned long long x = 0;
+        for (uint32_t w = 0; w < blockIdx.x; ++w)
+            x += block_tot[(size_t)t * nblk + w];
+        s_pre[t] = x;
+    }
+    // the last block also writes the grand totals
+    if (blockIdx.x == nblk - 1 && t >= 64 && t < 64 + (uint32_t)kScanSums) {
+        const uint32_t a = t - 64;
+        unsigned long long x = 0;
+        for (uint32_t w = 0; w < nblk; ++w)
+            x += block_tot[(size_t)a * nblk + w];
+        switch (a) {
+        case 0: bucket_offset[nb] = (uint32_t)x; break;
+        case 1: unit_offset[nb] = (uint32_t)x; break;
+        case 2: {
+            unsigned long long all = 0;
+            for (uint32_t w = 0; w < nblk; ++w)
+                all += block_tot[(size_t)1 * nblk + w];
+            num_units[0] = (uint32_t)x;
+            num_units[1] = (uint32_t)(all - x);
+            break;
+        }
+        case 3: stats[0] = x; break;
+        case 4: stats[1] = x; break;
+        case 5: stats[2] = x; break;
+        case 6: stats[9] = x; break;
+        default: stats[10] = x; break;
         }
     }
-    if (t == kScanThreads - 1) {
-        bucket_offset[nb] = (uint32_t)v[0];
-        unit_offset[nb] = (uint32_t)v[1];
-        num_units[0] = (uint32_t)v[2];
-        num_units[1] = (uint32_t)(v[1] - v[2]);
-        stats[0] = v[3];
-        stats[1] = v[4];
-        stats[2] = v[5];
-        stats[9] = v[6];
-        stats[10] = v[7];
+    unsigned long long v[kScanSums];
+    bucket_terms(b, nb, count, meta, nlist, batch_q, van_batch, bpv, v);
+    // inclusive scans of pairs and units within the wave, then the waves before
+    uint32_t inc[2] = {(uint32_t)v[0], (uint32_t)v[1]};
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(inc[a], o);
+            if (lane >= (uint32_t)o)
+                inc[a] += y;
+        }
+        if (lane == 63)
+            s_w[a][wave] = inc[a];
     }
+    __syncthreads();
+    if (b >= nb)
+        return;
+    uint32_t off[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        uint32_t x = (uint32_t)s_pre[a] + inc[a] - (uint32_t)v[a];
+        for (uint32_t w = 0; w < wave; ++w)
+            x += s_w[a][w];
+        off[a] = x;
+    }
+    bucket_offset[b] = off[0];
+    unit_offset[b] = off[1];
+    cursor[b] = 0u;
+    count[b] = 0u;  // read above (bucket_terms) and by the totals kernel before
 }
 
 __global__ void scatter_pairs_kernel(const int32_t *__restrict__ probe_idx, uint32_t nq,
@@ -240,6 +265,10 @@ __global__ void build_units_kernel(const uint32_t *__restrict__ bucket_offset,
 
 }  // namespace
 
+size_t bucket_scan_words(uint32_t nlist) {
+    return (size_t)kScanSums * ((2 * (size_t)nlist + kScanBlock - 1) / kScanBlock);
+}
+
 void launch_fill_u32(uint32_t *p, uint32_t value, size_t n, hipStream_t s) {
     if (!n)
         return;
@@ -260,10 +289,10 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
                         uint32_t *bucket_cursor,
                         uint32_t *bucket_offset, uint32_t *unit_offset, Pair *pairs, Unit *units,
                         uint64_t max_units, uint32_t *num_units, unsigned long long *scan_stats,
-                        hipStream_t s) {
+                        unsigned long long *block_tot, bool counts_zero, hipStream_t s) {
     const size_t np = (size_t)nq * nprobe;
-    launch_fill_u32(bucket_count, 0, 2 * (size_t)nlist, s);
-    launch_fill_u32(bucket_cursor, 0, 2 * (size_t)nlist, s);
+    if (!counts_zero)
+        launch_fill_u32(bucket_count, 0, 2 * (size_t)nlist, s);
     const uint32_t grid = (uint32_t)((np + 255) / 256);
     const bool lds = 2 * (size_t)nlist <= kLdsBuckets;
     const uint32_t hgrid = (uint32_t)((np + kHistPairs - 1) / kHistPairs);
@@ -282,9 +311,13 @@ void launch_build_pairs(const int32_t *probe_idx, const ClusterMeta *meta, uint3
                                                                   bucket_count);
     else
         count_pairs_kernel<<<grid, 256, 0, s>>>(probe_idx, nq, nprobe, nlist, vanguard, bucket_count);
-    scan_buckets_kernel<<<1, kScanThreads, 0, s>>>(bucket_count, meta, nlist, batch_q, van_batch,
-                                                   bytes_per_vector, bucket_offset, unit_offset,
-                                                   num_units, scan_stats);
+    const uint32_t sgrid = (2 * nlist + kScanBlock - 1) / kScanBlock;
+    bucket_totals_kernel<<<sgrid, kScanBlock, 0, s>>>(bucket_count, meta, nlist, batch_q, van_batch,
+                                                      bytes_per_vector, block_tot);
+    bucket_scan_kernel<<<sgrid, kScanBlock, 0, s>>>(bucket_count, meta, nlist, batch_q, van_batch,
+                                                    bytes_per_vector, block_tot, bucket_cursor,
+                                                    bucket_offset, unit_offset,
+                                                    num_units, scan_stats);
     if (lds)
         scatter_pairs_lds_kernel<<<hgrid, kHistThreads, hbytes, s>>>(probe_idx, np, nprobe, nlist, vanguard,
                                                                     bucket_offset, bucket_cursor, pairs);

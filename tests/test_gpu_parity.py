@@ -1111,16 +1111,18 @@ def test_recall_at_least_reference_cpu_path(n, dim, n_centers, nlist, nq, metric
     eng.close()
 
 
-@pytest.mark.parametrize("dim,metric", [(128, 0), (768, 1)])
-def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, tmp_path):
-    """Pair scheduling at nlist 16,384 (the 10M/20M configurations' nlist: global-atomic
-    bucket counting) and the scan statistics the benchmark's roofline is computed from:
-    the scheduled pairs are exactly the probe lists, vanguard pairs first; the far-pass
-    bytes are sum over clusters of ceil(m_c / unit) * n_c * (P/8 + 12), the vanguard bytes
-    ceil(m_c / 16) * n_c * (P/8 + 12) for the vanguard lows pass and 4 m_c n_c plus the
-    refined vectors' (P + 8) for the per-query vanguard pass."""
-    rng = np.random.default_rng(dim)
-    nlist, n, nq, nprobe, vanguard = 16384, 40000, 192, 32, 5
+@pytest.mark.parametrize("dim,metric,nlist", [(128, 0, 16384), (768, 1, 16384), (128, 0, 40000)])
+def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, nlist, tmp_path):
+    """Pair scheduling at nlist 16,384 (the 10M/20M configurations' nlist: LDS bucket
+    histograms) and 40,000 (global-atomic bucket counting, a bucket scan over 79 workgroups)
+    and the scan statistics the benchmark's roofline is computed from: the scheduled pairs
+    are exactly the probe lists, vanguard pairs first; the far-pass bytes are sum over
+    clusters of ceil(m_c / unit) * n_c * (P/8 + 12), the vanguard bytes ceil(m_c / 16) * n_c *
+    (P/8 + 12) for the vanguard lows pass and 4 m_c n_c plus the refined vectors' (P + 8)
+    for the per-query vanguard pass. A second, smaller search on the same engine checks that
+    the bucket counts and cursors the first one left behind were cleared."""
+    rng = np.random.default_rng(dim + nlist)
+    n, nq, nprobe, vanguard = 40000, 192, 32, 5
     cent = rng.normal(0, 1, (nlist, dim)).astype(np.float32)
     assign = rng.integers(0, nlist, n).astype(np.uint32)
     x = (cent[assign] + rng.normal(0, 0.3, (n, dim))).astype(np.float32)
@@ -1134,34 +1136,36 @@ def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, tmp_path):
                  (cent.astype(np.float64) @ R).astype(np.float32), assign, R, metric=metric)
     case = Case(path, q)
     P = case.file.padded_dim
-    say(f"[gpu] pair schedule + scan bytes, nlist={nlist} P={P}")
-    eng = make_engine(case, nprobe, 10, vanguard=vanguard, frozen=False, secondary=True,
-                      gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=ca.FLAG_VANGUARD_MFMA)
-    eng.reset_buffer(q)
-    eng.search(q, 10, nprobe)
-    st = eng.stats()
-    pidx = eng.debug_read(ca.DBG_PROBE_IDX, (nq, nprobe), np.int32)
-    pairs = eng.debug_read(ca.DBG_PAIRS, (nq * nprobe, 3), np.int32)
-    assert pidx.min() >= 0 and pidx.max() < nlist
-    # the scheduled pairs are the probe lists (as a multiset), vanguard pairs first
-    want = np.stack([pidx.reshape(-1), np.repeat(np.arange(nq), nprobe), np.tile(np.arange(nprobe), nq)], 1)
-    key = lambda a: np.lexsort((a[:, 2], a[:, 1], a[:, 0]))
-    assert np.array_equal(pairs[key(pairs)], want[key(want)])
-    nvan = nq * vanguard
-    assert np.all(pairs[:nvan, 2] < vanguard) and np.all(pairs[nvan:, 2] >= vanguard)
-    assert np.all(np.diff(pairs[nvan:, 0]) >= 0)  # far pairs grouped by cluster
     sizes = case.sd.cluster_sizes.astype(np.int64)
     bpv = P // 8 + 12
-    far_m = np.bincount(pidx[:, vanguard:].reshape(-1), minlength=nlist)
-    van_m = np.bincount(pidx[:, :vanguard].reshape(-1), minlength=nlist)
     unit = 16 if (P // 32) in (2, 4, 6, 8, 16, 24, 32) else 4  # matrix-core far scan, else batch-q 4
-    assert st["scan_vectors"] == int((far_m * sizes).sum())
-    assert st["scan_bytes"] == int((-(-far_m // unit) * sizes).sum()) * bpv
-    # the vanguard lows pass reads each cluster once per unit of up to 16 vanguard pairs; the
-    # per-query pass streams one 4-byte bound per (vector, pair), plus the refined vectors'
-    # sign code, ex-code and ex-factors
-    assert st["vanguard_lows_bytes"] == int((-(-van_m // 16) * sizes).sum()) * bpv
-    assert st["vanguard_bytes"] == 4 * int((van_m * sizes).sum()) + st["gpu_refined"] * (P + 8)
+    eng = make_engine(case, nprobe, 10, vanguard=vanguard, frozen=False, secondary=True,
+                      gpu_seed_refine=True, gpu_refine_filter=True, extra_flags=ca.FLAG_VANGUARD_MFMA)
+    for nqs in (nq, 77):
+        say(f"[gpu] pair schedule + scan bytes, nlist={nlist} P={P} nq={nqs}")
+        qs = np.ascontiguousarray(q[:nqs])
+        eng.reset_buffer(qs)
+        eng.search(qs, 10, nprobe)
+        st = eng.stats()
+        pidx = eng.debug_read(ca.DBG_PROBE_IDX, (nqs, nprobe), np.int32)
+        pairs = eng.debug_read(ca.DBG_PAIRS, (nqs * nprobe, 3), np.int32)
+        assert pidx.min() >= 0 and pidx.max() < nlist
+        # the scheduled pairs are the probe lists (as a multiset), vanguard pairs first
+        want = np.stack([pidx.reshape(-1), np.repeat(np.arange(nqs), nprobe), np.tile(np.arange(nprobe), nqs)], 1)
+        key = lambda a: np.lexsort((a[:, 2], a[:, 1], a[:, 0]))
+        assert np.array_equal(pairs[key(pairs)], want[key(want)])
+        nvan = nqs * vanguard
+        assert np.all(pairs[:nvan, 2] < vanguard) and np.all(pairs[nvan:, 2] >= vanguard)
+        assert np.all(np.diff(pairs[nvan:, 0]) >= 0)  # far pairs grouped by cluster
+        far_m = np.bincount(pidx[:, vanguard:].reshape(-1), minlength=nlist)
+        van_m = np.bincount(pidx[:, :vanguard].reshape(-1), minlength=nlist)
+        assert st["scan_vectors"] == int((far_m * sizes).sum())
+        assert st["scan_bytes"] == int((-(-far_m // unit) * sizes).sum()) * bpv
+        # the vanguard lows pass reads each cluster once per unit of up to 16 vanguard pairs;
+        # the per-query pass streams one 4-byte bound per (vector, pair), plus the refined
+        # vectors' sign code, ex-code and ex-factors
+        assert st["vanguard_lows_bytes"] == int((-(-van_m // 16) * sizes).sum()) * bpv
+        assert st["vanguard_bytes"] == 4 * int((van_m * sizes).sum()) + st["gpu_refined"] * (P + 8)
     eng.close()
 
 
