@@ -158,7 +158,8 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
-                                   "(query sharding design in DESIGN.md)", "n_gpus": args.gpus}))
+                                   "(N GPUs would each hold the whole index and search 1/N of the queries)",
+                          "n_gpus": args.gpus}))
         sys.exit(2)
 
     import coraanns_amd as ca
