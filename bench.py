@@ -85,18 +85,74 @@ def cpu_baseline(index_path, queries, gt, topk, nprobe, threads, workdir, sample
                       f"{', numactl --interleave=all' if numactl else ' (no numactl on this host)'}"}
 
 
-def hbm_traffic(cfg, nprobe, kernel):
+def hbm_traffic(run, kernel):
     """HBM bytes per launch of the kernel (FETCH_SIZE + WRITE_SIZE, each scaled by the
-    reading of a 1 GiB copy) from the committed rocprofv3 summary of this workload, or
-    None when there is none."""
-    f = REPO / "profiles" / f"hbm_traffic_cfg{cfg}_nprobe{nprobe}.json"
-    if not f.exists():
-        return None
-    data = json.loads(f.read_text())
-    for name, v in data.get("kernels", {}).items():
-        if v.get("role") == kernel:
-            return int(v["fetch_bytes"] + v["write_bytes"])
+    reading of a 1 GiB copy) from the committed rocprofv3 summary whose "match" block names
+    exactly this run's workload and mode (config, nprobe, top-k, batch-q, estimator, GPU-final
+    top-k, vanguard mode), or None when no summary matches."""
+    for f in sorted((REPO / "profiles").glob("hbm_traffic_*.json")):
+        data = json.loads(f.read_text())
+        if data.get("match") != run:
+            continue
+        for v in data.get("kernels", {}).values():
+            if v.get("role") == kernel:
+                return int(v["fetch_bytes"] + v["write_bytes"])
     return None
+
+
+def extra_lines(eng, eng_cfg, queries, gt, c, nprobe, args, traffic_key):
+    """Two further measurements on the resident index at the headline nprobe, each 1 warmup +
+    args.extra_steps timed searches:
+    - scan_q1: the RaBitQ popcount scan at Q = 1 (cross-query reuse off, every far
+      (query, probe) pair a unit of its own), its HIP-event time and algorithmic bytes
+      sum n_c (P/8 + 12) over the units, against the HBM peak;
+    - reference_structure: the reference's structure, GPU filter -> ring -> CPU refinement of
+      every candidate (GPU seed thresholds and GPU refined pre-filter off), its QPS and recall.
+    The engine is configured back to eng_cfg afterwards."""
+    import coraanns_amd as ca  # noqa: F401  (loaded by main)
+
+    def timed(cfg, batch_q):
+        eng.configure(**cfg)
+        rows = []
+        for it in range(1 + args.extra_steps):
+            t0 = time.perf_counter()
+            eng.reset_buffer(queries)
+            _, ids = eng.search(queries, c.topk, nprobe, batch_q)
+            dt = time.perf_counter() - t0
+            if it:
+                rows.append((dt, ids, eng.stats()))
+        return rows
+
+    out = {}
+    W = c.padded_dim // 32
+    rows = timed(dict(eng_cfg, cross_query_reuse=False), 1)
+    ms = float(np.mean([st["scan_ms"] for _, _, st in rows]))
+    nbytes = float(np.mean([st["scan_bytes"] for _, _, st in rows]))
+    ach = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+    key = dict(traffic_key, batch_q=1, mode="scan_q1")
+    out["scan_q1"] = {"kernel": f"scan_kernel<{W}, 1, 0, {1 if args.ip_kernel == 'lut4' else 0}> "
+                                "(far-pair RaBitQ scan, one (query, probe) pair per unit, cross-query reuse off)",
+                      "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                      "frac": round(ach / HBM_PEAK_GBPS, 4), "bytes_per_launch": int(nbytes),
+                      "avg_launch_ms": round(ms, 4), "traffic": hbm_traffic(key, "scan_q1"),
+                      "recall_at_10": round(float(np.mean([recall_at_k(i, gt, 10) for _, i, _ in rows])), 4),
+                      "qps": round(queries.shape[0] * len(rows) / sum(dt for dt, _, _ in rows), 1)}
+    log(f"[scan_q1] nprobe={nprobe} scan {ms:.3f}ms {nbytes / 1e6:.1f}MB -> {ach:.1f} GB/s "
+        f"({ach / HBM_PEAK_GBPS:.3f} of peak)")
+    rows = timed(dict(eng_cfg, gpu_seed_refine=False, gpu_refine_filter=False, gpu_final_topk=False),
+                 args.batch_q or c.batch_q)
+    qps = queries.shape[0] * len(rows) / sum(dt for dt, _, _ in rows)
+    out["reference_structure"] = {
+        "what": "GPU filter -> ring -> CPU refinement of every candidate (--no-gpu-seed --no-gpu-prefilter), "
+                "the reference's structure, same index, queries, nprobe and batch-q",
+        "qps": round(qps, 1), "ms_per_step": round(1000.0 * sum(dt for dt, _, _ in rows) / len(rows), 3),
+        "recall_at_10": round(float(np.mean([recall_at_k(i, gt, 10) for _, i, _ in rows])), 4),
+        f"recall_at_{c.topk}": round(float(np.mean([recall_at_k(i, gt, c.topk) for _, i, _ in rows])), 4),
+        "candidates_per_query": round(float(np.mean([st["submitted"] for _, _, st in rows])) / queries.shape[0], 1)}
+    log(f"[reference_structure] nprobe={nprobe} QPS={qps:.1f} "
+        f"recall@10={out['reference_structure']['recall_at_10']:.4f}")
+    eng.configure(**eng_cfg)
+    return out
 
 
 def copy_calibration():
@@ -140,6 +196,11 @@ def main():
                     help="GPU-final top-k: the GPU forms the final top-k from its refined distances, no CPU refinement")
     ap.add_argument("--no-vanguard-mfma", action="store_true",
                     help="vanguard lower bounds inside the per-query pass instead of the matrix-core lows pass")
+    ap.add_argument("--vanguard-one-pass", action="store_true",
+                    help="after the lows pass, run the vanguard pairs in the one per-query kernel instead of the "
+                         "staged pass (per-query select and merge around grid-wide refinement)")
+    ap.add_argument("--vanguard-mfma", action="store_true",
+                    help="run the matrix-core vanguard lows pass whatever the index size and dimension")
     ap.add_argument("--ip-kernel", choices=["bitwise", "lut4"], default="bitwise",
                     help="estimator: bitwise (Bq=8 popcount bound, the default here) or lut4 (the reference's "
                          "FP16 nibble-LUT estimator, set_ip_kernel_type(Lut4Bit))")
@@ -150,6 +211,9 @@ def main():
                     help="query rotation and coarse-probe distances from the FP32 matrix-core GEMMs instead of the split-FP16 ones")
     ap.add_argument("--workdir", default="",
                     help="keep the built index and ground truth in this directory and reuse them")
+    ap.add_argument("--no-extra-lines", action="store_true",
+                    help="configs 4 and 5: skip the Q=1 scan roofline and the reference-structure line")
+    ap.add_argument("--extra-steps", type=int, default=3, help="timed steps of each extra line (after 1 warmup)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (PMC byte-count calibration)")
     args = ap.parse_args()
@@ -202,15 +266,18 @@ def main():
 
     ivf = ca.IvfIndex(index_path)
     vanguard = c.vanguard if args.vanguard < 0 else args.vanguard
-    eng = ca.HybridIndex(0, vanguard_size=vanguard, cpu_secondary_filter=c.secondary_filter,
-                         cross_query_reuse=True, gpu_filter_timing=True, metric=c.metric,
-                         cpu_threads=threads, gpu_seed_refine=not args.no_gpu_seed,
-                         gpu_refine_filter=not args.no_gpu_prefilter,
-                         extra_flags=(ca.FLAG_FP32_GEMM if args.fp32_gemm else 0) |
-                                     (ca.FLAG_NO_VANGUARD_MFMA if args.no_vanguard_mfma else 0) |
-                                     (ca.FLAG_UNFUSED_PROBE if args.unfused_probe else 0),
-                         lower_bound_scale=args.lower_bound_scale or None, gpu_final_topk=args.gpu_final,
-                         ip_kernel_type=args.ip_kernel)
+    eng_cfg = dict(vanguard_size=vanguard, cpu_secondary_filter=c.secondary_filter,
+                   cross_query_reuse=True, gpu_filter_timing=True, metric=c.metric,
+                   cpu_threads=threads, gpu_seed_refine=not args.no_gpu_seed,
+                   gpu_refine_filter=not args.no_gpu_prefilter,
+                   extra_flags=(ca.FLAG_FP32_GEMM if args.fp32_gemm else 0) |
+                               (ca.FLAG_NO_VANGUARD_MFMA if args.no_vanguard_mfma else 0) |
+                               (ca.FLAG_VANGUARD_MFMA if args.vanguard_mfma else 0) |
+                               (ca.FLAG_VANGUARD_ONE_PASS if args.vanguard_one_pass else 0) |
+                               (ca.FLAG_UNFUSED_PROBE if args.unfused_probe else 0),
+                   lower_bound_scale=args.lower_bound_scale or None, gpu_final_topk=args.gpu_final,
+                   ip_kernel_type=args.ip_kernel)
+    eng = ca.HybridIndex(0, **eng_cfg)
     eng.load_ivf(ivf)
     chunk = min(queries.shape[0], 65535)
     eng.prepare_workspace(chunk, c.topk, max(c.nprobes))
@@ -257,7 +324,8 @@ def main():
     times, times_search, scan_ms, scan_bytes, recalls, probe_ms, probe_flops = [], [], [], [], [], [], []
     select_ms = []
     recalls_k = []
-    van_ms, van_bytes, lows_ms, lows_bytes = [], [], [], []
+    van_ms, van_bytes, lows_ms, lows_bytes, ref_ms, ref_bytes, van_modes = [], [], [], [], [], [], []
+    staged_counts = []
     last_ids = None
     for _ in range(args.steps):
         dt, ids, st = step(nprobe)
@@ -273,6 +341,13 @@ def main():
         van_bytes.append(st["vanguard_bytes"])
         lows_ms.append(st["vanguard_lows_ms"])
         lows_bytes.append(st["vanguard_lows_bytes"])
+        ref_ms.append(st["vanguard_refine_ms"])
+        ref_bytes.append(st["vanguard_refine_bytes"])
+        van_modes.append(st["vanguard_mode"])
+        if st["vanguard_mode"] == 4 and not staged_counts:
+            staged_counts.extend(int(x) for x in eng.debug_read(ca.DBG_STAGED_COUNTS, (4,), np.uint64))
+            log(f"[staged] seeds {staged_counts[0]}, list {staged_counts[1]}, lists from a second pass "
+                f"{staged_counts[2]}, queries left to the one-pass kernel {staged_counts[3]}")
         recalls.append(recall_at_k(ids, gt, 10))
         recalls_k.append(recall_at_k(ids, gt, c.topk))
     total = sum(times)
@@ -287,6 +362,10 @@ def main():
     avg_lows_ms = float(np.mean(lows_ms))
     lows_bpl = float(np.mean(lows_bytes))
     lows_achieved = lows_bpl / (avg_lows_ms * 1e-3) / 1e9 if avg_lows_ms > 0 else 0.0
+    avg_ref_ms = float(np.mean(ref_ms))
+    ref_bpl = float(np.mean(ref_bytes))
+    ref_achieved = ref_bpl / (avg_ref_ms * 1e-3) / 1e9 if avg_ref_ms > 0 else 0.0
+    staged = avg_ref_ms > 0
     avg_probe_ms = float(np.mean(probe_ms))
     probe_tflops = float(np.mean(probe_flops)) / (avg_probe_ms * 1e-3) / 1e12 if avg_probe_ms > 0 else 0.0
     if args.fp32_gemm:
@@ -307,7 +386,9 @@ def main():
     probe_line["select_and_gadd_ms"] = round(float(np.mean(select_ms)), 4)
     log(f"[timed] nprobe={nprobe} steps={args.steps} QPS={qps:.1f} recall={np.mean(recalls):.4f} "
         f"vanguard lows={avg_lows_ms:.3f}ms {lows_bpl / 1e6:.1f}MB -> {lows_achieved:.1f} GB/s; "
-        f"vanguard={avg_van_ms:.3f}ms {van_bpl / 1e6:.1f}MB -> {van_achieved:.1f} GB/s; "
+        f"vanguard={avg_van_ms:.3f}ms {van_bpl / 1e6:.1f}MB -> {van_achieved:.1f} GB/s "
+        f"(mode {van_modes[-1] if van_modes else 0}; refinement {avg_ref_ms:.3f}ms {ref_bpl / 1e6:.1f}MB -> "
+        f"{ref_achieved:.1f} GB/s); "
         f"far scan={avg_scan_ms:.3f}ms {bytes_per_launch / 1e6:.1f}MB -> {achieved:.1f} GB/s; "
         f"probe GEMM {avg_probe_ms:.3f}ms -> {probe_tflops:.2f} TFLOP/s; "
         f"probe select + g_add {float(np.mean(select_ms)):.3f}ms")
@@ -327,6 +408,10 @@ def main():
                       f"vanguard pass: {'streamed lower bounds' if avg_lows_ms > 0 else 'popcount lower bounds'}, "
                       "GPU refinement, top-k threshold)",
             "avg_launch_ms": round(avg_van_ms, 4), "bytes_per_launch": int(van_bpl), "achieved": van_achieved},
+        "vs_refine_kernel": {
+            "kernel": f"vs_refine_kernel<{W}> (staged vanguard pass: grid-wide refinement of the seeds and of the "
+                      "candidate list, two launches; time and bytes are their sum)",
+            "avg_launch_ms": round(avg_ref_ms, 4), "bytes_per_launch": int(ref_bpl), "achieved": ref_achieved},
         "vanguard_lows": {
             "kernel": f"{lows_name} (vanguard lower bounds on the matrix cores, cluster-major, units of 16 "
                       "same-cluster pairs)",
@@ -338,13 +423,30 @@ def main():
             "avg_launch_ms": round(avg_scan_ms, 4), "bytes_per_launch": int(bytes_per_launch),
             "achieved": achieved},
     }
+    if staged:
+        # the staged pass is five kernels: its whole time and bytes are reported beside the
+        # kernels, and its refinement kernel competes for the dominant one
+        staged_pass = dict(kernels.pop("vanguard_query_kernel"))
+        staged_pass["kernel"] = (f"staged vanguard pass (vs_seed_kernel, vs_refine_kernel<{W}> x2, vs_list_kernel, "
+                                 "vs_merge_kernel): streamed lower bounds, GPU refinement, top-k threshold")
+    else:
+        kernels.pop("vs_refine_kernel")
     dom = max(kernels, key=lambda k: kernels[k]["avg_launch_ms"])
+    # the counter profile applies to exactly this workload and mode
+    traffic_key = {"config": args.config, "nprobe": nprobe, "topk": c.topk, "batch_q": batch_q,
+                   "ip_kernel": args.ip_kernel, "gpu_final": bool(args.gpu_final),
+                   "vanguard_mode": int(van_modes[-1]) if van_modes else 0}
     d = kernels[dom]
     roofline = {"bound": "hbm", "achieved": round(d["achieved"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(d["achieved"] / HBM_PEAK_GBPS, 4),
-                "traffic": hbm_traffic(args.config, nprobe, dom), "kernel": d["kernel"],
+                "traffic": hbm_traffic(traffic_key, dom), "kernel": d["kernel"],
                 "bytes_per_launch": d["bytes_per_launch"], "avg_launch_ms": d["avg_launch_ms"],
-                "other": [dict(v, achieved=round(v["achieved"], 1)) for k, v in kernels.items() if k != dom]}
+                "other": [dict(v, achieved=round(v["achieved"], 1)) for k, v in kernels.items() if k != dom] +
+                         ([dict(staged_pass, achieved=round(staged_pass["achieved"], 1))] if staged else [])}
+
+    extra = {}
+    if not args.no_extra_lines and c.cfg in (4, 5):
+        extra = extra_lines(eng, eng_cfg, queries, gt, c, nprobe, args, traffic_key)
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -376,12 +478,16 @@ def main():
                    "qps_search_only": round(queries.shape[0] * args.steps / sum(times_search), 1),
                    "step_ms": [round(1000.0 * t, 3) for t in times],
                    "batch_q": batch_q, "vanguard": vanguard, "cpu_secondary_filter": c.secondary_filter,
+                   "vanguard_mode": {0: "none", 1: "per-pair seed and recovery passes", 2: "fused per-query pass",
+                                     3: "lows pass + fused per-query pass",
+                                     4: "lows pass + staged pass"}.get(van_modes[-1] if van_modes else 0),
                    "lower_bound_scale": eng.lower_bound_scale, "gpu_final_topk": args.gpu_final,
                    "ip_kernel_type": args.ip_kernel,
                    "cpu_refine_threads": threads, "cpu_refine_isa": f"avx{ca.cpu_refine_isa()}",
                    "gpu_seed_thresholds": not args.no_gpu_seed, "gpu_refined_prefilter": not args.no_gpu_prefilter,
                    "query_chunk": chunk, "sweep": sweep},
         "roofline": roofline,
+        **extra,
         "probe_mfma": probe_line,
         "cpu_baseline": baseline,
     }

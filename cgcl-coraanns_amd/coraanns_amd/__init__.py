@@ -39,6 +39,7 @@ DBG_ROTATED_QUERIES, DBG_K1XSUMQ, DBG_KBXSUMQ, DBG_Q_WIDTH, DBG_Q_PLANES = range
 DBG_PROBE_IDX, DBG_PROBE_GADD, DBG_PROBE_GERR, DBG_PAIRS, DBG_Q_WIDTH2 = range(5, 10)
 DBG_SEED_DIST, DBG_THRESHOLDS, DBG_PROBE_DIST, DBG_VANGUARD_LOWS, DBG_LUT = 10, 11, 12, 13, 14
 DBG_PROBE_FALLBACK = 15
+DBG_STAGED_COUNTS = 16
 FLAG_NO_GPU_SEED, FLAG_GPU_SEED_FROZEN, FLAG_NO_GPU_PREFILTER = 1 << 3, 1 << 4, 1 << 5
 FLAG_PAIR_SEEDS = 1 << 6
 FLAG_NO_MFMA_SCAN = 1 << 7
@@ -48,6 +49,7 @@ FLAG_VANGUARD_MFMA = 1 << 10
 FLAG_GPU_FINAL = 1 << 11
 FLAG_LUT4 = 1 << 12
 FLAG_UNFUSED_PROBE = 1 << 13
+FLAG_VANGUARD_ONE_PASS = 1 << 14
 KERNEL_TYPES = {None: 0, "lut4": 1, "bitwise": 2}
 
 
@@ -92,7 +94,8 @@ class cora_search_stats(C.Structure):
                 ("prefilter_dropped", C.c_uint64), ("seed_ms", C.c_float), ("recovery_ms", C.c_float),
                 ("gpu_refined", C.c_uint64), ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64),
                 ("vanguard_lows_ms", C.c_float), ("vanguard_lows_bytes", C.c_uint64),
-                ("vanguard_mode", C.c_int32), ("phase_ms", C.c_float * 4)]
+                ("vanguard_mode", C.c_int32), ("phase_ms", C.c_float * 4),
+                ("vanguard_refine_ms", C.c_float), ("vanguard_refine_bytes", C.c_uint64)]
 
 
 class cora_queue_view(C.Structure):
@@ -119,7 +122,8 @@ class cora_hybrid_stats(C.Structure):
                 ("seed_ms", C.c_float), ("recovery_ms", C.c_float), ("gpu_refined", C.c_uint64),
                 ("vanguard_ms", C.c_float), ("vanguard_bytes", C.c_uint64),
                 ("vanguard_lows_ms", C.c_float), ("vanguard_lows_bytes", C.c_uint64),
-                ("vanguard_mode", C.c_int32), ("phase_ms", C.c_float * 4)]
+                ("vanguard_mode", C.c_int32), ("phase_ms", C.c_float * 4),
+                ("vanguard_refine_ms", C.c_float), ("vanguard_refine_bytes", C.c_uint64)]
 
 
 class cora_ivf_info(C.Structure):

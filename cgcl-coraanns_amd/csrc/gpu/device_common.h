@@ -153,30 +153,33 @@ __device__ __forceinline__ float two_stage_ip(float width, int ip, float width2,
 }
 
 // <q', ex_code> over one 8-dimension chunk c (group g = c / 8 of 64 dimensions, k = c % 8)
-// of a packed 7-bit ex-code (pack_excode.hpp:216-265): per 64 dimensions, bytes 0..47
-// hold the low six bits of dimensions 0..47, and in their top two bits the bit pairs of
-// dimensions 48..63 (bits 0-1 in bytes 0..15, 2-3 in 16..31, 4-5 in 32..47); the u64 at
-// bytes 48..55 holds bit 6 of dimension 8k+j at bit 8j+k. l1 accumulates sum |q'|.
-// kL1: also accumulate sum |q'| of the chunk into *l1. Unpacked in 32-bit halves (four
-// dimensions per word) so each code byte converts with one byte-to-float instruction.
+// of a packed 7-bit ex-code (pack_excode.hpp:216-265) in a refinement record (rec, padded
+// dimension P; engine_internal.h): per 64 dimensions, bytes 0..47 hold the low six bits of
+// dimensions 0..47, and in their top two bits the bit pairs of dimensions 48..63 (bits 0-1
+// in bytes 0..15, 2-3 in 16..31, 4-5 in 32..47); the u64 at bytes 48..55 holds bit 6 of
+// dimension 8k+j at bit 8j+k. kL1: also accumulate sum |q'| of the chunk into *l1. Unpacked in
+// 32-bit halves (four dimensions per word) so each code byte converts with one byte-to-float
+// instruction.
 template <bool kL1 = true>
-__device__ __forceinline__ float excode_chunk_ip(const uint8_t *__restrict__ code,
+__device__ __forceinline__ float excode_chunk_ip(const uint8_t *__restrict__ rec, uint32_t P,
                                                  const float *__restrict__ q, uint32_t c,
                                                  float *l1 = nullptr) {
     const uint32_t g = c >> 3, k = c & 7;
-    const uint2 *grp = reinterpret_cast<const uint2 *>(code + (size_t)g * 56);
+    const auto word = [&](uint32_t kk) {
+        return *reinterpret_cast<const uint2 *>(rec + ex_record_group_word(P, g, kk));
+    };
     uint32_t lo, hi;
     if (k < 6) {
-        const uint2 v = grp[k];
+        const uint2 v = word(k);
         lo = v.x & 0x3F3F3F3Fu;
         hi = v.y & 0x3F3F3F3Fu;
     } else {
         const uint32_t o = k - 6;
-        const uint2 a = grp[o], b = grp[2 + o], d = grp[4 + o];
+        const uint2 a = word(o), b = word(2 + o), d = word(4 + o);
         lo = ((a.x >> 6) & 0x03030303u) | ((b.x >> 4) & 0x0C0C0C0Cu) | ((d.x >> 2) & 0x30303030u);
         hi = ((a.y >> 6) & 0x03030303u) | ((b.y >> 4) & 0x0C0C0C0Cu) | ((d.y >> 2) & 0x30303030u);
     }
-    const uint2 top = grp[6];
+    const uint2 top = word(6);
     lo |= ((top.x >> k) & 0x01010101u) << 6;
     hi |= ((top.y >> k) & 0x01010101u) << 6;
     const float4 q0 = *reinterpret_cast<const float4 *>(q + 64 * g + 8 * k);
@@ -228,6 +231,30 @@ __device__ __forceinline__ float excode_group_ip(const uint2 (&grp)[7], const fl
     return sum;
 }
 
+// The slice of 64-dimension group g of a refinement record (engine_internal.h) in 16 words:
+// words 0..13 the group's seven 8-byte ex-code words, words 14 and 15 sign-code words 2g and
+// 2g + 1. Loaded as four 16-byte chunks; the lanes that load the slices of the G groups of
+// one vector read 16 G contiguous bytes per load.
+struct GroupSlice {
+    uint32_t d[16];
+    __device__ __forceinline__ void load(const uint8_t *rec, uint32_t G, uint32_t g) {
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+            const uint4 v = gload<uint4>(rec + 16 * (G * k + g));
+            d[4 * k] = v.x;
+            d[4 * k + 1] = v.y;
+            d[4 * k + 2] = v.z;
+            d[4 * k + 3] = v.w;
+        }
+    }
+    __device__ __forceinline__ void group(uint2 (&w)[7]) const {
+#pragma unroll
+        for (int k = 0; k < 7; ++k)
+            w[k] = make_uint2(d[2 * k], d[2 * k + 1]);
+    }
+    __device__ __forceinline__ uint32_t sign_word(int e) const { return d[14 + e]; }
+};
+
 // Refined distance of a candidate (cpu_refinement.cpp:183-192) from the HBM copy of the
 // ex-codes, evaluated by one lane, and a bound on its rounding difference from the CPU
 // consumer's evaluation (1e-4 of the magnitude of the terms).
@@ -237,7 +264,7 @@ __device__ __forceinline__ float refine_one(const ScanParams &p, uint32_t query,
     const float *qv = p.qrot + (size_t)query * p.P;
     float ip = 0.0f, l1 = 0.0f;
     for (uint32_t c = 0; c < p.P / 8; ++c)
-        ip += excode_chunk_ip(code, qv, c, &l1);
+        ip += excode_chunk_ip(code, p.P, qv, c, &l1);
     const float2 f = *reinterpret_cast<const float2 *>(code + ex_record_factor_offset(p.P));
     const float fa = f.x, fr = f.y;
     const float gadd = p.pgadd[(size_t)query * p.nprobe + probe], kbq = p.kb[query];

@@ -2,6 +2,7 @@
 // the host-coherent GPU->CPU candidate ring and the launch sequence of
 // HybridIndex::search's GPU side (reference src/search/hybrid.cu:35-689).
 #include <float.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -19,6 +20,10 @@ namespace {
 constexpr unsigned long long kDrainMaxSeconds = 20;        // drain wait for the CPU consumer
 constexpr uint64_t kMaxQueryChunk = 65535;                  // parameters.hpp:12
 constexpr uint64_t kMaxProbeCount = 65536;                  // parameters.hpp:13
+// seeds per query the staged vanguard pass refines first: at least 128 and twice the top-k
+// (their cut is a rank among 512 sub-stream minima of the query's group minima)
+constexpr uint32_t kVsSeeds = 128;
+uint32_t vs_seed_target(uint32_t topk) { return std::min<uint32_t>(512, std::max<uint32_t>(kVsSeeds, 2 * topk)); }
 
 template <class T>
 void dfree(T *&p) {
@@ -64,6 +69,7 @@ struct cora_gpu_engine {
                ev_s0 = nullptr, ev_s1 = nullptr, ev_p0 = nullptr, ev_p1 = nullptr, ev_v0 = nullptr,
                ev_v1 = nullptr, ev_a0 = nullptr, ev_a1 = nullptr, ev_q0 = nullptr, ev_sched = nullptr,
                ev_done = nullptr;
+    hipEvent_t ev_r[4] = {};  // the staged vanguard pass's two refinement launches (timing)
     // index
     bool loaded = false;
     uint64_t N = 0, dim = 0, P = 0, nl = 0, ex_bits = 0, max_cluster = 0, total_tiles = 0;
@@ -98,6 +104,7 @@ struct cora_gpu_engine {
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
     uint4 *d_seed_rec = nullptr;
     float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
+    float *d_van_mins = nullptr;  // [max_q][vanguard][van_stride / 4] their group minima (staged pass)
     unsigned long long *d_selbig = nullptr;  // [max_q][2][max_nprobe] probe select scratch, nprobe > 4096
     uint32_t *d_probe_fb = nullptr;          // [1 + max_q] fused probe select: fallback count, rows
     // GPU-final top-k: per-query counts/offsets/cursor, grouped keys [spill_cap], results
@@ -105,6 +112,17 @@ struct cora_gpu_engine {
     unsigned long long *d_fkeys = nullptr;
     float *d_fdist = nullptr;
     uint64_t van_stride = 0;
+    // staged vanguard pass (vanguard_staged.hip): per-query regions of seeds, tier and list,
+    // per-query state, counters and the overflow list
+    uint32_t *d_vs_seed_pos = nullptr, *d_vs_list_pos = nullptr;
+    float2 *d_vs_seed_rd = nullptr, *d_vs_seed_aux = nullptr, *d_vs_list_rd = nullptr, *d_vs_list_aux = nullptr;
+    VsQuery *d_vs_qs = nullptr;
+    uint4 *d_vs_out = nullptr;
+    unsigned long long *d_vs_spread = nullptr;
+    uint32_t vs_out_cap = 0;
+    unsigned long long *d_vs_ctr = nullptr;
+    uint32_t *d_vs_ovf = nullptr;
+    uint32_t vs_seed_cap = 0, vs_list_cap = 0;
     Pair *d_pairs = nullptr;
     Unit *d_units = nullptr;
     unsigned long long *d_stats = nullptr;
@@ -129,6 +147,7 @@ struct cora_gpu_engine {
     cora_search_args last{};
     uint32_t last_depth = 0, last_batch = 1;
     bool last_timing = false, last_fused = false, last_mfma = false, last_van_lows = false, last_final = false;
+    bool last_staged = false;  // the vanguard pairs ran in the staged pass
     bool last_fused_probe = false;  // the last search selected its probes in the GEMM epilogue + merge
     int last_vanguard_mode = 0;  // cora_search_stats::vanguard_mode
 };
@@ -249,6 +268,19 @@ void release_workspace(cora_gpu_engine *E) {
     dfree(E->d_seed_err);
     dfree(E->d_seed_rec);
     dfree(E->d_van_lows);
+    dfree(E->d_van_mins);
+    dfree(E->d_vs_seed_pos);
+    dfree(E->d_vs_seed_rd);
+    dfree(E->d_vs_seed_aux);
+    dfree(E->d_vs_list_pos);
+    dfree(E->d_vs_list_rd);
+    dfree(E->d_vs_list_aux);
+    dfree(E->d_vs_qs);
+    dfree(E->d_vs_out);
+    dfree(E->d_vs_spread);
+    dfree(E->d_vs_ctr);
+    dfree(E->d_vs_ovf);
+    E->vs_seed_cap = E->vs_list_cap = 0;
     dfree(E->d_selbig);
     dfree(E->d_probe_fb);
     dfree(E->d_fcount);
@@ -352,6 +384,8 @@ int cora_gpu_create(cora_gpu_engine **out, int device) {
                                &E->ev_p0, &E->ev_p1, &E->ev_v0, &E->ev_v1, &E->ev_a0, &E->ev_a1, &E->ev_q0,
                                &E->ev_sched, &E->ev_done})
             HIPCHK(hipEventCreate(ev));
+        for (hipEvent_t &ev : E->ev_r)
+            HIPCHK(hipEventCreate(&ev));
         return CORA_OK;
     };
     const int rc = init();
@@ -394,7 +428,7 @@ int cora_gpu_destroy(cora_gpu_engine *E) {
         (void)hipStreamDestroy(E->stream_d2h);
     if (E->stream_h2d)
         (void)hipStreamDestroy(E->stream_h2d);
-    for (hipEvent_t ev : {E->ev_fork, E->ev_join})
+    for (hipEvent_t ev : {E->ev_fork, E->ev_join, E->ev_r[0], E->ev_r[1], E->ev_r[2], E->ev_r[3]})
         if (ev)
             (void)hipEventDestroy(ev);
     if (E->stream_aux)
@@ -653,6 +687,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
             // a multiple of 256: the fused pass streams a pair's bounds 256 at a time
             E->van_stride = (E->max_cluster + 255) / 256 * 256;
             TRY(dalloc(E, E->d_van_lows, max_q * depth * std::max<uint64_t>(E->van_stride, 1)));
+            TRY(dalloc(E, E->d_van_mins, max_q * depth * std::max<uint64_t>(E->van_stride / 4, 1)));
         }
         if (E->d_exrec) {
             TRY(dalloc(E, E->d_fcount, max_q));
@@ -661,6 +696,31 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
             TRY(dalloc(E, E->d_fidx, max_q * max_topk));
             TRY(dalloc(E, E->d_fdist, max_q * max_topk));
             TRY(dalloc(E, E->d_fkeys, std::max<uint64_t>(1, E->spill_cap)));
+            if (depth > 0 && vanguard_staged_supported(E->W)) {
+                // the staged vanguard pass: per query, room for about four times its seeds, and
+                // for the list sixteen times (at least 4,096); a query whose seeds or list do not
+                // fit is left to the one-pass kernel
+                const auto up256 = [](uint64_t x) { return (x + 255) / 256 * 256; };
+                const uint64_t seeds = vs_seed_target((uint32_t)max_topk);
+                uint64_t seed_cap = up256(4 * seeds), list_cap = std::max<uint64_t>(4096, up256(16 * seeds));
+                // CORA_VANGUARD_REGION_CAP: smaller regions (tests of the overflow path)
+                if (const char *env = getenv("CORA_VANGUARD_REGION_CAP"))
+                    seed_cap = list_cap = std::max<uint64_t>(64, strtoull(env, nullptr, 10));
+                E->vs_seed_cap = (uint32_t)seed_cap;
+                E->vs_list_cap = (uint32_t)list_cap;
+                TRY(dalloc(E, E->d_vs_seed_pos, max_q * seed_cap));
+                TRY(dalloc(E, E->d_vs_seed_rd, max_q * seed_cap));
+                TRY(dalloc(E, E->d_vs_seed_aux, max_q * seed_cap));
+                TRY(dalloc(E, E->d_vs_list_pos, max_q * list_cap));
+                TRY(dalloc(E, E->d_vs_list_rd, max_q * list_cap));
+                TRY(dalloc(E, E->d_vs_list_aux, max_q * list_cap));
+                TRY(dalloc(E, E->d_vs_qs, max_q));
+                E->vs_out_cap = (uint32_t)up256(std::max<uint64_t>(256, 4 * max_topk));
+                TRY(dalloc(E, E->d_vs_out, max_q * E->vs_out_cap));
+                TRY(dalloc(E, E->d_vs_spread, kVsSpread * kVsSpreadWords));
+                TRY(dalloc(E, E->d_vs_ctr, kVsCtrWords));
+                TRY(dalloc(E, E->d_vs_ovf, max_q));
+            }
             const uint64_t slots = max_q * depth * std::max<uint64_t>(max_topk, 20);
             TRY(dalloc(E, E->d_seed_dist, slots));
             TRY(dalloc(E, E->d_seed_low, slots));
@@ -837,10 +897,10 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         (!E->d_exrec || !E->d_fkeys ||
          (a->flags & (CORA_FLAG_NO_GPU_SEED | CORA_FLAG_NO_GPU_PREFILTER | CORA_FLAG_PAIR_SEEDS | CORA_FLAG_LUT4)) ||
          ((a->flags & CORA_FLAG_FROZEN_THRESHOLDS) && !(a->flags & CORA_FLAG_GPU_SEED_FROZEN)) ||
-         std::min<uint64_t>(a->vanguard, a->nprobe) > kVanguardMaxPairs || a->topk > kVanguardMaxTopk))
+         want_depth == 0 || want_depth > kVanguardMaxPairs || a->topk > kVanguardMaxTopk))
         return fail(E, CORA_ERR_LOGIC,
                     "GPU-final top-k needs the ex-codes in HBM, GPU seed thresholds and the refined "
-                    "pre-filter, the fused vanguard pass (vanguard <= 64, topk <= 128, Bitwise estimator) "
+                    "pre-filter, the fused vanguard pass (vanguard 1..64, topk <= 128, Bitwise estimator) "
                     "and live thresholds");
     HIPCHK(hipSetDevice(E->device));
     E->final_mode = want_final;
@@ -1022,9 +1082,13 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     p.prefilter = prefilter ? 1 : 0;
     p.dropped = E->d_stats + 7;
     VanguardArgs va{};
+    // the staged pass (grid-wide refinement) where the lows pass wrote every vanguard bound
+    const bool staged = van_lows && E->d_vs_seed_pos && !(a->flags & CORA_FLAG_VANGUARD_ONE_PASS);
+    p.van_mins = staged ? E->d_van_mins : nullptr;
     E->last_fused = fused && depth > 0;
     E->last_van_lows = van_lows;
-    E->last_vanguard_mode = depth == 0 ? 0 : !fused ? 1 : van_lows ? 3 : 2;
+    E->last_staged = staged;
+    E->last_vanguard_mode = depth == 0 ? 0 : !fused ? 1 : staged ? 4 : van_lows ? 3 : 2;
     if (fused) {
         va.probe_idx = E->d_pidx;
         va.nq = nq;
@@ -1056,7 +1120,30 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
         snapshot();
         if (timing)
             HIPCHK(hipEventRecord(E->ev_v0, s));
-        launch_vanguard_query(p, va, E->W, nq, s);
+        if (staged) {
+            VsArgs vs{};
+            vs.seed_pos = E->d_vs_seed_pos;
+            vs.seed_rd = E->d_vs_seed_rd;
+            vs.seed_aux = E->d_vs_seed_aux;
+            vs.list_pos = E->d_vs_list_pos;
+            vs.list_rd = E->d_vs_list_rd;
+            vs.list_aux = E->d_vs_list_aux;
+            vs.seed_cap = E->vs_seed_cap;
+            vs.list_cap = E->vs_list_cap;
+            vs.qs = E->d_vs_qs;
+            vs.out = E->d_vs_out;
+            vs.out_cap = E->vs_out_cap;
+            vs.spread = E->d_vs_spread;
+            vs.ctr = E->d_vs_ctr;
+            vs.overflow = E->d_vs_ovf;
+            vs.seeds = vs_seed_target(a->topk);
+            launch_fill_u64(E->d_vs_ctr, 0ull, kVsCtrWords, s);
+            launch_fill_u64(E->d_vs_spread, 0ull, kVsSpread * kVsSpreadWords, s);
+            launch_vanguard_staged(p, va, vs, E->W, nq, timing ? E->ev_r[0] : nullptr, timing ? E->ev_r[1] : nullptr,
+                                   timing ? E->ev_r[2] : nullptr, timing ? E->ev_r[3] : nullptr, s);
+        } else {
+            launch_vanguard_query(p, va, E->W, nq, s);
+        }
         if (timing)
             HIPCHK(hipEventRecord(E->ev_v1, s));
     } else if (depth > 0) {
@@ -1157,6 +1244,11 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     if (E->last_fused && E->last_van_lows) {
         out.vanguard_bytes = 4 * stats[10] + stats[8] * (E->P + 8);
         out.vanguard_lows_bytes = stats[9];
+        // staged pass: the refinement launches read each refined vector's record and its pool
+        // position and lower bound, and write its result (the one-pass kernel's overflow
+        // queries, refined inside that kernel, are counted here too)
+        if (E->last_staged)
+            out.vanguard_refine_bytes = stats[8] * (E->P + 8 + 24);
     } else if (E->last_fused) {
         out.vanguard_bytes = stats[9] + stats[8] * (E->P + 8);
     }
@@ -1182,6 +1274,12 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
         }
         if (E->last_fused && E->last_van_lows)
             HIPCHK(hipEventElapsedTime(&out.vanguard_lows_ms, E->ev_a0, E->ev_a1));
+        if (E->last_staged) {
+            float r1 = 0.0f, r2 = 0.0f;
+            HIPCHK(hipEventElapsedTime(&r1, E->ev_r[0], E->ev_r[1]));
+            HIPCHK(hipEventElapsedTime(&r2, E->ev_r[2], E->ev_r[3]));
+            out.vanguard_refine_ms = r1 + r2;
+        }
         // the reference's profile phases (hybrid.cu:434-516, 679-681); the last ends now,
         // after the host's refinement, as the reference's stop event does
         HIPCHK(hipEventRecord(E->ev_done, E->stream));
@@ -1321,6 +1419,12 @@ int cora_gpu_debug_read(cora_gpu_engine *E, int which, void *dst, uint64_t bytes
         }
         src = E->d_probe_fb;
         size = (1 + nq) * 4;
+        break;
+    case CORA_DBG_STAGED_COUNTS:
+        if (!E->last_staged)
+            return fail(E, CORA_ERR_LOGIC, "debug_read: the last search ran no staged vanguard pass");
+        src = E->d_vs_ctr;
+        size = 4 * sizeof(unsigned long long);
         break;
     case CORA_DBG_PAIRS: {
         if (bytes != nq * np * 12)

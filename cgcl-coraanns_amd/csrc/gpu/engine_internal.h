@@ -34,12 +34,30 @@ constexpr uint64_t kLowsMinIndexBytes = 256ull << 20;
 constexpr uint32_t kLowsMinDim = 512;
 
 // Refinement record of one vector (cluster order), ex_record_bytes(P) = P + 16 bytes, so a
-// refined vector is one contiguous read: the packed 7-bit ex-code (P*7/8 bytes, the
-// reference's packing, pack_excode.hpp:216-265), its sign code (P/8 bytes, the tiles' words:
-// dimension 32w+l at bit l of word w), f_add_ex and f_rescale_ex, and 8 bytes of padding
-// (16-byte aligned records).
+// refined vector is one contiguous read: the packed 7-bit ex-code (P*7/8 bytes in 64-dimension
+// groups of 56 bytes, the reference's packing, pack_excode.hpp:216-265) and the sign code (P/8
+// bytes, the tiles' words: dimension 32w+l at bit l of word w), then f_add_ex, f_rescale_ex
+// and 8 bytes of padding (16-byte aligned records).
+//
+// The first P bytes are split by 64-dimension group g = 0 .. G - 1 (G = P / 64): the 64 bytes
+// of group g ("its slice": the group's 56 ex-code bytes, then sign-code words 2g and 2g + 1)
+// are four 16-byte chunks, chunk k at byte 16 (G k + g). A kernel that refines one vector with
+// one lane per group (or one lane per few groups) loads a slice as four 16-byte loads, and the
+// G lanes of a vector then read 16 G contiguous bytes per load.
 __host__ __device__ constexpr uint32_t ex_record_bytes(uint32_t P) { return P + 16; }
-__host__ __device__ constexpr uint32_t ex_record_sign_offset(uint32_t P) { return P * 7 / 8; }
+__host__ __device__ constexpr uint32_t ex_record_groups(uint32_t P) { return P / 64; }
+// byte b (0..63) of group g's slice
+__host__ __device__ constexpr uint32_t ex_record_slice_byte(uint32_t P, uint32_t g, uint32_t b) {
+    return 16 * (ex_record_groups(P) * (b / 16) + g) + b % 16;
+}
+// 8-byte word kk (0..6) of 64-dimension ex-code group g
+__host__ __device__ constexpr uint32_t ex_record_group_word(uint32_t P, uint32_t g, uint32_t kk) {
+    return ex_record_slice_byte(P, g, 8 * kk);
+}
+// sign-code word w (in the slice of group w / 2)
+__host__ __device__ constexpr uint32_t ex_record_sign_word(uint32_t P, uint32_t w) {
+    return ex_record_slice_byte(P, w / 2, 56 + 4 * (w % 2));
+}
 __host__ __device__ constexpr uint32_t ex_record_factor_offset(uint32_t P) { return P; }
 
 struct ClusterMeta {
@@ -156,6 +174,10 @@ struct ScanParams {
     // read by the recovery pass: [nq][vanguard][van_stride]
     float *van_lows;
     uint32_t van_stride;
+    // the smallest lower bound of each group of 4 consecutive vectors of a vanguard pair,
+    // written with van_lows by the lows pass when set: [nq][vanguard][van_stride / 4] (+inf for
+    // vectors past the cluster's end)
+    float *van_mins;
     uint32_t seed_buf;           // seed pass LDS buffer entries (power of two >= keep + 64)
     // refined pre-filter of the far and recovery passes (needs ex_rec)
     int prefilter;
@@ -182,7 +204,62 @@ struct VanguardArgs {
     unsigned long long *seeded;    // queries whose threshold the pass lowered
     unsigned long long *refined;   // vectors refined on the GPU
     int lows_ready;
+    // queries taken from a list whose length is on the device (the staged pass's overflow
+    // queries): workgroup b handles list[b] when b < *list_count; nullptr: every query
+    const uint32_t *list;
+    const unsigned long long *list_count;
 };
+
+// Staged vanguard pass (vanguard_staged.hip): the fused pass's work split into per-query
+// stages (seed select, threshold and candidate list, merge and publication) and grid-wide
+// refinement stages that gather the refinement records of every query at once.
+//
+// Each query has fixed regions: its seeds (seed_cap entries) and its list (list_cap) of other
+// vectors to refine. An entry's position
+// is its slot j * van_stride + v in the query's lower-bound rows (pair j, cluster position
+// v); the refinement writes rd = {refined distance, rounding bound} and aux = {exact_ip,
+// lower bound} beside it.
+struct VsQuery {
+    uint32_t seed_n, list_n;
+    uint32_t cut1;    // seeds: the bounds below thr_in with order key <= cut1
+    float thr_in;     // the threshold the pass started from
+    float thr;        // the threshold the seeds' refined distances back
+    uint32_t dk_key;  // order key of the seeds' topk-th refined distance (~0u: fewer seeds)
+    uint32_t flags;   // kVsOverflow: a region was too small; the one-pass kernel takes the query
+    uint32_t pub_n;   // records the merge left in the query's out region for publication
+    uint32_t pad[4];
+};
+constexpr uint32_t kVsOverflow = 1;
+// counters (VsArgs::ctr): seed entries, list entries, queries whose list needed a re-scan
+// of their bounds, queries left to the one-pass kernel
+constexpr uint32_t kVsCtrSeeds = 0, kVsCtrList = 1, kVsCtrRescan = 2, kVsCtrOverflow = 3, kVsCtrWords = 4;
+
+// statistics spread over kVsSpread 128-byte lines (a query adds to line q % kVsSpread) and
+// summed by one workgroup at the end of the pass
+constexpr uint32_t kVsSpread = 64, kVsSpreadWords = 16;
+constexpr uint32_t kVsStSeeds = 0, kVsStList = 1, kVsStRescan = 2, kVsStDropped = 3, kVsStRefined = 4,
+                   kVsStSeeded = 5;
+
+struct VsArgs {
+    uint32_t *seed_pos;       // [nq][seed_cap]
+    float2 *seed_rd, *seed_aux;
+    uint32_t *list_pos;       // [nq][list_cap]
+    float2 *list_rd, *list_aux;
+    uint32_t seed_cap, list_cap;
+    VsQuery *qs;              // [nq]
+    uint4 *out;               // [nq][out_cap] records to publish, written by the merge
+    uint32_t out_cap;
+    unsigned long long *spread;  // [kVsSpread][kVsSpreadWords], zeroed before the pass
+    unsigned long long *ctr;  // [kVsCtrWords], zeroed before the pass
+    uint32_t *overflow;       // [nq] queries left to the one-pass kernel (count in ctr)
+    uint32_t seeds;           // seed cut's rank among the sub-stream minima (>= topk, <= 512)
+};
+
+// the staged pass: P of 64..1024 with a compiled refinement kernel
+bool vanguard_staged_supported(uint32_t W);
+// refine_ms: optional events around the two refinement launches (timing)
+void launch_vanguard_staged(const ScanParams &p, const VanguardArgs &va, const VsArgs &vs, uint32_t W, uint32_t nq,
+                            hipEvent_t ev_r0, hipEvent_t ev_r1, hipEvent_t ev_r2, hipEvent_t ev_r3, hipStream_t s);
 
 // ---- launchers (each defined in the translation unit holding its kernel) ----
 void launch_repack(const uint32_t *ref_words, const float *ref_factors, const ClusterMeta *meta,

@@ -149,8 +149,13 @@ __global__ __launch_bounds__(kFinalThreads) void final_select_kernel(const unsig
         __syncthreads();
         for (uint32_t i = t; i < n; i += kFinalThreads) {
             const unsigned long long v = k[i];
-            if (v <= prefix)
-                s[atomicAdd(&s_n, 1u)] = v;
+            if (v <= prefix) {
+                // keys are unique per query, so at most topk land here; a duplicate record
+                // would add more, which the bound keeps inside the array
+                const uint32_t pos = atomicAdd(&s_n, 1u);
+                if (pos < kFinalLds)
+                    s[pos] = v;
+            }
         }
         __syncthreads();
         uint32_t pw = 1;

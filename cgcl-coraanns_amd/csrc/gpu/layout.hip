@@ -58,7 +58,8 @@ __global__ __launch_bounds__(256) void ex_record_fill_kernel(const uint8_t *__re
         const uint32_t k = (uint32_t)(i % (words + 1));
         uint8_t *dst = rec + (g0 + r) * stride;
         if (k < words)
-            reinterpret_cast<uint2 *>(dst)[k] = reinterpret_cast<const uint2 *>(codes + r * words * 8)[k];
+            *reinterpret_cast<uint2 *>(dst + ex_record_group_word(P, k / 7, k % 7)) =
+                reinterpret_cast<const uint2 *>(codes + r * words * 8)[k];
         else
             *reinterpret_cast<float2 *>(dst + ex_record_factor_offset(P)) =
                 make_float2(factors[2 * r], factors[2 * r + 1]);
@@ -75,14 +76,13 @@ __global__ __launch_bounds__(64) void ex_record_sign_kernel(const ClusterMeta *_
     for (uint32_t local = threadIdx.x; local < cm.n; local += kTileVectors) {
         const uint8_t *tile = tiles + (size_t)(cm.tile_base + local / kTileVectors) * tile_bytes;
         const uint32_t vl = local % kTileVectors;
-        uint32_t *dst = reinterpret_cast<uint32_t *>(rec + ((size_t)cm.start + local) * stride +
-                                                     ex_record_sign_offset(P));
+        uint8_t *dst = rec + ((size_t)cm.start + local) * stride;
         for (uint32_t w = 0; w < W; ++w) {
             const uint32_t g = w / 4, c = w % 4;
             const uint32_t *src =
                 g < full_groups ? reinterpret_cast<const uint32_t *>(tile + (size_t)(g * 64 + vl) * 16) + c
                                 : reinterpret_cast<const uint32_t *>(tile + (size_t)full_groups * 1024 + vl * 8) + c;
-            dst[w] = *src;
+            *reinterpret_cast<uint32_t *>(dst + ex_record_sign_word(P, w)) = *src;
         }
     }
 }

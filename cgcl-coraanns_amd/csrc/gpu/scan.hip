@@ -583,7 +583,7 @@ __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
                 const uint8_t *code = p.ex_rec + gid * p.ex_stride;
                 float ip = 0.0f, l1 = 0.0f;
                 for (uint32_t c = sub; c < chunks; c += 16)
-                    ip += excode_chunk_ip(code, qv, c, &l1);
+                    ip += excode_chunk_ip(code, p.P, qv, c, &l1);
 #pragma unroll
                 for (int o = 8; o > 0; o >>= 1) {
                     ip += __shfl_xor(ip, o, 16);

@@ -43,6 +43,53 @@ constexpr int kStage = 256;  // staged survivor records per wave
 // written with ip_int and ip_res to the debug arrays, or written to the vanguard lows.
 enum MfmaMode : int { kPublish = 0, kDenseDbg = 1, kLows = 2 };
 
+// The smallest of the lower bounds of vectors o .. o + 3 of a cluster of n vectors (+inf for
+// vectors past its end): the group minima of the vanguard lows pass (ScanParams::van_mins).
+__device__ __forceinline__ float group_min4(const float (&lw)[4], uint32_t o, uint32_t n) {
+    float mn = __int_as_float(0x7F800000);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        mn = o + r < n ? fminf(mn, lw[r]) : mn;
+    return mn;
+}
+
+// The lows pass stages a tile's lower bounds (64 vectors x the unit's 16 pair slots) in LDS
+// and writes them pair by pair: the MFMA result gives a lane 4 consecutive vectors of one
+// pair, so direct stores would write each pair's 256 bytes as sixteen 16-byte pieces from
+// four instructions; staged, a store instruction writes 4 whole pair rows of 256 bytes.
+constexpr uint32_t kLowPitch = 68;  // floats per staged pair row (64 + 4, staggering the banks)
+
+// lower bounds lw of vectors o .. o + 3 of pair slot col
+__device__ __forceinline__ void lows_put(float *s_low, uint32_t col, uint32_t o, const float (&lw)[4]) {
+    *reinterpret_cast<float4 *>(s_low + col * kLowPitch + o) = make_float4(lw[0], lw[1], lw[2], lw[3]);
+}
+
+// Writes the staged bounds of tile t to van_lows (and their group minima to van_mins). w0 is
+// the lane's pair word (lanes 0..15 hold slots 0..15), count the unit's pairs, n the cluster
+// size. One-wave workgroups: the barriers order the LDS writes, these reads and the next
+// tile's writes.
+__device__ __forceinline__ void lows_flush(const ScanParams &p, const float *s_low, uint32_t lane, uint32_t w0,
+                                           uint32_t count, uint32_t t, uint32_t n) {
+    __syncthreads();
+    const uint32_t c = lane & 15u, sub = lane >> 4;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t pr = 4 * i + sub;
+        const uint32_t w = __shfl(w0, (int)pr);
+        if (pr < count) {
+            const float4 v = *reinterpret_cast<const float4 *>(s_low + pr * kLowPitch + 4 * c);
+            const size_t row = (size_t)(w & 0xFFFFu) * p.vanguard + (w >> 16);
+            const uint32_t o = t * kTileVectors + 4 * c;
+            *reinterpret_cast<float4 *>(p.van_lows + row * p.van_stride + o) = v;
+            if (p.van_mins) {
+                const float lw[4] = {v.x, v.y, v.z, v.w};
+                p.van_mins[row * (p.van_stride / 4) + o / 4] = group_min4(lw, o, n);
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // Bits 0..7 of b as eight int8 0/1 values (bit e in byte e), the 64-bit MFMA operand.
 __device__ __forceinline__ long spread_byte(uint32_t b) {
     const uint32_t lo = ((b & 15u) * 0x00204081u) & 0x01010101u;
@@ -126,6 +173,7 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
     constexpr int G = (W + 3) / 4;  // code word groups of a tile
     __shared__ uint4 s_rec[kDense ? 1 : kStage];
     __shared__ float s_cut[kDense ? 1 : kStage];
+    __shared__ __align__(16) float s_low[kMode == kLows ? 16 * kLowPitch : 4];
     // bits 0..7 of a byte b as eight int8 0/1 values (the MFMA operand): s_spread[b]
     __shared__ long s_spread[256];
     const uint32_t lane = threadIdx.x, col = lane & 15, quad = lane >> 4;
@@ -228,15 +276,13 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
                 const float fev[4] = {fe[m].x, fe[m].y, fe[m].z, fe[m].w};
                 if constexpr (kMode == kLows) {
                     // rows 16 m + 4 quad + r of the pair's tile-padded slice (lanes past the
-                    // cluster's end write values nobody reads)
+                    // cluster's end stage values nobody reads)
                     if (slot) {
                         float lw[4];
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             lw[r] = fav[r] + gadd + frv[r] * (width * (float)acc[m][r] + k1) - fev[r] * gerr;
-                        *reinterpret_cast<float4 *>(p.van_lows + ((size_t)query * p.vanguard + probe) * p.van_stride +
-                                                    t * kTileVectors + 16 * m + 4 * quad) =
-                            make_float4(lw[0], lw[1], lw[2], lw[3]);
+                        lows_put(s_low, col, 16 * m + 4 * quad, lw);
                     }
                     continue;
                 }
@@ -274,6 +320,8 @@ __global__ __launch_bounds__(64) void far_mfma_kernel(const ScanParams p) {
                     }
                 }
             }
+            if constexpr (kMode == kLows)
+                lows_flush(p, s_low, lane, w0, count, t, n);
         }
     }
     if constexpr (!kDense) {
@@ -347,6 +395,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
     __shared__ uint4 s_rec[kDense ? 1 : kStageWide];
     __shared__ float s_cut[kDense ? 1 : kStageWide];
     __shared__ uint32_t s_loc[kDense ? 1 : kStageWide];
+    __shared__ __align__(16) float s_low[kMode == kLows ? 16 * kLowPitch : 4];
     // bits 0..7 of a byte b as eight int8 0/1 values: s_spread[b]
     __shared__ uint2 s_spread[256];
     const uint32_t lane = threadIdx.x, col = lane & 15, quad = lane >> 4;
@@ -445,7 +494,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                 const float fev[4] = {fe.x, fe.y, fe.z, fe.w};
                 if constexpr (kMode == kLows) {
                     // rows o + r of the pair's tile-padded slice (lanes past the cluster's
-                    // end write values nobody reads)
+                    // end stage values nobody reads)
                     if (slot) {
                         float lw[4];
 #pragma unroll
@@ -453,8 +502,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                             const float ex = width * (float)acc[r];
                             lw[r] = fav[r] + gadd + frv[r] * (ex + k1) - fev[r] * gerr;
                         }
-                        *reinterpret_cast<float4 *>(p.van_lows + ((size_t)query * p.vanguard + probe) * p.van_stride +
-                                                    t * kTileVectors + o) = make_float4(lw[0], lw[1], lw[2], lw[3]);
+                        lows_put(s_low, col, o, lw);
                     }
                     continue;
                 }
@@ -495,6 +543,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                     }
                 }
             }
+            if constexpr (kMode == kLows)
+                lows_flush(p, s_low, lane, w0, count, t, n);
         }
     }
     if constexpr (!kDense) {

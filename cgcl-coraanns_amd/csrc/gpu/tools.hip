@@ -135,6 +135,15 @@ static __device__ __align__(256) float scratch[kScratchFloats];
 
 std::mutex g_scratch_mu;
 std::map<int, float *> g_scratch_addr;  // device ordinal -> address of its scratch
+// one allocation-free call at a time per device: a call holds its device's lock from the
+// scratch address until its kernels have finished
+std::mutex g_scratch_use_mu;
+std::map<int, std::mutex> g_scratch_use;  // device ordinal -> lock of its scratch
+
+std::mutex &scratch_lock(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_use_mu);
+    return g_scratch_use[device];  // std::map never moves its elements
+}
 
 // The calling device's scratch address, resolved once per device (the device is current).
 int scratch_address(int device, float **out) {
@@ -317,8 +326,9 @@ int cora_tool_assign(const float *h_x, uint64_t n, uint64_t dim, const float *h_
 
 // The same assignment on device arrays the caller owns, with no allocation: centroid norms,
 // row norms and distance blocks in the static scratch array (nothing in it has to start at
-// zero: every value is written before it is read). Calls that overlap on one GPU (two host
-// threads) share that array and race; a call returns once its kernels have finished.
+// zero: every value is written before it is read). Calls on one GPU from several host threads
+// take turns (a per-device lock held until the call's kernels have finished), so they never
+// share the array at the same time.
 int cora_tool_assign_noalloc(const float *d_x, uint64_t n, uint64_t dim, const float *d_centroids,
                              uint64_t k, uint32_t *d_assign, int device) {
     if (!d_x || !d_centroids || !d_assign || !n || !dim || !k) {
@@ -332,6 +342,7 @@ int cora_tool_assign_noalloc(const float *d_x, uint64_t n, uint64_t dim, const f
         return CORA_ERR_INVALID_ARGUMENT;
     }
     TCHK(hipSetDevice(device));
+    std::lock_guard<std::mutex> use(scratch_lock(device));
     float *base = nullptr;
     if (int rc = scratch_address(device, &base))
         return rc;

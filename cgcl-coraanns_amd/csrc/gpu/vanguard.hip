@@ -37,6 +37,7 @@
 // reject.
 #include <float.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -263,11 +264,23 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
     // workgroup b runs on XCD b % 8 and takes the (b / 8)-th query of that XCD's slice of
     // the queries ordered by nearest cluster, so each XCD's L2 serves about an eighth of
     // the clusters
-    const uint32_t per_xcd = (va.nq + kNumXcd - 1) / kNumXcd;
-    const uint32_t slot = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
-    if (slot >= va.nq)
-        return;
-    const uint32_t qi = va.order ? va.order[slot] : slot;
+    // list mode: workgroup b takes list entries b, b + grid, ... in turn
+    uint32_t list_idx = blockIdx.x;
+next_query:
+    uint32_t qi;
+    if (va.list) {
+        // the queries of a device-side list (the staged pass's overflow)
+        if (list_idx >= *va.list_count)
+            return;
+        qi = va.list[list_idx];
+        list_idx += gridDim.x;
+    } else {
+        const uint32_t per_xcd = (va.nq + kNumXcd - 1) / kNumXcd;
+        const uint32_t slot = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+        if (slot >= va.nq)
+            return;
+        qi = va.order ? va.order[slot] : slot;
+    }
     const uint32_t V = va.depth, topk = va.topk;
     const uint32_t P = p.P, nw = W > 0 ? (uint32_t)W : P / 32;
     const QueueDev q = p.queue;
@@ -338,7 +351,6 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
     // every segment so they are not live across the list refinement
     uint32_t preg[W > 0 && W <= 4 ? kBq * W : 1];
     const ConstWords cplanes = (ConstWords)(p.qplanes + (size_t)qi * 2 * kBq * nw);
-    const size_t lc = (size_t)P * 7 / 8;
     auto process_list = [&]() {
         const uint32_t nl = S.nlist;
         for (;;) {
@@ -431,20 +443,15 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                         uint2 grp[kG][7];
                         float fa = 0.0f, fr = 0.0f;
                         if (have) {
-                            // sign-code words sub kWq .. sub kWq + kWq - 1, in 8-byte pairs
-                            const uint2 *wp = reinterpret_cast<const uint2 *>(rec + lc) + sub * (kWq / 2);
-#pragma unroll
-                            for (int i = 0; i < kWq / 2; ++i) {
-                                const uint2 v = wp[i];
-                                xw[2 * i] = v.x;
-                                xw[2 * i + 1] = v.y;
-                            }
+                            // the slices of the lane's groups sub, sub + 4, ...: their
+                            // ex-code words and sign-code words 2 (sub + 4 gi) + e
 #pragma unroll
                             for (int gi = 0; gi < kG; ++gi) {
-                                const uint2 *gp = reinterpret_cast<const uint2 *>(rec + (size_t)(sub + 4 * gi) * 56);
-#pragma unroll
-                                for (int k = 0; k < 7; ++k)
-                                    grp[gi][k] = gp[k];
+                                GroupSlice sl;
+                                sl.load(rec, W / 2, sub + 4 * gi);
+                                sl.group(grp[gi]);
+                                xw[2 * gi] = sl.sign_word(0);
+                                xw[2 * gi + 1] = sl.sign_word(1);
                             }
                             if (sub == 0) {
                                 const float2 f = *reinterpret_cast<const float2 *>(rec + P);
@@ -457,7 +464,7 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                         if (have) {
 #pragma unroll
                             for (int i = 0; i < kWq; ++i) {
-                                const uint32_t w = sub * kWq + i;
+                                const uint32_t w = 2 * (sub + 4 * (i / 2)) + (i % 2);
 #pragma unroll
                                 for (int b = 0; b < kBq - 1; ++b) {
                                     ipa += __popc(xw[i] & planes[b * W + w]) << b;
@@ -493,8 +500,7 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                     while (have && pos >= S.off[j + 1])
                         ++j;
                     const size_t gid = (size_t)S.start[j] + (pos - S.off[j]);
-                    const uint8_t *code = p.ex_rec + gid * p.ex_stride;  // the ex-code leads the record
-                    const uint32_t *sw = reinterpret_cast<const uint32_t *>(code + lc);
+                    const uint8_t *code = p.ex_rec + gid * p.ex_stride;
                     int ipa = 0, ipb = 0;
                     float ipx = 0.0f, fa = 0.0f, fr = 0.0f;
                     // an opaque zero: plane and q' reads indexed with it stay in the chunk
@@ -520,7 +526,7 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                         for (int i = 0; i < kWl; ++i) {
                             if ((uint32_t)i < half_w) {
                                 const uint32_t w = sub * half_w + i;
-                                const uint32_t xw = sw[w];
+                                const uint32_t xw = *reinterpret_cast<const uint32_t *>(code + ex_record_sign_word(P, w));
 #pragma unroll
                                 for (int b = 0; b < kBq - 1; ++b) {
                                     ipa += __popc(xw & planes[b * nw + w]) << b;
@@ -535,7 +541,7 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                         for (int i = 0; i < kCl; ++i) {
                             const uint32_t c = sub + 2 * i;
                             if (c < P / 8)
-                                ipx += excode_chunk_ip<false>(code, qv, c);
+                                ipx += excode_chunk_ip<false>(code, P, qv, c);
                         }
                     }
                     ipa += __shfl_xor(ipa, 1, 2);
@@ -883,12 +889,18 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
             atomicAdd(va.seeded, 1ull);
         }
     }
+    if (va.list) {
+        __syncthreads();  // the next query reuses the LDS
+        goto next_query;
+    }
 }
 
 template <int W>
 void launch_vq_w(const ScanParams &p, const VanguardArgs &va, uint32_t nq, hipStream_t s) {
     const size_t dyn = (size_t)p.P * sizeof(float);
-    const uint32_t grid = (nq + kNumXcd - 1) / kNumXcd * kNumXcd;
+    uint32_t grid = (nq + kNumXcd - 1) / kNumXcd * kNumXcd;
+    if (va.list)  // the listed queries are taken in turn by about the resident workgroups
+        grid = std::min<uint32_t>(grid, 512);
     if (va.lows_ready)
         vanguard_query_kernel<W, true><<<grid, kVqThreads, dyn, s>>>(p, va);
     else

@@ -195,6 +195,8 @@ int cora_hybrid_stats_get(cora_hybrid *h, cora_hybrid_stats *out) {
     out->vanguard_mode = x.get_last_vanguard_mode();
     for (int i = 0; i < 4; ++i)
         out->phase_ms[i] = x.get_last_phase_ms(i);
+    out->vanguard_refine_ms = x.get_last_vanguard_refine_ms();
+    out->vanguard_refine_bytes = x.get_last_vanguard_refine_bytes();
     return CORA_OK;
 }
 

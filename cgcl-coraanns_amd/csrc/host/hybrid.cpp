@@ -210,6 +210,8 @@ void HybridIndex::record_stats(const cora_search_stats &st, std::size_t refined)
     last_vanguard_mode_ = st.vanguard_mode;
     for (int i = 0; i < 4; ++i)
         last_phase_ms_[i] = st.phase_ms[i];
+    last_vanguard_refine_ms_ = st.vanguard_refine_ms;
+    last_vanguard_refine_bytes_ = st.vanguard_refine_bytes;
 }
 
 void HybridIndex::print_profile(const cora_search_stats &st, std::size_t refined) const {

@@ -105,7 +105,12 @@ enum cora_search_flags {
      * epilogue keeps 8 candidate keys per query and 128-cluster tile and a merge selects from
      * them, with the same result; the distance matrix is then not available to
      * CORA_DBG_PROBE_DIST (its memory holds the candidates). */
-    CORA_FLAG_UNFUSED_PROBE = 1u << 13
+    CORA_FLAG_UNFUSED_PROBE = 1u << 13,
+    /* Fused vanguard pass after the matrix-core lows pass: run it as one per-query kernel
+     * (each query selects, refines and publishes in turn) instead of the staged pass, whose
+     * refinement of every query's candidates runs grid-wide between per-query select and
+     * merge stages, with the same rules for what is refined, published and the threshold. */
+    CORA_FLAG_VANGUARD_ONE_PASS = 1u << 14
 };
 
 typedef struct cora_gpu_engine cora_gpu_engine;
@@ -169,12 +174,18 @@ typedef struct cora_search_stats {
                                      of the cluster, once per unit of up to 16 pairs */
     /* how the vanguard pairs ran: 0 none, 1 the per-pair seed and recovery passes (asked
      * for, no ex-codes in HBM, or beyond the fused pass's limits of 64 vanguard pairs and
-     * top-128), 2 the fused per-query pass, 3 the fused pass after the matrix-core lows pass */
+     * top-128), 2 the fused per-query pass, 3 the fused pass after the matrix-core lows pass,
+     * 4 the staged pass after the matrix-core lows pass */
     int32_t vanguard_mode;
     /* the reference's [Profile] phases (FILTER_TIMING only): query preparation and coarse
      * GEMM, probe selection, pair scheduling, then the scan pipeline up to cora_gpu_sync
      * (including the host's refinement) */
     float phase_ms[4];
+    /* staged pass: its two grid-wide refinement launches (FILTER_TIMING only), and their
+     * algorithmic bytes: sign code, ex-code and ex-factors of each refined vector, plus its
+     * 4-byte position and lower bound read and 16 bytes of result written */
+    float vanguard_refine_ms;
+    uint64_t vanguard_refine_bytes;
 } cora_search_stats;
 
 /* Lifecycle (HybridIndex ctor/dtor, hybrid.cu:35-85). device = HIP ordinal. */
@@ -288,9 +299,13 @@ enum cora_debug_array {
                                      cluster rounded up to 256; entries past a cluster's
                                      size are undefined) */
     CORA_DBG_LUT = 14,            /* f16 [nq][P/4][16] LUT4 tables (CORA_FLAG_LUT4 searches) */
-    CORA_DBG_PROBE_FALLBACK = 15  /* u32 [1 + nq]: the number of queries whose fused probe
+    CORA_DBG_PROBE_FALLBACK = 15, /* u32 [1 + nq]: the number of queries whose fused probe
                                      select fell back to their distance row, then those
                                      queries (any order); count 0 for an unfused search */
+    CORA_DBG_STAGED_COUNTS = 16   /* u64 [4] of the last staged vanguard pass: seeds and
+                                     list entries refined, queries whose list needed a second
+                                     pass over their bounds, queries left to the one-pass
+                                     kernel */
 };
 int cora_gpu_debug_read(cora_gpu_engine *engine, int which, void *dst, uint64_t bytes);
 
@@ -338,8 +353,8 @@ int cora_tool_quantize(const float *x, uint64_t n, uint64_t dim, const float *R,
  * norms and distance blocks go to a 16 MiB static device array that each GPU holds until the
  * process ends. Same result as cora_tool_assign (nearest centroid, ties -> lower id). At most
  * CORA_NOALLOC_MAX_CENTROIDS centroids and dimension CORA_NOALLOC_MAX_DIM (else
- * CORA_ERR_INVALID_ARGUMENT). Runs on the null stream and returns when done; calls that
- * overlap on one GPU share the scratch array and race. */
+ * CORA_ERR_INVALID_ARGUMENT). Runs on the null stream and returns when done; calls on one GPU
+ * take turns on its scratch array (a per-device lock), so several host threads may call it. */
 #define CORA_NOALLOC_MAX_CENTROIDS 1048576
 #define CORA_NOALLOC_MAX_DIM 4096
 int cora_tool_assign_noalloc(const float *x, uint64_t n, uint64_t dim, const float *centroids, uint64_t k,

@@ -71,6 +71,8 @@ typedef struct cora_hybrid_stats {
     uint64_t vanguard_lows_bytes; /* its algorithmic bytes */
     int32_t vanguard_mode;   /* get_last_vanguard_mode */
     float phase_ms[4];       /* get_last_phase_ms */
+    float vanguard_refine_ms;       /* staged vanguard pass: its grid-wide refinement launches */
+    uint64_t vanguard_refine_bytes; /* their algorithmic bytes */
 } cora_hybrid_stats;
 
 int cora_hybrid_create(cora_hybrid **out, int device);                 /* HybridIndex() */

@@ -142,8 +142,12 @@ class HybridIndex {
     float get_last_vanguard_ms() const { return last_vanguard_ms_; }
     uint64_t get_last_vanguard_bytes() const { return last_vanguard_bytes_; }
     float get_last_vanguard_lows_ms() const { return last_vanguard_lows_ms_; }
-    // 0 none, 1 per-pair seed and recovery passes, 2 fused per-query pass, 3 lows pass + fused
+    // 0 none, 1 per-pair seed and recovery passes, 2 fused per-query pass, 3 lows pass + fused,
+    // 4 lows pass + staged pass
     int get_last_vanguard_mode() const { return last_vanguard_mode_; }
+    // staged vanguard pass: its grid-wide refinement launches and their algorithmic bytes
+    float get_last_vanguard_refine_ms() const { return last_vanguard_refine_ms_; }
+    uint64_t get_last_vanguard_refine_bytes() const { return last_vanguard_refine_bytes_; }
     // [Profile] phases (with profiling or GPU filter timing): matrix math, probe select,
     // pair scheduling, scan pipeline including the CPU refinement
     float get_last_phase_ms(int phase) const { return phase >= 0 && phase < 4 ? last_phase_ms_[phase] : 0.0f; }
@@ -206,6 +210,8 @@ class HybridIndex {
     float last_vanguard_lows_ms_ = 0.0f;
     int last_vanguard_mode_ = 0;
     float last_phase_ms_[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float last_vanguard_refine_ms_ = 0.0f;
+    uint64_t last_vanguard_refine_bytes_ = 0;
 };
 
 }  // namespace coraanns

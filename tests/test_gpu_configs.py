@@ -7,8 +7,11 @@
   reference CPU path's on the same 2,000 queries, live against frozen results and the
   frozen-threshold candidate count against the oracle's band on a 64-query sample.
 - Configs 3-5 (10M x 96, 20M x 768 inner product, 100M x 96 at top-100 with vanguard 10):
-  the full index built, production recall on a 256-query sample at the grid's first nprobe,
-  and the exhaustive frozen top-k of 4 queries against the oracle, which reads only the
+  the full index built; production recall on a 256-query sample at the grid's first nprobe,
+  at least rabitq_cpu's on the same queries minus 0.001 (config 4 also at top-100, with CPU
+  refinement and with the GPU-final top-k); config 4's vanguard pass in its frozen test mode
+  with the matrix-core lows pass, its publication bands and top-k checked on 16 queries; and
+  the exhaustive frozen top-k of 4 queries against the oracle. The oracle reads only the
   probed clusters of the index file (open_ivf_lazy / cluster_data).
 """
 import dataclasses
@@ -216,34 +219,157 @@ def test_config2_full_size(tmp_path):
     eng.close()
 
 
+class LazyProbed:
+    """Every vector of a query's probed clusters, from the index file (only those clusters
+    are read): probe rank, external ids, oracle lower bound, refined distance (the CPU
+    consumer's formula) and its rounding bound; cluster slices are cached."""
+
+    def __init__(self, lz, g):
+        self.lz, self.g, self.cache = lz, g, {}
+        self.qint = qint_from_planes(g["planes"][:, :8])
+        self.qres = qint_from_planes(g["planes"][:, 8:])
+
+    def __call__(self, q, nprobe):
+        g, P = self.g, self.lz.padded_dim
+        l1 = float(np.abs(g["qr"][q]).sum())
+        out = []
+        for p in range(nprobe):
+            c = int(g["pidx"][q, p])
+            if c not in self.cache:
+                self.cache[c] = orc.cluster_data(self.lz, c)
+            bits, f, lc, exf, ids, _ = self.cache[c]
+            if bits.shape[0] == 0:
+                continue
+            ipi = orc.ip_int_direct(bits, self.qint[q])
+            low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p],
+                               orc.exact_ip_bitwise(ipi, g["width"][q]), g["k1"][q])
+            ex2 = orc.exact_ip_two_stage(ipi, orc.ip_int_direct(bits, self.qres[q]), g["width"][q], g["width2"][q])
+            fa, fr = exf[:, 0], exf[:, 1]
+            rd = orc.refine_dist(fa, fr, g["gadd"][q, p], ex2, orc.excode_ip(g["qr"][q], lc, P), g["kb"][q],
+                                 self.lz.ex_bits)
+            err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], self.lz.ex_bits)
+            out.append((p, ids, low.astype(np.float64), rd.astype(np.float64), err.astype(np.float64)))
+        return out
+
+
+def check_frozen_vanguard_bands(eng, lz, nq, P, nprobe, vanguard, topk, d, i):
+    """The vanguard pass's deterministic test mode (frozen snapshot lowered by the pass) on
+    the index file: the threshold is backed by topk vanguard vectors below it; the vanguard
+    pass publishes every vector with lower bound and refined distance below the threshold and
+    nothing beyond its rounding bound; the far pass exactly the vectors with lower bound below
+    the threshold and refined distance within the bound; the returned top-k are oracle
+    distances at or below the threshold and miss no closer vector below it; and they agree
+    with the oracle's exhaustive top-k over the probed clusters."""
+    st = eng.stats()
+    g = query_side(eng, nq, P, nprobe)
+    thr = eng.debug_read(ca.DBG_THRESHOLDS, (nq,), np.float32)
+    assert st["seeded_queries"] == nq
+    probed = LazyProbed(lz, g)
+    van_lo = van_hi = far_lo = far_hi = 0
+    overlap = []
+    for q in range(nq):
+        T = float(thr[q])
+        assert np.isfinite(T), q
+        band = 1e-5 * (abs(T) + 1)
+        backing = 0
+        info = {}
+        items = []
+        for p, ids, low, rd, err in probed(q, nprobe):
+            if p < vanguard:
+                backing += int(((rd < T) & (low < T + band)).sum())
+                van_lo += int(((low < T - band) & (rd <= T + 0.9 * err)).sum())
+                van_hi += int((rd <= T + 1.1 * err).sum())
+            else:
+                far_lo += int(((low < T - band) & (rd <= T + 0.9 * err)).sum())
+                far_hi += int(((low < T + band) & (rd <= T + 1.1 * err)).sum())
+            for k in range(ids.size):
+                info[int(ids[k])] = (p, low[k], rd[k], err[k])
+            items += list(zip(rd.tolist(), ids.tolist()))
+        assert backing >= topk, (q, backing)
+        scale = abs(T) + 1
+        for r in range(topk):
+            p, low, rd, err = info[int(i[q, r])]
+            assert abs(float(d[q, r]) - rd) <= 1e-5 * scale + err, (q, r)
+            assert low < T + band or (p < vanguard and rd <= T + 1.1 * err), (q, r)
+        assert float(d[q, topk - 1]) <= T + band, q
+        got = set(i[q].tolist())
+        kth = float(d[q, topk - 1])
+        for pid, (p, low, rd, err) in info.items():
+            if low < T - band and rd < kth - 1e-5 * scale - 2 * err:
+                assert pid in got, (q, pid)
+        items.sort()
+        overlap.append(len(got & {pid for _, pid in items[:topk]}) / topk)
+    produced = st["pass_produced"]
+    say(f"[gpu]   frozen bands on {nq} queries: vanguard published {produced[0]} in [{van_lo}, {van_hi}], far "
+        f"{produced[1] - produced[0]} in [{far_lo}, {far_hi}], exhaustive top-{topk} overlap {np.mean(overlap):.4f}")
+    assert van_lo <= produced[0] <= van_hi
+    assert far_lo <= produced[1] - produced[0] <= far_hi
+    assert produced[2] == produced[1]
+    assert np.mean(overlap) >= 0.99
+
+
 @pytest.mark.parametrize("cfg", [3, 4, 5])
 def test_large_config_full_size(cfg, tmp_path):
+    """Production recall on a 256-query sample at the grid's first nprobe, at least the
+    reference CPU path's (rabitq_cpu on the same index file and queries) minus 0.001;
+    config 4 also at top-100 with CPU refinement and with the GPU-final top-k, and the
+    vanguard pass's frozen bands on 16 queries with the matrix-core lows pass on; then the
+    exhaustive frozen top-k of 4 queries against the oracle."""
     c = dataclasses.replace(wl.CONFIGS[cfg], nq=256)
     say(f"[gpu] {c.describe()}: generating and building the full index")
     base, q = wl.generate(c)
     path = tmp_path / f"cfg{cfg}.index"
+    kmax = 100 if cfg == 4 else c.topk
     try:
         wl.build_index(c, base, path, log=say)
-        gt = wl.ground_truth(base, q, c.topk, c.metric)
+        gt = wl.ground_truth(base, q, kmax, c.metric)
         del base
         nprobe = c.nprobes[0]
+        nq = q.shape[0]
+        ref = rabitq_cpu_recall(path, q, gt, c.topk, [nprobe], tmp_path)[nprobe]
         say(f"[gpu]   cfg{cfg}: loading the index")
-        ivf, eng = engine(path, c.metric, q.shape[0], c.topk, nprobe, c.vanguard, cpu_secondary_filter=True)
+        prod = dict(vanguard_size=c.vanguard, metric=c.metric, gpu_filter_timing=True, cpu_secondary_filter=True)
+        ivf = ca.IvfIndex(path)
+        eng = ca.HybridIndex(0, **prod)
+        eng.load_ivf(ivf)
+        eng.prepare_workspace(nq, kmax, nprobe)
         eng.reset_buffer(q)
         _, i = eng.search(q, c.topk, nprobe, c.batch_q)
         r10, rk = orc.recall_at_k(i, gt, 10), orc.recall_at_k(i, gt, c.topk)
-        say(f"[gpu]   cfg{cfg} nprobe={nprobe}: recall@10 {r10:.4f} recall@{c.topk} {rk:.4f} "
-            f"(vanguard mode {eng.stats()['vanguard_mode']})")
-        assert r10 >= 0.9 and rk >= 0.9
+        say(f"[gpu]   cfg{cfg} nprobe={nprobe}: recall@10 {r10:.4f} recall@{c.topk} {rk:.4f}, rabitq_cpu "
+            f"recall@{c.topk} {ref:.4f} (vanguard mode {eng.stats()['vanguard_mode']})")
+        assert rk >= ref - 0.001 and r10 >= 0.9
+        if cfg == 4:
+            ref100 = rabitq_cpu_recall(path, q, gt, 100, [nprobe], tmp_path)[nprobe]
+            for final in (False, True):
+                eng.configure(**dict(prod, gpu_final_topk=final))
+                eng.reset_buffer(q)
+                _, i = eng.search(q, 100, nprobe, c.batch_q)
+                r100 = orc.recall_at_k(i, gt, 100)
+                say(f"[gpu]   cfg4 top-100 ({'GPU-final' if final else 'CPU refinement'}): recall@100 {r100:.4f}, "
+                    f"rabitq_cpu {ref100:.4f}")
+                assert r100 >= ref100 - 0.001, (final, r100, ref100)
         eng.close()
+        lz = orc.open_ivf_lazy(path)
+        if cfg == 4:
+            qs = q[:16]
+            eng = ca.HybridIndex(0, vanguard_size=5, metric=c.metric, gpu_filter_timing=True, frozen_thresholds=True,
+                                 cpu_secondary_filter=False, lower_bound_scale=1.0,
+                                 extra_flags=ca.FLAG_GPU_SEED_FROZEN | ca.FLAG_VANGUARD_MFMA)
+            eng.load_ivf(ivf)
+            eng.prepare_workspace(16, c.topk, nprobe)
+            eng.reset_buffer(qs)
+            d, i = eng.search(qs, c.topk, nprobe)
+            assert eng.stats()["vanguard_mode"] in (3, 4), eng.stats()["vanguard_mode"]
+            check_frozen_vanguard_bands(eng, lz, 16, c.padded_dim, nprobe, 5, c.topk, d, i)
+            eng.close()
         # four queries: the exhaustive frozen search against the oracle over their probe lists
         qs = q[:4]
         ivf, eng = engine(path, c.metric, 4, c.topk, nprobe, 0, frozen_thresholds=True,
                           cpu_secondary_filter=False, lower_bound_scale=1.0)
         eng.reset_buffer(qs)
         d, i = eng.search(qs, c.topk, nprobe)
-        want, _, _ = oracle_topk(orc.open_ivf_lazy(path), query_side(eng, 4, c.padded_dim, nprobe), nprobe,
-                                 c.topk)
+        want, _, _ = oracle_topk(lz, query_side(eng, 4, c.padded_dim, nprobe), nprobe, c.topk)
         assert_matches_oracle(d, i, want)
         eng.close()
         say(f"[gpu]   cfg{cfg}: frozen top-{c.topk} of 4 queries matches the oracle")

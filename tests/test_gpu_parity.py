@@ -634,22 +634,27 @@ def test_batch_q_and_reuse_do_not_change_results(synth, batch_q):
     assert np.allclose(d, d0, rtol=1e-6)
 
 
-@pytest.mark.parametrize("mode", ["fused", "fused_lows", "pair", "none"])
+@pytest.mark.parametrize("mode", ["fused", "fused_lows", "staged", "pair", "none"])
 @pytest.mark.parametrize("topk", [10, 100])
 def test_live_thresholds_match_frozen_results(synth, mode, topk):
     """Default production mode (live thresholds, secondary filter, vanguard 5; the fused
-    vanguard pass, the per-pair seed and recovery passes, or no GPU seed thresholds)
-    returns the same top-k as the exhaustive frozen search, except where refine distances
-    tie."""
+    vanguard pass in one per-query kernel, with or without the lows pass before it, the
+    staged pass, the per-pair seed and recovery passes, or no GPU seed thresholds) returns
+    the same top-k as the exhaustive frozen search, except where refine distances tie."""
     nprobe = 16
     say(f"[gpu] live vs frozen, vanguard mode {mode}")
     _, d0, i0 = run_frozen(synth, nprobe, topk, vanguard=0)
     eng = make_engine(synth, nprobe, topk, vanguard=5, frozen=False, secondary=True,
                       gpu_seed_refine=mode != "none",
-                      extra_flags={"pair": ca.FLAG_PAIR_SEEDS, "fused_lows": ca.FLAG_VANGUARD_MFMA}.get(mode, 0))
+                      extra_flags={"pair": ca.FLAG_PAIR_SEEDS,
+                                   "fused_lows": ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_ONE_PASS,
+                                   "staged": ca.FLAG_VANGUARD_MFMA}.get(mode, 0))
     eng.reset_buffer(synth.queries)
     d, i = eng.search(synth.queries, topk, nprobe, 4)
     st = eng.stats()
+    want_mode = {"fused": 2, "fused_lows": 3, "staged": 4, "pair": 1}.get(mode)
+    if want_mode is not None:
+        assert st["vanguard_mode"] == want_mode, st["vanguard_mode"]
     say(f"[gpu]   candidates per query {st['submitted'] / synth.queries.shape[0]:.1f}")
     assert st["submitted"] < synth.queries.shape[0] * 20000  # the filter prunes
     same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), i0.tolist())])
@@ -658,7 +663,7 @@ def test_live_thresholds_match_frozen_results(synth, mode, topk):
 
 @pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
 @pytest.mark.parametrize("topk", [10, 100])
-@pytest.mark.parametrize("lows", [False, True])
+@pytest.mark.parametrize("lows", [False, True, "staged"])
 def test_gpu_final_topk_matches_cpu_refinement(case_name, topk, lows, request):
     """GPU-final top-k (the GPU forms the final top-k from the refined distances it computed
     on the HBM ex-codes; nothing published to the ring) against the CPU consumer's top-k of
@@ -675,7 +680,8 @@ def test_gpu_final_topk_matches_cpu_refinement(case_name, topk, lows, request):
     case = request.getfixturevalue(case_name)
     nprobe, nq = 16, case.queries.shape[0]
     say(f"[gpu] GPU-final top-{topk} vs CPU refinement on {case_name} lows={lows}")
-    flags = ca.FLAG_GPU_SEED_FROZEN | (ca.FLAG_VANGUARD_MFMA if lows else 0)
+    flags = ca.FLAG_GPU_SEED_FROZEN | (ca.FLAG_VANGUARD_MFMA if lows else 0) | \
+        (ca.FLAG_VANGUARD_ONE_PASS if lows is True else 0)
     res = {}
     for final in (False, True):
         eng = make_engine(case, nprobe, topk, vanguard=5, frozen=True, extra_flags=flags, gpu_final_topk=final,
@@ -710,6 +716,10 @@ def test_gpu_final_topk_rejects_unsupported_modes(synth):
     eng.reset_buffer(synth.queries)
     with pytest.raises(ca.LogicError):  # the per-pair passes publish unrefined seeds
         eng.search(synth.queries, 10, 8)
+    eng.configure(vanguard_size=0, metric=synth.file.metric, gpu_final_topk=True)
+    eng.reset_buffer(synth.queries)
+    with pytest.raises(ca.LogicError):  # no vanguard pass: no refined threshold for any query
+        eng.search(synth.queries, 10, 8)
     eng.configure(vanguard_size=5, metric=synth.file.metric, gpu_final_topk=True)
     eng.reset_buffer(synth.queries)
     d, i = eng.search(synth.queries, 10, 8)  # live thresholds: supported
@@ -722,7 +732,8 @@ def test_vanguard_mode_reported(synth):
     beyond the fused pass's limits (top-k above 128)."""
     nprobe = 16
     eng = make_engine(synth, nprobe, 129, vanguard=5, frozen=False, secondary=True)
-    for topk, flags, mode in [(10, 0, 2), (10, ca.FLAG_VANGUARD_MFMA, 3), (129, 0, 1), (10, ca.FLAG_PAIR_SEEDS, 1)]:
+    for topk, flags, mode in [(10, 0, 2), (10, ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_ONE_PASS, 3),
+                              (10, ca.FLAG_VANGUARD_MFMA, 4), (129, 0, 1), (10, ca.FLAG_PAIR_SEEDS, 1)]:
         eng.configure(vanguard_size=5, cpu_secondary_filter=True, metric=synth.file.metric, gpu_filter_timing=True,
                       extra_flags=flags, lower_bound_scale=1.0)
         eng.reset_buffer(synth.queries)
@@ -730,6 +741,8 @@ def test_vanguard_mode_reported(synth):
         st = eng.stats()
         assert st["vanguard_mode"] == mode, (topk, flags, st["vanguard_mode"])
         assert all(t > 0 for t in st["phase_ms"]), st["phase_ms"]
+        assert (st["vanguard_refine_ms"] > 0) == (mode == 4), st["vanguard_refine_ms"]
+        assert st["vanguard_refine_bytes"] == (st["gpu_refined"] * (synth.file.padded_dim + 32) if mode == 4 else 0)
     eng.configure(vanguard_size=0, metric=synth.file.metric)
     eng.reset_buffer(synth.queries)
     eng.search(synth.queries, 10, nprobe)
@@ -923,7 +936,7 @@ def test_vanguard_lows_pass_matches_oracle(case_name, vanguard, request):
 
 @pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
 @pytest.mark.parametrize("vanguard,topk", [(3, 10), (8, 10), (5, 100), (10, 100)])
-@pytest.mark.parametrize("lows", [True, False])
+@pytest.mark.parametrize("lows", [True, False, "staged"])
 def test_fused_vanguard_frozen_parity(case_name, vanguard, topk, lows, request):
     """Fused per-query vanguard pass in its deterministic test mode (frozen snapshot,
     lowered by the pass): the threshold is backed by topk published vanguard vectors below
@@ -931,7 +944,9 @@ def test_fused_vanguard_frozen_parity(case_name, vanguard, topk, lows, request):
     threshold and nothing beyond its rounding bound; the far pass publishes exactly the
     vectors with low < threshold and refined distance within the bound; the final top-k is
     the top-k of that candidate set by the CPU consumer's distance. lows: the bounds come
-    from the matrix-core lows pass, else from the per-query pass itself. Top-100 with
+    from the matrix-core lows pass, else from the per-query pass itself; "staged": after
+    the lows pass, the staged pass (per-query select, grid-wide refinement, per-query
+    merge and publication) instead of the one per-query kernel. Top-100 with
     vanguard 10 is the 100M configuration's mode (top-k window, held list and threshold
     over many refinement rounds)."""
     nprobe = 16
@@ -939,10 +954,12 @@ def test_fused_vanguard_frozen_parity(case_name, vanguard, topk, lows, request):
     nq = case.queries.shape[0]
     say(f"[gpu] fused vanguard pass, frozen parity, {case_name} vanguard={vanguard} lows={lows}")
     eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True,
-                      extra_flags=ca.FLAG_GPU_SEED_FROZEN | (ca.FLAG_VANGUARD_MFMA if lows else ca.FLAG_NO_VANGUARD_MFMA))
+                      extra_flags=ca.FLAG_GPU_SEED_FROZEN | (ca.FLAG_VANGUARD_MFMA if lows else ca.FLAG_NO_VANGUARD_MFMA) |
+                      (ca.FLAG_VANGUARD_ONE_PASS if lows is True else 0))
     eng.reset_buffer(case.queries)
     d, i = eng.search(case.queries, topk, nprobe)
     st = eng.stats()
+    assert st["vanguard_mode"] == (4 if lows == "staged" else 3 if lows else 2), st["vanguard_mode"]
     g = gpu_intermediates(eng, case, nprobe)
     thr = eng.debug_read(ca.DBG_THRESHOLDS, (nq,), np.float32)
     assert st["seeded_queries"] == nq
@@ -997,6 +1014,46 @@ def test_fused_vanguard_frozen_parity(case_name, vanguard, topk, lows, request):
     ed, ei, cands = oracle_topk_from_gpu(case, g, nprobe, topk)
     same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), ei.tolist())])
     say(f"[gpu]   candidates {st['submitted']} of {sum(len(c) for c in cands)}, top-k overlap {same:.4f}")
+    assert same >= 0.99, same
+
+
+@pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
+@pytest.mark.parametrize("topk", [10, 100])
+def test_staged_vanguard_pool_overflow(case_name, topk, request, monkeypatch):
+    """The staged vanguard pass with per-query regions too small for many queries: the
+    queries whose seeds or candidate list do not fit are listed and run by the one-pass
+    kernel afterwards; every query still gets its GPU threshold, and the top-k matches the
+    staged pass with regions that fit (frozen thresholds, GPU-seeded test mode)."""
+    nprobe, vanguard = 16, 5
+    case = request.getfixturevalue(case_name)
+    nq = case.queries.shape[0]
+    flags = ca.FLAG_GPU_SEED_FROZEN | ca.FLAG_VANGUARD_MFMA
+    say(f"[gpu] staged vanguard pass, pool overflow, {case_name} top-{topk}")
+    eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True, extra_flags=flags)
+    eng.reset_buffer(case.queries)
+    d0, i0 = eng.search(case.queries, topk, nprobe)
+    st0 = eng.stats()
+    counts0 = eng.debug_read(ca.DBG_STAGED_COUNTS, (4,), np.uint64)
+    eng.close()
+    assert st0["vanguard_mode"] == 4
+    # every query's seeds and list fit their regions: each refined vector is a seed or listed
+    assert counts0[3] == 0 and counts0[0] + counts0[1] == st0["gpu_refined"], counts0
+    # regions of 128 entries: top-100 seeds (at least 200) do not fit
+    monkeypatch.setenv("CORA_VANGUARD_REGION_CAP", "128")
+    eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True, extra_flags=flags)
+    eng.reset_buffer(case.queries)
+    d1, i1 = eng.search(case.queries, topk, nprobe)
+    st1 = eng.stats()
+    counts1 = eng.debug_read(ca.DBG_STAGED_COUNTS, (4,), np.uint64)
+    eng.close()
+    say(f"[gpu]   queries left to the one-pass kernel: {counts1[3]} of {nq}")
+    if topk == 100:
+        assert counts1[3] > 0, counts1
+    assert st1["vanguard_mode"] == 4 and st1["seeded_queries"] == nq
+    # the two passes refine the same vectors below the final threshold; they differ only on
+    # the rare vector whose lower bound misses (above its refined distance)
+    same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i1.tolist(), i0.tolist())])
+    say(f"[gpu]   top-k overlap with the pool that fits {same:.4f}")
     assert same >= 0.99, same
 
 
