@@ -231,29 +231,6 @@ __device__ __forceinline__ float excode_group_ip(const uint2 (&grp)[7], const fl
     return sum;
 }
 
-// The slice of 64-dimension group g of a refinement record (engine_internal.h) in 16 words:
-// words 0..13 the group's seven 8-byte ex-code words, words 14 and 15 sign-code words 2g and
-// 2g + 1. Loaded as four 16-byte chunks; the lanes that load the slices of the G groups of
-// one vector read 16 G contiguous bytes per load.
-struct GroupSlice {
-    uint32_t d[16];
-    __device__ __forceinline__ void load(const uint8_t *rec, uint32_t G, uint32_t g) {
-#pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) {
-            const uint4 v = gload<uint4>(rec + 16 * (G * k + g));
-            d[4 * k] = v.x;
-            d[4 * k + 1] = v.y;
-            d[4 * k + 2] = v.z;
-            d[4 * k + 3] = v.w;
-        }
-    }
-    __device__ __forceinline__ void group(uint2 (&w)[7]) const {
-#pragma unroll
-        for (int k = 0; k < 7; ++k)
-            w[k] = make_uint2(d[2 * k], d[2 * k + 1]);
-    }
-    __device__ __forceinline__ uint32_t sign_word(int e) const { return d[14 + e]; }
-};
 
 // Refined distance of a candidate (cpu_refinement.cpp:183-192) from the HBM copy of the
 // ex-codes, evaluated by one lane, and a bound on its rounding difference from the CPU

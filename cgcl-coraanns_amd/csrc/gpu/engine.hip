@@ -939,7 +939,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // the fused select keeps its candidates in the distance matrix's memory
     const bool fused_probe = split_probe && !(a->flags & CORA_FLAG_UNFUSED_PROBE) &&
                              fused_probe_supported((uint32_t)E->nl, np) &&
-                             fused_probe_scratch_bytes(nq, (uint32_t)E->nl) <= (size_t)nq * E->nl * sizeof(float);
+                             fused_probe_scratch_bytes(nq, (uint32_t)E->nl, np) <= (size_t)nq * E->nl * sizeof(float);
     E->last_fused_probe = fused_probe;
     // queries uploaded in slices (cora_gpu_reset): each slice is rotated, prepared and probed
     // by the fused GEMM as soon as it has landed; every other path waits for the whole upload
@@ -976,7 +976,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
                 HIPCHK(hipEventRecord(E->ev_pg[i][0], s));
             launch_fused_probe_gemm_rows(E->d_q_hl, E->d_q_hl + (size_t)nq * P, E->d_qscale, E->d_qnorm,
                                          E->d_cent_hl, E->d_cscale, E->d_cnorm, r0, rows, nq, (uint32_t)E->nl, P,
-                                         E->d_dist, s);
+                                         np, E->d_dist, s);
             if (timing)
                 HIPCHK(hipEventRecord(E->ev_pg[i][1], s));
         }
@@ -1004,7 +1004,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
             launch_split_f16(E->d_qrot, nq, P, E->d_q_hl, E->d_qscale, s);
             if (fused_probe)
                 launch_fused_probe_gemm(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
-                                        nq, (uint32_t)E->nl, P, E->d_dist, E->d_probe_fb, s);
+                                        nq, (uint32_t)E->nl, P, np, E->d_dist, E->d_probe_fb, s);
             else
                 launch_dist_gemm_f16x3(E->d_q_hl, E->d_qscale, E->d_qnorm, E->d_cent_hl, E->d_cscale, E->d_cnorm,
                                        nq, (uint32_t)E->nl, P, E->d_dist, s);

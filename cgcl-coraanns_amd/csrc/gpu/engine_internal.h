@@ -34,30 +34,21 @@ constexpr uint64_t kLowsMinIndexBytes = 256ull << 20;
 constexpr uint32_t kLowsMinDim = 512;
 
 // Refinement record of one vector (cluster order), ex_record_bytes(P) = P + 16 bytes, so a
-// refined vector is one contiguous read: the packed 7-bit ex-code (P*7/8 bytes in 64-dimension
-// groups of 56 bytes, the reference's packing, pack_excode.hpp:216-265) and the sign code (P/8
-// bytes, the tiles' words: dimension 32w+l at bit l of word w), then f_add_ex, f_rescale_ex
-// and 8 bytes of padding (16-byte aligned records).
-//
-// The first P bytes are split by 64-dimension group g = 0 .. G - 1 (G = P / 64): the 64 bytes
-// of group g ("its slice": the group's 56 ex-code bytes, then sign-code words 2g and 2g + 1)
-// are four 16-byte chunks, chunk k at byte 16 (G k + g). A kernel that refines one vector with
-// one lane per group (or one lane per few groups) loads a slice as four 16-byte loads, and the
-// G lanes of a vector then read 16 G contiguous bytes per load.
+// refined vector is one contiguous read: the packed 7-bit ex-code (P*7/8 bytes, 64-dimension
+// group g at bytes 56g .. 56g + 55, the reference's packing, pack_excode.hpp:216-265), its sign
+// code (P/8 bytes at P*7/8, the tiles' words: dimension 32w+l at bit l of word w), f_add_ex and
+// f_rescale_ex at P, and 8 bytes of padding (16-byte aligned records). The readers address it
+// through the functions below. (Records with each lane's bytes interleaved in 16-byte chunks,
+// per 4-lane split or per 64-dimension group, were measured slower for the refinement kernels
+// at P = 768: 1.39 and 1.60 ms against 1.27 ms.)
 __host__ __device__ constexpr uint32_t ex_record_bytes(uint32_t P) { return P + 16; }
 __host__ __device__ constexpr uint32_t ex_record_groups(uint32_t P) { return P / 64; }
-// byte b (0..63) of group g's slice
-__host__ __device__ constexpr uint32_t ex_record_slice_byte(uint32_t P, uint32_t g, uint32_t b) {
-    return 16 * (ex_record_groups(P) * (b / 16) + g) + b % 16;
-}
 // 8-byte word kk (0..6) of 64-dimension ex-code group g
 __host__ __device__ constexpr uint32_t ex_record_group_word(uint32_t P, uint32_t g, uint32_t kk) {
-    return ex_record_slice_byte(P, g, 8 * kk);
+    return 56 * g + 8 * kk;
 }
-// sign-code word w (in the slice of group w / 2)
-__host__ __device__ constexpr uint32_t ex_record_sign_word(uint32_t P, uint32_t w) {
-    return ex_record_slice_byte(P, w / 2, 56 + 4 * (w % 2));
-}
+// sign-code word w (words 2g, 2g + 1 hold group g's dimensions, an aligned 8-byte pair)
+__host__ __device__ constexpr uint32_t ex_record_sign_word(uint32_t P, uint32_t w) { return P * 7 / 8 + 4 * w; }
 __host__ __device__ constexpr uint32_t ex_record_factor_offset(uint32_t P) { return P; }
 
 struct ClusterMeta {
@@ -301,23 +292,26 @@ void launch_rotate_f16x3_rows(const uint16_t *xhi, const uint16_t *xlo, const fl
 void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const float *qnorm,
                             const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t nq,
                             uint32_t nl, uint32_t P, float *dist, hipStream_t s);
-// Fused coarse-probe select (nl >= 8,192, nprobe <= 64, nl <= kFusedProbeMaxList): the split-FP16
-// distance GEMM keeps 8 candidate keys per query and 128-cluster tile in scratch (the distance
-// matrix's memory: at least fused_probe_scratch_bytes, and nq x nl floats for the fallback);
+// Fused coarse-probe select (fused_probe_supported: nl >= 8,192, nl <= kFusedProbeMaxList, and
+// nprobe <= 64, or up to 1,024 while a 128-cluster tile holds at most ~4.5 probes on average):
+// the split-FP16 distance GEMM keeps fused_probe_slots(nprobe) (8 or 16) candidate keys per
+// query and 128-cluster tile in scratch (the distance matrix's memory: at least
+// fused_probe_scratch_bytes, and nq x nl floats for the fallback);
 // the select part merges them into the top-nprobe idx, and the queries the candidates cannot
 // settle (fb: 1 + nq words, [0] their count, then their rows) are selected again from their
 // distance rows, computed again into the same scratch.
 constexpr uint32_t kFusedProbeMaxList = 65536;
 bool fused_probe_supported(uint32_t nl, uint32_t nprobe);
-size_t fused_probe_scratch_bytes(uint32_t nq, uint32_t nl);
+uint32_t fused_probe_slots(uint32_t nprobe);
+size_t fused_probe_scratch_bytes(uint32_t nq, uint32_t nl, uint32_t nprobe);
 void launch_fused_probe_gemm(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
                              const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
-                             void *scratch, uint32_t *fb, hipStream_t s);
+                             uint32_t nprobe, void *scratch, uint32_t *fb, hipStream_t s);
 // the GEMM part for query rows [r0, r0 + rows) of qhi / qlo ([nq][P] each); fb is not touched
 void launch_fused_probe_gemm_rows(const uint16_t *qhi, const uint16_t *qlo, const float *qscale, const float *qnorm,
                                   const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t r0,
-                                  uint32_t rows, uint32_t nq, uint32_t nl, uint32_t P, void *scratch,
-                                  hipStream_t s);
+                                  uint32_t rows, uint32_t nq, uint32_t nl, uint32_t P, uint32_t nprobe,
+                                  void *scratch, hipStream_t s);
 void launch_fused_probe_select(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
                                const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
                                uint32_t nprobe, void *scratch, uint32_t *fb, int32_t *idx, hipStream_t s);

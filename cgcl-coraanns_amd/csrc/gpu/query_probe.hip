@@ -316,16 +316,18 @@ __device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t x)
 }
 
 // Fused probe select: the GEMM epilogue keeps, per query row and 128-cluster tile, the
-// kProbeSlots smallest (distance, cluster) keys, compared on the order key with its low 7 bits
+// kSlots smallest (distance, cluster) keys (kProbeSlots, or kProbeSlotsWide for larger
+// nprobe), compared on the order key with its low 7 bits
 // replaced by the column in the tile (so the 128 keys of a row are distinct 32-bit values
 // and the comparison is one v_med3 per slot); the exact keys of the kept columns are stored.
-constexpr int kProbeSlots = 8;  // a power of two
+constexpr int kProbeSlots = 8;       // a power of two
+constexpr int kProbeSlotsWide = 16;  // nprobe above 64: up to ~4.5 probes per 128-cluster tile
 constexpr int kEs = kHT + 4;  // LDS row stride (floats) of the epilogue's half tile: no bank conflicts
 
 // kMode 0: C = A . B^T (the query rotation Q . R with B = R^T). kMode 1: the distance matrix
 // an[m] + bn[n] - 2 <a_m, b_n> (coarse probe). kMode 2: the same distances reduced in the
-// epilogue to each row's kProbeSlots smallest keys per 128-column tile, written to
-// cand [M][ntiles][kProbeSlots] as (order key << 32 | column) (the distance matrix is not
+// epilogue to each row's kSlots smallest keys per 128-column tile, written to
+// cand [M][ntiles][kSlots] as (order key << 32 | column) (the distance matrix is not
 // written). kMode 3: distance rows of selected operand rows: output row m is A's row rmap[m],
 // for m < *mcount (at most M), the grid's row tiles sweeping them mstep rows at a time.
 // A [M][K] and B [N][K] are split-FP16 rows (Ah/Al, scale as; Bh/Bl, scale bs);
@@ -338,7 +340,7 @@ constexpr int kEs = kHT + 4;  // LDS row stride (floats) of the epilogue's half 
 // D[4 (l / 16) + r][l % 16]. Tile order: XCD x (blockIdx.x % 8) owns column tiles
 // [x ncx, (x + 1) ncx), swept by groups of four row tiles, so the workgroups resident on
 // an XCD share their operand tiles in its L2.
-template <int kMode>
+template <int kMode, int kSlots = kProbeSlots>
 __global__ __launch_bounds__(256, 3) void dist_gemm_f16x3_kernel(
     const _Float16 *__restrict__ Ah, const _Float16 *__restrict__ Al, const float *__restrict__ as,
     const _Float16 *__restrict__ Bh, const _Float16 *__restrict__ Bl, const float *__restrict__ bs,
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(256, 3) void dist_gemm_f16x3_kernel(
                 }
         } else {
             // one half tile (64 rows x 128 columns) at a time through the LDS; four threads per
-            // row each take the columns eq, eq + 4, ... and keep their kProbeSlots smallest
+            // row each take the columns eq, eq + 4, ... and keep their kSlots smallest
             // packed keys (sorted, one v_med3 per slot and column), then the row's four
             // threads merge their lists by shuffles; thread eq stores slots eq, eq + 4, ...
             float *Et = reinterpret_cast<float *>(s_raw);
@@ -475,34 +477,34 @@ __global__ __launch_bounds__(256, 3) void dist_gemm_f16x3_kernel(
                 }
                 __syncthreads();
                 const float *erow = Et + er * kEs;
-                uint32_t t[kProbeSlots];
+                uint32_t t[kSlots];
 #pragma unroll
-                for (int sl = 0; sl < kProbeSlots; ++sl)
+                for (int sl = 0; sl < kSlots; ++sl)
                     t[sl] = ~0u;
 #pragma unroll 2
                 for (int j = 0; j < kHT / 4; ++j) {
                     const uint32_t col = eq + 4 * j;
                     const uint32_t x = n0 + col < N ? (order_key(erow[col]) & ~127u) | col : ~0u;
 #pragma unroll
-                    for (int sl = kProbeSlots - 1; sl > 0; --sl)
+                    for (int sl = kSlots - 1; sl > 0; --sl)
                         t[sl] = med3_u32(t[sl - 1], t[sl], x);
                     t[0] = min(t[0], x);
                 }
 #pragma unroll
                 for (int o = 1; o < 4; o <<= 1) {
-                    // the kProbeSlots smallest of two sorted lists: the partner's reversed
+                    // the kSlots smallest of two sorted lists: the partner's reversed
                     // against ours gives a bitonic sequence holding them, which is then sorted
-                    uint32_t p[kProbeSlots];
+                    uint32_t p[kSlots];
 #pragma unroll
-                    for (int sl = 0; sl < kProbeSlots; ++sl)
+                    for (int sl = 0; sl < kSlots; ++sl)
                         p[sl] = __shfl_xor(t[sl], o);
 #pragma unroll
-                    for (int sl = 0; sl < kProbeSlots; ++sl)
-                        t[sl] = min(t[sl], p[kProbeSlots - 1 - sl]);
+                    for (int sl = 0; sl < kSlots; ++sl)
+                        t[sl] = min(t[sl], p[kSlots - 1 - sl]);
 #pragma unroll
-                    for (int st = kProbeSlots / 2; st > 0; st >>= 1)
+                    for (int st = kSlots / 2; st > 0; st >>= 1)
 #pragma unroll
-                        for (int sl = 0; sl < kProbeSlots; ++sl)
+                        for (int sl = 0; sl < kSlots; ++sl)
                             if ((sl & st) == 0) {
                                 const uint32_t a = t[sl], b = t[sl + st];
                                 t[sl] = min(a, b);
@@ -511,15 +513,15 @@ __global__ __launch_bounds__(256, 3) void dist_gemm_f16x3_kernel(
                 }
                 const uint32_t gm = m0 + h * 64 + er;
 #pragma unroll
-                for (int u = 0; u < kProbeSlots / 4; ++u) {
+                for (int u = 0; u < kSlots / 4; ++u) {
                     const int slot = eq + 4 * u;
                     uint32_t mine = t[0];
 #pragma unroll
-                    for (int sl = 1; sl < kProbeSlots; ++sl)
+                    for (int sl = 1; sl < kSlots; ++sl)
                         mine = sl == slot ? t[sl] : mine;
                     const uint32_t col = mine & 127u;
                     if (gm < Me)
-                        cand[((size_t)gm * ntiles + tile) * kProbeSlots + slot] =
+                        cand[((size_t)gm * ntiles + tile) * kSlots + slot] =
                             n0 + col < N ? ((unsigned long long)order_key(erow[col]) << 32) | (n0 + col) : ~0ull;
                 }
             }
@@ -1056,6 +1058,129 @@ __global__ __launch_bounds__(64 * kMergeWaves) void probe_merge_kernel(
         fb_rows[atomicAdd(fb_count, 1u)] = q;
 }
 
+// Fused probe select, second half for nprobe above 64 (kProbeSlotsWide keys per tile), one
+// workgroup per query. The k-th smallest order key T among the candidates is found bit by bit
+// from the top (each step counts the keys at or below a trial value over the workgroup; the
+// order keys are held in registers, 32 a thread); every candidate whose order key is at most
+// T (k of them, plus the ties of T) is compacted into LDS and sorted by (order key, cluster),
+// and the first k are the result, ties falling to the lower cluster id. The proof and the
+// fallback are those of probe_merge_kernel: more than kMergeBigCap keys at or below T, or a
+// tile whose last kept key, truncated, lies at or below T, send the query to the fallback list.
+constexpr uint32_t kMergeBigThreads = 256;
+constexpr uint32_t kMergeBigPer = 32;  // candidate keys per thread: 512 tiles x 16 slots
+constexpr uint32_t kMergeBigCap = 2048;
+constexpr uint32_t kMergeBigMaxProbe = 1024;
+
+template <int kSlots>
+__global__ __launch_bounds__(kMergeBigThreads) void probe_merge_big_kernel(
+    const unsigned long long *__restrict__ cand, uint32_t nq, uint32_t ntiles, uint32_t k,
+    int32_t *__restrict__ idx, uint32_t *__restrict__ fb_count, uint32_t *__restrict__ fb_rows) {
+    __shared__ unsigned long long s_sel[kMergeBigCap];
+    __shared__ uint32_t s_red[2][kMergeBigThreads / 64];
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t q = blockIdx.x;
+    const unsigned long long *cq = cand + (size_t)q * ntiles * kSlots;
+    const uint32_t n = ntiles * kSlots;  // <= kMergeBigPer * kMergeBigThreads (checked by the launcher)
+    uint32_t hk[kMergeBigPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kMergeBigPer; ++r) {
+        const uint32_t i = r * kMergeBigThreads + t;
+        hk[r] = i < n ? (uint32_t)(cq[i] >> 32) : ~0u;  // an empty slot's key is ~0
+    }
+    // the workgroup's count of keys at or below x (one barrier; the two halves of s_red
+    // alternate between consecutive calls)
+    uint32_t parity = 0;
+    auto count_le = [&](uint32_t x, bool strict) -> uint32_t {
+        uint32_t c = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < kMergeBigPer; ++r)
+            c += hk[r] != ~0u && (strict ? hk[r] < x : hk[r] <= x) ? 1u : 0u;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+            c += __shfl_xor(c, o);
+        if (lane == 0)
+            s_red[parity][wave] = c;
+        __syncthreads();
+        uint32_t all = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kMergeBigThreads / 64; ++w)
+            all += s_red[parity][w];
+        parity ^= 1u;
+        return all;
+    };
+    uint32_t T = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t trial = T | ((1u << bit) - 1u);
+        if (count_le(trial, false) < k)
+            T |= 1u << bit;
+    }
+    const uint32_t n_le = count_le(T, false);
+    bool fallback = n_le > kMergeBigCap;
+    if (!fallback) {
+        // compact the keys at or below T (thread order), then sort them
+        uint32_t mine = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < kMergeBigPer; ++r)
+            mine += hk[r] != ~0u && hk[r] <= T ? 1u : 0u;
+        uint32_t x = mine;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(x, o);
+            if (lane >= (uint32_t)o)
+                x += y;
+        }
+        if (lane == 63)
+            s_red[parity][wave] = x;
+        __syncthreads();
+        uint32_t pos = x - mine;
+        for (uint32_t w = 0; w < wave; ++w)
+            pos += s_red[parity][w];
+#pragma unroll
+        for (uint32_t r = 0; r < kMergeBigPer; ++r) {
+            const uint32_t i = r * kMergeBigThreads + t;
+            if (hk[r] != ~0u && hk[r] <= T) {
+                const unsigned long long key = cq[i];
+                s_sel[pos++] = (key & 0xFFFFFFFF00000000ull) | (uint32_t)key;
+            }
+        }
+        uint32_t m = 1;
+        while (m < n_le)
+            m <<= 1;
+        for (uint32_t i = n_le + t; i < m; i += kMergeBigThreads)
+            s_sel[i] = ~0ull;
+        __syncthreads();
+        for (uint32_t size = 2; size <= m; size <<= 1)
+            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                for (uint32_t i = t; i < m; i += kMergeBigThreads) {
+                    const uint32_t j = i ^ stride;
+                    if (j > i) {
+                        const bool asc = (i & size) == 0;
+                        const unsigned long long a = s_sel[i], b = s_sel[j];
+                        if ((a > b) == asc) {
+                            s_sel[i] = b;
+                            s_sel[j] = a;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        // proven unless a tile dropped a column whose truncated key is at most the k-th's
+        const uint32_t kth_key = (uint32_t)(s_sel[k - 1] >> 32);
+        bool open = false;
+        for (uint32_t tl = t; tl < ntiles; tl += kMergeBigThreads) {
+            const unsigned long long last = cq[(size_t)tl * kSlots + kSlots - 1];
+            open |= last != ~0ull && ((uint32_t)(last >> 32) & ~127u) <= kth_key;
+        }
+        fallback = __syncthreads_or(open) != 0;
+        if (!fallback)
+            for (uint32_t i = t; i < k; i += kMergeBigThreads)
+                idx[(size_t)q * k + i] = (int32_t)(uint32_t)(s_sel[i] & 0xFFFFFFFFull);
+    }
+    if (fallback && t == 0)
+        fb_rows[atomicAdd(fb_count, 1u)] = q;
+    (void)nq;
+}
+
 // The fallback rows of the fused select: row r of dist (the distances of query rows[r],
 // computed again) through the generic block select, rows swept by the grid.
 __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(const float *__restrict__ dist, uint32_t nl,
@@ -1569,13 +1694,23 @@ void launch_dist_gemm_f16x3(const uint16_t *qhl, const float *qscale, const floa
 }
 
 bool fused_probe_supported(uint32_t nl, uint32_t nprobe) {
-    // the merge's bound takes the k-th of 64 lane minima (k <= 64, every lane a tile); the
-    // candidates (nl / 32 keys per query) fit in the distance matrix they replace
-    return nprobe >= 1 && nprobe <= 64 && nl >= 64 * kHT && nl <= kFusedProbeMaxList;
+    // nprobe <= 64: the merge's bound takes the k-th of 64 lane minima (every lane a tile);
+    // above, kProbeSlotsWide slots a tile while the tiles hold at most ~4.5 probes each on
+    // average (nl / 8 keys per query), and the large-k merge's limits. The candidates fit in
+    // the distance matrix they replace.
+    if (nprobe < 1 || nl < 64 * kHT || nl > kFusedProbeMaxList)
+        return false;
+    if (nprobe <= 64)
+        return true;
+    const uint64_t ntiles = (nl + kHT - 1) / kHT;
+    return nprobe <= kMergeBigMaxProbe && (uint64_t)nprobe * 2 * kHT <= 9ull * nl &&
+           ntiles * kProbeSlotsWide <= (uint64_t)kMergeBigPer * kMergeBigThreads;
 }
 
-size_t fused_probe_scratch_bytes(uint32_t nq, uint32_t nl) {
-    return (size_t)nq * ((nl + kHT - 1) / kHT) * kProbeSlots * sizeof(unsigned long long);
+uint32_t fused_probe_slots(uint32_t nprobe) { return nprobe <= 64 ? kProbeSlots : kProbeSlotsWide; }
+
+size_t fused_probe_scratch_bytes(uint32_t nq, uint32_t nl, uint32_t nprobe) {
+    return (size_t)nq * ((nl + kHT - 1) / kHT) * fused_probe_slots(nprobe) * sizeof(unsigned long long);
 }
 
 namespace {
@@ -1591,29 +1726,36 @@ struct FusedGeometry {
 
 void launch_fused_probe_gemm(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
                              const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
-                             void *scratch, uint32_t *fb, hipStream_t s) {
+                             uint32_t nprobe, void *scratch, uint32_t *fb, hipStream_t s) {
     if (!nq)
         return;
     // fb: [0] the fallback count, [1 .. nq] the fallback query rows
     launch_fill_u32(fb, 0u, 1, s);
     launch_fused_probe_gemm_rows(qhl, qhl + (size_t)nq * P, qscale, qnorm, chl, cscale, cnorm, 0, nq, nq, nl, P,
-                                 scratch, s);
+                                 nprobe, scratch, s);
 }
 
 void launch_fused_probe_gemm_rows(const uint16_t *qhi, const uint16_t *qlo, const float *qscale, const float *qnorm,
                                   const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t r0,
-                                  uint32_t rows, uint32_t nq, uint32_t nl, uint32_t P, void *scratch,
-                                  hipStream_t s) {
+                                  uint32_t rows, uint32_t nq, uint32_t nl, uint32_t P, uint32_t nprobe,
+                                  void *scratch, hipStream_t s) {
     if (!rows)
         return;
     // rows [r0, r0 + rows) of the [nq] query operands, as a GEMM of its own whose candidate
-    // keys land in those rows of the [nq][nct][kProbeSlots] candidate array
+    // keys land in those rows of the [nq][nct][slots] candidate array
     const FusedGeometry f(qhi, chl, rows, nl);
     const _Float16 *lo = reinterpret_cast<const _Float16 *>(qlo);
-    dist_gemm_f16x3_kernel<2><<<kNumXcd * f.ncx * 4 * f.groups, 256, 0, s>>>(
-        f.qh + (size_t)r0 * P, lo + (size_t)r0 * P, qscale + r0, f.ch, f.ch + (size_t)nl * P, cscale, nullptr, rows,
-        nl, P, qnorm + r0, cnorm, f.ncx, f.groups * 4 * kHT, nullptr, nullptr,
-        static_cast<unsigned long long *>(scratch) + (size_t)r0 * f.nct * kProbeSlots, f.nct);
+    const uint32_t slots = fused_probe_slots(nprobe);
+    auto *cand = static_cast<unsigned long long *>(scratch) + (size_t)r0 * f.nct * slots;
+    const dim3 grid(kNumXcd * f.ncx * 4 * f.groups);
+    if (slots == kProbeSlots)
+        dist_gemm_f16x3_kernel<2, kProbeSlots><<<grid, 256, 0, s>>>(
+            f.qh + (size_t)r0 * P, lo + (size_t)r0 * P, qscale + r0, f.ch, f.ch + (size_t)nl * P, cscale, nullptr,
+            rows, nl, P, qnorm + r0, cnorm, f.ncx, f.groups * 4 * kHT, nullptr, nullptr, cand, f.nct);
+    else
+        dist_gemm_f16x3_kernel<2, kProbeSlotsWide><<<grid, 256, 0, s>>>(
+            f.qh + (size_t)r0 * P, lo + (size_t)r0 * P, qscale + r0, f.ch, f.ch + (size_t)nl * P, cscale, nullptr,
+            rows, nl, P, qnorm + r0, cnorm, f.ncx, f.groups * 4 * kHT, nullptr, nullptr, cand, f.nct);
     (void)nq;
 }
 
@@ -1623,8 +1765,12 @@ void launch_fused_probe_select(const uint16_t *qhl, const float *qscale, const f
     if (!nq)
         return;
     const FusedGeometry f(qhl, chl, nq, nl);
-    probe_merge_kernel<<<(nq + kMergeWaves - 1) / kMergeWaves, 64 * kMergeWaves, 0, s>>>(
-        static_cast<const unsigned long long *>(scratch), nq, f.nct, nprobe, idx, fb, fb + 1);
+    if (fused_probe_slots(nprobe) == kProbeSlots)
+        probe_merge_kernel<<<(nq + kMergeWaves - 1) / kMergeWaves, 64 * kMergeWaves, 0, s>>>(
+            static_cast<const unsigned long long *>(scratch), nq, f.nct, nprobe, idx, fb, fb + 1);
+    else
+        probe_merge_big_kernel<kProbeSlotsWide><<<nq, kMergeBigThreads, 0, s>>>(
+            static_cast<const unsigned long long *>(scratch), nq, f.nct, nprobe, idx, fb, fb + 1);
     // fallback: those rows again as a distance matrix (the candidates are no longer needed, so
     // it takes their memory), a grid of up to kFallbackRowTiles row tiles sweeping the *fb rows
     const uint32_t fgroups = min(f.groups, (uint32_t)kFallbackRowTiles / 4);

@@ -37,7 +37,6 @@
 // reject.
 #include <float.h>
 
-#include <algorithm>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -264,16 +263,13 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
     // workgroup b runs on XCD b % 8 and takes the (b / 8)-th query of that XCD's slice of
     // the queries ordered by nearest cluster, so each XCD's L2 serves about an eighth of
     // the clusters
-    // list mode: workgroup b takes list entries b, b + grid, ... in turn
-    uint32_t list_idx = blockIdx.x;
-next_query:
     uint32_t qi;
     if (va.list) {
-        // the queries of a device-side list (the staged pass's overflow)
-        if (list_idx >= *va.list_count)
+        // list mode: workgroup b takes entry b of a device-side list of queries (the staged
+        // pass's overflow), the grid sized for the longest list; the others return at once
+        if (blockIdx.x >= *va.list_count)
             return;
-        qi = va.list[list_idx];
-        list_idx += gridDim.x;
+        qi = va.list[blockIdx.x];
     } else {
         const uint32_t per_xcd = (va.nq + kNumXcd - 1) / kNumXcd;
         const uint32_t slot = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
@@ -443,15 +439,21 @@ next_query:
                         uint2 grp[kG][7];
                         float fa = 0.0f, fr = 0.0f;
                         if (have) {
-                            // the slices of the lane's groups sub, sub + 4, ...: their
-                            // ex-code words and sign-code words 2 (sub + 4 gi) + e
+                            // sign-code words sub kWq .. sub kWq + kWq - 1, in 8-byte pairs
+                            const uint2 *wp = reinterpret_cast<const uint2 *>(rec + ex_record_sign_word(P, sub * kWq));
+#pragma unroll
+                            for (int i = 0; i < kWq / 2; ++i) {
+                                const uint2 v = wp[i];
+                                xw[2 * i] = v.x;
+                                xw[2 * i + 1] = v.y;
+                            }
 #pragma unroll
                             for (int gi = 0; gi < kG; ++gi) {
-                                GroupSlice sl;
-                                sl.load(rec, W / 2, sub + 4 * gi);
-                                sl.group(grp[gi]);
-                                xw[2 * gi] = sl.sign_word(0);
-                                xw[2 * gi + 1] = sl.sign_word(1);
+                                const uint2 *gp =
+                                    reinterpret_cast<const uint2 *>(rec + ex_record_group_word(P, sub + 4 * gi, 0));
+#pragma unroll
+                                for (int k = 0; k < 7; ++k)
+                                    grp[gi][k] = gp[k];
                             }
                             if (sub == 0) {
                                 const float2 f = *reinterpret_cast<const float2 *>(rec + P);
@@ -464,7 +466,7 @@ next_query:
                         if (have) {
 #pragma unroll
                             for (int i = 0; i < kWq; ++i) {
-                                const uint32_t w = 2 * (sub + 4 * (i / 2)) + (i % 2);
+                                const uint32_t w = sub * kWq + i;
 #pragma unroll
                                 for (int b = 0; b < kBq - 1; ++b) {
                                     ipa += __popc(xw[i] & planes[b * W + w]) << b;
@@ -889,18 +891,12 @@ next_query:
             atomicAdd(va.seeded, 1ull);
         }
     }
-    if (va.list) {
-        __syncthreads();  // the next query reuses the LDS
-        goto next_query;
-    }
 }
 
 template <int W>
 void launch_vq_w(const ScanParams &p, const VanguardArgs &va, uint32_t nq, hipStream_t s) {
     const size_t dyn = (size_t)p.P * sizeof(float);
-    uint32_t grid = (nq + kNumXcd - 1) / kNumXcd * kNumXcd;
-    if (va.list)  // the listed queries are taken in turn by about the resident workgroups
-        grid = std::min<uint32_t>(grid, 512);
+    const uint32_t grid = (nq + kNumXcd - 1) / kNumXcd * kNumXcd;
     if (va.lows_ready)
         vanguard_query_kernel<W, true><<<grid, kVqThreads, dyn, s>>>(p, va);
     else

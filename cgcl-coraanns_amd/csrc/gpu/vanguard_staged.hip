@@ -436,205 +436,165 @@ __global__ __launch_bounds__(kVsThreads) void vs_seed_kernel(const ScanParams p,
 }
 
 // ---- 2. and 4. refinement ----
-// One lane per 64-dimension group: a wave refines kR = 64 / G entries of one query at a time
-// (G = W / 2 groups; the lanes past kR G idle), the lane of group g reading that group's slice
-// of the entry's refinement record (four 16-byte loads) and holding the query's q' over the
-// group (64 floats) and the group's Bq=8 and residual plane words (2 x 16) in registers for
-// all of the query's rounds, so a round is loads, then register arithmetic, then a reduction
-// over the entry's G lanes. The waves work independently, each on a contiguous range of
-// (query, round) slots, the queries taken in the order of their nearest cluster (va.order);
-// workgroup b runs on XCD b % 8 and each XCD takes an eighth of that order, so an XCD's waves
-// refine vectors of nearby clusters at the same time. The next round's loads are issued before
-// a round is computed.
+// L lanes per entry (L = min(4, G), G = W / 2 groups of 64 dimensions): lane sub reads the
+// sign-code words [sub W/L, (sub + 1) W/L) and the ex-code groups sub, sub + L, ... of the
+// entry's refinement record (8-byte loads), all before any arithmetic; q' and the Bq=8 and
+// residual planes are read from LDS. A chunk of 256 / L entries is one round of the
+// workgroup.
 template <int W>
 struct VsShape {
-    static constexpr int kG = W / 2;      // 64-dimension groups, lanes per entry
-    static constexpr int kR = 64 / kG;    // entries per wave and round
-};
-
-// Sum over the G lanes of each entry (entry r on lanes [r G, r G + G)); lane r G gets it.
-template <int G, class T>
-__device__ __forceinline__ T entry_sum(T v, uint32_t lane) {
-    if constexpr ((G & (G - 1)) == 0) {
-#pragma unroll
-        for (int o = 1; o < G; o <<= 1)
-            v += __shfl_xor(v, o, G);
-    } else {
-        static_assert(G == 12, "entry width");
-        v += __shfl(v, (int)lane + 6);
-        v += __shfl(v, (int)lane + 3);
-        v += __shfl(v, (int)lane + 1) + __shfl(v, (int)lane + 2);
-    }
-    return v;
-}
-
-// <q', ex_code> of one group whose q' values are in registers (excode_group_ip's layout and
-// arithmetic), one 8-dimension step at a time.
-__device__ __forceinline__ float excode_group_ip_regs(const uint2 (&grp)[7], const float (&q)[64]) {
-    float sum = 0.0f;
-#pragma unroll
-    for (uint32_t k = 0; k < 8; ++k) {
-        uint32_t lo, hi;
-        if (k < 6) {
-            lo = grp[k].x & 0x3F3F3F3Fu;
-            hi = grp[k].y & 0x3F3F3F3Fu;
-        } else {
-            const uint32_t o = k - 6;
-            const uint2 a = grp[o], b = grp[2 + o], d = grp[4 + o];
-            lo = ((a.x >> 6) & 0x03030303u) | ((b.x >> 4) & 0x0C0C0C0Cu) | ((d.x >> 2) & 0x30303030u);
-            hi = ((a.y >> 6) & 0x03030303u) | ((b.y >> 4) & 0x0C0C0C0Cu) | ((d.y >> 2) & 0x30303030u);
-        }
-        lo |= ((grp[6].x >> k) & 0x01010101u) << 6;
-        hi |= ((grp[6].y >> k) & 0x01010101u) << 6;
-        // the step's conversions after the previous step's products: converted all at once,
-        // the group's 64 values would take 64 registers
-        asm volatile("" : "+v"(lo), "+v"(hi) : "v"(sum));
-        sum = fmaf((float)(lo & 0xFFu), q[8 * k], sum);
-        sum = fmaf((float)((lo >> 8) & 0xFFu), q[8 * k + 1], sum);
-        sum = fmaf((float)((lo >> 16) & 0xFFu), q[8 * k + 2], sum);
-        sum = fmaf((float)(lo >> 24), q[8 * k + 3], sum);
-        sum = fmaf((float)(hi & 0xFFu), q[8 * k + 4], sum);
-        sum = fmaf((float)((hi >> 8) & 0xFFu), q[8 * k + 5], sum);
-        sum = fmaf((float)((hi >> 16) & 0xFFu), q[8 * k + 6], sum);
-        sum = fmaf((float)(hi >> 24), q[8 * k + 7], sum);
-    }
-    return sum;
-}
-
-// One round's loads of a lane: its group's slice of the entry's record and, on the entry's
-// first lane, the ex-factors and the entry's lower bound.
-struct VsRound {
-    GroupSlice sl;
-    float fa, fr, low;
-    uint32_t j;
-    bool have;
+    static constexpr int kGroups = W / 2;  // 64-dimension groups
+    static constexpr int kLanes = kGroups >= 4 ? 4 : kGroups;
+    static constexpr int kGrp = kGroups / kLanes;  // groups per lane
+    static constexpr uint32_t kChunk = kVsThreads / kLanes;
+    static_assert(kGroups % kLanes == 0, "lane split");
 };
 
 template <int W>
-__global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(3))) void vs_refine_kernel(const ScanParams p, const VanguardArgs va,
+__global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >= 32 ? 3 : 4))) void vs_refine_kernel(const ScanParams p, const VanguardArgs va,
                                                                const VsArgs vs, uint32_t stage) {
-    constexpr int G = VsShape<W>::kG, R = VsShape<W>::kR;
-    constexpr uint32_t P = 32 * W;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t er = lane / G, g = lane % G;  // entry slot of the round, group
-    const bool lane_on = er < (uint32_t)R;
+    using S = VsShape<W>;
+    constexpr int L = S::kLanes, kG = S::kGrp, kW = 2 * S::kGrp;  // groups and sign-code words per lane
+    constexpr uint32_t P = 32 * W, E = S::kChunk;
+    __shared__ __align__(16) float s_q[P];
+    __shared__ uint32_t s_planes[2 * kBq * W];
+    __shared__ uint32_t s_start[kVanguardMaxPairs];
+    __shared__ float s_gadd[kVanguardMaxPairs];
+    __shared__ uint32_t s_red[kVsWaves];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t sub = tid % L, el = tid / L;
     const uint32_t cap = stage ? vs.list_cap : vs.seed_cap;
     const uint32_t *pos_r = stage ? vs.list_pos : vs.seed_pos;
     float2 *rd_r = stage ? vs.list_rd : vs.seed_rd;
     float2 *aux_r = stage ? vs.list_aux : vs.seed_aux;
     const uint32_t V = va.depth, stride = p.van_stride;
-    const uint32_t cpq = (cap + R - 1) / R;  // round slots per query
+    // a contiguous range of (query, chunk) slots per workgroup, cpq chunk slots per query, the
+    // queries taken in the order of their nearest cluster (va.order); workgroup b runs on XCD
+    // b % 8, and each XCD takes an eighth of that order, so an XCD's workgroups refine vectors
+    // of nearby clusters at the same time
+    const uint32_t cpq = (cap + E - 1) / E;
     const uint64_t nslots = (uint64_t)va.nq * cpq;
-    const uint32_t waves = gridDim.x * kVsWaves;
-    const uint64_t per = (nslots + waves - 1) / waves;
-    const uint32_t wg =
+    const uint64_t per = (nslots + gridDim.x - 1) / gridDim.x;
+    const uint32_t range =
         gridDim.x % kNumXcd == 0 ? (blockIdx.x % kNumXcd) * (gridDim.x / kNumXcd) + blockIdx.x / kNumXcd : blockIdx.x;
-    const uint64_t v_begin = (uint64_t)(wg * kVsWaves + wave) * per, v_end = min(nslots, v_begin + per);
+    const uint64_t v_begin = (uint64_t)range * per, v_end = min(nslots, v_begin + per);
     for (uint64_t v = v_begin; v < v_end;) {
         const uint32_t qs = (uint32_t)(v / cpq), c0 = (uint32_t)(v % cpq);
-        const uint32_t q = va.order ? gload<uint32_t>(va.order + qs) : qs;
+        const uint32_t q = va.order ? va.order[qs] : qs;
         const uint64_t q_end = (uint64_t)(qs + 1) * cpq;
-        const uint32_t flags = gload<uint32_t>(&vs.qs[q].flags);
-        const uint32_t n = (flags & kVsOverflow) ? 0u : gload<uint32_t>(stage ? &vs.qs[q].list_n : &vs.qs[q].seed_n);
-        const uint32_t c1 = (uint32_t)min<uint64_t>((n + R - 1) / R, min(q_end, v_end) - (uint64_t)qs * cpq);
+        const VsQuery st = vs.qs[q];
+        const uint32_t n = (st.flags & kVsOverflow) ? 0u : stage ? st.list_n : st.seed_n;
+        const uint32_t c1 = (uint32_t)min<uint64_t>((n + E - 1) / E, min(q_end, v_end) - (uint64_t)qs * cpq);
         v = q_end;
         if (c0 >= c1)
-            continue;  // nothing of this query in the range (wave-uniform)
-        // the query's q' over the lane's group, its plane words 2g, 2g + 1, sum |q'|, the
-        // vanguard pairs' first vectors and g_add (lane j holds pair j's), its scalars
-        float qv[64];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float4 x = gload<float4>(p.qrot + (size_t)q * P + 64 * g + 4 * i);
-            qv[4 * i] = x.x;
-            qv[4 * i + 1] = x.y;
-            qv[4 * i + 2] = x.z;
-            qv[4 * i + 3] = x.w;
-        }
-        uint32_t pl[2 * kBq][2];
-#pragma unroll
-        for (int b = 0; b < 2 * kBq; ++b) {
-            const uint2 x = gload<uint2>(p.qplanes + (size_t)q * 2 * kBq * W + b * W + 2 * g);
-            pl[b][0] = x.x;
-            pl[b][1] = x.y;
-        }
-        uint32_t start_l = 0;
-        float gadd_l = 0.0f;
-        if (lane < V) {
-            const size_t pi = (size_t)q * p.nprobe + lane;
-            start_l = gload<uint4>(p.meta + gload<int32_t>(va.probe_idx + pi)).x;
-            gadd_l = gload<float>(p.pgadd + pi);
-        }
+            continue;  // nothing of this query in the range (every thread reads the same)
+        // the query's q', Bq=8 and residual planes, pair constants and scalars, once every
+        // wave is done with the previous query's
+        __syncthreads();
         float l1p = 0.0f;
+        for (uint32_t i = tid; i < P; i += kVsThreads) {
+            const float x = p.qrot[(size_t)q * P + i];
+            s_q[i] = x;
+            l1p += fabsf(x);
+        }
+        for (uint32_t i = tid; i < 2 * kBq * W; i += kVsThreads)
+            s_planes[i] = p.qplanes[(size_t)q * 2 * kBq * W + i];
+        if (tid < V) {
+            const size_t pi = (size_t)q * p.nprobe + tid;
+            s_start[tid] = p.meta[va.probe_idx[pi]].start;
+            s_gadd[tid] = p.pgadd[pi];
+        }
 #pragma unroll
-        for (int i = 0; i < 64; ++i)
-            l1p += fabsf(qv[i]);
-        const float l1q = uniformf(__shfl(entry_sum<G>(l1p, lane), 0));
-        const float width = uniformf(gload<float>(p.qwidth + q)), width2 = uniformf(gload<float>(p.qwidth2 + q)),
-                    kbq = uniformf(gload<float>(p.kb + q));
-        const float *lows = p.van_lows + (size_t)q * V * stride;
-        const size_t ebase = (size_t)q * cap + er;
-        auto pos_of = [&](uint32_t c) -> uint32_t {
-            return lane_on && c < c1 && c * R + er < n ? gload<uint32_t>(pos_r + ebase + c * R) : ~0u;
-        };
-        auto issue = [&](uint32_t pos, VsRound &b) {
-            b.have = pos != ~0u;
-            b.j = b.have ? pos / stride : 0u;
-            const uint32_t start = __shfl(start_l, (int)b.j);
-            b.fa = b.fr = b.low = 0.0f;
-            if (b.have) {
-                const uint8_t *rec = p.ex_rec + ((size_t)start + (pos - b.j * stride)) * p.ex_stride;
-                b.sl.load(rec, G, g);
-                if (g == 0) {
+        for (int o = 32; o > 0; o >>= 1)
+            l1p += __shfl_xor(l1p, o);
+        if (lane == 0)
+            s_red[wave] = __float_as_uint(l1p);
+        __syncthreads();
+        float l1q = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kVsWaves; ++w)
+            l1q += __uint_as_float(s_red[w]);
+        const float width = p.qwidth[q], width2 = p.qwidth2[q], kbq = p.kb[q];
+        for (uint32_t c = c0; c < c1; ++c) {
+            const uint32_t idx = c * E + el;
+            const bool have = idx < n;
+            const size_t e = (size_t)q * cap + idx;
+            uint2 grp[kG][7];
+            uint32_t xw[kW];
+            float fa = 0.0f, fr = 0.0f, low = 0.0f;
+            uint32_t j = 0;
+            if (have) {
+                const uint32_t pos = pos_r[e];
+                j = pos / stride;
+                const size_t gid = (size_t)s_start[j] + (pos - j * stride);
+                const uint8_t *rec = p.ex_rec + gid * p.ex_stride;
+                // sign-code words sub kW .. sub kW + kW - 1, then the groups' ex-code words
+                const uint2 *wp = reinterpret_cast<const uint2 *>(rec + ex_record_sign_word(P, sub * kW));
+#pragma unroll
+                for (int i = 0; i < kW / 2; ++i) {
+                    const uint2 x = gload<uint2>(wp + i);
+                    xw[2 * i] = x.x;
+                    xw[2 * i + 1] = x.y;
+                }
+#pragma unroll
+                for (int gi = 0; gi < kG; ++gi) {
+                    const uint2 *gp = reinterpret_cast<const uint2 *>(rec + ex_record_group_word(P, sub + L * gi, 0));
+#pragma unroll
+                    for (int k = 0; k < 7; ++k)
+                        grp[gi][k] = gload<uint2>(gp + k);
+                }
+                if (sub == 0) {
                     const uint2 f = gload<uint2>(rec + P);
-                    b.fa = __uint_as_float(f.x);
-                    b.fr = __uint_as_float(f.y);
-                    b.low = gload<float>(lows + pos);
+                    fa = __uint_as_float(f.x);
+                    fr = __uint_as_float(f.y);
+                    low = gload<float>(p.van_lows + (size_t)q * V * stride + pos);
                 }
             }
-        };
-        auto finish = [&](uint32_t c, const VsRound &b) {
+            // the plane and q' reads stay behind the record loads (hoisted above them, the
+            // query's planes alone would take many registers and halve the waves that keep
+            // records in flight)
+            asm volatile("" ::: "memory");
             int ipa = 0, ipb = 0;
             float ipx = 0.0f;
-            if (b.have) {
-                const uint32_t x0 = b.sl.sign_word(0), x1 = b.sl.sign_word(1);
+            if (have) {
+                uint32_t pz = 0;
+                asm volatile("" : "+s"(pz));
+                const uint32_t *planes = s_planes + pz + sub * kW;
+                const float *qv = s_q + pz;
+                // plane by plane (Bq=8 planes 0..7, residual planes 8..15), so only one
+                // plane's words of the lane are in registers at a time
+#pragma unroll 2
+                for (int b = 0; b < 2 * kBq; ++b) {
+                    int cnt = 0;
 #pragma unroll
-                for (int bp = 0; bp < 2 * kBq; ++bp) {
-                    const int cnt = __popc(x0 & pl[bp][0]) + __popc(x1 & pl[bp][1]);
-                    const int bb = bp & (kBq - 1);
+                    for (int i = 0; i < kW; ++i)
+                        cnt += __popc(xw[i] & planes[b * W + i]);
+                    const int bb = b & (kBq - 1);
                     const int term = bb < kBq - 1 ? cnt << bb : -(cnt << (kBq - 1));
-                    if (bp < kBq)
+                    if (b < kBq)
                         ipa += term;
                     else
                         ipb += term;
                 }
-                uint2 grp[7];
-                b.sl.group(grp);
-                ipx = excode_group_ip_regs(grp, qv);
+#pragma unroll
+                for (int gi = 0; gi < kG; ++gi)
+                    ipx += excode_group_ip(grp[gi], qv + 64 * (sub + L * gi));
             }
-            ipa = entry_sum<G>(ipa, lane);
-            ipb = entry_sum<G>(ipb, lane);
-            ipx = entry_sum<G>(ipx, lane);
-            const float gadd = __shfl(gadd_l, (int)b.j);
-            if (b.have && g == 0) {
+#pragma unroll
+            for (int o = 1; o < L; o <<= 1) {
+                ipa += __shfl_xor(ipa, o, L);
+                ipb += __shfl_xor(ipb, o, L);
+                ipx += __shfl_xor(ipx, o, L);
+            }
+            if (have && sub == 0) {
                 const float ex = two_stage_ip(width, ipa, width2, ipb);
-                const float rd = b.fa + gadd + b.fr * (128.0f * ex + ipx + kbq);
-                const float err = 1e-4f * (fabsf(b.fa) + fabsf(gadd) +
-                                           fabsf(b.fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
-                const size_t e = ebase + (size_t)c * R;
+                const float gadd = s_gadd[j];
+                const float rd = fa + gadd + fr * (128.0f * ex + ipx + kbq);
+                const float err =
+                    1e-4f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
                 rd_r[e] = make_float2(rd, err);
-                aux_r[e] = make_float2(ex, b.low);
+                aux_r[e] = make_float2(ex, low);
             }
-        };
-        uint32_t pn = pos_of(c0);
-        for (uint32_t c = c0; c < c1; ++c) {
-            // the next round's position in flight while this round's records are loaded and
-            // computed
-            VsRound ra;
-            const uint32_t pc = pn;
-            pn = pos_of(c + 1);
-            issue(pc, ra);
-            finish(c, ra);
         }
     }
 }

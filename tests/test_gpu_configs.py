@@ -4,8 +4,9 @@
   against the oracle's restatement at every nprobe, and production recall@10 against the
   reference CPU path (rabitq_cpu, built from the reference sources) on the same index file.
 - Config 2 (1M x 128, 10,000 queries, nlist 1,024): production recall@10 at least the
-  reference CPU path's on the same 2,000 queries, live against frozen results and the
-  frozen-threshold candidate count against the oracle's band on a 64-query sample.
+  reference CPU path's on the same 2,000 queries over the whole nprobe grid, at batch-q 64 and
+  4; live against frozen results and the frozen-threshold candidate count against the oracle's
+  band on a 64-query sample.
 - Configs 3-5 (10M x 96, 20M x 768 inner product, 100M x 96 at top-100 with vanguard 10):
   the full index built; production recall on a 256-query sample at the grid's first nprobe,
   at least rabitq_cpu's on the same queries minus 0.001 (config 4 also at top-100, with CPU
@@ -181,20 +182,24 @@ def test_config2_full_size(tmp_path):
     wl.build_index(c, base, path, log=say)
     gt = wl.ground_truth(base, q, 10, c.metric)
     del base
-    nq, sample, nprobes = q.shape[0], 2000, [8, 16]
+    nq, sample, nprobes = q.shape[0], 2000, list(c.nprobes)
     ref = rabitq_cpu_recall(path, q[:sample], gt[:sample], 10, nprobes, tmp_path)
     ivf, eng = engine(path, c.metric, nq, c.topk, max(nprobes), c.vanguard, cpu_secondary_filter=True)
     live = {}
-    for nprobe in nprobes:
-        eng.reset_buffer(q)
-        _, i = eng.search(q, c.topk, nprobe, c.batch_q)
-        live[nprobe] = i
-        r_all = orc.recall_at_k(i, gt, 10)
-        r = orc.recall_at_k(i[:sample], gt[:sample], 10)
-        say(f"[gpu]   cfg2 nprobe={nprobe}: recall@10 gpu {r:.4f} (all {r_all:.4f}) rabitq_cpu {ref[nprobe]:.4f} "
-            f"on the same {sample} queries")
-        assert r >= ref[nprobe] - 0.001, (nprobe, r, ref[nprobe])
-        assert r_all >= 0.98
+    # the whole nprobe grid at the configuration's batch-q 64, and the reference's own batch-q
+    # range (1..6) at 4
+    for batch_q in (c.batch_q, 4):
+        for nprobe in nprobes:
+            eng.reset_buffer(q)
+            _, i = eng.search(q, c.topk, nprobe, batch_q)
+            if batch_q == c.batch_q:
+                live[nprobe] = i
+            r_all = orc.recall_at_k(i, gt, 10)
+            r = orc.recall_at_k(i[:sample], gt[:sample], 10)
+            say(f"[gpu]   cfg2 nprobe={nprobe} batch-q {batch_q}: recall@10 gpu {r:.4f} (all {r_all:.4f}) "
+                f"rabitq_cpu {ref[nprobe]:.4f} on the same {sample} queries")
+            assert r >= ref[nprobe] - 0.001, (nprobe, batch_q, r, ref[nprobe])
+            assert r_all >= 0.98
     eng.close()
     # a 64-query sample: frozen exhaustive vs live results, and the frozen candidate count
     qs = q[:64]

@@ -280,6 +280,9 @@ def order_keys(d):
                                                    (16384, 40, 32), (12000, 7, 64), (20000, 0, 32),
                                                    (40000, 0, 16), (65536, 0, 64), (65536, 0, 33),
                                                    (40000, 50, 64),
+                                                   # the fused select's wide slots (16 keys per tile)
+                                                   (16384, 0, 128), (16384, 0, 512), (16384, 40, 256),
+                                                   (40000, 50, 300), (65536, 0, 1024),
                                                    # beyond the LDS-held selects: up to the reference's 65,536
                                                    (16384, 0, 8192), (12000, 7, 5000), (40000, 50, 20000),
                                                    (65536, 0, 65536)])
@@ -289,9 +292,11 @@ def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
     below a bound from minima, ranked by (distance, cluster id); heavy ties fall back to the
     radix select; nprobe > 4,096: radix select of the k-th key, ordered compaction, stable
     radix sort in global scratch) against an exact sort of the GPU's own distance matrix by
-    (distance key, cluster id); then, where the fused select applies (nprobe <= 64), the
-    default search, whose GEMM epilogue keeps 8 keys per 128-cluster tile and whose merge
-    selects from them, must give the same probe lists. distinct > 0 repeats that many
+    (distance key, cluster id); then, where the fused select applies (nprobe <= 64, or up to
+    1,024 with at most ~4.5 probes per 128-cluster tile on average), the default search, whose
+    GEMM epilogue keeps 8 (16 above nprobe 64) keys per 128-cluster tile and whose merge
+    selects from them (above nprobe 64 a bitwise search for the k-th key, then a sort of the
+    keys up to it), must give the same probe lists. distinct > 0 repeats that many
     centroids over the whole list, so every distance is tied nlist / distinct times: the
     fused select cannot settle such queries from its candidates and sends them to its
     fallback (the query's distance row computed again, the generic select)."""
@@ -321,7 +326,9 @@ def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
     want = np.stack([np.lexsort((ids, keys[qi]))[:nprobe] for qi in range(nq)])
     for qi in range(nq):
         assert np.array_equal(pidx[qi], want[qi]), qi
-    if nprobe > 64:
+    fused_applies = 8192 <= nlist <= 65536 and (nprobe <= 64 or (
+        nprobe <= 1024 and nprobe * 256 <= 9 * nlist and -(-nlist // 128) * 16 <= 8192))
+    if not fused_applies:
         return
     say(f"[gpu] fused select, nlist={nlist} distinct={distinct} nprobe={nprobe}")
     eng, _, _ = run_frozen(case, nprobe, 10)
@@ -336,7 +343,7 @@ def test_select_exact_on_gpu_distances(nlist, distinct, nprobe, tmp_path):
     assert len(set(rows.tolist())) == len(rows) and np.all(rows < nq)
     if 0 < distinct < 16:
         # every 128-cluster tile holds 8 or more copies of the nearest centroid: more than the
-        # epilogue keeps
+        # epilogue keeps (nprobe <= 64)
         assert fb[0] > 0, "tied distances never reached the fallback"
     elif not distinct:
         assert fb[0] <= nq // 4, "the merge settled too few queries"
