@@ -147,6 +147,17 @@ __device__ __forceinline__ float lut4_ip(const uint32_t (&x)[Words<W>::kMax], co
     return a0 + a1;
 }
 
+// LUT4 with the matrix-core kernels: how far the LUT4 lower bound of a vector can lie below
+// its Bitwise lower bound (ex the Bitwise estimate, delta the query's lut_margin): |f_rescale|
+// delta in exact arithmetic, plus the rounding of the two FP32 evaluations (at most 12 ulps of
+// the magnitude of their terms). low_Bitwise - lut_slack < cutoff holds for every vector whose
+// LUT4 lower bound is below the cutoff.
+__device__ __forceinline__ float lut_slack(float delta, float fa, float fr, float fe, float gadd, float gerr,
+                                           float ex, float k1) {
+    return fabsf(fr) * delta +
+           7.2e-7f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (fabsf(ex) + delta + fabsf(k1)) + fabsf(fe * gerr));
+}
+
 // Two-stage <q',b>: width * ip_int rounded, then width2 * ip_res added with one rounding.
 __device__ __forceinline__ float two_stage_ip(float width, int ip, float width2, int ip_res) {
     return __fmaf_rn(width2, (float)ip_res, __fmul_rn(width, (float)ip));

@@ -101,6 +101,7 @@ struct cora_gpu_engine {
     uint32_t *d_qorder = nullptr;  // queries by nearest cluster (fused vanguard pass)
     int8_t *d_qbytes = nullptr;    // [max_q][2][P] qint, qres (MFMA far scan operands)
     uint16_t *d_lut = nullptr;     // [max_q][P/4][16] FP16 nibble tables (LUT4 estimator)
+    float *d_lut_margin = nullptr;  // [max_q] |LUT4 - Bitwise estimate| bound (launch_lut_margin)
     float *d_seed_dist = nullptr, *d_seed_low = nullptr, *d_seed_err = nullptr;
     uint4 *d_seed_rec = nullptr;
     float *d_van_lows = nullptr;  // [max_q][vanguard][van_stride] lower bounds of vanguard pairs
@@ -193,6 +194,7 @@ ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool f
     p.qplanes = E->d_planes;
     p.qbytes = E->d_qbytes;
     p.lut = (E->last.flags & CORA_FLAG_LUT4) ? reinterpret_cast<const uint32_t *>(E->d_lut) : nullptr;
+    p.lut_margin = E->d_lut_margin;
     p.qwidth = E->d_qwidth;
     p.qwidth2 = E->d_qwidth2;
     p.k1 = E->d_k1;
@@ -263,6 +265,7 @@ void release_workspace(cora_gpu_engine *E) {
     dfree(E->d_qorder);
     dfree(E->d_qbytes);
     dfree(E->d_lut);
+    dfree(E->d_lut_margin);
     dfree(E->d_seed_dist);
     dfree(E->d_seed_low);
     dfree(E->d_seed_err);
@@ -665,6 +668,7 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
         TRY(dalloc(E, E->d_qorder, max_q));
         TRY(dalloc(E, E->d_qbytes, max_q * 2 * E->P));
         TRY(dalloc(E, E->d_lut, max_q * 4 * E->P));
+        TRY(dalloc(E, E->d_lut_margin, max_q));
         TRY(dalloc(E, E->d_gadd, np));
         TRY(dalloc(E, E->d_gerr, np));
         TRY(dalloc(E, E->d_bcount, nb));
@@ -915,7 +919,13 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // far and recovery passes of the popcount kernels with the FP16 tables in place of the
     // q-planes, at most kLutMaxBatchQ pairs per pass.
     const bool reuse = (a->flags & CORA_FLAG_CROSS_QUERY_REUSE) != 0;
-    const bool mfma_far = !lut && reuse && far_mfma_supported(E->W) && !(a->flags & CORA_FLAG_NO_MFMA_SCAN);
+    // LUT4 on the matrix cores (wide codes): the far scan and the vanguard lows pass filter
+    // with Bitwise bounds lowered by the query's LUT4 margin and evaluate the LUT4 bound of
+    // the survivors exactly; the vanguard pass is the staged one, refining with the LUT4
+    // estimate
+    const bool lut_mfma = lut && reuse && far_mfma_lut_supported(E->W) && !(a->flags & CORA_FLAG_NO_MFMA_SCAN);
+    const bool mfma_far = (!lut || lut_mfma) && reuse && far_mfma_supported(E->W) &&
+                          !(a->flags & CORA_FLAG_NO_MFMA_SCAN);
     const uint32_t batch = mfma_far ? kMfmaBatchQ
                            : reuse  ? std::min<uint32_t>(a->batch_q, lut ? kLutMaxBatchQ : (uint32_t)kMaxBatchQ)
                                     : 1u;
@@ -993,6 +1003,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
                           E->d_qwidth, E->d_qwidth2, E->d_planes, E->d_qbytes, s);
         if (lut)
             launch_lut_build(E->d_qrot, nq, P, E->d_lut, s);
+        if (lut_mfma)
+            launch_lut_margin(E->d_qrot, E->d_planes, E->d_qwidth, nq, P, E->d_lut_margin, s);
         HIPCHK(hipEventRecord(E->ev_prep, s));
         HIPCHK(hipStreamWaitEvent(E->stream_d2h, E->ev_prep, 0));
         HIPCHK(hipMemcpyAsync(E->h_qrot, E->d_qrot, (size_t)nq * P * 4, hipMemcpyDeviceToHost,
@@ -1029,7 +1041,8 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool prefilter = E->d_exrec && ex_stage_mode && !(a->flags & CORA_FLAG_NO_GPU_PREFILTER);
     // fused per-query vanguard pass (vanguard.hip) unless the reference's per-pair passes
     // are asked for or the shape exceeds its limits
-    const bool fused = gpu_seed && !lut && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
+    const bool lut_staged = lut_mfma && E->d_van_lows && E->d_vs_seed_pos && !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA);
+    const bool fused = gpu_seed && (!lut || lut_staged) && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
                        a->topk <= kVanguardMaxTopk;
     // its lower bounds first on the matrix cores, cluster-major, into the per-pair lows
     // array [nq][depth][van_stride] of the workspace
@@ -1039,7 +1052,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool lows_by_size = (uint64_t)E->N * (E->P / 8 + 12) > kLowsMinIndexBytes && E->P >= kLowsMinDim;
     const bool van_lows = fused && depth > 0 && far_mfma_supported(E->W) && E->d_van_lows &&
                           !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA) &&
-                          (lows_by_size || (a->flags & CORA_FLAG_VANGUARD_MFMA));
+                          (lows_by_size || (a->flags & CORA_FLAG_VANGUARD_MFMA) || lut);
     // fork: pair scheduling (and the fused pass's query order) on stream_aux
     HIPCHK(hipEventRecord(E->ev_fork, s));
     HIPCHK(hipStreamWaitEvent(E->stream_aux, E->ev_fork, 0));
@@ -1083,7 +1096,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     p.dropped = E->d_stats + 7;
     VanguardArgs va{};
     // the staged pass (grid-wide refinement) where the lows pass wrote every vanguard bound
-    const bool staged = van_lows && E->d_vs_seed_pos && !(a->flags & CORA_FLAG_VANGUARD_ONE_PASS);
+    const bool staged = van_lows && E->d_vs_seed_pos && (lut || !(a->flags & CORA_FLAG_VANGUARD_ONE_PASS));
     p.van_mins = staged ? E->d_van_mins : nullptr;
     E->last_fused = fused && depth > 0;
     E->last_van_lows = van_lows;

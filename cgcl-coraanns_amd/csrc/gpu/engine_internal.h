@@ -129,6 +129,10 @@ struct ScanParams {
     // LUT4 estimator (CORA_FLAG_LUT4): per query the FP16 nibble table [P/4][16], 2P u32
     // words; nullptr selects the Bitwise estimator
     const uint32_t *lut;
+    // LUT4 with the matrix-core kernels: per query a bound on |LUT4 estimate - Bitwise
+    // estimate| over all codes (launch_lut_margin), by which their Bitwise lower bounds are
+    // lowered (lut_slack) before the LUT4 bound of the survivors is evaluated exactly
+    const float *lut_margin;
     const float *qwidth;      // [nq] Bq=8 step
     const float *qwidth2;     // [nq] residual step (qwidth / 254)
     const float *k1;          // [nq]
@@ -312,6 +316,11 @@ void launch_fused_probe_gemm_rows(const uint16_t *qhi, const uint16_t *qlo, cons
                                   const uint16_t *chl, const float *cscale, const float *cnorm, uint32_t r0,
                                   uint32_t rows, uint32_t nq, uint32_t nl, uint32_t P, uint32_t nprobe,
                                   void *scratch, hipStream_t s);
+// Per query, delta >= |LUT4 estimate - Bitwise estimate| for every code: the Bq=8 quantisation
+// error's largest subset sum, the FP16 tables' and the FP32 sums' rounding (an upper bound,
+// rounded up).
+void launch_lut_margin(const float *qrot, const uint32_t *planes, const float *width, uint32_t nq, uint32_t P,
+                       float *margin, hipStream_t s);
 void launch_fused_probe_select(const uint16_t *qhl, const float *qscale, const float *qnorm, const uint16_t *chl,
                                const float *cscale, const float *cnorm, uint32_t nq, uint32_t nl, uint32_t P,
                                uint32_t nprobe, void *scratch, uint32_t *fb, int32_t *idx, hipStream_t s);
@@ -372,6 +381,8 @@ constexpr uint32_t kLutMaxBatchQ = 4;
 // far-pair scan on the matrix cores (scan_mfma.hip): units of up to kMfmaBatchQ pairs
 constexpr uint32_t kMfmaBatchQ = 16;
 bool far_mfma_supported(uint32_t W);
+// the LUT4 estimator on the matrix-core kernels (the wide kernel: P = 512, 768, 1024)
+bool far_mfma_lut_supported(uint32_t W);
 void launch_far_mfma(const ScanParams &p, uint32_t W, bool dense, hipStream_t s);
 // The vanguard units (units of up to kMfmaBatchQ pairs, set 0) on the matrix cores: the lower
 // bound of every (vector, pair) to p.van_lows[(query * p.vanguard + probe) * p.van_stride + v]

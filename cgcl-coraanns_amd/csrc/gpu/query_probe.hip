@@ -644,6 +644,45 @@ __global__ __launch_bounds__(256) void lut_build_kernel(const float *__restrict_
     lut[(size_t)q * entries + i] = __builtin_bit_cast(uint16_t, (_Float16)sum);
 }
 
+// One wave per query: e_i = width qint_i - q'_i (qint from the Bq=8 planes, two's complement),
+// E+ and E- the sums of its positive and negative parts (in FP64), l1 = sum |q'_i|:
+//   |Bitwise - exact| <= max(E+, E-) + 2^-24 |width ip_int| (the product's rounding),
+//   |LUT4 - exact| <= (2^-11 + 2^-21) l1 + P 2^-25 (FP32 sums of up to 4 terms, rounded to
+//   FP16, subnormal spacing 2^-24) + (P/8 + 1) 2^-23 l1 (the two FP32 accumulators of P/8
+//   entries and their sum, with room for the entries' own rounding).
+__global__ __launch_bounds__(64) void lut_margin_kernel(const float *__restrict__ qrot,
+                                                         const uint32_t *__restrict__ planes,
+                                                         const float *__restrict__ width, uint32_t P,
+                                                         float *__restrict__ margin) {
+    const uint32_t q = blockIdx.x, lane = threadIdx.x, W = P / 32;
+    const float *v = qrot + (size_t)q * P;
+    const uint32_t *pl = planes + (size_t)q * 2 * kBq * W;
+    const double w = width[q];
+    double ep = 0.0, en = 0.0, l1 = 0.0;
+    for (uint32_t i = lane; i < P; i += 64) {
+        int u = 0;
+        for (int b = 0; b < kBq; ++b)
+            u |= (int)((pl[b * W + i / 32] >> (i % 32)) & 1u) << b;
+        const int qint = u >= 128 ? u - 256 : u;
+        const double e = w * (double)qint - (double)v[i];
+        ep += e > 0.0 ? e : 0.0;
+        en += e < 0.0 ? -e : 0.0;
+        l1 += fabs((double)v[i]);
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        ep += __shfl_xor(ep, o);
+        en += __shfl_xor(en, o);
+        l1 += __shfl_xor(l1, o);
+    }
+    if (lane == 0) {
+        const double u24 = 5.9604644775390625e-08;  // 2^-24
+        const double d = (ep > en ? ep : en) + u24 * w * 128.0 * P +
+                         (4.8828125e-04 + 4.76837158203125e-07 + (P / 8.0 + 1.0) * 2.0 * u24) * l1 +
+                         P * 2.9802322387695312e-08;
+        margin[q] = (float)(d * (1.0 + 1e-6)) * (1.0f + 1.0e-6f);
+    }
+}
+
 __global__ __launch_bounds__(64) void row_norms_kernel(const float *__restrict__ x, uint32_t rows,
                                                        uint32_t P, float *__restrict__ out) {
     for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
@@ -1636,6 +1675,12 @@ void launch_query_prep(const float *qrot, uint32_t nq, uint32_t P, uint32_t ex_b
                        float *kb, float *qnorm, float *qwidth, float *qwidth2, uint32_t *qplanes,
                        int8_t *qbytes, hipStream_t s) {
     query_prep_kernel<<<nq, 64, 0, s>>>(qrot, P, ex_bits, k1, kb, qnorm, qwidth, qwidth2, qplanes, qbytes);
+}
+
+void launch_lut_margin(const float *qrot, const uint32_t *planes, const float *width, uint32_t nq, uint32_t P,
+                       float *margin, hipStream_t s) {
+    if (nq)
+        lut_margin_kernel<<<nq, 64, 0, s>>>(qrot, planes, width, P, margin);
 }
 
 void launch_lut_build(const float *qrot, uint32_t nq, uint32_t P, uint16_t *lut, hipStream_t s) {

@@ -41,7 +41,9 @@ constexpr int kStage = 256;  // staged survivor records per wave
 
 // What a unit's lower bounds are used for: published below the cutoff (far pairs),
 // written with ip_int and ip_res to the debug arrays, or written to the vanguard lows.
-enum MfmaMode : int { kPublish = 0, kDenseDbg = 1, kLows = 2 };
+// kPublishLut / kLowsLut: the same with the LUT4 estimator (the wide kernel only): the Bitwise
+// bounds lowered by lut_slack, and the survivors' LUT4 bounds evaluated exactly.
+enum MfmaMode : int { kPublish = 0, kDenseDbg = 1, kLows = 2, kPublishLut = 3, kLowsLut = 4, kDenseLut = 5 };
 
 // The smallest of the lower bounds of vectors o .. o + 3 of a cluster of n vectors (+inf for
 // vectors past its end): the group minima of the vanguard lows pass (ScanParams::van_mins).
@@ -126,8 +128,8 @@ __device__ void flush_records(const ScanParams &p, const QueueDev &q, uint32_t n
         uint4 rec = make_uint4(0u, 0u, 0u, 0u);
         if (i < n) {
             rec = s_rec[i];
-            keep = true;
-            if (p.prefilter) {
+            keep = rec.x != ~0u;  // ~0: dropped by finalize_records (LUT4 bound)
+            if (keep && p.prefilter) {
                 float err;
                 const float dist = refine_one(p, rec.x & 0xFFFFu, rec.x >> 16, rec.y,
                                               __uint_as_float(rec.z), err);
@@ -137,8 +139,9 @@ __device__ void flush_records(const ScanParams &p, const QueueDev &q, uint32_t n
             }
         }
         const unsigned long long m = __ballot(keep);
+        const unsigned long long live = __ballot(i < n && rec.x != ~0u);
         if (p.prefilter && lane == 0) {
-            const uint32_t dropped = min(64u, n - i0) - (uint32_t)__popcll(m);
+            const uint32_t dropped = (uint32_t)__popcll(live) - (uint32_t)__popcll(m);
             if (dropped)
                 atomicAdd(p.dropped, (unsigned long long)dropped);
         }
@@ -348,27 +351,51 @@ __device__ __forceinline__ int tile_ip_res(const uint8_t *__restrict__ tile, uin
     return popc_ip<W>(x, rplanes, W);
 }
 
-// Survivors staged with their ip_int and tile position get their two-stage exact_ip.
-template <int W>
+// Survivors staged with their ip_int and tile position get their two-stage exact_ip. With
+// LUT4 they get the LUT4 estimate (filter_kernels.cuh:655-708, one lane per record, in the
+// reference's order) and its lower bound, and those whose bound is not below their cutoff are
+// marked dropped (x = ~0).
+template <int W, bool kLut>
 __device__ void finalize_records(const ScanParams &p, uint32_t n, uint4 *s_rec, const uint32_t *s_loc,
-                                 uint32_t lane) {
+                                 const float *s_cut, uint32_t lane) {
     __syncthreads();
     for (uint32_t i = lane; i < n; i += 64) {
         uint4 rec = s_rec[i];
         const uint32_t query = rec.x & 0xFFFFu, loc = s_loc[i];
-        const int ipr = tile_ip_res<W>(p.tiles + (size_t)(loc >> 6) * p.tile_bytes, loc & 63u,
-                                       p.qplanes + ((size_t)query * 16 + 8) * W);
-        rec.z = __float_as_uint(two_stage_ip(p.qwidth[query], (int)rec.z, p.qwidth2[query], ipr));
+        const uint8_t *tile = p.tiles + (size_t)(loc >> 6) * p.tile_bytes;
+        const uint32_t v = loc & 63u;
+        if constexpr (kLut) {
+            uint32_t x[W];
+#pragma unroll
+            for (int g = 0; g < W / 4; ++g) {
+                const uint4 c = *reinterpret_cast<const uint4 *>(tile + (size_t)g * 1024 + v * 16);
+                x[4 * g] = c.x;
+                x[4 * g + 1] = c.y;
+                x[4 * g + 2] = c.z;
+                x[4 * g + 3] = c.w;
+            }
+            const float ex = lut4_ip<W>(x, p.lut + (size_t)query * 2 * p.P, W);
+            const float *fac = reinterpret_cast<const float *>(tile + 256u * W);
+            const size_t pi = (size_t)query * p.nprobe + (rec.x >> 16);
+            const float low = fac[v] + p.pgadd[pi] + fac[64 + v] * (ex + p.k1[query]) - fac[128 + v] * p.pgerr[pi];
+            rec.z = __float_as_uint(ex);
+            rec.w = __float_as_uint(low);
+            if (!(low < s_cut[i]))
+                rec.x = ~0u;
+        } else {
+            const int ipr = tile_ip_res<W>(tile, v, p.qplanes + ((size_t)query * 16 + 8) * W);
+            rec.z = __float_as_uint(two_stage_ip(p.qwidth[query], (int)rec.z, p.qwidth2[query], ipr));
+        }
         s_rec[i] = rec;
     }
 }
 
 // Finalize and publish the wide kernel's staged survivors; out of line, so the unrolled
 // scan loop carries one call instead of the refinement and publication code.
-template <int W>
+template <int W, bool kLut>
 __device__ __noinline__ void flush_wide(const ScanParams &p, uint32_t n, uint4 *s_rec, const float *s_cut,
                                         const uint32_t *s_loc, unsigned long long &limit, uint32_t lane) {
-    finalize_records<W>(p, n, s_rec, s_loc, lane);
+    finalize_records<W, kLut>(p, n, s_rec, s_loc, s_cut, lane);
     flush_records(p, p.queue, n, s_rec, s_cut, limit, lane);
 }
 
@@ -385,8 +412,13 @@ constexpr int kStageWide = 384;  // wide kernel: flushed when a row block could 
 // The sixteen code bits of an operand become sixteen int8 0/1 bytes through a 256-entry
 // table in LDS (two 8-byte reads per operand): widening them arithmetically took 16 VALU
 // instructions per operand and bounded the kernel (10-13% faster at P = 768).
-template <int W, int kMode>
+template <int W, int kModeT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void far_mfma_wide_kernel(const ScanParams p) {
+    constexpr bool kLut = kModeT == kPublishLut || kModeT == kLowsLut || kModeT == kDenseLut;
+    constexpr int kMode = kModeT == kPublishLut ? kPublish
+                          : kModeT == kLowsLut  ? kLows
+                          : kModeT == kDenseLut ? kDenseDbg
+                                                : kModeT;
     constexpr bool kDense = kMode != kPublish;
     static_assert(W % 8 == 0 && W >= 16 && W <= 32, "lane-group word ranges of even length");
     constexpr int WQ = W / 4;  // code words per lane-group
@@ -435,11 +467,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
         const bool slot = col < count;
         const uint32_t w0 = slot ? gload<uint32_t>(&p.pairs[uniform(un.y) + col].word0) : 0u;
         const uint32_t query = w0 & 0xFFFFu, probe = w0 >> 16;
-        float width = 0.0f, k1 = 0.0f, gadd = 0.0f, gerr = 0.0f, cutoff = -FLT_MAX;
+        float width = 0.0f, k1 = 0.0f, gadd = 0.0f, gerr = 0.0f, cutoff = -FLT_MAX, delta = 0.0f;
         v4i32 bq[S];
         if (slot) {
             width = gload<float>(p.qwidth + query);
             k1 = gload<float>(p.k1 + query);
+            if constexpr (kLut)
+                delta = gload<float>(p.lut_margin + query);
             const size_t pi = (size_t)query * p.nprobe + probe;
             gadd = gload<float>(p.pgadd + pi);
             gerr = gload<float>(p.pgerr + pi);
@@ -501,6 +535,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                         for (int r = 0; r < 4; ++r) {
                             const float ex = width * (float)acc[r];
                             lw[r] = fav[r] + gadd + frv[r] * (ex + k1) - fev[r] * gerr;
+                            // LUT4: a lower bound of the LUT4 bound
+                            if constexpr (kLut)
+                                lw[r] -= lut_slack(delta, fav[r], frv[r], fev[r], gadd, gerr, ex, k1);
                         }
                         lows_put(s_low, col, o, lw);
                     }
@@ -509,7 +546,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                 if constexpr (!kDense) {
                     // a row block stages at most 4 x 64 records
                     if (staged + 4 * 64 > (uint32_t)kStageWide) {
-                        flush_wide<W>(p, staged, s_rec, s_cut, s_loc, limit, lane);
+                        flush_wide<W, kLut>(p, staged, s_rec, s_cut, s_loc, limit, lane);
                         staged = 0;
                     }
                 }
@@ -523,12 +560,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                     if constexpr (kDense) {
                         if (valid) {
                             const size_t od = ((size_t)query * p.nprobe + probe) * p.dbg_stride + local;
-                            p.dbg_ip[od] = ip;
-                            p.dbg_ip2[od] = tile_ip_res<W>(tile, o + r, p.qplanes + ((size_t)query * 16 + 8) * W);
-                            p.dbg_low[od] = low;
+                            if constexpr (kLut) {
+                                // the LUT4 estimate (its FP32 bits) and bound, as finalize_records
+                                // evaluates them for survivors
+                                uint32_t x[W];
+#pragma unroll
+                                for (int g = 0; g < W / 4; ++g) {
+                                    const uint4 c =
+                                        *reinterpret_cast<const uint4 *>(tile + (size_t)g * 1024 + (o + r) * 16);
+                                    x[4 * g] = c.x;
+                                    x[4 * g + 1] = c.y;
+                                    x[4 * g + 2] = c.z;
+                                    x[4 * g + 3] = c.w;
+                                }
+                                const float exl = lut4_ip<W>(x, p.lut + (size_t)query * 2 * P, W);
+                                p.dbg_ip[od] = (int32_t)__float_as_uint(exl);
+                                p.dbg_ip2[od] = 0;
+                                p.dbg_low[od] = fav[r] + gadd + frv[r] * (exl + k1) - fev[r] * gerr;
+                            } else {
+                                p.dbg_ip[od] = ip;
+                                p.dbg_ip2[od] = tile_ip_res<W>(tile, o + r, p.qplanes + ((size_t)query * 16 + 8) * W);
+                                p.dbg_low[od] = low;
+                            }
                         }
                     } else {
-                        const bool survive = valid && low < cutoff;
+                        // LUT4: every vector whose LUT4 bound can lie below the cutoff;
+                        // finalize_records evaluates that bound and drops the others
+                        const bool survive =
+                            valid && (kLut ? low - lut_slack(delta, fav[r], frv[r], fev[r], gadd, gerr, ex, k1)
+                                            : low) < cutoff;
                         const unsigned long long mask = __ballot(survive);
                         if (mask == 0)
                             continue;
@@ -549,7 +609,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
     }
     if constexpr (!kDense) {
         if (staged)
-            flush_wide<W>(p, staged, s_rec, s_cut, s_loc, limit, lane);
+            flush_wide<W, kLut>(p, staged, s_rec, s_cut, s_loc, limit, lane);
     }
 }
 
@@ -578,6 +638,7 @@ uint32_t resident_grid_mfma(F kernel) {
 template <int W, int kMode>
 void launch_w(const ScanParams &p, hipStream_t s) {
     if constexpr (W <= 8) {
+        static_assert(kMode != kPublishLut && kMode != kLowsLut && kMode != kDenseLut, "LUT4 on the wide kernel only");
         auto *k = far_mfma_kernel<W, kMode>;
         k<<<resident_grid_mfma(k), 64, 0, s>>>(p);
     } else {
@@ -588,6 +649,14 @@ void launch_w(const ScanParams &p, hipStream_t s) {
 
 template <int W>
 void launch_mode(const ScanParams &p, int mode, hipStream_t s) {
+    if constexpr (W >= 16) {
+        if (mode == kLowsLut)
+            return launch_w<W, kLowsLut>(p, s);
+        if (mode == kPublishLut)
+            return launch_w<W, kPublishLut>(p, s);
+        if (mode == kDenseLut)
+            return launch_w<W, kDenseLut>(p, s);
+    }
     if (mode == kLows)
         launch_w<W, kLows>(p, s);
     else if (mode == kDenseDbg)
@@ -602,12 +671,14 @@ bool far_mfma_supported(uint32_t W) {
     return W == 2 || W == 4 || W == 6 || W == 8 || W == 16 || W == 24 || W == 32;
 }
 
+bool far_mfma_lut_supported(uint32_t W) { return W == 16 || W == 24 || W == 32; }
+
 void launch_far_mfma(const ScanParams &p, uint32_t W, bool dense, hipStream_t s) {
-    launch_mfma_units(p, W, dense ? kDenseDbg : kPublish, s);
+    launch_mfma_units(p, W, dense ? (p.lut ? kDenseLut : kDenseDbg) : p.lut ? kPublishLut : kPublish, s);
 }
 
 void launch_vanguard_lows(const ScanParams &p, uint32_t W, hipStream_t s) {
-    launch_mfma_units(p, W, kLows, s);
+    launch_mfma_units(p, W, p.lut ? kLowsLut : kLows, s);
 }
 
 void launch_mfma_units(const ScanParams &p, uint32_t W, int mode, hipStream_t s) {

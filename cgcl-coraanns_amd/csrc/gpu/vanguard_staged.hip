@@ -450,7 +450,7 @@ struct VsShape {
     static_assert(kGroups % kLanes == 0, "lane split");
 };
 
-template <int W>
+template <int W, bool kLut>
 __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >= 32 ? 3 : 4))) void vs_refine_kernel(const ScanParams p, const VanguardArgs va,
                                                                const VsArgs vs, uint32_t stage) {
     using S = VsShape<W>;
@@ -458,11 +458,13 @@ __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >=
     constexpr uint32_t P = 32 * W, E = S::kChunk;
     __shared__ __align__(16) float s_q[P];
     __shared__ uint32_t s_planes[2 * kBq * W];
-    __shared__ uint32_t s_start[kVanguardMaxPairs];
-    __shared__ float s_gadd[kVanguardMaxPairs];
+    __shared__ uint32_t s_lut[kLut ? 2 * P : 1];  // LUT4: the query's FP16 nibble table
+    __shared__ uint32_t s_start[kVanguardMaxPairs], s_tbase[kVanguardMaxPairs];
+    __shared__ float s_gadd[kVanguardMaxPairs], s_gerr[kVanguardMaxPairs];
     __shared__ uint32_t s_red[kVsWaves];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t sub = tid % L, el = tid / L;
+    constexpr bool lut = kLut;
     const uint32_t cap = stage ? vs.list_cap : vs.seed_cap;
     const uint32_t *pos_r = stage ? vs.list_pos : vs.seed_pos;
     float2 *rd_r = stage ? vs.list_rd : vs.seed_rd;
@@ -497,12 +499,19 @@ __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >=
             s_q[i] = x;
             l1p += fabsf(x);
         }
-        for (uint32_t i = tid; i < 2 * kBq * W; i += kVsThreads)
-            s_planes[i] = p.qplanes[(size_t)q * 2 * kBq * W + i];
+        if constexpr (lut)
+            for (uint32_t i = tid; i < 2 * P; i += kVsThreads)
+                s_lut[i] = p.lut[(size_t)q * 2 * P + i];
+        else
+            for (uint32_t i = tid; i < 2 * kBq * W; i += kVsThreads)
+                s_planes[i] = p.qplanes[(size_t)q * 2 * kBq * W + i];
         if (tid < V) {
             const size_t pi = (size_t)q * p.nprobe + tid;
-            s_start[tid] = p.meta[va.probe_idx[pi]].start;
+            const ClusterMeta cm = p.meta[va.probe_idx[pi]];
+            s_start[tid] = cm.start;
+            s_tbase[tid] = cm.tile_base;
             s_gadd[tid] = p.pgadd[pi];
+            s_gerr[tid] = p.pgerr[pi];
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1)
@@ -514,14 +523,14 @@ __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >=
 #pragma unroll
         for (int w = 0; w < kVsWaves; ++w)
             l1q += __uint_as_float(s_red[w]);
-        const float width = p.qwidth[q], width2 = p.qwidth2[q], kbq = p.kb[q];
+        const float width = p.qwidth[q], width2 = p.qwidth2[q], kbq = p.kb[q], k1 = p.k1[q];
         for (uint32_t c = c0; c < c1; ++c) {
             const uint32_t idx = c * E + el;
             const bool have = idx < n;
             const size_t e = (size_t)q * cap + idx;
             uint2 grp[kG][7];
             uint32_t xw[kW];
-            float fa = 0.0f, fr = 0.0f, low = 0.0f;
+            float fa = 0.0f, fr = 0.0f, low = 0.0f, sfa = 0.0f, sfr = 0.0f, sfe = 0.0f;
             uint32_t j = 0;
             if (have) {
                 const uint32_t pos = pos_r[e];
@@ -547,7 +556,18 @@ __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >=
                     const uint2 f = gload<uint2>(rec + P);
                     fa = __uint_as_float(f.x);
                     fr = __uint_as_float(f.y);
-                    low = gload<float>(p.van_lows + (size_t)q * V * stride + pos);
+                    if constexpr (lut) {
+                        // LUT4: the vector's own lower bound is evaluated below (the lows are
+                        // lowered Bitwise bounds), from its short factors in the tile
+                        const uint32_t lv = pos - j * stride;
+                        const float *fac = reinterpret_cast<const float *>(
+                            p.tiles + (size_t)(s_tbase[j] + lv / kTileVectors) * p.tile_bytes + 256u * W);
+                        sfa = gload<float>(fac + lv % kTileVectors);
+                        sfr = gload<float>(fac + 64 + lv % kTileVectors);
+                        sfe = gload<float>(fac + 128 + lv % kTileVectors);
+                    } else {
+                        low = gload<float>(p.van_lows + (size_t)q * V * stride + pos);
+                    }
                 }
             }
             // the plane and q' reads stay behind the record loads (hoisted above them, the
@@ -555,7 +575,23 @@ __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >=
             // records in flight)
             asm volatile("" ::: "memory");
             int ipa = 0, ipb = 0;
-            float ipx = 0.0f;
+            float ipx = 0.0f, a0 = 0.0f, a1 = 0.0f;
+            if (lut && have) {
+                // LUT4 estimate of the lane's sign-code words (nibble j = 8 w + i of word w,
+                // even j into a0, odd into a1, filter_kernels.cuh:655-708); the lanes' partial
+                // sums are added below
+                const uint16_t *h = reinterpret_cast<const uint16_t *>(s_lut);
+#pragma unroll
+                for (int i = 0; i < kW; ++i) {
+                    const uint32_t c = __builtin_bitreverse32(xw[i]);
+                    const uint16_t *t = h + (size_t)(sub * kW + i) * 128;
+#pragma unroll
+                    for (int n = 0; n < 8; n += 2) {
+                        a0 += (float)__builtin_bit_cast(_Float16, t[n * 16 + ((c >> (28 - 4 * n)) & 15u)]);
+                        a1 += (float)__builtin_bit_cast(_Float16, t[(n + 1) * 16 + ((c >> (24 - 4 * n)) & 15u)]);
+                    }
+                }
+            }
             if (have) {
                 uint32_t pz = 0;
                 asm volatile("" : "+s"(pz));
@@ -564,7 +600,7 @@ __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >=
                 // plane by plane (Bq=8 planes 0..7, residual planes 8..15), so only one
                 // plane's words of the lane are in registers at a time
 #pragma unroll 2
-                for (int b = 0; b < 2 * kBq; ++b) {
+                for (int b = 0; b < (lut ? 0 : 2 * kBq); ++b) {
                     int cnt = 0;
 #pragma unroll
                     for (int i = 0; i < kW; ++i)
@@ -585,10 +621,14 @@ __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >=
                 ipa += __shfl_xor(ipa, o, L);
                 ipb += __shfl_xor(ipb, o, L);
                 ipx += __shfl_xor(ipx, o, L);
+                a0 += __shfl_xor(a0, o, L);
+                a1 += __shfl_xor(a1, o, L);
             }
             if (have && sub == 0) {
-                const float ex = two_stage_ip(width, ipa, width2, ipb);
+                const float ex = lut ? a0 + a1 : two_stage_ip(width, ipa, width2, ipb);
                 const float gadd = s_gadd[j];
+                if (lut)
+                    low = sfa + gadd + sfr * (ex + k1) - sfe * s_gerr[j];
                 const float rd = fa + gadd + fr * (128.0f * ex + ipx + kbq);
                 const float err =
                     1e-4f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
@@ -980,7 +1020,7 @@ uint32_t vs_resident_grid(F kernel) {
 template <int W>
 void launch_vs_w(const ScanParams &p, const VanguardArgs &va, const VsArgs &vs, uint32_t nq, hipEvent_t ev_r0,
                  hipEvent_t ev_r1, hipEvent_t ev_r2, hipEvent_t ev_r3, hipStream_t s) {
-    auto *rk = vs_refine_kernel<W>;
+    auto *rk = p.lut ? vs_refine_kernel<W, true> : vs_refine_kernel<W, false>;
     const uint32_t grid = vs_resident_grid(rk);
     vs_seed_kernel<<<nq, kVsThreads, 0, s>>>(p, va, vs);
     if (ev_r0)
@@ -997,7 +1037,9 @@ void launch_vs_w(const ScanParams &p, const VanguardArgs &va, const VsArgs &vs, 
     vs_merge_kernel<<<nq, kVsThreads, 0, s>>>(p, va, vs);
     vs_publish_kernel<<<std::min<uint32_t>(kVsPubGrid, nq), kVsThreads, 0, s>>>(p, va, vs);
     vs_stats_kernel<<<1, 64, 0, s>>>(p, va, vs);
-    // the queries whose seeds or list did not fit: the fused per-query kernel
+    // the queries whose seeds or list did not fit: the fused per-query kernel (with LUT4 it
+    // refines them with the two-stage Bitwise estimate, and selects and publishes on the
+    // lowered bounds)
     VanguardArgs fb = va;
     fb.list = vs.overflow;
     fb.list_count = &vs.ctr[kVsCtrOverflow];

@@ -1172,6 +1172,10 @@ def test_recall_at_least_reference_cpu_path(n, dim, n_centers, nlist, nq, metric
         agree = np.mean([len(set(a) & set(b)) / topk for a, b in zip(ids.tolist(), ref_ids[li].tolist())])
         say(f"[gpu]   nprobe={nprobe}: recall gpu {r_gpu:.4f} ref {r_ref:.4f}, id agreement {agree:.4f}")
         assert r_gpu >= r_ref - 0.001, (nprobe, r_gpu, r_ref)
+        # the two top-k lists differ only where one of them misses a true neighbour (measured:
+        # 0.9975 at 200k x 128 against recalls 0.9865 / 0.9848; 0.9522 at 100k x 768, where the
+        # reference's FastScan search has recall 0.9357 against 0.9823)
+        assert agree >= min(r_gpu, r_ref) - 0.005, (nprobe, agree, r_gpu, r_ref)
     eng.close()
 
 
@@ -1301,7 +1305,9 @@ def test_lut4_end_to_end_frozen(case_name, vanguard, request):
 def test_lut4_live_thresholds_match_frozen(case_name, topk, request):
     """LUT4 in the production setting (live thresholds, secondary filter, vanguard 5, the GPU
     seed thresholds and refined pre-filter on the HBM ex-codes, batch-q 4) returns the top-k
-    of the exhaustive frozen LUT4 search, and GPU-final top-k is refused for it."""
+    of the exhaustive frozen LUT4 search, and GPU-final top-k is refused for it. At P = 768
+    the matrix-core lows pass and far scan (lowered Bitwise bounds, exact LUT4 bounds of the
+    survivors) and the staged vanguard pass run it; at P = 128 the per-pair passes."""
     case = request.getfixturevalue(case_name)
     nprobe = 16
     say(f"[gpu] LUT4 live vs frozen on {case_name} top-{topk}")
@@ -1310,7 +1316,7 @@ def test_lut4_live_thresholds_match_frozen(case_name, topk, request):
     eng.reset_buffer(case.queries)
     d, i = eng.search(case.queries, topk, nprobe, 4)
     st = eng.stats()
-    assert st["vanguard_mode"] == 1  # per-pair seed and recovery passes
+    assert st["vanguard_mode"] == (4 if case.file.padded_dim >= 512 else 1), st["vanguard_mode"]
     assert st["submitted"] < case.queries.shape[0] * case.file.num  # the filter prunes
     same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), i0.tolist())])
     assert same >= 0.99, same
@@ -1318,4 +1324,92 @@ def test_lut4_live_thresholds_match_frozen(case_name, topk, request):
     eng.reset_buffer(case.queries)
     with pytest.raises(ca.LogicError):
         eng.search(case.queries, topk, nprobe)
+    eng.close()
+
+
+def probed_vectors_lut(case, g, q, nprobe, lut):
+    """probed_vectors with the LUT4 estimate (the query's FP16 tables lut) as the bound's and
+    refinement's exact_ip."""
+    sd, P = case.sd, case.file.padded_dim
+    l1 = float(np.abs(g["qr"][q]).sum())
+    out = []
+    for p in range(nprobe):
+        c = int(g["pidx"][q, p])
+        s, n = int(sd.cluster_start[c]), int(sd.cluster_sizes[c])
+        gid = s + np.arange(n)
+        ex = orc.lut4_ip(cluster_words(sd, s, n), lut)
+        f = sd.short_factors[gid]
+        low = orc.low_dist(f[:, 0], f[:, 1], f[:, 2], g["gadd"][q, p], g["gerr"][q, p], ex, g["k1"][q])
+        fa, fr = sd.ex_factors[gid, 0], sd.ex_factors[gid, 1]
+        rd = orc.refine_dist(fa, fr, g["gadd"][q, p], ex, orc.excode_ip(g["qr"][q], sd.long_codes[gid], P),
+                             g["kb"][q], 7)
+        err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex, l1, g["kb"][q], 7)
+        out.append((p, gid, low.astype(np.float64), rd.astype(np.float64), err.astype(np.float64)))
+    return out
+
+
+@pytest.mark.parametrize("topk", [10, 100])
+def test_lut4_staged_vanguard_frozen_parity(topk, synth_ip768):
+    """LUT4 on the matrix cores with the staged vanguard pass, in its deterministic test mode
+    (frozen snapshot lowered by the pass; vanguard 5): the lows pass writes Bitwise bounds
+    lowered by the query's LUT4 margin, the staged pass refines with the LUT4 estimate and
+    evaluates each refined vector's LUT4 bound, and the far scan publishes exactly the vectors
+    whose LUT4 bound lies below the threshold (within the refined pre-filter's rounding bound),
+    all against the oracle's LUT4 restatement (filter_kernels.cuh:655-708): the threshold is
+    backed by topk vanguard vectors below it, the publication counts lie in the oracle's bands,
+    and the final top-k are oracle distances at or below the threshold, complete below it, and
+    the exhaustive LUT4 top-k of the probed clusters."""
+    case, nprobe, vanguard = synth_ip768, 16, 5
+    nq, P = case.queries.shape[0], case.file.padded_dim
+    say(f"[gpu] LUT4 staged vanguard pass, frozen parity, top-{topk}")
+    eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True, ip_kernel_type="lut4",
+                      extra_flags=ca.FLAG_GPU_SEED_FROZEN)
+    eng.reset_buffer(case.queries)
+    d, i = eng.search(case.queries, topk, nprobe)
+    st = eng.stats()
+    assert st["vanguard_mode"] == 4, st["vanguard_mode"]
+    g = gpu_intermediates(eng, case, nprobe)
+    luts = eng.debug_read(ca.DBG_LUT, (nq, P // 4, 16), np.uint16).view(np.float16)
+    thr = eng.debug_read(ca.DBG_THRESHOLDS, (nq,), np.float32)
+    assert st["seeded_queries"] == nq
+    van_lo = van_hi = far_lo = far_hi = 0
+    sd = case.sd
+    for q in range(nq):
+        T = float(thr[q])
+        assert np.isfinite(T), q
+        band = 1e-5 * (abs(T) + 1)
+        backing = 0
+        info = {}
+        for p, gid, low, rd, err in probed_vectors_lut(case, g, q, nprobe, luts[q]):
+            if p < vanguard:
+                backing += int(((rd < T) & (low < T + band)).sum())
+                van_lo += int(((low < T - band) & (rd <= T + 0.9 * err)).sum())
+                van_hi += int((rd <= T + 1.1 * err).sum())
+            else:
+                far_lo += int(((low < T - band) & (rd <= T + 0.9 * err)).sum())
+                far_hi += int(((low < T + band) & (rd <= T + 1.1 * err)).sum())
+            for k in range(gid.size):
+                info[int(sd.ids[gid[k]])] = (p, low[k], rd[k], err[k])
+        assert backing >= topk, (q, backing)
+        scale = abs(T) + 1
+        for r in range(topk):
+            p, low, rd, err = info[int(i[q, r])]
+            assert abs(float(d[q, r]) - rd) <= 1e-5 * scale + err, (q, r)
+            assert low < T + band or (p < vanguard and rd <= T + 1.1 * err), (q, r)
+        assert float(d[q, topk - 1]) <= T + band, q
+        got = set(i[q].tolist())
+        kth = float(d[q, topk - 1])
+        for pid, (p, low, rd, err) in info.items():
+            if low < T - band and rd < kth - 1e-5 * scale - 2 * err:
+                assert pid in got, (q, pid)
+    produced = st["pass_produced"]
+    say(f"[gpu]   vanguard published {produced[0]} in [{van_lo}, {van_hi}], far "
+        f"{produced[1] - produced[0]} in [{far_lo}, {far_hi}], refined on the GPU {st['gpu_refined']}")
+    assert van_lo <= produced[0] <= van_hi
+    assert far_lo <= produced[1] - produced[0] <= far_hi
+    assert produced[2] == produced[1]
+    ed, ei, _ = oracle_topk_from_gpu(case, g, nprobe, topk, luts=luts)
+    same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), ei.tolist())])
+    say(f"[gpu]   top-k overlap with the exhaustive LUT4 search {same:.4f}")
+    assert same >= 0.99, same
     eng.close()
