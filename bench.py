@@ -197,8 +197,11 @@ def main():
     ap.add_argument("--no-vanguard-mfma", action="store_true",
                     help="vanguard lower bounds inside the per-query pass instead of the matrix-core lows pass")
     ap.add_argument("--vanguard-one-pass", action="store_true",
-                    help="after the lows pass, run the vanguard pairs in the one per-query kernel instead of the "
-                         "staged pass (per-query select and merge around grid-wide refinement)")
+                    help="after the lows pass, run the vanguard pairs in the one per-query kernel (the default up "
+                         "to top-32 with the Bitwise estimator)")
+    ap.add_argument("--vanguard-staged", action="store_true",
+                    help="after the lows pass, run the staged vanguard pass (per-query select and merge around "
+                         "grid-wide refinement; the default above top-32 and with LUT4)")
     ap.add_argument("--vanguard-mfma", action="store_true",
                     help="run the matrix-core vanguard lows pass whatever the index size and dimension")
     ap.add_argument("--ip-kernel", choices=["bitwise", "lut4"], default="bitwise",
@@ -274,6 +277,7 @@ def main():
                                (ca.FLAG_NO_VANGUARD_MFMA if args.no_vanguard_mfma else 0) |
                                (ca.FLAG_VANGUARD_MFMA if args.vanguard_mfma else 0) |
                                (ca.FLAG_VANGUARD_ONE_PASS if args.vanguard_one_pass else 0) |
+                               (ca.FLAG_VANGUARD_STAGED if args.vanguard_staged else 0) |
                                (ca.FLAG_UNFUSED_PROBE if args.unfused_probe else 0),
                    lower_bound_scale=args.lower_bound_scale or None, gpu_final_topk=args.gpu_final,
                    ip_kernel_type=args.ip_kernel)

@@ -50,6 +50,7 @@ FLAG_GPU_FINAL = 1 << 11
 FLAG_LUT4 = 1 << 12
 FLAG_UNFUSED_PROBE = 1 << 13
 FLAG_VANGUARD_ONE_PASS = 1 << 14
+FLAG_VANGUARD_STAGED = 1 << 15
 KERNEL_TYPES = {None: 0, "lut4": 1, "bitwise": 2}
 
 

@@ -1096,7 +1096,11 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     p.dropped = E->d_stats + 7;
     VanguardArgs va{};
     // the staged pass (grid-wide refinement) where the lows pass wrote every vanguard bound
-    const bool staged = van_lows && E->d_vs_seed_pos && (lut || !(a->flags & CORA_FLAG_VANGUARD_ONE_PASS));
+    // (measured at config 4: top-10 1.56M QPS one-pass against 1.51M staged, top-100 512k
+    // against 593k)
+    const bool staged = van_lows && E->d_vs_seed_pos &&
+                        (lut || (a->flags & CORA_FLAG_VANGUARD_STAGED) ||
+                         (a->topk > CORA_VANGUARD_STAGED_TOPK && !(a->flags & CORA_FLAG_VANGUARD_ONE_PASS)));
     p.van_mins = staged ? E->d_van_mins : nullptr;
     E->last_fused = fused && depth > 0;
     E->last_van_lows = van_lows;

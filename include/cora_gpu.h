@@ -96,22 +96,30 @@ enum cora_search_flags {
     /* LUT4 estimator, the reference's KernelType::Lut4Bit (query_kernels.cuh:199-221,
      * filter_kernels.cuh:283-306,586-770): <q',b> is the FP32 sum of FP16 nibble-table
      * entries (even and odd nibbles in two accumulators), used for the lower bound and handed
-     * to refinement as exact_ip. Runs the per-pair seed, far and recovery passes (no fused
-     * vanguard pass, no matrix-core scans) with at most 4 same-cluster pairs per pass.
+     * to refinement as exact_ip. For padded dimension 512, 768 or 1024 with cross-query
+     * reuse, the matrix-core lows pass and far scan filter with Bitwise bounds lowered by a
+     * per-query bound on |LUT4 - Bitwise| and evaluate the survivors' LUT4 bounds exactly, and
+     * the staged vanguard pass refines with the LUT4 estimate; otherwise the per-pair seed,
+     * far and recovery passes run with at most 4 same-cluster pairs per pass.
      * Without it the Bitwise estimator runs (Bq=8 popcount bound; two-stage exact_ip). */
     CORA_FLAG_LUT4 = 1u << 12,
     /* Coarse probe through the whole [nq][nlist] distance matrix and a select pass over it.
-     * Without it, for 8,192 <= nlist <= 65,536 and nprobe <= 64 (split-FP16 GEMM), the GEMM's
-     * epilogue keeps 8 candidate keys per query and 128-cluster tile and a merge selects from
-     * them, with the same result; the distance matrix is then not available to
-     * CORA_DBG_PROBE_DIST (its memory holds the candidates). */
+     * Without it, for 8,192 <= nlist <= 65,536 and nprobe <= 64, or up to 1,024 while the
+     * 128-cluster tiles hold at most ~4.5 probes each on average (split-FP16 GEMM), the GEMM's
+     * epilogue keeps 8 (16 above nprobe 64) candidate keys per query and 128-cluster tile and
+     * a merge selects from them, with the same result; the distance matrix is then not
+     * available to CORA_DBG_PROBE_DIST (its memory holds the candidates). */
     CORA_FLAG_UNFUSED_PROBE = 1u << 13,
-    /* Fused vanguard pass after the matrix-core lows pass: run it as one per-query kernel
-     * (each query selects, refines and publishes in turn) instead of the staged pass, whose
-     * refinement of every query's candidates runs grid-wide between per-query select and
-     * merge stages, with the same rules for what is refined, published and the threshold. */
-    CORA_FLAG_VANGUARD_ONE_PASS = 1u << 14
+    /* Fused vanguard pass after the matrix-core lows pass: the one per-query kernel (each
+     * query selects, refines and publishes in turn), or the staged pass, whose refinement of
+     * every query's candidates runs grid-wide between per-query select and merge stages, with
+     * the same rules for what is refined, published and the threshold. By default the staged
+     * pass runs for top-k above CORA_VANGUARD_STAGED_TOPK and with the LUT4 estimator (which
+     * only it supports), the one-pass kernel otherwise; these flags choose one. */
+    CORA_FLAG_VANGUARD_ONE_PASS = 1u << 14,
+    CORA_FLAG_VANGUARD_STAGED = 1u << 15
 };
+#define CORA_VANGUARD_STAGED_TOPK 32
 
 typedef struct cora_gpu_engine cora_gpu_engine;
 

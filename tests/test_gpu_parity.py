@@ -655,7 +655,7 @@ def test_live_thresholds_match_frozen_results(synth, mode, topk):
                       gpu_seed_refine=mode != "none",
                       extra_flags={"pair": ca.FLAG_PAIR_SEEDS,
                                    "fused_lows": ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_ONE_PASS,
-                                   "staged": ca.FLAG_VANGUARD_MFMA}.get(mode, 0))
+                                   "staged": ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_STAGED}.get(mode, 0))
     eng.reset_buffer(synth.queries)
     d, i = eng.search(synth.queries, topk, nprobe, 4)
     st = eng.stats()
@@ -688,7 +688,7 @@ def test_gpu_final_topk_matches_cpu_refinement(case_name, topk, lows, request):
     nprobe, nq = 16, case.queries.shape[0]
     say(f"[gpu] GPU-final top-{topk} vs CPU refinement on {case_name} lows={lows}")
     flags = ca.FLAG_GPU_SEED_FROZEN | (ca.FLAG_VANGUARD_MFMA if lows else 0) | \
-        (ca.FLAG_VANGUARD_ONE_PASS if lows is True else 0)
+        (ca.FLAG_VANGUARD_ONE_PASS if lows is True else ca.FLAG_VANGUARD_STAGED if lows else 0)
     res = {}
     for final in (False, True):
         eng = make_engine(case, nprobe, topk, vanguard=5, frozen=True, extra_flags=flags, gpu_final_topk=final,
@@ -740,7 +740,8 @@ def test_vanguard_mode_reported(synth):
     nprobe = 16
     eng = make_engine(synth, nprobe, 129, vanguard=5, frozen=False, secondary=True)
     for topk, flags, mode in [(10, 0, 2), (10, ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_ONE_PASS, 3),
-                              (10, ca.FLAG_VANGUARD_MFMA, 4), (129, 0, 1), (10, ca.FLAG_PAIR_SEEDS, 1)]:
+                              (10, ca.FLAG_VANGUARD_MFMA, 3), (10, ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_STAGED, 4),
+                              (100, ca.FLAG_VANGUARD_MFMA, 4), (129, 0, 1), (10, ca.FLAG_PAIR_SEEDS, 1)]:
         eng.configure(vanguard_size=5, cpu_secondary_filter=True, metric=synth.file.metric, gpu_filter_timing=True,
                       extra_flags=flags, lower_bound_scale=1.0)
         eng.reset_buffer(synth.queries)
@@ -962,7 +963,7 @@ def test_fused_vanguard_frozen_parity(case_name, vanguard, topk, lows, request):
     say(f"[gpu] fused vanguard pass, frozen parity, {case_name} vanguard={vanguard} lows={lows}")
     eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True,
                       extra_flags=ca.FLAG_GPU_SEED_FROZEN | (ca.FLAG_VANGUARD_MFMA if lows else ca.FLAG_NO_VANGUARD_MFMA) |
-                      (ca.FLAG_VANGUARD_ONE_PASS if lows is True else 0))
+                      (ca.FLAG_VANGUARD_ONE_PASS if lows is True else ca.FLAG_VANGUARD_STAGED if lows else 0))
     eng.reset_buffer(case.queries)
     d, i = eng.search(case.queries, topk, nprobe)
     st = eng.stats()
@@ -1034,7 +1035,7 @@ def test_staged_vanguard_pool_overflow(case_name, topk, request, monkeypatch):
     nprobe, vanguard = 16, 5
     case = request.getfixturevalue(case_name)
     nq = case.queries.shape[0]
-    flags = ca.FLAG_GPU_SEED_FROZEN | ca.FLAG_VANGUARD_MFMA
+    flags = ca.FLAG_GPU_SEED_FROZEN | ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_STAGED
     say(f"[gpu] staged vanguard pass, pool overflow, {case_name} top-{topk}")
     eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True, extra_flags=flags)
     eng.reset_buffer(case.queries)
