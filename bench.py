@@ -109,15 +109,18 @@ def extra_lines(eng, eng_cfg, queries, gt, c, nprobe, args, traffic_key):
     - reference_structure: the reference's structure, GPU filter -> ring -> CPU refinement of
       every candidate (GPU seed thresholds and GPU refined pre-filter off), its QPS and recall.
     The engine is configured back to eng_cfg afterwards."""
-    import coraanns_amd as ca  # noqa: F401  (loaded by main)
+    import coraanns_amd as ca
 
-    def timed(cfg, batch_q):
+    def timed(cfg, batch_q, chunk=None):
         eng.configure(**cfg)
         rows = []
         for it in range(1 + args.extra_steps):
             t0 = time.perf_counter()
-            eng.reset_buffer(queries)
-            _, ids = eng.search(queries, c.topk, nprobe, batch_q)
+            if chunk:
+                _, ids = eng.search_all(queries, c.topk, nprobe, batch_q, chunk=chunk)
+            else:
+                eng.reset_buffer(queries)
+                _, ids = eng.search(queries, c.topk, nprobe, batch_q)
             dt = time.perf_counter() - t0
             if it:
                 rows.append((dt, ids, eng.stats()))
@@ -139,13 +142,28 @@ def extra_lines(eng, eng_cfg, queries, gt, c, nprobe, args, traffic_key):
                       "qps": round(queries.shape[0] * len(rows) / sum(dt for dt, _, _ in rows), 1)}
     log(f"[scan_q1] nprobe={nprobe} scan {ms:.3f}ms {nbytes / 1e6:.1f}MB -> {ach:.1f} GB/s "
         f"({ach / HBM_PEAK_GBPS:.3f} of peak)")
-    rows = timed(dict(eng_cfg, gpu_seed_refine=False, gpu_refine_filter=False, gpu_final_topk=False),
-                 args.batch_q or c.batch_q)
+    if args.no_reference_structure:
+        eng.configure(**eng_cfg)
+        return out
+    # every candidate goes to the ring: when a chunk of all queries publishes more than the
+    # ring and its HBM spill hold (the reference's default sizes), the queries go in smaller
+    # chunks, as the reference driver's --query-chunk does
+    ref_cfg = dict(eng_cfg, gpu_seed_refine=False, gpu_refine_filter=False, gpu_final_topk=False)
+    chunk = None
+    for chunk in (None, 2048, 512):
+        try:
+            rows = timed(ref_cfg, args.batch_q or c.batch_q, chunk)
+            break
+        except ca.EngineError as e:
+            if e.code != 4 or chunk == 512:  # CORA_ERR_SPILL_EXHAUSTED
+                raise
+            log(f"[reference_structure] {e}; query chunks of {2048 if chunk is None else 512}")
     qps = queries.shape[0] * len(rows) / sum(dt for dt, _, _ in rows)
     out["reference_structure"] = {
         "what": "GPU filter -> ring -> CPU refinement of every candidate (--no-gpu-seed --no-gpu-prefilter), "
                 "the reference's structure, same index, queries, nprobe and batch-q",
         "qps": round(qps, 1), "ms_per_step": round(1000.0 * sum(dt for dt, _, _ in rows) / len(rows), 3),
+        "query_chunk": chunk or queries.shape[0],
         "recall_at_10": round(float(np.mean([recall_at_k(i, gt, 10) for _, i, _ in rows])), 4),
         f"recall_at_{c.topk}": round(float(np.mean([recall_at_k(i, gt, c.topk) for _, i, _ in rows])), 4),
         "candidates_per_query": round(float(np.mean([st["submitted"] for _, _, st in rows])) / queries.shape[0], 1)}
@@ -217,6 +235,8 @@ def main():
     ap.add_argument("--no-extra-lines", action="store_true",
                     help="configs 4 and 5: skip the Q=1 scan roofline and the reference-structure line")
     ap.add_argument("--extra-steps", type=int, default=3, help="timed steps of each extra line (after 1 warmup)")
+    ap.add_argument("--no-reference-structure", action="store_true",
+                    help="of the extra lines, measure the Q=1 scan only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (PMC byte-count calibration)")
     args = ap.parse_args()

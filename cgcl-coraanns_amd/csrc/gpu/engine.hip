@@ -20,10 +20,11 @@ namespace {
 constexpr unsigned long long kDrainMaxSeconds = 20;        // drain wait for the CPU consumer
 constexpr uint64_t kMaxQueryChunk = 65535;                  // parameters.hpp:12
 constexpr uint64_t kMaxProbeCount = 65536;                  // parameters.hpp:13
-// seeds per query the staged vanguard pass refines first: at least 128 and twice the top-k
-// (their cut is a rank among 512 sub-stream minima of the query's group minima)
+static_assert(kVanguardStagedMaxTopk == CORA_VANGUARD_STAGED_MAX_TOPK, "staged top-k limit");
+// seeds per query the staged vanguard pass refines first: at least 128 and twice the top-k, at
+// most 2,048 (their cut is a rank among 4,096 sub-stream minima of the query's group minima)
 constexpr uint32_t kVsSeeds = 128;
-uint32_t vs_seed_target(uint32_t topk) { return std::min<uint32_t>(512, std::max<uint32_t>(kVsSeeds, 2 * topk)); }
+uint32_t vs_seed_target(uint32_t topk) { return std::min<uint32_t>(2048, std::max<uint32_t>(kVsSeeds, 2 * topk)); }
 
 template <class T>
 void dfree(T *&p) {
@@ -154,6 +155,15 @@ struct cora_gpu_engine {
 };
 
 namespace {
+
+// The staged pass can serve top-k above kVanguardMaxTopk at this vanguard depth: its kernels
+// are there and its seed and list regions hold every vanguard vector of a query, so no query
+// overflows to the one-pass kernel.
+bool staged_high_k_ok(const cora_gpu_engine *E, uint32_t flags, uint32_t depth) {
+    const uint64_t all = (uint64_t)depth * E->van_stride;
+    return depth > 0 && E->d_van_lows && E->d_vs_seed_pos && far_mfma_supported(E->W) &&
+           !(flags & CORA_FLAG_NO_VANGUARD_MFMA) && E->vs_seed_cap >= all && E->vs_list_cap >= all;
+}
 
 int fail(cora_gpu_engine *e, int code, const std::string &msg) {
     if (e)
@@ -707,6 +717,12 @@ int cora_gpu_prepare_workspace(cora_gpu_engine *E, uint64_t max_q, uint64_t max_
                 const auto up256 = [](uint64_t x) { return (x + 255) / 256 * 256; };
                 const uint64_t seeds = vs_seed_target((uint32_t)max_topk);
                 uint64_t seed_cap = up256(4 * seeds), list_cap = std::max<uint64_t>(4096, up256(16 * seeds));
+                // above the one-pass kernel's top-k only the staged pass serves a query, so its
+                // regions hold every vanguard vector and cannot overflow
+                if (max_topk > kVanguardMaxTopk) {
+                    seed_cap = std::max<uint64_t>(seed_cap, depth * E->van_stride);
+                    list_cap = std::max<uint64_t>(list_cap, depth * E->van_stride);
+                }
                 // CORA_VANGUARD_REGION_CAP: smaller regions (tests of the overflow path)
                 if (const char *env = getenv("CORA_VANGUARD_REGION_CAP"))
                     seed_cap = list_cap = std::max<uint64_t>(64, strtoull(env, nullptr, 10));
@@ -897,15 +913,17 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // frozen snapshot in its GPU-seeded test mode)
     const bool want_final = (a->flags & CORA_FLAG_GPU_FINAL) != 0;
     const bool lut = (a->flags & CORA_FLAG_LUT4) != 0;
+    const uint32_t final_max_topk =
+        staged_high_k_ok(E, a->flags, (uint32_t)want_depth) ? kVanguardStagedMaxTopk : kVanguardMaxTopk;
     if (want_final &&
         (!E->d_exrec || !E->d_fkeys ||
          (a->flags & (CORA_FLAG_NO_GPU_SEED | CORA_FLAG_NO_GPU_PREFILTER | CORA_FLAG_PAIR_SEEDS | CORA_FLAG_LUT4)) ||
          ((a->flags & CORA_FLAG_FROZEN_THRESHOLDS) && !(a->flags & CORA_FLAG_GPU_SEED_FROZEN)) ||
-         want_depth == 0 || want_depth > kVanguardMaxPairs || a->topk > kVanguardMaxTopk))
+         want_depth == 0 || want_depth > kVanguardMaxPairs || a->topk > final_max_topk))
         return fail(E, CORA_ERR_LOGIC,
                     "GPU-final top-k needs the ex-codes in HBM, GPU seed thresholds and the refined "
-                    "pre-filter, the fused vanguard pass (vanguard 1..64, topk <= 128, Bitwise estimator) "
-                    "and live thresholds");
+                    "pre-filter, the fused vanguard pass (vanguard 1..64, topk <= 128, or <= 1024 with "
+                    "the staged pass's regions, Bitwise estimator) and live thresholds");
     HIPCHK(hipSetDevice(E->device));
     E->final_mode = want_final;
     E->last_final = want_final;
@@ -1041,9 +1059,15 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool prefilter = E->d_exrec && ex_stage_mode && !(a->flags & CORA_FLAG_NO_GPU_PREFILTER);
     // fused per-query vanguard pass (vanguard.hip) unless the reference's per-pair passes
     // are asked for or the shape exceeds its limits
-    const bool lut_staged = lut_mfma && E->d_van_lows && E->d_vs_seed_pos && !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA);
+    const bool staged_ok = E->d_van_lows && E->d_vs_seed_pos && far_mfma_supported(E->W) &&
+                           !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA);
+    const bool lut_staged = lut_mfma && staged_ok;
+    // above kVanguardMaxTopk (up to kVanguardStagedMaxTopk) only the staged pass, with regions
+    // that hold every vanguard vector
     const bool fused = gpu_seed && (!lut || lut_staged) && !(a->flags & CORA_FLAG_PAIR_SEEDS) && depth <= kVanguardMaxPairs &&
-                       a->topk <= kVanguardMaxTopk;
+                       (a->topk <= kVanguardMaxTopk ||
+                        (a->topk <= kVanguardStagedMaxTopk && staged_high_k_ok(E, a->flags, depth)));
+    const bool high_k = a->topk > kVanguardMaxTopk;
     // its lower bounds first on the matrix cores, cluster-major, into the per-pair lows
     // array [nq][depth][van_stride] of the workspace
     // (by default only for wide codes whose sign codes and factors exceed the last-level
@@ -1052,7 +1076,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool lows_by_size = (uint64_t)E->N * (E->P / 8 + 12) > kLowsMinIndexBytes && E->P >= kLowsMinDim;
     const bool van_lows = fused && depth > 0 && far_mfma_supported(E->W) && E->d_van_lows &&
                           !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA) &&
-                          (lows_by_size || (a->flags & CORA_FLAG_VANGUARD_MFMA) || lut);
+                          (lows_by_size || (a->flags & CORA_FLAG_VANGUARD_MFMA) || lut || high_k);
     // fork: pair scheduling (and the fused pass's query order) on stream_aux
     HIPCHK(hipEventRecord(E->ev_fork, s));
     HIPCHK(hipStreamWaitEvent(E->stream_aux, E->ev_fork, 0));
@@ -1099,7 +1123,7 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     // (measured at config 4: top-10 1.56M QPS one-pass against 1.51M staged, top-100 512k
     // against 593k)
     const bool staged = van_lows && E->d_vs_seed_pos &&
-                        (lut || (a->flags & CORA_FLAG_VANGUARD_STAGED) ||
+                        (lut || high_k || (a->flags & CORA_FLAG_VANGUARD_STAGED) ||
                          (a->topk > CORA_VANGUARD_STAGED_TOPK && !(a->flags & CORA_FLAG_VANGUARD_ONE_PASS)));
     p.van_mins = staged ? E->d_van_mins : nullptr;
     E->last_fused = fused && depth > 0;

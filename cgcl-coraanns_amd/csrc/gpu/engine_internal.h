@@ -24,7 +24,8 @@ constexpr int kMaxVanguardKeep = 1024;
 constexpr int kSelectMaxProbe = 4096;       // top-nprobe select held in LDS
 constexpr uint32_t kNumXcd = 8;
 constexpr uint32_t kVanguardMaxPairs = 64;  // fused vanguard pass: vanguard depth limit
-constexpr uint32_t kVanguardMaxTopk = 128;  // fused vanguard pass: top-k limit
+constexpr uint32_t kVanguardMaxTopk = 128;  // one-pass vanguard kernel: top-k limit
+constexpr uint32_t kVanguardStagedMaxTopk = 1024;  // staged vanguard pass: top-k limit
 // the vanguard lows pass runs by default for sign codes + factors beyond MI355X's 256 MB
 // last-level cache and at least this padded dimension: a query's own pass reads P/8 + 12
 // bytes per vanguard vector against the lows pass's 4, a saving that pays for the extra

@@ -357,16 +357,22 @@ struct Compactor {
     }
 };
 
-// The k-th smallest (1 <= k <= 512) of the workgroup's 512 keys (two per thread), bit by bit
-// from the top: bit b of the answer is 0 when at least k keys lie at or below the answer's
+// Sub-stream minima a thread keeps in the seed select (kVsSub x 256 in all).
+constexpr int kVsSub = 16;
+
+// The k-th smallest (1 <= k <= kVsSub x 256) of the workgroup's keys (kVsSub per thread), bit by
+// bit from the top: bit b of the answer is 0 when at least k keys lie at or below the answer's
 // higher bits followed by b ones. Each step counts by wave ballots and adds the four waves'
 // counts through red2 (2 x kVsWaves words, alternating, so one barrier a step suffices).
-__device__ __forceinline__ uint32_t block_kth2(uint32_t a, uint32_t b, uint32_t k, uint32_t *red2) {
+__device__ __forceinline__ uint32_t block_kth_sub(const uint32_t (&keys)[kVsSub], uint32_t k, uint32_t *red2) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     uint32_t res = 0;
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t t = res | ((1u << bit) - 1u);
-        const uint32_t n = (uint32_t)__popcll(__ballot(a <= t)) + (uint32_t)__popcll(__ballot(b <= t));
+        uint32_t n = 0;
+#pragma unroll
+        for (int i = 0; i < kVsSub; ++i)
+            n += (uint32_t)__popcll(__ballot(keys[i] <= t));
         uint32_t *r = red2 + (bit & 1) * kVsWaves;
         if (lane == 0)
             r[wave] = n;
@@ -384,11 +390,13 @@ __device__ __forceinline__ uint32_t block_kth2(uint32_t a, uint32_t b, uint32_t 
 
 // ---- 1. seed select ----
 // The seeds are the bounds below thr_in in the groups of 4 whose minimum's key is at most
-// cut1, the `seeds`-th smallest (at most 512) of 512 sub-stream minima of the query's group
-// minima (two per thread: its elements r * 256 + t with r even, and with r odd). At least
-// `seeds` bounds lie at or below cut1, one per sub-stream, and with the groups spread over the
-// sub-streams by position, not by value, not many more. With fewer sub-streams holding a
-// bound below thr_in, every bound below thr_in is a seed.
+// cut1, the `seeds`-th smallest (at most 2,048) of 4,096 sub-stream minima of the query's
+// group minima (kVsSub per thread: its elements r * 256 + t with r = s mod kVsSub, s = 0 ..
+// kVsSub - 1; with at most 4,096 groups each sub-stream holds one, and cut1 is the exact
+// seeds-th smallest group minimum). At least `seeds` bounds lie at or below cut1, one per
+// sub-stream, and with the groups spread over the sub-streams by position, not by value, not
+// many more. With fewer sub-streams holding a bound below thr_in, every bound below thr_in is a
+// seed.
 __global__ __launch_bounds__(kVsThreads) void vs_seed_kernel(const ScanParams p, const VanguardArgs va,
                                                              const VsArgs vs) {
     __shared__ uint32_t s_n[kVanguardMaxPairs], s_off[kVanguardMaxPairs + 1], s_goff[kVanguardMaxPairs + 1];
@@ -402,18 +410,21 @@ __global__ __launch_bounds__(kVsThreads) void vs_seed_kernel(const ScanParams p,
     const uint32_t V = va.depth, gstride = p.van_stride / 4;
     const QueryRows qb{p.van_lows + (size_t)q * V * p.van_stride, s_off, p.van_stride, s_off[V]};
     const QueryRows qg{p.van_mins + (size_t)q * V * gstride, s_goff, gstride, s_goff[V]};
-    uint32_t key[kVsRegs], mn[2] = {0xFFFFFFFFu, 0xFFFFFFFFu};
+    uint32_t key[kVsRegs], mn[kVsSub];
+#pragma unroll
+    for (int i = 0; i < kVsSub; ++i)
+        mn[i] = 0xFFFFFFFFu;
     const uint32_t chunks = num_chunks(qg);
     for (uint32_t c = 0; c < chunks; ++c) {
         load_keys(qg, c, thr_in, key);
 #pragma unroll
         for (int r = 0; r < kVsRegs; ++r)
-            mn[r & 1] = min(mn[r & 1], key[r]);
+            mn[r % kVsSub] = min(mn[r % kVsSub], key[r]);
     }
     // 0xFFFFFFFF (fewer valid minima than `seeds`) becomes 0xFFFFFFFE: every bound below
     // thr_in, the invalid keys left out
-    const uint32_t want = min(vs.seeds, 2u * kVsThreads);
-    const uint32_t cut1 = min(block_kth2(mn[0], mn[1], want, s_red2), 0xFFFFFFFEu);
+    const uint32_t want = min(vs.seeds, (uint32_t)kVsSub * kVsThreads);
+    const uint32_t cut1 = min(block_kth_sub(mn, want, s_red2), 0xFFFFFFFEu);
     uint32_t nseed = 0;
     uint32_t *seed_pos = vs.seed_pos + (size_t)q * vs.seed_cap;
     auto is_seed = [cut1](uint32_t k) { return k <= cut1; };
@@ -1040,6 +1051,10 @@ void launch_vs_w(const ScanParams &p, const VanguardArgs &va, const VsArgs &vs, 
     // the queries whose seeds or list did not fit: the fused per-query kernel (with LUT4 it
     // refines them with the two-stage Bitwise estimate, and selects and publishes on the
     // lowered bounds)
+    // (above the one-pass kernel's top-k the regions hold every vanguard vector: no query
+    // overflows)
+    if (va.topk > kVanguardMaxTopk)
+        return;
     VanguardArgs fb = va;
     fb.list = vs.overflow;
     fb.list_count = &vs.ctr[kVsCtrOverflow];

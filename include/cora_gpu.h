@@ -65,7 +65,8 @@ enum cora_search_flags {
     CORA_FLAG_NO_GPU_PREFILTER = 1u << 5,
     /* Run the vanguard pairs as the reference does, a per-pair seed pass followed by a
      * recovery pass over each pair, instead of the fused per-query vanguard pass that is
-     * used when the ex-codes are resident in HBM (vanguard depth <= 64, topk <= 128). */
+     * used when the ex-codes are resident in HBM (vanguard depth <= 64, topk <= 128, or up to
+     * CORA_VANGUARD_STAGED_MAX_TOPK in the staged pass; see CORA_FLAG_VANGUARD_STAGED). */
     CORA_FLAG_PAIR_SEEDS = 1u << 6,
     /* Scan the far pairs with the popcount kernel even where the matrix-core kernel
      * applies (cross-query reuse with padded dimension 64..256, 512, 768 or 1024). */
@@ -91,7 +92,8 @@ enum cora_search_flags {
      * form the final per-query top-k on the GPU (cora_gpu_final_results); nothing goes to
      * the ring and no CPU refinement runs (the reference's GPU baseline engine refines on
      * the GPU likewise, src/baselines/gpu.cu:630-700). Needs the ex-codes in HBM, the fused
-     * vanguard pass (topk <= 128, vanguard <= 64) and the refined pre-filter. */
+     * vanguard pass (vanguard <= 64, topk <= 128, or <= CORA_VANGUARD_STAGED_MAX_TOPK where
+     * the staged pass serves it) and the refined pre-filter. */
     CORA_FLAG_GPU_FINAL = 1u << 11,
     /* LUT4 estimator, the reference's KernelType::Lut4Bit (query_kernels.cuh:199-221,
      * filter_kernels.cuh:283-306,586-770): <q',b> is the FP32 sum of FP16 nibble-table
@@ -115,11 +117,15 @@ enum cora_search_flags {
      * every query's candidates runs grid-wide between per-query select and merge stages, with
      * the same rules for what is refined, published and the threshold. By default the staged
      * pass runs for top-k above CORA_VANGUARD_STAGED_TOPK and with the LUT4 estimator (which
-     * only it supports), the one-pass kernel otherwise; these flags choose one. */
+     * only it supports), the one-pass kernel otherwise; these flags choose one. Top-k above
+     * 128 (up to CORA_VANGUARD_STAGED_MAX_TOPK) is served by the staged pass alone, when the
+     * workspace was prepared for it (its per-query regions then hold every vanguard vector)
+     * and the matrix-core lows pass applies; otherwise the per-pair passes run. */
     CORA_FLAG_VANGUARD_ONE_PASS = 1u << 14,
     CORA_FLAG_VANGUARD_STAGED = 1u << 15
 };
 #define CORA_VANGUARD_STAGED_TOPK 32
+#define CORA_VANGUARD_STAGED_MAX_TOPK 1024
 
 typedef struct cora_gpu_engine cora_gpu_engine;
 

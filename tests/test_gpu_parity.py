@@ -735,13 +735,14 @@ def test_gpu_final_topk_rejects_unsupported_modes(synth):
 
 
 def test_vanguard_mode_reported(synth):
-    """Which vanguard passes ran is reported, including the fallback to the per-pair passes
-    beyond the fused pass's limits (top-k above 128)."""
+    """Which vanguard passes ran is reported: top-k above 128 in the staged pass (the
+    workspace prepared for it), or the per-pair passes where the staged pass cannot run."""
     nprobe = 16
     eng = make_engine(synth, nprobe, 129, vanguard=5, frozen=False, secondary=True)
     for topk, flags, mode in [(10, 0, 2), (10, ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_ONE_PASS, 3),
                               (10, ca.FLAG_VANGUARD_MFMA, 3), (10, ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_STAGED, 4),
-                              (100, ca.FLAG_VANGUARD_MFMA, 4), (129, 0, 1), (10, ca.FLAG_PAIR_SEEDS, 1)]:
+                              (100, ca.FLAG_VANGUARD_MFMA, 4), (129, 0, 4), (129, ca.FLAG_NO_VANGUARD_MFMA, 1),
+                              (10, ca.FLAG_PAIR_SEEDS, 1)]:
         eng.configure(vanguard_size=5, cpu_secondary_filter=True, metric=synth.file.metric, gpu_filter_timing=True,
                       extra_flags=flags, lower_bound_scale=1.0)
         eng.reset_buffer(synth.queries)
@@ -1414,3 +1415,38 @@ def test_lut4_staged_vanguard_frozen_parity(topk, synth_ip768):
     say(f"[gpu]   top-k overlap with the exhaustive LUT4 search {same:.4f}")
     assert same >= 0.99, same
     eng.close()
+
+
+@pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
+@pytest.mark.parametrize("vanguard,topk", [(16, 513), (5, 1024), (16, 1024)])
+def test_high_k_staged_vanguard(case_name, vanguard, topk, request):
+    """Top-k above the one-pass kernel's limit (128) with the GPU ex-code stages on: the
+    staged pass serves it (mode 4). GPU-final top-k in the GPU-seeded frozen mode (bound
+    scale 3, every bound valid) against the oracle's exhaustive top-k of the probed vectors;
+    the default live-threshold search with the CPU consumer against the exhaustive frozen
+    search without vanguard pairs."""
+    case = request.getfixturevalue(case_name)
+    nprobe, nq = 16, case.queries.shape[0]
+    say(f"[gpu] high-k staged on {case_name} vanguard={vanguard} topk={topk}")
+    eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=True, extra_flags=ca.FLAG_GPU_SEED_FROZEN,
+                      gpu_final_topk=True, lower_bound_scale=3.0)
+    eng.reset_buffer(case.queries)
+    dg, ig = eng.search(case.queries, topk, nprobe)
+    st = eng.stats()
+    assert st["vanguard_mode"] == 4, st["vanguard_mode"]
+    assert st["refined"] == 0 and st["submitted"] > 0
+    g = gpu_intermediates(eng, case, nprobe)
+    eng.close()
+    od, oi, _ = oracle_topk_from_gpu(case, g, nprobe, topk)
+    assert_topk_equal(dg, ig, od, oi, rtol=2e-4)
+    _, d0, i0 = run_frozen(case, nprobe, topk, vanguard=0)
+    eng = make_engine(case, nprobe, topk, vanguard=vanguard, frozen=False, secondary=True)
+    eng.reset_buffer(case.queries)
+    d, i = eng.search(case.queries, topk, nprobe, 4)
+    st = eng.stats()
+    eng.close()
+    assert st["vanguard_mode"] == 4, st["vanguard_mode"]
+    if vanguard == nprobe:  # every probed vector is a vanguard vector: at least topk of them
+        assert st["seeded_queries"] == nq, st["seeded_queries"]
+    same = np.mean([len(set(a) & set(b)) / topk for a, b in zip(i.tolist(), i0.tolist())])
+    assert same >= 0.99, same

@@ -159,10 +159,14 @@ def test_spill_exhaustion_reports_error_then_recovers(allpass):
 
 
 @pytest.mark.parametrize("k", [10, 100, 513, 1024])
-def test_high_k_vanguard_on_off_identical(k):
-    say(f"[gpu] high-k k={k}")
+@pytest.mark.parametrize("stages", [False, True])
+def test_high_k_vanguard_on_off_identical(k, stages):
+    """The reference's high-k scenario (tests/gpu_cpu_highk_vanguard_test.cpp:81-90) with the
+    vanguard pairs on and off; with the GPU ex-code stages on (stages), the vanguard pairs run
+    in the fused pass, above top-128 in its staged form."""
+    say(f"[gpu] high-k k={k} stages={stages}")
     f = AllPass(k=1024)
-    e = f.engine(1 << 20, 1 << 20, 5)
+    e = f.engine(1 << 20, 1 << 20, 5, gpu_seed_refine=stages, gpu_refine_filter=stages)
     order = np.argsort(f.lf[:, 0], kind="stable")
     expected = np.sort(order[:k])
     results = []
@@ -175,6 +179,13 @@ def test_high_k_vanguard_on_off_identical(k):
                 q = f.query[b:b + chunk]
                 e.reset_buffer(q)
                 d, i = e.search(q, k, f.clusters)
+                mode = e.stats()["vanguard_mode"]
+                if vanguard == 0:
+                    assert mode == 0, mode
+                elif not stages:
+                    assert mode == 1, mode
+                else:
+                    assert mode == (4 if k > 128 else 2), mode
                 ids.append(i)
                 dists.append(d)
             ids = np.vstack(ids)
