@@ -349,6 +349,7 @@ def main():
     select_ms = []
     recalls_k = []
     van_ms, van_bytes, lows_ms, lows_bytes, ref_ms, ref_bytes, van_modes = [], [], [], [], [], [], []
+    cands = []
     staged_counts = []
     last_ids = None
     for _ in range(args.steps):
@@ -368,6 +369,7 @@ def main():
         ref_ms.append(st["vanguard_refine_ms"])
         ref_bytes.append(st["vanguard_refine_bytes"])
         van_modes.append(st["vanguard_mode"])
+        cands.append(st["submitted"])
         if st["vanguard_mode"] == 4 and not staged_counts:
             staged_counts.extend(int(x) for x in eng.debug_read(ca.DBG_STAGED_COUNTS, (4,), np.uint64))
             log(f"[staged] seeds {staged_counts[0]}, list {staged_counts[1]}, lists from a second pass "
@@ -409,6 +411,7 @@ def main():
                       "fp32_equivalent_tflops": round(probe_tflops, 3)}
     probe_line["select_and_gadd_ms"] = round(float(np.mean(select_ms)), 4)
     log(f"[timed] nprobe={nprobe} steps={args.steps} QPS={qps:.1f} recall={np.mean(recalls):.4f} "
+        f"cand/q={np.mean(cands) / queries.shape[0]:.1f} "
         f"vanguard lows={avg_lows_ms:.3f}ms {lows_bpl / 1e6:.1f}MB -> {lows_achieved:.1f} GB/s; "
         f"vanguard={avg_van_ms:.3f}ms {van_bpl / 1e6:.1f}MB -> {van_achieved:.1f} GB/s "
         f"(mode {van_modes[-1] if van_modes else 0}; refinement {avg_ref_ms:.3f}ms {ref_bpl / 1e6:.1f}MB -> "

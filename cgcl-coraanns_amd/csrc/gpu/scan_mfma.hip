@@ -1,15 +1,17 @@
-// Far-pair scan on the matrix cores (gfx950 v_mfma_i32_16x16x32_i8).
+// Far-pair scan on the matrix cores (gfx950 v_mfma_i32_16x16x64_i8, and 16x16x32 for
+// P = 64 and 192).
 //
 // The Bitwise estimator's integer inner product (filter_kernels.cuh:79-114)
 //     ip_int = sum_i b_i * qint_i        (b_i the sign bit of dimension i, qint_i in [-128, 127])
 // is a product of a 0/1 matrix with an int8 matrix, exact in int32. A scan unit serves up
 // to 16 same-cluster pairs, so a 64-vector tile against the unit's queries is a
-// [64 x P] x [P x 16] integer product: four 16x16 output blocks, P/32 K-steps each, plus
-// the same product against the residual query (qres) for the two-stage exact_ip. The
-// code bits are widened to int8 through a 256-entry table in LDS (one 8-byte read per
-// code byte); the queries' int8 values come from the query preparation. ip_int and ip_res are
-// therefore bit-identical to the popcount kernel's (scan.hip), and the lower bound uses
-// the same expression, so the candidate set is the same.
+// [64 x P] x [P x 16] integer product: four 16x16 output blocks, P/64 (P/32) K-steps each.
+// The residual product against qres for the two-stage exact_ip is formed by popcount for
+// the survivors only (and, at P = 64 and 192, as a second MFMA product). The code bits are
+// widened to int8 through a 256-entry table in LDS (one 8-byte read per code byte); the
+// queries' int8 values come from the query preparation. ip_int and ip_res are therefore
+// bit-identical to the popcount kernel's (scan.hip), and the lower bound uses the same
+// expression, so the candidate set is the same.
 //
 // MFMA lane layout (16x16x32 i8): lane l supplies A[l%16][8(l/16)+e] and B[8(l/16)+e][l%16]
 // (byte e of a 64-bit operand) and holds D[4(l/16)+r][l%16], r = 0..3. Here rows are
@@ -165,7 +167,9 @@ __device__ void flush_records(const ScanParams &p, const QueueDev &q, uint32_t n
     __syncthreads();
 }
 
-// W = P / 32 words per vector (W even, W <= 8: the unit's query operands stay in VGPRs).
+// W = P / 32 words per vector, W = 2 or 6 (P = 64, 192; the other widths run the wide
+// kernel below): the unit's query operands stay in VGPRs, one v_mfma_i32_16x16x32_i8 per
+// code word and row block.
 // kDenseDbg: write ip_int, ip_res and the lower bound of every (vector, pair) to the debug
 // arrays instead of publishing (the estimator parity test of the kernel the search runs).
 // kLows: the vanguard units; every lower bound goes to van_lows, ip_res is not formed.
@@ -401,12 +405,44 @@ __device__ __noinline__ void flush_wide(const ScanParams &p, uint32_t n, uint4 *
 
 constexpr int kStageWide = 384;  // wide kernel: flushed when a row block could overflow it
 
-// Wide codes (W = 16, 24, 32: P = 512, 768, 1024) on v_mfma_i32_16x16x64_i8. Lane-group
-// g = lane / 16 owns code words [g W/4, (g+1) W/4) of every vector: K-step s (64
-// dimensions) takes the 16-bit half s % 2 of word g W/4 + s / 2, i.e. dimensions
-// 8 W g + 16 s + e, e = 0..15, and the query operand the same 16 bytes of qint, so
-// each lane loads W/8 aligned 8-byte pairs per row block and the unit's qint operands
-// (W/2 x 16 bytes) stay in VGPRs. Only the dimension pairing between the two operands
+// A tile's operands for the wide kernel's lane (col, quad): code words [WQ quad, WQ quad +
+// WQ) of vectors 16 m + col, and the factors of vectors 16 m + 4 quad + r, m = 0..3.
+template <int WQ>
+struct TileRegs {
+    uint32_t xt[4][WQ];
+    float4 fa[4], fr[4], fe[4];
+};
+
+template <int W>
+__device__ __forceinline__ void load_tile(const uint8_t *tile, uint32_t col, uint32_t quad, TileRegs<W / 4> &r) {
+    constexpr int WQ = W / 4;
+    const float *fac = reinterpret_cast<const float *>(tile + 256u * W);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const uint32_t v = 16 * m + col;
+        r.fa[m] = gload<float4>(fac + 16 * m + 4 * quad);
+        r.fr[m] = gload<float4>(fac + 64 + 16 * m + 4 * quad);
+        r.fe[m] = gload<float4>(fac + 128 + 16 * m + 4 * quad);
+        if constexpr (WQ == 1) {
+            r.xt[m][0] = gload<uint32_t>(tile + v * 16 + quad * 4);
+        } else {
+#pragma unroll
+            for (int j = 0; j < WQ; j += 2) {
+                const uint32_t w = WQ * quad + j;  // even: the pair lies in one 4-word group
+                const uint2 c = gload<uint2>(tile + (size_t)(w >> 2) * 1024 + v * 16 + (w & 3u) * 4);
+                r.xt[m][j] = c.x;
+                r.xt[m][j + 1] = c.y;
+            }
+        }
+    }
+}
+
+// Codes of W = 4, 8, 16, 24, 32 words (P = 128, 256, 512, 768, 1024) on
+// v_mfma_i32_16x16x64_i8. Lane-group g = lane / 16 owns code words [g W/4, (g+1) W/4) of
+// every vector: K-step s (64 dimensions) takes the 16-bit half s % 2 of word g W/4 + s / 2,
+// i.e. dimensions 8 W g + 16 s + e, e = 0..15, and the query operand the same 16 bytes of
+// qint, so each lane loads W/8 aligned 8-byte pairs (one word at W = 4) per row block and
+// the unit's qint operands (W/2 x 16 bytes) stay in VGPRs. Only the dimension pairing between the two operands
 // matters to the sum, so ip_int is exact. The lower bound uses the popcount kernels'
 // expression; ip_res is evaluated for survivors when they are published.
 // The sixteen code bits of an operand become sixteen int8 0/1 bytes through a 256-entry
@@ -420,10 +456,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                           : kModeT == kDenseLut ? kDenseDbg
                                                 : kModeT;
     constexpr bool kDense = kMode != kPublish;
-    static_assert(W % 8 == 0 && W >= 16 && W <= 32, "lane-group word ranges of even length");
+    static_assert(W == 4 || W == 8 || (W % 8 == 0 && W >= 16 && W <= 32), "whole words per lane-group");
+    static_assert(!kLut || W >= 16, "LUT4 modes for P >= 512");
     constexpr int WQ = W / 4;  // code words per lane-group
     constexpr int S = W / 2;   // K-steps of 64 dimensions
     constexpr uint32_t P = 32u * W;
+    constexpr bool kPrefetch = W == 4;
     __shared__ uint4 s_rec[kDense ? 1 : kStageWide];
     __shared__ float s_cut[kDense ? 1 : kStageWide];
     __shared__ uint32_t s_loc[kDense ? 1 : kStageWide];
@@ -487,27 +525,51 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
             for (int s = 0; s < S; ++s)
                 bq[s] = v4i32{0, 0, 0, 0};
         }
+        // the tile's code words and factors for all four row blocks go out first (one
+        // memory round trip per tile; at P >= 512 two waves per SIMD hold them in 251 VGPRs
+        // without spilling, measured 22% faster than three waves loading per row block); then
+        // one row block of 16 vectors at a time: its K-steps and its lower bounds. For
+        // P = 128 (W = 4, 52 VGPRs a tile) the next tile's loads are issued before the
+        // current tile's MFMAs, so each wave keeps a tile's loads in flight while it computes.
+        TileRegs<WQ> cur, nxt;
+        if constexpr (kPrefetch)
+            load_tile<W>(p.tiles + (size_t)(tbase + t_begin) * p.tile_bytes, col, quad, cur);
         for (uint32_t t = t_begin; t < t_end; ++t) {
             const uint8_t *tile = p.tiles + (size_t)(tbase + t) * p.tile_bytes;
-            const float *fac = reinterpret_cast<const float *>(tile + 256u * W);
-            // the tile's code words and factors for all four row blocks go out first (one
-            // memory round trip per tile; two waves per SIMD hold them in 251 VGPRs without
-            // spilling, measured 22% faster than three waves loading per row block); then
-            // one row block of 16 vectors at a time: its K-steps and its lower bounds
+            if constexpr (kPrefetch) {
+                // the last tile's successor is itself again (a cached reload, no branch)
+                const uint32_t tn = t + 1 < t_end ? t + 1 : t;
+                load_tile<W>(p.tiles + (size_t)(tbase + tn) * p.tile_bytes, col, quad, nxt);
+            }
+            // (at P >= 512 the loads are written out here: through the TileRegs helper the
+            // compiler schedules the wide tiles' code differently, measured 11% slower)
             uint32_t xt[4][WQ];
             float4 fat[4], frt[4], fet[4];
+            if constexpr (kPrefetch) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const uint32_t v = 16 * m + col;
-                fat[m] = gload<float4>(fac + 16 * m + 4 * quad);
-                frt[m] = gload<float4>(fac + 64 + 16 * m + 4 * quad);
-                fet[m] = gload<float4>(fac + 128 + 16 * m + 4 * quad);
+                for (int m = 0; m < 4; ++m) {
+                    fat[m] = cur.fa[m];
+                    frt[m] = cur.fr[m];
+                    fet[m] = cur.fe[m];
 #pragma unroll
-                for (int j = 0; j < WQ; j += 2) {
-                    const uint32_t w = WQ * quad + j;  // even: the pair lies in one 4-word group
-                    const uint2 c = gload<uint2>(tile + (size_t)(w >> 2) * 1024 + v * 16 + (w & 3u) * 4);
-                    xt[m][j] = c.x;
-                    xt[m][j + 1] = c.y;
+                    for (int j = 0; j < WQ; ++j)
+                        xt[m][j] = cur.xt[m][j];
+                }
+            } else {
+                const float *fac = reinterpret_cast<const float *>(tile + 256u * W);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const uint32_t v = 16 * m + col;
+                    fat[m] = gload<float4>(fac + 16 * m + 4 * quad);
+                    frt[m] = gload<float4>(fac + 64 + 16 * m + 4 * quad);
+                    fet[m] = gload<float4>(fac + 128 + 16 * m + 4 * quad);
+#pragma unroll
+                    for (int j = 0; j < WQ; j += 2) {
+                        const uint32_t w = WQ * quad + j;  // even: the pair lies in one 4-word group
+                        const uint2 c = gload<uint2>(tile + (size_t)(w >> 2) * 1024 + v * 16 + (w & 3u) * 4);
+                        xt[m][j] = c.x;
+                        xt[m][j + 1] = c.y;
+                    }
                 }
             }
 #pragma unroll
@@ -605,6 +667,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
             }
             if constexpr (kMode == kLows)
                 lows_flush(p, s_low, lane, w0, count, t, n);
+            if constexpr (kPrefetch)
+                cur = nxt;
         }
     }
     if constexpr (!kDense) {
@@ -637,7 +701,7 @@ uint32_t resident_grid_mfma(F kernel) {
 
 template <int W, int kMode>
 void launch_w(const ScanParams &p, hipStream_t s) {
-    if constexpr (W <= 8) {
+    if constexpr (W == 2 || W == 6) {
         static_assert(kMode != kPublishLut && kMode != kLowsLut && kMode != kDenseLut, "LUT4 on the wide kernel only");
         auto *k = far_mfma_kernel<W, kMode>;
         k<<<resident_grid_mfma(k), 64, 0, s>>>(p);
