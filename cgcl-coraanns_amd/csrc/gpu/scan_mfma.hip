@@ -405,6 +405,38 @@ __device__ __noinline__ void flush_wide(const ScanParams &p, uint32_t n, uint4 *
 
 constexpr int kStageWide = 384;  // wide kernel: flushed when a row block could overflow it
 
+// The Bitwise lower bound of a (vector, pair) from its ip_int (the popcount kernels'
+// expression, filter_kernels.cuh:96-112), in one place so that the publication test and
+// the staged record see the same value.
+__device__ __forceinline__ float lower_bound_of(float fa, float fr, float fe, float gadd, float gerr, float width,
+                                                float k1, int ip) {
+    const float ex = width * (float)ip;
+    return fa + gadd + fr * (ex + k1) - fe * gerr;
+}
+
+// ip_int of a row block: at W <= 8 one accumulator chain through the K-steps (the four row
+// blocks are independent chains), above that two chains (low and high halves of the words).
+template <int WQ, class Spread>
+__device__ __forceinline__ v4i32 tile_ip_int(const uint32_t (&xw)[WQ], const v4i32 *bq, const Spread &spread16) {
+    v4i32 acc = v4i32{0, 0, 0, 0};
+    if constexpr (WQ <= 2) {
+#pragma unroll
+        for (int j = 0; j < WQ; ++j) {
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16(xw[j] & 0xFFFFu), bq[2 * j], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16(xw[j] >> 16), bq[2 * j + 1], acc, 0, 0, 0);
+        }
+    } else {
+        v4i32 acc1 = v4i32{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < WQ; ++j) {
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16(xw[j] & 0xFFFFu), bq[2 * j], acc, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(spread16(xw[j] >> 16), bq[2 * j + 1], acc1, 0, 0, 0);
+        }
+        acc += acc1;
+    }
+    return acc;
+}
+
 // A tile's operands for the wide kernel's lane (col, quad): code words [WQ quad, WQ quad +
 // WQ) of vectors 16 m + col, and the factors of vectors 16 m + 4 quad + r, m = 0..3.
 template <int WQ>
@@ -462,6 +494,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
     constexpr int S = W / 2;   // K-steps of 64 dimensions
     constexpr uint32_t P = 32u * W;
     constexpr bool kPrefetch = W == 4;
+    // publication test without per-element validity or pair-slot terms: the cutoff of an
+    // empty pair slot is -inf and the rows past the cluster's end are masked per tile in
+    // SGPRs, so each (vector, pair) costs its bound and one compare
+    // (measured: far scan 2.38 -> 2.13 ms at P = 128, config 5; 1.37 -> 1.31 ms at P = 768,
+    // config 4)
+    constexpr bool kFastPub = kMode == kPublish && !kLut;
     __shared__ uint4 s_rec[kDense ? 1 : kStageWide];
     __shared__ float s_cut[kDense ? 1 : kStageWide];
     __shared__ uint32_t s_loc[kDense ? 1 : kStageWide];
@@ -571,6 +609,67 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                         xt[m][j + 1] = c.y;
                     }
                 }
+            }
+            if constexpr (kFastPub) {
+                const float cut_eff = slot ? cutoff : -__builtin_inff();
+                // rows of the tile past the cluster's end: lane-group quad holds rows
+                // 16 m + 4 quad + r, valid while that is below n - 64 t
+                const uint32_t n_rem = n - t * kTileVectors;  // >= 1
+                v4i32 accs[4];
+                unsigned long long masks[4][4], any = 0;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    accs[m] = tile_ip_int<WQ>(xt[m], bq, spread16_lds);
+                    const float4 fa = fat[m], fr = frt[m], fe = fet[m];
+                    const float fav[4] = {fa.x, fa.y, fa.z, fa.w};
+                    const float frv[4] = {fr.x, fr.y, fr.z, fr.w};
+                    const float fev[4] = {fe.x, fe.y, fe.z, fe.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float low = lower_bound_of(fav[r], frv[r], fev[r], gadd, gerr, width, k1, accs[m][r]);
+                        unsigned long long mk = __ballot(low < cut_eff);
+                        if (n_rem < kTileVectors) {
+                            const int rows = (int)n_rem - 16 * m - r;  // valid lane-groups: 4 quad < rows
+                            const int groups = rows <= 0 ? 0 : min(4, (rows + 3) >> 2);
+                            mk &= groups >= 4 ? ~0ull : (1ull << (16 * groups)) - 1ull;
+                        }
+                        masks[m][r] = mk;
+                        any |= mk;
+                    }
+                }
+                if (any) {
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        const uint32_t o = 16 * m + 4 * quad;
+                        const float4 fa = fat[m], fr = frt[m], fe = fet[m];
+                        const float fav[4] = {fa.x, fa.y, fa.z, fa.w};
+                        const float frv[4] = {fr.x, fr.y, fr.z, fr.w};
+                        const float fev[4] = {fe.x, fe.y, fe.z, fe.w};
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const unsigned long long mk = masks[m][r];
+                            if (mk == 0)
+                                continue;
+                            if (staged + 64 > (uint32_t)kStageWide) {
+                                flush_wide<W, kLut>(p, staged, s_rec, s_cut, s_loc, limit, lane);
+                                staged = 0;
+                            }
+                            if ((mk >> lane) & 1ull) {
+                                const int ip = accs[m][r];
+                                const float low = lower_bound_of(fav[r], frv[r], fev[r], gadd, gerr, width, k1, ip);
+                                const uint32_t k = staged + lane_rank(mk);
+                                s_rec[k] = make_uint4(w0, start + t * kTileVectors + o + r, (uint32_t)ip,
+                                                      __float_as_uint(low));
+                                s_cut[k] = cutoff;
+                                s_loc[k] = (tbase + t) * kTileVectors + o + r;
+                            }
+                            staged += (uint32_t)__popcll(mk);
+                        }
+                    }
+                }
+                if constexpr (kPrefetch)
+                    cur = nxt;
+                continue;
             }
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
