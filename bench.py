@@ -425,10 +425,11 @@ def main():
     lut = args.ip_kernel == "lut4"
     # the engine's matrix-core far scan (cross-query reuse is on; Bitwise estimator only)
     mfma_far = W in (2, 4, 6, 8, 16, 24, 32) and not lut
-    far_name = (f"far_mfma_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA ip_int/ip_res" if W <= 8 else
-                f"far_mfma_wide_kernel<{W}, false> (far-pair RaBitQ scan, int8 MFMA 16x16x64 ip_int, popcount "
+    narrow = W in (2, 6)  # P = 64, 192: the 16x16x32 kernel; the other widths the 16x16x64 one
+    far_name = (f"far_mfma_kernel<{W}, 0> (far-pair RaBitQ scan, int8 MFMA 16x16x32 ip_int/ip_res" if narrow else
+                f"far_mfma_wide_kernel<{W}, 0> (far-pair RaBitQ scan, int8 MFMA 16x16x64 ip_int, popcount "
                 "ip_res for survivors")
-    lows_name = (f"far_mfma_kernel<{W}, 2>" if W <= 8 else f"far_mfma_wide_kernel<{W}, 2>")
+    lows_name = (f"far_mfma_kernel<{W}, 2>" if narrow else f"far_mfma_wide_kernel<{W}, 2>")
     kernels = {
         "vanguard_query_kernel": {
             "kernel": f"vanguard_query_kernel<{W}, {'true' if avg_lows_ms > 0 else 'false'}> (fused per-query "
