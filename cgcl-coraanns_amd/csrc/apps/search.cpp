@@ -295,7 +295,7 @@ int main(int argc, char **argv) {
         const auto nprobes = parse_nprobes(opt.get("nprobes", ""), ivf.nlist);
         const std::size_t max_nprobe = *std::max_element(nprobes.begin(), nprobes.end());
         coraanns::validate_search_shape(chunk, topk, max_nprobe, ivf.nlist, ivf.padded_dim);
-        std::vector<uint32_t> ids;
+        coraanns::index::HugeVector<uint32_t> ids;
         const std::unique_ptr<coraanns::index::SearchData> packed_ptr =
             coraanns::index::SearchData::load(argv[1], !exact, static_cast<int>(threads), nullptr, &ids);
         const coraanns::index::SearchData &packed = *packed_ptr;

@@ -30,7 +30,7 @@ struct cora_hybrid {
 
 struct cora_ivf {
     index::IvfHeader header;
-    std::vector<uint32_t> ids;
+    index::HugeVector<uint32_t> ids;
     std::unique_ptr<index::SearchData> data;
 };
 

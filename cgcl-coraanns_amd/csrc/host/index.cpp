@@ -391,7 +391,7 @@ SearchData::SearchData(IvfFile &src, bool include_extended, int cpu_threads) {
 }
 
 std::unique_ptr<SearchData> SearchData::load(const std::string &path, bool include_extended, int cpu_threads,
-                                             IvfHeader *header, std::vector<uint32_t> *ids) {
+                                             IvfHeader *header, HugeVector<uint32_t> *ids) {
     const IvfReader rd(path);
     const IvfHeader &h = rd.header();
     const std::size_t P = h.padded_dim, W = P / 32, N = h.num, nl = h.nlist;
@@ -466,12 +466,12 @@ std::unique_ptr<SearchData> SearchData::load(const std::string &path, bool inclu
     if (include_extended && h.ex_bits > 0) {
         const std::size_t lc = h.ex_code_bytes(), stride = h.ex_stride();
         sd->host_ex_factors.assign(N * 2, 0.0f);
-        sd->extended_storage_.resize(N * lc);
+        sd->extended_huge_.resize(N * lc);
         const uint64_t per = std::max<uint64_t>(1, chunk / stride);
         std::vector<std::pair<uint64_t, uint64_t>> vplan;
         for (uint64_t v0 = 0; v0 < N; v0 += per)
             vplan.emplace_back(v0, std::min<uint64_t>(N, v0 + per));
-        uint8_t *codes = sd->extended_storage_.data();
+        uint8_t *codes = sd->extended_huge_.data();
         float *fac = sd->host_ex_factors.data();
         pipeline(
             vplan,

@@ -6,15 +6,63 @@
 // layout from these arrays.
 #pragma once
 
+#include <sys/mman.h>
+
 #include <cstddef>
 #include <cstdint>
+#include <cstdlib>
 #include <memory>
+#include <new>
 #include <string>
 #include <vector>
 
 #include "coraanns/index/ivf_file.hpp"
 
 namespace coraanns::index {
+
+// Allocator of the multi-GB host arrays that the CPU refinement reads at random (ex-codes,
+// ex-factors, ids): blocks of 4 MB and more are 2 MB aligned and marked MADV_HUGEPAGE before
+// their first touch, so that where transparent huge pages are in madvise mode the kernel
+// backs them with huge pages and a random record read rarely misses the TLB (measured on
+// the benchmark host: a config-5-sized consumer run 12.6 -> 8.8 ms). Smaller blocks come from
+// operator new. The advice is best effort: without huge pages the memory is ordinary.
+template <class T>
+class HugePageAllocator {
+  public:
+    using value_type = T;
+    static constexpr std::size_t kHuge = std::size_t{2} << 20, kMin = std::size_t{4} << 20;
+    HugePageAllocator() noexcept = default;
+    template <class U>
+    HugePageAllocator(const HugePageAllocator<U> &) noexcept {}
+    T *allocate(std::size_t n) {
+        const std::size_t bytes = n * sizeof(T);
+        if (bytes < kMin)
+            return static_cast<T *>(::operator new(bytes));
+        const std::size_t size = (bytes + kHuge - 1) / kHuge * kHuge;
+        void *p = std::aligned_alloc(kHuge, size);
+        if (!p)
+            throw std::bad_alloc();
+        (void)madvise(p, size, MADV_HUGEPAGE);
+        return static_cast<T *>(p);
+    }
+    void deallocate(T *p, std::size_t n) noexcept {
+        if (n * sizeof(T) < kMin)
+            ::operator delete(p);
+        else
+            std::free(p);
+    }
+    template <class U>
+    bool operator==(const HugePageAllocator<U> &) const noexcept {
+        return true;
+    }
+    template <class U>
+    bool operator!=(const HugePageAllocator<U> &) const noexcept {
+        return false;
+    }
+};
+
+template <class T>
+using HugeVector = std::vector<T, HugePageAllocator<T>>;
 
 class SearchData {
   public:
@@ -30,9 +78,10 @@ class SearchData {
     // the cluster-order ids.
     static std::unique_ptr<SearchData> load(const std::string &path, bool include_extended,
                                             int cpu_threads = 0, IvfHeader *header = nullptr,
-                                            std::vector<uint32_t> *ids = nullptr);
+                                            HugeVector<uint32_t> *ids = nullptr);
 
-    std::vector<float> h_centroids, host_rotator, host_short_factors, host_ex_factors;
+    std::vector<float> h_centroids, host_rotator, host_short_factors;
+    HugeVector<float> host_ex_factors;
     std::vector<uint32_t> host_short_data;
     std::vector<std::size_t> cluster_sizes;
     uint8_t *host_long_codes = nullptr;
@@ -40,7 +89,8 @@ class SearchData {
 
   private:
     SearchData() = default;
-    std::vector<uint8_t> extended_storage_;
+    std::vector<uint8_t> extended_storage_;  // the IVF's own ex-data, compacted (in-memory constructor)
+    HugeVector<uint8_t> extended_huge_;      // streamed load
 };
 
 // Sign bits of one 32-vector FastScan block, restating the unpack of
