@@ -244,8 +244,8 @@ __device__ __forceinline__ float excode_group_ip(const uint2 (&grp)[7], const fl
 
 
 // Refined distance of a candidate (cpu_refinement.cpp:183-192) from the HBM copy of the
-// ex-codes, evaluated by one lane, and a bound on its rounding difference from the CPU
-// consumer's evaluation (1e-4 of the magnitude of the terms).
+// ex-codes, evaluated by one lane, and its rounding bound against the CPU consumer's
+// evaluation (refine_err_scale).
 __device__ __forceinline__ float refine_one(const ScanParams &p, uint32_t query, uint32_t probe,
                                             uint32_t gid, float ex, float &err) {
     const uint8_t *code = p.ex_rec + (size_t)gid * p.ex_stride;
@@ -256,7 +256,7 @@ __device__ __forceinline__ float refine_one(const ScanParams &p, uint32_t query,
     const float2 f = *reinterpret_cast<const float2 *>(code + ex_record_factor_offset(p.P));
     const float fa = f.x, fr = f.y;
     const float gadd = p.pgadd[(size_t)query * p.nprobe + probe], kbq = p.kb[query];
-    err = 1e-4f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq)));
+    err = p.refine_err * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1 + fabsf(kbq)));
     return fa + gadd + fr * (128.0f * ex + ip + kbq);
 }
 

@@ -205,6 +205,7 @@ ScanParams scan_params(cora_gpu_engine *E, uint32_t depth, uint32_t keep, bool f
     p.qbytes = E->d_qbytes;
     p.lut = (E->last.flags & CORA_FLAG_LUT4) ? reinterpret_cast<const uint32_t *>(E->d_lut) : nullptr;
     p.lut_margin = E->d_lut_margin;
+    p.refine_err = refine_err_scale((uint32_t)E->P);
     p.qwidth = E->d_qwidth;
     p.qwidth2 = E->d_qwidth2;
     p.k1 = E->d_k1;

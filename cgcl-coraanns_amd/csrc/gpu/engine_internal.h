@@ -122,6 +122,18 @@ struct QueueDev {
     int final_mode;
 };
 
+// Bound on the difference between two FP32 evaluations of the refined distance
+// (cpu_refinement.cpp:183-192) in any orders of summation, per unit of the magnitude of its
+// terms |f_add| + |g_add| + |f_rescale| (128 |exact_ip| + 127 ||q'||_1 + |kb|): each evaluation
+// lies within gamma_n = n u / (1 - n u) (u = 2^-24) of the exact value times that magnitude,
+// n = P + 8 the longest chain of roundings a term passes (the P multiplications and
+// additions of the ex-code dot product, fused or not, and the outer formula's five), so two
+// differ by at most 2 gamma_n of it; 2.002 also covers the rounding of the magnitude.
+// (P = 128: 1.62e-5, P = 768: 9.26e-5, P = 1024: 1.23e-4.)
+__host__ __device__ constexpr float refine_err_scale(uint32_t P) {
+    return (float)(2.002 * (P + 8.0) * 0x1p-24 / (1.0 - (P + 8.0) * 0x1p-24));
+}
+
 struct ScanParams {
     const uint8_t *tiles;
     const ClusterMeta *meta;
@@ -134,6 +146,7 @@ struct ScanParams {
     // estimate| over all codes (launch_lut_margin), by which their Bitwise lower bounds are
     // lowered (lut_slack) before the LUT4 bound of the survivors is evaluated exactly
     const float *lut_margin;
+    float refine_err;  // refine_err_scale(P): the refined distance's rounding bound per unit of magnitude
     const float *qwidth;      // [nq] Bq=8 step
     const float *qwidth2;     // [nq] residual step (qwidth / 254)
     const float *k1;          // [nq]

@@ -599,7 +599,7 @@ __global__ __launch_bounds__(64) void seed_kernel(const ScanParams p) {
                     const size_t o = ((size_t)query * p.vanguard + probe) * keep + sidx;
                     p.seed_dist[o] = dist;
                     p.seed_low[o] = key_to_float((uint32_t)(key >> 32));
-                    p.seed_err[o] = 1e-4f * mag;
+                    p.seed_err[o] = p.refine_err * mag;
                 }
             }
         }

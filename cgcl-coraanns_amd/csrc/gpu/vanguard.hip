@@ -218,6 +218,58 @@ __device__ void publish_held(VqShared &S, const QueueDev &q) {
     __syncthreads();
 }
 
+// Make room among the held refined vectors without publishing: those whose distance is
+// beyond their rounding bound of the current threshold can never be published (the
+// threshold only falls), so they are counted as dropped and the others are compacted in
+// order. Publication then happens with the final threshold, as in the staged pass, instead
+// of with the threshold of the moment the buffer filled (config 5, top-100: 146 -> ~103
+// records a query to the CPU). kVqHeld = kVqThreads: one held vector per thread.
+__device__ void compact_held(VqShared &S) {
+    static_assert(kVqHeld == kVqThreads, "one held vector per thread");
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float thr = S.thr;
+    const uint32_t nheld = S.nheld;
+    bool keep = false, drop = false;
+    uint32_t w0 = 0, gid = 0;
+    float ex = 0.0f, low = 0.0f, rd = 0.0f, err = 0.0f;
+    if (tid < nheld) {
+        w0 = S.h_word0[tid];
+        gid = S.h_gid[tid];
+        ex = S.h_ex[tid];
+        low = S.h_low[tid];
+        rd = S.h_rd[tid];
+        err = S.h_err[tid];
+        keep = rd <= thr + err;
+        drop = !keep && !isnan(rd);
+    }
+    const unsigned long long m = __ballot(keep), dm = __ballot(drop);
+    if (lane == 0) {
+        S.red[wave] = (uint32_t)__popcll(m);
+        if (dm)
+            atomicAdd(&S.ndropped, (uint32_t)__popcll(dm));
+    }
+    __syncthreads();  // every held vector is in registers before any is overwritten
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < (uint32_t)kVqWaves; ++w) {
+        before += w < wave ? S.red[w] : 0u;
+        total += S.red[w];
+    }
+    if (keep) {
+        const uint32_t k = before + lane_rank(m);
+        S.h_word0[k] = w0;
+        S.h_gid[k] = gid;
+        S.h_ex[k] = ex;
+        S.h_low[k] = low;
+        S.h_rd[k] = rd;
+        S.h_err[k] = err;
+    }
+    __syncthreads();  // S.red is read above before anyone reuses it
+    if (tid == 0)
+        S.nheld = total;
+    __syncthreads();
+}
+
 // The query's Bq=8 planes [kBq][W] in the constant address space: wave-uniform reads
 // become scalar loads whose words feed the AND as scalar operands.
 typedef __attribute__((address_space(4))) const uint32_t *ConstWords;
@@ -383,6 +435,8 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
             for (uint32_t c0 = 0; c0 < nwin; c0 += kVqChunk) {
                 const float thr = S.thr;
                 if (S.nheld + kVqChunk > kVqHeld)
+                    compact_held(S);
+                if (S.nheld + kVqChunk > kVqHeld)
                     publish_held(S, q);
                 const uint32_t cn = min(kVqChunk, nwin - c0);
                 const uint32_t held0 = S.nheld;
@@ -399,7 +453,7 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                     const float ex = two_stage_ip(width, ipa, width2, ipb);
                     const float gadd = S.gadd[j];
                     const float rd = fa + gadd + fr * (128.0f * ex + ipx + kbq);
-                    const float err = 1e-4f * (fabsf(fa) + fabsf(gadd) +
+                    const float err = p.refine_err * (fabsf(fa) + fabsf(gadd) +
                                                fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
                     S.c_key[e] = ((unsigned long long)order_key(rd) << 32) | pos;
                     S.c_err[e] = err;

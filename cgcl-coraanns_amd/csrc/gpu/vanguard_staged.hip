@@ -642,7 +642,7 @@ __global__ __launch_bounds__(kVsThreads) __attribute__((amdgpu_waves_per_eu(W >=
                     low = sfa + gadd + sfr * (ex + k1) - sfe * s_gerr[j];
                 const float rd = fa + gadd + fr * (128.0f * ex + ipx + kbq);
                 const float err =
-                    1e-4f * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
+                    refine_err_scale(P) * (fabsf(fa) + fabsf(gadd) + fabsf(fr) * (128.0f * fabsf(ex) + 127.0f * l1q + fabsf(kbq)));
                 rd_r[e] = make_float2(rd, err);
                 aux_r[e] = make_float2(ex, low);
             }

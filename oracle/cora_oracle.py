@@ -654,16 +654,31 @@ def vanguard_seeds(low: np.ndarray, keep: int, cutoff) -> np.ndarray:
     return valid[np.argsort(np.asarray(low)[valid], kind="stable")][:keep]
 
 
-def refine_error_bound(f_ex_add, f_ex_rescale, g_add, exact_ip, q_l1, kb, ex_bits):
+def refine_error_scale(padded_dim: int) -> float:
+    """Per unit of magnitude, the bound on the difference between two FP32 evaluations of
+    refine_dist (cpu_refinement.cpp:183-192) in any summation orders: each lies within
+    gamma_n = n u / (1 - n u), u = 2^-24, of the exact value times the magnitude of its terms,
+    n = P + 8 the longest chain of roundings a term passes (the P products and sums of the
+    ex-code dot product, fused or not, and the outer formula's five); two differ by at most
+    2 gamma_n, and 2.002 covers the FP32 rounding of the magnitude. The engine's kernels use
+    the same constant (refine_err_scale, engine_internal.h)."""
+    n = float(padded_dim) + 8.0
+    u = 2.0 ** -24
+    return float(np.float32(2.002 * n * u / (1.0 - n * u)))
+
+
+def refine_error_bound(f_ex_add, f_ex_rescale, g_add, exact_ip, q_l1, kb, ex_bits, padded_dim):
     """Bound on the rounding difference between two FP32 evaluations of refine_dist in
-    different summation orders (GPU seed refinement vs the CPU consumer): 1e-4 times the
-    magnitude of its terms, |f_add| + |g_add| + |f_rescale| (2^ex |ip| + (2^ex - 1) ||q'||_1
-    + |kb|). The ex-code inner product is at most (2^ex - 1) ||q'||_1."""
+    different summation orders (GPU refinement vs the CPU consumer): refine_error_scale(P)
+    times the magnitude of its terms, |f_add| + |g_add| + |f_rescale| (2^ex |ip| +
+    (2^ex - 1) ||q'||_1 + |kb|). The ex-code inner product is at most (2^ex - 1) ||q'||_1.
+    Pinned by test_refine_error_bound_covers_f32_evaluation (sequential FP32 order against
+    FP64, and two FP32 orders against each other, at half and the full bound)."""
     s = float(1 << ex_bits)
     mag = np.abs(np.asarray(f_ex_add, np.float64)) + abs(float(g_add)) + np.abs(
         np.asarray(f_ex_rescale, np.float64)) * (s * np.abs(np.asarray(exact_ip, np.float64)) +
                                                  (s - 1) * float(q_l1) + abs(float(kb)))
-    return (1e-4 * mag).astype(np.float32)
+    return (refine_error_scale(padded_dim) * mag).astype(np.float32)
 
 
 def seed_threshold(dists, lows, errs, topk: int):
@@ -801,7 +816,9 @@ PINNED = {
     "refine_dist": "golden: reproduces reference est_exdist from est_ipx0 (split_distance_boosting), 1e-5",
     "hybrid_search": "composition of the pinned functions; top-k ids vs brute force on all-probe search",
     "vanguard_seeds": "brute force: equals the first min(keep, #valid) of a full stable sort of valid lows",
-    "refine_error_bound": "property: bounds |f32 refine - f64 refine| of refine_dist on golden ex-codes",
+    "refine_error_bound": "property: two FP32 orders of refine_dist on golden ex-codes each within half of it "
+                          "of FP64, and the all-positive worst case of sequential summation at P = 1,024",
+    "refine_error_scale": "closed form 2.002 gamma_{P+8}; covered by the refine_error_bound property test",
     "seed_threshold": "properties: >= topk seeds strictly below it with lows below it; >= true topk-th",
     "excode_residual_abs": "golden: quantize_excode reproduces the reference builder's ex-codes (quant_d128)",
     "best_rescale_factor": "golden: quantize_excode reproduces the reference builder's ex-codes (quant_d128); "

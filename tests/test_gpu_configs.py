@@ -252,7 +252,7 @@ class LazyProbed:
             fa, fr = exf[:, 0], exf[:, 1]
             rd = orc.refine_dist(fa, fr, g["gadd"][q, p], ex2, orc.excode_ip(g["qr"][q], lc, P), g["kb"][q],
                                  self.lz.ex_bits)
-            err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], self.lz.ex_bits)
+            err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], self.lz.ex_bits, P)
             out.append((p, ids, low.astype(np.float64), rd.astype(np.float64), err.astype(np.float64)))
         return out
 

@@ -810,7 +810,7 @@ def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
             ipx = orc.excode_ip(g["qr"][q], sd.long_codes[gids], P)
             fa, fr = sd.ex_factors[gids, 0], sd.ex_factors[gids, 1]
             rd = orc.refine_dist(fa, fr, g["gadd"][q, p], ex2, ipx, g["kb"][q], 7)
-            err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], 7)
+            err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], 7, P)
             got = sdist[q, p][np.isfinite(sdist[q, p])]
             assert got.size == seeds.size, (q, p)
             assert np.all(np.abs(np.sort(got) - np.sort(rd)) <= np.sort(err)[::-1][0]), (q, p)
@@ -845,7 +845,7 @@ def test_gpu_seed_thresholds_frozen_parity(synth, prefilter):
             fa, fr = sd.ex_factors[gall, 0], sd.ex_factors[gall, 1]
             rda = orc.refine_dist(fa, fr, g["gadd"][q, p], exa,
                                   orc.excode_ip(g["qr"][q], sd.long_codes[gall], P), g["kb"][q], 7)
-            erra = orc.refine_error_bound(fa, fr, g["gadd"][q, p], exa, l1, g["kb"][q], 7)
+            erra = orc.refine_error_bound(fa, fr, g["gadd"][q, p], exa, l1, g["kb"][q], 7, P)
             if idx is not None:
                 # seeds refined on the GPU are published when within their bound of the threshold
                 lo_cnt += int((rda[idx] <= thr[q] + 0.9 * erra[idx]).sum())
@@ -896,7 +896,7 @@ def probed_vectors(case, g, q, nprobe):
         fa, fr = sd.ex_factors[gid, 0], sd.ex_factors[gid, 1]
         rd = orc.refine_dist(fa, fr, g["gadd"][q, p], ex2, orc.excode_ip(g["qr"][q], sd.long_codes[gid], P),
                              g["kb"][q], 7)
-        err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], 7)
+        err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex2, l1, g["kb"][q], 7, P)
         out.append((p, gid, low.astype(np.float64), rd.astype(np.float64), err.astype(np.float64)))
     return out
 
@@ -1345,7 +1345,7 @@ def probed_vectors_lut(case, g, q, nprobe, lut):
         fa, fr = sd.ex_factors[gid, 0], sd.ex_factors[gid, 1]
         rd = orc.refine_dist(fa, fr, g["gadd"][q, p], ex, orc.excode_ip(g["qr"][q], sd.long_codes[gid], P),
                              g["kb"][q], 7)
-        err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex, l1, g["kb"][q], 7)
+        err = orc.refine_error_bound(fa, fr, g["gadd"][q, p], ex, l1, g["kb"][q], 7, P)
         out.append((p, gid, low.astype(np.float64), rd.astype(np.float64), err.astype(np.float64)))
     return out
 

@@ -285,6 +285,11 @@ def test_vanguard_seed_selection_brute_force():
 
 
 def test_refine_error_bound_covers_f32_evaluation(fx):
+    """The refined distance's rounding bound (refine_error_scale(P) times the magnitude of
+    its terms) against FP32 evaluations in two different orders: each lies within half the
+    bound of the FP64 value (the gamma_{P+8} half of the derivation), so the two differ by
+    less than the bound; the same with adversarial terms (all of one sign, the worst case of
+    sequential summation) at P = 1,024."""
     name, ref, ivf, sd, q = fx
     P = ivf.padded_dim
     qr = orc.rotate(q, sd.rotator)
@@ -292,19 +297,39 @@ def test_refine_error_bound_covers_f32_evaluation(fx):
     rng = np.random.default_rng(22)
     for i in range(min(8, q.shape[0])):
         gids = rng.integers(0, ivf.num, 64)
-        ip_ex = orc.excode_ip(qr[i], sd.long_codes[gids], P)
         ex = rng.normal(0, 1, 64).astype(np.float32)
         g = np.float32(abs(rng.normal(0, 5)))
         fa, fr = sd.ex_factors[gids, 0], sd.ex_factors[gids, 1]
-        d64 = fa.astype(np.float64) + g + fr.astype(np.float64) * (128.0 * ex + ip_ex.astype(np.float64) + kb[i])
-        # a deliberately different f32 order: sequential accumulation of the ex-code dot
         codes = orc.unpack_excode7(sd.long_codes[gids], P).astype(np.float32)
-        dot32 = np.zeros(64, np.float32)
+        ip64 = codes.astype(np.float64) @ qr[i].astype(np.float64)
+        d64 = fa.astype(np.float64) + g + fr.astype(np.float64) * (128.0 * ex + ip64 + kb[i])
+        # order 1: sequential accumulation of the ex-code dot; order 2: eight-wide chunks
+        dot_seq = np.zeros(64, np.float32)
         for d in range(P):
-            dot32 = (dot32 + codes[:, d] * qr[i, d]).astype(np.float32)
-        d32 = (fa + g + fr * ((np.float32(128) * ex + dot32).astype(np.float32) + kb[i])).astype(np.float32)
-        bound = orc.refine_error_bound(fa, fr, g, ex, np.abs(qr[i]).sum(), kb[i], 7)
-        assert np.all(np.abs(d32 - d64) <= bound), name
+            dot_seq = (dot_seq + codes[:, d] * qr[i, d]).astype(np.float32)
+        dot_chunk = np.zeros(64, np.float32)
+        for c in range(P // 8):
+            part = np.zeros(64, np.float32)
+            for d in range(8 * c, 8 * c + 8):
+                part = (part + codes[:, d] * qr[i, d]).astype(np.float32)
+            dot_chunk = (dot_chunk + part).astype(np.float32)
+        outs = [(fa + g + fr * ((np.float32(128) * ex + dot).astype(np.float32) + kb[i])).astype(np.float32)
+                for dot in (dot_seq, dot_chunk)]
+        bound = orc.refine_error_bound(fa, fr, g, ex, np.abs(qr[i]).sum(), kb[i], 7, P).astype(np.float64)
+        for d32 in outs:
+            assert np.all(np.abs(d32 - d64) <= 0.5 * bound), name
+        assert np.all(np.abs(outs[0].astype(np.float64) - outs[1]) <= bound), name
+    # worst case of sequential summation: 1,024 positive terms of one size
+    P = 1024
+    qv = np.full(P, np.float32(0.7), np.float32)
+    code = np.full(P, np.float32(127), np.float32)
+    acc = np.float32(0)
+    for d in range(P):
+        acc = np.float32(acc + code[d] * qv[d])
+    exact = 127.0 * 0.699999988079071 * P
+    b = orc.refine_error_bound(np.float32(0), np.float32(1), np.float32(0), np.float32(0), float(qv.sum()), 0.0, 7, P)
+    assert abs(float(acc) - exact) <= 0.5 * float(b)
+    assert orc.refine_error_scale(128) < 2e-5 and orc.refine_error_scale(768) < 1e-4
 
 
 def test_seed_threshold_properties():
