@@ -168,8 +168,11 @@ __device__ __forceinline__ void append_window(VqShared &S, uint32_t i, bool take
 
 // Publish the held refined vectors whose distance is within their rounding bound of the
 // current threshold (one ring reservation per round of 256), count the others as dropped
-// (S.ndropped).
-__device__ void publish_held(VqShared &S, const QueueDev &q) {
+// (S.ndropped). last: the query's final publication, after which the workgroup only ends,
+// so no barrier follows the last round's stores (a barrier waits for their write-through
+// to host memory), and the dropped ones are counted straight into last_dropped.
+__device__ void publish_held(VqShared &S, const QueueDev &q, bool last = false,
+                             unsigned long long *last_dropped = nullptr) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float thr = S.thr;
     const uint32_t nheld = S.nheld;
@@ -184,8 +187,12 @@ __device__ void publish_held(VqShared &S, const QueueDev &q) {
         const unsigned long long m = __ballot(pub), dm = __ballot(drop);
         if (lane == 0) {
             S.red[wave] = (uint32_t)__popcll(m);
-            if (dm)
-                atomicAdd(&S.ndropped, (uint32_t)__popcll(dm));
+            if (dm) {
+                if (last)
+                    atomicAdd(last_dropped, (unsigned long long)__popcll(dm));
+                else
+                    atomicAdd(&S.ndropped, (uint32_t)__popcll(dm));
+            }
         }
         __syncthreads();
         uint32_t before = 0, total = 0;
@@ -211,8 +218,12 @@ __device__ void publish_held(VqShared &S, const QueueDev &q) {
                                         __float_as_uint(q.final_mode ? S.h_rd[i] : S.h_ex[i]),
                                         __float_as_uint(S.h_low[i])));
         }
+        if (last && r0 + kVqThreads >= nheld)
+            return;
         __syncthreads();  // S.red / S.base reused by the next round
     }
+    if (last)
+        return;
     if (tid == 0)
         S.nheld = 0;
     __syncthreads();
@@ -379,6 +390,7 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
     __syncthreads();
     const uint32_t T = S.toff[V];
     const float thr_in = S.thr;
+    bool early_pub = false;  // held records went out before the final threshold
     // sum |q'| for the rounding bound (the same for every vector of the query)
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1)
@@ -436,8 +448,10 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
                 const float thr = S.thr;
                 if (S.nheld + kVqChunk > kVqHeld)
                     compact_held(S);
-                if (S.nheld + kVqChunk > kVqHeld)
+                if (S.nheld + kVqChunk > kVqHeld) {
                     publish_held(S, q);
+                    early_pub = true;
+                }
                 const uint32_t cn = min(kVqChunk, nwin - c0);
                 const uint32_t held0 = S.nheld;
                 // the refined distance of chunk vector e (lane sub == 0 of its group) into the
@@ -925,8 +939,7 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
         }
     }
 
-    // ---- 3. publication and the query's threshold ----
-    publish_held(S, q);
+    // ---- 3. the query's threshold and publication ----
     if (tid == 0) {
         if (S.ndropped)
             atomicAdd(p.dropped, (unsigned long long)S.ndropped);
@@ -935,16 +948,24 @@ __global__ __launch_bounds__(kVqThreads, kPre && W >= 16 ? 2 : (W > 0 && W <= 4)
         const float thr = S.thr;
         if (S.kc == topk && thr < thr_in) {
             uint32_t *slot = reinterpret_cast<uint32_t *>(va.thr_out) + qi;
-            uint32_t cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            while (thr < __uint_as_float(cur)) {
-                if (__hip_atomic_compare_exchange_strong(slot, &cur, __float_as_uint(thr),
-                                                         __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_SYSTEM))
-                    break;
+            if (!early_pub) {
+                // none of the query's records has been published in this search yet (the far
+                // pass runs after this kernel), so no consumer has changed its threshold since
+                // the snapshot thr_in: a store lowers it without a host round trip
+                __hip_atomic_store(slot, __float_as_uint(thr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            } else {
+                uint32_t cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                while (thr < __uint_as_float(cur)) {
+                    if (__hip_atomic_compare_exchange_strong(slot, &cur, __float_as_uint(thr),
+                                                             __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_SYSTEM))
+                        break;
+                }
             }
             atomicAdd(va.seeded, 1ull);
         }
     }
+    publish_held(S, q, true, p.dropped);
 }
 
 template <int W>
