@@ -215,11 +215,11 @@ def main():
     ap.add_argument("--no-vanguard-mfma", action="store_true",
                     help="vanguard lower bounds inside the per-query pass instead of the matrix-core lows pass")
     ap.add_argument("--vanguard-one-pass", action="store_true",
-                    help="after the lows pass, run the vanguard pairs in the one per-query kernel (the default up "
-                         "to top-32 with the Bitwise estimator)")
+                    help="after the lows pass, run the vanguard pairs in the one per-query kernel (the default "
+                         "with the Bitwise estimator up to top-128)")
     ap.add_argument("--vanguard-staged", action="store_true",
                     help="after the lows pass, run the staged vanguard pass (per-query select and merge around "
-                         "grid-wide refinement; the default above top-32 and with LUT4)")
+                         "grid-wide refinement; the default with LUT4 and above top-128)")
     ap.add_argument("--vanguard-mfma", action="store_true",
                     help="run the matrix-core vanguard lows pass whatever the index size and dimension")
     ap.add_argument("--ip-kernel", choices=["bitwise", "lut4"], default="bitwise",

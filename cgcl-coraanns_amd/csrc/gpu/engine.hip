@@ -1071,10 +1071,12 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     const bool high_k = a->topk > kVanguardMaxTopk;
     // its lower bounds first on the matrix cores, cluster-major, into the per-pair lows
     // array [nq][depth][van_stride] of the workspace
-    // (by default only for wide codes whose sign codes and factors exceed the last-level
-    // cache: a cache-resident index, or 28 bytes a vector at P = 128, is read cheaply enough
-    // by each query's own pass)
-    const bool lows_by_size = (uint64_t)E->N * (E->P / 8 + 12) > kLowsMinIndexBytes && E->P >= kLowsMinDim;
+    // (by default for wide codes whose sign codes and factors exceed the last-level cache, and
+    // for any index beyond 1 GiB: a nearly cache-resident index is read cheaply enough by each
+    // query's own pass)
+    const uint64_t index_bytes = (uint64_t)E->N * (E->P / 8 + 12);
+    const bool lows_by_size =
+        (index_bytes > kLowsMinIndexBytes && E->P >= kLowsMinDim) || index_bytes > kLowsAnyDimBytes;
     const bool van_lows = fused && depth > 0 && far_mfma_supported(E->W) && E->d_van_lows &&
                           !(a->flags & CORA_FLAG_NO_VANGUARD_MFMA) &&
                           (lows_by_size || (a->flags & CORA_FLAG_VANGUARD_MFMA) || lut || high_k);
@@ -1120,12 +1122,14 @@ int cora_gpu_launch_search(cora_gpu_engine *E, const cora_search_args *a) {
     p.prefilter = prefilter ? 1 : 0;
     p.dropped = E->d_stats + 7;
     VanguardArgs va{};
-    // the staged pass (grid-wide refinement) where the lows pass wrote every vanguard bound
-    // (measured at config 4: top-10 1.56M QPS one-pass against 1.51M staged, top-100 512k
-    // against 593k)
+    // the staged pass (grid-wide refinement) where the lows pass wrote every vanguard bound:
+    // for LUT4 and above the one-pass kernel's top-k, or when asked for. The one-pass kernel
+    // publishes each query as it ends, so the CPU consumer starts early (measured, config 4:
+    // top-10 1.53-1.60M QPS one-pass against 1.50M staged, top-100 988k against 713k, 1.08M
+    // both with GPU-final top-k; config 5: 1.33M against 1.16M)
     const bool staged = van_lows && E->d_vs_seed_pos &&
-                        (lut || high_k || (a->flags & CORA_FLAG_VANGUARD_STAGED) ||
-                         (a->topk > CORA_VANGUARD_STAGED_TOPK && !(a->flags & CORA_FLAG_VANGUARD_ONE_PASS)));
+                        (lut || high_k ||
+                         ((a->flags & CORA_FLAG_VANGUARD_STAGED) && !(a->flags & CORA_FLAG_VANGUARD_ONE_PASS)));
     p.van_mins = staged ? E->d_van_mins : nullptr;
     E->last_fused = fused && depth > 0;
     E->last_van_lows = van_lows;

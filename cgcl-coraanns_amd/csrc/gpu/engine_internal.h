@@ -27,12 +27,15 @@ constexpr uint32_t kVanguardMaxPairs = 64;  // fused vanguard pass: vanguard dep
 constexpr uint32_t kVanguardMaxTopk = 128;  // one-pass vanguard kernel: top-k limit
 constexpr uint32_t kVanguardStagedMaxTopk = 1024;  // staged vanguard pass: top-k limit
 // the vanguard lows pass runs by default for sign codes + factors beyond MI355X's 256 MB
-// last-level cache and at least this padded dimension: a query's own pass reads P/8 + 12
-// bytes per vanguard vector against the lows pass's 4, a saving that pays for the extra
-// pass at P = 768 (config 4: 0.98M -> 1.43M QPS) but not at P = 128 (config 3, 280 MB:
-// 4.05M without it, 3.28M with it; config 5, 2.8 GB: 1.01M against 0.94M)
+// last-level cache at a padded dimension of at least kLowsMinDim, and at any dimension beyond
+// kLowsAnyDimBytes: a query's own pass reads P/8 + 12 bytes per vanguard vector against the
+// lows pass's 4, a saving that pays for the extra pass at P = 768 (config 4: 0.98M -> 1.43M
+// QPS) and for a 2.8 GB index at P = 128 (config 5: 1.27M -> 1.33M), not for a nearly
+// cache-resident one (config 3, 280 MB: 4.45-4.50M without it, 3.81-3.96M with it; config 2,
+// 28 MB: 4.39M against 4.27M)
 constexpr uint64_t kLowsMinIndexBytes = 256ull << 20;
 constexpr uint32_t kLowsMinDim = 512;
+constexpr uint64_t kLowsAnyDimBytes = 1ull << 30;
 
 // Refinement record of one vector (cluster order), ex_record_bytes(P) = P + 16 bytes, so a
 // refined vector is one contiguous read: the packed 7-bit ex-code (P*7/8 bytes, 64-dimension

@@ -79,7 +79,8 @@ enum cora_search_flags {
     CORA_FLAG_FP32_GEMM = 1u << 8,
     /* Fused vanguard pass: where its lower bounds come from (same candidates either way).
      * By default, when the index's sign codes and factors exceed the last-level cache
-     * (256 MB) and the padded dimension is at least 512, they are evaluated first on the
+     * (256 MB) and the padded dimension is at least 512, or exceed 1 GiB at any padded
+     * dimension, they are evaluated first on the
      * matrix cores, cluster-major, in units of up to 16 same-cluster pairs (each cluster read
      * once per unit), and the per-query pass streams them; for a cache-resident index, or
      * narrow codes (P/8 + 12 bytes a vector against 4 bytes of bound), each query evaluating
@@ -116,15 +117,15 @@ enum cora_search_flags {
      * query selects, refines and publishes in turn), or the staged pass, whose refinement of
      * every query's candidates runs grid-wide between per-query select and merge stages, with
      * the same rules for what is refined, published and the threshold. By default the staged
-     * pass runs for top-k above CORA_VANGUARD_STAGED_TOPK and with the LUT4 estimator (which
-     * only it supports), the one-pass kernel otherwise; these flags choose one. Top-k above
+     * pass runs with the LUT4 estimator (which only it supports), the one-pass kernel
+     * otherwise, whose queries' records reach the CPU consumer as each query ends; these
+     * flags choose one (ONE_PASS wins when both are given). Top-k above
      * 128 (up to CORA_VANGUARD_STAGED_MAX_TOPK) is served by the staged pass alone, when the
      * workspace was prepared for it (its per-query regions then hold every vanguard vector)
      * and the matrix-core lows pass applies; otherwise the per-pair passes run. */
     CORA_FLAG_VANGUARD_ONE_PASS = 1u << 14,
     CORA_FLAG_VANGUARD_STAGED = 1u << 15
 };
-#define CORA_VANGUARD_STAGED_TOPK 32
 #define CORA_VANGUARD_STAGED_MAX_TOPK 1024
 
 typedef struct cora_gpu_engine cora_gpu_engine;

@@ -741,7 +741,8 @@ def test_vanguard_mode_reported(synth):
     eng = make_engine(synth, nprobe, 129, vanguard=5, frozen=False, secondary=True)
     for topk, flags, mode in [(10, 0, 2), (10, ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_ONE_PASS, 3),
                               (10, ca.FLAG_VANGUARD_MFMA, 3), (10, ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_STAGED, 4),
-                              (100, ca.FLAG_VANGUARD_MFMA, 4), (129, 0, 4), (129, ca.FLAG_NO_VANGUARD_MFMA, 1),
+                              (100, ca.FLAG_VANGUARD_MFMA, 3), (100, ca.FLAG_VANGUARD_MFMA | ca.FLAG_VANGUARD_STAGED, 4),
+                              (129, 0, 4), (129, ca.FLAG_NO_VANGUARD_MFMA, 1),
                               (10, ca.FLAG_PAIR_SEEDS, 1)]:
         eng.configure(vanguard_size=5, cpu_secondary_filter=True, metric=synth.file.metric, gpu_filter_timing=True,
                       extra_flags=flags, lower_bound_scale=1.0)
