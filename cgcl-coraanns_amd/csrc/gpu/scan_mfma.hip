@@ -493,7 +493,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
     constexpr int WQ = W / 4;  // code words per lane-group
     constexpr int S = W / 2;   // K-steps of 64 dimensions
     constexpr uint32_t P = 32u * W;
-    constexpr bool kPrefetch = W == 4;
+    constexpr bool kPrefetch = W == 4 || (kMode == kLows && W <= 24);
     // publication test without per-element validity or pair-slot terms: the cutoff of an
     // empty pair slot is -inf and the rows past the cluster's end are masked per tile in
     // SGPRs, so each (vector, pair) costs its bound and one compare
@@ -567,7 +567,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
         // memory round trip per tile; at P >= 512 two waves per SIMD hold them in 251 VGPRs
         // without spilling, measured 22% faster than three waves loading per row block); then
         // one row block of 16 vectors at a time: its K-steps and its lower bounds. For
-        // P = 128 (W = 4, 52 VGPRs a tile) the next tile's loads are issued before the
+        // P = 128 (W = 4, 52 VGPRs a tile), and in the lows pass up to P = 768 (whose bounds
+        // need no survivor staging: 250 VGPRs at P = 768, 0.78 -> 0.73 ms at config 4), the
+        // next tile's loads are issued before the
         // current tile's MFMAs, so each wave keeps a tile's loads in flight while it computes.
         TileRegs<WQ> cur, nxt;
         if constexpr (kPrefetch)
