@@ -202,7 +202,7 @@ def test_ring_protocol_zero_candidates():
     assert np.all(d == np.finfo(np.float32).max) and np.all(i == 0)
 
 
-CPP_TESTS = ["release_tracker_test.cpp", "parameters_test.cpp", "recall_evaluator_test.cpp"]
+CPP_TESTS = ["release_tracker_test.cpp", "parameters_test.cpp", "recall_evaluator_test.cpp", "huge_pages_test.cpp"]
 
 
 @pytest.mark.parametrize("src", CPP_TESTS)
