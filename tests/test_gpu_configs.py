@@ -37,8 +37,8 @@ F32_MAX = np.finfo(np.float32).max
 
 
 def say(msg):
-    """Progress on stdout and, on the GPU box, in a file under gpurun_out/ (index builds of
-    the large configurations run for minutes)."""
+    """Progress on stdout and, where the run's output directory exists, in a progress file
+    there (index builds of the large configurations run for minutes)."""
     print(msg, flush=True)
     sys.stdout.flush()
     root = os.environ.get("GRAFT_REPO_ROOT")
