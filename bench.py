@@ -349,6 +349,7 @@ def main():
     select_ms = []
     recalls_k = []
     van_ms, van_bytes, lows_ms, lows_bytes, ref_ms, ref_bytes, van_modes = [], [], [], [], [], [], []
+    refined, pair_vectors = [], []
     cands = []
     staged_counts = []
     last_ids = None
@@ -369,6 +370,11 @@ def main():
         ref_ms.append(st["vanguard_refine_ms"])
         ref_bytes.append(st["vanguard_refine_bytes"])
         van_modes.append(st["vanguard_mode"])
+        refined.append(st["gpu_refined"])
+        if st["vanguard_lows_ms"] > 0:
+            # with the lows pass the per-query pass's bytes are 4 per vanguard (query, vector)
+            # bound plus P + 8 per refined vector: the (query, vector) count of the vanguard pairs
+            pair_vectors.append((st["vanguard_bytes"] - st["gpu_refined"] * (c.padded_dim + 8)) / 4)
         cands.append(st["submitted"])
         if st["vanguard_mode"] == 4 and not staged_counts:
             staged_counts.extend(int(x) for x in eng.debug_read(ca.DBG_STAGED_COUNTS, (4,), np.uint64))
@@ -411,7 +417,7 @@ def main():
                       "fp32_equivalent_tflops": round(probe_tflops, 3)}
     probe_line["select_and_gadd_ms"] = round(float(np.mean(select_ms)), 4)
     log(f"[timed] nprobe={nprobe} steps={args.steps} QPS={qps:.1f} recall={np.mean(recalls):.4f} "
-        f"cand/q={np.mean(cands) / queries.shape[0]:.1f} "
+        f"cand/q={np.mean(cands) / queries.shape[0]:.1f} refined/q={np.mean(refined) / queries.shape[0]:.1f} "
         f"vanguard lows={avg_lows_ms:.3f}ms {lows_bpl / 1e6:.1f}MB -> {lows_achieved:.1f} GB/s; "
         f"vanguard={avg_van_ms:.3f}ms {van_bpl / 1e6:.1f}MB -> {van_achieved:.1f} GB/s "
         f"(mode {van_modes[-1] if van_modes else 0}; refinement {avg_ref_ms:.3f}ms {ref_bpl / 1e6:.1f}MB -> "
@@ -443,7 +449,12 @@ def main():
         "vanguard_lows": {
             "kernel": f"{lows_name} (vanguard lower bounds on the matrix cores, cluster-major, units of 16 "
                       "same-cluster pairs)",
-            "avg_launch_ms": round(avg_lows_ms, 4), "bytes_per_launch": int(lows_bpl), "achieved": lows_achieved},
+            "avg_launch_ms": round(avg_lows_ms, 4), "bytes_per_launch": int(lows_bpl), "achieved": lows_achieved,
+            # of which written: a 4-byte bound per vanguard (query, vector), and for the staged
+            # pass the minimum of each 4 of them
+            "pair_vectors": int(np.mean(pair_vectors)) if pair_vectors else 0,
+            "bytes_written": int((5 if van_modes and van_modes[-1] == 4 else 4) * np.mean(pair_vectors))
+            if pair_vectors else 0},
         "far_mfma_kernel" if mfma_far else "scan_kernel": {
             "kernel": f"{far_name}, units of 16 same-cluster pairs)" if mfma_far else
                       f"scan_kernel<0, {4 if batch_q > 1 else 1}, 0, 1> (far-pair LUT4 scan, FP16 nibble tables in LDS)"

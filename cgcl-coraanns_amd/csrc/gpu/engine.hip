@@ -1286,10 +1286,11 @@ int cora_gpu_sync(cora_gpu_engine *E, cora_search_stats *st) {
     out.gpu_refined = stats[8];
     // the per-query pass: code + factors of every vanguard vector (or its 4-byte lower bound
     // when the lows pass ran), then P/8 + 7P/8 + 8 per refined one; the lows pass: code +
-    // factors of the cluster once per unit
+    // factors of the cluster once per unit read, a 4-byte bound per (vector, vanguard pair)
+    // written, and for the staged pass the minimum of each 4 of them
     if (E->last_fused && E->last_van_lows) {
         out.vanguard_bytes = 4 * stats[10] + stats[8] * (E->P + 8);
-        out.vanguard_lows_bytes = stats[9];
+        out.vanguard_lows_bytes = stats[9] + stats[10] * (E->last_staged ? 5 : 4);
         // staged pass: the refinement launches read each refined vector's record and its pool
         // position and lower bound, and write its result (the one-pass kernel's overflow
         // queries, refined inside that kernel, are counted here too)

@@ -186,7 +186,9 @@ typedef struct cora_search_stats {
                                 ex-factor bytes of every vector it refined */
     float vanguard_lows_ms;  /* the matrix-core vanguard lows pass alone (0 when it did not run) */
     uint64_t vanguard_lows_bytes; /* its algorithmic bytes: code + factor bytes of every vector
-                                     of the cluster, once per unit of up to 16 pairs */
+                                     of the cluster read once per unit of up to 16 pairs, and a
+                                     4-byte bound per (vector, vanguard pair) written (5 bytes
+                                     with the staged pass's group minima) */
     /* how the vanguard pairs ran: 0 none, 1 the per-pair seed and recovery passes (asked
      * for, no ex-codes in HBM, or beyond the fused pass's limits of 64 vanguard pairs and
      * top-128), 2 the fused per-query pass, 3 the fused pass after the matrix-core lows pass,

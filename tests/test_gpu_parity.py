@@ -936,11 +936,13 @@ def test_vanguard_lows_pass_matches_oracle(case_name, vanguard, request):
             assert np.all(np.abs(lows[q, p, :n] - want) <= 1e-5 * sc), (q, p, c)
             checked += n
     assert checked > 0
-    # the lows pass reads each cluster once per unit of up to 16 of its vanguard pairs
+    # the lows pass reads each cluster once per unit of up to 16 of its vanguard pairs and
+    # writes a 4-byte bound per (vector, vanguard pair)
     P = case.file.padded_dim
     m = np.bincount(g["pidx"][:, :vanguard].reshape(-1), minlength=case.file.nlist)
     sizes = sd.cluster_sizes.astype(np.int64)
-    assert st["vanguard_lows_bytes"] == int((-(-m // 16) * sizes).sum()) * (P // 8 + 12)
+    assert st["vanguard_lows_bytes"] == (int((-(-m // 16) * sizes).sum()) * (P // 8 + 12) +
+                                         4 * int((m * sizes).sum()))
     eng.close()
 
 
@@ -1189,8 +1191,8 @@ def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, nlist, tmp_path):
     and the scan statistics the benchmark's roofline is computed from: the scheduled pairs
     are exactly the probe lists, vanguard pairs first; the far-pass bytes are sum over
     clusters of ceil(m_c / unit) * n_c * (P/8 + 12), the vanguard bytes ceil(m_c / 16) * n_c *
-    (P/8 + 12) for the vanguard lows pass and 4 m_c n_c plus the refined vectors' (P + 8)
-    for the per-query vanguard pass. A second, smaller search on the same engine checks that
+    (P/8 + 12) + 4 m_c n_c for the vanguard lows pass and 4 m_c n_c plus the refined vectors'
+    (P + 8) for the per-query vanguard pass. A second, smaller search on the same engine checks that
     the bucket counts and cursors the first one left behind were cleared."""
     rng = np.random.default_rng(dim + nlist)
     n, nq, nprobe, vanguard = 40000, 192, 32, 5
@@ -1232,10 +1234,11 @@ def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, nlist, tmp_path):
         van_m = np.bincount(pidx[:, :vanguard].reshape(-1), minlength=nlist)
         assert st["scan_vectors"] == int((far_m * sizes).sum())
         assert st["scan_bytes"] == int((-(-far_m // unit) * sizes).sum()) * bpv
-        # the vanguard lows pass reads each cluster once per unit of up to 16 vanguard pairs;
-        # the per-query pass streams one 4-byte bound per (vector, pair), plus the refined
-        # vectors' sign code, ex-code and ex-factors
-        assert st["vanguard_lows_bytes"] == int((-(-van_m // 16) * sizes).sum()) * bpv
+        # the vanguard lows pass reads each cluster once per unit of up to 16 vanguard pairs
+        # and writes one 4-byte bound per (vector, pair), which the per-query pass streams,
+        # plus the refined vectors' sign code, ex-code and ex-factors
+        assert st["vanguard_lows_bytes"] == (int((-(-van_m // 16) * sizes).sum()) * bpv +
+                                             4 * int((van_m * sizes).sum()))
         assert st["vanguard_bytes"] == 4 * int((van_m * sizes).sum()) + st["gpu_refined"] * (P + 8)
     eng.close()
 
