@@ -517,6 +517,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
         return v4i32{(int)a.x, (int)a.y, (int)b.x, (int)b.y};
     };
     const QueueDev q = p.queue;
+    // read once: p's address escapes to the out-of-line flush, so p lives in scratch and a
+    // read of it inside the tile loop is a scratch load, whose wait also waits for every tile
+    // load in flight
+    const uint8_t *const tiles = p.tiles;
+    const size_t tile_bytes = p.tile_bytes;
     // kLows runs over the vanguard unit set, kPublish over the far units, the dense debug
     // output over either
     const uint32_t set = kMode == kLows ? 0u : kMode == kPublish ? 1u : p.dbg_set;
@@ -571,16 +576,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
         // need no survivor staging: 250 VGPRs at P = 768, 0.78 -> 0.73 ms at config 4), the
         // next tile's loads are issued before the
         // current tile's MFMAs, so each wave keeps a tile's loads in flight while it computes.
-        TileRegs<WQ> cur, nxt;
-        if constexpr (kPrefetch)
-            load_tile<W>(p.tiles + (size_t)(tbase + t_begin) * p.tile_bytes, col, quad, cur);
-        for (uint32_t t = t_begin; t < t_end; ++t) {
-            const uint8_t *tile = p.tiles + (size_t)(tbase + t) * p.tile_bytes;
-            if constexpr (kPrefetch) {
-                // the last tile's successor is itself again (a cached reload, no branch)
-                const uint32_t tn = t + 1 < t_end ? t + 1 : t;
-                load_tile<W>(p.tiles + (size_t)(tbase + tn) * p.tile_bytes, col, quad, nxt);
-            }
+        // The tile loop's body, for tile t: its code words and factors come from cur when
+        // they were prefetched, else it loads them.
+        const auto tile_pass = [&](const uint32_t t, const TileRegs<WQ> &cur) __attribute__((always_inline)) {
+            const uint8_t *tile = tiles + (size_t)(tbase + t) * tile_bytes;
             // (at P >= 512 the loads are written out here: through the TileRegs helper the
             // compiler schedules the wide tiles' code differently, measured 11% slower)
             uint32_t xt[4][WQ];
@@ -669,9 +668,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
                         }
                     }
                 }
-                if constexpr (kPrefetch)
-                    cur = nxt;
-                continue;
+                return;
             }
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
@@ -768,8 +765,40 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
             }
             if constexpr (kMode == kLows)
                 lows_flush(p, s_low, lane, w0, count, t, n);
-            if constexpr (kPrefetch)
+        };
+        const auto tile_at = [&](uint32_t t) { return tiles + (size_t)(tbase + t) * tile_bytes; };
+        if constexpr (kPrefetch && W <= 16) {
+            // two register sets in turn, so the loads of the tile after next are issued before
+            // the wait for the next tile's: while a wave waits, two tiles' loads are in flight
+            // (copying one prefetched set into the other made it wait for all of them first)
+            TileRegs<WQ> ra, rb;
+            load_tile<W>(tile_at(t_begin), col, quad, ra);
+            for (uint32_t t = t_begin; t < t_end; t += 2) {
+                // past the last tile its successor is that tile again (a cached reload, no branch)
+                // (the scheduling barriers keep the loads ahead of the waits for the other set)
+                load_tile<W>(tile_at(t + 1 < t_end ? t + 1 : t), col, quad, rb);
+                __builtin_amdgcn_sched_barrier(0);
+                tile_pass(t, ra);
+                if (t + 1 == t_end)
+                    break;
+                load_tile<W>(tile_at(t + 2 < t_end ? t + 2 : t + 1), col, quad, ra);
+                __builtin_amdgcn_sched_barrier(0);
+                tile_pass(t + 1, rb);
+            }
+        } else if constexpr (kPrefetch) {
+            // P = 768 (the lows pass): two sets in turn would spill; the next tile's set is
+            // copied into the current one instead
+            TileRegs<WQ> cur, nxt;
+            load_tile<W>(tile_at(t_begin), col, quad, cur);
+            for (uint32_t t = t_begin; t < t_end; ++t) {
+                load_tile<W>(tile_at(t + 1 < t_end ? t + 1 : t), col, quad, nxt);
+                tile_pass(t, cur);
                 cur = nxt;
+            }
+        } else {
+            const TileRegs<WQ> none{};
+            for (uint32_t t = t_begin; t < t_end; ++t)
+                tile_pass(t, none);
         }
     }
     if constexpr (!kDense) {
