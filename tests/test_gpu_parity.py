@@ -113,6 +113,43 @@ def synth_ip768(tmp_path_factory):
     return Case(path, q, x)
 
 
+
+def _small_case(tmp_path_factory, name, seed, n, dim, nl, nq, metric):
+    """n x dim Gaussian-mixture vectors in nl clusters (unit norm for inner product), nq
+    queries from the same mixture, clustered by nearest center and built by this
+    repository's builder."""
+    rng = np.random.default_rng(seed)
+    centers = rng.normal(0, 1, (nl, dim))
+    x = centers[rng.integers(0, nl, n)] + rng.normal(0, 0.5, (n, dim))
+    q = centers[rng.integers(0, nl, nq)] + rng.normal(0, 0.5, (nq, dim))
+    if metric == 1:
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+        assign = (x @ centers.T).argmax(1).astype(np.uint32)
+    else:
+        assign = ((x[:, None, :] - centers[None]) ** 2).sum(2).argmin(1).astype(np.uint32)
+    x, q = x.astype(np.float32), q.astype(np.float32)
+    cent = np.stack([x[assign == c].mean(0) for c in range(nl)])
+    R = np.linalg.qr(rng.normal(size=(dim, dim)))[0].T.astype(np.float32)
+    path = tmp_path_factory.mktemp(name) / f"{name}.index"
+    ca.build_ivf(path, (x.astype(np.float64) @ R).astype(np.float32),
+                 (cent @ R).astype(np.float32), assign, R, metric=metric)
+    return Case(path, q, x)
+
+
+@pytest.fixture(scope="module")
+def synth_l2_256(tmp_path_factory):
+    """4,000 x 256 (P = 256, 8 words per code), 16 clusters, L2, 32 queries: the
+    matrix-core kernels at W = 8."""
+    return _small_case(tmp_path_factory, "synth256", 256, 4000, 256, 16, 32, 0)
+
+
+@pytest.fixture(scope="module")
+def synth_ip512(tmp_path_factory):
+    """4,000 x 512 unit vectors (P = 512, 16 words per code), 16 clusters, inner product, 32
+    queries: the matrix-core kernels at W = 16, with LUT4 on the matrix cores."""
+    return _small_case(tmp_path_factory, "synth512", 512, 4000, 512, 16, 32, 1)
+
 def run_frozen(case, nprobe, topk, thresholds=None, **kw):
     eng = make_engine(case, nprobe, topk, **kw)
     nq = case.queries.shape[0]
@@ -141,6 +178,8 @@ def gpu_intermediates(eng, case, nprobe):
 
 
 CASES = ["golden_l2", "golden_ip", "synth", "synth_ip768"]
+# P = 256 and 512: the matrix-core kernels' other code widths
+CASES_WIDE = ["synth_l2_256", "synth_ip512"]
 
 
 @pytest.mark.parametrize("case_name", CASES)
@@ -483,7 +522,7 @@ def test_coarse_probe_large_nlist(nlist, tmp_path):
         assert len(set(got.tolist())) == nprobe
 
 
-@pytest.mark.parametrize("case_name", CASES)
+@pytest.mark.parametrize("case_name", CASES + CASES_WIDE)
 @pytest.mark.parametrize("mfma,vanguard", [(True, 0), (False, 0), (True, 4)])
 def test_popcount_estimator_bit_exact(case_name, mfma, vanguard, request):
     """ip_int and ip_res of every (vector, probe) bit-exact, the lower bound within 1e-5,
@@ -588,7 +627,7 @@ def assert_topk_equal(d, i, od, oi, rtol=1e-5):
                 assert i[q, r] in set(oi[q][close].tolist()), (q, r)
 
 
-@pytest.mark.parametrize("case_name", CASES)
+@pytest.mark.parametrize("case_name", CASES + CASES_WIDE)
 @pytest.mark.parametrize("vanguard", [0, 3])
 def test_end_to_end_frozen_infinite_thresholds(case_name, vanguard, request):
     case = request.getfixturevalue(case_name)
@@ -902,7 +941,7 @@ def probed_vectors(case, g, q, nprobe):
     return out
 
 
-@pytest.mark.parametrize("case_name", ["synth", "synth_ip768"])
+@pytest.mark.parametrize("case_name", ["synth", "synth_ip768"] + CASES_WIDE)
 @pytest.mark.parametrize("vanguard", [5, 16])
 def test_vanguard_lows_pass_matches_oracle(case_name, vanguard, request):
     """The matrix-core vanguard lows pass (vanguard units of up to 16 same-cluster pairs):
@@ -1246,7 +1285,7 @@ def test_pair_schedule_and_scan_bytes_large_nlist(dim, metric, nlist, tmp_path):
 # ---------------------------------------------------------------------------------------
 # LUT4 estimator (HybridIndex::set_ip_kernel_type(Lut4Bit), CORA_FLAG_LUT4)
 # ---------------------------------------------------------------------------------------
-@pytest.mark.parametrize("case_name", CASES)
+@pytest.mark.parametrize("case_name", CASES + CASES_WIDE)
 @pytest.mark.parametrize("vanguard", [0, 3])
 def test_lut4_tables_and_estimator_bit_exact(case_name, vanguard, request):
     """The FP16 nibble tables equal the oracle's (precompute_lut_fp16_kernel,
