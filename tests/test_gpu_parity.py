@@ -145,6 +145,20 @@ def synth_l2_256(tmp_path_factory):
 
 
 @pytest.fixture(scope="module")
+def synth_l2_192(tmp_path_factory):
+    """4,000 x 192 (P = 192, 6 words per code), 16 clusters, L2, 32 queries: the
+    16x16x32 matrix-core kernel at W = 6."""
+    return _small_case(tmp_path_factory, "synth192", 192, 4000, 192, 16, 32, 0)
+
+
+@pytest.fixture(scope="module")
+def synth_ip1024(tmp_path_factory):
+    """4,000 x 1,024 unit vectors (P = 1,024, 32 words per code), 16 clusters, inner
+    product, 24 queries: the matrix-core kernels at W = 32."""
+    return _small_case(tmp_path_factory, "synth1024", 1024, 4000, 1024, 16, 24, 1)
+
+
+@pytest.fixture(scope="module")
 def synth_ip512(tmp_path_factory):
     """4,000 x 512 unit vectors (P = 512, 16 words per code), 16 clusters, inner product, 32
     queries: the matrix-core kernels at W = 16, with LUT4 on the matrix cores."""
@@ -178,8 +192,8 @@ def gpu_intermediates(eng, case, nprobe):
 
 
 CASES = ["golden_l2", "golden_ip", "synth", "synth_ip768"]
-# P = 256 and 512: the matrix-core kernels' other code widths
-CASES_WIDE = ["synth_l2_256", "synth_ip512"]
+# P = 192, 256, 512 and 1,024: the matrix-core kernels' other code widths
+CASES_WIDE = ["synth_l2_192", "synth_l2_256", "synth_ip512", "synth_ip1024"]
 
 
 @pytest.mark.parametrize("case_name", CASES)
