@@ -574,8 +574,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
         // one row block of 16 vectors at a time: its K-steps and its lower bounds. For
         // P = 128 (W = 4, 52 VGPRs a tile), and in the lows pass up to P = 768 (whose bounds
         // need no survivor staging: 250 VGPRs at P = 768, 0.78 -> 0.73 ms at config 4), the
-        // next tile's loads are issued before the
-        // current tile's MFMAs, so each wave keeps a tile's loads in flight while it computes.
+        // next tile's loads are issued before the current tile's MFMAs, so each wave keeps a
+        // tile's loads in flight while it computes.
         // The tile loop's body, for tile t: its code words and factors come from cur when
         // they were prefetched, else it loads them.
         const auto tile_pass = [&](const uint32_t t, const TileRegs<WQ> &cur) __attribute__((always_inline)) {
@@ -774,8 +774,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void fa
             TileRegs<WQ> ra, rb;
             load_tile<W>(tile_at(t_begin), col, quad, ra);
             for (uint32_t t = t_begin; t < t_end; t += 2) {
-                // past the last tile its successor is that tile again (a cached reload, no branch)
-                // (the scheduling barriers keep the loads ahead of the waits for the other set)
+                // past the last tile its successor is that tile again (a cached reload, no
+                // branch); the scheduling barriers keep the loads ahead of the other set's waits
                 load_tile<W>(tile_at(t + 1 < t_end ? t + 1 : t), col, quad, rb);
                 __builtin_amdgcn_sched_barrier(0);
                 tile_pass(t, ra);
